@@ -1,0 +1,181 @@
+#!/usr/bin/env python3
+"""Benchmark of the SNNtome wave hot path on one MI355X.
+
+Workload: the ultra-sparse gather-bound wave — substrate of
+40,000,000 positions x batch 256 fp16 (20.5 GB, generated on the device), 65,536 neurons, each
+reading 4 dendritic clusters of S=16 consecutive positions (16-aligned uniform starts),
+W ~ N(0, 0.05), b ~ N(0, 0.01), ReLU, fp32 accumulation.  One step = one execution of the
+compiled one-wave plan through libk44wavec.so (inputs resident in HBM).
+
+Metric: effective TFLOP/s = 2 * nnz * batch / t  (nnz = 65,536 x 64 synapses, batch = 256),
+reported with the achieved HBM GB/s of the wave kernel against the 8 TB/s roofline, and the
+CPU path (OpenMP fp32 oracle) timed on the host cores on a bounded sample of the same wave.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def workload(cfg: int):
+    from snntome_amd import synth
+
+    return {1: synth.config1, 2: synth.config2, 3: synth.config3, 4: synth.config4}[cfg]()
+
+
+def traffic_from_profiles(kernel_key: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters (profiles/*.json), if any."""
+    p = ROOT / "profiles" / f"{kernel_key}_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(wl, budget_s: float = 12.0, sample_neurons: int = 4096):
+    """OpenMP fp32 oracle on a bounded sample of the first wave (same weights / starts),
+    gathering from a compact host copy of exactly the substrate rows the sample reads."""
+    from oracle import oracle
+
+    w = wl.waves[0]
+    n = min(sample_neurons, w.cout)
+    n -= n % w.cluster
+    rows = n // w.cluster
+    stride = (wl.tokens + 63) // 64 * 64
+    starts = w.starts[:rows].astype(np.uint64)
+    compact = oracle.fill_segments(wl.seed, starts.ravel(), w.S, wl.tokens, stride)
+    seg = (np.arange(rows * w.K, dtype=np.uint64) * w.S * stride)
+    canvas = np.concatenate([compact.ravel(), np.zeros(n * stride, np.uint16)])
+    y_off = compact.size
+    threads = len(os.sched_getaffinity(0))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        used = oracle.wave_f32_omp(canvas, seg, w.weights[:n], w.bias[:n], None, w.K, w.S,
+                                   w.cluster, stride, stride, stride, w.act, y_off,
+                                   threads=threads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    t = float(np.median(times))
+    flops = 2.0 * n * w.K * w.S * wl.tokens
+    return {
+        "value": round(flops / t / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": int(used),
+        "kind": "port",
+        "sample": (f"{n} of {w.cout} neurons of {w.name} ({n * w.K} segments, "
+                   f"{n * w.K * w.S} substrate rows x {wl.tokens} tokens), median of "
+                   f"{len(times)} passes, fp32 OpenMP oracle/wave_oracle.c:orc_wave_f32_omp"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4])
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(the wave shards by batch columns with no communication; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from snntome_amd import synth, wavec
+
+    t_start = time.perf_counter()
+    wl = workload(args.config)
+    log(f"[bench] workload {wl.name}: {wl.description}")
+    plan = synth.build_graph(wl, wavec).compile()
+    plan.init_gpu()
+    plan.fill_input_uniform(wl.seed)
+    rep = plan.exec_report()
+    for wv in rep["waves"]:
+        log(f"[bench] {wv['name']}: path={wv['path']} K={wv['K']} S={wv['S']} "
+            f"slab={wv['slab']} tokens={wv['tokens']}")
+    log(f"[bench] setup {time.perf_counter() - t_start:.1f}s; warmup {args.warmup}")
+    if args.warmup > 0:
+        plan.execute(args.warmup)
+    plan.sync()
+
+    # Timed region: K plan executions, device synchronised on both sides.
+    t0 = time.perf_counter()
+    ev_ms = plan.execute(args.steps)  # HIP events on the executor stream, average per step
+    plan.sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    log(f"[bench] {args.steps} steps: {wall_ms:.4f} ms/step wall, {ev_ms:.4f} ms/step events")
+
+    flops = wl.flops
+    comp = sum(synth.compulsory_bytes(wl, w) for w in wl.waves)
+    value = flops / (wall_ms * 1e-3) / 1e12
+    achieved_gbs = comp / (ev_ms * 1e-3) / 1e9
+    kernel_key = "gather_dot_" + wl.name.split("_")[0]
+    traffic = traffic_from_profiles(kernel_key)
+    w0 = wl.waves[0]
+    out = {
+        "metric": "effective TFLOP/s (2*nnz*batch) + achieved HBM GB/s per wave, 1xMI355X",
+        "value": round(value, 4),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (fp32 accumulate)",
+        "data": "synthetic (device-generated counter-hash substrate; numpy PCG64 weights)",
+        "config": {
+            "workload": wl.name,
+            "substrate_positions": wl.substrate,
+            "batch": wl.tokens,
+            "neurons_per_wave": w0.cout,
+            "clusters_per_neuron": w0.K,
+            "S": w0.S,
+            "waves": len(wl.waves),
+            "act": w0.act,
+            "path": rep["waves"][0]["path"],
+        },
+        "hbm_gbs": round(achieved_gbs, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": comp,
+            "kernel_ms": round(ev_ms, 5),
+        },
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(wl)
+        log(f"[bench] cpu baseline {out['cpu_baseline']}")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

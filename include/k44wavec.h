@@ -1,0 +1,141 @@
+/*
+ * k44wavec.h — C ABI of libk44wavec.so, the MI355X (gfx950) wave executor.
+ *
+ * The first 30 entry points are the reference's C ABI (wavec/k44_wave_executor.cu:642-988 of
+ * 7BitLogic/SNNtome) with identical names, signatures, argument meaning and return convention
+ * (0 = success, -1 = failure; pointers NULL on failure).  They are what the reference's ctypes
+ * binding (wavec/wavec.py:28-132) binds.  Differences in behaviour, all on error paths:
+ *   - a HIP runtime error returns -1 (the reference calls exit(EXIT_FAILURE));
+ *   - a plan the executor cannot run (2-D spatial layouts, aux command types other than
+ *     K44_WAVE) fails wavec_gpu_init_plan with -1 instead of silently skipping commands;
+ *   - the message of the last failure on the calling thread is available from wavec_last_error().
+ *
+ * The entry points after "build extensions" have no counterpart in the reference.
+ * Plain C types only; no torch or HIP types cross this boundary.
+ */
+#ifndef K44WAVEC_H
+#define K44WAVEC_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Activation ids (wavec/wavec.py:13-16 ACT_MAP, k44_plan_types.hpp:103); 5 = GELU (extension). */
+enum { K44_ACT_NONE = 0, K44_ACT_RELU = 1, K44_ACT_SIGMOID = 2, K44_ACT_SILU = 3,
+       K44_ACT_LEAKY_RELU = 4, K44_ACT_GELU = 5 };
+
+/* ---- graph handle (k44_wave_executor.cu:644-683) ------------------------------------------- */
+void *wavec_create(int max_B_per_wave, int default_S, int kv_cache_max_seq, int fold_rmsnorm_gamma);
+void wavec_destroy(void *handle);
+int wavec_gpu_release(void *handle);
+
+/* ---- graph builders (k44_wave_executor.cu:685-873) ------------------------------------------ */
+int wavec_add_input(void *handle, const char *name, int c, int h, int w, int is_1d);
+int wavec_add_flatten(void *handle, const char *name, const char *in_tensor, const char *out_tensor);
+/* w_f32: [cout][cin][kh][kw]; bias_f32 and residual_tensor may be NULL. (:704-716) */
+int wavec_add_conv2d(void *handle, const char *name, const char *in_tensor, const char *out_tensor,
+                     int cin, int cout, int kh, int kw, int stride, int pad, int act,
+                     const float *w_f32, const float *bias_f32, const char *residual_tensor);
+int wavec_add_conv2d_f16(void *handle, const char *name, const char *in_tensor,
+                         const char *out_tensor, int cin, int cout, int kh, int kw, int stride,
+                         int pad, int act, const uint16_t *w_f16, const float *bias_f32,
+                         const char *residual_tensor);                                  /* :718-731 */
+int wavec_add_linear_f32(void *handle, const char *name, const char *in_tensor,
+                         const char *out_tensor, int din, int dout, int act, const float *w_f32,
+                         const float *bias_f32, const char *residual_tensor);           /* :733-738 */
+int wavec_add_linear_f16(void *handle, const char *name, const char *in_tensor,
+                         const char *out_tensor, int din, int dout, int act,
+                         const uint16_t *w_f16, const float *bias_f32,
+                         const char *residual_tensor);                                  /* :740-745 */
+int wavec_add_linear_bf16(void *handle, const char *name, const char *in_tensor,
+                          const char *out_tensor, int din, int dout, int act,
+                          const uint16_t *w_bf16, const float *bias_f32,
+                          const char *residual_tensor);                                 /* :747-759 */
+int wavec_add_upconv2x2(void *handle, const char *name, const char *in_tensor,
+                        const char *out_tensor, int cin, int cout, const float *w_f32,
+                        const float *bias_f32);                                          /* :761-771 */
+int wavec_add_maxpool(void *handle, const char *name, const char *in_tensor, const char *out_tensor,
+                      int k, int stride, int pad);                                      /* :773-781 */
+int wavec_add_upsample2x(void *handle, const char *name, const char *in_tensor,
+                         const char *out_tensor);                                        /* :783-791 */
+int wavec_add_rmsnorm(void *handle, const char *name, const char *in_tensor, const char *out_tensor,
+                      int dim, float eps, const float *gamma_f32, int pre_folded);     /* :793-801 */
+int wavec_add_swiglu(void *handle, const char *name, const char *gate_tensor,
+                     const char *up_tensor, const char *out_tensor);                     /* :803-811 */
+int wavec_add_rope_gqa_attn(void *handle, const char *name, const char *q_tensor,
+                            const char *k_tensor, const char *v_tensor, const char *out_tensor,
+                            int h_q, int h_kv, int head_dim, float rope_theta,
+                            int llama3_scaling);                                         /* :813-824 */
+int wavec_add_split(void *handle, const char *name, const char *in_tensor, int num_outs,
+                    const char **out_tensors);                                           /* :826-839 */
+int wavec_add_slice(void *handle, const char *name, const char *in_tensor, int num_outs,
+                    const char **out_tensors, const int *slice_sizes);                  /* :841-858 */
+int wavec_add_concat(void *handle, const char *name, int num_ins, const char **in_tensors,
+                     const char *out_tensor);                                            /* :860-873 */
+
+/* ---- options, compile, summary, .tcff (k44_wave_executor.cu:875-954) ------------------------ */
+int wavec_set_output(void *handle, const char *out_tensor);
+int wavec_set_reuse_canvas(void *handle, int reuse_canvas);
+int wavec_set_batch_size(void *handle, int batch_size);
+int wavec_set_target_preset(void *handle, const char *preset_name);
+int wavec_compile(void *handle);
+/* JSON owned by the handle, valid until the next compile (:923-929). */
+const char *wavec_get_summary_json(void *handle);
+int wavec_save_tcff(void *handle, const char *tcff_path, const char *model_prefix);
+int wavec_save_tcff_ex(void *handle, const char *tcff_path, const char *model_prefix,
+                       int include_canvas, int include_geometry);
+int wavec_load_tcff_weights(void *handle, const char *tcff_path);
+
+/* ---- GPU execution (k44_wave_executor.cu:956-986) ------------------------------------------- */
+int wavec_gpu_init_plan(void *handle);
+/* in: [c][h][w] fp32 of the plan input; out: [c][h][w] fp32 of the plan output. */
+int wavec_gpu_infer_f32(void *handle, const float *h_in, int in_elems, float *h_out,
+                        int out_elems, float *out_gpu_ms);
+
+/* ================================ build extensions ========================================== */
+
+/* Text of the last failure on the calling thread ("" if none).  No reference counterpart. */
+const char *wavec_last_error(void);
+
+/* Sparse wave: `cout` neurons, each with `fan_in` synapses; neurons [r*cluster, (r+1)*cluster)
+ * share index row r.  rows: [cout/cluster][fan_in] input-channel (substrate position) indices;
+ * w_f16: [cout][fan_in] fp16 bits; bias_f16: [cout] fp16 bits or NULL; act: K44_ACT_*.
+ * Replaces nothing in the reference: its builders only emit dense rows
+ * (k44_wave_compiler.hpp:692-807). */
+int wavec_add_sparse_wave(void *handle, const char *name, const char *in_tensor,
+                          const char *out_tensor, int cout, int fan_in, int cluster,
+                          const uint32_t *rows, const uint16_t *w_f16, const uint16_t *bias_f16,
+                          int act, const char *residual_tensor);
+
+/* Dendritic-cluster form: row r = K segments of S consecutive input channels starting at
+ * starts[r*K + k]; w_f16: [cout][K*S]. */
+int wavec_add_cluster_wave(void *handle, const char *name, const char *in_tensor,
+                           const char *out_tensor, int cout, int K, int S, int cluster,
+                           const uint32_t *starts, const uint16_t *w_f16, const uint16_t *bias_f16,
+                           int act, const char *residual_tensor);
+
+/* Fills the plan input on the device with the synthetic substrate
+ * x(pos, t) = fp16_rne((int32(h >> 40) - 2^23) * 2^-23),
+ * h = splitmix64(((pos << 20) | t) ^ splitmix64(seed)); padding tokens are 0. */
+int wavec_gpu_fill_input_uniform(void *handle, unsigned long long seed);
+
+/* Runs the whole plan `iters` times on the executor stream; average ms per run (HIP events). */
+int wavec_gpu_execute(void *handle, int iters, float *out_ms_per_iter);
+int wavec_gpu_sync(void *handle);
+
+/* Raw fp16 access to the canvas (element offsets / counts). */
+int wavec_gpu_read_canvas(void *handle, unsigned long long elem_off, unsigned long long n_elems,
+                          uint16_t *dst);
+int wavec_gpu_write_canvas(void *handle, unsigned long long elem_off, unsigned long long n_elems,
+                           const uint16_t *src);
+
+/* JSON: per wave the kernel path taken and why, its segment schedule (K, S, step) and
+ * accounting (flops, distinct substrate rows).  "{}" before a successful init. */
+const char *wavec_gpu_exec_report_json(void *handle);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* K44WAVEC_H */

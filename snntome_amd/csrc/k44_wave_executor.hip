@@ -1,0 +1,829 @@
+// k44_wave_executor.hip — MI355X executor for compiled wave plans + the wavec C ABI.
+//
+// Replaces the reference's wavec/k44_wave_executor.cu (K44GpuExecutorState and the extern "C"
+// frontend at :642-988).  The C ABI keeps the reference's 30 entry points with the same
+// signatures, argument meaning and 0 / -1 return convention, and adds the build extensions
+// declared in include/k44wavec.h.
+//
+// Executor design (gfx950):
+//  * One hipMalloc'd fp16 canvas per plan, zeroed at init; all tensors are views into it.
+//  * Every K44_WAVE command is turned at upload into a device schedule: the per-synapse index
+//    rows are compressed into dendritic segments (start offset, S consecutive positions at a
+//    fixed canvas step), the RDNA4-ordered weight blocks are re-laid out into the order the
+//    chosen kernel consumes, and every address the kernel can touch is bounds-checked against
+//    the canvas on the host before any launch.
+//  * Kernels run on a private non-blocking stream (default priority); timing uses HIP events on
+//    that stream.
+//  * Errors never terminate the process: each entry point returns -1 and records a message
+//    readable through wavec_last_error().
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <memory>
+#include <mutex>
+#include <numeric>
+#include <sstream>
+
+#include "k44_wave_compiler.hpp"
+#include "k44wavec.h"
+#include "kernels/k44_gather_dot.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+void set_error(const std::string &m) {
+    g_last_error = m;
+    std::fprintf(stderr, "[k44wavec] %s\n", m.c_str());
+}
+
+struct HipFail : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define K44_HIP(call)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (call);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            throw HipFail(std::string("HIP error '") + hipGetErrorString(e_) + "' in " #call); \
+    } while (0)
+
+template <typename T>
+struct DevBuf {
+    T *p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    ~DevBuf() { reset(); }
+    void reset() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    void alloc(size_t count) {
+        reset();
+        if (count) K44_HIP(hipMalloc(&p, count * sizeof(T)));
+        n = count;
+    }
+    void upload(const std::vector<T> &h) {
+        alloc(h.size());
+        if (!h.empty()) K44_HIP(hipMemcpy(p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
+    }
+};
+
+// Device schedule of one K44_WAVE command.
+struct WaveExec {
+    std::string name;
+    std::string path;      // "valu_gather_dot"
+    std::string why;
+    uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
+    uint64_t step = 1;
+    uint32_t tokens = 0, out_stride = 0;
+    uint32_t slab = 256, U = 4, n_batch = 1;
+    uint64_t y_off = 0, res_off = 0;
+    int act = 0;
+    bool has_res = false;
+    double flops = 0.0;          // 2 * nnz * tokens (padded neurons included)
+    uint64_t unique_rows = 0;    // distinct substrate positions read
+    DevBuf<uint64_t> seg;
+    DevBuf<__half> w, bias;
+    DevBuf<uint16_t> cmap;
+};
+
+uint32_t pick_slab(uint32_t tokens) {
+    if (tokens % 256u == 0u) return 256u;
+    if (tokens % 128u == 0u) return 128u;
+    return 64u;
+}
+
+}  // namespace
+
+namespace k44_host {
+
+struct K44GpuExecutorState {
+    K44WavePlan plan_meta;  // plan without payload vectors
+    std::vector<std::unique_ptr<WaveExec>> waves;
+    DevBuf<__half> canvas;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    bool initialized = false;
+    std::string report_json;
+
+    ~K44GpuExecutorState() { free_all(); }
+
+    void free_all() {
+        waves.clear();
+        canvas.reset();
+        if (ev0) (void)hipEventDestroy(ev0);
+        if (ev1) (void)hipEventDestroy(ev1);
+        if (stream) (void)hipStreamDestroy(stream);
+        ev0 = ev1 = nullptr;
+        stream = nullptr;
+        initialized = false;
+    }
+
+    // Index rows -> dendritic segments.  Canvas element offsets e[s] of a row are split at
+    // every s where e[s] != e[s-1] + step; the segment length S is the gcd of B_raw and all
+    // split points, so every row is K = B_raw / S runs of S consecutive positions.
+    static void segment_rows(const K44ExecCmd &c, uint64_t step, uint32_t &S_out,
+                             std::vector<uint64_t> &starts) {
+        const uint32_t B = c.B, b_raw = c.B_raw;
+        const size_t rows = c.h_idx.size() / B;
+        auto off = [&](size_t r, uint32_t s) -> uint64_t {
+            const uint64_t v = c.h_idx[r * B + s];
+            return c.idx_mode == 1u ? c.x_base_off + v * c.idx_stride : c.x_base_off + v;
+        };
+        uint32_t S = b_raw;
+        for (size_t r = 0; r < rows && S > 1u; ++r) {
+            uint64_t prev = off(r, 0);
+            for (uint32_t s = 1; s < b_raw; ++s) {
+                const uint64_t e = off(r, s);
+                if (e != prev + step) S = std::gcd(S, s);
+                prev = e;
+            }
+        }
+        const uint32_t K = b_raw / S;
+        starts.resize(rows * K);
+        for (size_t r = 0; r < rows; ++r)
+            for (uint32_t k = 0; k < K; ++k) starts[r * K + k] = off(r, k * S);
+        S_out = S;
+    }
+
+    void build_wave(const K44ExecCmd &c, WaveExec &wx) {
+        const auto &Lo = plan_meta.res_map.at(c.res_key_out);
+        auto itin = plan_meta.res_map.find(c.res_key_in);
+        if (!Lo.is_1d_tokens || itin == plan_meta.res_map.end() || !itin->second.is_1d_tokens)
+            throw std::runtime_error("wave '" + c.name +
+                                     "': 2-D spatial layouts are not supported by this executor");
+        if (c.h_idx.empty() || c.B == 0u || c.B_raw == 0u || c.h_idx.size() % c.B != 0u)
+            throw std::runtime_error("wave '" + c.name + "': missing or malformed index table");
+        if (c.h_w_wmma.size() * 8u < (size_t)c.Cout * c.B)
+            throw std::runtime_error("wave '" + c.name + "': weight block smaller than Cout x B");
+        const size_t rows = c.h_idx.size() / c.B;
+        if (rows * c.cluster_size != c.Cout)
+            throw std::runtime_error("wave '" + c.name + "': index rows x cluster != Cout");
+        if (c.has_cout_map && c.h_cout_map.size() < c.Cout)
+            throw std::runtime_error("wave '" + c.name + "': cout_map shorter than Cout");
+
+        wx.name = c.name;
+        wx.cout = c.Cout;
+        wx.cluster = c.cluster_size;
+        wx.rows = (uint32_t)rows;
+        wx.tokens = Lo.channel_stride;  // single-frame 1-D: tiles 64t .. 64t+63 of the row
+        wx.out_stride = Lo.channel_stride;
+        wx.step = c.idx_mode == 1u ? c.idx_stride : itin->second.channel_stride;
+        wx.y_off = c.y_off;
+        wx.res_off = c.res_off;
+        wx.has_res = c.has_residual;
+        wx.act = (int)c.act;
+        if (wx.act < 0 || wx.act > 5)
+            throw std::runtime_error("wave '" + c.name + "': unknown activation id");
+
+        std::vector<uint64_t> starts;
+        segment_rows(c, wx.step, wx.S, starts);
+        wx.K = c.B_raw / wx.S;
+
+        // Row-major [Cout][B] weights from the on-disk WMMA order; padded synapses must be 0.
+        std::vector<uint16_t> wraw((size_t)c.Cout * c.B);
+        convert_wmma_to_raw(reinterpret_cast<uint4_host *>(wraw.data()), c.h_w_wmma.data(),
+                            c.Cout, c.B / 8u);
+        for (size_t j = 0; j < c.Cout; ++j)
+            for (uint32_t s = c.B_raw; s < c.B; ++s)
+                if (wraw[j * c.B + s] != 0u)
+                    throw std::runtime_error("wave '" + c.name +
+                                             "': non-zero weight on a padded synapse");
+
+        // Host-side bounds check of every canvas element the kernel may touch.
+        const uint64_t n_canvas = plan_meta.canvas_elems;
+        uint64_t x_hi = 0;
+        for (uint64_t s0 : starts) x_hi = std::max(x_hi, s0);
+        x_hi += (uint64_t)(wx.S - 1u) * wx.step + wx.tokens;
+        if (x_hi > n_canvas)
+            throw std::runtime_error("wave '" + c.name + "': gather reaches past the canvas");
+        uint64_t oj_hi = c.Cout - 1u;
+        if (c.has_cout_map) {
+            oj_hi = 0;
+            for (uint32_t j = 0; j < c.Cout; ++j) oj_hi = std::max<uint64_t>(oj_hi, c.h_cout_map[j]);
+        }
+        const uint64_t span = oj_hi * wx.out_stride + wx.tokens;
+        if (wx.y_off + span > n_canvas || (wx.has_res && wx.res_off + span > n_canvas))
+            throw std::runtime_error("wave '" + c.name + "': output/residual past the canvas");
+        if (wx.tokens % 64u != 0u || wx.out_stride % 4u != 0u || wx.y_off % 4u != 0u ||
+            wx.res_off % 4u != 0u || wx.step % 4u != 0u)
+            throw std::runtime_error("wave '" + c.name + "': canvas rows not 8-byte aligned");
+        for (uint64_t s0 : starts)
+            if (s0 % 4u != 0u)
+                throw std::runtime_error("wave '" + c.name +
+                                         "': token-shifted (unaligned) gathers not supported yet");
+
+        // Distinct substrate positions (compulsory-traffic accounting).
+        {
+            std::vector<std::pair<uint64_t, uint64_t>> iv;
+            iv.reserve(starts.size());
+            for (uint64_t s0 : starts) iv.push_back({s0, s0 + (uint64_t)wx.S * wx.step});
+            std::sort(iv.begin(), iv.end());
+            uint64_t covered = 0, cur_lo = 0, cur_hi = 0;
+            bool open = false;
+            for (auto &p : iv) {
+                if (!open || p.first > cur_hi) {
+                    if (open) covered += cur_hi - cur_lo;
+                    cur_lo = p.first;
+                    cur_hi = p.second;
+                    open = true;
+                } else {
+                    cur_hi = std::max(cur_hi, p.second);
+                }
+            }
+            if (open) covered += cur_hi - cur_lo;
+            wx.unique_rows = wx.step ? covered / wx.step : 0;
+        }
+
+        // VALU gather-dot schedule.
+        wx.path = "valu_gather_dot";
+        wx.why = "neurons do not share index rows (cluster < 16) or the segment run is shorter "
+                 "than one 32-deep MFMA K-step: no dense contraction, gather-bound";
+        wx.slab = pick_slab(wx.tokens);
+        const uint32_t rpi = 256u / wx.slab;
+        wx.U = 16u / rpi;
+        const uint32_t per_batch = rpi * wx.U;
+        wx.n_batch = (wx.S + per_batch - 1u) / per_batch;
+        std::vector<uint16_t> wk((size_t)c.Cout * wx.K * wx.n_batch * per_batch, 0u);
+        for (size_t j = 0; j < c.Cout; ++j)
+            for (uint32_t k = 0; k < wx.K; ++k)
+                for (uint32_t s = 0; s < wx.S; ++s) {
+                    const uint32_t b = s / per_batch, q = s % per_batch;  // q = g*U + u
+                    wk[((j * wx.K + k) * wx.n_batch + b) * per_batch + q] =
+                        wraw[j * c.B + (size_t)k * wx.S + s];
+                }
+        std::vector<__half> wh(wk.size());
+        std::memcpy(wh.data(), wk.data(), wk.size() * 2u);
+        wx.w.upload(wh);
+        wx.seg.upload(starts);
+        std::vector<__half> bh(c.Cout);
+        for (size_t j = 0; j < c.Cout; ++j) {
+            const uint16_t v = j < c.h_bias.size() ? c.h_bias[j] : 0u;
+            std::memcpy(&bh[j], &v, 2);
+        }
+        if (c.has_bias) wx.bias.upload(bh);
+        if (c.has_cout_map)
+            wx.cmap.upload(std::vector<uint16_t>(c.h_cout_map.begin(), c.h_cout_map.begin() + c.Cout));
+        wx.flops = 2.0 * (double)c.Cout * c.B_raw * wx.tokens;
+    }
+
+    void init(const K44WavePlan &plan) {
+        free_all();
+        plan_meta.res_map = plan.res_map;
+        plan_meta.canvas_elems = plan.canvas_elems;
+        plan_meta.input_off = plan.input_off;
+        plan_meta.input_c = plan.input_c;
+        plan_meta.input_h = plan.input_h;
+        plan_meta.input_w = plan.input_w;
+        plan_meta.input_res_key = plan.input_res_key;
+        plan_meta.output_off = plan.output_off;
+        plan_meta.output_c = plan.logical_output_c;
+        plan_meta.output_h = plan.output_h;
+        plan_meta.output_w = plan.output_w;
+        plan_meta.output_res_key = plan.output_res_key;
+        plan_meta.batch_size = plan.batch_size;
+        for (const auto &c : plan.cmds) {
+            if (c.type != K44CmdType::K44_WAVE)
+                throw std::runtime_error(std::string("command '") + c.name + "' of type " +
+                                         cmd_type_str(c.type) +
+                                         " is not supported by this executor");
+            auto wx = std::make_unique<WaveExec>();
+            build_wave(c, *wx);
+            waves.push_back(std::move(wx));
+        }
+        K44_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+        K44_HIP(hipEventCreate(&ev0));
+        K44_HIP(hipEventCreate(&ev1));
+        canvas.alloc(plan.canvas_elems);
+        K44_HIP(hipMemsetAsync(canvas.p, 0, plan.canvas_elems * 2u, stream));
+        K44_HIP(hipStreamSynchronize(stream));
+        build_report();
+        initialized = true;
+    }
+
+    void build_report() {
+        std::ostringstream o;
+        o << "{\"waves\": [";
+        for (size_t i = 0; i < waves.size(); ++i) {
+            const WaveExec &w = *waves[i];
+            o << (i ? ", " : "") << "{\"name\": \"" << w.name << "\", \"path\": \"" << w.path
+              << "\", \"why\": \"" << w.why << "\", \"cout\": " << w.cout << ", \"K\": " << w.K
+              << ", \"S\": " << w.S << ", \"cluster\": " << w.cluster << ", \"step\": " << w.step
+              << ", \"tokens\": " << w.tokens << ", \"slab\": " << w.slab << ", \"U\": " << w.U
+              << ", \"flops\": " << (long long)w.flops << ", \"unique_rows\": " << w.unique_rows
+              << ", \"y_off\": " << w.y_off << "}";
+        }
+        o << "], \"canvas_elems\": " << plan_meta.canvas_elems << "}";
+        report_json = o.str();
+    }
+
+    void launch_wave(const WaveExec &w) {
+        k44dev::GatherDotArgs a{};
+        a.X = canvas.p;
+        a.seg = w.seg.p;
+        a.W = w.w.p;
+        a.bias = w.bias.p;
+        a.cmap = w.cmap.p;
+        a.Y = canvas.p + w.y_off;
+        a.R = w.has_res ? canvas.p + w.res_off : nullptr;
+        a.step = w.step;
+        a.K = w.K;
+        a.S = w.S;
+        a.n_batch = w.n_batch;
+        a.cluster = w.cluster;
+        a.cout = w.cout;
+        a.out_stride = w.out_stride;
+        a.act = w.act;
+        const dim3 grid((w.cout + 3u) / 4u, w.tokens / w.slab, 1u), block(256u, 1u, 1u);
+        switch (w.slab) {
+        case 256u: hipLaunchKernelGGL((k44dev::k44_gather_dot_kernel<256, 16>), grid, block, 0, stream, a); break;
+        case 128u: hipLaunchKernelGGL((k44dev::k44_gather_dot_kernel<128, 8>), grid, block, 0, stream, a); break;
+        default: hipLaunchKernelGGL((k44dev::k44_gather_dot_kernel<64, 4>), grid, block, 0, stream, a); break;
+        }
+        K44_HIP(hipGetLastError());
+    }
+
+    void execute_plan() {
+        for (const auto &w : waves) launch_wave(*w);
+    }
+
+    const K44ResDesc &layout(uint32_t key) const { return plan_meta.res_map.at(key); }
+
+    void upload_input_f32(const float *in, size_t n) {
+        const K44ResDesc &L = layout(plan_meta.input_res_key);
+        if (!L.is_1d_tokens) throw std::runtime_error("2-D input layouts are not supported");
+        std::vector<uint16_t> pad((size_t)plan_meta.input_c * L.channel_stride, 0u);
+        for (uint32_t ch = 0; ch < plan_meta.input_c; ++ch)
+            for (uint32_t y = 0; y < plan_meta.input_h; ++y)
+                for (uint32_t x = 0; x < plan_meta.input_w; ++x) {
+                    const size_t src = ((size_t)ch * plan_meta.input_h + y) * plan_meta.input_w + x;
+                    if (src < n) pad[L.canvas_offset(ch, y, x)] = float_to_half(in[src]);
+                }
+        K44_HIP(hipMemcpyAsync(canvas.p + plan_meta.input_off, pad.data(), pad.size() * 2u,
+                               hipMemcpyHostToDevice, stream));
+        K44_HIP(hipStreamSynchronize(stream));
+    }
+
+    std::vector<float> download_output_f32() {
+        const K44ResDesc &L = layout(plan_meta.output_res_key);
+        std::vector<uint16_t> pad((size_t)plan_meta.output_c * L.channel_stride);
+        K44_HIP(hipMemcpyAsync(pad.data(), canvas.p + plan_meta.output_off, pad.size() * 2u,
+                               hipMemcpyDeviceToHost, stream));
+        K44_HIP(hipStreamSynchronize(stream));
+        std::vector<float> out((size_t)plan_meta.output_c * plan_meta.output_h * plan_meta.output_w);
+        for (uint32_t ch = 0; ch < plan_meta.output_c; ++ch)
+            for (uint32_t y = 0; y < plan_meta.output_h; ++y)
+                for (uint32_t x = 0; x < plan_meta.output_w; ++x)
+                    out[((size_t)ch * plan_meta.output_h + y) * plan_meta.output_w + x] =
+                        half_to_float(pad[L.canvas_offset(ch, y, x)]);
+        return out;
+    }
+
+    int infer_f32(const float *in, int in_elems, float *out, int out_elems, float *ms_out) {
+        if (!initialized) throw std::runtime_error("executor not initialised");
+        upload_input_f32(in, (size_t)std::max(0, in_elems));
+        K44_HIP(hipEventRecord(ev0, stream));
+        execute_plan();
+        K44_HIP(hipEventRecord(ev1, stream));
+        K44_HIP(hipEventSynchronize(ev1));
+        float ms = 0.0f;
+        K44_HIP(hipEventElapsedTime(&ms, ev0, ev1));
+        if (ms_out) *ms_out = ms;
+        const std::vector<float> y = download_output_f32();
+        std::memcpy(out, y.data(), std::min((size_t)std::max(0, out_elems), y.size()) * 4u);
+        return 0;
+    }
+};
+
+static std::mutex g_exec_mu;
+// Executors by graph handle.  Heap-held and never destroyed, so no HIP call runs from a static
+// destructor after the HIP runtime has shut down at process exit.
+static auto &g_gpu_executors = *new std::map<void *, std::unique_ptr<K44GpuExecutorState>>();
+
+static K44GpuExecutorState *find_exec(void *h) {
+    std::lock_guard<std::mutex> lk(g_exec_mu);
+    auto it = g_gpu_executors.find(h);
+    return (it == g_gpu_executors.end() || !it->second || !it->second->initialized)
+               ? nullptr
+               : it->second.get();
+}
+
+}  // namespace k44_host
+
+// =================================================================================================
+// C ABI
+// =================================================================================================
+using k44_host::K44Act;
+using k44_host::K44WaveGraphCompiler;
+
+namespace {
+
+K44WaveGraphCompiler *comp_of(void *h) { return static_cast<K44WaveGraphCompiler *>(h); }
+
+// Runs f, mapping every exception to -1 + last-error text.
+template <typename F>
+int guarded(const char *what, F &&f) {
+    try {
+        return f();
+    } catch (const std::exception &e) {
+        set_error(std::string(what) + ": " + e.what());
+    } catch (...) {
+        set_error(std::string(what) + ": unknown error");
+    }
+    return -1;
+}
+
+K44WaveGraphCompiler *compiled(void *h) {
+    K44WaveGraphCompiler *c = comp_of(h);
+    if (c && !c->is_compiled) c->compile();
+    return c;
+}
+
+std::string opt_str(const char *s) { return s ? std::string(s) : std::string(); }
+
+}  // namespace
+
+extern "C" {
+
+void *wavec_create(int max_B_per_wave, int default_S, int kv_cache_max_seq,
+                   int fold_rmsnorm_gamma) {
+    auto *c = new K44WaveGraphCompiler();
+    c->opts.max_B_per_wave = (uint32_t)std::max(0, max_B_per_wave);
+    c->opts.force_cluster_size = (uint32_t)std::max(0, default_S);
+    c->opts.kv_cache_max_seq = (uint32_t)std::max(0, kv_cache_max_seq);
+    c->opts.fold_rmsnorm_gamma = fold_rmsnorm_gamma != 0;
+    c->opts.keep_host_plan_buffers = true;
+    return c;
+}
+
+void wavec_destroy(void *h) {
+    if (!h) return;
+    {
+        std::lock_guard<std::mutex> lk(k44_host::g_exec_mu);
+        k44_host::g_gpu_executors.erase(h);
+    }
+    delete comp_of(h);
+}
+
+int wavec_gpu_release(void *h) {
+    if (!h) return -1;
+    std::lock_guard<std::mutex> lk(k44_host::g_exec_mu);
+    k44_host::g_gpu_executors.erase(h);
+    return 0;
+}
+
+int wavec_add_input(void *h, const char *name, int c, int hh, int w, int is_1d) {
+    if (!h || !name) return -1;
+    return guarded("wavec_add_input", [&] {
+        comp_of(h)->add_input(name, (uint32_t)c, (uint32_t)hh, (uint32_t)w, is_1d != 0);
+        return 0;
+    });
+}
+
+int wavec_add_flatten(void *h, const char *name, const char *in, const char *out) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_flatten", [&] {
+        comp_of(h)->add_flatten(name, in, out);
+        return 0;
+    });
+}
+
+int wavec_add_conv2d(void *h, const char *name, const char *in, const char *out, int cin,
+                     int cout, int kh, int kw, int stride, int pad, int act, const float *w_f32,
+                     const float *bias_f32, const char *residual) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_conv2d", [&] {
+        comp_of(h)->add_conv2d(name, in, out, (uint32_t)cin, (uint32_t)cout, (uint32_t)kh,
+                               (uint32_t)kw, (uint32_t)stride, (uint32_t)pad, (K44Act)act, w_f32,
+                               bias_f32, opt_str(residual));
+        return 0;
+    });
+}
+
+int wavec_add_conv2d_f16(void *h, const char *name, const char *in, const char *out, int cin,
+                         int cout, int kh, int kw, int stride, int pad, int act,
+                         const uint16_t *w_f16, const float *bias_f32, const char *residual) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_conv2d_f16", [&] {
+        comp_of(h)->add_conv2d_f16(name, in, out, (uint32_t)cin, (uint32_t)cout, (uint32_t)kh,
+                                   (uint32_t)kw, (uint32_t)stride, (uint32_t)pad, (K44Act)act,
+                                   w_f16, bias_f32, opt_str(residual));
+        return 0;
+    });
+}
+
+int wavec_add_linear_f32(void *h, const char *name, const char *in, const char *out, int din,
+                         int dout, int act, const float *w_f32, const float *bias_f32,
+                         const char *residual) {
+    return wavec_add_conv2d(h, name, in, out, din, dout, 1, 1, 1, 0, act, w_f32, bias_f32,
+                            residual);
+}
+
+int wavec_add_linear_f16(void *h, const char *name, const char *in, const char *out, int din,
+                         int dout, int act, const uint16_t *w_f16, const float *bias_f32,
+                         const char *residual) {
+    return wavec_add_conv2d_f16(h, name, in, out, din, dout, 1, 1, 1, 0, act, w_f16, bias_f32,
+                                residual);
+}
+
+int wavec_add_linear_bf16(void *h, const char *name, const char *in, const char *out, int din,
+                          int dout, int act, const uint16_t *w_bf16, const float *bias_f32,
+                          const char *residual) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_linear_bf16", [&] {
+        comp_of(h)->add_linear_bf16(name, in, out, (uint32_t)din, (uint32_t)dout, (K44Act)act,
+                                    w_bf16, bias_f32, opt_str(residual));
+        return 0;
+    });
+}
+
+int wavec_add_upconv2x2(void *h, const char *name, const char *in, const char *out, int cin,
+                        int cout, const float *w_f32, const float *bias_f32) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_upconv2x2", [&] {
+        comp_of(h)->add_upconv2x2(name, in, out, (uint32_t)cin, (uint32_t)cout, w_f32, bias_f32);
+        return 0;
+    });
+}
+
+int wavec_add_maxpool(void *h, const char *name, const char *in, const char *out, int k,
+                      int stride, int pad) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_maxpool", [&] {
+        comp_of(h)->add_maxpool(name, in, out, (uint32_t)k, (uint32_t)stride, (uint32_t)pad);
+        return 0;
+    });
+}
+
+int wavec_add_upsample2x(void *h, const char *name, const char *in, const char *out) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_upsample2x", [&] {
+        comp_of(h)->add_upsample2x(name, in, out);
+        return 0;
+    });
+}
+
+int wavec_add_rmsnorm(void *h, const char *name, const char *in, const char *out, int dim,
+                      float eps, const float *gamma_f32, int pre_folded) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_rmsnorm", [&] {
+        comp_of(h)->add_rmsnorm(name, in, out, (uint32_t)dim, eps, gamma_f32, pre_folded != 0);
+        return 0;
+    });
+}
+
+int wavec_add_swiglu(void *h, const char *name, const char *gate, const char *up,
+                     const char *out) {
+    if (!h || !name || !gate || !up || !out) return -1;
+    return guarded("wavec_add_swiglu", [&] {
+        comp_of(h)->add_swiglu_mul(name, gate, up, out);
+        return 0;
+    });
+}
+
+int wavec_add_rope_gqa_attn(void *h, const char *name, const char *q, const char *k,
+                            const char *v, const char *out, int h_q, int h_kv, int head_dim,
+                            float rope_theta, int llama3_scaling) {
+    if (!h || !name || !q || !k || !v || !out) return -1;
+    return guarded("wavec_add_rope_gqa_attn", [&] {
+        comp_of(h)->add_rope_gqa_attention(name, q, k, v, out, (uint32_t)h_q, (uint32_t)h_kv,
+                                           (uint32_t)head_dim, rope_theta, llama3_scaling != 0);
+        return 0;
+    });
+}
+
+int wavec_add_split(void *h, const char *name, const char *in, int num_outs, const char **outs) {
+    if (!h || !name || !in || num_outs <= 0 || !outs) return -1;
+    return guarded("wavec_add_split", [&] {
+        comp_of(h)->add_split(name, in, std::vector<std::string>(outs, outs + num_outs));
+        return 0;
+    });
+}
+
+int wavec_add_slice(void *h, const char *name, const char *in, int num_outs, const char **outs,
+                    const int *slice_sizes) {
+    if (!h || !name || !in || num_outs <= 0 || !outs) return -1;
+    return guarded("wavec_add_slice", [&] {
+        std::vector<uint32_t> sizes;
+        if (slice_sizes)
+            for (int i = 0; i < num_outs; ++i) sizes.push_back((uint32_t)slice_sizes[i]);
+        comp_of(h)->add_slice(name, in, std::vector<std::string>(outs, outs + num_outs), sizes);
+        return 0;
+    });
+}
+
+int wavec_add_concat(void *h, const char *name, int num_ins, const char **ins, const char *out) {
+    if (!h || !name || num_ins <= 0 || !ins || !out) return -1;
+    return guarded("wavec_add_concat", [&] {
+        comp_of(h)->add_concat(name, std::vector<std::string>(ins, ins + num_ins), out);
+        return 0;
+    });
+}
+
+int wavec_set_output(void *h, const char *out) {
+    if (!h || !out) return -1;
+    comp_of(h)->default_output_tensor = out;
+    comp_of(h)->is_compiled = false;
+    return 0;
+}
+
+int wavec_set_reuse_canvas(void *h, int reuse) {
+    if (!h) return -1;
+    comp_of(h)->opts.reuse_canvas = reuse != 0;
+    comp_of(h)->is_compiled = false;
+    return 0;
+}
+
+int wavec_set_batch_size(void *h, int batch) {
+    if (!h) return -1;
+    comp_of(h)->opts.batch_size = (uint32_t)std::max(1, batch);
+    comp_of(h)->is_compiled = false;
+    return 0;
+}
+
+int wavec_set_target_preset(void *h, const char *preset) {
+    if (!h) return -1;
+    comp_of(h)->opts.hw_profile = k44_host::K44HardwareProfile::from_preset(preset);
+    comp_of(h)->is_compiled = false;
+    return 0;
+}
+
+int wavec_compile(void *h) {
+    if (!h) return -1;
+    return guarded("wavec_compile", [&] {
+        comp_of(h)->compile();
+        return 0;
+    });
+}
+
+const char *wavec_get_summary_json(void *h) {
+    if (!h) return "{}";
+    if (guarded("wavec_get_summary_json", [&] {
+            compiled(h);
+            return 0;
+        }) != 0)
+        return "{}";
+    return comp_of(h)->cached_summary_json.c_str();
+}
+
+int wavec_save_tcff_ex(void *h, const char *path, const char *prefix, int include_canvas,
+                       int include_geometry) {
+    if (!h || !path) return -1;
+    (void)include_canvas;  // as in the reference: canvas pages are never written
+    return guarded("wavec_save_tcff", [&] {
+        return k44_host::save_plan_to_tcff(compiled(h)->compiled_plan, path, prefix, false,
+                                           include_geometry != 0, nullptr)
+                   ? 0
+                   : -1;
+    });
+}
+
+int wavec_save_tcff(void *h, const char *path, const char *prefix) {
+    return wavec_save_tcff_ex(h, path, prefix, 1, 1);
+}
+
+int wavec_load_tcff_weights(void *h, const char *path) {
+    if (!h || !path) return -1;
+    return guarded("wavec_load_tcff_weights", [&] {
+        if (!k44_host::load_weights_from_tcff(compiled(h)->compiled_plan, path)) {
+            set_error(std::string("wavec_load_tcff_weights: rejected ") + path);
+            return -1;
+        }
+        return 0;
+    });
+}
+
+int wavec_gpu_init_plan(void *h) {
+    if (!h) return -1;
+    return guarded("wavec_gpu_init_plan", [&] {
+        K44WaveGraphCompiler *c = compiled(h);
+        auto ex = std::make_unique<k44_host::K44GpuExecutorState>();
+        ex->init(c->compiled_plan);
+        std::lock_guard<std::mutex> lk(k44_host::g_exec_mu);
+        k44_host::g_gpu_executors[h] = std::move(ex);
+        return 0;
+    });
+}
+
+int wavec_gpu_infer_f32(void *h, const float *in, int in_elems, float *out, int out_elems,
+                        float *out_gpu_ms) {
+    if (!h || !in || !out) return -1;
+    return guarded("wavec_gpu_infer_f32", [&] {
+        k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+        if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+        return ex->infer_f32(in, in_elems, out, out_elems, out_gpu_ms);
+    });
+}
+
+// ------------------------------- build extensions --------------------------------------------
+
+const char *wavec_last_error(void) { return g_last_error.c_str(); }
+
+int wavec_add_sparse_wave(void *h, const char *name, const char *in, const char *out, int cout,
+                          int fan_in, int cluster, const uint32_t *rows, const uint16_t *w_f16,
+                          const uint16_t *bias_f16, int act, const char *residual) {
+    if (!h || !name || !in || !out || cout <= 0 || fan_in <= 0 || cluster <= 0) return -1;
+    return guarded("wavec_add_sparse_wave", [&] {
+        comp_of(h)->add_sparse_wave(name, in, out, (uint32_t)cout, (uint32_t)fan_in,
+                                    (uint32_t)cluster, rows, w_f16, bias_f16, (K44Act)act,
+                                    opt_str(residual));
+        return 0;
+    });
+}
+
+int wavec_add_cluster_wave(void *h, const char *name, const char *in, const char *out, int cout,
+                           int K, int S, int cluster, const uint32_t *starts,
+                           const uint16_t *w_f16, const uint16_t *bias_f16, int act,
+                           const char *residual) {
+    if (!h || !name || !in || !out || cout <= 0 || K <= 0 || S <= 0 || cluster <= 0) return -1;
+    return guarded("wavec_add_cluster_wave", [&] {
+        comp_of(h)->add_cluster_wave(name, in, out, (uint32_t)cout, (uint32_t)K, (uint32_t)S,
+                                     (uint32_t)cluster, starts, w_f16, bias_f16, (K44Act)act,
+                                     opt_str(residual));
+        return 0;
+    });
+}
+
+int wavec_gpu_fill_input_uniform(void *h, unsigned long long seed) {
+    if (!h) return -1;
+    return guarded("wavec_gpu_fill_input_uniform", [&] {
+        k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+        if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+        const auto &L = ex->layout(ex->plan_meta.input_res_key);
+        if (!L.is_1d_tokens) throw std::runtime_error("2-D input layouts are not supported");
+        const uint64_t rows = ex->plan_meta.input_c;
+        const uint64_t seed_mix = k44dev::splitmix64((uint64_t)seed);
+        const uint64_t total = rows * L.channel_stride;
+        const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255u) / 256u, 65536u);
+        hipLaunchKernelGGL(k44dev::k44_fill_uniform_kernel, dim3(std::max(1u, blocks)), dim3(256),
+                           0, ex->stream, ex->canvas.p + ex->plan_meta.input_off, rows,
+                           L.channel_stride, ex->plan_meta.input_w, (uint64_t)0, seed_mix);
+        K44_HIP(hipGetLastError());
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+int wavec_gpu_execute(void *h, int iters, float *out_ms_per_iter) {
+    if (!h || iters <= 0) return -1;
+    return guarded("wavec_gpu_execute", [&] {
+        k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+        if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+        K44_HIP(hipEventRecord(ex->ev0, ex->stream));
+        for (int i = 0; i < iters; ++i) ex->execute_plan();
+        K44_HIP(hipEventRecord(ex->ev1, ex->stream));
+        K44_HIP(hipEventSynchronize(ex->ev1));
+        float ms = 0.0f;
+        K44_HIP(hipEventElapsedTime(&ms, ex->ev0, ex->ev1));
+        if (out_ms_per_iter) *out_ms_per_iter = ms / (float)iters;
+        return 0;
+    });
+}
+
+int wavec_gpu_sync(void *h) {
+    if (!h) return -1;
+    return guarded("wavec_gpu_sync", [&] {
+        k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+        if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+int wavec_gpu_read_canvas(void *h, unsigned long long off, unsigned long long n, uint16_t *dst) {
+    if (!h || (!dst && n)) return -1;
+    return guarded("wavec_gpu_read_canvas", [&] {
+        k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+        if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+        if (off > ex->plan_meta.canvas_elems || n > ex->plan_meta.canvas_elems - off)
+            throw std::runtime_error("range outside the canvas");
+        K44_HIP(hipMemcpyAsync(dst, ex->canvas.p + off, n * 2u, hipMemcpyDeviceToHost, ex->stream));
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+int wavec_gpu_write_canvas(void *h, unsigned long long off, unsigned long long n,
+                           const uint16_t *src) {
+    if (!h || (!src && n)) return -1;
+    return guarded("wavec_gpu_write_canvas", [&] {
+        k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+        if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+        if (off > ex->plan_meta.canvas_elems || n > ex->plan_meta.canvas_elems - off)
+            throw std::runtime_error("range outside the canvas");
+        K44_HIP(hipMemcpyAsync(ex->canvas.p + off, src, n * 2u, hipMemcpyHostToDevice, ex->stream));
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+const char *wavec_gpu_exec_report_json(void *h) {
+    k44_host::K44GpuExecutorState *ex = h ? k44_host::find_exec(h) : nullptr;
+    return ex ? ex->report_json.c_str() : "{}";
+}
+
+}  // extern "C"

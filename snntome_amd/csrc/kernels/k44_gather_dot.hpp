@@ -1,0 +1,170 @@
+// k44_gather_dot.hpp — VALU gather-dot wave kernel for gfx950 (wave64).
+//
+// Computes one K44_WAVE command on a 1-D token canvas (semantics of the reference's
+// kernels/rocm/kernel44_rocm_pack.cuh:145-237, re-designed for CDNA4):
+//   v[j][m] = bias[j] + sum_k sum_s W[j][k*S+s] * X[seg[j/cluster][k] + s*step + m]
+//   y       = cmap ? act(v + r) : act(v) + r        (r = residual, 0 if none)
+//   Y[y_off + out_j*out_stride + m] = fp16_rne(y)
+// Used for waves whose neurons do not share index rows (per-neuron dendritic clusters): there
+// is no dense contraction to hand to MFMA, the wave is a batched GEMV streaming 2*M bytes per
+// gathered position, bound by HBM (or MALL/L2 when the substrate is cache resident).
+//
+// Mapping.  One wave64 = one neuron x one slab of SLAB tokens.  A position row of the slab is
+// SLAB*2 contiguous bytes; lane = (g, c) with c = 4-token chunk (8 bytes) and g = row group, so
+// one load instruction reads RPI = 256/SLAB rows of the segment, fully coalesced.  Rows are
+// consumed in batches of RPI*U: every lane issues U independent 8-byte loads before the first
+// FMA (U = 16/RPI loads in flight per lane), and one aligned vector load of the U weights it
+// needs — the host stores W in exactly this batch order ([j][k][batch][g][u], zero padded), so
+// weight traffic is one 8..32-byte load per lane per batch.  Row groups are reduced with
+// cross-lane shuffles at the end; group 0 runs the fused epilogue and stores 8 bytes per lane.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k44dev {
+
+enum : int { ACT_NONE = 0, ACT_RELU = 1, ACT_SIGMOID = 2, ACT_SILU = 3, ACT_LEAKY = 4, ACT_GELU = 5 };
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+    switch (act) {
+    case ACT_RELU: return fmaxf(v, 0.0f);
+    case ACT_SIGMOID: return 1.0f / (1.0f + __expf(-v));
+    case ACT_SILU: return v / (1.0f + __expf(-v));
+    case ACT_LEAKY: return fmaxf(v, 0.1f * v);
+    case ACT_GELU: return 0.5f * v * (1.0f + erff(v * 0.70710678f));
+    default: return v;
+    }
+}
+
+struct GatherDotArgs {
+    const __half *X;         // canvas base
+    const uint64_t *seg;     // [rows][K] canvas element offset of each segment start
+    const __half *W;         // [cout][K][n_batch][RPI][U] fp16, zero padded past S
+    const __half *bias;      // [cout] or nullptr
+    const uint16_t *cmap;    // [cout] or nullptr
+    __half *Y;               // canvas + y_off
+    const __half *R;         // canvas + res_off, or nullptr
+    uint64_t step;           // canvas elements between consecutive positions of a segment
+    uint32_t K, S, n_batch;  // segments per row, positions per segment, batches per segment
+    uint32_t cluster;        // neurons per index row
+    uint32_t cout;           // neurons (padded count)
+    uint32_t out_stride;     // canvas elements between consecutive output neurons
+    int act;
+};
+
+__device__ __forceinline__ void fma4(float (&acc)[4], float w, uint2 x) {
+    const __half2 lo = *reinterpret_cast<const __half2 *>(&x.x);
+    const __half2 hi = *reinterpret_cast<const __half2 *>(&x.y);
+    const float2 a = __half22float2(lo), b = __half22float2(hi);
+    acc[0] = fmaf(w, a.x, acc[0]);
+    acc[1] = fmaf(w, a.y, acc[1]);
+    acc[2] = fmaf(w, b.x, acc[2]);
+    acc[3] = fmaf(w, b.y, acc[3]);
+}
+
+template <int U>
+__device__ __forceinline__ void load_weights(float (&w)[U], const __half *p) {
+    if constexpr (U == 4) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        const __half *h = reinterpret_cast<const __half *>(&v);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = __half2float(h[u]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < U / 8; ++q) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(p + 8 * q);
+            const __half *h = reinterpret_cast<const __half *>(&v);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) w[8 * q + u] = __half2float(h[u]);
+        }
+    }
+}
+
+// SLAB in {64, 128, 256}: tokens per wave.  U = rows per lane per batch.
+template <int SLAB, int U>
+__global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
+    constexpr int LPR = SLAB / 4;  // lanes per position row
+    constexpr int RPI = 64 / LPR;  // rows per load instruction
+    const int lane = (int)(threadIdx.x & 63u);
+    const uint32_t j = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (j >= a.cout) return;  // wave-uniform
+    const int g = lane / LPR, c = lane % LPR;
+    const uint32_t slab0 = blockIdx.y * (uint32_t)SLAB;
+
+    const uint64_t *seg = a.seg + (uint64_t)(j / a.cluster) * a.K;
+    const uint64_t batches = (uint64_t)a.K * a.n_batch;
+    const __half *wl = a.W + (uint64_t)j * batches * (RPI * U) + g * U;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (uint32_t k = 0; k < a.K; ++k) {
+        const __half *xs = a.X + seg[k] + slab0 + 4u * (uint32_t)c;
+        for (uint32_t b = 0; b < a.n_batch; ++b) {
+            const uint32_t s0 = b * (uint32_t)(RPI * U) + (uint32_t)(g * U);
+            uint2 x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t s = s0 + (uint32_t)u;
+                x[u] = s < a.S ? *reinterpret_cast<const uint2 *>(xs + (uint64_t)s * a.step)
+                               : make_uint2(0u, 0u);
+            }
+            float w[U];
+            load_weights<U>(w, wl + ((uint64_t)k * a.n_batch + b) * (RPI * U));
+#pragma unroll
+            for (int u = 0; u < U; ++u) fma4(acc, w[u], x[u]);
+        }
+    }
+
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] += __shfl_xor(acc[t], off, 64);
+    if (g != 0) return;
+
+    const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
+    const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
+    const uint64_t o = oj * a.out_stride + slab0 + 4u * (uint32_t)c;
+    float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.R) {
+        const uint2 rv = *reinterpret_cast<const uint2 *>(a.R + o);
+        const __half *rh = reinterpret_cast<const __half *>(&rv);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) r[t] = __half2float(rh[t]);
+    }
+    __half out[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const float v = acc[t] + b;
+        const float y = a.cmap ? apply_act(v + r[t], a.act) : apply_act(v, a.act) + r[t];
+        out[t] = __float2half_rn(y);
+    }
+    *reinterpret_cast<uint2 *>(a.Y + o) = *reinterpret_cast<const uint2 *>(out);
+}
+
+// Synthetic substrate: X[pos][t] = fp16_rne((int32(h >> 40) - 2^23) * 2^-23) with
+// h = splitmix64(((pos << 20) | t) ^ splitmix64(seed)); tokens t >= valid are zero.
+__host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    uint64_t z = x + 0x9e3779b97f4a7c15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void k44_fill_uniform_kernel(__half *dst, uint64_t rows,
+                                                               uint32_t stride, uint32_t valid,
+                                                               uint64_t pos0, uint64_t seed_mix) {
+    const uint64_t total = rows * stride;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = i / stride;
+        const uint32_t t = (uint32_t)(i - r * stride);
+        float v = 0.0f;
+        if (t < valid) {
+            const uint64_t h = splitmix64((((pos0 + r) << 20) | t) ^ seed_mix);
+            v = (float)((int32_t)(h >> 40) - 8388608) * (1.0f / 8388608.0f);
+        }
+        dst[i] = __float2half_rn(v);
+    }
+}
+
+}  // namespace k44dev

@@ -1,0 +1,127 @@
+"""GPU parity of the wave kernels through the C ABI (libk44wavec.so) against the fp64 oracle.
+
+Tolerance (north_star): max |y - ref| / (|ref| + 1e-2) <= 2e-3, y = fp16 output of the GPU,
+ref = fp64 accumulation over the same fp16 operands (oracle/wave_oracle.c:orc_wave_f64).
+"""
+import numpy as np
+import pytest
+
+from snntome_amd import synth
+
+from wave_cases import TOL, cluster_rows, random_rows, run_sparse_case, stride_of
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def test_config1_full_wave(wavec, orc):
+    """Config 1 (plumbing) at full size: 4,096 neurons x 8 clusters x S=64, batch 64."""
+    wl = synth.config1(seed=1)
+    w = wl.waves[0]
+    _log(f"[c1] {wl.description}")
+    y, ref, plan = run_sparse_case(wavec, orc, C=wl.substrate, tokens=wl.tokens,
+                                   rows=cluster_rows(w.starts, w.S), weights=w.weights,
+                                   bias=w.bias, act=w.act, seed=wl.seed)
+    rep = plan.exec_report()["waves"][0]
+    assert rep["path"] == "valu_gather_dot"
+    assert (rep["K"], rep["S"]) == (8, 64)  # the upload recovered the dendritic segments
+    err = orc.rel_err(y, ref)
+    _log(f"[c1] rel err {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("tokens", [64, 128, 256, 320, 512, 100])
+@pytest.mark.parametrize("act", ["none", "relu", "sigmoid", "silu", "leaky_relu", "gelu"])
+def test_activation_and_slab_shapes(wavec, orc, tokens, act):
+    """Every activation x every slab width (64/128/256 and ragged token counts)."""
+    acts = ["none", "relu", "sigmoid", "silu", "leaky_relu", "gelu"]
+    rng = np.random.default_rng(tokens * 16 + acts.index(act))
+    C, cout, K, S = 3000, 48, 3, 24
+    starts = rng.integers(0, C - S, size=(cout, K)).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.1)
+    b = synth.normal_f16(rng, (cout,), 0.1)
+    y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens, rows=cluster_rows(starts, S),
+                                   weights=w, bias=b, act=act, seed=5)
+    assert plan.exec_report()["waves"][0]["S"] == S
+    assert orc.rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("fan", [1, 7, 33, 64])
+def test_generic_gather_rows(wavec, orc, fan):
+    """Arbitrary (non-contiguous) index rows: every synapse its own segment (S = 1)."""
+    rng = np.random.default_rng(fan)
+    C, cout, tokens = 5000, 40, 128
+    rows = random_rows(rng, cout, fan, C)
+    w = synth.normal_f16(rng, (cout, fan), 0.2)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens, rows=rows, weights=w, bias=b,
+                                   act="relu", seed=9)
+    assert orc.rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("cluster", [2, 16, 64])
+def test_shared_rows_and_residual(wavec, orc, cluster):
+    """Neurons sharing index rows (cluster > 1) with a residual add (y = act(v) + r)."""
+    rng = np.random.default_rng(cluster)
+    C, cout, K, S, tokens = 4096, 128, 4, 32, 256
+    starts = rng.integers(0, C - S, size=(cout // cluster, K)).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
+                                   rows=cluster_rows(starts, S), weights=w, bias=b,
+                                   cluster=cluster, act="silu", residual=True, seed=3)
+    assert orc.rel_err(y, ref) <= TOL
+
+
+def test_infer_f32_host_roundtrip(wavec, orc):
+    """The reference entry point wavec_gpu_infer_f32: host fp32 input -> fp32 output."""
+    rng = np.random.default_rng(0)
+    C, cout, K, S, tokens = 1024, 64, 2, 16, 96
+    starts = rng.integers(0, C - S, size=(cout, K)).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.1)
+    b = synth.normal_f16(rng, (cout,), 0.1)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", C, 1, tokens, is_1d=True)
+    g.add_cluster_wave("w0", "x", "y", starts, S, w, b, act="relu")
+    plan = g.compile()
+    x = rng.uniform(-1, 1, size=(C, 1, tokens)).astype(np.float32)
+    out, ms = plan.infer_f32(x)
+    assert out.shape == (cout, 1, tokens)
+    st = stride_of(tokens)
+    xs = np.zeros((C, st), np.float16)
+    xs[:, :tokens] = x[:, 0, :].astype(np.float16)
+    seg = (starts.astype(np.uint64) * st).reshape(-1)
+    ref = orc.wave_f64(xs.view(np.uint16).ravel(), seg, w, b, None, K, S, 1, st, st, st, "relu")
+    assert orc.rel_err(out[:, 0, :], ref[:, :tokens]) <= TOL
+
+
+def test_tcff_roundtrip_on_gpu(wavec, orc, tmp_path):
+    """Save a plan, load its weights into a freshly compiled plan, run both: identical bits."""
+    rng = np.random.default_rng(1)
+    C, cout, K, S, tokens = 2048, 96, 4, 16, 128
+    starts = rng.integers(0, C - S, size=(cout, K)).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.1)
+    b = synth.normal_f16(rng, (cout,), 0.1)
+
+    def make(weights):
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("x", C, 1, tokens, is_1d=True)
+        g.add_cluster_wave("w0", "x", "y", starts, S, weights, b, act="gelu")
+        return g, g.compile()
+
+    g1, p1 = make(w)
+    path = tmp_path / "plan.tcff"
+    p1.save_tcff(path)
+    g2, p2 = make(np.zeros_like(w))
+    p2.load_tcff_weights(path)
+    outs = []
+    for p in (p1, p2):
+        p.init_gpu()
+        p.fill_input_uniform(21)
+        p.execute(1)
+        cmd = p.cmds[0]
+        outs.append(p.read_canvas(int(cmd["y_off"]), cout * stride_of(tokens)))
+    assert np.array_equal(outs[0], outs[1])
