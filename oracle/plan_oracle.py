@@ -1,0 +1,431 @@
+"""Pure-Python restatement of the wave-plan compiler and the TCFF v1.0 writer —
+TEST INFRASTRUCTURE ONLY (used by tests/ to check libk44wavec.so's plans and .tcff bytes).
+
+Scope: 1-D token graphs — Input, linear (1x1 Convolution), the build's sparse waves,
+Concat / Split / Slice views, RMSNorm / SwiGLU nodes (they take canvas space) — i.e. every
+graph a 1-D wave plan is built from.  Restated from the reference's documented behaviour:
+  res descriptors        wavec/k44_plan_types.hpp:491-516 (1-D mode)
+  cluster size           wavec/k44_plan_types.hpp:157-186, 328-343
+  WMMA weight order      wavec/k44_plan_types.hpp:363-375
+  passes 1, 3, 4, 5      wavec/k44_wave_compiler.hpp:78-223, 315-366, 388-593, 824-988
+  dense 1-D waves        wavec/k44_wave_compiler.hpp:692-807
+  pack_wave_buffers      wavec/k44_wave_compiler.hpp:1031-1076
+  .tcff writer           wavec/k44_tcff_io.hpp:100-300
+The sparse-wave emission and the 0x8445 extension tag follow this build's specification
+(include/k44wavec.h, snntome_amd/csrc/k44_tcff_io.hpp).
+"""
+import math
+import struct
+
+import numpy as np
+
+ACT_NAMES = ["NONE", "RELU", "SIGMOID", "SILU", "LEAKY_RELU", "GELU"]
+
+
+def fnv1a64(data: bytes) -> int:
+    h = 0xCBF29CE484222325
+    for b in data:
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def fnv1a64_np(data: bytes) -> int:
+    # Same function, chunked through python ints for large blocks (speed only).
+    return fnv1a64(data)
+
+
+def round_up_16(v):
+    return max(16, (v + 15) & ~15)
+
+
+def round_up_32(v):
+    return max(64, (v + 31) & ~31)
+
+
+def choose_cluster_size(cout, num_tiles, force=0):
+    s = force
+    while s >= 16:
+        if cout % s == 0:
+            return s
+        s >>= 1
+    if cout % 128 == 0 and (cout >= 640 or num_tiles <= 64):
+        return 128
+    if cout % 64 == 0:
+        return 64
+    if cout % 32 == 0:
+        return 32
+    return 16
+
+
+def res_key_1d(w):
+    return 0x80000000 | w
+
+
+class Layout1D:
+    def __init__(self, w):
+        self.W = w
+        self.tiles = (w + 63) // 64
+        self.channel_stride = self.tiles * 64
+        self.W_pad = self.channel_stride
+        self.num_tiles = self.tiles
+
+
+def to_wmma(w_rows: np.ndarray) -> np.ndarray:
+    """[Cout][B] fp16 bits -> WMMA block order (flat uint16)."""
+    cout, B = w_rows.shape
+    out = np.empty(cout * B, dtype=np.uint16)
+    g = 0
+    for rb in range(cout // 16):
+        for kb in range(B // 16):
+            for l in range(32):
+                r = 16 * rb + (l & 15)
+                c = 16 * kb + 8 * (l >> 4)
+                out[8 * g:8 * g + 8] = w_rows[r, c:c + 8]
+                g += 1
+    return out
+
+
+class Node:
+    def __init__(self, op, name, ins=(), outs=(), **kw):
+        self.op, self.name = op, name
+        self.ins, self.outs = list(ins), list(outs)
+        self.cin = kw.get("cin", 0)
+        self.cout = kw.get("cout", 0)
+        self.h_in = self.w_in = self.h_out = self.w_out = 0
+        self.is_1d = kw.get("is_1d", False)
+        self.act = kw.get("act", 0)
+        self.residual = kw.get("residual", "")
+        self.weights = kw.get("weights")  # fp16 bits [cout][fan]
+        self.bias = kw.get("bias")  # fp16 bits [cout]
+        self.rows = kw.get("rows")  # sparse: [cout/cluster][fan] channel ids
+        self.cluster = kw.get("cluster", 1)
+        self.seg_len = kw.get("seg_len", 0)
+        self.slice_sizes = kw.get("slice_sizes", [])
+
+
+class Graph:
+    def __init__(self, force_cluster_size=0, batch_size=1):
+        self.nodes = []
+        self.output = "out0"
+        self.force = force_cluster_size
+        self.batch = batch_size
+
+    def _add(self, n, set_out=True):
+        if set_out and n.outs:
+            self.output = n.outs[0]
+        self.nodes.append(n)
+
+    def input(self, name, c, h, w, is_1d):
+        n = Node("Input", name, outs=[name], cin=c, cout=c)
+        n.h_in = n.h_out = h
+        n.w_in = n.w_out = w
+        n.is_1d = is_1d or (h == 1 and (w < 4 or w % 4 != 0))
+        self._add(n)
+
+    def linear(self, name, i, o, din, dout, w_bits, b_bits, act=0, residual=""):
+        self._add(Node("Convolution", name, [i], [o], cin=din, cout=dout, weights=w_bits,
+                       bias=b_bits, act=act, residual=residual))
+
+    def sparse(self, name, i, o, rows, w_bits, b_bits, cluster=1, act=0, residual="",
+               seg_len=0):
+        cout = w_bits.shape[0]
+        self._add(Node("SparseWave", name, [i], [o], cout=cout, weights=w_bits, bias=b_bits,
+                       rows=rows, cluster=cluster, act=act, residual=residual,
+                       seg_len=seg_len))
+
+    def concat(self, name, ins, o):
+        self._add(Node("Concat", name, ins, [o]))
+
+    def split(self, name, i, outs):
+        self._add(Node("Split", name, [i], outs), set_out=False)
+
+    def slice(self, name, i, outs, sizes):
+        self._add(Node("Slice", name, [i], outs, slice_sizes=list(sizes)), set_out=False)
+
+    def rmsnorm(self, name, i, o, dim):
+        self._add(Node("RMSNorm", name, [i], [o], cin=dim, cout=dim))
+
+    def swiglu(self, name, g, u, o):
+        self._add(Node("SwiGLU", name, [g, u], [o]))
+
+
+def compile_plan(g: Graph) -> dict:
+    nodes = g.nodes
+    if nodes and nodes[0].op == "Input" and nodes[0].is_1d and g.batch > 1 and nodes[0].w_out == 1:
+        nodes[0].w_in = nodes[0].w_out = g.batch
+    shapes = {}
+    for n in nodes:  # pass 1 (1-D subset)
+        if n.op == "Input":
+            assert n.is_1d
+            shapes[n.outs[0]] = (n.cout, n.h_out, n.w_out)
+            plan_in = (n.cout, n.h_out, n.w_out)
+        elif n.op in ("Convolution", "SparseWave"):
+            c, h, w = shapes[n.ins[0]]
+            if n.op == "SparseWave":
+                n.cin = c
+            n.h_in, n.w_in, n.h_out, n.w_out = h, w, 1, w
+            shapes[n.outs[0]] = (n.cout, 1, w)
+        elif n.op == "Concat":
+            c0, h, w = shapes[n.ins[0]]
+            shapes[n.outs[0]] = (sum(shapes[t][0] for t in n.ins), h, w)
+        elif n.op == "Split":
+            for o in n.outs:
+                shapes[o] = shapes[n.ins[0]]
+        elif n.op == "Slice":
+            c, h, w = shapes[n.ins[0]]
+            for k, o in enumerate(n.outs):
+                cc = n.slice_sizes[k] if n.slice_sizes else c // len(n.outs)
+                shapes[o] = (cc, h, w)
+        elif n.op in ("RMSNorm", "SwiGLU"):
+            c, h, w = shapes[n.ins[0]]
+            n.h_in = n.h_out = h
+            n.w_in = n.w_out = w
+            if n.op == "SwiGLU":
+                n.cin = n.cout = c
+            shapes[n.outs[0]] = (c, h, w)
+    # pass 3: one layout per token width; wave configs
+    res = {}
+    for t in sorted(shapes):
+        c, h, w = shapes[t]
+        res.setdefault(res_key_1d(w), Layout1D(w))
+    cfg = {}
+    for i, n in enumerate(nodes):
+        if n.op == "Convolution":
+            cp = round_up_16(n.cout)
+            tiles = max(1, res[res_key_1d(n.w_out)].num_tiles)
+            cfg[i] = (choose_cluster_size(cp, tiles, g.force), cp)
+        elif n.op == "SparseWave":
+            lcm = 16 * n.cluster // math.gcd(16, n.cluster)
+            cfg[i] = (n.cluster, (n.cout + lcm - 1) // lcm * lcm)
+    # pass 4: allocation ids, liveness, best-fit placement
+    ids, allocs, out_aid = {}, {}, {}
+    nxt = 0
+    for i, n in enumerate(nodes):
+        if n.op in ("Split", "Slice"):
+            for o in n.outs:
+                ids[o] = set(ids[n.ins[0]])
+        elif n.op == "Concat":
+            ids[n.outs[0]] = set().union(*[ids[t] for t in n.ins])
+        else:
+            ch = cfg[i][1] if n.op in ("Convolution", "SparseWave") else n.cout
+            allocs[nxt] = [res_key_1d(n.w_out), ch, 0]
+            ids[n.outs[0]] = {nxt}
+            out_aid[i] = nxt
+            nxt += 1
+    last = {0: len(nodes)}
+    for a in ids.get(g.output, ()):
+        last[a] = len(nodes)
+    for i, n in enumerate(nodes):
+        for t in n.ins + ([n.residual] if n.residual else []):
+            for a in ids.get(t, ()):
+                last[a] = max(last.get(a, 0), i)
+    free, peak, placed, live = [], 0, {}, []
+    for i, n in enumerate(nodes):
+        if i in out_aid:
+            a = out_aid[i]
+            key, ch, _ = allocs[a]
+            need = (ch * res[key].channel_stride + 63) // 64 * 64
+            fits = [k for k, f in enumerate(free) if f[1] >= need]
+            if fits:
+                k = min(fits, key=lambda q: (free[q][1], q))
+                at = free[k][0]
+                if free[k][1] == need:
+                    free.pop(k)
+                else:
+                    free[k] = (free[k][0] + need, free[k][1] - need)
+            elif free and free[-1][0] + free[-1][1] == peak:
+                at = free.pop()[0]
+                peak = at + need
+            else:
+                at = peak
+                peak += need
+            placed[a] = (at, need)
+            allocs[a][2] = at
+            live.append(a)
+        gone = sorted(a for a in live if last.get(a, 0) <= i)
+        for a in gone:
+            live.remove(a)
+            free.append(placed[a])
+        if gone and len(free) > 1:
+            free.sort()
+            merged = []
+            for f in free:
+                if merged and merged[-1][0] + merged[-1][1] == f[0]:
+                    merged[-1] = (merged[-1][0], merged[-1][1] + f[1])
+                else:
+                    merged.append(f)
+            free = merged
+    canvas = (peak + 63) // 64 * 64
+    canvas = (canvas + 127) // 128 * 128 or 128
+    plan = {"canvas_elems": canvas, "input_off": allocs[0][2], "cmds": [], "res": res,
+            "total_w_bytes": 0, "total_idx_bytes": 0, "input": plan_in}
+    # pass 5
+    chan = {}
+    for i, n in enumerate(nodes):
+        if n.op == "Input":
+            key, ch, at = allocs[out_aid[i]]
+            chan[n.outs[0]] = [at + c * res[key].channel_stride for c in range(n.cout)]
+        elif n.op == "Split":
+            for o in n.outs:
+                chan[o] = list(chan[n.ins[0]])
+        elif n.op == "Slice":
+            src, at = chan[n.ins[0]], 0
+            for k, o in enumerate(n.outs):
+                ln = n.slice_sizes[k] if n.slice_sizes else len(src) // len(n.outs)
+                chan[o] = src[at:at + ln]
+                at += ln
+        elif n.op == "Concat":
+            chan[n.outs[0]] = [x for t in n.ins for x in chan[t]]
+        elif n.op in ("RMSNorm", "SwiGLU"):
+            key, ch, at = allocs[out_aid[i]]
+            chan[n.outs[0]] = [at + c * res[key].channel_stride for c in range(n.cout)]
+            plan["cmds"].append({"type": 7 if n.op == "RMSNorm" else 8, "name": n.name})
+        elif n.op in ("Convolution", "SparseWave"):
+            key, ch, dst = allocs[out_aid[i]]
+            Lo = res[key]
+            chan[n.outs[0]] = [dst + c * Lo.channel_stride for c in range(n.cout)]
+            in_chs = chan[n.ins[0]]
+            S_cl, cout_pad = cfg[i]
+            has_res = bool(n.residual)
+            res_off = chan[n.residual][0] if has_res else 0
+            if has_res:
+                end = res_off + cout_pad * Lo.channel_stride
+                if end > plan["canvas_elems"]:
+                    plan["canvas_elems"] = (end + 127) // 128 * 128
+            idx_mode, idx_stride = 0, 1
+            if n.op == "Convolution":
+                b_raw = n.cin
+                B = round_up_32(b_raw)
+                rows = cout_pad // S_cl
+                row = [in_chs[c] for c in range(n.cin)]
+                idx = np.zeros((rows, B), dtype=np.uint64)
+                idx[:, :b_raw] = np.asarray(row, dtype=np.uint64)[None, :]
+                log_c = min(cout_pad, n.cout)
+                seg_len = n.cin
+            else:
+                b_raw = n.weights.shape[1]
+                B = round_up_32(b_raw)
+                rows = cout_pad // n.cluster
+                offs = np.asarray(in_chs, dtype=np.uint64)[np.asarray(n.rows, dtype=np.int64)]
+                idx = np.zeros((rows, B), dtype=np.uint64)
+                if int(offs.max()) > 0xFFFFFFFF:
+                    idx_mode, idx_stride = 1, res[res_key_1d(n.w_in)].channel_stride
+                    idx[: n.rows.shape[0], :b_raw] = np.asarray(n.rows, dtype=np.uint64)
+                else:
+                    idx[: n.rows.shape[0], :b_raw] = offs
+                log_c = n.cout
+                seg_len = n.seg_len
+            w = np.zeros((cout_pad, B), dtype=np.uint16)
+            w[:log_c, :b_raw] = n.weights[:log_c]
+            bias = np.zeros(cout_pad, dtype=np.uint16)
+            bias[:log_c] = n.bias[:log_c]
+            x_base = 0
+            if idx_mode == 0:
+                real = idx[:, :b_raw]
+                if int(real.max()) >= 0x70000000:
+                    x_base = int(real.min()) & ~63
+                    idx[:, :b_raw] -= np.uint64(x_base)
+                    idx[:, b_raw:] = 0
+            else:
+                x_base = in_chs[0]
+            plan["total_w_bytes"] += cout_pad * B * 2
+            plan["total_idx_bytes"] += idx.size * 4 + cout_pad * 2
+            plan["cmds"].append({
+                "type": 0, "name": n.name, "Cin": n.cin, "Cout": cout_pad, "logical_Cout": log_c,
+                "cluster": S_cl, "B": B, "B_raw": b_raw, "act": n.act, "has_res": has_res,
+                "h_out": 1, "w_out": n.w_out, "src_off": in_chs[0], "y_off": dst,
+                "res_off": res_off, "x_base_off": x_base, "idx_mode": idx_mode,
+                "idx_stride": idx_stride, "seg_len": seg_len,
+                "idx": idx.astype(np.uint32), "w_rows": w, "bias": bias,
+                "out_stride": Lo.channel_stride,
+            })
+    out_c, out_h, out_w = shapes[g.output]
+    plan["output"] = (out_c, out_h, out_w)
+    plan["output_off"] = chan[g.output][0]
+    return plan
+
+
+def tcff_bytes(plan: dict, prefix="K44Model", include_geometry=True) -> bytes:
+    waves = [c for c in plan["cmds"] if c["type"] == 0]
+    A = 256
+    buf = bytearray()
+
+    def pad():
+        buf.extend(b"\0" * ((-len(buf)) % A))
+
+    buf += b"II" + struct.pack("<HI", 42, 0) + b"TCFFv1.0"
+    buf += struct.pack("<IIII", A, len(waves), (plan["canvas_elems"] * 2) & 0xFFFFFFFF, 1)
+    buf += struct.pack("<Q", fnv1a64(bytes(buf[8:32])))
+    pad()
+    link = 4
+    lo = lambda v: v & 0xFFFFFFFF
+    for wi, c in enumerate(waves):
+        start = len(buf)
+        w_off = len(buf)
+        wb = to_wmma(c["w_rows"]).tobytes()
+        buf += wb
+        pad()
+        i_off = len(buf)
+        ib = c["idx"].astype("<u4").tobytes()
+        buf += ib
+        pad()
+        b_off = len(buf)
+        bb = c["bias"].astype("<u2").tobytes()
+        buf += bb
+        pad()
+        end = len(buf)
+        h64 = fnv1a64(bytes(buf[start:end]))
+        ifd = len(buf)
+        struct.pack_into("<I", buf, link, ifd)
+        ext = (c["idx_mode"] != 0 or max(c["x_base_off"], c["src_off"], c["y_off"],
+                                         c["res_off"]) >= 1 << 32)
+        ntags = 21 + (1 if include_geometry else 0) + (1 if ext else 0)
+        base = ifd + 2 + 12 * ntags + 4
+        tail = bytearray()
+
+        def stash(data: bytes) -> int:
+            if len(tail) & 1:
+                tail.append(0)
+            at = base + len(tail)
+            tail.extend(data)
+            return at
+
+        u32s = lambda *v: struct.pack("<%dI" % len(v), *v)
+        act = ACT_NAMES[c["act"]]
+        page = "%s_Wave_%03u_%ux%u_S%u" % (prefix, wi, c["B"], c["Cout"], c["cluster"])
+        desc = ("TCFF %s Wave %u/%u | Cin=%u Cout=%u(log=%u) B=%u S=%u Act=%s Res=%d | "
+                "W=0x%x Idx=0x%x Bias=0x%x | FNV1a64=0x%016x" % (
+                    prefix, wi, len(waves), c["Cin"], c["Cout"], c["logical_Cout"], c["B"],
+                    c["cluster"], act, int(c["has_res"]), w_off, i_off, b_off, h64))
+        d_at = stash(desc.encode() + b"\0")
+        p_at = stash(page.encode() + b"\0")
+        r_at = stash(u32s(1, 1))
+        par_at = stash(u32s(c["Cin"], c["Cout"], c["B"], c["cluster"], 16, 3, c["act"],
+                            int(c["has_res"]), c["h_out"], c["w_out"]))
+        aux_at = stash(u32s(w_off, len(wb), i_off, len(ib), b_off, len(bb), lo(c["src_off"]),
+                            lo(c["y_off"]), start, end, lo(c["res_off"])))
+        h_at = stash(u32s(h64 & 0xFFFFFFFF, h64 >> 32))
+        tags = [(254, 4, 1, 2), (256, 4, 1, c["B"]), (257, 4, 1, c["Cout"]), (258, 3, 1, 16),
+                (259, 3, 1, 1), (262, 3, 1, 1), (266, 3, 1, 1), (270, 2, len(desc) + 1, d_at),
+                (273, 4, 1, w_off), (277, 3, 1, 1), (278, 4, 1, c["Cout"]), (279, 4, 1, len(wb)),
+                (282, 5, 1, r_at), (283, 5, 1, r_at), (285, 2, len(page) + 1, p_at),
+                (297, 3, 2, wi | (len(waves) << 16)), (339, 3, 1, 3), (0x8440, 4, 1, 0x45564157),
+                (0x8441, 4, 10, par_at), (0x8442, 4, 11, aux_at), (0x8443, 4, 2, h_at)]
+        if include_geometry:
+            toks = max(1, c["w_out"])
+            g_at = stash(u32s(2 if toks > 1 else 1, toks, c["logical_Cout"], 1, 1, 1,
+                              c["out_stride"], 1, 1, 0))
+            tags.append((0x8444, 4, 10, g_at))
+        if ext:
+            v = [c["idx_mode"], lo(c["idx_stride"]), c["idx_stride"] >> 32, lo(c["x_base_off"]),
+                 c["x_base_off"] >> 32, lo(c["src_off"]), c["src_off"] >> 32, lo(c["y_off"]),
+                 c["y_off"] >> 32, lo(c["res_off"]), c["res_off"] >> 32, c["seg_len"]]
+            tags.append((0x8445, 4, 12, stash(u32s(*v))))
+        buf += struct.pack("<H", len(tags))
+        for t in tags:
+            buf += struct.pack("<HHII", *t)
+        link = len(buf)
+        buf += struct.pack("<I", 0)
+        buf += tail
+        pad()
+    return bytes(buf)
