@@ -89,6 +89,20 @@ def cpu_baseline(wl, budget_s: float = 12.0, sample_neurons: int = 4096):
     }
 
 
+def copy_probe(gib: float):
+    """Plain device-to-device copy kernel of known size: the calibration run for the
+    FETCH_SIZE / WRITE_SIZE counters (reads and writes exactly n bytes per launch)."""
+    import torch
+
+    n = int(gib * (1 << 30))
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[copy-probe] 5 launches of a {n}-byte device copy")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -96,7 +110,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-gib", type=float, default=0.0,
+                    help="only run a plain device copy of this many GiB (PMC calibration)")
     args = ap.parse_args()
+    if args.copy_probe_gib > 0:
+        copy_probe(args.copy_probe_gib)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the wave shards by batch columns with no communication; see DESIGN.md)",

@@ -34,6 +34,8 @@ def lib():
         L = ctypes.CDLL(str(LIB))
         L.orc_f32_to_f16.restype = ctypes.c_uint16
         L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_f32bits_to_f16.restype = ctypes.c_uint16
+        L.orc_f32bits_to_f16.argtypes = [ctypes.c_uint32]
         L.orc_f16_to_f32.restype = ctypes.c_float
         L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.orc_bf16_to_f32.restype = ctypes.c_float
@@ -73,6 +75,10 @@ def _p(a, t):
 
 def f32_to_f16(x: float) -> int:
     return int(lib().orc_f32_to_f16(float(x)))
+
+
+def f32bits_to_f16(bits: int) -> int:
+    return int(lib().orc_f32bits_to_f16(int(bits)))
 
 
 def f16_to_f32(h: int) -> float:

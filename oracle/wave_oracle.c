@@ -72,6 +72,13 @@ uint16_t orc_f32_to_f16(float f) {
     return (uint16_t)(sign | q);
 }
 
+/* Same conversion taking the float's bit pattern (keeps signalling-NaN payloads intact). */
+uint16_t orc_f32bits_to_f16(uint32_t bits) {
+    float f;
+    memcpy(&f, &bits, 4);
+    return orc_f32_to_f16(f);
+}
+
 float orc_f16_to_f32(uint16_t h) {
     uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
     uint32_t e = (h >> 10) & 0x1fu;

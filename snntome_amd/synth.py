@@ -20,10 +20,11 @@ _M2 = np.uint64(0x94D049BB133111EB)
 
 def splitmix64(x) -> np.ndarray:
     """SplitMix64 output for state x (vectorised, wrapping uint64 arithmetic)."""
-    z = np.asarray(x, dtype=np.uint64) + _GOLDEN
-    z = (z ^ (z >> np.uint64(30))) * _M1
-    z = (z ^ (z >> np.uint64(27))) * _M2
-    return z ^ (z >> np.uint64(31))
+    with np.errstate(over="ignore"):
+        z = np.asarray(x, dtype=np.uint64) + _GOLDEN
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        return z ^ (z >> np.uint64(31))
 
 
 def substrate_rows(seed: int, positions, tokens: int, valid: Optional[int] = None) -> np.ndarray:
