@@ -150,7 +150,7 @@ def main():
     comp = sum(synth.compulsory_bytes(wl, w) for w in wl.waves)
     value = flops / (wall_ms * 1e-3) / 1e12
     achieved_gbs = comp / (ev_ms * 1e-3) / 1e9
-    kernel_key = "gather_dot_" + wl.name.split("_")[0]
+    kernel_key = rep["waves"][0]["path"] + "_" + wl.name.split("_")[0]
     traffic = traffic_from_profiles(kernel_key)
     w0 = wl.waves[0]
     out = {
@@ -187,6 +187,7 @@ def main():
             "traffic": traffic,
             "algorithmic_bytes": comp,
             "kernel_ms": round(ev_ms, 5),
+            "mfma_tflops_frac": round(flops / (ev_ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4),
         },
     }
     if not args.no_cpu:

@@ -27,20 +27,49 @@ HIPCC_FLAGS = [
 ]
 
 
+SOURCES = ["k44_wave_executor.hip", "kernels/k44_valu.hip", "kernels/k44_mfma_dispatch.hip",
+           "kernels/k44_mfma_nt16.hip", "kernels/k44_mfma_nt32.hip", "kernels/k44_mfma_nt64.hip",
+           "kernels/k44_mfma_nt128.hip"]
+BUILD_DIR = HERE / "_build"
+
+
+def _clean(stderr: str) -> str:
+    return "\n".join(l for l in stderr.splitlines() if "packed-fp32-ops" not in l)
+
+
 def build(verbose: bool = True) -> Path:
+    """Compiles every translation unit for gfx950 (in parallel) and links libk44wavec.so."""
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    BUILD_DIR.mkdir(exist_ok=True)
+    objs, procs = [], []
+    for src in SOURCES:
+        obj = BUILD_DIR / (Path(src).stem + ".o")
+        cmd = [hipcc, *[f for f in HIPCC_FLAGS if f != "-shared"], "-c", str(CSRC / src),
+               "-o", str(obj)]
+        if verbose:
+            print("[build]", " ".join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                            text=True)))
+        objs.append(obj)
+    failed = []
+    for src, p in procs:
+        _, err = p.communicate()
+        err = _clean(err)
+        if p.returncode != 0:
+            failed.append(src)
+            sys.stderr.write(err + "\n")
+        elif verbose and err.strip():
+            sys.stderr.write(err + "\n")
+    if failed:
+        raise RuntimeError(f"hipcc failed on {failed}")
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc, *HIPCC_FLAGS, str(CSRC / "k44_wave_executor.hip"), "-o", str(tmp)]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print("[build]", " ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "packed-fp32-ops"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
     if res.returncode != 0:
-        sys.stderr.write(err + "\n")
-        raise RuntimeError(f"hipcc failed ({res.returncode}) building {LIB.name}")
-    if verbose and err.strip():
-        sys.stderr.write(err + "\n")
+        sys.stderr.write(_clean(res.stderr) + "\n")
+        raise RuntimeError(f"hipcc link failed ({res.returncode}) for {LIB.name}")
     os.replace(tmp, LIB)
     return LIB
 

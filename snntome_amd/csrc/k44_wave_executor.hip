@@ -26,7 +26,7 @@
 
 #include "k44_wave_compiler.hpp"
 #include "k44wavec.h"
-#include "kernels/k44_gather_dot.hpp"
+#include "kernels/k44_launch.hpp"
 
 namespace {
 
@@ -75,8 +75,10 @@ struct DevBuf {
 // Device schedule of one K44_WAVE command.
 struct WaveExec {
     std::string name;
-    std::string path;      // "valu_gather_dot"
+    std::string path;      // "valu_gather_dot" | "mfma_tile"
     std::string why;
+    bool mfma = false;
+    uint32_t mt = 0, rows_per_stage = 32, ksteps = 0;  // MFMA tile: tokens, positions/stage
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
     uint64_t step = 1;
     uint32_t tokens = 0, out_stride = 0;
@@ -90,6 +92,11 @@ struct WaveExec {
     DevBuf<__half> w, bias;
     DevBuf<uint16_t> cmap;
 };
+
+uint32_t pick_mt(uint32_t tokens) {
+    for (uint32_t mt : {512u, 256u, 128u}) if (tokens % mt == 0u) return mt;
+    return 64u;
+}
 
 uint32_t pick_slab(uint32_t tokens) {
     if (tokens % 256u == 0u) return 256u;
@@ -239,26 +246,70 @@ struct K44GpuExecutorState {
             wx.unique_rows = wx.step ? covered / wx.step : 0;
         }
 
-        // VALU gather-dot schedule.
-        wx.path = "valu_gather_dot";
-        wx.why = "neurons do not share index rows (cluster < 16) or the segment run is shorter "
-                 "than one 32-deep MFMA K-step: no dense contraction, gather-bound";
-        wx.slab = pick_slab(wx.tokens);
-        const uint32_t rpi = 256u / wx.slab;
-        wx.U = 16u / rpi;
-        const uint32_t per_batch = rpi * wx.U;
-        wx.n_batch = (wx.S + per_batch - 1u) / per_batch;
-        std::vector<uint16_t> wk((size_t)c.Cout * wx.K * wx.n_batch * per_batch, 0u);
-        for (size_t j = 0; j < c.Cout; ++j)
-            for (uint32_t k = 0; k < wx.K; ++k)
-                for (uint32_t s = 0; s < wx.S; ++s) {
-                    const uint32_t b = s / per_batch, q = s % per_batch;  // q = g*U + u
-                    wk[((j * wx.K + k) * wx.n_batch + b) * per_batch + q] =
-                        wraw[j * c.B + (size_t)k * wx.S + s];
-                }
-        std::vector<__half> wh(wk.size());
-        std::memcpy(wh.data(), wk.data(), wk.size() * 2u);
-        wx.w.upload(wh);
+        // Path selection.  MFMA needs a real dense contraction: >= 16 neurons sharing every
+        // index row (tile NT in {16, 32, 64, 128}), segments of whole 32-deep K-steps and
+        // 16-byte aligned rows.  Everything else is a batched GEMV: VALU gather-dot.
+        const char *force = std::getenv("K44WAVEC_PATH");
+        bool aligned8 = wx.step % 8u == 0u;
+        for (uint64_t s0 : starts) aligned8 = aligned8 && s0 % 8u == 0u;
+        const uint32_t cl = c.cluster_size;
+        const bool nt_ok = cl == 16u || cl == 32u || cl == 64u || cl == 128u;
+        const bool mfma_ok = nt_ok && wx.S % 32u == 0u && aligned8 && wx.tokens % 64u == 0u;
+        wx.mfma = mfma_ok && !(force && std::string(force) == "valu");
+        if (force && std::string(force) == "mfma" && !mfma_ok)
+            throw std::runtime_error("wave '" + c.name + "': K44WAVEC_PATH=mfma but the wave has "
+                                     "no dense MFMA tiling (cluster/segment/alignment)");
+        if (wx.mfma) {
+            wx.path = "mfma_tile";
+            wx.why = "neurons share index rows in tiles of " + std::to_string(cl) +
+                     " and segments are whole 32-position K-steps: dense " + std::to_string(cl) +
+                     " x " + std::to_string(c.B_raw) + " x " + std::to_string(wx.tokens) +
+                     " contraction per tile on v_mfma_f32_16x16x32_f16";
+            wx.mt = pick_mt(wx.tokens);
+            wx.rows_per_stage = wx.S % 64u == 0u ? 64u : 32u;
+            wx.ksteps = c.B_raw / 32u;
+            const uint32_t nb = cl / 16u;
+            // A fragments: [tile][k-step][16-neuron block][lane][8]; lane l holds neuron
+            // 16*blk + (l & 15), positions 32*ks + 8*(l >> 4) .. +8 of the tile's index row.
+            std::vector<uint16_t> wf((size_t)c.Cout * c.B_raw);
+            for (size_t t = 0; t < rows; ++t)
+                for (uint32_t ks = 0; ks < wx.ksteps; ++ks)
+                    for (uint32_t b = 0; b < nb; ++b)
+                        for (uint32_t l = 0; l < 64u; ++l) {
+                            const size_t dst = (((t * wx.ksteps + ks) * nb + b) * 64u + l) * 8u;
+                            const size_t j = t * cl + 16u * b + (l & 15u);
+                            const size_t src = j * c.B + 32u * ks + 8u * (l >> 4);
+                            std::memcpy(&wf[dst], &wraw[src], 16);
+                        }
+            std::vector<__half> wh(wf.size());
+            std::memcpy(wh.data(), wf.data(), wf.size() * 2u);
+            wx.w.upload(wh);
+        } else {
+            wx.path = "valu_gather_dot";
+            wx.why = !nt_ok ? "neurons do not share index rows in tiles of 16..128 (cluster " +
+                                  std::to_string(cl) + "): no dense contraction, batched GEMV"
+                     : wx.S % 32u != 0u
+                         ? "segments of " + std::to_string(wx.S) +
+                               " positions do not fill 32-deep MFMA K-steps"
+                         : (force ? std::string("forced by K44WAVEC_PATH")
+                                  : std::string("segment rows not 16-byte aligned"));
+            wx.slab = pick_slab(wx.tokens);
+            const uint32_t rpi = 256u / wx.slab;
+            wx.U = 16u / rpi;
+            const uint32_t per_batch = rpi * wx.U;
+            wx.n_batch = (wx.S + per_batch - 1u) / per_batch;
+            std::vector<uint16_t> wk((size_t)c.Cout * wx.K * wx.n_batch * per_batch, 0u);
+            for (size_t j = 0; j < c.Cout; ++j)
+                for (uint32_t k = 0; k < wx.K; ++k)
+                    for (uint32_t s = 0; s < wx.S; ++s) {
+                        const uint32_t b = s / per_batch, q = s % per_batch;  // q = g*U + u
+                        wk[((j * wx.K + k) * wx.n_batch + b) * per_batch + q] =
+                            wraw[j * c.B + (size_t)k * wx.S + s];
+                    }
+            std::vector<__half> wh(wk.size());
+            std::memcpy(wh.data(), wk.data(), wk.size() * 2u);
+            wx.w.upload(wh);
+        }
         wx.seg.upload(starts);
         std::vector<__half> bh(c.Cout);
         for (size_t j = 0; j < c.Cout; ++j) {
@@ -313,7 +364,8 @@ struct K44GpuExecutorState {
             o << (i ? ", " : "") << "{\"name\": \"" << w.name << "\", \"path\": \"" << w.path
               << "\", \"why\": \"" << w.why << "\", \"cout\": " << w.cout << ", \"K\": " << w.K
               << ", \"S\": " << w.S << ", \"cluster\": " << w.cluster << ", \"step\": " << w.step
-              << ", \"tokens\": " << w.tokens << ", \"slab\": " << w.slab << ", \"U\": " << w.U
+              << ", \"tokens\": " << w.tokens << ", \"slab\": " << (w.mfma ? w.mt : w.slab)
+              << ", \"U\": " << (w.mfma ? w.rows_per_stage : w.U)
               << ", \"flops\": " << (long long)w.flops << ", \"unique_rows\": " << w.unique_rows
               << ", \"y_off\": " << w.y_off << "}";
         }
@@ -321,7 +373,30 @@ struct K44GpuExecutorState {
         report_json = o.str();
     }
 
+    void launch_mfma(const WaveExec &w) {
+        k44dev::MfmaTileArgs a{};
+        a.X = canvas.p;
+        a.seg = w.seg.p;
+        a.Wf = w.w.p;
+        a.bias = w.bias.p;
+        a.cmap = w.cmap.p;
+        a.Y = canvas.p + w.y_off;
+        a.R = w.has_res ? canvas.p + w.res_off : nullptr;
+        a.step = w.step;
+        a.K = w.K;
+        a.S = w.S;
+        a.ksteps = w.ksteps;
+        a.out_stride = w.out_stride;
+        a.act = w.act;
+        K44_HIP(k44dev::launch_mfma_tile(a, w.cluster, w.mt, w.rows_per_stage, w.rows, w.tokens,
+                                         stream));
+    }
+
     void launch_wave(const WaveExec &w) {
+        if (w.mfma) {
+            launch_mfma(w);
+            return;
+        }
         k44dev::GatherDotArgs a{};
         a.X = canvas.p;
         a.seg = w.seg.p;
@@ -338,13 +413,7 @@ struct K44GpuExecutorState {
         a.cout = w.cout;
         a.out_stride = w.out_stride;
         a.act = w.act;
-        const dim3 grid((w.cout + 3u) / 4u, w.tokens / w.slab, 1u), block(256u, 1u, 1u);
-        switch (w.slab) {
-        case 256u: hipLaunchKernelGGL((k44dev::k44_gather_dot_kernel<256, 16>), grid, block, 0, stream, a); break;
-        case 128u: hipLaunchKernelGGL((k44dev::k44_gather_dot_kernel<128, 8>), grid, block, 0, stream, a); break;
-        default: hipLaunchKernelGGL((k44dev::k44_gather_dot_kernel<64, 4>), grid, block, 0, stream, a); break;
-        }
-        K44_HIP(hipGetLastError());
+        K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.tokens, stream));
     }
 
     void execute_plan() {
@@ -756,13 +825,9 @@ int wavec_gpu_fill_input_uniform(void *h, unsigned long long seed) {
         const auto &L = ex->layout(ex->plan_meta.input_res_key);
         if (!L.is_1d_tokens) throw std::runtime_error("2-D input layouts are not supported");
         const uint64_t rows = ex->plan_meta.input_c;
-        const uint64_t seed_mix = k44dev::splitmix64((uint64_t)seed);
-        const uint64_t total = rows * L.channel_stride;
-        const uint32_t blocks = (uint32_t)std::min<uint64_t>((total + 255u) / 256u, 65536u);
-        hipLaunchKernelGGL(k44dev::k44_fill_uniform_kernel, dim3(std::max(1u, blocks)), dim3(256),
-                           0, ex->stream, ex->canvas.p + ex->plan_meta.input_off, rows,
-                           L.channel_stride, ex->plan_meta.input_w, (uint64_t)0, seed_mix);
-        K44_HIP(hipGetLastError());
+        K44_HIP(k44dev::launch_fill_uniform(ex->canvas.p + ex->plan_meta.input_off, rows,
+                                            L.channel_stride, ex->plan_meta.input_w, 0u,
+                                            (uint64_t)seed, ex->stream));
         K44_HIP(hipStreamSynchronize(ex->stream));
         return 0;
     });

@@ -150,21 +150,4 @@ __host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
     return z ^ (z >> 31);
 }
 
-__global__ __launch_bounds__(256) void k44_fill_uniform_kernel(__half *dst, uint64_t rows,
-                                                               uint32_t stride, uint32_t valid,
-                                                               uint64_t pos0, uint64_t seed_mix) {
-    const uint64_t total = rows * stride;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t r = i / stride;
-        const uint32_t t = (uint32_t)(i - r * stride);
-        float v = 0.0f;
-        if (t < valid) {
-            const uint64_t h = splitmix64((((pos0 + r) << 20) | t) ^ seed_mix);
-            v = (float)((int32_t)(h >> 40) - 8388608) * (1.0f / 8388608.0f);
-        }
-        dst[i] = __float2half_rn(v);
-    }
-}
-
 }  // namespace k44dev

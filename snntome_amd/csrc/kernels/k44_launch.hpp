@@ -1,0 +1,26 @@
+// k44_launch.hpp — host-side launchers of the wave kernels (one translation unit per kernel
+// family, compiled in parallel; see kernels/*.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "k44_gather_dot.hpp"
+#include "k44_mfma_tile.hpp"
+
+namespace k44dev {
+
+// VALU gather-dot over `cout` neurons x `tokens` tokens with the given slab (64/128/256).
+hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t tokens,
+                             hipStream_t stream);
+
+// MFMA tile kernel: grid (tiles, tokens / mt), block mt; nt in {16,32,64,128},
+// mt in {64,128,256,512}, rows_per_stage in {32,64}.
+hipError_t launch_mfma_tile(const MfmaTileArgs &a, uint32_t nt, uint32_t mt,
+                            uint32_t rows_per_stage, uint32_t tiles, uint32_t tokens,
+                            hipStream_t stream);
+
+// Synthetic substrate fill (see k44_fill_uniform_kernel).
+hipError_t launch_fill_uniform(__half *dst, uint64_t rows, uint32_t stride, uint32_t valid,
+                               uint64_t pos0, uint64_t seed, hipStream_t stream);
+
+}  // namespace k44dev

@@ -1,0 +1,28 @@
+// Translation unit of the MFMA tile kernel for 64-neuron tiles.
+#include "k44_launch.hpp"
+
+namespace k44dev {
+
+hipError_t launch_mfma_tile_nt64(const MfmaTileArgs &a, uint32_t mt, uint32_t rows_per_stage,
+                                 uint32_t tiles, uint32_t tokens, hipStream_t stream) {
+    const dim3 grid(tiles, tokens / mt, 1u), block(mt, 1u, 1u);
+#define K44_MFMA_CASE(MT)                                                                       \
+    case MT:                                                                                    \
+        if (rows_per_stage == 64u)                                                              \
+            hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 64>), grid, block, 0, stream, a); \
+        else                                                                                    \
+            hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 32>), grid, block, 0, stream, a); \
+        break;
+    switch (mt) {
+        K44_MFMA_CASE(512u)
+        K44_MFMA_CASE(256u)
+        K44_MFMA_CASE(128u)
+        K44_MFMA_CASE(64u)
+    default:
+        return hipErrorInvalidValue;
+    }
+#undef K44_MFMA_CASE
+    return hipGetLastError();
+}
+
+}  // namespace k44dev

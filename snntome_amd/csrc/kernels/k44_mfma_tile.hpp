@@ -1,0 +1,151 @@
+// k44_mfma_tile.hpp — MFMA dense-cluster wave kernel for gfx950.
+//
+// For waves whose neurons come in tiles of NT (16..128) that share one index row ("cluster"
+// in the reference's plan, k44_plan_types.hpp:167-186), and whose dendritic segments are
+// multiples of 32 positions: the tile is a dense contraction
+//     Y[NT neurons][M tokens] = W[NT][K*S] x X_gathered[K*S][M]
+// fed to v_mfma_f32_16x16x32_f16 (fp16 in, fp32 accumulate).
+//
+// Data path (one workgroup = one neuron tile x MT tokens, MT/64 waves):
+//  * X: each stage is ROWS consecutive substrate positions of one segment x MT tokens, read
+//    from HBM with 16-byte loads (a position row is token-contiguous on the canvas) into
+//    registers one stage ahead, then stored to LDS unchanged ([row][token], padded pitch).
+//    The B operand needs 8 consecutive positions for one token per lane; ds_read_b64_tr_b16
+//    delivers exactly that from the untransposed tile: lane 16g+4j+m reads row 8g+j (+4),
+//    tokens t0+4m..+3, and after the transpose lane 16g+i holds positions 8g..8g+3 (+4..+7)
+//    of token t0+i.  Two LDS buffers ping-pong; one barrier per stage.
+//  * W: pre-arranged at upload in MFMA A-fragment order ([tile][k-step][16-neuron block]
+//    [lane][8]), so each wave loads every A fragment with one coalesced 16-byte-per-lane load.
+//  * Each wave owns 64 tokens: NT/16 x 4 accumulator tiles of 16x16 fp32.
+//  * Epilogue fused: bias, activation, residual / cout_map, fp16 (RNE) store.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "k44_gather_dot.hpp"
+
+namespace k44dev {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef short s4_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 on an LDS address: 4 x 16-bit, transposed across each 16-lane group.
+__device__ __forceinline__ h4_t lds_read_tr16(const _Float16 *p) {
+    const s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4_t *)(p));
+    return __builtin_bit_cast(h4_t, v);
+}
+
+struct MfmaTileArgs {
+    const __half *X;       // canvas base
+    const uint64_t *seg;   // [rows][K] canvas element offset of each segment start
+    const __half *Wf;      // A-fragment ordered weights
+    const __half *bias;    // [cout] or nullptr
+    const uint16_t *cmap;  // [cout] or nullptr
+    __half *Y;             // canvas + y_off
+    const __half *R;       // canvas + res_off or nullptr
+    uint64_t step;         // canvas elements between consecutive positions of a segment
+    uint32_t K, S;         // segments per row, positions per segment (S % ROWS == 0)
+    uint32_t ksteps;       // K*S/32
+    uint32_t out_stride;
+    int act;
+};
+
+template <int NT, int MT, int ROWS>
+__global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
+    constexpr int NB = NT / 16;              // 16-neuron blocks per tile
+    constexpr int PITCH = MT + 16;           // LDS row pitch in halves (32-byte skew)
+    constexpr int CPR = MT / 8;              // 16-byte chunks per position row
+    constexpr int CPT = ROWS * CPR / MT;     // chunks per thread per stage (= ROWS / 8)
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2][ROWS][PITCH];
+
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tile = blockIdx.x;
+    const uint32_t tok0 = blockIdx.y * (uint32_t)MT;
+    const uint64_t *segr = a.seg + (uint64_t)tile * a.K;
+    const uint32_t stages = a.K * a.S / (uint32_t)ROWS;
+
+    uint4 regs[CPT];
+    auto load_stage = [&](uint32_t st) {
+        const uint32_t kk = st * (uint32_t)ROWS;
+        const uint32_t k = kk / a.S, s0 = kk - k * a.S;
+        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + tok0;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * MT, rr = c / CPR, col = (c % CPR) * 8;
+            regs[i] = *reinterpret_cast<const uint4 *>(base + (uint64_t)rr * a.step + col);
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * MT, rr = c / CPR, col = (c % CPR) * 8;
+            *reinterpret_cast<uint4 *>(&lds[buf][rr][col]) = regs[i];
+        }
+    };
+
+    f4_t acc[NB][4];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) acc[nb][tb] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int g = lane >> 4;
+    const int tr_row = 8 * g + ((lane & 15) >> 2);  // row read by this lane (first half)
+    const int tr_col = wave * 64 + 4 * (lane & 3);  // token column (+16 per token block)
+    const h8_t *wf = reinterpret_cast<const h8_t *>(a.Wf) +
+                     (uint64_t)tile * a.ksteps * NB * 64 + lane;
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (uint32_t st = 0; st < stages; ++st) {
+        const int buf = (int)(st & 1u);
+        if (st + 1 < stages) load_stage(st + 1);
+#pragma unroll
+        for (int sub = 0; sub < ROWS / 32; ++sub) {
+            const uint32_t ks = st * (ROWS / 32) + sub;
+            h8_t af[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) af[nb] = wf[((uint64_t)ks * NB + nb) * 64];
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const _Float16 *p = &lds[buf][sub * 32 + tr_row][tr_col + 16 * tb];
+                const h4_t lo = lds_read_tr16(p);
+                const h4_t hi = lds_read_tr16(p + 4 * PITCH);
+                const h8_t b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[nb], b, acc[nb][tb],
+                                                                         0, 0, 0);
+            }
+        }
+        if (st + 1 < stages) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds C[4g + i][lane & 15] of every 16x16 tile.
+    const uint32_t n_base = tile * (uint32_t)NT + 4u * (uint32_t)g;
+    const uint32_t t_base = tok0 + (uint32_t)wave * 64u + (uint32_t)(lane & 15);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t j = n_base + 16u * nb + (uint32_t)i;
+            const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
+            const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const uint64_t o = oj * a.out_stride + t_base + 16u * tb;
+                const float r = a.R ? __half2float(a.R[o]) : 0.0f;
+                const float v = acc[nb][tb][i] + b;
+                const float y = a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r;
+                a.Y[o] = __float2half_rn(y);
+            }
+        }
+}
+
+}  // namespace k44dev

@@ -1,0 +1,121 @@
+"""GPU parity of the MFMA dense-cluster path (k44_mfma_tile_kernel) against the fp64 oracle,
+and agreement with the VALU path on the same plans.  Tolerance as in test_gpu_wave.py."""
+import os
+
+import numpy as np
+import pytest
+
+from snntome_amd import synth
+
+from wave_cases import TOL, cluster_rows, run_sparse_case, sampled_parity, stride_of
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def test_config3_full_wave_sampled(wavec, orc):
+    """Config 3 at full size (1,048,576 x 512 substrate, 16,384 neurons, 64-neuron tiles of
+    16 x S=512 clusters, GELU) on the MFMA path; 6 tiles (384 neurons) checked exhaustively."""
+    wl = synth.config3()
+    _log(f"[c3] {wl.description}")
+    plan = synth.build_graph(wl, wavec).compile()
+    plan.init_gpu()
+    rep = plan.exec_report()["waves"][0]
+    _log(f"[c3] path={rep['path']} K={rep['K']} S={rep['S']} tile={rep['cluster']}")
+    assert rep["path"] == "mfma_tile" and (rep["K"], rep["S"]) == (16, 512)
+    plan.fill_input_uniform(wl.seed)
+    plan.execute(1)
+    tiles = [0, 1, 77, 128, 200, 255]
+    neurons = np.concatenate([np.arange(t * 64, (t + 1) * 64) for t in tiles])
+    y, ref = sampled_parity(orc, plan, wl, 0, neurons)
+    err = orc.rel_err(y, ref)
+    _log(f"[c3] rel err over {len(neurons)} neurons x 512 tokens: {err:.3e}")
+    assert err <= TOL
+
+
+def test_config3_mfma_matches_valu(wavec, orc):
+    """Same reduced config-3 plan on both paths: each within tolerance of the oracle."""
+    wl = synth.config3(neurons=512, substrate=65536, tokens=256)
+    outs = {}
+    for path in ("mfma", "valu"):
+        os.environ["K44WAVEC_PATH"] = path
+        try:
+            plan = synth.build_graph(wl, wavec).compile()
+            plan.init_gpu()
+        finally:
+            del os.environ["K44WAVEC_PATH"]
+        assert plan.exec_report()["waves"][0]["path"].startswith(path)
+        plan.fill_input_uniform(wl.seed)
+        plan.execute(1)
+        neurons = np.arange(512)
+        y, ref = sampled_parity(orc, plan, wl, 0, neurons)
+        assert orc.rel_err(y, ref) <= TOL
+        outs[path] = y
+    # both paths round the same fp32-ish sums to fp16: they agree to a few fp16 ulps
+    assert orc.rel_err(outs["mfma"], outs["valu"]) <= TOL
+
+
+@pytest.mark.parametrize("nt", [16, 32, 64, 128])
+@pytest.mark.parametrize("tokens", [64, 128, 256, 512, 192, 640])
+def test_mfma_tile_shapes(wavec, orc, nt, tokens):
+    """Every tile size x token tiling (incl. ragged 192/640 -> 64/128-token workgroups)."""
+    rng = np.random.default_rng(nt * 1000 + tokens)
+    C, tiles, K, S = 4096, 3, 2, 64
+    cout = tiles * nt
+    starts = (rng.integers(0, (C - S) // 8, size=(tiles, K)) * 8).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens, rows=cluster_rows(starts, S),
+                                   weights=w, bias=b, cluster=nt, act="gelu", seed=13)
+    rep = plan.exec_report()["waves"][0]
+    assert rep["path"] == "mfma_tile"
+    assert orc.rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("S", [32, 96, 128, 160])
+def test_mfma_segment_lengths_and_residual(wavec, orc, S):
+    """Segments of 32..160 positions (32- and 64-row stages) with a residual add."""
+    rng = np.random.default_rng(S)
+    C, nt, tiles, K, tokens = 8192, 64, 2, 3, 256
+    starts = (rng.integers(0, (C - S) // 8, size=(tiles, K)) * 8).astype(np.uint32)
+    w = synth.normal_f16(rng, (tiles * nt, K * S), 0.05)
+    b = synth.normal_f16(rng, (tiles * nt,), 0.05)
+    y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens, rows=cluster_rows(starts, S),
+                                   weights=w, bias=b, cluster=nt, act="relu", residual=True,
+                                   seed=17)
+    assert plan.exec_report()["waves"][0]["path"] == "mfma_tile"
+    assert orc.rel_err(y, ref) <= TOL
+
+
+def test_dense_linear_layer_takes_mfma(wavec, orc):
+    """A reference-style dense 1x1 linear layer (every index row = all input channels, one
+    contiguous segment) is tiled onto MFMA and matches the oracle."""
+    rng = np.random.default_rng(2)
+    din, dout, tokens = 512, 256, 128
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", din, 1, tokens, is_1d=True)
+    wt = (rng.standard_normal((dout, din)) * 0.05).astype(np.float32)
+    bs = (rng.standard_normal(dout) * 0.05).astype(np.float32)
+    g.add_linear("fc", "x", "y", din, dout, wt, bs, act="silu")
+    plan = g.compile()
+    plan.init_gpu()
+    rep = plan.exec_report()["waves"][0]
+    assert rep["path"] == "mfma_tile" and rep["K"] == 1 and rep["S"] == din
+    plan.fill_input_uniform(5)
+    plan.execute(1)
+    st = stride_of(tokens)
+    canvas = plan.read_canvas(0, int(plan.summary["canvas_elems"]))
+    cmd = plan.cmds[0]
+    x0 = int(cmd["src_off"])
+    rows = (x0 + np.arange(din, dtype=np.uint64) * st)
+    seg = np.tile(rows[:1], dout // int(rep["cluster"]))
+    w16 = wt.astype(np.float16)
+    b16 = bs.astype(np.float16)
+    ref = orc.wave_f64(canvas, seg, w16, b16, None, 1, din, int(rep["cluster"]), st, st, st,
+                       "silu")
+    y0 = int(cmd["y_off"])
+    y = canvas[y0:y0 + dout * st].view(np.float16).reshape(dout, st).astype(np.float64)
+    assert orc.rel_err(y, ref) <= TOL

@@ -48,3 +48,29 @@ def cluster_rows(starts: np.ndarray, S: int) -> np.ndarray:
     r, K = starts.shape
     return (starts[:, :, None].astype(np.int64) + np.arange(S)[None, None, :]).reshape(
         r, K * S).astype(np.uint32)
+
+
+def sampled_parity(orc, plan, wl, wave_idx, neurons, read_out=True):
+    """Oracle check of selected neurons of a workload wave whose input is the plan input 'x'
+    filled on the device with wl.seed: the oracle gathers from a compact host copy of exactly
+    the substrate rows those neurons read (host generator), the GPU rows are read back."""
+    w = wl.waves[wave_idx]
+    st = stride_of(wl.tokens)
+    neurons = np.asarray(neurons, dtype=np.int64)
+    rows = np.unique(neurons // w.cluster)
+    starts = w.starts[rows].astype(np.uint64)  # [len(rows), K]
+    compact = orc.fill_segments(wl.seed, starts.ravel(), w.S, wl.tokens, st)
+    # row r of `rows` -> its K segments are consecutive blocks of S rows in `compact`
+    seg = (np.arange(rows.size * w.K, dtype=np.uint64) * w.S * st)
+    remap = {int(r): i for i, r in enumerate(rows)}
+    sel_local = np.array([remap[int(j // w.cluster)] * w.cluster + int(j % w.cluster)
+                          for j in neurons], dtype=np.uint32)
+    # weights / bias of the selected rows' neurons, in local order
+    wl_idx = np.concatenate([np.arange(r * w.cluster, (r + 1) * w.cluster) for r in rows])
+    ref = orc.wave_f64(compact.ravel(), seg, w.weights[wl_idx], w.bias[wl_idx], None, w.K, w.S,
+                       w.cluster, st, st, st, w.act, sel=sel_local)
+    cmd = plan.cmds[wave_idx]
+    y0 = int(cmd["y_off"])
+    ys = np.stack([plan.read_canvas(y0 + int(j) * st, st) for j in neurons])
+    y = ys.view(np.float16).astype(np.float64)
+    return y, ref
