@@ -266,7 +266,7 @@ struct K44GpuExecutorState {
                      " x " + std::to_string(c.B_raw) + " x " + std::to_string(wx.tokens) +
                      " contraction per tile on v_mfma_f32_16x16x32_f16";
             wx.mt = pick_mt(wx.tokens);
-            wx.rows_per_stage = wx.S % 64u == 0u ? 64u : 32u;
+            wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
             wx.ksteps = c.B_raw / 32u;
             const uint32_t nb = cl / 16u;
             // A fragments: [tile][k-step][16-neuron block][lane][8]; lane l holds neuron

@@ -1,4 +1,5 @@
-// Translation unit of the MFMA tile kernel for 128-neuron tiles.
+// Translation unit of the MFMA tile kernel for 128-neuron tiles (32-position stages only: the
+// 64-position stage needs more than 256 registers per lane at 2 waves per SIMD).
 #include "k44_launch.hpp"
 
 namespace k44dev {
@@ -8,10 +9,8 @@ hipError_t launch_mfma_tile_nt128(const MfmaTileArgs &a, uint32_t mt, uint32_t r
     const dim3 grid(tiles, tokens / mt, 1u), block(mt, 1u, 1u);
 #define K44_MFMA_CASE(MT)                                                                       \
     case MT:                                                                                    \
-        if (rows_per_stage == 64u)                                                              \
-            hipLaunchKernelGGL((k44_mfma_tile_kernel<128, MT, 64>), grid, block, 0, stream, a); \
-        else                                                                                    \
-            hipLaunchKernelGGL((k44_mfma_tile_kernel<128, MT, 32>), grid, block, 0, stream, a); \
+        if (rows_per_stage != 32u) return hipErrorInvalidValue;                                 \
+        hipLaunchKernelGGL((k44_mfma_tile_kernel<128, MT, 32>), grid, block, 0, stream, a);     \
         break;
     switch (mt) {
         K44_MFMA_CASE(512u)

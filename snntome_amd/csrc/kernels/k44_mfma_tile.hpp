@@ -31,6 +31,7 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef short s4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u4_t __attribute__((ext_vector_type(4)));
 
 // ds_read_b64_tr_b16 on an LDS address: 4 x 16-bit, transposed across each 16-lane group.
 __device__ __forceinline__ h4_t lds_read_tr16(const _Float16 *p) {
@@ -68,25 +69,6 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
     const uint64_t *segr = a.seg + (uint64_t)tile * a.K;
     const uint32_t stages = a.K * a.S / (uint32_t)ROWS;
 
-    uint4 regs[CPT];
-    auto load_stage = [&](uint32_t st) {
-        const uint32_t kk = st * (uint32_t)ROWS;
-        const uint32_t k = kk / a.S, s0 = kk - k * a.S;
-        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + tok0;
-#pragma unroll
-        for (int i = 0; i < CPT; ++i) {
-            const int c = tid + i * MT, rr = c / CPR, col = (c % CPR) * 8;
-            regs[i] = *reinterpret_cast<const uint4 *>(base + (uint64_t)rr * a.step + col);
-        }
-    };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < CPT; ++i) {
-            const int c = tid + i * MT, rr = c / CPR, col = (c % CPR) * 8;
-            *reinterpret_cast<uint4 *>(&lds[buf][rr][col]) = regs[i];
-        }
-    };
-
     f4_t acc[NB][4];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -96,34 +78,78 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
     const int g = lane >> 4;
     const int tr_row = 8 * g + ((lane & 15) >> 2);  // row read by this lane (first half)
     const int tr_col = wave * 64 + 4 * (lane & 3);  // token column (+16 per token block)
+    constexpr int SUBS = ROWS / 32;                  // 32-deep MFMA K-steps per stage
     const h8_t *wf = reinterpret_cast<const h8_t *>(a.Wf) +
                      (uint64_t)tile * a.ksteps * NB * 64 + lane;
 
-    load_stage(0);
-    store_stage(0);
+    // Stage st covers index-row positions [st*ROWS, st*ROWS + ROWS) — inside one segment.
+    // Thread chunk i of a stage: row (tid + i*MT) / CPR, tokens ((tid + i*MT) % CPR) * 8 .. +8.
+    u4_t xr[CPT];  // X of the next stage, in flight during the current stage's MFMAs
+    h8_t wn[SUBS][NB], wc[SUBS][NB];  // A fragments: next stage (in flight), current stage
+    {
+        const __half *base = a.X + segr[0] + tok0;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * MT;
+            xr[i] = *reinterpret_cast<const u4_t *>(base + (uint64_t)(c / CPR) * a.step +
+                                                     (c % CPR) * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < SUBS; ++u)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) wc[u][nb] = wf[((uint64_t)u * NB + nb) * 64];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * MT;
+            *reinterpret_cast<u4_t *>(&lds[0][c / CPR][(c % CPR) * 8]) = xr[i];
+        }
+    }
     __syncthreads();
+
     for (uint32_t st = 0; st < stages; ++st) {
         const int buf = (int)(st & 1u);
-        if (st + 1 < stages) load_stage(st + 1);
+        const bool more = st + 1 < stages;
+        if (more) {  // issue next stage's X and W loads; consumed only after this stage's math
+            const uint32_t kk = (st + 1) * (uint32_t)ROWS;
+            const uint32_t k = kk / a.S, s0 = kk - k * a.S;
+            const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + tok0;
 #pragma unroll
-        for (int sub = 0; sub < ROWS / 32; ++sub) {
-            const uint32_t ks = st * (ROWS / 32) + sub;
-            h8_t af[NB];
+            for (int i = 0; i < CPT; ++i) {
+                const int c = tid + i * MT;
+                xr[i] = *reinterpret_cast<const u4_t *>(base + (uint64_t)(c / CPR) * a.step +
+                                                         (c % CPR) * 8);
+            }
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) af[nb] = wf[((uint64_t)ks * NB + nb) * 64];
+            for (int u = 0; u < SUBS; ++u)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    wn[u][nb] = wf[((uint64_t)((st + 1) * SUBS + u) * NB + nb) * 64];
+        }
+#pragma unroll
+        for (int u = 0; u < SUBS; ++u) {
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
-                const _Float16 *p = &lds[buf][sub * 32 + tr_row][tr_col + 16 * tb];
+                const _Float16 *p = &lds[buf][u * 32 + tr_row][tr_col + 16 * tb];
                 const h4_t lo = lds_read_tr16(p);
                 const h4_t hi = lds_read_tr16(p + 4 * PITCH);
                 const h8_t b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
-                    acc[nb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[nb], b, acc[nb][tb],
-                                                                         0, 0, 0);
+                    acc[nb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wc[u][nb], b,
+                                                                         acc[nb][tb], 0, 0, 0);
             }
         }
-        if (st + 1 < stages) store_stage(buf ^ 1);
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) {
+                const int c = tid + i * MT;
+                *reinterpret_cast<u4_t *>(&lds[buf ^ 1][c / CPR][(c % CPR) * 8]) = xr[i];
+            }
+#pragma unroll
+            for (int u = 0; u < SUBS; ++u)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) wc[u][nb] = wn[u][nb];
+        }
         __syncthreads();
     }
 
