@@ -82,7 +82,8 @@ struct WaveExec {
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
     uint64_t step = 1;
     uint32_t tokens = 0, out_stride = 0;
-    uint32_t slab = 256, U = 4, n_batch = 1;
+    uint32_t slab = 256, U = 4, n_batch = 1, ksplit = 1;
+    bool sorted_segments = false;
     uint64_t y_off = 0, res_off = 0;
     int act = 0;
     bool has_res = false;
@@ -201,6 +202,36 @@ struct K44GpuExecutorState {
                     throw std::runtime_error("wave '" + c.name +
                                              "': non-zero weight on a padded synapse");
 
+        // Address-sorted segments: every index row visits its segments in ascending canvas
+        // order (weight columns permuted with them; only the fp32 summation order changes), so
+        // concurrently running rows sweep the substrate together and overlapping segments of
+        // different rows are read close in time (cache reuse instead of a second HBM read).
+        const char *sort_env = std::getenv("K44WAVEC_SORT");
+        wx.sorted_segments = wx.K > 1u && !(sort_env && std::string(sort_env) == "0");
+        if (wx.sorted_segments) {
+            std::vector<uint32_t> order(wx.K);
+            std::vector<uint64_t> st(wx.K);
+            std::vector<uint16_t> row_w((size_t)c.B_raw);
+            for (size_t r = 0; r < rows; ++r) {
+                uint64_t *sr = starts.data() + r * wx.K;
+                for (uint32_t k = 0; k < wx.K; ++k) order[k] = k;
+                std::stable_sort(order.begin(), order.end(),
+                                 [&](uint32_t x, uint32_t y) { return sr[x] < sr[y]; });
+                bool identity = true;
+                for (uint32_t k = 0; k < wx.K; ++k) identity = identity && order[k] == k;
+                if (identity) continue;
+                for (uint32_t k = 0; k < wx.K; ++k) st[k] = sr[order[k]];
+                std::copy(st.begin(), st.end(), sr);
+                for (size_t j = r * c.cluster_size; j < (r + 1) * c.cluster_size; ++j) {
+                    uint16_t *wj = wraw.data() + j * c.B;
+                    for (uint32_t k = 0; k < wx.K; ++k)
+                        std::memcpy(&row_w[(size_t)k * wx.S], wj + (size_t)order[k] * wx.S,
+                                    wx.S * 2u);
+                    std::memcpy(wj, row_w.data(), (size_t)c.B_raw * 2u);
+                }
+            }
+        }
+
         // Host-side bounds check of every canvas element the kernel may touch.
         const uint64_t n_canvas = plan_meta.canvas_elems;
         uint64_t x_hi = 0;
@@ -294,6 +325,9 @@ struct K44GpuExecutorState {
                          : (force ? std::string("forced by K44WAVEC_PATH")
                                   : std::string("segment rows not 16-byte aligned"));
             wx.slab = pick_slab(wx.tokens);
+            const char *ks_env = std::getenv("K44WAVEC_KSPLIT");
+            wx.ksplit = (wx.K >= 2u && wx.K <= 8u) ? 4u : 1u;
+            if (ks_env) wx.ksplit = std::string(ks_env) == "4" ? 4u : 1u;
             const uint32_t rpi = 256u / wx.slab;
             wx.U = 16u / rpi;
             const uint32_t per_batch = rpi * wx.U;
@@ -365,7 +399,8 @@ struct K44GpuExecutorState {
               << "\", \"why\": \"" << w.why << "\", \"cout\": " << w.cout << ", \"K\": " << w.K
               << ", \"S\": " << w.S << ", \"cluster\": " << w.cluster << ", \"step\": " << w.step
               << ", \"tokens\": " << w.tokens << ", \"slab\": " << (w.mfma ? w.mt : w.slab)
-              << ", \"U\": " << (w.mfma ? w.rows_per_stage : w.U)
+              << ", \"U\": " << (w.mfma ? w.rows_per_stage : w.U) << ", \"ksplit\": " << w.ksplit
+              << ", \"sorted_segments\": " << (w.sorted_segments ? "true" : "false")
               << ", \"flops\": " << (long long)w.flops << ", \"unique_rows\": " << w.unique_rows
               << ", \"y_off\": " << w.y_off << "}";
         }
@@ -413,7 +448,7 @@ struct K44GpuExecutorState {
         a.cout = w.cout;
         a.out_stride = w.out_stride;
         a.act = w.act;
-        K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.tokens, stream));
+        K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream));
     }
 
     void execute_plan() {

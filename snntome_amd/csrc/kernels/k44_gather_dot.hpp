@@ -81,14 +81,21 @@ __device__ __forceinline__ void load_weights(float (&w)[U], const __half *p) {
     }
 }
 
+typedef unsigned int gd_u2 __attribute__((ext_vector_type(2)));
+
 // SLAB in {64, 128, 256}: tokens per wave.  U = rows per lane per batch.
-template <int SLAB, int U>
+// KSPLIT = 1: the 4 waves of a workgroup are 4 neurons.  KSPLIT = 4: the 4 waves share one
+// neuron and take its segments round-robin (k = wave, wave + 4, ...); partial sums meet in LDS.
+// Splitting keeps one short, fully parallel segment stream per wave when a neuron has only a
+// few segments (the ultra-sparse regime), instead of serialising K load-wait-FMA phases.
+template <int SLAB, int U, int KSPLIT>
 __global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
     constexpr int LPR = SLAB / 4;  // lanes per position row
     constexpr int RPI = 64 / LPR;  // rows per load instruction
     const int lane = (int)(threadIdx.x & 63u);
-    const uint32_t j = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (j >= a.cout) return;  // wave-uniform
+    const int wave = (int)(threadIdx.x >> 6);
+    const uint32_t j = KSPLIT == 1 ? blockIdx.x * 4u + (uint32_t)wave : blockIdx.x;
+    if (j >= a.cout) return;  // uniform per wave (KSPLIT == 1) or per workgroup (KSPLIT == 4)
     const int g = lane / LPR, c = lane % LPR;
     const uint32_t slab0 = blockIdx.y * (uint32_t)SLAB;
 
@@ -97,21 +104,21 @@ __global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
     const __half *wl = a.W + (uint64_t)j * batches * (RPI * U) + g * U;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (uint32_t k = 0; k < a.K; ++k) {
+    for (uint32_t k = KSPLIT == 1 ? 0u : (uint32_t)wave; k < a.K; k += KSPLIT) {
         const __half *xs = a.X + seg[k] + slab0 + 4u * (uint32_t)c;
         for (uint32_t b = 0; b < a.n_batch; ++b) {
             const uint32_t s0 = b * (uint32_t)(RPI * U) + (uint32_t)(g * U);
-            uint2 x[U];
+            gd_u2 x[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const uint32_t s = s0 + (uint32_t)u;
-                x[u] = s < a.S ? *reinterpret_cast<const uint2 *>(xs + (uint64_t)s * a.step)
-                               : make_uint2(0u, 0u);
+                x[u] = s < a.S ? *reinterpret_cast<const gd_u2 *>(xs + (uint64_t)s * a.step)
+                               : gd_u2{0u, 0u};
             }
             float w[U];
             load_weights<U>(w, wl + ((uint64_t)k * a.n_batch + b) * (RPI * U));
 #pragma unroll
-            for (int u = 0; u < U; ++u) fma4(acc, w[u], x[u]);
+            for (int u = 0; u < U; ++u) fma4(acc, w[u], make_uint2(x[u].x, x[u].y));
         }
     }
 
@@ -119,6 +126,22 @@ __global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
     for (int off = LPR; off < 64; off <<= 1)
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[t] += __shfl_xor(acc[t], off, 64);
+    if constexpr (KSPLIT > 1) {
+        __shared__ float part[KSPLIT][SLAB];
+        if (g == 0) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) part[wave][4 * c + t] = acc[t];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < KSPLIT; ++w2) v += part[w2][4 * c + t];
+            acc[t] = v;
+        }
+    }
     if (g != 0) return;
 
     const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
@@ -126,7 +149,7 @@ __global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
     const uint64_t o = oj * a.out_stride + slab0 + 4u * (uint32_t)c;
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.R) {
-        const uint2 rv = *reinterpret_cast<const uint2 *>(a.R + o);
+        const gd_u2 rv = *reinterpret_cast<const gd_u2 *>(a.R + o);
         const __half *rh = reinterpret_cast<const __half *>(&rv);
 #pragma unroll
         for (int t = 0; t < 4; ++t) r[t] = __half2float(rh[t]);
@@ -138,7 +161,7 @@ __global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
         const float y = a.cmap ? apply_act(v + r[t], a.act) : apply_act(v, a.act) + r[t];
         out[t] = __float2half_rn(y);
     }
-    *reinterpret_cast<uint2 *>(a.Y + o) = *reinterpret_cast<const uint2 *>(out);
+    *reinterpret_cast<gd_u2 *>(a.Y + o) = *reinterpret_cast<const gd_u2 *>(out);
 }
 
 // Synthetic substrate: X[pos][t] = fp16_rne((int32(h >> 40) - 2^23) * 2^-23) with

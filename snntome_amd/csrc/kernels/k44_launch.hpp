@@ -9,9 +9,10 @@
 
 namespace k44dev {
 
-// VALU gather-dot over `cout` neurons x `tokens` tokens with the given slab (64/128/256).
-hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t tokens,
-                             hipStream_t stream);
+// VALU gather-dot over `cout` neurons x `tokens` tokens with the given slab (64/128/256);
+// ksplit 4 = one neuron per workgroup, its segments split over the 4 waves.
+hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
+                             uint32_t tokens, hipStream_t stream);
 
 // MFMA tile kernel: grid (tiles, tokens / mt), block mt; nt in {16,32,64,128},
 // mt in {64,128,256,512}, rows_per_stage in {32,64}.

@@ -21,15 +21,22 @@ __global__ __launch_bounds__(256) void k44_fill_uniform_kernel(__half *dst, uint
 }
 
 
-hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t tokens,
-                             hipStream_t stream) {
-    const dim3 grid((a.cout + 3u) / 4u, tokens / slab, 1u), block(256u, 1u, 1u);
+hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
+                             uint32_t tokens, hipStream_t stream) {
+    const dim3 grid(ksplit == 4u ? a.cout : (a.cout + 3u) / 4u, tokens / slab, 1u);
+    const dim3 block(256u, 1u, 1u);
+#define K44_GD(SLAB, U)                                                                        \
+    if (ksplit == 4u)                                                                          \
+        hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 4>), grid, block, 0, stream, a);     \
+    else                                                                                       \
+        hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 1>), grid, block, 0, stream, a);
     switch (slab) {
-    case 256u: hipLaunchKernelGGL((k44_gather_dot_kernel<256, 16>), grid, block, 0, stream, a); break;
-    case 128u: hipLaunchKernelGGL((k44_gather_dot_kernel<128, 8>), grid, block, 0, stream, a); break;
-    case 64u: hipLaunchKernelGGL((k44_gather_dot_kernel<64, 4>), grid, block, 0, stream, a); break;
+    case 256u: K44_GD(256, 16) break;
+    case 128u: K44_GD(128, 8) break;
+    case 64u: K44_GD(64, 4) break;
     default: return hipErrorInvalidValue;
     }
+#undef K44_GD
     return hipGetLastError();
 }
 
