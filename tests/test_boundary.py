@@ -1,0 +1,104 @@
+"""The C-ABI boundary: libk44wavec.so loads, exports every entry point include/k44wavec.h
+declares (the reference's 30 plus the build extensions), and behaves on error paths."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+# The reference's extern "C" entry points (wavec/k44_wave_executor.cu:644-986).
+REFERENCE_ABI = [
+    "wavec_create", "wavec_destroy", "wavec_gpu_release", "wavec_add_input", "wavec_add_flatten",
+    "wavec_add_conv2d", "wavec_add_conv2d_f16", "wavec_add_linear_f32", "wavec_add_linear_f16",
+    "wavec_add_linear_bf16", "wavec_add_upconv2x2", "wavec_add_maxpool", "wavec_add_upsample2x",
+    "wavec_add_rmsnorm", "wavec_add_swiglu", "wavec_add_rope_gqa_attn", "wavec_add_split",
+    "wavec_add_slice", "wavec_add_concat", "wavec_set_output", "wavec_set_reuse_canvas",
+    "wavec_set_batch_size", "wavec_set_target_preset", "wavec_compile", "wavec_get_summary_json",
+    "wavec_save_tcff", "wavec_save_tcff_ex", "wavec_load_tcff_weights", "wavec_gpu_init_plan",
+    "wavec_gpu_infer_f32",
+]
+
+
+def header_symbols():
+    text = (ROOT / "include" / "k44wavec.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wavec_\w+)\s*\(", text)))
+
+
+def test_header_declares_reference_abi_and_extensions(wavec):
+    hdr = header_symbols()
+    assert set(REFERENCE_ABI) <= set(hdr)
+    assert len(REFERENCE_ABI) == 30
+    assert set(hdr) == set(wavec.REFERENCE_SYMBOLS) | set(wavec.EXTENSION_SYMBOLS)
+    assert list(wavec.REFERENCE_SYMBOLS) == REFERENCE_ABI
+
+
+def test_library_exports_every_declared_symbol(wavec):
+    lib = ctypes.CDLL(str(wavec.LIB_PATH))
+    missing = [s for s in header_symbols() if not hasattr(lib, s)]
+    assert not missing
+
+
+def test_null_handle_returns_error(wavec):
+    lib = wavec.get_lib()
+    assert lib.wavec_compile(None) == -1
+    assert lib.wavec_gpu_init_plan(None) == -1
+    assert lib.wavec_gpu_release(None) == -1
+    assert lib.wavec_add_input(None, b"x", 1, 1, 64, 1) == -1
+    assert lib.wavec_save_tcff(None, b"/tmp/x.tcff", b"p") == -1
+    assert lib.wavec_load_tcff_weights(None, b"/tmp/x.tcff") == -1
+    assert lib.wavec_get_summary_json(None) == b"{}"
+    assert lib.wavec_gpu_exec_report_json(None) == b"{}"
+    lib.wavec_destroy(None)  # no-op
+
+
+def test_gpu_entry_points_require_init(wavec):
+    lib = wavec.get_lib()
+    h = lib.wavec_create(0, 0, 0, 1)
+    try:
+        x = np.zeros(4, np.float32)
+        out = np.zeros(4, np.float32)
+        ms = ctypes.c_float()
+        p = x.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        q = out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        assert lib.wavec_gpu_infer_f32(h, p, 4, q, 4, ctypes.byref(ms)) == -1
+        assert "wavec_gpu_init_plan" in wavec.last_error()
+        assert lib.wavec_gpu_execute(h, 1, ctypes.byref(ms)) == -1
+    finally:
+        lib.wavec_destroy(h)
+
+
+def test_invalid_sparse_wave_is_rejected(wavec):
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", 100, 1, 64, is_1d=True)
+    rows = np.zeros((3, 4), np.uint32)
+    w = np.zeros((6, 4), np.uint16)
+    rc = g._lib.wavec_add_sparse_wave(
+        g._handle, b"s", b"x", b"y", 6, 4, 4,  # cluster 4 does not divide cout 6
+        rows.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+        w.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), None, 1, None)
+    assert rc == -1 and "cluster" in wavec.last_error()
+    # a synapse position beyond the input's channel count fails at compile time
+    g.add_sparse_wave("s2", "x", "y2", np.full((2, 4), 100, np.uint32), np.zeros((2, 4),
+                                                                                 np.float16))
+    with pytest.raises(RuntimeError, match="beyond the input"):
+        g.compile()
+
+
+def test_unsupported_plans_fail_init_with_message(wavec):
+    """The executor refuses what it cannot run instead of silently skipping it."""
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("img", 8, 16, 64)  # 2-D image
+    g.add_conv2d("c", "img", "y", 8, 16, 3, 3, np.zeros((16, 8, 3, 3), np.float32), act="relu")
+    plan = g.compile()
+    with pytest.raises(RuntimeError, match="2-D"):
+        plan.init_gpu()
+    g2 = wavec.WaveGraph(kv_cache_max_seq=0)
+    g2.add_input("t", 64, 1, 64, is_1d=True)
+    g2.add_rmsnorm("n", "t", "u", 64, np.ones(64, np.float32))
+    plan2 = g2.compile()
+    with pytest.raises(RuntimeError, match="RMSNORM_1D"):
+        plan2.init_gpu()

@@ -1,0 +1,297 @@
+"""Plan compilation and the .tcff format, checked bit-exactly against an independent Python
+restatement of the reference's compiler and writer (oracle/plan_oracle.py), plus format
+invariants, tamper rejection and the 64-bit extension tag.  Host only (no GPU)."""
+import json
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import plan_oracle as po
+from snntome_amd import synth
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _f16(a):
+    return np.asarray(a, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def _pair(wavec, build):
+    """Build the same graph with the library and with the Python restatement."""
+    g = wavec.WaveGraph(kv_cache_max_seq=0, fold_rmsnorm_gamma=False)
+    pg = po.Graph()
+    build(g, pg)
+    return g, g.compile(), po.compile_plan(pg)
+
+
+def _linear(g, pg, name, i, o, din, dout, rng, act=None, res=None):
+    w = (rng.standard_normal((dout, din)) * 0.1).astype(np.float32)
+    b = (rng.standard_normal(dout) * 0.1).astype(np.float32)
+    g.add_linear(name, i, o, din, dout, w, b, act=act, res_blob=res)
+    pg.linear(name, i, o, din, dout, _f16(w).reshape(dout, din), _f16(b),
+              act=po.ACT_NAMES.index((act or "none").upper()) if act else 0,
+              residual=res or "")
+
+
+def _sparse(g, pg, name, i, o, rows, cout, cluster, rng, act="relu", res=None, seg_len=0):
+    fan = rows.shape[1]
+    w = synth.normal_f16(rng, (cout, fan), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    if seg_len:
+        K = fan // seg_len
+        g.add_cluster_wave(name, i, o, rows[:, ::seg_len], seg_len, w, b, cluster=cluster,
+                           act=act, res_blob=res)
+    else:
+        g.add_sparse_wave(name, i, o, rows, w, b, cluster=cluster, act=act, res_blob=res)
+    pg.sparse(name, i, o, rows, w.view(np.uint16), b.view(np.uint16), cluster=cluster,
+              act=po.ACT_NAMES.index(act.upper()), residual=res or "", seg_len=seg_len)
+
+
+def _assert_same_tcff(plan, pplan, tmp_path, prefix="K44Model"):
+    path = tmp_path / "p.tcff"
+    plan.save_tcff(path, prefix)
+    got = path.read_bytes()
+    want = po.tcff_bytes(pplan, prefix)
+    if got != want:
+        n = min(len(got), len(want))
+        first = next((i for i in range(n) if got[i] != want[i]), n)
+        pytest.fail(f".tcff differs: sizes {len(got)} vs {len(want)}, first diff at {first}")
+    return got
+
+
+def _assert_same_plan(plan, pplan):
+    s = plan.summary
+    assert s["canvas_elems"] == pplan["canvas_elems"]
+    waves = [c for c in s["cmds"] if c["type"] == "K44_WAVE"]
+    pw = [c for c in pplan["cmds"] if c["type"] == 0]
+    assert len(waves) == len(pw)
+    for c, p in zip(waves, pw):
+        for k_lib, k_or in (("Cout", "Cout"), ("logical_Cout", "logical_Cout"), ("B", "B"),
+                            ("B_raw", "B_raw"), ("S", "cluster"), ("src_off", "src_off"),
+                            ("y_off", "y_off"), ("Cin", "Cin")):
+            assert c[k_lib] == p[k_or], (c["name"], k_lib, c[k_lib], p[k_or])
+    assert list(s["output_shape"]) == list(pplan["output"])
+
+
+def test_linear_chain_with_views(wavec, tmp_path):
+    rng = np.random.default_rng(0)
+
+    def build(g, pg):
+        for G in (g, pg):
+            (G.add_input if G is g else G.input)("x", 96, 1, 100, True)
+        _linear(g, pg, "fc1", "x", "h1", 96, 200, rng, act="relu")
+        g.add_split("sp", "h1", ["a", "b"])
+        pg.split("sp", "h1", ["a", "b"])
+        g.add_slice("sl", "a", ["a0", "a1"], [72, 128])
+        pg.slice("sl", "a", ["a0", "a1"], [72, 128])
+        _linear(g, pg, "fc2", "a1", "h2", 128, 48, rng, act="silu")
+        g.add_concat("cat", ["a0", "h2"], "h3")
+        pg.concat("cat", ["a0", "h2"], "h3")
+        _linear(g, pg, "fc3", "h3", "h4", 120, 72, rng, act="sigmoid", res="a0")
+        _linear(g, pg, "fc4", "h4", "out", 72, 33, rng)
+        g.set_output("out")
+        pg.output = "out"
+
+    g, plan, pplan = _pair(wavec, build)
+    _assert_same_plan(plan, pplan)
+    _assert_same_tcff(plan, pplan, tmp_path)
+
+
+def test_sparse_waves_over_concat(wavec, tmp_path):
+    """A small config-4-style plan: sparse waves over concatenations of earlier outputs."""
+    wl = synth.config4(waves=3, width=2048, neurons=128, K=4, S=32, tokens=64)
+
+    def build(g, pg):
+        g.add_input("x", wl.substrate, 1, wl.tokens, is_1d=True)
+        pg.input("x", wl.substrate, 1, wl.tokens, True)
+        for i, w in enumerate(wl.waves):
+            src = w.sources[0] if len(w.sources) == 1 else f"cat{i}"
+            if len(w.sources) > 1:
+                g.add_concat(f"cat{i}", w.sources, src)
+                pg.concat(f"cat{i}", w.sources, src)
+            rows = (w.starts[:, :, None].astype(np.int64) + np.arange(w.S)).reshape(
+                w.cout, -1).astype(np.uint32)
+            g.add_cluster_wave(w.name, src, f"y{i}", w.starts, w.S, w.weights, w.bias,
+                               act=w.act)
+            pg.sparse(w.name, src, f"y{i}", rows, w.weights.view(np.uint16),
+                      w.bias.view(np.uint16), act=1, seg_len=w.S)
+        g.set_output("y2")
+        pg.output = "y2"
+
+    g, plan, pplan = _pair(wavec, build)
+    _assert_same_plan(plan, pplan)
+    _assert_same_tcff(plan, pplan, tmp_path)
+
+
+@pytest.mark.parametrize("cluster", [1, 16, 64])
+def test_sparse_wave_clusters_and_residual(wavec, tmp_path, cluster):
+    rng = np.random.default_rng(cluster)
+    C, cout, fan = 1500, 128, 48
+    rows = rng.integers(0, C, size=(cout // cluster, fan)).astype(np.uint32)
+
+    def build(g, pg):
+        g.add_input("x", C, 1, 192, is_1d=True)
+        pg.input("x", C, 1, 192, True)
+        _sparse(g, pg, "s", "x", "y", rows, cout, cluster, rng, act="gelu", res="x")
+
+    g, plan, pplan = _pair(wavec, build)
+    _assert_same_plan(plan, pplan)
+    _assert_same_tcff(plan, pplan, tmp_path)
+
+
+def test_summary_json_keys(wavec):
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", 64, 1, 64, is_1d=True)
+    g.add_linear("fc", "x", "y", 64, 32, np.ones((32, 64), np.float32))
+    plan = g.compile()
+    for key in ("batch_size", "num_waves", "num_cmds", "canvas_elems", "canvas_bytes",
+                "kv_cache_elems", "total_w_bytes", "total_idx_bytes", "single_frame_gflops",
+                "total_gflops", "single_frame_gsyn", "total_gsyn", "input_shape",
+                "output_shape", "max_B_per_wave", "target_profile", "target_num_cus",
+                "persistent_neurons", "reuse_canvas", "cmds"):
+        assert key in plan.summary
+    assert plan.canvas_bytes == 2 * plan.summary["canvas_elems"]
+    assert plan.num_wave_dispatches == 1
+    assert plan.total_gflops == pytest.approx(2 * 64 * 32 * 64 / 1e9, rel=1e-5)
+
+
+def _tcff_ifds(data: bytes):
+    """Minimal TIFF walk: list of {tag: (type, count, value)} per IFD."""
+    out = []
+    off = struct.unpack_from("<I", data, 4)[0]
+    while off:
+        n = struct.unpack_from("<H", data, off)[0]
+        tags = {}
+        for i in range(n):
+            t, ty, cnt, val = struct.unpack_from("<HHII", data, off + 2 + 12 * i)
+            tags[t] = (ty, cnt, val)
+        out.append(tags)
+        off = struct.unpack_from("<I", data, off + 2 + 12 * n)[0]
+    return out
+
+
+def test_tcff_header_layout_by_hand(wavec, tmp_path):
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", 64, 1, 64, is_1d=True)
+    g.add_linear("fc", "x", "y", 64, 32, np.ones((32, 64), np.float32))
+    plan = g.compile()
+    p = tmp_path / "h.tcff"
+    plan.save_tcff(p, "Hand")
+    d = p.read_bytes()
+    assert d[:4] == b"II*\x00"
+    assert d[8:16] == b"TCFFv1.0"
+    align, waves, canvas_bytes, flags = struct.unpack_from("<IIII", d, 16)
+    assert (align, waves, flags) == (256, 1, 1)
+    assert canvas_bytes == plan.canvas_bytes
+    assert struct.unpack_from("<Q", d, 32)[0] == po.fnv1a64(d[8:32])
+    assert struct.unpack_from("<I", d, 4)[0] % 256 == 0 and len(d) % 256 == 0
+    (ifd,) = _tcff_ifds(d)
+    assert ifd[0x8440] == (4, 1, 0x45564157)
+    assert ifd[256][2] == 64 and ifd[257][2] == 32  # B, Cout
+    aux = struct.unpack_from("<11I", d, ifd[0x8442][2])
+    w_off, w_bytes, i_off, i_bytes, b_off, b_bytes = aux[:6]
+    assert w_bytes == 32 * 64 * 2 and i_bytes == (32 // 32) * 64 * 4 and b_bytes == 64
+    h = struct.unpack_from("<II", d, ifd[0x8443][2])
+    assert (h[1] << 32 | h[0]) == po.fnv1a64(d[aux[8]:aux[9]])
+    assert 0x8445 not in ifd  # no extension tag for a plain 32-bit plan
+
+
+def test_tcff_roundtrip_and_tamper_rejection(wavec, tmp_path):
+    rng = np.random.default_rng(4)
+    starts = rng.integers(0, 900, size=(64, 2)).astype(np.uint32)
+    w = synth.normal_f16(rng, (64, 32), 0.1)
+    b = synth.normal_f16(rng, (64,), 0.1)
+
+    def make(weights):
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("x", 1000, 1, 64, is_1d=True)
+        g.add_cluster_wave("w", "x", "y", starts, 16, weights, b, act="relu")
+        return g, g.compile()
+
+    g1, p1 = make(w)
+    path = tmp_path / "a.tcff"
+    p1.save_tcff(path)
+    good = path.read_bytes()
+    g2, p2 = make(np.zeros_like(w))
+    p2.load_tcff_weights(path)
+    # loaded plan re-saves to the identical file
+    path2 = tmp_path / "b.tcff"
+    p2.save_tcff(path2)
+    assert path2.read_bytes() == good
+    ifd = _tcff_ifds(good)[0]
+    aux = struct.unpack_from("<11I", good, ifd[0x8442][2])
+    for where in (9, 20, 33, aux[0] + 5, aux[2] + 1, aux[4]):  # header, hash, payloads
+        bad = bytearray(good)
+        bad[where] ^= 0x40
+        p = tmp_path / f"bad{where}.tcff"
+        p.write_bytes(bytes(bad))
+        with pytest.raises(RuntimeError):
+            p2.load_tcff_weights(p)
+    trunc = tmp_path / "trunc.tcff"
+    trunc.write_bytes(good[: len(good) // 2])
+    with pytest.raises(RuntimeError):
+        p2.load_tcff_weights(trunc)
+
+
+def test_index_rebase_above_0x70000000(wavec, tmp_path):
+    """Indices >= 0x70000000 fp16 elements are re-based on min & ~63 (x_base_off) and the
+    padded synapses zeroed (reference pack_wave_buffers).  30M channels x 64 tokens."""
+    C = 30_000_000
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", C, 1, 64, is_1d=True)
+    rows = np.full((16, 3), 29_500_000, np.uint32)  # 16 neurons: no padded (all-zero) rows
+    rows[0] = [29_999_000, 29_999_001, 5]
+    rows[1] = [29_000_000, 29_000_007, 29_999_999]
+    g.add_sparse_wave("s", "x", "y", rows, np.ones((16, 3), np.float16))
+    plan = g.compile()
+    p = tmp_path / "r.tcff"
+    plan.save_tcff(p)
+    d = p.read_bytes()
+    ifd = _tcff_ifds(d)[0]
+    aux = struct.unpack_from("<11I", d, ifd[0x8442][2])
+    idx = np.frombuffer(d, dtype="<u4", count=aux[3] // 4, offset=aux[2]).reshape(-1, 64)
+    base = (5 * 64) & ~63
+    assert idx[0, 0] == 29_999_000 * 64 - base and idx[0, 2] == 5 * 64 - base
+    assert idx[1, 2] == 29_999_999 * 64 - base
+    assert idx[2, 0] == 29_500_000 * 64 - base
+    assert not idx[:, 3:].any()
+
+
+def test_row_index_mode_beyond_4g_elements(wavec, tmp_path):
+    """A 70M-position x 64-token input is 4.48 G fp16 elements: the sparse wave is emitted in
+    row-index mode and the 0x8445 tag records the 64-bit offsets."""
+    C = 70_000_000
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", C, 1, 64, is_1d=True)
+    rows = np.array([[69_999_990 + i for i in range(8)]] * 16, np.uint32)
+    g.add_sparse_wave("s", "x", "y", rows, np.ones((16, 8), np.float16))
+    plan = g.compile()
+    cmd = plan.cmds[0]
+    assert cmd["idx_mode"] == 1 and cmd["y_off"] == C * 64
+    p = tmp_path / "big.tcff"
+    plan.save_tcff(p)
+    d = p.read_bytes()
+    ifd = _tcff_ifds(d)[0]
+    ext = struct.unpack_from("<12I", d, ifd[0x8445][2])
+    assert ext[0] == 1 and ext[1] == 64 and ext[2] == 0  # mode, idx_stride
+    assert (ext[8] << 32 | ext[7]) == C * 64  # y_off (64-bit)
+    aux = struct.unpack_from("<11I", d, ifd[0x8442][2])
+    idx = np.frombuffer(d, dtype="<u4", count=aux[3] // 4, offset=aux[2]).reshape(-1, 64)
+    assert idx[0, 0] == 69_999_990 and idx[0, 7] == 69_999_997
+
+
+def test_golden_fixture(wavec, tmp_path):
+    """Regression pin: the committed golden plan file (tests/golden/make_golden.py) is
+    reproduced byte for byte, and equals the Python restatement's bytes."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("make_golden", GOLDEN / "make_golden.py")
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    data = mg.build_tcff(wavec, tmp_path / "g.tcff")
+    assert data == (GOLDEN / "small_plan.tcff").read_bytes()
+    assert po.tcff_bytes(po.compile_plan(mg.oracle_graph(po)), "Golden") == data
+    meta = json.loads((GOLDEN / "small_plan.json").read_text())
+    assert mg.summary_fields(wavec) == meta
