@@ -6,8 +6,8 @@
  * (0 = success, -1 = failure; pointers NULL on failure).  They are what the reference's ctypes
  * binding (wavec/wavec.py:28-132) binds.  Differences in behaviour, all on error paths:
  *   - a HIP runtime error returns -1 (the reference calls exit(EXIT_FAILURE));
- *   - a plan the executor cannot run (2-D spatial layouts, aux command types other than
- *     K44_WAVE) fails wavec_gpu_init_plan with -1 instead of silently skipping commands;
+ *   - a plan the executor cannot run (2-D spatial layouts and their aux commands, RoPE/GQA
+ *     attention) fails wavec_gpu_init_plan with -1 instead of silently skipping commands;
  *   - the message of the last failure on the calling thread is available from wavec_last_error().
  *
  * The entry points after "build extensions" have no counterpart in the reference.
@@ -130,6 +130,35 @@ int wavec_gpu_read_canvas(void *handle, unsigned long long elem_off, unsigned lo
                           uint16_t *dst);
 int wavec_gpu_write_canvas(void *handle, unsigned long long elem_off, unsigned long long n_elems,
                            const uint16_t *src);
+
+/* ---- 1-D token ops of LLM-shaped plans (no reference counterpart: its executor has no token
+ * shift, embedding or argmax, and no decode state) -------------------------------------------- */
+/* Causal depth-wise mix y[c][t] = sum_{i<rf} mu[c][i] * x[c][t-i] inside requests of seq_len
+ * tokens (decode = 0, prefill), or one token per request with the rf-1 previous inputs carried in
+ * a per-plan state block [dim][rf-1][64] (decode = 1).  mu_f16: [dim][rf]. */
+int wavec_add_token_shift(void *handle, const char *name, const char *in_tensor,
+                          const char *out_tensor, int dim, int rf, int seq_len,
+                          const uint16_t *mu_f16, int decode);
+/* y[c][t] = table[id[t]][c]; ids from wavec_gpu_set_ids or the previous run's argmax; tok_in is a
+ * 1-D tensor that supplies the token axis.  table_f16: [vocab][dim]. */
+int wavec_add_embedding(void *handle, const char *name, const char *tok_in, const char *out_tensor,
+                        int vocab, int dim, const uint16_t *table_f16);
+/* id[t] = argmax_c x[c][t] (lowest index on ties) into the plan's token-id buffer. */
+int wavec_add_argmax(void *handle, const char *name, const char *in_tensor, const char *out_tensor);
+
+int wavec_gpu_set_ids(void *handle, const uint32_t *ids, int n);
+int wavec_gpu_get_ids(void *handle, uint32_t *ids, int n);
+/* Record the argmax ids of the next `steps` plan runs (device-side counter); get_history returns
+ * the number of steps recorded and copies up to n ids ([step][token]). */
+int wavec_gpu_set_history(void *handle, int steps);
+int wavec_gpu_get_history(void *handle, uint32_t *out, int n);
+/* Replay each plan run as one captured HIP graph (enable = 1) instead of kernel by kernel. */
+int wavec_gpu_use_graph(void *handle, int enable);
+/* Device-to-device copies between two initialised plans (same GPU). */
+int wavec_gpu_copy_canvas(void *dst_handle, unsigned long long dst_elem_off, void *src_handle,
+                          unsigned long long src_elem_off, unsigned long long n_elems);
+int wavec_gpu_copy_ids(void *dst_handle, int dst_first, void *src_handle, int src_first,
+                       int src_step, int n);
 
 /* JSON: per wave the kernel path taken and why, its segment schedule (K, S, step) and
  * accounting (flops, distinct substrate rows).  "{}" before a successful init. */

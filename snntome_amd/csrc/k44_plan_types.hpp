@@ -96,16 +96,21 @@ enum class K44CmdType : int {
     SCATTER_UP2X2 = 5,
     RMSNORM_1D = 7,
     SWIGLU_MUL_1D = 8,
-    ROPE_GQA_ATTN_1D = 9
+    ROPE_GQA_ATTN_1D = 9,
+    // build extensions (1-D token ops of LLM-shaped wave plans)
+    TOKEN_SHIFT_1D = 10,
+    EMBED_1D = 11,
+    ARGMAX_1D = 12
 };
 
 static inline const char *cmd_type_str(K44CmdType t) {
-    static const char *const names[] = {"K44_WAVE",      "S2D_2X2",       "MAXPOOL_2X2",
-                                        "MAXPOOL_5X5",   "UPSAMPLE_2X",   "SCATTER_UP2X2",
-                                        "UNKNOWN",       "RMSNORM_1D",    "SWIGLU_MUL_1D",
-                                        "ROPE_GQA_ATTN_1D"};
+    static const char *const names[] = {"K44_WAVE",       "S2D_2X2",        "MAXPOOL_2X2",
+                                        "MAXPOOL_5X5",    "UPSAMPLE_2X",    "SCATTER_UP2X2",
+                                        "UNKNOWN",        "RMSNORM_1D",     "SWIGLU_MUL_1D",
+                                        "ROPE_GQA_ATTN_1D", "TOKEN_SHIFT_1D", "EMBED_1D",
+                                        "ARGMAX_1D"};
     const int i = (int)t;
-    return (i >= 0 && i <= 9) ? names[i] : "UNKNOWN";
+    return (i >= 0 && i <= 12) ? names[i] : "UNKNOWN";
 }
 
 static inline const char *act_str(K44Act a) {
@@ -376,6 +381,11 @@ struct K44ExecCmd {
     uint32_t idx_mode = 0;    // 0: h_idx = fp16-element offsets; 1: substrate row indices
     uint64_t idx_stride = 1;  // fp16 elements per row index (idx_mode 1)
     uint32_t seg_len = 0;     // positions per dendritic cluster (0 = unknown)
+    uint32_t rf = 0;          // TOKEN_SHIFT_1D: receptive field (taps)
+    uint32_t seq_len = 0;     // TOKEN_SHIFT_1D: tokens per request (prefill)
+    bool decode_state = false;  // TOKEN_SHIFT_1D: one token per request, state carried
+    uint64_t state_off = 0;   // TOKEN_SHIFT_1D: canvas offset of the [C][rf-1][64] state block
+    std::vector<uint16_t> h_table;  // EMBED_1D: [vocab][dim] fp16; TOKEN_SHIFT_1D: [C][rf] mix
     std::vector<uint4_host> h_w_wmma;
     std::vector<uint32_t> h_idx;
     std::vector<uint16_t> h_bias;
@@ -460,6 +470,10 @@ struct K44IRNode {
     uint32_t cluster = 1;        // neurons sharing one index row
     uint32_t seg_len = 0;        // positions per dendritic cluster (hint, 0 = unknown)
     std::vector<uint32_t> rows;  // [cout/cluster][fan_in] input channel index of every synapse
+    // --- build extension: 1-D token ops ("TokenShift", "Embedding", "ArgMax") ---
+    uint32_t rf = 0, seq_len = 0, vocab = 0;
+    bool decode_state = false;
+    std::vector<uint16_t> table;  // Embedding [vocab][dim]; TokenShift [C][rf]
 };
 
 }  // namespace k44_host

@@ -35,6 +35,7 @@ class K44WaveGraphCompiler {
         uint64_t canvas_off;
     };
     using ChanMap = std::map<std::string, std::vector<uint64_t>>;
+    std::map<size_t, uint64_t> state_offs;  // TokenShift node -> state block offset
 
     static uint32_t make_res_key(uint32_t h, uint32_t w, bool is_1d) {
         if (is_1d) return 0x80000000u | w;
@@ -170,6 +171,24 @@ class K44WaveGraphCompiler {
                 n.h_out = 1u;
                 n.w_out = s.w;
                 shapes[n.out_tensors[0]] = {n.cout, 1u, s.w, true};
+            } else if (op == "TokenShift" || op == "ArgMax" || op == "Embedding") {
+                const Shape3D s = in_shape();
+                if (!s.is_1d)
+                    throw std::runtime_error("node '" + n.name + "': needs a 1-D token tensor");
+                n.is_1d_tokens = true;
+                n.h_in = n.h_out = s.h;
+                n.w_in = n.w_out = s.w;
+                if (op == "TokenShift") {
+                    n.cin = n.cout = s.c;
+                    if (n.table.size() != (size_t)s.c * n.rf)
+                        throw std::runtime_error("token shift '" + n.name +
+                                                 "': mix table is not [channels][rf]");
+                }
+                if (op == "ArgMax") {
+                    n.cin = s.c;
+                    n.cout = 1u;
+                }
+                shapes[n.out_tensors[0]] = {n.cout, s.h, s.w, true};
             } else if (op == "Deconvolution") {
                 const Shape3D s = in_shape();
                 n.is_1d_tokens = false;
@@ -310,6 +329,7 @@ class K44WaveGraphCompiler {
                                std::map<uint32_t, uint64_t> &quad_base,
                                std::map<size_t, std::pair<uint64_t, uint64_t>> &kv_offs,
                                uint64_t &probs_off) {
+        state_offs.clear();
         std::map<std::string, std::set<int>> ids;
         out_aid.assign(nodes.size(), -1);
         int next_id = 0;
@@ -470,6 +490,13 @@ class K44WaveGraphCompiler {
                 probs_off = cur;
                 cur += (uint64_t)max_hq * opts.kv_cache_max_seq;
             }
+        }
+        // Token-shift state blocks (build extension): [C][rf-1][64] per TokenShift node.
+        for (size_t i = 0; i < nodes.size(); ++i) {
+            const K44IRNode &n = nodes[i];
+            if (n.op_type != "TokenShift" || n.rf < 2u) continue;
+            state_offs[i] = cur;
+            cur += round_up((uint64_t)n.cout * (n.rf - 1u) * 64u, 64u);
         }
         cur = round_up(cur, 128u);
         plan.kv_cache_elems = kv_total;
@@ -796,6 +823,28 @@ class K44WaveGraphCompiler {
                 c.gflops = (double)plan.wave_batch_size * sf;
                 plan.single_frame_gflops += sf;
                 plan.total_gflops += c.gflops;
+                plan.cmds.push_back(std::move(c));
+            } else if (op == "TokenShift" || op == "Embedding" || op == "ArgMax") {
+                const uint32_t rk = allocs.at(id).res_key;
+                const uint64_t dst = place(n, id, n.cout);
+                const std::vector<uint64_t> &src = chan.at(n.in_tensors[0]);
+                const uint64_t st = plan.res_map.at(rk).channel_stride;
+                for (size_t c = 0; c < src.size(); ++c)
+                    if (src[c] != src[0] + c * st)
+                        throw std::runtime_error("node '" + n.name +
+                                                 "': input channels must be one contiguous tensor");
+                const K44CmdType t = op == "TokenShift" ? K44CmdType::TOKEN_SHIFT_1D
+                                     : op == "Embedding" ? K44CmdType::EMBED_1D
+                                                         : K44CmdType::ARGMAX_1D;
+                K44ExecCmd c = make_base_cmd(n, t, rk, rk, src[0], dst);
+                c.rf = n.rf;
+                c.seq_len = n.seq_len;
+                c.decode_state = n.decode_state;
+                c.h_table = n.table;
+                if (op == "Embedding") c.Cin = n.vocab;
+                if (op == "ArgMax") c.Cin = n.cin;
+                auto so = state_offs.find(i);
+                if (so != state_offs.end()) c.state_off = so->second;
                 plan.cmds.push_back(std::move(c));
             } else if (op == "Deconvolution") {
                 const uint32_t rk_in = make_res_key(n.h_in, n.w_in, false);
@@ -1138,6 +1187,52 @@ class K44WaveGraphCompiler {
                 for (uint32_t s = 0; s < S; ++s) rows[r * fan + (size_t)k * S + s] = starts[r * K + k] + s;
         add_sparse_wave(name, in, out, cout, (uint32_t)fan, cluster, rows.data(), w_f16, bias_f16,
                         act, res, S);
+    }
+
+    // Build extension: causal depth-wise token mix y[c][t] = sum_{i<rf} mu[c][i] x[c][t-i] within
+    // requests of seq_len tokens (prefill), or one token per request with carried state (decode).
+    void add_token_shift(const std::string &name, const std::string &in, const std::string &out,
+                         uint32_t dim, uint32_t rf, uint32_t seq_len, const uint16_t *mu_f16,
+                         bool decode) {
+        if (rf == 0u || rf > 9u || seq_len == 0u || !mu_f16 || dim == 0u)
+            throw std::invalid_argument("add_token_shift: need 1 <= rf <= 9, seq_len > 0, mix");
+        K44IRNode n;
+        n.op_type = "TokenShift";
+        n.name = name;
+        n.in_tensors = {in};
+        n.out_tensors = {out};
+        n.rf = rf;
+        n.seq_len = seq_len;
+        n.decode_state = decode;
+        n.table.assign(mu_f16, mu_f16 + (size_t)dim * rf);
+        append_node_to_graph(std::move(n));
+    }
+
+    // Build extension: y[c][t] = table[id[t]][c]; ids come from the executor's id buffer
+    // (wavec_gpu_set_ids, or the previous run's ArgMax).  `tok_in` supplies the token axis.
+    void add_embedding(const std::string &name, const std::string &tok_in, const std::string &out,
+                       uint32_t vocab, uint32_t dim, const uint16_t *table_f16) {
+        if (vocab == 0u || dim == 0u || !table_f16)
+            throw std::invalid_argument("add_embedding: need vocab, dim and a table");
+        K44IRNode n;
+        n.op_type = "Embedding";
+        n.name = name;
+        n.in_tensors = {tok_in};
+        n.out_tensors = {out};
+        n.vocab = vocab;
+        n.cout = dim;
+        n.table.assign(table_f16, table_f16 + (size_t)vocab * dim);
+        append_node_to_graph(std::move(n));
+    }
+
+    // Build extension: id[t] = argmax_c x[c][t] into the executor's id buffer.
+    void add_argmax(const std::string &name, const std::string &in, const std::string &out) {
+        K44IRNode n;
+        n.op_type = "ArgMax";
+        n.name = name;
+        n.in_tensors = {in};
+        n.out_tensors = {out};
+        append_node_to_graph(std::move(n), false);
     }
 
     const K44WavePlan &compile() {

@@ -94,6 +94,18 @@ struct WaveExec {
     DevBuf<uint16_t> cmap;
 };
 
+// Device schedule of one 1-D token op (RMSNORM_1D, SWIGLU_MUL_1D, TOKEN_SHIFT_1D, EMBED_1D,
+// ARGMAX_1D).
+struct AuxExec {
+    k44_host::K44CmdType type;
+    std::string name;
+    uint64_t y_off = 0, src_off = 0, src2_off = 0, state_off = 0;
+    uint32_t D = 0, stride = 0, tokens = 0, rf = 0, seq_len = 0, vocab = 0;
+    bool decode = false, has_state = false;
+    float eps = 1e-5f;
+    DevBuf<__half> table;  // gamma (RMSNORM), mix (TOKEN_SHIFT), embedding table (EMBED)
+};
+
 uint32_t pick_mt(uint32_t tokens) {
     for (uint32_t mt : {512u, 256u, 128u}) if (tokens % mt == 0u) return mt;
     return 64u;
@@ -112,16 +124,37 @@ namespace k44_host {
 struct K44GpuExecutorState {
     K44WavePlan plan_meta;  // plan without payload vectors
     std::vector<std::unique_ptr<WaveExec>> waves;
+    std::vector<std::unique_ptr<AuxExec>> aux;
+    std::vector<std::pair<bool, size_t>> ops;  // plan order: (is_wave, index)
     DevBuf<__half> canvas;
+    DevBuf<uint32_t> ids, history, step_ctr;  // token ids (EMBED / ARGMAX), greedy history
+    uint32_t id_tokens = 0, hist_steps = 0;
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    bool use_graph = false;
     bool initialized = false;
     std::string report_json;
 
     ~K44GpuExecutorState() { free_all(); }
 
+    void drop_graph() {
+        if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        graph_exec = nullptr;
+        graph = nullptr;
+    }
+
     void free_all() {
+        drop_graph();
         waves.clear();
+        aux.clear();
+        ops.clear();
+        ids.reset();
+        history.reset();
+        step_ctr.reset();
+        id_tokens = hist_steps = 0;
         canvas.reset();
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
@@ -356,6 +389,114 @@ struct K44GpuExecutorState {
         wx.flops = 2.0 * (double)c.Cout * c.B_raw * wx.tokens;
     }
 
+    void build_aux(const K44ExecCmd &c, AuxExec &ax) {
+        const K44ResDesc &L = plan_meta.res_map.at(c.res_key_out);
+        if (!L.is_1d_tokens)
+            throw std::runtime_error("command '" + c.name + "': needs a 1-D token layout");
+        ax.type = c.type;
+        ax.name = c.name;
+        ax.y_off = c.y_off;
+        ax.src_off = c.src_off;
+        ax.src2_off = c.src2_off;
+        ax.stride = L.channel_stride;
+        ax.tokens = L.W;
+        ax.eps = c.eps;
+        const uint64_t n_canvas = plan_meta.canvas_elems;
+        auto need = [&](uint64_t off, uint64_t n, const char *what) {
+            if (off > n_canvas || n > n_canvas - off)
+                throw std::runtime_error("command '" + c.name + "': " + what + " past the canvas");
+        };
+        auto upload_f16 = [&](DevBuf<__half> &buf, const std::vector<uint16_t> &v) {
+            std::vector<__half> h(v.size());
+            std::memcpy(h.data(), v.data(), v.size() * 2u);
+            buf.upload(h);
+        };
+        if (ax.stride % 64u != 0u) throw std::runtime_error("command '" + c.name + "': stride");
+        switch (c.type) {
+        case K44CmdType::RMSNORM_1D:
+            ax.D = c.Cin;
+            need(ax.src_off, (uint64_t)ax.D * ax.stride, "input");
+            need(ax.y_off, (uint64_t)ax.D * ax.stride, "output");
+            if (!c.gamma_folded) {
+                if (c.h_bias.size() < ax.D) throw std::runtime_error("RMSNorm gamma too short");
+                upload_f16(ax.table, std::vector<uint16_t>(c.h_bias.begin(), c.h_bias.begin() + ax.D));
+            }
+            break;
+        case K44CmdType::SWIGLU_MUL_1D:
+            ax.D = c.Cout;
+            need(ax.src_off, (uint64_t)ax.D * ax.stride, "gate");
+            need(ax.src2_off, (uint64_t)ax.D * ax.stride, "up");
+            need(ax.y_off, (uint64_t)ax.D * ax.stride, "output");
+            break;
+        case K44CmdType::TOKEN_SHIFT_1D:
+            ax.D = c.Cin;
+            ax.rf = c.rf;
+            ax.seq_len = c.seq_len;
+            ax.decode = c.decode_state;
+            ax.has_state = c.rf >= 2u;
+            ax.state_off = c.state_off;
+            need(ax.src_off, (uint64_t)ax.D * ax.stride, "input");
+            need(ax.y_off, (uint64_t)ax.D * ax.stride, "output");
+            if (ax.has_state) need(ax.state_off, (uint64_t)ax.D * (ax.rf - 1u) * 64u, "state");
+            if (ax.decode ? ax.tokens > 64u : (ax.tokens % ax.seq_len != 0u ||
+                                               ax.tokens / ax.seq_len > 64u))
+                throw std::runtime_error("command '" + c.name +
+                                         "': token shift supports at most 64 requests of equal length");
+            if (c.h_table.size() != (size_t)ax.D * ax.rf)
+                throw std::runtime_error("command '" + c.name + "': mix table size");
+            upload_f16(ax.table, c.h_table);
+            break;
+        case K44CmdType::EMBED_1D:
+            ax.D = c.Cout;
+            ax.vocab = c.Cin;
+            need(ax.y_off, (uint64_t)ax.D * ax.stride, "output");
+            if (c.h_table.size() != (size_t)ax.D * ax.vocab)
+                throw std::runtime_error("command '" + c.name + "': embedding table size");
+            upload_f16(ax.table, c.h_table);
+            id_tokens = std::max(id_tokens, ax.tokens);
+            break;
+        case K44CmdType::ARGMAX_1D:
+            ax.D = c.Cin;
+            need(ax.src_off, (uint64_t)ax.D * ax.stride, "input");
+            id_tokens = std::max(id_tokens, ax.tokens);
+            break;
+        default:
+            throw std::runtime_error(std::string("command '") + c.name + "' of type " +
+                                     cmd_type_str(c.type) + " is not supported by this executor");
+        }
+    }
+
+    void launch_aux(const AuxExec &a) {
+        __half *cv = canvas.p;
+        switch (a.type) {
+        case K44CmdType::RMSNORM_1D:
+            K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D, a.stride,
+                                           a.tokens, a.eps, stream));
+            break;
+        case K44CmdType::SWIGLU_MUL_1D:
+            K44_HIP(k44dev::launch_mul(cv + a.y_off, cv + a.src_off, cv + a.src2_off,
+                                       (uint64_t)a.D * a.stride, stream));
+            break;
+        case K44CmdType::TOKEN_SHIFT_1D:
+            K44_HIP(k44dev::launch_token_shift(cv + a.y_off, cv + a.src_off, a.table.p,
+                                               a.has_state ? cv + a.state_off : nullptr, a.D,
+                                               a.stride, a.tokens, a.rf, a.seq_len,
+                                               a.decode ? 1 : 0, stream));
+            break;
+        case K44CmdType::EMBED_1D:
+            K44_HIP(k44dev::launch_embed(cv + a.y_off, a.table.p, ids.p, a.D, a.vocab, a.stride,
+                                         a.tokens, stream));
+            break;
+        case K44CmdType::ARGMAX_1D:
+            K44_HIP(k44dev::launch_argmax(ids.p, hist_steps ? history.p : nullptr, step_ctr.p,
+                                          hist_steps, cv + a.src_off, a.D, a.stride, a.tokens,
+                                          stream));
+            break;
+        default:
+            throw std::runtime_error("unsupported aux command");
+        }
+    }
+
     void init(const K44WavePlan &plan) {
         free_all();
         plan_meta.res_map = plan.res_map;
@@ -372,19 +513,29 @@ struct K44GpuExecutorState {
         plan_meta.output_res_key = plan.output_res_key;
         plan_meta.batch_size = plan.batch_size;
         for (const auto &c : plan.cmds) {
-            if (c.type != K44CmdType::K44_WAVE)
-                throw std::runtime_error(std::string("command '") + c.name + "' of type " +
-                                         cmd_type_str(c.type) +
-                                         " is not supported by this executor");
-            auto wx = std::make_unique<WaveExec>();
-            build_wave(c, *wx);
-            waves.push_back(std::move(wx));
+            if (c.type == K44CmdType::K44_WAVE) {
+                auto wx = std::make_unique<WaveExec>();
+                build_wave(c, *wx);
+                ops.push_back({true, waves.size()});
+                waves.push_back(std::move(wx));
+            } else {
+                auto ax = std::make_unique<AuxExec>();
+                build_aux(c, *ax);
+                ops.push_back({false, aux.size()});
+                aux.push_back(std::move(ax));
+            }
         }
         K44_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         K44_HIP(hipEventCreate(&ev0));
         K44_HIP(hipEventCreate(&ev1));
         canvas.alloc(plan.canvas_elems);
         K44_HIP(hipMemsetAsync(canvas.p, 0, plan.canvas_elems * 2u, stream));
+        if (id_tokens) {
+            ids.alloc(id_tokens);
+            step_ctr.alloc(1);
+            K44_HIP(hipMemsetAsync(ids.p, 0, id_tokens * 4u, stream));
+            K44_HIP(hipMemsetAsync(step_ctr.p, 0, 4u, stream));
+        }
         K44_HIP(hipStreamSynchronize(stream));
         build_report();
         initialized = true;
@@ -404,7 +555,13 @@ struct K44GpuExecutorState {
               << ", \"flops\": " << (long long)w.flops << ", \"unique_rows\": " << w.unique_rows
               << ", \"y_off\": " << w.y_off << "}";
         }
-        o << "], \"canvas_elems\": " << plan_meta.canvas_elems << "}";
+        o << "], \"aux\": [";
+        for (size_t i = 0; i < aux.size(); ++i)
+            o << (i ? ", " : "") << "{\"name\": \"" << aux[i]->name << "\", \"type\": \""
+              << cmd_type_str(aux[i]->type) << "\", \"channels\": " << aux[i]->D
+              << ", \"tokens\": " << aux[i]->tokens << "}";
+        o << "], \"canvas_elems\": " << plan_meta.canvas_elems << ", \"id_tokens\": " << id_tokens
+          << "}";
         report_json = o.str();
     }
 
@@ -451,8 +608,47 @@ struct K44GpuExecutorState {
         K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream));
     }
 
+    void launch_ops() {
+        for (const auto &op : ops) {
+            if (op.first)
+                launch_wave(*waves[op.second]);
+            else
+                launch_aux(*aux[op.second]);
+        }
+    }
+
+    // One plan run on the executor stream: kernel by kernel, or as one replay of a HIP graph
+    // captured from the same launches (no memset/memcpy nodes in it).
     void execute_plan() {
-        for (const auto &w : waves) launch_wave(*w);
+        if (!use_graph) {
+            launch_ops();
+            return;
+        }
+        if (!graph_exec) {
+            K44_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+            try {
+                launch_ops();
+            } catch (...) {
+                hipGraph_t g = nullptr;
+                (void)hipStreamEndCapture(stream, &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            K44_HIP(hipStreamEndCapture(stream, &graph));
+            K44_HIP(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0));
+        }
+        K44_HIP(hipGraphLaunch(graph_exec, stream));
+    }
+
+    void set_history(uint32_t steps) {
+        if (!id_tokens) throw std::runtime_error("plan has no token-id buffer (no embed/argmax)");
+        K44_HIP(hipStreamSynchronize(stream));
+        drop_graph();  // the history pointer is baked into captured launches
+        history.alloc((size_t)std::max(1u, steps) * id_tokens);
+        hist_steps = steps;
+        K44_HIP(hipMemsetAsync(history.p, 0, history.n * 4u, stream));
+        K44_HIP(hipMemsetAsync(step_ctr.p, 0, 4u, stream));
+        K44_HIP(hipStreamSynchronize(stream));
     }
 
     const K44ResDesc &layout(uint32_t key) const { return plan_meta.res_map.at(key); }
@@ -917,6 +1113,132 @@ int wavec_gpu_write_canvas(void *h, unsigned long long off, unsigned long long n
             throw std::runtime_error("range outside the canvas");
         K44_HIP(hipMemcpyAsync(ex->canvas.p + off, src, n * 2u, hipMemcpyHostToDevice, ex->stream));
         K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+int wavec_add_token_shift(void *h, const char *name, const char *in, const char *out, int dim,
+                          int rf, int seq_len, const uint16_t *mu_f16, int decode) {
+    if (!h || !name || !in || !out || dim <= 0 || rf <= 0 || seq_len <= 0) return -1;
+    return guarded("wavec_add_token_shift", [&] {
+        comp_of(h)->add_token_shift(name, in, out, (uint32_t)dim, (uint32_t)rf,
+                                    (uint32_t)seq_len, mu_f16, decode != 0);
+        return 0;
+    });
+}
+
+int wavec_add_embedding(void *h, const char *name, const char *tok_in, const char *out,
+                        int vocab, int dim, const uint16_t *table_f16) {
+    if (!h || !name || !tok_in || !out || vocab <= 0 || dim <= 0) return -1;
+    return guarded("wavec_add_embedding", [&] {
+        comp_of(h)->add_embedding(name, tok_in, out, (uint32_t)vocab, (uint32_t)dim, table_f16);
+        return 0;
+    });
+}
+
+int wavec_add_argmax(void *h, const char *name, const char *in, const char *out) {
+    if (!h || !name || !in || !out) return -1;
+    return guarded("wavec_add_argmax", [&] {
+        comp_of(h)->add_argmax(name, in, out);
+        return 0;
+    });
+}
+
+static k44_host::K44GpuExecutorState *exec_or_throw(void *h) {
+    k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+    if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+    return ex;
+}
+
+int wavec_gpu_set_ids(void *h, const uint32_t *ids, int n) {
+    if (!h || !ids || n < 0) return -1;
+    return guarded("wavec_gpu_set_ids", [&] {
+        auto *ex = exec_or_throw(h);
+        if ((uint32_t)n > ex->id_tokens) throw std::runtime_error("more ids than plan tokens");
+        K44_HIP(hipMemcpyAsync(ex->ids.p, ids, (size_t)n * 4u, hipMemcpyHostToDevice, ex->stream));
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+int wavec_gpu_get_ids(void *h, uint32_t *ids, int n) {
+    if (!h || !ids || n < 0) return -1;
+    return guarded("wavec_gpu_get_ids", [&] {
+        auto *ex = exec_or_throw(h);
+        if ((uint32_t)n > ex->id_tokens) throw std::runtime_error("more ids than plan tokens");
+        K44_HIP(hipMemcpyAsync(ids, ex->ids.p, (size_t)n * 4u, hipMemcpyDeviceToHost, ex->stream));
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+int wavec_gpu_set_history(void *h, int steps) {
+    if (!h || steps <= 0) return -1;
+    return guarded("wavec_gpu_set_history", [&] {
+        exec_or_throw(h)->set_history((uint32_t)steps);
+        return 0;
+    });
+}
+
+int wavec_gpu_get_history(void *h, uint32_t *out, int n) {
+    if (!h || !out || n < 0) return -1;
+    return guarded("wavec_gpu_get_history", [&] {
+        auto *ex = exec_or_throw(h);
+        if (!ex->hist_steps) throw std::runtime_error("no history buffer (wavec_gpu_set_history)");
+        uint32_t steps = 0;
+        K44_HIP(hipMemcpyAsync(&steps, ex->step_ctr.p, 4u, hipMemcpyDeviceToHost, ex->stream));
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        const size_t avail = (size_t)std::min(steps, ex->hist_steps) * ex->id_tokens;
+        const size_t cnt = std::min(avail, (size_t)n);
+        if (cnt)
+            K44_HIP(hipMemcpyAsync(out, ex->history.p, cnt * 4u, hipMemcpyDeviceToHost, ex->stream));
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return (int)std::min(steps, ex->hist_steps);
+    });
+}
+
+int wavec_gpu_use_graph(void *h, int enable) {
+    if (!h) return -1;
+    return guarded("wavec_gpu_use_graph", [&] {
+        auto *ex = exec_or_throw(h);
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        ex->use_graph = enable != 0;
+        if (!ex->use_graph) ex->drop_graph();
+        return 0;
+    });
+}
+
+int wavec_gpu_copy_canvas(void *dst_h, unsigned long long dst_off, void *src_h,
+                          unsigned long long src_off, unsigned long long n) {
+    if (!dst_h || !src_h) return -1;
+    return guarded("wavec_gpu_copy_canvas", [&] {
+        auto *d = exec_or_throw(dst_h);
+        auto *s = exec_or_throw(src_h);
+        if (dst_off > d->plan_meta.canvas_elems || n > d->plan_meta.canvas_elems - dst_off ||
+            src_off > s->plan_meta.canvas_elems || n > s->plan_meta.canvas_elems - src_off)
+            throw std::runtime_error("range outside a canvas");
+        K44_HIP(hipStreamSynchronize(s->stream));
+        K44_HIP(hipMemcpyAsync(d->canvas.p + dst_off, s->canvas.p + src_off, n * 2u,
+                               hipMemcpyDeviceToDevice, d->stream));
+        K44_HIP(hipStreamSynchronize(d->stream));
+        return 0;
+    });
+}
+
+int wavec_gpu_copy_ids(void *dst_h, int dst_first, void *src_h, int src_first, int src_step,
+                       int n) {
+    if (!dst_h || !src_h || dst_first < 0 || src_first < 0 || src_step <= 0 || n < 0) return -1;
+    return guarded("wavec_gpu_copy_ids", [&] {
+        auto *d = exec_or_throw(dst_h);
+        auto *s = exec_or_throw(src_h);
+        if ((uint64_t)dst_first + n > d->id_tokens ||
+            (n && (uint64_t)src_first + (uint64_t)(n - 1) * src_step >= s->id_tokens))
+            throw std::runtime_error("id range outside a plan's token-id buffer");
+        K44_HIP(hipStreamSynchronize(s->stream));
+        K44_HIP(hipMemcpy2DAsync(d->ids.p + dst_first, 4u, s->ids.p + src_first,
+                                 (size_t)src_step * 4u, 4u, (size_t)n, hipMemcpyDeviceToDevice,
+                                 d->stream));
+        K44_HIP(hipStreamSynchronize(d->stream));
         return 0;
     });
 }

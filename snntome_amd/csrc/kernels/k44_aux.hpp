@@ -1,0 +1,37 @@
+// k44_aux.hpp — VALU kernels of the 1-D token ops around the waves (LLM-shaped plans).
+//
+// All tensors are channel-major on the canvas: element (c, t) at base + c*stride + t.
+//  * RMSNORM_1D (reference kernels/common/kernel44_valu_pack.cuh:104-134): per token t,
+//    y[c][t] = x[c][t] * rsqrt(sum_c x[c][t]^2 / D + eps) * gamma[c]   (gamma = 1 when folded).
+//  * SWIGLU_MUL_1D (reference :135-143): y = gate * up, element-wise (SiLU is fused into the gate
+//    projection's epilogue).
+//  * TOKEN_SHIFT_1D (build extension): causal depth-wise mix over the last RF tokens of the same
+//    request, y[c][t] = sum_{i<RF} mu[c][i] * x[c][t-i] (x[c][t-i] = 0 before the request
+//    start).  Decode mode: one token per request, the RF-1 previous inputs come from a state
+//    block [c][RF-1][64] that the kernel shifts in place.  Prefill mode writes the same state
+//    block (the last RF-1 inputs of every request) for the decode plan to continue from.
+//  * EMBED_1D / ARGMAX_1D (build extension): y[c][t] = E[id[t]][c]; id[t] = argmax_c x[c][t]
+//    (lowest index on ties), optionally also appended to a history buffer.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k44dev {
+
+hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
+                          uint32_t stride, uint32_t tokens, float eps, hipStream_t stream);
+hipError_t launch_mul(__half *y, const __half *a, const __half *b, uint64_t n,
+                      hipStream_t stream);
+hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __half *state,
+                              uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf,
+                              uint32_t seq_len, int decode, hipStream_t stream);
+hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uint32_t D,
+                        uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream);
+// history (nullable): ids are also stored at history[*step_ctr][t] while *step_ctr <
+// hist_steps, and *step_ctr is incremented after the argmax (device-side, graph-safe).
+hipError_t launch_argmax(uint32_t *ids, uint32_t *history, uint32_t *step_ctr,
+                         uint32_t hist_steps, const __half *x, uint32_t V, uint32_t stride,
+                         uint32_t tokens, hipStream_t stream);
+
+}  // namespace k44dev

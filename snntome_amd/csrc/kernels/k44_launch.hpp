@@ -6,6 +6,7 @@
 
 #include "k44_gather_dot.hpp"
 #include "k44_mfma_tile.hpp"
+#include "k44_aux.hpp"
 
 namespace k44dev {
 

@@ -195,3 +195,127 @@ def compulsory_bytes(wl: Workload, wave: WaveSpec) -> int:
     u = distinct_positions(wave.starts, wave.S)
     return (2 * wl.tokens * u + 2 * wave.nnz + 4 * wave.starts.size + 2 * wave.cout
             + 2 * wave.cout * wl.tokens)
+
+
+# ---------------------------------------------------------------------------------------------
+# Config 5: LLM-shaped compiled decoder
+# ---------------------------------------------------------------------------------------------
+@dataclass
+class LLMSpec:
+    """LLM-shaped decoder compiled to waves.  Per layer (x: [d][tokens], fp16 canvas tensors):
+        u = RMSNorm(x);  s = TokenShift_rf(u)        (causal, per request; carried state in decode)
+        q = sigmoid(Wq s);  k = silu(Wk s);  v = Wv s;  m = q * (k * v)
+        x = x + Wo m
+        n = RMSNorm(x);  h = silu(Wg n) * (Wu n);  x = x + Wd h
+    then logits = Whead RMSNorm(x), next id = argmax.  Every projection is a dendritic-cluster
+    wave: its input row is split into clusters of S consecutive channels and a random `keep`
+    fraction of them is kept, drawn per tile of `tile` output neurons (neurons of a tile share
+    their cluster pattern, which makes every tile a dense MFMA contraction).  RMSNorm gamma = 1."""
+    layers: int = 16
+    d: int = 2048
+    ffn: int = 5632
+    vocab: int = 32000
+    S: int = 512
+    keep: float = 0.5
+    tile: int = 64
+    rf: int = 4
+    requests: int = 16
+    prompt: int = 512
+    decode_steps: int = 128
+    seed: int = 5
+
+    def kept(self, fan: int) -> int:
+        n = fan // self.S
+        return max(1, int(np.ceil(n * self.keep - 1e-9)))
+
+    @property
+    def nnz_per_token(self) -> int:
+        kd, kf = self.kept(self.d) * self.S, self.kept(self.ffn) * self.S
+        per_layer = 4 * self.d * kd + 2 * self.ffn * kd + self.d * kf
+        return self.layers * per_layer + self.vocab * kd
+
+
+@dataclass
+class Projection:
+    starts: np.ndarray  # [cout/tile, K] uint32 first input channel of each kept cluster
+    weights: np.ndarray  # [cout, K*S] fp16
+    bias: np.ndarray  # [cout] fp16
+
+
+def _projection(rng, spec: LLMSpec, fan_in: int, cout: int) -> Projection:
+    n_cl = fan_in // spec.S
+    K = spec.kept(fan_in)
+    tiles = cout // spec.tile
+    pick = np.argsort(rng.random((tiles, n_cl)), axis=1)[:, :K]
+    starts = (np.sort(pick, axis=1) * spec.S).astype(np.uint32)
+    sigma = 1.0 / np.sqrt(K * spec.S)
+    w = (rng.standard_normal((cout, K * spec.S), dtype=np.float32) * np.float32(sigma)).astype(
+        np.float16)
+    b = (rng.standard_normal(cout, dtype=np.float32) * np.float32(0.01)).astype(np.float16)
+    return Projection(starts, w, b)
+
+
+@dataclass
+class LLMWeights:
+    embed: np.ndarray  # [vocab, d] fp16
+    mix: List[np.ndarray]  # per layer [d, rf] fp16 (rows sum to ~1)
+    proj: List[dict]  # per layer {"q","k","v","o","g","u","dn"} -> Projection
+    head: Projection
+
+
+def llm_weights(spec: LLMSpec) -> LLMWeights:
+    rng = np.random.default_rng(spec.seed)
+    embed = rng.standard_normal((spec.vocab, spec.d), dtype=np.float32).astype(np.float16)
+    mix, proj = [], []
+    for _ in range(spec.layers):
+        m = rng.random((spec.d, spec.rf), dtype=np.float32) + np.float32(0.05)
+        m[:, 0] += np.float32(spec.rf)  # the current token dominates the mix
+        mix.append((m / m.sum(axis=1, keepdims=True)).astype(np.float16))
+        p = {}
+        for name in ("q", "k", "v", "o"):
+            p[name] = _projection(rng, spec, spec.d, spec.d)
+        p["g"] = _projection(rng, spec, spec.d, spec.ffn)
+        p["u"] = _projection(rng, spec, spec.d, spec.ffn)
+        p["dn"] = _projection(rng, spec, spec.ffn, spec.d)
+        proj.append(p)
+    head = _projection(rng, spec, spec.d, spec.vocab)
+    return LLMWeights(embed, mix, proj, head)
+
+
+def build_llm_graph(spec: LLMSpec, wts: LLMWeights, decode: bool, wavec_mod=None):
+    """Prefill (decode=False: requests x prompt tokens) or decode (one token per request)."""
+    if wavec_mod is None:
+        from . import wavec as wavec_mod
+    T = spec.requests if decode else spec.requests * spec.prompt
+    seq = 1 if decode else spec.prompt
+    g = wavec_mod.WaveGraph(kv_cache_max_seq=0, fold_rmsnorm_gamma=True)
+    g.add_input("tok", 1, 1, T, is_1d=True)
+    g.add_embedding("embed", "tok", "x0", wts.embed)
+    ones = np.ones(spec.d, np.float32)
+
+    def proj(name, src, out, p: Projection, act=None, res=None):
+        g.add_cluster_wave(name, src, out, p.starts, spec.S, p.weights, p.bias,
+                           cluster=spec.tile, act=act, res_blob=res)
+
+    x = "x0"
+    for l in range(spec.layers):
+        P = wts.proj[l]
+        g.add_rmsnorm(f"l{l}.n1", x, f"l{l}.u", spec.d, ones)
+        g.add_token_shift(f"l{l}.shift", f"l{l}.u", f"l{l}.s", wts.mix[l], seq, decode=decode)
+        proj(f"l{l}.q", f"l{l}.s", f"l{l}.q", P["q"], act="sigmoid")
+        proj(f"l{l}.k", f"l{l}.s", f"l{l}.k", P["k"], act="silu")
+        proj(f"l{l}.v", f"l{l}.s", f"l{l}.v", P["v"])
+        g.add_swiglu(f"l{l}.kv", f"l{l}.k", f"l{l}.v", f"l{l}.kv")
+        g.add_swiglu(f"l{l}.m", f"l{l}.q", f"l{l}.kv", f"l{l}.m")
+        proj(f"l{l}.o", f"l{l}.m", f"l{l}.x1", P["o"], res=x)
+        g.add_rmsnorm(f"l{l}.n2", f"l{l}.x1", f"l{l}.n", spec.d, ones)
+        proj(f"l{l}.g", f"l{l}.n", f"l{l}.g", P["g"], act="silu")
+        proj(f"l{l}.u", f"l{l}.n", f"l{l}.up", P["u"])
+        g.add_swiglu(f"l{l}.h", f"l{l}.g", f"l{l}.up", f"l{l}.h")
+        proj(f"l{l}.dn", f"l{l}.h", f"l{l}.x2", P["dn"], res=f"l{l}.x1")
+        x = f"l{l}.x2"
+    g.add_rmsnorm("final.n", x, "z", spec.d, ones)
+    proj("head", "z", "logits", wts.head)
+    g.add_argmax("argmax", "logits", "next")
+    g.set_output("logits")
+    return g

@@ -71,6 +71,16 @@ _SIGNATURES = {
     "wavec_gpu_sync": (_i, [_vp]),
     "wavec_gpu_read_canvas": (_i, [_vp, _ull, _ull, _pu16]),
     "wavec_gpu_write_canvas": (_i, [_vp, _ull, _ull, _pu16]),
+    "wavec_add_token_shift": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _pu16, _i]),
+    "wavec_add_embedding": (_i, [_vp, _cp, _cp, _cp, _i, _i, _pu16]),
+    "wavec_add_argmax": (_i, [_vp, _cp, _cp, _cp]),
+    "wavec_gpu_set_ids": (_i, [_vp, _pu32, _i]),
+    "wavec_gpu_get_ids": (_i, [_vp, _pu32, _i]),
+    "wavec_gpu_set_history": (_i, [_vp, _i]),
+    "wavec_gpu_get_history": (_i, [_vp, _pu32, _i]),
+    "wavec_gpu_use_graph": (_i, [_vp, _i]),
+    "wavec_gpu_copy_canvas": (_i, [_vp, _ull, _vp, _ull, _ull]),
+    "wavec_gpu_copy_ids": (_i, [_vp, _i, _vp, _i, _i, _i]),
     "wavec_gpu_exec_report_json": (_cp, [_vp]),
 }
 
@@ -222,6 +232,41 @@ class WavePlan:
     @property
     def cmds(self) -> List[dict]:
         return list(self.summary.get("cmds", []))
+
+    def set_ids(self, ids) -> None:
+        a = np.ascontiguousarray(ids, dtype=np.uint32)
+        _check(self._lib.wavec_gpu_set_ids(self._handle, _ptr(a, ctypes.c_uint32), int(a.size)),
+               "wavec_gpu_set_ids")
+
+    def get_ids(self, n: int) -> np.ndarray:
+        out = np.empty(int(n), dtype=np.uint32)
+        _check(self._lib.wavec_gpu_get_ids(self._handle, _ptr(out, ctypes.c_uint32), int(n)),
+               "wavec_gpu_get_ids")
+        return out
+
+    def set_history(self, steps: int) -> None:
+        _check(self._lib.wavec_gpu_set_history(self._handle, int(steps)), "wavec_gpu_set_history")
+
+    def get_history(self, steps: int, tokens: int) -> np.ndarray:
+        out = np.zeros(int(steps) * int(tokens), dtype=np.uint32)
+        n = self._lib.wavec_gpu_get_history(self._handle, _ptr(out, ctypes.c_uint32), out.size)
+        if n < 0:
+            raise RuntimeError("wavec_gpu_get_history failed: " + last_error())
+        return out.reshape(int(steps), int(tokens))[:n]
+
+    def use_graph(self, enable: bool = True) -> None:
+        _check(self._lib.wavec_gpu_use_graph(self._handle, 1 if enable else 0),
+               "wavec_gpu_use_graph")
+
+    def copy_canvas_from(self, src: "WavePlan", dst_off: int, src_off: int, n: int) -> None:
+        _check(self._lib.wavec_gpu_copy_canvas(self._handle, int(dst_off), src._handle,
+                                               int(src_off), int(n)), "wavec_gpu_copy_canvas")
+
+    def copy_ids_from(self, src: "WavePlan", dst_first: int, src_first: int, src_step: int,
+                      n: int) -> None:
+        _check(self._lib.wavec_gpu_copy_ids(self._handle, int(dst_first), src._handle,
+                                            int(src_first), int(src_step), int(n)),
+               "wavec_gpu_copy_ids")
 
 
 class WaveGraph:
@@ -396,6 +441,31 @@ class WaveGraph:
             int(seg_len), int(cluster), _ptr(st, ctypes.c_uint32), _ptr(w, ctypes.c_uint16),
             _ptr(b, ctypes.c_uint16), ACT_MAP.get(act, 0),
             res_blob.encode() if res_blob else None), "wavec_add_cluster_wave")
+        return out_blob
+
+    def add_token_shift(self, name: str, in_blob: str, out_blob: str, mu: np.ndarray,
+                        seq_len: int, decode: bool = False) -> str:
+        """Causal depth-wise mix over the last rf tokens of each request; mu: [dim, rf]."""
+        m = _f16_bits(mu)
+        dim, rf = m.shape
+        _check(self._lib.wavec_add_token_shift(self._handle, name.encode(), in_blob.encode(),
+                                               out_blob.encode(), int(dim), int(rf),
+                                               int(seq_len), _ptr(m, ctypes.c_uint16),
+                                               1 if decode else 0), "wavec_add_token_shift")
+        return out_blob
+
+    def add_embedding(self, name: str, tok_blob: str, out_blob: str, table: np.ndarray) -> str:
+        """y[c][t] = table[id[t]][c]; table: [vocab, dim]."""
+        t = _f16_bits(table)
+        vocab, dim = t.shape
+        _check(self._lib.wavec_add_embedding(self._handle, name.encode(), tok_blob.encode(),
+                                             out_blob.encode(), int(vocab), int(dim),
+                                             _ptr(t, ctypes.c_uint16)), "wavec_add_embedding")
+        return out_blob
+
+    def add_argmax(self, name: str, in_blob: str, out_blob: str) -> str:
+        _check(self._lib.wavec_add_argmax(self._handle, name.encode(), in_blob.encode(),
+                                          out_blob.encode()), "wavec_add_argmax")
         return out_blob
 
     def save_tcff(self, path: Union[str, Path], model_prefix: str = "K44Model",

@@ -97,8 +97,8 @@ def test_unsupported_plans_fail_init_with_message(wavec):
     with pytest.raises(RuntimeError, match="2-D"):
         plan.init_gpu()
     g2 = wavec.WaveGraph(kv_cache_max_seq=0)
-    g2.add_input("t", 64, 1, 64, is_1d=True)
-    g2.add_rmsnorm("n", "t", "u", 64, np.ones(64, np.float32))
+    g2.add_input("t", 128, 1, 64, is_1d=True)
+    g2.add_rope_gqa_attn("a", "t", "t", "t", "o", 2, 2, 64)
     plan2 = g2.compile()
-    with pytest.raises(RuntimeError, match="RMSNORM_1D"):
+    with pytest.raises(RuntimeError, match="ROPE_GQA_ATTN_1D"):
         plan2.init_gpu()
