@@ -124,6 +124,9 @@ int wavec_gpu_fill_input_uniform(void *handle, unsigned long long seed);
 /* Runs the whole plan `iters` times on the executor stream; average ms per run (HIP events). */
 int wavec_gpu_execute(void *handle, int iters, float *out_ms_per_iter);
 int wavec_gpu_sync(void *handle);
+/* Runs plan commands [first_cmd, first_cmd + n_cmds) kernel by kernel and waits for them: lets a
+ * caller inspect every intermediate tensor before the canvas allocator reuses its memory. */
+int wavec_gpu_execute_range(void *handle, int first_cmd, int n_cmds);
 
 /* Raw fp16 access to the canvas (element offsets / counts). */
 int wavec_gpu_read_canvas(void *handle, unsigned long long elem_off, unsigned long long n_elems,

@@ -1287,11 +1287,23 @@ class K44WaveGraphCompiler {
         js.reserve(js.size() + p.cmds.size() * 300u + 16u);
         for (size_t i = 0; i < p.cmds.size(); ++i) {
             const K44ExecCmd &c = p.cmds[i];
-            char extra[96] = "";
+            // Build-extension keys (the reference's readers ignore unknown keys).
+            char extra[256] = "";
+            size_t ne = 0;
+            auto add = [&](const char *fmt, unsigned long long a, unsigned long long b = 0,
+                           unsigned long long c3 = 0, unsigned long long d = 0) {
+                if (ne < sizeof(extra))
+                    ne += (size_t)std::snprintf(extra + ne, sizeof(extra) - ne, fmt, a, b, c3, d);
+            };
             if (c.seg_len || c.idx_mode)
-                std::snprintf(extra, sizeof(extra), ", \"seg_len\": %u, \"idx_mode\": %u",
-                              c.seg_len, c.idx_mode);
-            char line[768];
+                add(", \"seg_len\": %llu, \"idx_mode\": %llu", c.seg_len, c.idx_mode);
+            if (c.has_residual) add(", \"res_off\": %llu", (unsigned long long)c.res_off);
+            if (c.type == K44CmdType::SWIGLU_MUL_1D)
+                add(", \"src2_off\": %llu", (unsigned long long)c.src2_off);
+            if (c.type == K44CmdType::TOKEN_SHIFT_1D)
+                add(", \"rf\": %llu, \"seq_len\": %llu, \"decode\": %llu, \"state_off\": %llu",
+                    c.rf, c.seq_len, c.decode_state ? 1u : 0u, (unsigned long long)c.state_off);
+            char line[1024];
             std::snprintf(
                 line, sizeof(line),
                 "    {\"idx\": %zu, \"name\": \"%s\", \"type\": \"%s\", \"Cin\": %u, \"Cout\": %u, "

@@ -608,13 +608,16 @@ struct K44GpuExecutorState {
         K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream));
     }
 
+    void launch_op(size_t i) {
+        const auto &op = ops.at(i);
+        if (op.first)
+            launch_wave(*waves[op.second]);
+        else
+            launch_aux(*aux[op.second]);
+    }
+
     void launch_ops() {
-        for (const auto &op : ops) {
-            if (op.first)
-                launch_wave(*waves[op.second]);
-            else
-                launch_aux(*aux[op.second]);
-        }
+        for (size_t i = 0; i < ops.size(); ++i) launch_op(i);
     }
 
     // One plan run on the executor stream: kernel by kernel, or as one replay of a HIP graph
@@ -1076,6 +1079,19 @@ int wavec_gpu_execute(void *h, int iters, float *out_ms_per_iter) {
         float ms = 0.0f;
         K44_HIP(hipEventElapsedTime(&ms, ex->ev0, ex->ev1));
         if (out_ms_per_iter) *out_ms_per_iter = ms / (float)iters;
+        return 0;
+    });
+}
+
+int wavec_gpu_execute_range(void *h, int first_cmd, int n_cmds) {
+    if (!h || first_cmd < 0 || n_cmds < 0) return -1;
+    return guarded("wavec_gpu_execute_range", [&] {
+        k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+        if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+        if ((size_t)first_cmd + (size_t)n_cmds > ex->ops.size())
+            throw std::runtime_error("command range past the end of the plan");
+        for (int i = first_cmd; i < first_cmd + n_cmds; ++i) ex->launch_op((size_t)i);
+        K44_HIP(hipStreamSynchronize(ex->stream));
         return 0;
     });
 }

@@ -319,3 +319,16 @@ def build_llm_graph(spec: LLMSpec, wts: LLMWeights, decode: bool, wavec_mod=None
     g.add_argmax("argmax", "logits", "next")
     g.set_output("logits")
     return g
+
+
+def llm_handoff(spec: LLMSpec, prefill, decode) -> None:
+    """Device-side hand-over from a finished prefill plan to the decode plan: every layer's
+    token-shift state block, and the argmax id of each request's last prompt token as the
+    first decode input."""
+    pre = {c["name"]: c for c in prefill.cmds if c["type"] == "TOKEN_SHIFT_1D"}
+    n = spec.d * (spec.rf - 1) * 64
+    for c in decode.cmds:
+        if c["type"] != "TOKEN_SHIFT_1D":
+            continue
+        decode.copy_canvas_from(prefill, int(c["state_off"]), int(pre[c["name"]]["state_off"]), n)
+    decode.copy_ids_from(prefill, 0, spec.prompt - 1, spec.prompt, spec.requests)

@@ -69,6 +69,7 @@ _SIGNATURES = {
     "wavec_gpu_fill_input_uniform": (_i, [_vp, _ull]),
     "wavec_gpu_execute": (_i, [_vp, _i, _pf]),
     "wavec_gpu_sync": (_i, [_vp]),
+    "wavec_gpu_execute_range": (_i, [_vp, _i, _i]),
     "wavec_gpu_read_canvas": (_i, [_vp, _ull, _ull, _pu16]),
     "wavec_gpu_write_canvas": (_i, [_vp, _ull, _ull, _pu16]),
     "wavec_add_token_shift": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _pu16, _i]),
@@ -211,6 +212,12 @@ class WavePlan:
 
     def sync(self) -> None:
         _check(self._lib.wavec_gpu_sync(self._handle), "wavec_gpu_sync")
+
+    def execute_range(self, first_cmd: int, n_cmds: int = 1) -> None:
+        """Runs plan commands [first_cmd, first_cmd + n_cmds) and waits for them."""
+        self.init_gpu()
+        _check(self._lib.wavec_gpu_execute_range(self._handle, int(first_cmd), int(n_cmds)),
+               "wavec_gpu_execute_range")
 
     def read_canvas(self, off: int, n: int) -> np.ndarray:
         out = np.empty(int(n), dtype=np.uint16)

@@ -1,0 +1,220 @@
+"""LLM-shaped plans on the GPU (the decoder of config 5 at a tiny size): every command checked
+against the CPU restatement on the inputs the device itself read, the whole prefill against the
+oracle run end to end, prefill -> decode hand-over, decode steps, and HIP-graph replay with the
+device-side id history."""
+import numpy as np
+import pytest
+
+from oracle import llm_oracle as lo
+from snntome_amd import synth
+
+from wave_cases import TOL, stride_of
+
+pytestmark = pytest.mark.gpu
+
+TINY = synth.LLMSpec(layers=2, d=256, ffn=384, vocab=640, S=64, requests=2, prompt=64,
+                     decode_steps=4, seed=9)
+# End-to-end tolerance, relative to the largest logit: the device and the oracle round every
+# stored tensor to fp16 and may round a value differently by one ulp (each command alone stays
+# within TOL); through 2 layers of residual streams, RMSNorms and gates these differences add up
+# to a few fp16 ulps of the logits' scale (one ulp at the largest logit is ~1e-3 of it).  The
+# per-element metric of TOL does not apply end to end: its 1e-2 floor makes a 1-ulp difference
+# on a logit near zero look like a 10 % error.
+E2E_TOL = 1e-2
+ACTS = {"q": "sigmoid", "k": "silu", "g": "silu"}
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def _read(plan, off, c, t):
+    return plan.read_canvas(int(off), int(c) * t).view(np.float16).reshape(int(c), t)
+
+
+def _projections(spec, wts):
+    out = {"head": (wts.head, None)}
+    for l in range(spec.layers):
+        for k, p in wts.proj[l].items():
+            out[f"l{l}.{k}"] = (p, ACTS.get(k))
+    return out
+
+
+def _check_commands(plan, spec, wts, ids, decode, tag):
+    """Runs the plan command by command; each output is compared with the CPU restatement of
+    that command applied to the canvas contents the command read."""
+    valid = len(ids)
+    T = stride_of(valid)
+    projs = _projections(spec, wts)
+    mixes = {f"l{l}.shift": wts.mix[l] for l in range(spec.layers)}
+    plan.set_ids(ids)
+    worst = {}
+    for i, c in enumerate(plan.cmds):
+        typ, name = c["type"], c["name"]
+        if typ == "K44_WAVE":
+            x = _read(plan, c["src_off"], c["Cin"], T)
+            res = _read(plan, c["res_off"], c["Cout"], T) if c["has_residual"] else None
+        elif typ in ("RMSNORM_1D", "TOKEN_SHIFT_1D", "ARGMAX_1D"):
+            x = _read(plan, c["src_off"], c["Cin"], T)
+        elif typ == "SWIGLU_MUL_1D":
+            a = _read(plan, c["src_off"], c["Cout"], T)
+            b = _read(plan, c["src2_off"], c["Cout"], T)
+        if typ == "TOKEN_SHIFT_1D" and decode:
+            st_in = _read(plan, c["state_off"], spec.d * (spec.rf - 1), 64).reshape(
+                spec.d, spec.rf - 1, 64)
+        plan.execute_range(i, 1)
+        if typ == "ARGMAX_1D":
+            got = plan.get_ids(valid)
+            assert np.array_equal(got, lo.argmax(x, valid)), f"{tag} {name}"
+            continue
+        y = _read(plan, c["y_off"], c["Cout"], T)
+        if typ == "EMBED_1D":
+            assert np.array_equal(y.view(np.uint16), lo.embed(wts.embed, ids, T).view(np.uint16))
+            continue
+        if typ == "SWIGLU_MUL_1D":  # a product of two fp16 is exact in fp32: one rounding
+            assert np.array_equal(y.view(np.uint16), lo.mul(a, b).view(np.uint16)), name
+            continue
+        if typ == "K44_WAVE":
+            p, act = projs[name]
+            ref = lo.project(x, p.starts, spec.S, spec.tile, p.weights, p.bias, act, res,
+                             f64=True)
+        elif typ == "RMSNORM_1D":
+            ref = lo.rmsnorm_f64(x)
+        else:  # TOKEN_SHIFT_1D
+            st = _read(plan, c["state_off"], spec.d * (spec.rf - 1), 64).reshape(
+                spec.d, spec.rf - 1, 64)
+            if decode:
+                ref, st_ref = lo.token_shift_decode(x, mixes[name], st_in, valid, f64=True)
+            else:
+                ref, st_ref = lo.token_shift(x, mixes[name], spec.prompt, valid, f64=True)
+            assert np.array_equal(st.view(np.uint16), st_ref.view(np.uint16)), f"{name} state"
+        err = lo.orc.rel_err(y.astype(np.float64), ref)
+        worst[typ] = max(worst.get(typ, 0.0), err)
+        assert err <= TOL, f"{tag} {name}: rel err {err:.3e}"
+    _log(f"[{tag}] per-command worst rel err: "
+         + ", ".join(f"{k} {v:.2e}" for k, v in sorted(worst.items())))
+
+
+@pytest.mark.parametrize("path", ["auto", "valu"])
+def test_llm_prefill_commandwise_and_end_to_end(wavec, monkeypatch, path):
+    if path != "auto":
+        monkeypatch.setenv("K44WAVEC_PATH", path)
+    wts = synth.llm_weights(TINY)
+    plan = synth.build_llm_graph(TINY, wts, decode=False, wavec_mod=wavec).compile()
+    plan.init_gpu()
+    paths = {w["path"] for w in plan.exec_report()["waves"]}
+    _log(f"[llm prefill {path}] wave paths {sorted(paths)}")
+    assert paths == ({"mfma_tile"} if path == "auto" else {"valu_gather_dot"})
+    rng = np.random.default_rng(1)
+    ids = rng.integers(0, TINY.vocab, TINY.requests * TINY.prompt).astype(np.uint32)
+    _check_commands(plan, TINY, wts, ids, False, f"llm prefill {path}")
+    # the whole prefill once more in one call, against the oracle run end to end
+    plan.set_ids(ids)
+    plan.execute(1)
+    valid = ids.size
+    T = stride_of(valid)
+    head = next(c for c in plan.cmds if c["name"] == "head")
+    logits = _read(plan, head["y_off"], head["Cout"], T)[:, :valid].astype(np.float64)
+    ref = lo.llm_forward(TINY, wts, ids, decode=False)
+    want = ref.tensors["logits"][:, :valid].astype(np.float64)
+    scale = np.abs(want).max()
+    err = np.abs(logits - want).max() / scale
+    _log(f"[llm prefill {path}] end-to-end max|d| / max|logit| = {err:.3e} (max|logit| "
+         f"{scale:.2f}, per-element metric {lo.orc.rel_err(logits, want):.2e})")
+    assert err <= E2E_TOL
+    got = plan.get_ids(valid)
+    srt = np.sort(ref.tensors["logits"][:, :valid].astype(np.float64), axis=0)
+    clear = (srt[-1] - srt[-2]) > 0.05  # ids whose top-2 margin dwarfs the logit error
+    assert clear.mean() > 0.5
+    assert np.array_equal(got[clear], ref.ids[clear])
+
+
+def test_llm_decode_handoff_and_steps(wavec):
+    wts = synth.llm_weights(TINY)
+    pre = synth.build_llm_graph(TINY, wts, decode=False, wavec_mod=wavec).compile()
+    dec = synth.build_llm_graph(TINY, wts, decode=True, wavec_mod=wavec).compile()
+    pre.init_gpu()
+    dec.init_gpu()
+    R, P = TINY.requests, TINY.prompt
+    rng = np.random.default_rng(2)
+    ids = rng.integers(0, TINY.vocab, R * P).astype(np.uint32)
+    pre.set_ids(ids)
+    pre.execute(1)
+    synth.llm_handoff(TINY, pre, dec)
+    assert np.array_equal(dec.get_ids(R), pre.get_ids(R * P)[P - 1::P])
+    shifts_pre = {c["name"]: c for c in pre.cmds if c["type"] == "TOKEN_SHIFT_1D"}
+    n_st = TINY.d * (TINY.rf - 1)
+    for c in dec.cmds:
+        if c["type"] == "TOKEN_SHIFT_1D":
+            a = dec.read_canvas(int(c["state_off"]), n_st * 64)
+            b = pre.read_canvas(int(shifts_pre[c["name"]]["state_off"]), n_st * 64)
+            assert np.array_equal(a, b)
+    for step in range(TINY.decode_steps):
+        _check_commands(dec, TINY, wts, dec.get_ids(R), True, f"llm decode step {step}")
+
+
+def test_llm_decode_graph_replay_matches_eager(wavec):
+    """Two decode plans start from the same hand-over; one runs kernel by kernel, the other as
+    replays of one captured HIP graph with the device-side id history; every step agrees bit for
+    bit (ids and the logits canvas)."""
+    spec = TINY
+    steps = 6
+    wts = synth.llm_weights(spec)
+    pre = synth.build_llm_graph(spec, wts, decode=False, wavec_mod=wavec).compile()
+    eager = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
+    graph = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
+    for p in (pre, eager, graph):
+        p.init_gpu()
+    R = spec.requests
+    pre.set_ids(np.random.default_rng(3).integers(0, spec.vocab, R * spec.prompt))
+    pre.execute(1)
+    synth.llm_handoff(spec, pre, eager)
+    synth.llm_handoff(spec, pre, graph)
+    graph.use_graph(True)
+    graph.set_history(steps)
+    head = next(c for c in eager.cmds if c["name"] == "head")
+    want_ids, want_logits = [], []
+    for _ in range(steps):
+        eager.execute(1)
+        want_ids.append(eager.get_ids(R))
+        want_logits.append(eager.read_canvas(int(head["y_off"]), spec.vocab * 64))
+    # replays 1 and 2 one at a time with host reads between them, then the rest in one call
+    for s in range(2):
+        graph.execute(1)
+        assert np.array_equal(graph.get_ids(R), want_ids[s])
+        assert np.array_equal(graph.read_canvas(int(head["y_off"]), spec.vocab * 64),
+                              want_logits[s])
+    graph.execute(steps - 2)
+    assert np.array_equal(graph.read_canvas(int(head["y_off"]), spec.vocab * 64),
+                          want_logits[-1])
+    hist = graph.get_history(steps, R)
+    assert hist.shape == (steps, R)
+    assert np.array_equal(hist, np.stack(want_ids))
+    _log(f"[llm graph] {steps} decode steps, ids {hist.tolist()}")
+
+
+def test_token_shift_long_rf_and_many_requests(wavec):
+    """Token shift alone at rf = 9 (the kernel's maximum) with 64 requests of 3 tokens (the
+    maximum number of requests) and a non-multiple-of-64 token count."""
+    D, rf, seq, req = 80, 9, 3, 64
+    valid = seq * req  # 192 tokens
+    rng = np.random.default_rng(4)
+    mu = (rng.standard_normal((D, rf)) * 0.5).astype(np.float16)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", D, 1, valid, is_1d=True)
+    g.add_token_shift("ts", "x", "y", mu, seq)
+    plan = g.compile()
+    plan.init_gpu()
+    T = stride_of(valid)
+    x = (rng.standard_normal((D, T)) * 2).astype(np.float16)
+    x[:, valid:] = 0
+    c = plan.cmds[0]
+    plan.write_canvas(int(c["src_off"]), x)
+    plan.execute(1)
+    y = _read(plan, c["y_off"], D, T)
+    ref, st = lo.token_shift(x, mu, seq, valid, f64=True)
+    assert lo.orc.rel_err(y.astype(np.float64), ref) <= TOL
+    assert not y[:, valid:].any()
+    got_st = _read(plan, c["state_off"], D * (rf - 1), 64).reshape(D, rf - 1, 64)
+    # requests shorter than rf - 1 leave the older state slots untouched (zero)
+    assert np.array_equal(got_st.view(np.uint16), st.view(np.uint16))
