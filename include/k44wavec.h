@@ -116,6 +116,15 @@ int wavec_add_cluster_wave(void *handle, const char *name, const char *in_tensor
                            const uint32_t *starts, const uint16_t *w_f16, const uint16_t *bias_f16,
                            int act, const char *residual_tensor);
 
+/* Pruned projection: neuron j keeps its own K clusters of S consecutive input channels starting
+ * at starts[j*K + k]; w_f16: [cout][K*S] in the same cluster order.  Compiled to pattern-sorted
+ * tiles of `tile` neurons (one sub-wave per cluster-union size, outputs restored through
+ * cout_map, epilogue y = act(v + r)); cout < 65535. */
+int wavec_add_pruned_wave(void *handle, const char *name, const char *in_tensor,
+                          const char *out_tensor, int cout, int K, int S, int tile,
+                          const uint32_t *starts, const uint16_t *w_f16, const uint16_t *bias_f16,
+                          int act, const char *residual_tensor);
+
 /* Fills the plan input on the device with the synthetic substrate
  * x(pos, t) = fp16_rne((int32(h >> 40) - 2^23) * 2^-23),
  * h = splitmix64(((pos << 20) | t) ^ splitmix64(seed)); padding tokens are 0. */

@@ -133,8 +133,8 @@ def llm_forward(spec, wts, tok_ids: np.ndarray, decode: bool,
     ts["x0"] = x
     states = []
 
-    def proj(p, src, act=None, res=None):
-        return project(src, p.starts, spec.S, spec.tile, p.weights, p.bias, act, res)
+    def proj(p, src, act=None, res=None):  # per-neuron clusters: index row = neuron
+        return project(src, p.starts, spec.S, 1, p.weights, p.bias, act, res)
 
     for l in range(spec.layers):
         P = wts.proj[l]

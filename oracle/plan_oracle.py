@@ -133,6 +133,12 @@ class Graph:
                        rows=rows, cluster=cluster, act=act, residual=residual,
                        seg_len=seg_len))
 
+    def pruned(self, name, i, o, starts, S, w_bits, b_bits, tile=64, act=0, residual=""):
+        """Per-neuron clusters starts [cout][K] of S channels; compiled by pruned_parts."""
+        self._add(Node("PrunedWave", name, [i], [o], cout=w_bits.shape[0], weights=w_bits,
+                       bias=b_bits, rows=np.asarray(starts), cluster=tile, act=act,
+                       residual=residual, seg_len=S))
+
     def concat(self, name, ins, o):
         self._add(Node("Concat", name, ins, [o]))
 
@@ -149,6 +155,52 @@ class Graph:
         self._add(Node("SwiGLU", name, [g, u], [o]))
 
 
+def pruned_parts(starts: np.ndarray, S: int, w: np.ndarray, bias: np.ndarray, tile: int):
+    """Pattern-sorted tiles of a pruned projection (restatement of the build's
+    K44WaveGraphCompiler::add_pruned_wave): neurons grouped by their sorted cluster pattern
+    (groups in lexicographic order), full tiles per group, the groups' remainders packed in order
+    into tiles whose index row is the union of their clusters, one part per union size
+    (ascending).  Returns [(union starts [tiles][U], weights [tiles*tile][U*S] u16,
+    bias [tiles*tile] u16, cmap [tiles*tile] u16 (0xFFFF = empty))]."""
+    cout, K = starts.shape
+    order = np.argsort(starts, axis=1, kind="stable")
+    pat = np.take_along_axis(starts, order, axis=1)
+    groups = {}
+    for j in range(cout):
+        groups.setdefault(tuple(int(v) for v in pat[j]), []).append(j)
+    tiles, rest = [], []
+    for key in sorted(groups):
+        g = groups[key]
+        full = len(g) // tile
+        for f in range(full):
+            tiles.append((g[f * tile:(f + 1) * tile], list(key)))
+        rest += g[full * tile:]
+    for b in range(0, len(rest), tile):
+        slots = rest[b:b + tile]
+        uni = sorted({int(v) for j in slots for v in pat[j]})
+        tiles.append((slots + [-1] * (tile - len(slots)), uni))
+    parts = []
+    for U in sorted({len(t[1]) for t in tiles}):
+        sel = [t for t in tiles if len(t[1]) == U]
+        rows = np.array([t[1] for t in sel], dtype=np.uint32)
+        wp = np.zeros((len(sel) * tile, U * S), dtype=np.uint16)
+        bp = np.zeros(len(sel) * tile, dtype=np.uint16)
+        cm = np.full(len(sel) * tile, 0xFFFF, dtype=np.uint16)
+        for ti, (slots, uni) in enumerate(sel):
+            for q, j in enumerate(slots):
+                if j < 0:
+                    continue
+                r = ti * tile + q
+                cm[r], bp[r] = j, bias[j]
+                for k, u in enumerate(uni):
+                    hit = np.nonzero(starts[j] == u)[0]
+                    if hit.size:
+                        src = int(hit[0])
+                        wp[r, k * S:(k + 1) * S] = w[j, src * S:(src + 1) * S]
+        parts.append((rows, wp, bp, cm))
+    return parts
+
+
 def compile_plan(g: Graph) -> dict:
     nodes = g.nodes
     if nodes and nodes[0].op == "Input" and nodes[0].is_1d and g.batch > 1 and nodes[0].w_out == 1:
@@ -159,9 +211,9 @@ def compile_plan(g: Graph) -> dict:
             assert n.is_1d
             shapes[n.outs[0]] = (n.cout, n.h_out, n.w_out)
             plan_in = (n.cout, n.h_out, n.w_out)
-        elif n.op in ("Convolution", "SparseWave"):
+        elif n.op in ("Convolution", "SparseWave", "PrunedWave"):
             c, h, w = shapes[n.ins[0]]
-            if n.op == "SparseWave":
+            if n.op in ("SparseWave", "PrunedWave"):
                 n.cin = c
             n.h_in, n.w_in, n.h_out, n.w_out = h, w, 1, w
             shapes[n.outs[0]] = (n.cout, 1, w)
@@ -280,6 +332,48 @@ def compile_plan(g: Graph) -> dict:
             key, ch, at = allocs[out_aid[i]]
             chan[n.outs[0]] = [at + c * res[key].channel_stride for c in range(n.cout)]
             plan["cmds"].append({"type": 7 if n.op == "RMSNorm" else 8, "name": n.name})
+        elif n.op == "PrunedWave":
+            key, ch, dst = allocs[out_aid[i]]
+            Lo = res[key]
+            chan[n.outs[0]] = [dst + c * Lo.channel_stride for c in range(n.cout)]
+            in_chs = np.asarray(chan[n.ins[0]], dtype=np.uint64)
+            has_res = bool(n.residual)
+            res_off = chan[n.residual][0] if has_res else 0
+            S = n.seg_len
+            parts = pruned_parts(n.rows, S, n.weights, n.bias, n.cluster)
+            for p, (rows_u, wp, bp, cm) in enumerate(parts):
+                slots, U = wp.shape[0], rows_u.shape[1]
+                b_raw = U * S
+                B = round_up_32(b_raw)
+                lcm = 16 * n.cluster // math.gcd(16, n.cluster)
+                cout_pad = (slots + lcm - 1) // lcm * lcm
+                syn = (rows_u[:, :, None].astype(np.int64) + np.arange(S)[None, None, :]).reshape(
+                    rows_u.shape[0], b_raw)
+                idx = np.zeros((cout_pad // n.cluster, B), dtype=np.uint64)
+                idx[: syn.shape[0], :b_raw] = in_chs[syn]
+                w = np.zeros((cout_pad, B), dtype=np.uint16)
+                w[:slots, :b_raw] = wp
+                bias = np.zeros(cout_pad, dtype=np.uint16)
+                bias[:slots] = bp
+                cmap = np.full(cout_pad, 0xFFFF, dtype=np.uint16)
+                cmap[:slots] = cm
+                x_base = 0
+                real = idx[:, :b_raw]
+                if int(real.max()) >= 0x70000000:
+                    x_base = int(real.min()) & ~63
+                    idx[:, :b_raw] -= np.uint64(x_base)
+                    idx[:, b_raw:] = 0
+                plan["total_w_bytes"] += cout_pad * B * 2
+                plan["total_idx_bytes"] += idx.size * 4 + cout_pad * 2 + cout_pad * 2
+                plan["cmds"].append({
+                    "type": 0, "name": n.name if len(parts) == 1 else f"{n.name}/{p}",
+                    "Cin": n.cin, "Cout": cout_pad, "logical_Cout": n.cout,
+                    "cluster": n.cluster, "B": B, "B_raw": b_raw, "act": n.act,
+                    "has_res": has_res, "h_out": 1, "w_out": n.w_out, "src_off": int(in_chs[0]),
+                    "y_off": dst, "res_off": res_off, "x_base_off": x_base, "idx_mode": 0,
+                    "idx_stride": 1, "seg_len": S, "idx": idx.astype(np.uint32), "w_rows": w,
+                    "bias": bias, "cmap": cmap, "out_stride": Lo.channel_stride,
+                })
         elif n.op in ("Convolution", "SparseWave"):
             key, ch, dst = allocs[out_aid[i]]
             Lo = res[key]

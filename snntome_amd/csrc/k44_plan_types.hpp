@@ -470,6 +470,13 @@ struct K44IRNode {
     uint32_t cluster = 1;        // neurons sharing one index row
     uint32_t seg_len = 0;        // positions per dendritic cluster (hint, 0 = unknown)
     std::vector<uint32_t> rows;  // [cout/cluster][fan_in] input channel index of every synapse
+    // --- build extension: pattern-sorted pruned projection ("PrunedWave"): sub-wave p has
+    // part_tiles[p] tiles of `cluster` slots whose index rows are part_k[p] segments of seg_len
+    // channels; rows holds the segment starts of every tile, weights_f16 / bias_f16 / cout_map the
+    // slots of every sub-wave in order (cout_map 0xFFFF = empty slot, no output). ---
+    std::vector<uint32_t> part_tiles, part_k;
+    std::vector<uint16_t> cout_map;
+    uint64_t nnz = 0;  // real synapses (cout x K x seg_len): the effective FLOP count
     // --- build extension: 1-D token ops ("TokenShift", "Embedding", "ArgMax") ---
     uint32_t rf = 0, seq_len = 0, vocab = 0;
     bool decode_state = false;

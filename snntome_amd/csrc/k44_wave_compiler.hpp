@@ -15,7 +15,9 @@
 // whose offsets do not fit the reference's u32 index words is emitted in row-index mode
 // (K44ExecCmd::idx_mode = 1).
 #pragma once
+#include <map>
 #include <numeric>
+#include <set>
 #include <stdexcept>
 
 #include "k44_plan_types.hpp"
@@ -159,7 +161,7 @@ class K44WaveGraphCompiler {
                 n.h_out = s.is_1d ? 1u : s.h / n.stride;
                 n.w_out = s.is_1d ? s.w : s.w / n.stride;
                 shapes[n.out_tensors[0]] = {n.cout, n.h_out, n.w_out, s.is_1d};
-            } else if (op == "SparseWave") {
+            } else if (op == "SparseWave" || op == "PrunedWave") {
                 const Shape3D s = in_shape();
                 if (!s.is_1d)
                     throw std::runtime_error("sparse wave '" + n.name +
@@ -349,7 +351,7 @@ class K44WaveGraphCompiler {
                 const int id = next_id++;
                 const uint32_t ch = (n.op_type == "Convolution" || n.op_type == "SparseWave")
                                         ? cfg[i].total_cout_pad()
-                                        : n.cout;
+                                        : n.cout;  // PrunedWave: mapped stores, no padding
                 allocs[id] = {make_res_key(n.h_out, n.w_out, n.is_1d_tokens), ch, 0u};
                 ids[n.out_tensors[0]] = {id};
                 out_aid[i] = id;
@@ -652,24 +654,40 @@ class K44WaveGraphCompiler {
         plan.num_wave_dispatches++;
     }
 
-    // Sparse wave (build extension).  Index row r of the wave lists the input channel of every
-    // synapse; its canvas offsets come from the input tensor's channel offset list, so views
-    // (Concat / Slice) work as they do for dense waves.
-    void emit_sparse_wave(K44IRNode &n, const K44WaveConfig &wc, uint32_t rkey_in,
+    // One K44_WAVE over explicit index rows (build extension): `cout` neurons, neurons
+    // [r*cluster, (r+1)*cluster) share row r, which lists the input channel of each of the fan_in
+    // synapses.  Canvas offsets come from the input tensor's channel offset list, so views
+    // (Concat / Slice) work as they do for dense waves.  cmap (optional, one entry per neuron)
+    // sends neuron j to output channel cmap[j]; 0xFFFF marks an empty slot that stores nothing.
+    struct SparseRows {
+        std::string name;
+        uint32_t cout, fan_in, cluster, seg_len;
+        const uint32_t *rows;   // [cout/cluster][fan_in]
+        const uint16_t *w;      // [cout][fan_in]
+        const uint16_t *bias;   // [cout] or nullptr
+        std::vector<uint16_t> cmap;
+        uint64_t nnz;           // real synapses (effective FLOPs = 2 nnz tokens)
+    };
+
+    void emit_sparse_rows(const K44IRNode &n, const SparseRows &sr, uint32_t rkey_in,
                           uint32_t rkey_out, uint64_t dst_off, const ChanMap &chan,
                           K44WavePlan &plan) {
         const K44ResDesc &Lo = plan.res_map.at(rkey_out);
         const std::vector<uint64_t> &in_chs = chan.at(n.in_tensors[0]);
         const bool has_res = !n.residual_tensor.empty();
         const uint64_t res_off = has_res ? chan.at(n.residual_tensor)[0] : 0u;
-        const uint32_t cout_pad = wc.Cout_pad1, cl = std::max(1u, n.cluster);
-        if (has_res) reserve_residual(plan, res_off, cout_pad, Lo.channel_stride);
-        const uint32_t b_raw = n.fan_in, B = round_up_32(b_raw);
-        const uint32_t rows_real = n.cout / cl, rows = cout_pad / cl;
+        const uint32_t cl = std::max(1u, sr.cluster);
+        const uint32_t cout_pad =
+            (uint32_t)round_up(sr.cout, std::lcm<uint64_t>(16u, cl));
+        const bool mapped = !sr.cmap.empty();
+        if (has_res && !mapped) reserve_residual(plan, res_off, cout_pad, Lo.channel_stride);
+        const uint32_t b_raw = sr.fan_in, B = round_up_32(b_raw);
+        const uint32_t rows_real = sr.cout / cl, rows = cout_pad / cl;
         uint64_t hi_off = 0u;
-        for (uint32_t p : n.rows) {
+        for (size_t i = 0; i < (size_t)rows_real * b_raw; ++i) {
+            const uint32_t p = sr.rows[i];
             if (p >= in_chs.size())
-                throw std::runtime_error("sparse wave '" + n.name +
+                throw std::runtime_error("sparse wave '" + sr.name +
                                          "': synapse position beyond the input channel count");
             hi_off = std::max(hi_off, in_chs[p]);
         }
@@ -679,24 +697,30 @@ class K44WaveGraphCompiler {
             for (size_t c = 0; c < in_chs.size(); ++c)
                 if (in_chs[c] != in_chs[0] + c * stride)
                     throw std::runtime_error(
-                        "sparse wave '" + n.name +
+                        "sparse wave '" + sr.name +
                         "': input beyond 2^32 canvas elements must be one contiguous tensor");
         }
         std::vector<uint32_t> idx((size_t)rows * B, 0u);
         for (uint32_t r = 0; r < rows_real; ++r)
             for (uint32_t s = 0; s < b_raw; ++s) {
-                const uint32_t p = n.rows[(size_t)r * b_raw + s];
+                const uint32_t p = sr.rows[(size_t)r * b_raw + s];
                 idx[(size_t)r * B + s] = row_mode ? p : (uint32_t)in_chs[p];
             }
         std::vector<uint16_t> w((size_t)cout_pad * B, 0u), bias(cout_pad, 0u);
-        for (uint32_t j = 0; j < n.cout; ++j) {
-            std::memcpy(&w[(size_t)j * B], &n.weights_f16[(size_t)j * b_raw], b_raw * 2u);
-            if (j < n.bias_f16.size()) bias[j] = n.bias_f16[j];
+        for (uint32_t j = 0; j < sr.cout; ++j) {
+            std::memcpy(&w[(size_t)j * B], &sr.w[(size_t)j * b_raw], b_raw * 2u);
+            if (sr.bias) bias[j] = sr.bias[j];
+        }
+        std::vector<uint16_t> cmap;
+        if (mapped) {
+            cmap = sr.cmap;
+            cmap.resize(cout_pad, 0xffffu);
         }
         K44ExecCmd c =
             make_base_cmd(n, K44CmdType::K44_WAVE, rkey_in, rkey_out, in_chs[0], dst_off);
+        c.name = sr.name;
         c.Cout = cout_pad;
-        c.logical_Cout = n.cout;
+        c.logical_Cout = mapped ? n.cout : sr.cout;
         c.cluster_size = cl;
         c.B = B;
         c.B_raw = b_raw;
@@ -705,17 +729,68 @@ class K44WaveGraphCompiler {
         c.act = n.act;
         c.has_residual = has_res;
         c.res_off = has_res ? res_off : 0u;
-        c.seg_len = n.seg_len;
+        c.seg_len = sr.seg_len;
         c.idx_mode = row_mode ? 1u : 0u;
         c.idx_stride = row_mode ? stride : 1u;
-        const double sf = 2.0 * b_raw * (double)n.cout * (double)(n.h_out * n.w_out) / 1e9;
+        const double sf = 2.0 * (double)sr.nnz * (double)(n.h_out * n.w_out) / 1e9;
         c.gflops = (double)plan.wave_batch_size * sf;
         plan.single_frame_gflops += sf;
         plan.total_gflops += c.gflops;
-        pack_wave_buffers(c, w, idx, bias, plan);
+        pack_wave_buffers(c, w, idx, bias, plan, cmap);
         if (row_mode) c.x_base_off = in_chs[0];
         plan.cmds.push_back(std::move(c));
         plan.num_wave_dispatches++;
+    }
+
+    void emit_sparse_wave(K44IRNode &n, uint32_t rkey_in, uint32_t rkey_out, uint64_t dst_off,
+                          const ChanMap &chan, K44WavePlan &plan) {
+        SparseRows sr{n.name,        n.cout,
+                      n.fan_in,      std::max(1u, n.cluster),
+                      n.seg_len,     n.rows.data(),
+                      n.weights_f16.data(), n.bias_f16.empty() ? nullptr : n.bias_f16.data(),
+                      {},            (uint64_t)n.cout * n.fan_in};
+        emit_sparse_rows(n, sr, rkey_in, rkey_out, dst_off, chan, plan);
+    }
+
+    // Pattern-sorted pruned projection: one K44_WAVE per sub-wave, all writing the node's output
+    // tensor through their cout_map.
+    void emit_pruned_wave(K44IRNode &n, uint32_t rkey_in, uint32_t rkey_out, uint64_t dst_off,
+                          const ChanMap &chan, K44WavePlan &plan) {
+        const uint32_t tile = n.cluster, S = n.seg_len;
+        size_t row_at = 0, slot_at = 0;
+        std::vector<uint32_t> rows;
+        for (size_t p = 0; p < n.part_tiles.size(); ++p) {
+            const uint32_t tiles = n.part_tiles[p], K = n.part_k[p], fan = K * S;
+            rows.assign((size_t)tiles * fan, 0u);
+            for (uint32_t t = 0; t < tiles; ++t)
+                for (uint32_t k = 0; k < K; ++k)
+                    for (uint32_t s = 0; s < S; ++s)
+                        rows[((size_t)t * K + k) * S + s] = n.rows[row_at + (size_t)t * K + k] + s;
+            const uint32_t slots = tiles * tile;
+            uint64_t real = 0;
+            for (uint32_t j = 0; j < slots; ++j) real += n.cout_map[slot_at + j] != 0xffffu;
+            SparseRows sr{n.part_tiles.size() > 1u ? n.name + "/" + std::to_string(p) : n.name,
+                          slots,
+                          fan,
+                          tile,
+                          S,
+                          rows.data(),
+                          n.weights_f16.data() + n_weights_before(n, p),
+                          n.bias_f16.data() + slot_at,
+                          std::vector<uint16_t>(n.cout_map.begin() + slot_at,
+                                                n.cout_map.begin() + slot_at + slots),
+                          real * (n.nnz / std::max<uint32_t>(1u, n.cout))};
+            emit_sparse_rows(n, sr, rkey_in, rkey_out, dst_off, chan, plan);
+            row_at += (size_t)tiles * K;
+            slot_at += slots;
+        }
+    }
+
+    static size_t n_weights_before(const K44IRNode &n, size_t part) {
+        size_t at = 0;
+        for (size_t p = 0; p < part; ++p)
+            at += (size_t)n.part_tiles[p] * n.cluster * n.part_k[p] * n.seg_len;
+        return at;
     }
 
     // ---------------------------------------------------------------------------------------
@@ -861,7 +936,12 @@ class K44WaveGraphCompiler {
                 const uint32_t rk_in = make_res_key(n.h_in, n.w_in, true);
                 const uint32_t rk_out = allocs.at(id).res_key;
                 const uint64_t dst = place(n, id, n.cout);
-                emit_sparse_wave(n, cfg[i], rk_in, rk_out, dst, chan, plan);
+                emit_sparse_wave(n, rk_in, rk_out, dst, chan, plan);
+            } else if (op == "PrunedWave") {
+                const uint32_t rk_in = make_res_key(n.h_in, n.w_in, true);
+                const uint32_t rk_out = allocs.at(id).res_key;
+                const uint64_t dst = place(n, id, n.cout);
+                emit_pruned_wave(n, rk_in, rk_out, dst, chan, plan);
             }
         }
         auto it = chan.find(default_output_tensor);
@@ -935,6 +1015,7 @@ class K44WaveGraphCompiler {
         }
         c.h_bias = bias;
         c.h_cout_map = cout_map;
+        c.has_cout_map = !cout_map.empty();
     }
 
     void add_input(const std::string &name, uint32_t ch, uint32_t h, uint32_t w,
@@ -1187,6 +1268,126 @@ class K44WaveGraphCompiler {
                 for (uint32_t s = 0; s < S; ++s) rows[r * fan + (size_t)k * S + s] = starts[r * K + k] + s;
         add_sparse_wave(name, in, out, cout, (uint32_t)fan, cluster, rows.data(), w_f16, bias_f16,
                         act, res, S);
+    }
+
+    // Build extension: projection whose neurons each keep their own K dendritic clusters of S
+    // consecutive input channels (starts: [cout][K], w_f16: [cout][K*S] in the same cluster
+    // order).  Compiled into pattern-sorted tiles of `tile` neurons for dense MFMA tiles:
+    //   1. each neuron's clusters are sorted by start (weight segments move with them);
+    //   2. neurons are grouped by identical cluster pattern, groups in lexicographic pattern
+    //      order, neurons of a group in index order;
+    //   3. every group contributes floor(n / tile) full tiles of its own pattern; the remainders
+    //      of all groups, in group order, are cut into tiles of `tile` slots (the last one
+    //      partly empty), whose index row is the sorted union of their neurons' clusters;
+    //   4. tiles are gathered into one sub-wave per union size (ascending); a neuron's weights
+    //      are zero on the clusters of the union it does not keep; each sub-wave's cout_map
+    //      sends slot j to the neuron's own output channel (0xFFFF: empty slot).
+    // The output keeps the caller's channel order; the cout_map epilogue is y = act(v + r).
+    void add_pruned_wave(const std::string &name, const std::string &in, const std::string &out,
+                         uint32_t cout, uint32_t K, uint32_t S, uint32_t tile,
+                         const uint32_t *starts, const uint16_t *w_f16, const uint16_t *bias_f16,
+                         K44Act act, const std::string &res = "") {
+        if (cout == 0u || cout >= 0xffffu || K == 0u || S == 0u || tile == 0u || !starts ||
+            !w_f16)
+            throw std::invalid_argument("add_pruned_wave: need 0 < cout < 65535, K, S, tile > 0, "
+                                        "cluster starts and weights");
+        const size_t fan = (size_t)K * S;
+        // 1. per-neuron sorted pattern + the source cluster of each sorted position
+        std::vector<uint32_t> pat((size_t)cout * K), src((size_t)cout * K);
+        for (uint32_t j = 0; j < cout; ++j) {
+            uint32_t *pj = &pat[(size_t)j * K], *sj = &src[(size_t)j * K];
+            std::iota(sj, sj + K, 0u);
+            std::sort(sj, sj + K, [&](uint32_t a, uint32_t b) {
+                return starts[(size_t)j * K + a] < starts[(size_t)j * K + b];
+            });
+            for (uint32_t k = 0; k < K; ++k) {
+                pj[k] = starts[(size_t)j * K + sj[k]];
+                if (k && pj[k] < pj[k - 1] + S)
+                    throw std::invalid_argument("add_pruned_wave '" + name +
+                                                "': clusters of a neuron overlap");
+            }
+        }
+        // 2. groups by pattern, lexicographic
+        std::map<std::vector<uint32_t>, std::vector<uint32_t>> groups;
+        for (uint32_t j = 0; j < cout; ++j)
+            groups[std::vector<uint32_t>(pat.begin() + (size_t)j * K,
+                                         pat.begin() + (size_t)(j + 1) * K)]
+                .push_back(j);
+        // 3. full tiles, then remainder tiles; each tile = slots (neuron or -1) + union row
+        struct Tile {
+            std::vector<int64_t> slots;
+            std::vector<uint32_t> uni;
+        };
+        std::vector<Tile> tiles;
+        std::vector<uint32_t> rest;
+        for (const auto &g : groups) {
+            const size_t full = g.second.size() / tile;
+            for (size_t f = 0; f < full; ++f) {
+                Tile t;
+                t.slots.assign(g.second.begin() + f * tile, g.second.begin() + (f + 1) * tile);
+                t.uni = g.first;
+                tiles.push_back(std::move(t));
+            }
+            rest.insert(rest.end(), g.second.begin() + full * tile, g.second.end());
+        }
+        for (size_t b = 0; b < rest.size(); b += tile) {
+            Tile t;
+            std::set<uint32_t> u;
+            for (size_t q = b; q < b + tile; ++q) {
+                if (q < rest.size()) {
+                    t.slots.push_back(rest[q]);
+                    u.insert(pat.begin() + (size_t)rest[q] * K,
+                             pat.begin() + (size_t)(rest[q] + 1) * K);
+                } else {
+                    t.slots.push_back(-1);
+                }
+            }
+            t.uni.assign(u.begin(), u.end());
+            tiles.push_back(std::move(t));
+        }
+        // 4. one sub-wave per union size
+        std::map<size_t, std::vector<size_t>> by_size;
+        for (size_t i = 0; i < tiles.size(); ++i) by_size[tiles[i].uni.size()].push_back(i);
+        K44IRNode n;
+        n.op_type = "PrunedWave";
+        n.name = name;
+        n.in_tensors = {in};
+        n.out_tensors = {out};
+        n.cout = cout;
+        n.cluster = tile;
+        n.seg_len = S;
+        n.fan_in = (uint32_t)fan;
+        n.act = act;
+        n.residual_tensor = res;
+        n.nnz = (uint64_t)cout * fan;
+        for (const auto &bs : by_size) {
+            const uint32_t U = (uint32_t)bs.first;
+            n.part_tiles.push_back((uint32_t)bs.second.size());
+            n.part_k.push_back(U);
+            for (size_t ti : bs.second) {
+                const Tile &t = tiles[ti];
+                n.rows.insert(n.rows.end(), t.uni.begin(), t.uni.end());
+                for (int64_t j : t.slots) {
+                    const size_t at = n.weights_f16.size();
+                    n.weights_f16.resize(at + (size_t)U * S, 0u);
+                    if (j < 0) {
+                        n.bias_f16.push_back(0u);
+                        n.cout_map.push_back(0xffffu);
+                        continue;
+                    }
+                    const uint32_t *pj = &pat[(size_t)j * K], *sj = &src[(size_t)j * K];
+                    for (uint32_t k = 0, q = 0; k < U; ++k) {
+                        while (q < K && pj[q] < t.uni[k]) ++q;
+                        if (q < K && pj[q] == t.uni[k])
+                            std::memcpy(&n.weights_f16[at + (size_t)k * S],
+                                        &w_f16[(size_t)j * fan + (size_t)sj[q] * S], S * 2u);
+                    }
+                    n.bias_f16.push_back(bias_f16 ? bias_f16[j] : (uint16_t)0u);
+                    n.cout_map.push_back((uint16_t)j);
+                }
+            }
+        }
+        append_node_to_graph(std::move(n));
     }
 
     // Build extension: causal depth-wise token mix y[c][t] = sum_{i<rf} mu[c][i] x[c][t-i] within

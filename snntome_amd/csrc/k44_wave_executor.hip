@@ -87,7 +87,8 @@ struct WaveExec {
     uint64_t y_off = 0, res_off = 0;
     int act = 0;
     bool has_res = false;
-    double flops = 0.0;          // 2 * nnz * tokens (padded neurons included)
+    double flops = 0.0;          // executed: 2 * Cout * B_raw * tokens (padding included)
+    double eff_flops = 0.0;      // 2 * real synapses * valid tokens (the plan's gflops)
     uint64_t unique_rows = 0;    // distinct substrate positions read
     DevBuf<uint64_t> seg;
     DevBuf<__half> w, bias;
@@ -275,7 +276,9 @@ struct K44GpuExecutorState {
         uint64_t oj_hi = c.Cout - 1u;
         if (c.has_cout_map) {
             oj_hi = 0;
-            for (uint32_t j = 0; j < c.Cout; ++j) oj_hi = std::max<uint64_t>(oj_hi, c.h_cout_map[j]);
+            for (uint32_t j = 0; j < c.Cout; ++j)
+                if (c.h_cout_map[j] != 0xffffu)  // empty slot: the kernels store nothing
+                    oj_hi = std::max<uint64_t>(oj_hi, c.h_cout_map[j]);
         }
         const uint64_t span = oj_hi * wx.out_stride + wx.tokens;
         if (wx.y_off + span > n_canvas || (wx.has_res && wx.res_off + span > n_canvas))
@@ -387,6 +390,7 @@ struct K44GpuExecutorState {
         if (c.has_cout_map)
             wx.cmap.upload(std::vector<uint16_t>(c.h_cout_map.begin(), c.h_cout_map.begin() + c.Cout));
         wx.flops = 2.0 * (double)c.Cout * c.B_raw * wx.tokens;
+        wx.eff_flops = c.gflops * 1e9;
     }
 
     void build_aux(const K44ExecCmd &c, AuxExec &ax) {
@@ -552,7 +556,10 @@ struct K44GpuExecutorState {
               << ", \"tokens\": " << w.tokens << ", \"slab\": " << (w.mfma ? w.mt : w.slab)
               << ", \"U\": " << (w.mfma ? w.rows_per_stage : w.U) << ", \"ksplit\": " << w.ksplit
               << ", \"sorted_segments\": " << (w.sorted_segments ? "true" : "false")
-              << ", \"flops\": " << (long long)w.flops << ", \"unique_rows\": " << w.unique_rows
+              << ", \"flops\": " << (long long)w.flops
+              << ", \"effective_flops\": " << (long long)w.eff_flops
+              << ", \"mapped\": " << (w.cmap.p ? "true" : "false")
+              << ", \"unique_rows\": " << w.unique_rows
               << ", \"y_off\": " << w.y_off << "}";
         }
         o << "], \"aux\": [";
@@ -1047,6 +1054,18 @@ int wavec_add_cluster_wave(void *h, const char *name, const char *in, const char
         comp_of(h)->add_cluster_wave(name, in, out, (uint32_t)cout, (uint32_t)K, (uint32_t)S,
                                      (uint32_t)cluster, starts, w_f16, bias_f16, (K44Act)act,
                                      opt_str(residual));
+        return 0;
+    });
+}
+
+int wavec_add_pruned_wave(void *h, const char *name, const char *in, const char *out, int cout,
+                          int K, int S, int tile, const uint32_t *starts, const uint16_t *w_f16,
+                          const uint16_t *bias_f16, int act, const char *residual) {
+    if (!h || !name || !in || !out || cout <= 0 || K <= 0 || S <= 0 || tile <= 0) return -1;
+    return guarded("wavec_add_pruned_wave", [&] {
+        comp_of(h)->add_pruned_wave(name, in, out, (uint32_t)cout, (uint32_t)K, (uint32_t)S,
+                                    (uint32_t)tile, starts, w_f16, bias_f16, (K44Act)act,
+                                    opt_str(residual));
         return 0;
     });
 }

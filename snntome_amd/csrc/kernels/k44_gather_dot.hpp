@@ -4,7 +4,8 @@
 // kernels/rocm/kernel44_rocm_pack.cuh:145-237, re-designed for CDNA4):
 //   v[j][m] = bias[j] + sum_k sum_s W[j][k*S+s] * X[seg[j/cluster][k] + s*step + m]
 //   y       = cmap ? act(v + r) : act(v) + r        (r = residual, 0 if none)
-//   Y[y_off + out_j*out_stride + m] = fp16_rne(y)
+//   Y[y_off + out_j*out_stride + m] = fp16_rne(y),  out_j = cmap ? cmap[j] : j
+//   (cmap[j] = 0xFFFF: empty slot, nothing stored)
 // Used for waves whose neurons do not share index rows (per-neuron dendritic clusters): there
 // is no dense contraction to hand to MFMA, the wave is a batched GEMV streaming 2*M bytes per
 // gathered position, bound by HBM (or MALL/L2 when the substrate is cache resident).
@@ -25,6 +26,10 @@
 namespace k44dev {
 
 enum : int { ACT_NONE = 0, ACT_RELU = 1, ACT_SIGMOID = 2, ACT_SILU = 3, ACT_LEAKY = 4, ACT_GELU = 5 };
+
+// cout_map entry of an empty slot (a pattern-sorted tile with fewer neurons than slots): the
+// epilogue stores nothing for it.
+constexpr uint64_t K44_CMAP_EMPTY = 0xffffu;
 
 __device__ __forceinline__ float apply_act(float v, int act) {
     switch (act) {
@@ -146,6 +151,7 @@ __global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
 
     const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
     const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
+    if (oj == K44_CMAP_EMPTY) return;  // empty slot of a pattern-sorted tile: no output
     const uint64_t o = oj * a.out_stride + slab0 + 4u * (uint32_t)c;
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.R) {

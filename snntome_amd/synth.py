@@ -207,10 +207,11 @@ class LLMSpec:
         q = sigmoid(Wq s);  k = silu(Wk s);  v = Wv s;  m = q * (k * v)
         x = x + Wo m
         n = RMSNorm(x);  h = silu(Wg n) * (Wu n);  x = x + Wd h
-    then logits = Whead RMSNorm(x), next id = argmax.  Every projection is a dendritic-cluster
-    wave: its input row is split into clusters of S consecutive channels and a random `keep`
-    fraction of them is kept, drawn per tile of `tile` output neurons (neurons of a tile share
-    their cluster pattern, which makes every tile a dense MFMA contraction).  RMSNorm gamma = 1."""
+    then logits = Whead RMSNorm(x), next id = argmax.  Every projection is a pruned wave: its
+    input row is cut into clusters of S consecutive channels and every neuron keeps its own
+    random `keep` fraction of them (2 of 4 for d-wide inputs, 6 of 11 for FFN-wide inputs at the
+    default sizes); the compiler groups neurons into pattern-sorted tiles of `tile` for MFMA.
+    RMSNorm gamma = 1."""
     layers: int = 16
     d: int = 2048
     ffn: int = 5632
@@ -237,7 +238,7 @@ class LLMSpec:
 
 @dataclass
 class Projection:
-    starts: np.ndarray  # [cout/tile, K] uint32 first input channel of each kept cluster
+    starts: np.ndarray  # [cout, K] uint32 first input channel of each cluster neuron j keeps
     weights: np.ndarray  # [cout, K*S] fp16
     bias: np.ndarray  # [cout] fp16
 
@@ -245,9 +246,8 @@ class Projection:
 def _projection(rng, spec: LLMSpec, fan_in: int, cout: int) -> Projection:
     n_cl = fan_in // spec.S
     K = spec.kept(fan_in)
-    tiles = cout // spec.tile
-    pick = np.argsort(rng.random((tiles, n_cl)), axis=1)[:, :K]
-    starts = (np.sort(pick, axis=1) * spec.S).astype(np.uint32)
+    pick = np.argsort(rng.random((cout, n_cl)), axis=1)[:, :K]  # K distinct clusters per neuron
+    starts = (pick * spec.S).astype(np.uint32)  # random order: the compiler sorts them
     sigma = 1.0 / np.sqrt(K * spec.S)
     w = (rng.standard_normal((cout, K * spec.S), dtype=np.float32) * np.float32(sigma)).astype(
         np.float16)
@@ -294,8 +294,8 @@ def build_llm_graph(spec: LLMSpec, wts: LLMWeights, decode: bool, wavec_mod=None
     ones = np.ones(spec.d, np.float32)
 
     def proj(name, src, out, p: Projection, act=None, res=None):
-        g.add_cluster_wave(name, src, out, p.starts, spec.S, p.weights, p.bias,
-                           cluster=spec.tile, act=act, res_blob=res)
+        g.add_pruned_wave(name, src, out, p.starts, spec.S, p.weights, p.bias, tile=spec.tile,
+                          act=act, res_blob=res)
 
     x = "x0"
     for l in range(spec.layers):

@@ -66,6 +66,7 @@ _SIGNATURES = {
     "wavec_last_error": (_cp, []),
     "wavec_add_sparse_wave": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _pu32, _pu16, _pu16, _i, _cp]),
     "wavec_add_cluster_wave": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _i, _pu32, _pu16, _pu16, _i, _cp]),
+    "wavec_add_pruned_wave": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _i, _pu32, _pu16, _pu16, _i, _cp]),
     "wavec_gpu_fill_input_uniform": (_i, [_vp, _ull]),
     "wavec_gpu_execute": (_i, [_vp, _i, _pf]),
     "wavec_gpu_sync": (_i, [_vp]),
@@ -448,6 +449,25 @@ class WaveGraph:
             int(seg_len), int(cluster), _ptr(st, ctypes.c_uint32), _ptr(w, ctypes.c_uint16),
             _ptr(b, ctypes.c_uint16), ACT_MAP.get(act, 0),
             res_blob.encode() if res_blob else None), "wavec_add_cluster_wave")
+        return out_blob
+
+    def add_pruned_wave(self, name: str, in_blob: str, out_blob: str, starts: np.ndarray,
+                        seg_len: int, weights: np.ndarray, bias: Optional[np.ndarray] = None,
+                        tile: int = 64, act: Optional[str] = None,
+                        res_blob: Optional[str] = None) -> str:
+        """starts: [cout, K] first input channel of each cluster neuron j keeps; weights
+        [cout, K*seg_len] in the same cluster order.  Compiled to pattern-sorted tiles."""
+        w = _f16_bits(weights)
+        st = np.ascontiguousarray(starts, dtype=np.uint32)
+        cout, K = st.shape
+        if w.shape != (cout, K * seg_len):
+            raise ValueError("starts / weights shapes do not match cout, K, seg_len")
+        b = _f16_bits(bias) if bias is not None else None
+        _check(self._lib.wavec_add_pruned_wave(
+            self._handle, name.encode(), in_blob.encode(), out_blob.encode(), int(cout), int(K),
+            int(seg_len), int(tile), _ptr(st, ctypes.c_uint32), _ptr(w, ctypes.c_uint16),
+            _ptr(b, ctypes.c_uint16), ACT_MAP.get(act, 0),
+            res_blob.encode() if res_blob else None), "wavec_add_pruned_wave")
         return out_blob
 
     def add_token_shift(self, name: str, in_blob: str, out_blob: str, mu: np.ndarray,

@@ -40,34 +40,48 @@ def _projections(spec, wts):
     return out
 
 
+def _groups(cmds):
+    """Consecutive commands of one graph node (the sub-waves "name/0", "name/1", ... of a pruned
+    projection) -> [(node name, first index, count, first cmd)]."""
+    out = []
+    for i, c in enumerate(cmds):
+        base = c["name"].split("/")[0]
+        if out and out[-1][0] == base:
+            out[-1][2] += 1
+        else:
+            out.append([base, i, 1, c])
+    return out
+
+
 def _check_commands(plan, spec, wts, ids, decode, tag):
-    """Runs the plan command by command; each output is compared with the CPU restatement of
-    that command applied to the canvas contents the command read."""
+    """Runs the plan node by node; each node's output is compared with the CPU restatement of
+    that node applied to the canvas contents it read."""
     valid = len(ids)
     T = stride_of(valid)
     projs = _projections(spec, wts)
     mixes = {f"l{l}.shift": wts.mix[l] for l in range(spec.layers)}
     plan.set_ids(ids)
     worst = {}
-    for i, c in enumerate(plan.cmds):
-        typ, name = c["type"], c["name"]
+    for name, first, count, c in _groups(plan.cmds):
+        typ = c["type"]
+        cout = c["logical_Cout"]
         if typ == "K44_WAVE":
             x = _read(plan, c["src_off"], c["Cin"], T)
-            res = _read(plan, c["res_off"], c["Cout"], T) if c["has_residual"] else None
+            res = _read(plan, c["res_off"], cout, T) if c["has_residual"] else None
         elif typ in ("RMSNORM_1D", "TOKEN_SHIFT_1D", "ARGMAX_1D"):
             x = _read(plan, c["src_off"], c["Cin"], T)
         elif typ == "SWIGLU_MUL_1D":
-            a = _read(plan, c["src_off"], c["Cout"], T)
-            b = _read(plan, c["src2_off"], c["Cout"], T)
+            a = _read(plan, c["src_off"], cout, T)
+            b = _read(plan, c["src2_off"], cout, T)
         if typ == "TOKEN_SHIFT_1D" and decode:
             st_in = _read(plan, c["state_off"], spec.d * (spec.rf - 1), 64).reshape(
                 spec.d, spec.rf - 1, 64)
-        plan.execute_range(i, 1)
+        plan.execute_range(first, count)
         if typ == "ARGMAX_1D":
             got = plan.get_ids(valid)
             assert np.array_equal(got, lo.argmax(x, valid)), f"{tag} {name}"
             continue
-        y = _read(plan, c["y_off"], c["Cout"], T)
+        y = _read(plan, c["y_off"], cout, T)
         if typ == "EMBED_1D":
             assert np.array_equal(y.view(np.uint16), lo.embed(wts.embed, ids, T).view(np.uint16))
             continue
@@ -76,8 +90,7 @@ def _check_commands(plan, spec, wts, ids, decode, tag):
             continue
         if typ == "K44_WAVE":
             p, act = projs[name]
-            ref = lo.project(x, p.starts, spec.S, spec.tile, p.weights, p.bias, act, res,
-                             f64=True)
+            ref = lo.project(x, p.starts, spec.S, 1, p.weights, p.bias, act, res, f64=True)
         elif typ == "RMSNORM_1D":
             ref = lo.rmsnorm_f64(x)
         else:  # TOKEN_SHIFT_1D
@@ -91,7 +104,7 @@ def _check_commands(plan, spec, wts, ids, decode, tag):
         err = lo.orc.rel_err(y.astype(np.float64), ref)
         worst[typ] = max(worst.get(typ, 0.0), err)
         assert err <= TOL, f"{tag} {name}: rel err {err:.3e}"
-    _log(f"[{tag}] per-command worst rel err: "
+    _log(f"[{tag}] per-node worst rel err: "
          + ", ".join(f"{k} {v:.2e}" for k, v in sorted(worst.items())))
 
 
@@ -113,8 +126,8 @@ def test_llm_prefill_commandwise_and_end_to_end(wavec, monkeypatch, path):
     plan.execute(1)
     valid = ids.size
     T = stride_of(valid)
-    head = next(c for c in plan.cmds if c["name"] == "head")
-    logits = _read(plan, head["y_off"], head["Cout"], T)[:, :valid].astype(np.float64)
+    head = next(c for c in plan.cmds if c["name"].split("/")[0] == "head")
+    logits = _read(plan, head["y_off"], head["logical_Cout"], T)[:, :valid].astype(np.float64)
     ref = lo.llm_forward(TINY, wts, ids, decode=False)
     want = ref.tensors["logits"][:, :valid].astype(np.float64)
     scale = np.abs(want).max()
@@ -172,7 +185,7 @@ def test_llm_decode_graph_replay_matches_eager(wavec):
     synth.llm_handoff(spec, pre, graph)
     graph.use_graph(True)
     graph.set_history(steps)
-    head = next(c for c in eager.cmds if c["name"] == "head")
+    head = next(c for c in eager.cmds if c["name"].split("/")[0] == "head")
     want_ids, want_logits = [], []
     for _ in range(steps):
         eager.execute(1)

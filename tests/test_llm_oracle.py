@@ -159,5 +159,8 @@ def test_llm_spec_accounting():
     assert s.nnz_per_token == s.layers * (4 * s.d * kd + 2 * s.ffn * kd + s.d * kf) + s.vocab * kd
     w = synth.llm_weights(TINY)
     for p in w.proj[0].values():
-        assert np.all(np.diff(p.starts.astype(np.int64), axis=1) > 0)  # sorted, distinct
+        st = np.sort(p.starts.astype(np.int64), axis=1)
+        assert np.all(np.diff(st, axis=1) > 0)  # distinct clusters per neuron
         assert np.all(p.starts % TINY.S == 0)
+        assert p.starts.shape[0] == p.weights.shape[0]  # per-neuron patterns
+        assert len({tuple(r) for r in st.tolist()}) > 1

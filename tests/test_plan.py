@@ -295,3 +295,89 @@ def test_golden_fixture(wavec, tmp_path):
     assert po.tcff_bytes(po.compile_plan(mg.oracle_graph(po)), "Golden") == data
     meta = json.loads((GOLDEN / "small_plan.json").read_text())
     assert mg.summary_fields(wavec) == meta
+
+
+def _pruned_case(rng, n_cl, K, S, cout):
+    pick = np.argsort(rng.random((cout, n_cl)), axis=1)[:, :K]
+    starts = (pick * S).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    return starts, w, b
+
+
+@pytest.mark.parametrize("n_cl,K,tile,cout", [(4, 2, 64, 448), (11, 6, 16, 200), (6, 3, 32, 97)])
+def test_pruned_wave_plan_bit_exact(wavec, tmp_path, n_cl, K, tile, cout):
+    """Pattern-sorted tile schedule, index rows, zero-filled weights and biases of pruned waves
+    are identical to the Python restatement, byte for byte in the .tcff."""
+    rng = np.random.default_rng(n_cl * 100 + K)
+    S = 32
+    starts, w, b = _pruned_case(rng, n_cl, K, S, cout)
+
+    def build(g, pg):
+        g.add_input("x", n_cl * S, 1, 80, is_1d=True)
+        pg.input("x", n_cl * S, 1, 80, True)
+        g.add_pruned_wave("p", "x", "y", starts, S, w, b, tile=tile, act="silu", res_blob=None)
+        pg.pruned("p", "x", "y", starts, S, w.view(np.uint16), b.view(np.uint16), tile=tile,
+                  act=po.ACT_NAMES.index("SILU"))
+        g.add_pruned_wave("q", "y", "z", starts[:, :1] % (cout // S * S or S), S,
+                          w[:, :S], b, tile=tile, res_blob="y")
+        pg.pruned("q", "y", "z", starts[:, :1] % (cout // S * S or S), S,
+                  w[:, :S].view(np.uint16), b.view(np.uint16), tile=tile, residual="y")
+        g.set_output("z")
+        pg.output = "z"
+
+    g, plan, pplan = _pair(wavec, build)
+    _assert_same_plan(plan, pplan)
+    _assert_same_tcff(plan, pplan, tmp_path)
+    s = plan.summary
+    assert s["total_idx_bytes"] == sum(c["idx"].size * 4 + c["Cout"] * 4
+                                       for c in pplan["cmds"] if c["type"] == 0)
+    # effective FLOPs count real synapses only (2 nnz tokens), not the zero-filled unions
+    eff = sum(c["gflops"] for c in s["cmds"] if c["name"].split("/")[0] == "p")
+    assert eff == pytest.approx(2 * cout * K * S * 80 / 1e9, rel=1e-6)
+
+
+def test_pruned_parts_semantics():
+    """The decomposition reproduces every neuron's dot product (float64, any input) and places
+    each neuron in exactly one slot; full tiles of a single pattern keep the minimal union."""
+    rng = np.random.default_rng(7)
+    n_cl, K, S, cout, tile = 11, 6, 8, 300, 16
+    starts, w, b = _pruned_case(rng, n_cl, K, S, cout)
+    parts = po.pruned_parts(starts, S, w.view(np.uint16), b.view(np.uint16), tile)
+    x = rng.standard_normal((n_cl * S, 5))
+    want = np.stack([sum(w[j, k * S:(k + 1) * S].astype(np.float64) @ x[starts[j, k]:starts[j, k] + S]
+                         for k in range(K)) for j in range(cout)])
+    got = np.full((cout, 5), np.nan)
+    seen = []
+    prev_u = 0
+    for rows, wp, bp, cm in parts:
+        U = rows.shape[1]
+        assert U > prev_u and U >= K  # one part per union size, ascending
+        prev_u = U
+        assert np.all(np.diff(rows.astype(np.int64), axis=1) > 0)
+        wf = wp.view(np.float16).astype(np.float64)
+        for r in range(wp.shape[0]):
+            if cm[r] == 0xFFFF:
+                assert not wp[r].any() and bp[r] == 0
+                continue
+            j = int(cm[r])
+            seen.append(j)
+            assert set(starts[j].tolist()) <= set(rows[r // tile].tolist())
+            assert bp[r] == b.view(np.uint16)[j]
+            xs = np.concatenate([x[u:u + S] for u in rows[r // tile]])
+            got[j] = wf[r] @ xs
+    assert sorted(seen) == list(range(cout))
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+    # a projection whose neurons all share one pattern compiles to full tiles of width K
+    same = np.tile(np.array([[0, 2 * S]], np.uint32), (64, 1))
+    (rows, wp, _, cm), = po.pruned_parts(same, S, np.zeros((64, 2 * S), np.uint16),
+                                          np.zeros(64, np.uint16), 32)
+    assert rows.shape == (2, 2) and (cm != 0xFFFF).all()
+
+
+def test_pruned_wave_rejects_overlap(wavec):
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", 256, 1, 64, is_1d=True)
+    st = np.array([[0, 16]] * 16, np.uint32)  # clusters of 32 channels overlap
+    with pytest.raises(RuntimeError, match="overlap"):
+        g.add_pruned_wave("p", "x", "y", st, 32, np.zeros((16, 64), np.float16), tile=16)
