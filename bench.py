@@ -11,7 +11,9 @@ Metric: effective TFLOP/s = 2 * nnz * batch / t  (nnz = 65,536 x 64 synapses, ba
 reported with the achieved HBM GB/s of the wave kernel against the 8 TB/s roofline, and the
 CPU path (OpenMP fp32 oracle) timed on the host cores on a bounded sample of the same wave.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4] [--no-cpu]
+Config 5 (--config 5): the LLM-shaped decoder, prefill + 128 greedy decode steps per step.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5] [--no-cpu]
 """
 import argparse
 import json
@@ -103,12 +105,151 @@ def copy_probe(gib: float):
     log(f"[copy-probe] 5 launches of a {n}-byte device copy")
 
 
+def cpu_baseline_llm(spec, wts, tokens, budget_s: float = 12.0, sample_neurons: int = 256):
+    """OpenMP fp32 oracle on a bounded sample of the heaviest projection (layer 0's down
+    projection, per-neuron clusters) over the full prefill batch, input from the host generator."""
+    from oracle import oracle
+
+    p = wts.proj[0]["dn"]
+    n = min(sample_neurons, p.starts.shape[0])
+    K = p.starts.shape[1]
+    stride = (tokens + 63) // 64 * 64
+    x = oracle.fill_substrate(spec.seed, 0, spec.ffn, tokens, stride)
+    seg = p.starts[:n].astype(np.uint64).ravel() * np.uint64(stride)
+    canvas = np.concatenate([x.ravel(), np.zeros(n * stride, np.uint16)])
+    threads = len(os.sched_getaffinity(0))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        used = oracle.wave_f32_omp(canvas, seg, p.weights[:n], p.bias[:n], None, K, spec.S, 1,
+                                   stride, stride, stride, None, x.size, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 20:
+            break
+    t = float(np.median(times))
+    return {
+        "value": round(2.0 * n * K * spec.S * tokens / t / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": int(used),
+        "kind": "port",
+        "sample": (f"{n} of {p.starts.shape[0]} neurons of layer 0's down projection "
+                   f"({K} x {spec.S} inputs each) x {tokens} prefill tokens, median of "
+                   f"{len(times)} passes, fp32 OpenMP oracle/wave_oracle.c:orc_wave_f32_omp"),
+    }
+
+
+def bench_llm(args):
+    """Config 5: LLM-shaped decoder, 16 x 512-token prefill + 128 greedy decode steps.  One step =
+    prefill of all requests, device-side hand-over (token-shift state, last-token ids), then the
+    decode steps as replays of one captured HIP graph (argmax -> embedding chained on the device,
+    no host round trip).  The prompt ids (32 KB) are uploaded at the start of every step, since
+    the prefill's argmax overwrites the plan's id buffer."""
+    from snntome_amd import synth, wavec
+
+    t_start = time.perf_counter()
+    spec = synth.LLMSpec()
+    wts = synth.llm_weights(spec)
+    pre = synth.build_llm_graph(spec, wts, decode=False, wavec_mod=wavec).compile()
+    dec = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
+    pre.init_gpu()
+    dec.init_gpu()
+    pre.use_graph(True)
+    dec.use_graph(True)
+    R, P, D = spec.requests, spec.prompt, spec.decode_steps
+    prompt = np.random.default_rng(spec.seed).integers(0, spec.vocab, R * P).astype(np.uint32)
+    rep = pre.exec_report()["waves"]
+    paths = sorted({w["path"] for w in rep})
+    ex_flops = sum(w["flops"] for w in rep)
+    log(f"[bench] config5 setup {time.perf_counter() - t_start:.1f}s: {len(pre.cmds)} prefill "
+        f"commands ({len(rep)} waves, paths {paths}), executed/effective flops "
+        f"{ex_flops / (2 * spec.nnz_per_token * R * P):.3f}")
+
+    def one_step():
+        ms_p = pre.execute(1)
+        synth.llm_handoff(spec, pre, dec)
+        ms_d = dec.execute(D)
+        return ms_p, ms_d
+
+    pre.set_ids(prompt)
+    for _ in range(max(1, args.warmup)):
+        one_step()
+    pre.sync()
+    dec.sync()
+    t0 = time.perf_counter()
+    pms, dms = [], []
+    for _ in range(args.steps):
+        pre.set_ids(prompt)  # (prompt ids: host input, re-uploaded; 32 KB)
+        a, b = one_step()
+        pms.append(a)
+        dms.append(b)
+    dec.sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    prefill_ms, decode_ms = float(np.mean(pms)), float(np.mean(dms))
+    f_pre = 2.0 * spec.nnz_per_token * R * P
+    f_dec = 2.0 * spec.nnz_per_token * R
+    total = f_pre + D * f_dec
+    value = total / (wall_ms * 1e-3) / 1e12
+    w_bytes = dec.summary["total_w_bytes"]
+    dec_gbs = w_bytes / (decode_ms * 1e-3) / 1e9
+    pre_tf = f_pre / (prefill_ms * 1e-3) / 1e12
+    log(f"[bench] {args.steps} steps: {wall_ms:.2f} ms/step wall; prefill {prefill_ms:.3f} ms "
+        f"({pre_tf:.1f} TFLOP/s), decode {decode_ms:.4f} ms/step ({dec_gbs:.0f} GB/s weights)")
+    out = {
+        "metric": "effective TFLOP/s (2*nnz*batch) + achieved HBM GB/s per wave, 1xMI355X",
+        "value": round(value, 4),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (fp32 accumulate)",
+        "data": "synthetic (random-init fp16 weights, uniform random prompt ids)",
+        "config": {
+            "workload": "config5_llm_decoder",
+            "layers": spec.layers, "d": spec.d, "ffn": spec.ffn, "vocab": spec.vocab,
+            "S": spec.S, "clusters_kept": [spec.kept(spec.d), spec.kept(spec.ffn)],
+            "tile": spec.tile, "token_shift_rf": spec.rf, "requests": R, "prompt": P,
+            "decode_steps": D, "paths": paths,
+        },
+        "prefill_ms": round(prefill_ms, 4),
+        "prefill_tflops": round(pre_tf, 2),
+        "decode_ms_per_step": round(decode_ms, 5),
+        "decode_tokens_per_s": round(R / (decode_ms * 1e-3), 1),
+        "decode_weight_gbs": round(dec_gbs, 1),
+        "executed_over_effective_flops": round(ex_flops / f_pre, 4),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(pre_tf, 2),
+            "peak": FP16_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(pre_tf / FP16_MFMA_PEAK_TFLOPS, 4),
+            "traffic": traffic_from_profiles("llm_prefill_c5"),
+            "kernel_ms": round(prefill_ms, 4),
+            "scope": "whole prefill plan (all waves and token ops), effective FLOPs",
+        },
+        "decode_roofline": {
+            "bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+            "scope": "decode step: executed weight bytes / step time",
+        },
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline_llm(spec, wts, R * P)
+        log(f"[bench] cpu baseline {out['cpu_baseline']}")
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-gib", type=float, default=0.0,
                     help="only run a plain device copy of this many GiB (PMC calibration)")
@@ -121,6 +262,10 @@ def main():
               "(the wave shards by batch columns with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.config == 5:
+        bench_llm(args)
+        return
 
     from snntome_amd import synth, wavec
 

@@ -79,6 +79,7 @@ struct WaveExec {
     std::string why;
     bool mfma = false;
     uint32_t mt = 0, rows_per_stage = 32, ksteps = 0;  // MFMA tile: tokens, positions/stage
+    uint32_t kgroups = 1, stage_chunk = 0;  // MFMA split-K: workgroups per tile, stages each
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
     uint64_t step = 1;
     uint32_t tokens = 0, out_stride = 0;
@@ -130,6 +131,10 @@ struct K44GpuExecutorState {
     DevBuf<__half> canvas;
     DevBuf<uint32_t> ids, history, step_ctr;  // token ids (EMBED / ARGMAX), greedy history
     uint32_t id_tokens = 0, hist_steps = 0;
+    // Scratch shared by the commands of the plan (they run in order on one stream): split-K
+    // partials of MFMA waves, per-chunk (value, index) partials of ARGMAX.
+    DevBuf<float> scratch;
+    size_t scratch_need = 0;  // floats
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     hipGraph_t graph = nullptr;
@@ -157,6 +162,8 @@ struct K44GpuExecutorState {
         step_ctr.reset();
         id_tokens = hist_steps = 0;
         canvas.reset();
+        scratch.reset();
+        scratch_need = 0;
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
         if (stream) (void)hipStreamDestroy(stream);
@@ -334,6 +341,21 @@ struct K44GpuExecutorState {
                      " contraction per tile on v_mfma_f32_16x16x32_f16";
             wx.mt = pick_mt(wx.tokens);
             wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
+            // Split-K when tiles x token tiles leave the chip mostly idle (decode-sized token
+            // counts, one- or two-tile sub-waves): aim at ~1024 workgroups, >= 1 stage each.
+            {
+                const uint32_t stages = c.B_raw / wx.rows_per_stage;
+                const uint64_t wgs = (uint64_t)rows * (wx.tokens / wx.mt);
+                const char *sk_env = std::getenv("K44WAVEC_SPLITK");
+                uint32_t want = wgs >= 512u ? 1u : (uint32_t)((1024u + wgs - 1u) / wgs);
+                if (sk_env && std::string(sk_env) == "0") want = 1u;
+                want = std::max(1u, std::min(want, stages));
+                wx.stage_chunk = (stages + want - 1u) / want;
+                wx.kgroups = (stages + wx.stage_chunk - 1u) / wx.stage_chunk;
+                if (wx.kgroups > 1u)
+                    scratch_need = std::max(scratch_need,
+                                            (size_t)wx.kgroups * c.Cout * wx.tokens);
+            }
             wx.ksteps = c.B_raw / 32u;
             const uint32_t nb = cl / 16u;
             // A fragments: [tile][k-step][16-neuron block][lane][8]; lane l holds neuron
@@ -463,6 +485,7 @@ struct K44GpuExecutorState {
             ax.D = c.Cin;
             need(ax.src_off, (uint64_t)ax.D * ax.stride, "input");
             id_tokens = std::max(id_tokens, ax.tokens);
+            scratch_need = std::max(scratch_need, k44dev::argmax_scratch_floats(ax.D, ax.stride));
             break;
         default:
             throw std::runtime_error(std::string("command '") + c.name + "' of type " +
@@ -494,7 +517,7 @@ struct K44GpuExecutorState {
         case K44CmdType::ARGMAX_1D:
             K44_HIP(k44dev::launch_argmax(ids.p, hist_steps ? history.p : nullptr, step_ctr.p,
                                           hist_steps, cv + a.src_off, a.D, a.stride, a.tokens,
-                                          stream));
+                                          scratch.p, stream));
             break;
         default:
             throw std::runtime_error("unsupported aux command");
@@ -533,6 +556,7 @@ struct K44GpuExecutorState {
         K44_HIP(hipEventCreate(&ev0));
         K44_HIP(hipEventCreate(&ev1));
         canvas.alloc(plan.canvas_elems);
+        if (scratch_need) scratch.alloc(scratch_need);
         K44_HIP(hipMemsetAsync(canvas.p, 0, plan.canvas_elems * 2u, stream));
         if (id_tokens) {
             ids.alloc(id_tokens);
@@ -554,7 +578,8 @@ struct K44GpuExecutorState {
               << "\", \"why\": \"" << w.why << "\", \"cout\": " << w.cout << ", \"K\": " << w.K
               << ", \"S\": " << w.S << ", \"cluster\": " << w.cluster << ", \"step\": " << w.step
               << ", \"tokens\": " << w.tokens << ", \"slab\": " << (w.mfma ? w.mt : w.slab)
-              << ", \"U\": " << (w.mfma ? w.rows_per_stage : w.U) << ", \"ksplit\": " << w.ksplit
+              << ", \"U\": " << (w.mfma ? w.rows_per_stage : w.U)
+              << ", \"ksplit\": " << (w.mfma ? w.kgroups : w.ksplit)
               << ", \"sorted_segments\": " << (w.sorted_segments ? "true" : "false")
               << ", \"flops\": " << (long long)w.flops
               << ", \"effective_flops\": " << (long long)w.eff_flops
@@ -587,8 +612,13 @@ struct K44GpuExecutorState {
         a.ksteps = w.ksteps;
         a.out_stride = w.out_stride;
         a.act = w.act;
+        a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : a.K * a.S / w.rows_per_stage;
+        a.part = w.kgroups > 1u ? scratch.p : nullptr;
+        a.cout = w.cout;
+        a.tokens = w.tokens;
         K44_HIP(k44dev::launch_mfma_tile(a, w.cluster, w.mt, w.rows_per_stage, w.rows, w.tokens,
                                          stream));
+        if (w.kgroups > 1u) K44_HIP(k44dev::launch_splitk_epilogue(a, w.kgroups, stream));
     }
 
     void launch_wave(const WaveExec &w) {

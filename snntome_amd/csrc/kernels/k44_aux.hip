@@ -1,20 +1,38 @@
 // Translation unit of the 1-D token ops (see k44_aux.hpp for their semantics).
 #include "k44_aux.hpp"
+#include "k44_gather_dot.hpp"
 
 namespace k44dev {
 
-// One workgroup per 64-token tile: 256 threads = 8 token-octets x 32 channel lanes.  Each thread
-// reads 16-byte runs of 8 tokens down its channel stripe, sums squares per token, the 32 stripes
-// of a token octet reduce through LDS, and the same threads write the normalised values.
-__global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y,
-                                                          const __half *__restrict__ x,
-                                                          const __half *__restrict__ gamma,
-                                                          uint32_t D, uint32_t stride, float eps) {
-    __shared__ float part[32][65];
-    const uint32_t oct = threadIdx.x & 7u, lane_c = threadIdx.x >> 3;
-    const uint32_t t0 = blockIdx.x * 64u + oct * 8u;
+// One workgroup of 1024 threads per 32-token tile: 4 token-octets x 256 channel lanes.  Each
+// thread reads 16-byte runs of 8 tokens down its channel stripe (8 loads in flight), the 256
+// stripes of an octet reduce through LDS, and the same threads write the normalised values.
+__global__ __launch_bounds__(1024) void k44_rmsnorm_kernel(__half *__restrict__ y,
+                                                           const __half *__restrict__ x,
+                                                           const __half *__restrict__ gamma,
+                                                           uint32_t D, uint32_t stride, float eps) {
+    __shared__ float part[16][32];
+    __shared__ float inv_s[32];
+    const uint32_t oct = threadIdx.x & 3u, lane_c = threadIdx.x >> 2;
+    const uint32_t t0 = blockIdx.x * 32u + oct * 8u;
     float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (uint32_t c = lane_c; c < D; c += 32u) {
+    uint32_t c = lane_c;
+    for (; c + 7u * 256u < D; c += 8u * 256u) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            v[u] = *reinterpret_cast<const uint4 *>(x + (uint64_t)(c + u * 256u) * stride + t0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const __half *h = reinterpret_cast<const __half *>(&v[u]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float f = __half2float(h[k]);
+                ss[k] = fmaf(f, f, ss[k]);
+            }
+        }
+    }
+    for (; c < D; c += 256u) {
         const uint4 v = *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0);
         const __half *h = reinterpret_cast<const __half *>(&v);
 #pragma unroll
@@ -23,17 +41,29 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
             ss[k] = fmaf(f, f, ss[k]);
         }
     }
+    // reduce the 16 channel lanes of each wave that share an octet (lanes differ in bits 2..5),
+    // then the 16 waves in a fixed order
 #pragma unroll
-    for (int k = 0; k < 8; ++k) part[lane_c][oct * 8u + k] = ss[k];
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int m = 4; m < 64; m <<= 1) ss[k] += __shfl_xor(ss[k], m, 64);
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if (lane < 4u) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) part[wave][lane * 8u + k] = ss[k];
+    }
+    __syncthreads();
+    if (threadIdx.x < 32u) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tot += part[r][threadIdx.x];
+        inv_s[threadIdx.x] = rsqrtf(tot / (float)D + eps);
+    }
     __syncthreads();
     float inv[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        float tot = 0.0f;
-        for (int r = 0; r < 32; ++r) tot += part[r][oct * 8u + k];
-        inv[k] = rsqrtf(tot / (float)D + eps);
-    }
-    for (uint32_t c = lane_c; c < D; c += 32u) {
+    for (int k = 0; k < 8; ++k) inv[k] = inv_s[oct * 8u + k];
+    for (c = lane_c; c < D; c += 256u) {
         const uint4 v = *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0);
         const __half *h = reinterpret_cast<const __half *>(&v);
         const float g = gamma ? __half2float(gamma[c]) : 1.0f;
@@ -62,105 +92,167 @@ __global__ __launch_bounds__(256) void k44_mul_kernel(__half *__restrict__ y,
     }
 }
 
-// One thread per (channel, token).  State block of channel c: state[(c*(rf-1) + i)*64 + r] =
-// input of request r, i+1 tokens back.
-__global__ __launch_bounds__(256) void k44_token_shift_kernel(
+// Prefill: thread = (channel c = blockIdx.y + k*gridDim.y, 8 consecutive tokens), with the
+// 8 tokens before them in registers (rf - 1 <= 8), so every tap is a register read.  State
+// block of channel c: state[(c*(rf-1) + i)*64 + r] = input of request r, i+1 tokens back.
+__global__ __launch_bounds__(256) void k44_token_shift_prefill_kernel(
     __half *__restrict__ y, const __half *__restrict__ x, const __half *__restrict__ mu,
     __half *__restrict__ state, uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf,
-    uint32_t seq_len, int decode) {
+    uint32_t seq_len) {
+    const uint32_t chunk = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t t0 = chunk * 8u;
+    if (t0 >= stride) return;
+    for (uint32_t c = blockIdx.y; c < D; c += gridDim.y) {
+        const __half *xr = x + (uint64_t)c * stride;
+        float m[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            m[i] = (uint32_t)i < rf ? __half2float(mu[(uint64_t)c * rf + i]) : 0.0f;
+        float w[16];  // w[8 + k] = x[t0 + k], w[k] = x[t0 - 8 + k]
+        {
+            const uint4 cur = *reinterpret_cast<const uint4 *>(xr + t0);
+            const uint4 prv = t0 ? *reinterpret_cast<const uint4 *>(xr + t0 - 8u) : uint4{0, 0, 0, 0};
+            const __half *hc = reinterpret_cast<const __half *>(&cur);
+            const __half *hp = reinterpret_cast<const __half *>(&prv);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                w[8 + k] = __half2float(hc[k]);
+                w[k] = __half2float(hp[k]);
+            }
+        }
+        uint4 o;
+        __half *oh = reinterpret_cast<__half *>(&o);
+        uint32_t pos = t0 % seq_len;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t t = t0 + (uint32_t)k;
+            float acc = 0.0f;
+            if (t < tokens) {
+                acc = m[0] * w[8 + k];
+#pragma unroll
+                for (int i = 1; i < 9; ++i)  // taps stay in registers: i and k are unrolled
+                    if ((uint32_t)i < rf && (uint32_t)i <= pos) acc = fmaf(m[i], w[8 + k - i], acc);
+                if (state && pos + rf > seq_len) {  // last rf-1 tokens of the request -> state
+                    const uint32_t back = seq_len - 1u - pos;  // 0 = newest
+                    if (back < rf - 1u)
+                        state[((uint64_t)c * (rf - 1u) + back) * 64u + t / seq_len] = xr[t];
+                }
+            }
+            oh[k] = __float2half_rn(acc);
+            pos = pos + 1u == seq_len ? 0u : pos + 1u;
+        }
+        *reinterpret_cast<uint4 *>(y + (uint64_t)c * stride + t0) = o;
+    }
+}
+
+// Decode: one token per request (t < tokens <= 64); thread = (channel, token).
+__global__ __launch_bounds__(256) void k44_token_shift_decode_kernel(
+    __half *__restrict__ y, const __half *__restrict__ x, const __half *__restrict__ mu,
+    __half *__restrict__ state, uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf) {
     const uint64_t n = (uint64_t)D * stride;
     for (uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x; e < n;
          e += (uint64_t)gridDim.x * 256u) {
         const uint32_t c = (uint32_t)(e / stride), t = (uint32_t)(e - (uint64_t)c * stride);
-        const __half *m = mu + (uint64_t)c * rf;
-        const float xt = __half2float(x[e]);
-        float acc = __half2float(m[0]) * xt;
         if (t >= tokens) {
             y[e] = __float2half_rn(0.0f);
             continue;
         }
-        if (decode) {
-            __half *st = state + (uint64_t)c * (rf - 1u) * 64u + t;  // request r = token t
-            float prev[8];
-            for (uint32_t i = 1; i < rf; ++i) prev[i - 1] = __half2float(st[(i - 1u) * 64u]);
-            for (uint32_t i = 1; i < rf; ++i) acc = fmaf(__half2float(m[i]), prev[i - 1], acc);
-            for (uint32_t i = rf - 1u; i > 1u; --i) st[(i - 1u) * 64u] = __float2half_rn(prev[i - 2]);
-            if (rf > 1u) st[0] = x[e];
-        } else {
-            const uint32_t pos = t % seq_len;
-            for (uint32_t i = 1; i < rf && i <= pos; ++i)
-                acc = fmaf(__half2float(m[i]), __half2float(x[e - i]), acc);
-            if (state && pos + rf > seq_len) {  // last rf-1 tokens of the request -> state
-                const uint32_t back = seq_len - 1u - pos;  // 0 = newest
-                if (back < rf - 1u) {
-                    const uint32_t r = t / seq_len;
-                    state[((uint64_t)c * (rf - 1u) + back) * 64u + r] = x[e];
-                }
-            }
-        }
+        const __half *m = mu + (uint64_t)c * rf;
+        float acc = __half2float(m[0]) * __half2float(x[e]);
+        __half *st = state + (uint64_t)c * (rf - 1u) * 64u + t;  // request r = token t
+        float prev[8];
+        for (uint32_t i = 1; i < rf; ++i) prev[i - 1] = __half2float(st[(i - 1u) * 64u]);
+        for (uint32_t i = 1; i < rf; ++i) acc = fmaf(__half2float(m[i]), prev[i - 1], acc);
+        for (uint32_t i = rf - 1u; i > 1u; --i) st[(i - 1u) * 64u] = __float2half_rn(prev[i - 2]);
+        if (rf > 1u) st[0] = x[e];
         y[e] = __float2half_rn(acc);
     }
 }
 
+// Workgroup = 64 tokens x 64 channels: the 64 table rows (128 contiguous bytes each) go through
+// LDS and leave as 64 channel rows of 64 tokens (128 contiguous bytes each).
 __global__ __launch_bounds__(256) void k44_embed_kernel(__half *__restrict__ y,
                                                         const __half *__restrict__ table,
                                                         const uint32_t *__restrict__ ids,
                                                         uint32_t D, uint32_t vocab,
                                                         uint32_t stride, uint32_t tokens) {
-    const uint64_t n = (uint64_t)D * stride;
-    for (uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x; e < n;
-         e += (uint64_t)gridDim.x * 256u) {
-        const uint32_t c = (uint32_t)(e / stride), t = (uint32_t)(e - (uint64_t)c * stride);
+    __shared__ __half tile[64][66];
+    const uint32_t t0 = blockIdx.x * 64u, c0 = blockIdx.y * 64u;
+    for (uint32_t q = threadIdx.x; q < 64u * 64u; q += 256u) {
+        const uint32_t tt = q >> 6, cc = q & 63u;  // read: token tt, channel cc (row-contiguous)
+        const uint32_t t = t0 + tt, c = c0 + cc;
         __half v = __float2half_rn(0.0f);
-        if (t < tokens) {
+        if (t < tokens && c < D) {
             const uint32_t id = ids[t];
             if (id < vocab) v = table[(uint64_t)id * D + c];
         }
-        y[e] = v;
+        tile[tt][cc] = v;
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < 64u * 64u; q += 256u) {
+        const uint32_t cc = q >> 6, tt = q & 63u;  // write: channel cc, token tt (row-contiguous)
+        if (c0 + cc < D) y[(uint64_t)(c0 + cc) * stride + t0 + tt] = tile[tt][cc];
     }
 }
 
-// One workgroup per token: 256 threads scan the vocabulary with a stride, then reduce
-// (value, index) pairs in LDS; ties resolve to the lowest index.
-__global__ __launch_bounds__(256) void k44_argmax_kernel(uint32_t *__restrict__ ids,
-                                                         uint32_t *__restrict__ history,
-                                                         const uint32_t *__restrict__ step_ctr,
-                                                         uint32_t hist_steps, uint32_t tokens,
-                                                         const __half *__restrict__ x, uint32_t V,
-                                                         uint32_t stride) {
-    __shared__ float bv[256];
-    __shared__ uint32_t bi[256];
-    const uint32_t t = blockIdx.x;
-    float best = -INFINITY;
-    uint32_t arg = 0xffffffffu;
-    for (uint32_t c = threadIdx.x; c < V; c += 256u) {
-        const float v = __half2float(x[(uint64_t)c * stride + t]);
-        if (v > best || (v == best && c < arg)) {
-            best = v;
-            arg = c;
-        }
+// ARGMAX pass 1: workgroup = 64 tokens x one chunk of channels; lane (16 per channel row) owns
+// 4 tokens, the 16 row groups of the workgroup stride the chunk.  Ties keep the lowest channel
+// (channels are visited in ascending order per thread, and merged lowest-index-first).
+__device__ __forceinline__ void amax_merge(float &bv, uint32_t &bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
     }
-    bv[threadIdx.x] = best;
-    bi[threadIdx.x] = arg;
+}
+
+__global__ __launch_bounds__(256) void k44_argmax_partial_kernel(
+    float *__restrict__ pval, uint32_t *__restrict__ pidx, const __half *__restrict__ x,
+    uint32_t V, uint32_t stride, uint32_t chunk) {
+    __shared__ float sv[16][64];
+    __shared__ uint32_t si[16][64];
+    const uint32_t grp = threadIdx.x >> 4, q = threadIdx.x & 15u;
+    const uint32_t t0 = blockIdx.x * 64u + q * 4u;
+    const uint32_t c_begin = blockIdx.y * chunk, c_end = min(V, c_begin + chunk);
+    float bv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    uint32_t bi[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+    for (uint32_t c = c_begin + grp; c < c_end; c += 16u) {
+        const gd_u2 v = *reinterpret_cast<const gd_u2 *>(x + (uint64_t)c * stride + t0);
+        const __half *h = reinterpret_cast<const __half *>(&v);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) amax_merge(bv[k], bi[k], __half2float(h[k]), c);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        sv[grp][q * 4u + k] = bv[k];
+        si[grp][q * 4u + k] = bi[k];
+    }
     __syncthreads();
-    for (uint32_t s = 128u; s > 0u; s >>= 1) {
-        if (threadIdx.x < s) {
-            const float v = bv[threadIdx.x + s];
-            const uint32_t i = bi[threadIdx.x + s];
-            if (v > bv[threadIdx.x] || (v == bv[threadIdx.x] && i < bi[threadIdx.x])) {
-                bv[threadIdx.x] = v;
-                bi[threadIdx.x] = i;
-            }
-        }
-        __syncthreads();
+    if (threadIdx.x < 64u) {
+        float v = sv[0][threadIdx.x];
+        uint32_t i = si[0][threadIdx.x];
+        for (int g2 = 1; g2 < 16; ++g2) amax_merge(v, i, sv[g2][threadIdx.x], si[g2][threadIdx.x]);
+        const uint64_t o = (uint64_t)blockIdx.y * (gridDim.x * 64u) + blockIdx.x * 64u + threadIdx.x;
+        pval[o] = v;
+        pidx[o] = i;
     }
-    if (threadIdx.x == 0) {
-        const uint32_t id = bi[0] == 0xffffffffu ? 0u : bi[0];
-        ids[t] = id;
-        if (history) {
-            const uint32_t step = *step_ctr;
-            if (step < hist_steps) history[(uint64_t)step * tokens + t] = id;
-        }
+}
+
+// ARGMAX pass 2: per token, merge the chunk partials in chunk order.
+__global__ __launch_bounds__(256) void k44_argmax_final_kernel(
+    uint32_t *__restrict__ ids, uint32_t *__restrict__ history,
+    const uint32_t *__restrict__ step_ctr, uint32_t hist_steps, uint32_t tokens,
+    const float *__restrict__ pval, const uint32_t *__restrict__ pidx, uint32_t chunks,
+    uint32_t ld) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= tokens) return;
+    float v = pval[t];
+    uint32_t i = pidx[t];
+    for (uint32_t k = 1; k < chunks; ++k) amax_merge(v, i, pval[(uint64_t)k * ld + t], pidx[(uint64_t)k * ld + t]);
+    const uint32_t id = i == 0xffffffffu ? 0u : i;
+    ids[t] = id;
+    if (history) {
+        const uint32_t step = *step_ctr;
+        if (step < hist_steps) history[(uint64_t)step * tokens + t] = id;
     }
 }
 
@@ -173,7 +265,7 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
                           uint32_t stride, uint32_t tokens, float eps, hipStream_t stream) {
     (void)tokens;
     if (stride % 64u != 0u) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k44_rmsnorm_kernel, dim3(stride / 64u), dim3(256), 0, stream, y, x, gamma,
+    hipLaunchKernelGGL(k44_rmsnorm_kernel, dim3(stride / 32u), dim3(1024), 0, stream, y, x, gamma,
                        D, stride, eps);
     return hipGetLastError();
 }
@@ -189,27 +281,59 @@ hipError_t launch_mul(__half *y, const __half *a, const __half *b, uint64_t n,
 hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __half *state,
                               uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf,
                               uint32_t seq_len, int decode, hipStream_t stream) {
-    if (rf == 0u || rf > 9u || seq_len == 0u || (decode && (!state || tokens > 64u)))
+    if (rf == 0u || rf > 9u || seq_len == 0u || stride % 64u != 0u ||
+        (decode && (!state || tokens > 64u)))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k44_token_shift_kernel, dim3(grid_for((uint64_t)D * stride)), dim3(256), 0,
-                       stream, y, x, mu, state, D, stride, tokens, rf, seq_len, decode);
+    if (decode) {
+        hipLaunchKernelGGL(k44_token_shift_decode_kernel, dim3(grid_for((uint64_t)D * stride)),
+                           dim3(256), 0, stream, y, x, mu, state, D, stride, tokens, rf);
+    } else {
+        const uint32_t chunks = stride / 8u;
+        const uint32_t gx = (chunks + 255u) / 256u;
+        const uint32_t gy = D < 65535u ? D : 65535u;
+        hipLaunchKernelGGL(k44_token_shift_prefill_kernel, dim3(gx, gy), dim3(256), 0, stream, y,
+                           x, mu, state, D, stride, tokens, rf, seq_len);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uint32_t D,
                         uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream) {
-    hipLaunchKernelGGL(k44_embed_kernel, dim3(grid_for((uint64_t)D * stride)), dim3(256), 0,
+    if (stride % 64u != 0u || D == 0u) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k44_embed_kernel, dim3(stride / 64u, (D + 63u) / 64u), dim3(256), 0,
                        stream, y, table, ids, D, vocab, stride, tokens);
     return hipGetLastError();
 }
 
 __global__ void k44_step_inc_kernel(uint32_t *ctr) { *ctr += 1u; }
 
+static uint32_t argmax_chunk_len(uint32_t V, uint32_t stride) {
+    const uint32_t tiles = stride / 64u;
+    uint32_t chunks = (512u + tiles - 1u) / tiles;  // ~512 workgroups in pass 1
+    const uint32_t max_chunks = (V + 255u) / 256u;  // >= 256 channels per chunk
+    chunks = chunks < max_chunks ? chunks : max_chunks;
+    chunks = chunks ? chunks : 1u;
+    return (V + chunks - 1u) / chunks;
+}
+
+size_t argmax_scratch_floats(uint32_t V, uint32_t stride) {
+    const uint32_t chunk = argmax_chunk_len(V, stride);
+    return 2u * (size_t)((V + chunk - 1u) / chunk) * stride;
+}
+
 hipError_t launch_argmax(uint32_t *ids, uint32_t *history, uint32_t *step_ctr,
                          uint32_t hist_steps, const __half *x, uint32_t V, uint32_t stride,
-                         uint32_t tokens, hipStream_t stream) {
-    hipLaunchKernelGGL(k44_argmax_kernel, dim3(tokens), dim3(256), 0, stream, ids, history,
-                       step_ctr, hist_steps, tokens, x, V, stride);
+                         uint32_t tokens, float *scratch, hipStream_t stream) {
+    if (stride % 64u != 0u || V == 0u || !scratch) return hipErrorInvalidValue;
+    const uint32_t chunk = argmax_chunk_len(V, stride);
+    const uint32_t used = (V + chunk - 1u) / chunk;
+    float *pval = scratch;
+    uint32_t *pidx = reinterpret_cast<uint32_t *>(scratch + (uint64_t)used * stride);
+    hipLaunchKernelGGL(k44_argmax_partial_kernel, dim3(stride / 64u, used), dim3(256), 0, stream,
+                       pval, pidx, x, V, stride, chunk);
+    hipLaunchKernelGGL(k44_argmax_final_kernel, dim3((tokens + 255u) / 256u), dim3(256), 0,
+                       stream, ids, history, step_ctr, hist_steps, tokens, pval, pidx, used,
+                       stride);
     if (history) hipLaunchKernelGGL(k44_step_inc_kernel, dim3(1), dim3(1), 0, stream, step_ctr);
     return hipGetLastError();
 }

@@ -30,8 +30,11 @@ hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uin
                         uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream);
 // history (nullable): ids are also stored at history[*step_ctr][t] while *step_ctr <
 // hist_steps, and *step_ctr is incremented after the argmax (device-side, graph-safe).
+// Two passes: per-chunk (value, index) partials in `scratch` (argmax_scratch_floats(V, stride)
+// floats), then a per-token merge in chunk order.
+size_t argmax_scratch_floats(uint32_t V, uint32_t stride);
 hipError_t launch_argmax(uint32_t *ids, uint32_t *history, uint32_t *step_ctr,
                          uint32_t hist_steps, const __half *x, uint32_t V, uint32_t stride,
-                         uint32_t tokens, hipStream_t stream);
+                         uint32_t tokens, float *scratch, hipStream_t stream);
 
 }  // namespace k44dev

@@ -5,7 +5,7 @@ namespace k44dev {
 
 hipError_t launch_mfma_tile_nt16(const MfmaTileArgs &a, uint32_t mt, uint32_t rows_per_stage,
                                  uint32_t tiles, uint32_t tokens, hipStream_t stream) {
-    const dim3 grid(tiles, tokens / mt, 1u), block(mt, 1u, 1u);
+    const dim3 grid(tiles, tokens / mt, splitk_groups(a, rows_per_stage)), block(mt, 1u, 1u);
 #define K44_MFMA_CASE(MT)                                                                       \
     case MT:                                                                                    \
         if (rows_per_stage == 64u)                                                              \

@@ -18,6 +18,10 @@
 //    [lane][8]), so each wave loads every A fragment with one coalesced 16-byte-per-lane load.
 //  * Each wave owns 64 tokens: NT/16 x 4 accumulator tiles of 16x16 fp32.
 //  * Epilogue fused: bias, activation, residual / cout_map, fp16 (RNE) store.
+//  * Split-K for launches with too few tiles to fill the chip (decode-sized token counts, waves
+//    of one or two tiles): grid.z workgroups share a tile, each runs a contiguous range of
+//    stages and stores an fp32 partial; a second kernel reduces the partials in fixed order
+//    (bit-reproducible) and runs the epilogue.
 #pragma once
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -53,7 +57,21 @@ struct MfmaTileArgs {
     uint32_t ksteps;       // K*S/32
     uint32_t out_stride;
     int act;
+    // Split-K (part != nullptr): workgroup z covers stages [z*stage_chunk, +stage_chunk) and
+    // stores its fp32 partial tile to part[(z*cout + j)*tokens + t]; k44_splitk_epilogue_kernel
+    // sums the partials in z order and runs the epilogue.  part == nullptr: stage_chunk = all.
+    float *part;
+    uint32_t stage_chunk;
+    uint32_t cout;    // neurons of the wave (partial row count)
+    uint32_t tokens;  // tokens of the wave (partial row length)
 };
+
+// Workgroups per tile along grid.z (1 without split-K).
+inline uint32_t splitk_groups(const MfmaTileArgs &a, uint32_t rows_per_stage) {
+    if (!a.part) return 1u;
+    const uint32_t stages = a.K * a.S / rows_per_stage;
+    return (stages + a.stage_chunk - 1u) / a.stage_chunk;
+}
 
 template <int NT, int MT, int ROWS>
 __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
@@ -68,6 +86,8 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
     const uint32_t tok0 = blockIdx.y * (uint32_t)MT;
     const uint64_t *segr = a.seg + (uint64_t)tile * a.K;
     const uint32_t stages = a.K * a.S / (uint32_t)ROWS;
+    const uint32_t st_begin = blockIdx.z * a.stage_chunk;
+    const uint32_t st_end = min(stages, st_begin + a.stage_chunk);
 
     f4_t acc[NB][4];
 #pragma unroll
@@ -87,7 +107,9 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
     u4_t xr[CPT];  // X of the next stage, in flight during the current stage's MFMAs
     h8_t wn[SUBS][NB], wc[SUBS][NB];  // A fragments: next stage (in flight), current stage
     {
-        const __half *base = a.X + segr[0] + tok0;
+        const uint32_t kk = st_begin * (uint32_t)ROWS;
+        const uint32_t k = kk / a.S, s0 = kk - k * a.S;
+        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + tok0;
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = tid + i * MT;
@@ -97,7 +119,8 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
 #pragma unroll
         for (int u = 0; u < SUBS; ++u)
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) wc[u][nb] = wf[((uint64_t)u * NB + nb) * 64];
+            for (int nb = 0; nb < NB; ++nb)
+                wc[u][nb] = wf[((uint64_t)(st_begin * SUBS + u) * NB + nb) * 64];
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = tid + i * MT;
@@ -106,9 +129,9 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
     }
     __syncthreads();
 
-    for (uint32_t st = 0; st < stages; ++st) {
-        const int buf = (int)(st & 1u);
-        const bool more = st + 1 < stages;
+    for (uint32_t st = st_begin; st < st_end; ++st) {
+        const int buf = (int)((st - st_begin) & 1u);
+        const bool more = st + 1 < st_end;
         if (more) {  // issue next stage's X and W loads; consumed only after this stage's math
             const uint32_t kk = (st + 1) * (uint32_t)ROWS;
             const uint32_t k = kk / a.S, s0 = kk - k * a.S;
@@ -156,6 +179,19 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
     // Epilogue: lane holds C[4g + i][lane & 15] of every 16x16 tile.
     const uint32_t n_base = tile * (uint32_t)NT + 4u * (uint32_t)g;
     const uint32_t t_base = tok0 + (uint32_t)wave * 64u + (uint32_t)(lane & 15);
+    if (a.part) {  // split-K: fp32 partial tile, epilogue in k44_splitk_epilogue_kernel
+        float *pz = a.part + (uint64_t)blockIdx.z * a.cout * a.tokens;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t j = n_base + 16u * nb + (uint32_t)i;
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb)
+                    pz[(uint64_t)j * a.tokens + t_base + 16u * tb] = acc[nb][tb][i];
+            }
+        return;
+    }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll

@@ -231,3 +231,95 @@ def test_token_shift_long_rf_and_many_requests(wavec):
     got_st = _read(plan, c["state_off"], D * (rf - 1), 64).reshape(D, rf - 1, 64)
     # requests shorter than rf - 1 leave the older state slots untouched (zero)
     assert np.array_equal(got_st.view(np.uint16), st.view(np.uint16))
+
+
+@pytest.mark.parametrize("V,tokens", [(1000, 100), (32000, 64), (300, 1000)])
+def test_argmax_chunks_and_ties(wavec, V, tokens):
+    """Two-pass argmax (per-chunk partials, merge in chunk order) against the lowest-index rule,
+    with planted ties inside one chunk and across chunk boundaries."""
+    rng = np.random.default_rng(V)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", V, 1, tokens, is_1d=True)
+    g.add_argmax("am", "x", "ids")
+    plan = g.compile()
+    plan.init_gpu()
+    T = stride_of(tokens)
+    x = (rng.standard_normal((V, T)) * 3).astype(np.float16)
+    x[:, tokens:] = 0
+    top = np.float16(20.0)
+    for t in range(0, tokens, 3):  # ties: two or three equal maxima at random channels
+        cs = np.sort(rng.choice(V, size=2 + t % 2, replace=False))
+        x[cs, t] = top
+    x[:, 1] = np.float16(-np.inf)  # all -inf: channel 0
+    plan.write_canvas(int(plan.cmds[0]["src_off"]), x)
+    plan.execute(1)
+    got = plan.get_ids(tokens)
+    want = lo.argmax(x, tokens)
+    assert want[1] == 0
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("D,tokens", [(100, 70), (2048, 64), (300, 1000)])
+def test_rmsnorm_and_embed_shapes(wavec, D, tokens):
+    rng = np.random.default_rng(D)
+    V = 97
+    table = (rng.standard_normal((V, D)) * 2).astype(np.float16)
+    g = wavec.WaveGraph(kv_cache_max_seq=0, fold_rmsnorm_gamma=False)
+    g.add_input("tok", 1, 1, tokens, is_1d=True)
+    g.add_embedding("emb", "tok", "e", table)
+    gamma = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    g.add_rmsnorm("n", "e", "y", D, gamma)
+    plan = g.compile()
+    plan.init_gpu()
+    ids = rng.integers(0, V + 5, tokens).astype(np.uint32)  # some ids >= vocab -> zero rows
+    plan.set_ids(ids)
+    plan.execute(1)
+    T = stride_of(tokens)
+    ce, cn = plan.cmds[0], plan.cmds[1]
+    e = _read(plan, ce["y_off"], D, T)
+    assert np.array_equal(e.view(np.uint16), lo.embed(table, ids, T).view(np.uint16))
+    y = _read(plan, cn["y_off"], D, T)
+    ref = lo.rmsnorm_f64(e, gamma.astype(np.float16))
+    assert lo.orc.rel_err(y.astype(np.float64), ref) <= TOL
+
+
+@pytest.mark.parametrize("tokens,tiles", [(64, 2), (64, 40), (512, 1), (300, 3)])
+def test_mfma_split_k_matches_oracle_and_unsplit(wavec, orc, monkeypatch, tokens, tiles):
+    """Small tile x token-tile grids run split-K (partials + ordered reduction); the result is
+    within tolerance of the oracle and of the single-pass kernel, and identical across runs."""
+    rng = np.random.default_rng(tokens + tiles)
+    S, K, nt = 64, 6, 64
+    C = 4096
+    starts = (rng.integers(0, C // S, size=(tiles, K)) * S).astype(np.uint32)
+    cout = tiles * nt
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    outs = {}
+    for mode in ("split", "single"):
+        if mode == "single":
+            monkeypatch.setenv("K44WAVEC_SPLITK", "0")
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("x", C, 1, tokens, is_1d=True)
+        g.add_cluster_wave("w", "x", "y", starts, S, w, b, cluster=nt, act="gelu", res_blob="x")
+        plan = g.compile()
+        plan.init_gpu()
+        rep = plan.exec_report()["waves"][0]
+        assert rep["path"] == "mfma_tile"
+        assert (rep["ksplit"] > 1) == (mode == "split"), rep
+        plan.fill_input_uniform(3)
+        plan.execute(1)
+        st = stride_of(tokens)
+        canvas = plan.read_canvas(0, int(plan.summary["canvas_elems"]))
+        x0 = int(plan.cmds[0]["src_off"])
+        y0 = int(plan.cmds[0]["y_off"])
+        y = canvas[y0:y0 + cout * st].view(np.float16).reshape(cout, st).astype(np.float64)
+        seg = (x0 + starts.astype(np.uint64) * st).ravel()
+        ref = orc.wave_f64(canvas, seg, w, b, None, K, S, nt, st, st, st, "gelu", res_off=x0)
+        err = orc.rel_err(y, ref)
+        _log(f"[split-k {tokens}x{tiles} {mode}] ksplit {rep['ksplit']} rel err {err:.3e}")
+        assert err <= TOL
+        plan.execute(1)
+        again = plan.read_canvas(y0, cout * st)
+        assert np.array_equal(again, canvas[y0:y0 + cout * st])  # deterministic reduction
+        outs[mode] = y
+    assert orc.rel_err(outs["split"], outs["single"]) <= TOL
