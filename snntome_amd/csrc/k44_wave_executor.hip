@@ -342,12 +342,12 @@ struct K44GpuExecutorState {
             wx.mt = pick_mt(wx.tokens);
             wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
             // Split-K when tiles x token tiles leave the chip mostly idle (decode-sized token
-            // counts, one- or two-tile sub-waves): aim at ~1024 workgroups, >= 1 stage each.
+            // counts, one- or two-tile sub-waves): aim at ~512 workgroups, >= 1 stage each.
             {
                 const uint32_t stages = c.B_raw / wx.rows_per_stage;
                 const uint64_t wgs = (uint64_t)rows * (wx.tokens / wx.mt);
                 const char *sk_env = std::getenv("K44WAVEC_SPLITK");
-                uint32_t want = wgs >= 512u ? 1u : (uint32_t)((1024u + wgs - 1u) / wgs);
+                uint32_t want = wgs >= 256u ? 1u : (uint32_t)((512u + wgs - 1u) / wgs);
                 if (sk_env && std::string(sk_env) == "0") want = 1u;
                 want = std::max(1u, std::min(want, stages));
                 wx.stage_chunk = (stages + want - 1u) / want;

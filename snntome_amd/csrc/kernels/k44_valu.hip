@@ -51,11 +51,24 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(
     const uint32_t j = (uint32_t)(q / per_row), t = (uint32_t)(q - (uint64_t)j * per_row) * 4u;
     const uint64_t oj = cmap ? (uint64_t)cmap[j] : (uint64_t)j;
     if (oj == K44_CMAP_EMPTY) return;
-    const uint64_t plane = (uint64_t)cout * tokens;
+    const uint64_t plane4 = (uint64_t)cout * tokens / 4u;
     const float4 *p = reinterpret_cast<const float4 *>(part + (uint64_t)j * tokens + t);
     float4 v = p[0];
-    for (uint32_t z = 1; z < groups; ++z) {
-        const float4 w = p[z * plane / 4u];
+    uint32_t z = 1;
+    for (; z + 8u <= groups; z += 8u) {  // 8 partial loads in flight, summed in z order
+        float4 w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[u] = p[(uint64_t)(z + u) * plane4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            v.x += w[u].x;
+            v.y += w[u].y;
+            v.z += w[u].z;
+            v.w += w[u].w;
+        }
+    }
+    for (; z < groups; ++z) {
+        const float4 w = p[(uint64_t)z * plane4];
         v.x += w.x;
         v.y += w.y;
         v.z += w.z;
