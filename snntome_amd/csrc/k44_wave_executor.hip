@@ -94,7 +94,52 @@ struct WaveExec {
     DevBuf<uint64_t> seg;
     DevBuf<__half> w, bias;
     DevBuf<uint16_t> cmap;
+    // Canvas element ranges read (gather segments, residual rows) and written (output rows),
+    // merged and sorted: the host-side independence test of wave groups.
+    std::vector<std::pair<uint64_t, uint64_t>> rd, wr;
+    size_t part_floats = 0;  // split-K partials (kgroups * cout * tokens), 0 without split-K
+    // MFMA: descriptor of this wave alone (command-by-command execution).
+    DevBuf<k44dev::MfmaTileArgs> one_args;
+    DevBuf<uint32_t> one_start, one_epi;
+    uint32_t items = 0, epi_items = 0;
 };
+
+// A launch of several independent MFMA waves of one kernel configuration.
+struct MfmaGroupExec {
+    std::vector<size_t> members;  // wave indices, plan order
+    uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0;
+    size_t part_floats = 0;
+    DevBuf<k44dev::MfmaTileArgs> args;
+    DevBuf<uint32_t> start, epi;
+};
+
+// Sorted, merged [lo, hi) element ranges.
+using Ranges = std::vector<std::pair<uint64_t, uint64_t>>;
+
+Ranges merge_ranges(Ranges r) {
+    std::sort(r.begin(), r.end());
+    Ranges out;
+    for (const auto &x : r) {
+        if (!out.empty() && x.first <= out.back().second)
+            out.back().second = std::max(out.back().second, x.second);
+        else
+            out.push_back(x);
+    }
+    return out;
+}
+
+bool ranges_overlap(const Ranges &a, const Ranges &b) {
+    size_t i = 0, j = 0;
+    while (i < a.size() && j < b.size()) {
+        if (a[i].second <= b[j].first)
+            ++i;
+        else if (b[j].second <= a[i].first)
+            ++j;
+        else
+            return true;
+    }
+    return false;
+}
 
 // Device schedule of one 1-D token op (RMSNORM_1D, SWIGLU_MUL_1D, TOKEN_SHIFT_1D, EMBED_1D,
 // ARGMAX_1D).
@@ -127,7 +172,11 @@ struct K44GpuExecutorState {
     K44WavePlan plan_meta;  // plan without payload vectors
     std::vector<std::unique_ptr<WaveExec>> waves;
     std::vector<std::unique_ptr<AuxExec>> aux;
-    std::vector<std::pair<bool, size_t>> ops;  // plan order: (is_wave, index)
+    // Plan commands in order: (is_wave, index); the plan runs as `runs`: an aux command, a VALU
+    // wave, or a group of independent MFMA waves (kind 0 / 1 / 2, index).
+    std::vector<std::pair<bool, size_t>> ops;
+    std::vector<std::pair<int, size_t>> runs;
+    std::vector<std::unique_ptr<MfmaGroupExec>> groups;
     DevBuf<__half> canvas;
     DevBuf<uint32_t> ids, history, step_ctr;  // token ids (EMBED / ARGMAX), greedy history
     uint32_t id_tokens = 0, hist_steps = 0;
@@ -154,9 +203,11 @@ struct K44GpuExecutorState {
 
     void free_all() {
         drop_graph();
+        groups.clear();
         waves.clear();
         aux.clear();
         ops.clear();
+        runs.clear();
         ids.reset();
         history.reset();
         step_ctr.reset();
@@ -297,6 +348,22 @@ struct K44GpuExecutorState {
             if (s0 % 4u != 0u)
                 throw std::runtime_error("wave '" + c.name +
                                          "': token-shifted (unaligned) gathers not supported yet");
+        {
+            Ranges rd, wr;
+            rd.reserve(starts.size() + c.Cout);
+            for (uint64_t s0 : starts)
+                rd.push_back({s0, s0 + (uint64_t)(wx.S - 1u) * wx.step + wx.tokens});
+            for (uint32_t j = 0; j < c.Cout; ++j) {
+                const uint64_t oj = c.has_cout_map ? (uint64_t)c.h_cout_map[j] : (uint64_t)j;
+                if (c.has_cout_map && oj == 0xffffu) continue;
+                wr.push_back({wx.y_off + oj * wx.out_stride, wx.y_off + oj * wx.out_stride + wx.tokens});
+                if (wx.has_res)
+                    rd.push_back({wx.res_off + oj * wx.out_stride,
+                                  wx.res_off + oj * wx.out_stride + wx.tokens});
+            }
+            wx.rd = merge_ranges(std::move(rd));
+            wx.wr = merge_ranges(std::move(wr));
+        }
 
         // Distinct substrate positions (compulsory-traffic accounting).
         {
@@ -352,9 +419,7 @@ struct K44GpuExecutorState {
                 want = std::max(1u, std::min(want, stages));
                 wx.stage_chunk = (stages + want - 1u) / want;
                 wx.kgroups = (stages + wx.stage_chunk - 1u) / wx.stage_chunk;
-                if (wx.kgroups > 1u)
-                    scratch_need = std::max(scratch_need,
-                                            (size_t)wx.kgroups * c.Cout * wx.tokens);
+                if (wx.kgroups > 1u) wx.part_floats = (size_t)wx.kgroups * c.Cout * wx.tokens;
             }
             wx.ksteps = c.B_raw / 32u;
             const uint32_t nb = cl / 16u;
@@ -552,11 +617,13 @@ struct K44GpuExecutorState {
                 aux.push_back(std::move(ax));
             }
         }
+        form_runs();
         K44_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         K44_HIP(hipEventCreate(&ev0));
         K44_HIP(hipEventCreate(&ev1));
         canvas.alloc(plan.canvas_elems);
         if (scratch_need) scratch.alloc(scratch_need);
+        upload_mfma_descriptors();
         K44_HIP(hipMemsetAsync(canvas.p, 0, plan.canvas_elems * 2u, stream));
         if (id_tokens) {
             ids.alloc(id_tokens);
@@ -567,6 +634,127 @@ struct K44GpuExecutorState {
         K44_HIP(hipStreamSynchronize(stream));
         build_report();
         initialized = true;
+    }
+
+    // Plan order -> runs: consecutive MFMA waves of one kernel configuration join a group while
+    // no member writes what another reads or writes (checked on canvas element ranges).
+    void form_runs() {
+        const char *genv = std::getenv("K44WAVEC_GROUP");
+        const bool grouping = !(genv && std::string(genv) == "0");
+        runs.clear();
+        groups.clear();
+        for (const auto &op : ops) {
+            if (!op.first) {
+                runs.push_back({0, op.second});
+                continue;
+            }
+            const WaveExec &w = *waves[op.second];
+            scratch_need = std::max(scratch_need, w.part_floats);
+            if (!w.mfma) {
+                runs.push_back({1, op.second});
+                continue;
+            }
+            bool joined = false;
+            if (grouping && !runs.empty() && runs.back().first == 2) {
+                MfmaGroupExec &g = *groups[runs.back().second];
+                bool ok = g.nt == w.cluster && g.mt == w.mt && g.rows == w.rows_per_stage &&
+                          g.members.size() < 64u;
+                for (size_t m : g.members) {
+                    if (!ok) break;
+                    const WaveExec &o = *waves[m];
+                    ok = !ranges_overlap(w.wr, o.rd) && !ranges_overlap(w.rd, o.wr) &&
+                         !ranges_overlap(w.wr, o.wr);
+                }
+                if (ok) {
+                    g.members.push_back(op.second);
+                    g.part_floats += w.part_floats;
+                    joined = true;
+                }
+            }
+            if (!joined) {
+                auto g = std::make_unique<MfmaGroupExec>();
+                g->members = {op.second};
+                g->nt = w.cluster;
+                g->mt = w.mt;
+                g->rows = w.rows_per_stage;
+                g->part_floats = w.part_floats;
+                runs.push_back({2, groups.size()});
+                groups.push_back(std::move(g));
+            }
+        }
+        for (const auto &g : groups) scratch_need = std::max(scratch_need, g->part_floats);
+    }
+
+    k44dev::MfmaTileArgs mfma_args(const WaveExec &w, float *part) const {
+        k44dev::MfmaTileArgs a{};
+        a.X = canvas.p;
+        a.seg = w.seg.p;
+        a.Wf = w.w.p;
+        a.bias = w.bias.p;
+        a.cmap = w.cmap.p;
+        a.Y = canvas.p + w.y_off;
+        a.R = w.has_res ? canvas.p + w.res_off : nullptr;
+        a.step = w.step;
+        a.K = w.K;
+        a.S = w.S;
+        a.ksteps = w.ksteps;
+        a.out_stride = w.out_stride;
+        a.act = w.act;
+        a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : a.K * a.S / w.rows_per_stage;
+        a.part = w.kgroups > 1u ? part : nullptr;
+        a.cout = w.cout;
+        a.tokens = w.tokens;
+        a.tiles = w.rows;
+        a.ttiles = w.tokens / w.mt;
+        a.kgroups = w.kgroups;
+        return a;
+    }
+
+    static uint32_t epi_workgroups(const WaveExec &w) {
+        if (w.kgroups <= 1u) return 0u;
+        return (uint32_t)(((uint64_t)w.cout * (w.tokens / 4u) + 255u) / 256u);
+    }
+
+    // Device descriptors: every MFMA wave alone (command-by-command runs) and every group.
+    void upload_mfma_descriptors() {
+        for (auto &wp : waves) {
+            WaveExec &w = *wp;
+            if (!w.mfma) continue;
+            w.items = w.rows * (w.tokens / w.mt) * w.kgroups;
+            w.epi_items = epi_workgroups(w);
+            w.one_args.upload({mfma_args(w, scratch.p)});
+            w.one_start.upload({0u, w.items});
+            w.one_epi.upload({0u, w.epi_items});
+        }
+        for (auto &gp : groups) {
+            MfmaGroupExec &g = *gp;
+            std::vector<k44dev::MfmaTileArgs> args;
+            std::vector<uint32_t> start = {0u}, epi = {0u};
+            size_t off = 0;
+            for (size_t m : g.members) {
+                const WaveExec &w = *waves[m];
+                args.push_back(mfma_args(w, scratch.p ? scratch.p + off : nullptr));
+                off += w.part_floats;
+                start.push_back(start.back() + w.items);
+                epi.push_back(epi.back() + w.epi_items);
+            }
+            g.items = start.back();
+            g.epi_items = epi.back();
+            g.args.upload(args);
+            g.start.upload(start);
+            g.epi.upload(epi);
+        }
+    }
+
+    size_t launches_per_run() const {
+        size_t n = 0;
+        for (const auto &r : runs) {
+            if (r.first == 2) n += groups[r.second]->epi_items ? 2u : 1u;
+            else if (r.first == 0 && aux[r.second]->type == K44CmdType::ARGMAX_1D)
+                n += hist_steps ? 3u : 2u;
+            else n += 1u;
+        }
+        return n;
     }
 
     void build_report() {
@@ -592,33 +780,33 @@ struct K44GpuExecutorState {
             o << (i ? ", " : "") << "{\"name\": \"" << aux[i]->name << "\", \"type\": \""
               << cmd_type_str(aux[i]->type) << "\", \"channels\": " << aux[i]->D
               << ", \"tokens\": " << aux[i]->tokens << "}";
-        o << "], \"canvas_elems\": " << plan_meta.canvas_elems << ", \"id_tokens\": " << id_tokens
+        o << "], \"groups\": [";
+        for (size_t i = 0; i < groups.size(); ++i) {
+            o << (i ? ", " : "") << "[";
+            for (size_t k = 0; k < groups[i]->members.size(); ++k)
+                o << (k ? ", " : "") << groups[i]->members[k];
+            o << "]";
+        }
+        o << "], \"launches_per_run\": " << launches_per_run();
+        o << ", \"canvas_elems\": " << plan_meta.canvas_elems << ", \"id_tokens\": " << id_tokens
           << "}";
         report_json = o.str();
     }
 
+    void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
+                           uint32_t items, uint32_t epi_items) {
+        K44_HIP(k44dev::launch_mfma_tile(d, nt, mt, rows, items, stream));
+        if (epi_items) K44_HIP(k44dev::launch_splitk_epilogue(d, epi_items, stream));
+    }
+
     void launch_mfma(const WaveExec &w) {
-        k44dev::MfmaTileArgs a{};
-        a.X = canvas.p;
-        a.seg = w.seg.p;
-        a.Wf = w.w.p;
-        a.bias = w.bias.p;
-        a.cmap = w.cmap.p;
-        a.Y = canvas.p + w.y_off;
-        a.R = w.has_res ? canvas.p + w.res_off : nullptr;
-        a.step = w.step;
-        a.K = w.K;
-        a.S = w.S;
-        a.ksteps = w.ksteps;
-        a.out_stride = w.out_stride;
-        a.act = w.act;
-        a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : a.K * a.S / w.rows_per_stage;
-        a.part = w.kgroups > 1u ? scratch.p : nullptr;
-        a.cout = w.cout;
-        a.tokens = w.tokens;
-        K44_HIP(k44dev::launch_mfma_tile(a, w.cluster, w.mt, w.rows_per_stage, w.rows, w.tokens,
-                                         stream));
-        if (w.kgroups > 1u) K44_HIP(k44dev::launch_splitk_epilogue(a, w.kgroups, stream));
+        const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, w.one_epi.p, 1u};
+        launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items);
+    }
+
+    void launch_group(const MfmaGroupExec &g) {
+        const k44dev::MfmaGroup d{g.args.p, g.start.p, g.epi.p, (uint32_t)g.members.size()};
+        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items);
     }
 
     void launch_wave(const WaveExec &w) {
@@ -654,7 +842,14 @@ struct K44GpuExecutorState {
     }
 
     void launch_ops() {
-        for (size_t i = 0; i < ops.size(); ++i) launch_op(i);
+        for (const auto &r : runs) {
+            if (r.first == 0)
+                launch_aux(*aux[r.second]);
+            else if (r.first == 1)
+                launch_wave(*waves[r.second]);
+            else
+                launch_group(*groups[r.second]);
+        }
     }
 
     // One plan run on the executor stream: kernel by kernel, or as one replay of a HIP graph

@@ -15,14 +15,15 @@ namespace k44dev {
 hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
                              uint32_t tokens, hipStream_t stream);
 
-// MFMA tile kernel: grid (tiles, tokens / mt, split-K groups), block mt; nt in {16,32,64,128},
-// mt in {64,128,256,512}, rows_per_stage in {32,64}.
-hipError_t launch_mfma_tile(const MfmaTileArgs &a, uint32_t nt, uint32_t mt,
-                            uint32_t rows_per_stage, uint32_t tiles, uint32_t tokens,
-                            hipStream_t stream);
+// MFMA tile kernel over a group of waves (one kernel configuration): `items` workgroups (the
+// group's start[n]), block mt; nt in {16,32,64,128}, mt in {64,128,256,512}, rows_per_stage in
+// {32,64}.
+hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32_t rows_per_stage,
+                            uint32_t items, hipStream_t stream);
 
-// Split-K second pass of the MFMA tile kernel: sums `groups` fp32 partials, runs the epilogue.
-hipError_t launch_splitk_epilogue(const MfmaTileArgs &a, uint32_t groups, hipStream_t stream);
+// Split-K second pass over the same group: `epi_items` workgroups (the group's epi_start[n]);
+// each wave with kgroups > 1 sums its fp32 partials in z order and runs the epilogue.
+hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_items, hipStream_t stream);
 
 // Synthetic substrate fill (see k44_fill_uniform_kernel).
 hipError_t launch_fill_uniform(__half *dst, uint64_t rows, uint32_t stride, uint32_t valid,

@@ -3,19 +3,19 @@
 
 namespace k44dev {
 
-hipError_t launch_mfma_tile_nt16(const MfmaTileArgs &, uint32_t, uint32_t, uint32_t, uint32_t, hipStream_t);
-hipError_t launch_mfma_tile_nt32(const MfmaTileArgs &, uint32_t, uint32_t, uint32_t, uint32_t, hipStream_t);
-hipError_t launch_mfma_tile_nt64(const MfmaTileArgs &, uint32_t, uint32_t, uint32_t, uint32_t, hipStream_t);
-hipError_t launch_mfma_tile_nt128(const MfmaTileArgs &, uint32_t, uint32_t, uint32_t, uint32_t, hipStream_t);
+hipError_t launch_mfma_tile_nt16(const MfmaGroup &, uint32_t, uint32_t, uint32_t, hipStream_t);
+hipError_t launch_mfma_tile_nt32(const MfmaGroup &, uint32_t, uint32_t, uint32_t, hipStream_t);
+hipError_t launch_mfma_tile_nt64(const MfmaGroup &, uint32_t, uint32_t, uint32_t, hipStream_t);
+hipError_t launch_mfma_tile_nt128(const MfmaGroup &, uint32_t, uint32_t, uint32_t, hipStream_t);
 
-hipError_t launch_mfma_tile(const MfmaTileArgs &a, uint32_t nt, uint32_t mt,
-                            uint32_t rows_per_stage, uint32_t tiles, uint32_t tokens,
-                            hipStream_t stream) {
+hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32_t rows_per_stage,
+                            uint32_t items, hipStream_t stream) {
+    if (items == 0u) return hipSuccess;
     switch (nt) {
-    case 16u: return launch_mfma_tile_nt16(a, mt, rows_per_stage, tiles, tokens, stream);
-    case 32u: return launch_mfma_tile_nt32(a, mt, rows_per_stage, tiles, tokens, stream);
-    case 64u: return launch_mfma_tile_nt64(a, mt, rows_per_stage, tiles, tokens, stream);
-    case 128u: return launch_mfma_tile_nt128(a, mt, rows_per_stage, tiles, tokens, stream);
+    case 16u: return launch_mfma_tile_nt16(g, mt, rows_per_stage, items, stream);
+    case 32u: return launch_mfma_tile_nt32(g, mt, rows_per_stage, items, stream);
+    case 64u: return launch_mfma_tile_nt64(g, mt, rows_per_stage, items, stream);
+    case 128u: return launch_mfma_tile_nt128(g, mt, rows_per_stage, items, stream);
     default: return hipErrorInvalidValue;
     }
 }

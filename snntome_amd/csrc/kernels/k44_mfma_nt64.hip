@@ -3,9 +3,9 @@
 
 namespace k44dev {
 
-hipError_t launch_mfma_tile_nt64(const MfmaTileArgs &a, uint32_t mt, uint32_t rows_per_stage,
-                                 uint32_t tiles, uint32_t tokens, hipStream_t stream) {
-    const dim3 grid(tiles, tokens / mt, splitk_groups(a, rows_per_stage)), block(mt, 1u, 1u);
+hipError_t launch_mfma_tile_nt64(const MfmaGroup &a, uint32_t mt, uint32_t rows_per_stage,
+                                 uint32_t items, hipStream_t stream) {
+    const dim3 grid(items, 1u, 1u), block(mt, 1u, 1u);
 #define K44_MFMA_CASE(MT)                                                                       \
     case MT:                                                                                    \
         if (rows_per_stage == 64u)                                                              \

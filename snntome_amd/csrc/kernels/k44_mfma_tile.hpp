@@ -64,17 +64,28 @@ struct MfmaTileArgs {
     uint32_t stage_chunk;
     uint32_t cout;    // neurons of the wave (partial row count)
     uint32_t tokens;  // tokens of the wave (partial row length)
+    // Work items of the wave: tiles x token tiles x split-K groups (tile index fastest).
+    uint32_t tiles, ttiles, kgroups;
 };
 
-// Workgroups per tile along grid.z (1 without split-K).
-inline uint32_t splitk_groups(const MfmaTileArgs &a, uint32_t rows_per_stage) {
-    if (!a.part) return 1u;
-    const uint32_t stages = a.K * a.S / rows_per_stage;
-    return (stages + a.stage_chunk - 1u) / a.stage_chunk;
-}
+// A launch covers a group of independent waves of one kernel configuration (the sub-waves of a
+// pruned projection, projections reading the same input): workgroup i belongs to the wave w with
+// start[w] <= i < start[w+1]; the split-K epilogue workgroups likewise by epi_start.
+struct MfmaGroup {
+    const MfmaTileArgs *waves;  // [n]
+    const uint32_t *start;      // [n+1] prefix sums of tiles * ttiles * kgroups
+    const uint32_t *epi_start;  // [n+1] prefix sums of epilogue workgroups (0 without split-K)
+    uint32_t n;
+};
 
 template <int NT, int MT, int ROWS>
-__global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
+__global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
+    uint32_t w = 0;
+    while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
+    const MfmaTileArgs a = grp.waves[w];
+    const uint32_t local = blockIdx.x - grp.start[w];
+    const uint32_t tile = local % a.tiles, rest = local / a.tiles;
+    const uint32_t ytile = rest % a.ttiles, zgroup = rest / a.ttiles;
     constexpr int NB = NT / 16;              // 16-neuron blocks per tile
     constexpr int PITCH = MT + 16;           // LDS row pitch in halves (32-byte skew)
     constexpr int CPR = MT / 8;              // 16-byte chunks per position row
@@ -82,11 +93,10 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[2][ROWS][PITCH];
 
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t tile = blockIdx.x;
-    const uint32_t tok0 = blockIdx.y * (uint32_t)MT;
+    const uint32_t tok0 = ytile * (uint32_t)MT;
     const uint64_t *segr = a.seg + (uint64_t)tile * a.K;
     const uint32_t stages = a.K * a.S / (uint32_t)ROWS;
-    const uint32_t st_begin = blockIdx.z * a.stage_chunk;
+    const uint32_t st_begin = zgroup * a.stage_chunk;
     const uint32_t st_end = min(stages, st_begin + a.stage_chunk);
 
     f4_t acc[NB][4];
@@ -180,7 +190,7 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaTileArgs a) {
     const uint32_t n_base = tile * (uint32_t)NT + 4u * (uint32_t)g;
     const uint32_t t_base = tok0 + (uint32_t)wave * 64u + (uint32_t)(lane & 15);
     if (a.part) {  // split-K: fp32 partial tile, epilogue in k44_splitk_epilogue_kernel
-        float *pz = a.part + (uint64_t)blockIdx.z * a.cout * a.tokens;
+        float *pz = a.part + (uint64_t)zgroup * a.cout * a.tokens;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll

@@ -40,45 +40,47 @@ hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksp
     return hipGetLastError();
 }
 
-// Split-K reduction + epilogue: thread = (neuron j, 4 tokens); partials summed in z order.
-__global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(
-    const float *__restrict__ part, uint32_t groups, uint32_t cout, uint32_t tokens,
-    const __half *__restrict__ bias, const uint16_t *__restrict__ cmap, const __half *R,
-    __half *Y, uint32_t out_stride, int act) {
+// Split-K reduction + epilogue: thread = (neuron j, 4 tokens) of the wave that owns the
+// workgroup; partials summed in z order.
+__global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp) {
+    uint32_t w = 0;
+    while (w + 1u < grp.n && blockIdx.x >= grp.epi_start[w + 1u]) ++w;
+    const MfmaTileArgs a = grp.waves[w];
+    const uint32_t groups = a.kgroups, cout = a.cout, tokens = a.tokens;
     const uint32_t per_row = tokens / 4u;
-    const uint64_t q = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    const uint64_t q = (uint64_t)(blockIdx.x - grp.epi_start[w]) * 256u + threadIdx.x;
     if (q >= (uint64_t)cout * per_row) return;
     const uint32_t j = (uint32_t)(q / per_row), t = (uint32_t)(q - (uint64_t)j * per_row) * 4u;
-    const uint64_t oj = cmap ? (uint64_t)cmap[j] : (uint64_t)j;
+    const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
     if (oj == K44_CMAP_EMPTY) return;
     const uint64_t plane4 = (uint64_t)cout * tokens / 4u;
-    const float4 *p = reinterpret_cast<const float4 *>(part + (uint64_t)j * tokens + t);
+    const float4 *p = reinterpret_cast<const float4 *>(a.part + (uint64_t)j * tokens + t);
     float4 v = p[0];
     uint32_t z = 1;
     for (; z + 8u <= groups; z += 8u) {  // 8 partial loads in flight, summed in z order
-        float4 w[8];
+        float4 u8[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) w[u] = p[(uint64_t)(z + u) * plane4];
+        for (int u = 0; u < 8; ++u) u8[u] = p[(uint64_t)(z + u) * plane4];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            v.x += w[u].x;
-            v.y += w[u].y;
-            v.z += w[u].z;
-            v.w += w[u].w;
+            v.x += u8[u].x;
+            v.y += u8[u].y;
+            v.z += u8[u].z;
+            v.w += u8[u].w;
         }
     }
     for (; z < groups; ++z) {
-        const float4 w = p[(uint64_t)z * plane4];
-        v.x += w.x;
-        v.y += w.y;
-        v.z += w.z;
-        v.w += w.w;
+        const float4 u1 = p[(uint64_t)z * plane4];
+        v.x += u1.x;
+        v.y += u1.y;
+        v.z += u1.z;
+        v.w += u1.w;
     }
-    const float b = bias ? __half2float(bias[j]) : 0.0f;
-    const uint64_t o = oj * out_stride + t;
+    const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
+    const uint64_t o = oj * a.out_stride + t;
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (R) {
-        const gd_u2 rv = *reinterpret_cast<const gd_u2 *>(R + o);
+    if (a.R) {
+        const gd_u2 rv = *reinterpret_cast<const gd_u2 *>(a.R + o);
         const __half *rh = reinterpret_cast<const __half *>(&rv);
 #pragma unroll
         for (int k = 0; k < 4; ++k) r[k] = __half2float(rh[k]);
@@ -88,17 +90,14 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const float s = acc[k] + b;
-        out[k] = __float2half_rn(cmap ? apply_act(s + r[k], act) : apply_act(s, act) + r[k]);
+        out[k] = __float2half_rn(a.cmap ? apply_act(s + r[k], a.act) : apply_act(s, a.act) + r[k]);
     }
-    *reinterpret_cast<gd_u2 *>(Y + o) = *reinterpret_cast<const gd_u2 *>(out);
+    *reinterpret_cast<gd_u2 *>(a.Y + o) = *reinterpret_cast<const gd_u2 *>(out);
 }
 
-hipError_t launch_splitk_epilogue(const MfmaTileArgs &a, uint32_t groups, hipStream_t stream) {
-    if (!a.part || a.tokens % 4u != 0u) return hipErrorInvalidValue;
-    const uint64_t n = (uint64_t)a.cout * (a.tokens / 4u);
-    hipLaunchKernelGGL(k44_splitk_epilogue_kernel, dim3((uint32_t)((n + 255u) / 256u)),
-                       dim3(256), 0, stream, a.part, groups, a.cout, a.tokens, a.bias, a.cmap,
-                       a.R, a.Y, a.out_stride, a.act);
+hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_items, hipStream_t stream) {
+    if (epi_items == 0u) return hipSuccess;
+    hipLaunchKernelGGL(k44_splitk_epilogue_kernel, dim3(epi_items), dim3(256), 0, stream, g);
     return hipGetLastError();
 }
 

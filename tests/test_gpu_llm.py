@@ -323,3 +323,31 @@ def test_mfma_split_k_matches_oracle_and_unsplit(wavec, orc, monkeypatch, tokens
         assert np.array_equal(again, canvas[y0:y0 + cout * st])  # deterministic reduction
         outs[mode] = y
     assert orc.rel_err(outs["split"], outs["single"]) <= TOL
+
+
+@pytest.mark.parametrize("decode", [False, True])
+def test_grouped_launches_match_per_wave(wavec, monkeypatch, decode):
+    """Independent MFMA waves (sub-waves of a pruned projection, projections of one input) run
+    as one grouped launch; the logits are bit-identical to launching every wave alone."""
+    wts = synth.llm_weights(TINY)
+    R = TINY.requests
+    n = R if decode else R * TINY.prompt
+    ids = np.random.default_rng(8).integers(0, TINY.vocab, n).astype(np.uint32)
+    out = {}
+    for mode in ("grouped", "alone"):
+        if mode == "alone":
+            monkeypatch.setenv("K44WAVEC_GROUP", "0")
+        plan = synth.build_llm_graph(TINY, wts, decode=decode, wavec_mod=wavec).compile()
+        plan.init_gpu()
+        rep = plan.exec_report()
+        sizes = [len(g) for g in rep["groups"]]
+        _log(f"[groups {mode} decode={decode}] {len(sizes)} groups, largest {max(sizes)}, "
+             f"{rep['launches_per_run']} launches per run")
+        assert (max(sizes) > 1) == (mode == "grouped")
+        plan.set_ids(ids)
+        plan.execute(1)
+        head = next(c for c in plan.cmds if c["name"].split("/")[0] == "head")
+        out[mode] = plan.read_canvas(int(head["y_off"]), TINY.vocab * stride_of(n))
+        out[mode + "_ids"] = plan.get_ids(n)
+    assert np.array_equal(out["grouped"], out["alone"])
+    assert np.array_equal(out["grouped_ids"], out["alone_ids"])
