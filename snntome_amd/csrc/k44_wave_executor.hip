@@ -80,6 +80,8 @@ struct WaveExec {
     bool mfma = false;
     uint32_t mt = 0, rows_per_stage = 32, ksteps = 0;  // MFMA tile: tokens, positions/stage
     uint32_t kgroups = 1, stage_chunk = 0;  // MFMA split-K: workgroups per tile, stages each
+    bool narrow = false;       // MFMA over <= 16 tokens (decode): k44_mfma_narrow_kernel
+    uint32_t part_tokens = 0;  // row length of split-K partials (16 narrow, tokens wide)
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
     uint64_t step = 1;
     uint32_t tokens = 0, out_stride = 0;
@@ -408,9 +410,22 @@ struct K44GpuExecutorState {
                      " contraction per tile on v_mfma_f32_16x16x32_f16";
             wx.mt = pick_mt(wx.tokens);
             wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
-            // Split-K when tiles x token tiles leave the chip mostly idle (decode-sized token
-            // counts, one- or two-tile sub-waves): aim at ~512 workgroups, >= 1 stage each.
-            {
+            const char *nw_env = std::getenv("K44WAVEC_NARROW");
+            wx.narrow = Lo.W <= 16u && !(nw_env && std::string(nw_env) == "0");
+            wx.part_tokens = wx.narrow ? 16u : wx.tokens;
+            if (wx.narrow) {
+                // Contraction chunks of <= 16 k-steps (512 rows in LDS); ~512 workgroups.
+                wx.path = "mfma_narrow";
+                wx.why += " (at most 16 tokens: weight-streaming narrow tile)";
+                wx.mt = 16u;
+                const uint32_t ksteps = c.B_raw / 32u;
+                uint32_t want = std::max<uint32_t>((512u + (uint32_t)rows - 1u) / (uint32_t)rows,
+                                                   (ksteps + 15u) / 16u);
+                want = std::max(1u, std::min(want, ksteps));
+                wx.stage_chunk = (ksteps + want - 1u) / want;
+                wx.kgroups = (ksteps + wx.stage_chunk - 1u) / wx.stage_chunk;
+                if (wx.kgroups > 1u) wx.part_floats = (size_t)wx.kgroups * c.Cout * 16u;
+            } else {
                 const uint32_t stages = c.B_raw / wx.rows_per_stage;
                 const uint64_t wgs = (uint64_t)rows * (wx.tokens / wx.mt);
                 const char *sk_env = std::getenv("K44WAVEC_SPLITK");
@@ -700,19 +715,22 @@ struct K44GpuExecutorState {
         a.ksteps = w.ksteps;
         a.out_stride = w.out_stride;
         a.act = w.act;
-        a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : a.K * a.S / w.rows_per_stage;
+        if (w.narrow)  // chunk in k-steps
+            a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : w.ksteps;
+        else  // chunk in stages of rows_per_stage positions
+            a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : a.K * a.S / w.rows_per_stage;
         a.part = w.kgroups > 1u ? part : nullptr;
         a.cout = w.cout;
-        a.tokens = w.tokens;
+        a.tokens = w.part_tokens;
         a.tiles = w.rows;
-        a.ttiles = w.tokens / w.mt;
+        a.ttiles = w.narrow ? 1u : w.tokens / w.mt;
         a.kgroups = w.kgroups;
         return a;
     }
 
     static uint32_t epi_workgroups(const WaveExec &w) {
         if (w.kgroups <= 1u) return 0u;
-        return (uint32_t)(((uint64_t)w.cout * (w.tokens / 4u) + 255u) / 256u);
+        return (uint32_t)(((uint64_t)w.cout * (w.part_tokens / 4u) + 255u) / 256u);
     }
 
     // Device descriptors: every MFMA wave alone (command-by-command runs) and every group.
@@ -720,7 +738,7 @@ struct K44GpuExecutorState {
         for (auto &wp : waves) {
             WaveExec &w = *wp;
             if (!w.mfma) continue;
-            w.items = w.rows * (w.tokens / w.mt) * w.kgroups;
+            w.items = w.rows * (w.narrow ? 1u : w.tokens / w.mt) * w.kgroups;
             w.epi_items = epi_workgroups(w);
             w.one_args.upload({mfma_args(w, scratch.p)});
             w.one_start.upload({0u, w.items});
@@ -795,7 +813,10 @@ struct K44GpuExecutorState {
 
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
                            uint32_t items, uint32_t epi_items) {
-        K44_HIP(k44dev::launch_mfma_tile(d, nt, mt, rows, items, stream));
+        if (mt == 16u)  // narrow (<= 16 tokens)
+            K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream));
+        else
+            K44_HIP(k44dev::launch_mfma_tile(d, nt, mt, rows, items, stream));
         if (epi_items) K44_HIP(k44dev::launch_splitk_epilogue(d, epi_items, stream));
     }
 

@@ -21,6 +21,10 @@ hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksp
 hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32_t rows_per_stage,
                             uint32_t items, hipStream_t stream);
 
+// Narrow MFMA kernel (waves of at most 16 tokens) over a group: `items` workgroups (tiles x
+// contraction chunks per wave); nt in {16,32,64,128}.
+hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream);
+
 // Split-K second pass over the same group: `epi_items` workgroups (the group's epi_start[n]);
 // each wave with kgroups > 1 sums its fp32 partials in z order and runs the epilogue.
 hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_items, hipStream_t stream);

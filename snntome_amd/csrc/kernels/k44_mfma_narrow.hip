@@ -1,0 +1,142 @@
+// Translation unit of the narrow MFMA kernel: dense-cluster waves over at most 16 tokens
+// (decode steps).  The wide tile kernel (k44_mfma_tile.hpp) gives every wave 64 tokens; at 16
+// real tokens three quarters of its work and of its split-K partials would be padding, and the
+// wave is bound by streaming its weights once.  Here:
+//  * one workgroup (4 waves) = one NT-neuron tile x one chunk of the contraction (a range of
+//    32-deep k-steps) x 16 tokens;
+//  * the chunk's X rows (16 tokens = 32 bytes each) are gathered once into LDS, row-major; the
+//    B operand comes from ds_read_b64_tr_b16 exactly as in the wide kernel (lane 16g+4j+m reads
+//    row 8g+j (+4), tokens 4m..4m+3);
+//  * each wave owns 16-neuron blocks (NT = 64: one each; NT = 128: two) or, for NT < 64, the
+//    waves of a block take its k-steps round-robin and meet in LDS in a fixed order;
+//  * A fragments (host-arranged [tile][k-step][16-block][lane][8]) stream from HBM with 8 k-steps
+//    of loads in flight per wave before the first MFMA that needs them;
+//  * one chunk: fused epilogue; several: fp32 partials [z][cout][16] for
+//    k44_splitk_epilogue_kernel (summed in chunk order, bit-reproducible).
+// Columns 16..stride-1 of the output rows are not written.
+#include "k44_launch.hpp"
+
+namespace k44dev {
+
+constexpr int NARROW_MAX_ROWS = 512;  // rows of one chunk held in LDS
+constexpr int NARROW_PITCH = 24;      // halves per LDS row (16 tokens + 8 skew)
+
+template <int NT>
+__global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
+    constexpr int NB = NT / 16;                // 16-neuron blocks per tile
+    constexpr int BL = NB < 4 ? NB : 4;        // distinct blocks handled at once by the 4 waves
+    constexpr int KW = 4 / BL;                 // waves sharing a block (split k-steps)
+    constexpr int BPW = NB / BL;               // blocks per wave
+    __shared__ __attribute__((aligned(16))) _Float16 xl[NARROW_MAX_ROWS][NARROW_PITCH];
+    __shared__ f4_t red[KW > 1 ? 4 : 1][64];
+
+    uint32_t w = 0;
+    while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
+    const MfmaTileArgs a = grp.waves[w];
+    const uint32_t local = blockIdx.x - grp.start[w];
+    const uint32_t tile = local % a.tiles, zgroup = local / a.tiles;
+    const uint32_t ks_begin = zgroup * a.stage_chunk;
+    const uint32_t ks_end = min(a.ksteps, ks_begin + a.stage_chunk);
+    const uint32_t r0 = ks_begin * 32u, nrows = (ks_end - ks_begin) * 32u;
+
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t *segr = a.seg + (uint64_t)tile * a.K;
+
+    // X rows [r0, r0 + nrows) of the tile's index row, 16 tokens each, into LDS.
+    for (uint32_t q = (uint32_t)tid; q < nrows * 2u; q += 256u) {
+        const uint32_t r = r0 + (q >> 1), k = r / a.S, s = r - k * a.S;
+        const u4_t v = *reinterpret_cast<const u4_t *>(a.X + segr[k] + (uint64_t)s * a.step +
+                                                        (q & 1u) * 8u);
+        *reinterpret_cast<u4_t *>(&xl[q >> 1][(q & 1u) * 8u]) = v;
+    }
+    __syncthreads();
+
+    const int blk0 = wave % BL, kw = wave / BL;
+    const int g = lane >> 4;
+    const int tr_row = 8 * g + ((lane & 15) >> 2);
+    const int tr_col = 4 * (lane & 3);
+    const h8_t *wf = reinterpret_cast<const h8_t *>(a.Wf) + (uint64_t)tile * a.ksteps * NB * 64 +
+                     lane;
+    f4_t acc[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) acc[i] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (uint32_t ks = ks_begin + (uint32_t)kw; ks < ks_end; ks += 8u * KW) {
+        h8_t af[8][BPW];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t k2 = ks + (uint32_t)u * KW;
+            if (k2 < ks_end) {
+#pragma unroll
+                for (int i = 0; i < BPW; ++i)
+                    af[u][i] = wf[((uint64_t)k2 * NB + blk0 + BL * i) * 64];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t k2 = ks + (uint32_t)u * KW;
+            if (k2 < ks_end) {
+                const _Float16 *p = &xl[(k2 - ks_begin) * 32u + tr_row][tr_col];
+                const h4_t lo = lds_read_tr16(p);
+                const h4_t hi = lds_read_tr16(p + 4 * NARROW_PITCH);
+                const h8_t b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int i = 0; i < BPW; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u][i], b, acc[i], 0, 0, 0);
+            }
+        }
+    }
+
+    if constexpr (KW > 1) {  // waves kw = 0..KW-1 of a block: summed in kw order by wave kw = 0
+        red[wave][lane] = acc[0];
+        __syncthreads();
+        if (kw != 0) return;
+        f4_t s = red[blk0][lane];
+        for (int k2 = 1; k2 < KW; ++k2) {
+            const f4_t o = red[blk0 + BL * k2][lane];
+            s[0] += o[0];
+            s[1] += o[1];
+            s[2] += o[2];
+            s[3] += o[3];
+        }
+        acc[0] = s;
+    }
+
+    // Lane holds C[4g + i][lane & 15]: neuron 16*blk + 4g + i, token lane & 15.
+    const uint32_t t = (uint32_t)(lane & 15);
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi) {
+        const uint32_t blk = (uint32_t)(blk0 + BL * bi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
+            if (a.part) {
+                a.part[((uint64_t)zgroup * a.cout + j) * 16u + t] = acc[bi][i];
+                continue;
+            }
+            const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
+            if (oj == K44_CMAP_EMPTY) continue;
+            const uint64_t o = oj * a.out_stride + t;
+            const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
+            const float r = a.R ? __half2float(a.R[o]) : 0.0f;
+            const float v = acc[bi][i] + b;
+            a.Y[o] = __float2half_rn(a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r);
+        }
+    }
+}
+
+hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
+                              hipStream_t stream) {
+    if (items == 0u) return hipSuccess;
+    const dim3 grid(items), block(256);
+    switch (nt) {
+    case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, g); break;
+    case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, g); break;
+    case 64u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<64>, grid, block, 0, stream, g); break;
+    case 128u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<128>, grid, block, 0, stream, g); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace k44dev

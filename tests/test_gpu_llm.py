@@ -54,8 +54,8 @@ def _groups(cmds):
 
 
 def _check_commands(plan, spec, wts, ids, decode, tag):
-    """Runs the plan node by node; each node's output is compared with the CPU restatement of
-    that node applied to the canvas contents it read."""
+    """Runs the plan node by node; each node's output (token columns < the plan's token count)
+    is compared with the CPU restatement of that node applied to the canvas contents it read."""
     valid = len(ids)
     T = stride_of(valid)
     projs = _projections(spec, wts)
@@ -86,7 +86,8 @@ def _check_commands(plan, spec, wts, ids, decode, tag):
             assert np.array_equal(y.view(np.uint16), lo.embed(wts.embed, ids, T).view(np.uint16))
             continue
         if typ == "SWIGLU_MUL_1D":  # a product of two fp16 is exact in fp32: one rounding
-            assert np.array_equal(y.view(np.uint16), lo.mul(a, b).view(np.uint16)), name
+            assert np.array_equal(y[:, :valid].view(np.uint16),
+                                  lo.mul(a, b)[:, :valid].view(np.uint16)), name
             continue
         if typ == "K44_WAVE":
             p, act = projs[name]
@@ -101,7 +102,8 @@ def _check_commands(plan, spec, wts, ids, decode, tag):
             else:
                 ref, st_ref = lo.token_shift(x, mixes[name], spec.prompt, valid, f64=True)
             assert np.array_equal(st.view(np.uint16), st_ref.view(np.uint16)), f"{name} state"
-        err = lo.orc.rel_err(y.astype(np.float64), ref)
+        # token columns past the plan's token count are unspecified (narrow kernels skip them)
+        err = lo.orc.rel_err(y[:, :valid].astype(np.float64), ref[:, :valid])
         worst[typ] = max(worst.get(typ, 0.0), err)
         assert err <= TOL, f"{tag} {name}: rel err {err:.3e}"
     _log(f"[{tag}] per-node worst rel err: "

@@ -119,3 +119,43 @@ def test_dense_linear_layer_takes_mfma(wavec, orc):
     y0 = int(cmd["y_off"])
     y = canvas[y0:y0 + dout * st].view(np.float16).reshape(dout, st).astype(np.float64)
     assert orc.rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 16])
+@pytest.mark.parametrize("nt", [16, 32, 64, 128])
+def test_narrow_mfma_decode_sizes(wavec, orc, monkeypatch, tokens, nt):
+    """Waves over at most 16 tokens take the narrow MFMA kernel (16-token tiles, contraction
+    chunks in LDS, split-K partials); valid columns match the oracle and the wide kernel."""
+    rng = np.random.default_rng(tokens * 1000 + nt)
+    S, K, tiles = 512, 4, 3
+    C = 16384
+    starts = (rng.integers(0, C // S, size=(tiles, K)) * S).astype(np.uint32)
+    cout = tiles * nt
+    w = synth.normal_f16(rng, (cout, K * S), 0.02)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    ys = {}
+    for mode in ("narrow", "wide"):
+        if mode == "wide":
+            monkeypatch.setenv("K44WAVEC_NARROW", "0")
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("x", C, 1, tokens, is_1d=True)
+        g.add_cluster_wave("w", "x", "y", starts, S, w, b, cluster=nt, act="gelu", res_blob="x")
+        plan = g.compile()
+        plan.init_gpu()
+        rep = plan.exec_report()["waves"][0]
+        assert rep["path"] == ("mfma_narrow" if mode == "narrow" else "mfma_tile"), rep
+        plan.fill_input_uniform(9)
+        plan.execute(1)
+        st = stride_of(tokens)
+        canvas = plan.read_canvas(0, int(plan.summary["canvas_elems"]))
+        x0 = int(plan.cmds[0]["src_off"])
+        y0 = int(plan.cmds[0]["y_off"])
+        y = canvas[y0:y0 + cout * st].view(np.float16).reshape(cout, st)[:, :tokens]
+        seg = (x0 + starts.astype(np.uint64) * st).ravel()
+        ref = orc.wave_f64(canvas, seg, w, b, None, K, S, nt, st, st, st, "gelu", res_off=x0)
+        err = orc.rel_err(y.astype(np.float64), ref[:, :tokens])
+        print(f"[narrow {tokens} tok nt={nt} {mode}] ksplit {rep['ksplit']} rel err {err:.3e}",
+              flush=True)
+        assert err <= TOL
+        ys[mode] = y.astype(np.float64)
+    assert orc.rel_err(ys["narrow"], ys["wide"]) <= TOL
