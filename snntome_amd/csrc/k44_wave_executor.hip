@@ -414,13 +414,15 @@ struct K44GpuExecutorState {
             wx.narrow = Lo.W <= 16u && !(nw_env && std::string(nw_env) == "0");
             wx.part_tokens = wx.narrow ? 16u : wx.tokens;
             if (wx.narrow) {
-                // Contraction chunks of <= 16 k-steps (512 rows in LDS); ~512 workgroups.
+                // Contraction chunks of 8..16 k-steps (<= 512 rows in LDS), ~256 workgroups per
+                // wave when the wave has fewer tiles than that.
                 wx.path = "mfma_narrow";
                 wx.why += " (at most 16 tokens: weight-streaming narrow tile)";
                 wx.mt = 16u;
                 const uint32_t ksteps = c.B_raw / 32u;
-                uint32_t want = std::max<uint32_t>((512u + (uint32_t)rows - 1u) / (uint32_t)rows,
-                                                   (ksteps + 15u) / 16u);
+                uint32_t want = (256u + (uint32_t)rows - 1u) / (uint32_t)rows;
+                want = std::min(want, (ksteps + 7u) / 8u);
+                want = std::max(want, (ksteps + 15u) / 16u);
                 want = std::max(1u, std::min(want, ksteps));
                 wx.stage_chunk = (ksteps + want - 1u) / want;
                 wx.kgroups = (ksteps + wx.stage_chunk - 1u) / wx.stage_chunk;

@@ -4,17 +4,18 @@
 
 namespace k44dev {
 
-// One workgroup of 1024 threads per 32-token tile: 4 token-octets x 256 channel lanes.  Each
-// thread reads 16-byte runs of 8 tokens down its channel stripe (8 loads in flight), the 256
-// stripes of an octet reduce through LDS, and the same threads write the normalised values.
-__global__ __launch_bounds__(1024) void k44_rmsnorm_kernel(__half *__restrict__ y,
-                                                           const __half *__restrict__ x,
-                                                           const __half *__restrict__ gamma,
-                                                           uint32_t D, uint32_t stride, float eps) {
-    __shared__ float part[16][32];
-    __shared__ float inv_s[32];
-    const uint32_t oct = threadIdx.x & 3u, lane_c = threadIdx.x >> 2;
-    const uint32_t t0 = blockIdx.x * 32u + oct * 8u;
+// Workgroup = 8 consecutive tokens (one 16-byte column chunk) x 256 channel lanes: every lane
+// sums squares down its channel stripe with 8 loads in flight, the lanes reduce (shuffles, then
+// 4 waves in LDS, fixed order), and the workgroup writes the channel slice blockIdx.y of the
+// output.  Small token counts (decode) use several slices per token chunk, each recomputing the
+// (cache-resident) sum, so the grid still covers the chip.
+__global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y,
+                                                          const __half *__restrict__ x,
+                                                          const __half *__restrict__ gamma,
+                                                          uint32_t D, uint32_t stride, float eps,
+                                                          uint32_t cslice) {
+    __shared__ float part[4][8];
+    const uint32_t t0 = blockIdx.x * 8u, lane_c = threadIdx.x;
     float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t c = lane_c;
     for (; c + 7u * 256u < D; c += 8u * 256u) {
@@ -41,29 +42,22 @@ __global__ __launch_bounds__(1024) void k44_rmsnorm_kernel(__half *__restrict__ 
             ss[k] = fmaf(f, f, ss[k]);
         }
     }
-    // reduce the 16 channel lanes of each wave that share an octet (lanes differ in bits 2..5),
-    // then the 16 waves in a fixed order
 #pragma unroll
     for (int k = 0; k < 8; ++k)
 #pragma unroll
-        for (int m = 4; m < 64; m <<= 1) ss[k] += __shfl_xor(ss[k], m, 64);
+        for (int m = 1; m < 64; m <<= 1) ss[k] += __shfl_xor(ss[k], m, 64);
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    if (lane < 4u) {
+    if (lane == 0u) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) part[wave][lane * 8u + k] = ss[k];
-    }
-    __syncthreads();
-    if (threadIdx.x < 32u) {
-        float tot = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tot += part[r][threadIdx.x];
-        inv_s[threadIdx.x] = rsqrtf(tot / (float)D + eps);
+        for (int k = 0; k < 8; ++k) part[wave][k] = ss[k];
     }
     __syncthreads();
     float inv[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) inv[k] = inv_s[oct * 8u + k];
-    for (c = lane_c; c < D; c += 256u) {
+    for (int k = 0; k < 8; ++k)
+        inv[k] = rsqrtf((((part[0][k] + part[1][k]) + part[2][k]) + part[3][k]) / (float)D + eps);
+    const uint32_t c_end = min(D, (blockIdx.y + 1u) * cslice);
+    for (c = blockIdx.y * cslice + lane_c; c < c_end; c += 256u) {
         const uint4 v = *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0);
         const __half *h = reinterpret_cast<const __half *>(&v);
         const float g = gamma ? __half2float(gamma[c]) : 1.0f;
@@ -237,22 +231,31 @@ __global__ __launch_bounds__(256) void k44_argmax_partial_kernel(
     }
 }
 
-// ARGMAX pass 2: per token, merge the chunk partials in chunk order.
-__global__ __launch_bounds__(256) void k44_argmax_final_kernel(
+// ARGMAX pass 2: one wave per token; lanes take chunks lane, lane + 64, ... and the wave merges
+// them with the same rule (higher value, then lower channel), which is order-independent.
+__global__ __launch_bounds__(64) void k44_argmax_final_kernel(
     uint32_t *__restrict__ ids, uint32_t *__restrict__ history,
     const uint32_t *__restrict__ step_ctr, uint32_t hist_steps, uint32_t tokens,
     const float *__restrict__ pval, const uint32_t *__restrict__ pidx, uint32_t chunks,
     uint32_t ld) {
-    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
-    if (t >= tokens) return;
-    float v = pval[t];
-    uint32_t i = pidx[t];
-    for (uint32_t k = 1; k < chunks; ++k) amax_merge(v, i, pval[(uint64_t)k * ld + t], pidx[(uint64_t)k * ld + t]);
-    const uint32_t id = i == 0xffffffffu ? 0u : i;
-    ids[t] = id;
-    if (history) {
-        const uint32_t step = *step_ctr;
-        if (step < hist_steps) history[(uint64_t)step * tokens + t] = id;
+    const uint32_t t = blockIdx.x, lane = threadIdx.x;
+    float v = -INFINITY;
+    uint32_t i = 0xffffffffu;
+    for (uint32_t k = lane; k < chunks; k += 64u)
+        amax_merge(v, i, pval[(uint64_t)k * ld + t], pidx[(uint64_t)k * ld + t]);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const float ov = __shfl_xor(v, m, 64);
+        const uint32_t oi = __shfl_xor(i, m, 64);
+        amax_merge(v, i, ov, oi);
+    }
+    if (lane == 0u) {
+        const uint32_t id = i == 0xffffffffu ? 0u : i;
+        ids[t] = id;
+        if (history) {
+            const uint32_t step = *step_ctr;
+            if (step < hist_steps) history[(uint64_t)step * tokens + t] = id;
+        }
     }
 }
 
@@ -263,10 +266,15 @@ static uint32_t grid_for(uint64_t n) {
 
 hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
                           uint32_t stride, uint32_t tokens, float eps, hipStream_t stream) {
-    (void)tokens;
-    if (stride % 64u != 0u) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k44_rmsnorm_kernel, dim3(stride / 32u), dim3(1024), 0, stream, y, x, gamma,
-                       D, stride, eps);
+    if (stride % 64u != 0u || D == 0u || tokens == 0u || tokens > stride)
+        return hipErrorInvalidValue;
+    const uint32_t chunks = (tokens + 7u) / 8u;  // token columns >= tokens are not written
+    uint32_t slices = (256u + chunks - 1u) / chunks;
+    const uint32_t max_slices = (D + 255u) / 256u;
+    slices = slices < max_slices ? slices : max_slices;
+    const uint32_t cslice = (D + slices - 1u) / slices;
+    hipLaunchKernelGGL(k44_rmsnorm_kernel, dim3(chunks, (D + cslice - 1u) / cslice), dim3(256), 0,
+                       stream, y, x, gamma, D, stride, eps, cslice);
     return hipGetLastError();
 }
 
@@ -331,9 +339,8 @@ hipError_t launch_argmax(uint32_t *ids, uint32_t *history, uint32_t *step_ctr,
     uint32_t *pidx = reinterpret_cast<uint32_t *>(scratch + (uint64_t)used * stride);
     hipLaunchKernelGGL(k44_argmax_partial_kernel, dim3(stride / 64u, used), dim3(256), 0, stream,
                        pval, pidx, x, V, stride, chunk);
-    hipLaunchKernelGGL(k44_argmax_final_kernel, dim3((tokens + 255u) / 256u), dim3(256), 0,
-                       stream, ids, history, step_ctr, hist_steps, tokens, pval, pidx, used,
-                       stride);
+    hipLaunchKernelGGL(k44_argmax_final_kernel, dim3(tokens), dim3(64), 0, stream, ids, history,
+                       step_ctr, hist_steps, tokens, pval, pidx, used, stride);
     if (history) hipLaunchKernelGGL(k44_step_inc_kernel, dim3(1), dim3(1), 0, stream, step_ctr);
     return hipGetLastError();
 }

@@ -41,6 +41,21 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
 
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t *segr = a.seg + (uint64_t)tile * a.K;
+    const int blk0 = wave % BL, kw = wave / BL;
+    const h8_t *wf = reinterpret_cast<const h8_t *>(a.Wf) + (uint64_t)tile * a.ksteps * NB * 64 +
+                     lane;
+
+    // The first 8 k-steps' A fragments are requested before the X gather, so both are in
+    // flight together (the chunk is latency-bound: a few k-steps per workgroup).
+    h8_t af[8][BPW];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const uint32_t k2 = ks_begin + (uint32_t)kw + (uint32_t)u * KW;
+        if (k2 < ks_end) {
+#pragma unroll
+            for (int i = 0; i < BPW; ++i) af[u][i] = wf[((uint64_t)k2 * NB + blk0 + BL * i) * 64];
+        }
+    }
 
     // X rows [r0, r0 + nrows) of the tile's index row, 16 tokens each, into LDS.
     for (uint32_t q = (uint32_t)tid; q < nrows * 2u; q += 256u) {
@@ -51,25 +66,23 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
     }
     __syncthreads();
 
-    const int blk0 = wave % BL, kw = wave / BL;
     const int g = lane >> 4;
     const int tr_row = 8 * g + ((lane & 15) >> 2);
     const int tr_col = 4 * (lane & 3);
-    const h8_t *wf = reinterpret_cast<const h8_t *>(a.Wf) + (uint64_t)tile * a.ksteps * NB * 64 +
-                     lane;
     f4_t acc[BPW];
 #pragma unroll
     for (int i = 0; i < BPW; ++i) acc[i] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     for (uint32_t ks = ks_begin + (uint32_t)kw; ks < ks_end; ks += 8u * KW) {
-        h8_t af[8][BPW];
+        if (ks != ks_begin + (uint32_t)kw) {  // later batches: load this batch's fragments
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const uint32_t k2 = ks + (uint32_t)u * KW;
-            if (k2 < ks_end) {
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t k2 = ks + (uint32_t)u * KW;
+                if (k2 < ks_end) {
 #pragma unroll
-                for (int i = 0; i < BPW; ++i)
-                    af[u][i] = wf[((uint64_t)k2 * NB + blk0 + BL * i) * 64];
+                    for (int i = 0; i < BPW; ++i)
+                        af[u][i] = wf[((uint64_t)k2 * NB + blk0 + BL * i) * 64];
+                }
             }
         }
 #pragma unroll

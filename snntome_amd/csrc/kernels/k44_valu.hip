@@ -51,10 +51,11 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp)
     const uint64_t q = (uint64_t)(blockIdx.x - grp.epi_start[w]) * 256u + threadIdx.x;
     if (q >= (uint64_t)cout * per_row) return;
     const uint32_t j = (uint32_t)(q / per_row), t = (uint32_t)(q - (uint64_t)j * per_row) * 4u;
-    const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-    if (oj == K44_CMAP_EMPTY) return;
+    // cout_map entry, bias and the first partials are independent loads: issue them together.
     const uint64_t plane4 = (uint64_t)cout * tokens / 4u;
     const float4 *p = reinterpret_cast<const float4 *>(a.part + (uint64_t)j * tokens + t);
+    const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
+    const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
     float4 v = p[0];
     uint32_t z = 1;
     for (; z + 8u <= groups; z += 8u) {  // 8 partial loads in flight, summed in z order
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp)
         v.z += u1.z;
         v.w += u1.w;
     }
-    const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
+    if (oj == K44_CMAP_EMPTY) return;
     const uint64_t o = oj * a.out_stride + t;
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.R) {
