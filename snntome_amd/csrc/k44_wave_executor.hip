@@ -155,8 +155,11 @@ struct AuxExec {
     DevBuf<__half> table;  // gamma (RMSNORM), mix (TOKEN_SHIFT), embedding table (EMBED)
 };
 
-uint32_t pick_mt(uint32_t tokens) {
-    for (uint32_t mt : {512u, 256u, 128u}) if (tokens % mt == 0u) return mt;
+// Tokens per MFMA workgroup: the widest tile (most reuse of each weight fragment) that still
+// gives >= 256 workgroups over `tiles` neuron tiles; 64 otherwise (then split-K adds more).
+uint32_t pick_mt(uint32_t tokens, uint64_t tiles) {
+    for (uint32_t mt : {512u, 256u, 128u})
+        if (tokens % mt == 0u && tiles * (tokens / mt) >= 256u) return mt;
     return 64u;
 }
 
@@ -408,7 +411,7 @@ struct K44GpuExecutorState {
                      " and segments are whole 32-position K-steps: dense " + std::to_string(cl) +
                      " x " + std::to_string(c.B_raw) + " x " + std::to_string(wx.tokens) +
                      " contraction per tile on v_mfma_f32_16x16x32_f16";
-            wx.mt = pick_mt(wx.tokens);
+            wx.mt = pick_mt(wx.tokens, rows);
             wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
             const char *nw_env = std::getenv("K44WAVEC_NARROW");
             wx.narrow = Lo.W <= 16u && !(nw_env && std::string(nw_env) == "0");

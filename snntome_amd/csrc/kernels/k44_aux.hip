@@ -4,25 +4,29 @@
 
 namespace k44dev {
 
-// Workgroup = 8 consecutive tokens (one 16-byte column chunk) x 256 channel lanes: every lane
-// sums squares down its channel stripe with 8 loads in flight, the lanes reduce (shuffles, then
-// 4 waves in LDS, fixed order), and the workgroup writes the channel slice blockIdx.y of the
-// output.  Small token counts (decode) use several slices per token chunk, each recomputing the
-// (cache-resident) sum, so the grid still covers the chip.
+// Workgroup = OCT token octets (8 consecutive tokens = one 16-byte column chunk each) x
+// 256/OCT channel lanes: every lane sums squares down its channel stripe with 8 loads in flight
+// (OCT lanes side by side read 16*OCT contiguous bytes of a channel row), the lanes of an octet
+// reduce (shuffles, then the 4 waves in LDS in a fixed order), and the workgroup writes channel
+// slice blockIdx.y of its tokens.  Small token counts (decode) use OCT = 1 and several slices
+// per token chunk, each recomputing the (cache-resident) sum, so the grid still fills the chip.
+template <int OCT>
 __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y,
                                                           const __half *__restrict__ x,
                                                           const __half *__restrict__ gamma,
                                                           uint32_t D, uint32_t stride, float eps,
                                                           uint32_t cslice) {
-    __shared__ float part[4][8];
-    const uint32_t t0 = blockIdx.x * 8u, lane_c = threadIdx.x;
+    constexpr uint32_t CL = 256u / OCT;  // channel lanes
+    __shared__ float part[4][OCT * 8];
+    const uint32_t oct = threadIdx.x % OCT, lane_c = threadIdx.x / OCT;
+    const uint32_t t0 = (blockIdx.x * OCT + oct) * 8u;
     float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t c = lane_c;
-    for (; c + 7u * 256u < D; c += 8u * 256u) {
+    for (; c + 7u * CL < D; c += 8u * CL) {
         uint4 v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-            v[u] = *reinterpret_cast<const uint4 *>(x + (uint64_t)(c + u * 256u) * stride + t0);
+            v[u] = *reinterpret_cast<const uint4 *>(x + (uint64_t)(c + u * CL) * stride + t0);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const __half *h = reinterpret_cast<const __half *>(&v[u]);
@@ -33,7 +37,7 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
             }
         }
     }
-    for (; c < D; c += 256u) {
+    for (; c < D; c += CL) {
         const uint4 v = *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0);
         const __half *h = reinterpret_cast<const __half *>(&v);
 #pragma unroll
@@ -45,19 +49,21 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
 #pragma unroll
     for (int k = 0; k < 8; ++k)
 #pragma unroll
-        for (int m = 1; m < 64; m <<= 1) ss[k] += __shfl_xor(ss[k], m, 64);
+        for (int m = OCT; m < 64; m <<= 1) ss[k] += __shfl_xor(ss[k], m, 64);
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    if (lane == 0u) {
+    if (lane < OCT) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) part[wave][k] = ss[k];
+        for (int k = 0; k < 8; ++k) part[wave][lane * 8u + k] = ss[k];
     }
     __syncthreads();
     float inv[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-        inv[k] = rsqrtf((((part[0][k] + part[1][k]) + part[2][k]) + part[3][k]) / (float)D + eps);
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t q = oct * 8u + k;
+        inv[k] = rsqrtf((((part[0][q] + part[1][q]) + part[2][q]) + part[3][q]) / (float)D + eps);
+    }
     const uint32_t c_end = min(D, (blockIdx.y + 1u) * cslice);
-    for (c = blockIdx.y * cslice + lane_c; c < c_end; c += 256u) {
+    for (c = blockIdx.y * cslice + lane_c; c < c_end; c += CL) {
         const uint4 v = *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0);
         const __half *h = reinterpret_cast<const __half *>(&v);
         const float g = gamma ? __half2float(gamma[c]) : 1.0f;
@@ -268,13 +274,23 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
                           uint32_t stride, uint32_t tokens, float eps, hipStream_t stream) {
     if (stride % 64u != 0u || D == 0u || tokens == 0u || tokens > stride)
         return hipErrorInvalidValue;
-    const uint32_t chunks = (tokens + 7u) / 8u;  // token columns >= tokens are not written
+    // token columns >= tokens are not written; octets per workgroup: the widest that still
+    // gives >= 256 workgroups (coalesced rows), else 1 octet and channel slices
+    const uint32_t octets = (tokens + 7u) / 8u;
+    uint32_t oct = 8u;
+    while (oct > 1u && (octets + oct - 1u) / oct < 256u) oct >>= 1;
+    const uint32_t chunks = (octets + oct - 1u) / oct;
     uint32_t slices = (256u + chunks - 1u) / chunks;
     const uint32_t max_slices = (D + 255u) / 256u;
     slices = slices < max_slices ? slices : max_slices;
     const uint32_t cslice = (D + slices - 1u) / slices;
-    hipLaunchKernelGGL(k44_rmsnorm_kernel, dim3(chunks, (D + cslice - 1u) / cslice), dim3(256), 0,
-                       stream, y, x, gamma, D, stride, eps, cslice);
+    const dim3 grid(chunks, (D + cslice - 1u) / cslice);
+    switch (oct) {
+    case 8u: hipLaunchKernelGGL(k44_rmsnorm_kernel<8>, grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice); break;
+    case 4u: hipLaunchKernelGGL(k44_rmsnorm_kernel<4>, grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice); break;
+    case 2u: hipLaunchKernelGGL(k44_rmsnorm_kernel<2>, grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice); break;
+    default: hipLaunchKernelGGL(k44_rmsnorm_kernel<1>, grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice); break;
+    }
     return hipGetLastError();
 }
 

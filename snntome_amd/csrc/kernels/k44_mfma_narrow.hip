@@ -11,8 +11,10 @@
 //    waves of a block take its k-steps round-robin and meet in LDS in a fixed order;
 //  * A fragments (host-arranged [tile][k-step][16-block][lane][8]) stream from HBM with 8 k-steps
 //    of loads in flight per wave before the first MFMA that needs them;
-//  * one chunk: fused epilogue; several: fp32 partials [z][cout][16] for
-//    k44_splitk_epilogue_kernel (summed in chunk order, bit-reproducible).
+//  * one chunk: fused epilogue; several: fp32 partials [z][cout][16], summed in chunk order
+//    (bit-reproducible) by k44_splitk_epilogue_kernel.  (Reducing them in the kernel through a
+//    per-tile arrival counter needs a device-scope release per workgroup — an L2 write-back on
+//    this GPU — and measured 4x slower on decode-sized waves.)
 // Columns 16..stride-1 of the output rows are not written.
 #include "k44_launch.hpp"
 
@@ -27,6 +29,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
     constexpr int BL = NB < 4 ? NB : 4;        // distinct blocks handled at once by the 4 waves
     constexpr int KW = 4 / BL;                 // waves sharing a block (split k-steps)
     constexpr int BPW = NB / BL;               // blocks per wave
+    constexpr int AB = 16;                     // k-steps of A fragments in flight per wave
     __shared__ __attribute__((aligned(16))) _Float16 xl[NARROW_MAX_ROWS][NARROW_PITCH];
     __shared__ f4_t red[KW > 1 ? 4 : 1][64];
 
@@ -45,11 +48,11 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
     const h8_t *wf = reinterpret_cast<const h8_t *>(a.Wf) + (uint64_t)tile * a.ksteps * NB * 64 +
                      lane;
 
-    // The first 8 k-steps' A fragments are requested before the X gather, so both are in
-    // flight together (the chunk is latency-bound: a few k-steps per workgroup).
-    h8_t af[8][BPW];
+    // The first AB k-steps' A fragments are requested before the X gather, so both are in
+    // flight together (a chunk is a handful of k-steps: the workgroup is latency-bound).
+    h8_t af[AB][BPW];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < AB; ++u) {
         const uint32_t k2 = ks_begin + (uint32_t)kw + (uint32_t)u * KW;
         if (k2 < ks_end) {
 #pragma unroll
@@ -73,10 +76,10 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
 #pragma unroll
     for (int i = 0; i < BPW; ++i) acc[i] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (uint32_t ks = ks_begin + (uint32_t)kw; ks < ks_end; ks += 8u * KW) {
-        if (ks != ks_begin + (uint32_t)kw) {  // later batches: load this batch's fragments
+    for (uint32_t ks = ks_begin + (uint32_t)kw; ks < ks_end; ks += (uint32_t)AB * KW) {
+        if (ks != ks_begin + (uint32_t)kw) {  // later batches (chunks longer than AB k-steps)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < AB; ++u) {
                 const uint32_t k2 = ks + (uint32_t)u * KW;
                 if (k2 < ks_end) {
 #pragma unroll
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
             }
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < AB; ++u) {
             const uint32_t k2 = ks + (uint32_t)u * KW;
             if (k2 < ks_end) {
                 const _Float16 *p = &xl[(k2 - ks_begin) * 32u + tr_row][tr_col];
@@ -100,40 +103,56 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
         }
     }
 
+    bool writer = true;  // this wave holds the final (summed over its KW group) accumulators
     if constexpr (KW > 1) {  // waves kw = 0..KW-1 of a block: summed in kw order by wave kw = 0
         red[wave][lane] = acc[0];
         __syncthreads();
-        if (kw != 0) return;
-        f4_t s = red[blk0][lane];
-        for (int k2 = 1; k2 < KW; ++k2) {
-            const f4_t o = red[blk0 + BL * k2][lane];
-            s[0] += o[0];
-            s[1] += o[1];
-            s[2] += o[2];
-            s[3] += o[3];
+        writer = kw == 0;
+        if (writer) {
+            f4_t s = red[blk0][lane];
+            for (int k2 = 1; k2 < KW; ++k2) {
+                const f4_t o = red[blk0 + BL * k2][lane];
+                s[0] += o[0];
+                s[1] += o[1];
+                s[2] += o[2];
+                s[3] += o[3];
+            }
+            acc[0] = s;
         }
-        acc[0] = s;
     }
 
     // Lane holds C[4g + i][lane & 15]: neuron 16*blk + 4g + i, token lane & 15.
     const uint32_t t = (uint32_t)(lane & 15);
+    if (!a.part) {  // whole contraction in this workgroup: fused epilogue
+        if (!writer) return;
 #pragma unroll
-    for (int bi = 0; bi < BPW; ++bi) {
-        const uint32_t blk = (uint32_t)(blk0 + BL * bi);
+        for (int bi = 0; bi < BPW; ++bi) {
+            const uint32_t blk = (uint32_t)(blk0 + BL * bi);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
-            if (a.part) {
-                a.part[((uint64_t)zgroup * a.cout + j) * 16u + t] = acc[bi][i];
-                continue;
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
+                const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
+                if (oj == K44_CMAP_EMPTY) continue;
+                const uint64_t o = oj * a.out_stride + t;
+                const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
+                const float r = a.R ? __half2float(a.R[o]) : 0.0f;
+                const float v = acc[bi][i] + b;
+                a.Y[o] = __float2half_rn(a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r);
             }
-            const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-            if (oj == K44_CMAP_EMPTY) continue;
-            const uint64_t o = oj * a.out_stride + t;
-            const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
-            const float r = a.R ? __half2float(a.R[o]) : 0.0f;
-            const float v = acc[bi][i] + b;
-            a.Y[o] = __float2half_rn(a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r);
+        }
+        return;
+    }
+
+    // Split contraction: fp32 partial [z][cout][16] of this chunk.
+    if (writer) {
+#pragma unroll
+        for (int bi = 0; bi < BPW; ++bi) {
+            const uint32_t blk = (uint32_t)(blk0 + BL * bi);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
+                a.part[((uint64_t)zgroup * a.cout + j) * 16u + t] = acc[bi][i];
+            }
         }
     }
 }

@@ -143,7 +143,7 @@ def test_narrow_mfma_decode_sizes(wavec, orc, monkeypatch, tokens, nt):
         plan = g.compile()
         plan.init_gpu()
         rep = plan.exec_report()["waves"][0]
-        assert rep["path"] == ("mfma_narrow" if mode == "narrow" else "mfma_tile"), rep
+        assert rep["path"] == ("mfma_tile" if mode == "wide" else "mfma_narrow"), rep
         plan.fill_input_uniform(9)
         plan.execute(1)
         st = stride_of(tokens)
@@ -157,5 +157,9 @@ def test_narrow_mfma_decode_sizes(wavec, orc, monkeypatch, tokens, nt):
         print(f"[narrow {tokens} tok nt={nt} {mode}] ksplit {rep['ksplit']} rel err {err:.3e}",
               flush=True)
         assert err <= TOL
+        for _ in range(3):  # repeated launches (split-K scratch reused): identical results
+            plan.execute(1)
+            again = plan.read_canvas(y0, cout * st).view(np.float16).reshape(cout, st)
+            assert np.array_equal(again[:, :tokens].view(np.uint16), y.view(np.uint16))
         ys[mode] = y.astype(np.float64)
     assert orc.rel_err(ys["narrow"], ys["wide"]) <= TOL
