@@ -155,11 +155,11 @@ struct AuxExec {
     DevBuf<__half> table;  // gamma (RMSNORM), mix (TOKEN_SHIFT), embedding table (EMBED)
 };
 
-// Tokens per MFMA workgroup: the widest tile (most reuse of each weight fragment) that still
-// gives >= 256 workgroups over `tiles` neuron tiles; 64 otherwise (then split-K adds more).
-uint32_t pick_mt(uint32_t tokens, uint64_t tiles) {
-    for (uint32_t mt : {512u, 256u, 128u})
-        if (tokens % mt == 0u && tiles * (tokens / mt) >= 256u) return mt;
+// Tokens per MFMA workgroup: the widest tile that divides the token count (most reuse of each
+// weight fragment; a 64-token workgroup is one wave with a long serial loop, measured slower
+// than a wider tile plus split-K on the same wave).
+uint32_t pick_mt(uint32_t tokens) {
+    for (uint32_t mt : {512u, 256u, 128u}) if (tokens % mt == 0u) return mt;
     return 64u;
 }
 
@@ -411,7 +411,7 @@ struct K44GpuExecutorState {
                      " and segments are whole 32-position K-steps: dense " + std::to_string(cl) +
                      " x " + std::to_string(c.B_raw) + " x " + std::to_string(wx.tokens) +
                      " contraction per tile on v_mfma_f32_16x16x32_f16";
-            wx.mt = pick_mt(wx.tokens, rows);
+            wx.mt = pick_mt(wx.tokens);
             wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
             const char *nw_env = std::getenv("K44WAVEC_NARROW");
             wx.narrow = Lo.W <= 16u && !(nw_env && std::string(nw_env) == "0");
@@ -434,9 +434,15 @@ struct K44GpuExecutorState {
                 const uint32_t stages = c.B_raw / wx.rows_per_stage;
                 const uint64_t wgs = (uint64_t)rows * (wx.tokens / wx.mt);
                 const char *sk_env = std::getenv("K44WAVEC_SPLITK");
+                // Few workgroups: split the contraction.  Each split adds a partial plane of
+                // 4 * cout * tokens bytes, so prefill-sized token counts split at most 8 ways
+                // with >= 4 stages per workgroup; small token counts up to 32 ways.
+                const bool wide_tokens = wx.tokens >= 1024u;
                 uint32_t want = wgs >= 256u ? 1u : (uint32_t)((512u + wgs - 1u) / wgs);
                 if (sk_env && std::string(sk_env) == "0") want = 1u;
-                want = std::max(1u, std::min(want, stages));
+                want = std::min(want, wide_tokens ? 8u : 32u);
+                const uint32_t min_stages = wide_tokens ? 4u : 1u;
+                want = std::max(1u, std::min(want, std::max(1u, stages / min_stages)));
                 wx.stage_chunk = (stages + want - 1u) / want;
                 wx.kgroups = (stages + wx.stage_chunk - 1u) / wx.stage_chunk;
                 if (wx.kgroups > 1u) wx.part_floats = (size_t)wx.kgroups * c.Cout * wx.tokens;
