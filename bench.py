@@ -154,8 +154,8 @@ def bench_llm(args):
     dec = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
     pre.init_gpu()
     dec.init_gpu()
-    pre.use_graph(True)
-    dec.use_graph(True)
+    pre.use_graph(not args.eager)
+    dec.use_graph(not args.eager)
     R, P, D = spec.requests, spec.prompt, spec.decode_steps
     prompt = np.random.default_rng(spec.seed).integers(0, spec.vocab, R * P).astype(np.uint32)
     rep = pre.exec_report()["waves"]
@@ -213,7 +213,7 @@ def bench_llm(args):
             "layers": spec.layers, "d": spec.d, "ffn": spec.ffn, "vocab": spec.vocab,
             "S": spec.S, "clusters_kept": [spec.kept(spec.d), spec.kept(spec.ffn)],
             "tile": spec.tile, "token_shift_rf": spec.rf, "requests": R, "prompt": P,
-            "decode_steps": D, "paths": paths,
+            "decode_steps": D, "paths": paths, "hip_graphs": not args.eager,
         },
         "prefill_ms": round(prefill_ms, 4),
         "prefill_tflops": round(pre_tf, 2),
@@ -251,6 +251,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="config 5: launch kernel by kernel instead of replaying HIP graphs")
     ap.add_argument("--copy-probe-gib", type=float, default=0.0,
                     help="only run a plain device copy of this many GiB (PMC calibration)")
     args = ap.parse_args()
