@@ -81,6 +81,7 @@ struct WaveExec {
     uint32_t mt = 0, rows_per_stage = 32, ksteps = 0;  // MFMA tile: tokens, positions/stage
     uint32_t kgroups = 1, stage_chunk = 0;  // MFMA split-K: workgroups per tile, stages each
     bool narrow = false;       // MFMA over <= 16 tokens (decode): k44_mfma_narrow_kernel
+    bool lane8 = false;        // VALU: 8 tokens (16-byte loads) per lane
     uint32_t part_tokens = 0;  // row length of split-K partials (16 narrow, tokens wide)
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
     uint64_t step = 1;
@@ -353,6 +354,7 @@ struct K44GpuExecutorState {
             if (s0 % 4u != 0u)
                 throw std::runtime_error("wave '" + c.name +
                                          "': token-shifted (unaligned) gathers not supported yet");
+
         {
             Ranges rd, wr;
             rd.reserve(starts.size() + c.Cout);
@@ -474,6 +476,18 @@ struct K44GpuExecutorState {
                          : (force ? std::string("forced by K44WAVEC_PATH")
                                   : std::string("segment rows not 16-byte aligned"));
             wx.slab = pick_slab(wx.tokens);
+            {
+                // 8 tokens per lane (16-byte loads) when the rows it gathers fit the 256 MB MALL
+                // (measured: configs 1 and 4 13-28 % faster); 4 tokens per lane for HBM-bound
+                // gathers (config 2: 2.5 % faster).  16-byte accesses need 8-element alignment.
+                const char *l8 = std::getenv("K44WAVEC_LANE8");
+                const bool want8 = l8 ? std::string(l8) == "1"
+                                      : wx.unique_rows * (uint64_t)wx.tokens * 2u < (256ull << 20);
+                bool ok8 = wx.out_stride % 8u == 0u && wx.y_off % 8u == 0u &&
+                           wx.res_off % 8u == 0u && wx.step % 8u == 0u;
+                for (uint64_t s0 : starts) ok8 = ok8 && s0 % 8u == 0u;
+                wx.lane8 = want8 && ok8;
+            }
             const char *ks_env = std::getenv("K44WAVEC_KSPLIT");
             wx.ksplit = (wx.K >= 2u && wx.K <= 8u) ? 4u : 1u;
             if (ks_env) wx.ksplit = std::string(ks_env) == "4" ? 4u : 1u;
@@ -798,6 +812,7 @@ struct K44GpuExecutorState {
               << ", \"U\": " << (w.mfma ? w.rows_per_stage : w.U)
               << ", \"ksplit\": " << (w.mfma ? w.kgroups : w.ksplit)
               << ", \"sorted_segments\": " << (w.sorted_segments ? "true" : "false")
+              << ", \"tokens_per_lane\": " << (w.mfma ? 0 : (w.lane8 ? 8 : 4))
               << ", \"flops\": " << (long long)w.flops
               << ", \"effective_flops\": " << (long long)w.eff_flops
               << ", \"mapped\": " << (w.cmap.p ? "true" : "false")
@@ -862,7 +877,7 @@ struct K44GpuExecutorState {
         a.cout = w.cout;
         a.out_stride = w.out_stride;
         a.act = w.act;
-        K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream));
+        K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream, w.lane8));
     }
 
     void launch_op(size_t i) {

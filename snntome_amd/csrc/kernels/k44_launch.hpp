@@ -12,8 +12,9 @@ namespace k44dev {
 
 // VALU gather-dot over `cout` neurons x `tokens` tokens with the given slab (64/128/256);
 // ksplit 4 = one neuron per workgroup, its segments split over the 4 waves.
+// lane8: 8 tokens (16-byte loads) per lane instead of 4 (8-byte loads); same weight layout.
 hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
-                             uint32_t tokens, hipStream_t stream);
+                             uint32_t tokens, hipStream_t stream, bool lane8 = false);
 
 // MFMA tile kernel over a group of waves (one kernel configuration): `items` workgroups (the
 // group's start[n]), block mt; nt in {16,32,64,128}, mt in {64,128,256,512}, rows_per_stage in

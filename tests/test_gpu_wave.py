@@ -33,10 +33,13 @@ def test_config1_full_wave(wavec, orc):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("lanes", [4, 8])
 @pytest.mark.parametrize("tokens", [64, 128, 256, 320, 512, 100])
 @pytest.mark.parametrize("act", ["none", "relu", "sigmoid", "silu", "leaky_relu", "gelu"])
-def test_activation_and_slab_shapes(wavec, orc, tokens, act):
-    """Every activation x every slab width (64/128/256 and ragged token counts)."""
+def test_activation_and_slab_shapes(wavec, orc, monkeypatch, tokens, act, lanes):
+    """Every activation x every slab width (64/128/256 and ragged token counts) x both lane
+    widths of the gather kernel (4 tokens / 8-byte loads, 8 tokens / 16-byte loads)."""
+    monkeypatch.setenv("K44WAVEC_LANE8", "1" if lanes == 8 else "0")
     acts = ["none", "relu", "sigmoid", "silu", "leaky_relu", "gelu"]
     rng = np.random.default_rng(tokens * 16 + acts.index(act))
     C, cout, K, S = 3000, 48, 3, 24
@@ -45,7 +48,8 @@ def test_activation_and_slab_shapes(wavec, orc, tokens, act):
     b = synth.normal_f16(rng, (cout,), 0.1)
     y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens, rows=cluster_rows(starts, S),
                                    weights=w, bias=b, act=act, seed=5)
-    assert plan.exec_report()["waves"][0]["S"] == S
+    rep = plan.exec_report()["waves"][0]
+    assert rep["S"] == S and rep["tokens_per_lane"] == lanes
     assert orc.rel_err(y, ref) <= TOL
 
 
