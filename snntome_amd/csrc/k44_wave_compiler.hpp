@@ -100,7 +100,8 @@ class K44WaveGraphCompiler {
                 plan.input_c = n.cout;
                 plan.input_h = n.h_out;
                 plan.input_w = n.w_out;
-                plan.input_res_key = n.is_1d_tokens ? (0x80000000u | n.w_out) : n.h_out;
+                // (the reference keys 2-D inputs by h alone, which names no layout when h != w)
+                plan.input_res_key = make_res_key(n.h_out, n.w_out, n.is_1d_tokens);
             } else if (op == "Flatten") {
                 const Shape3D s = in_shape();
                 n.cin = s.c;

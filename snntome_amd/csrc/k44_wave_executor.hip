@@ -27,6 +27,7 @@
 #include "k44_wave_compiler.hpp"
 #include "k44wavec.h"
 #include "kernels/k44_launch.hpp"
+#include "kernels/k44_spatial.hpp"
 
 namespace {
 
@@ -101,6 +102,12 @@ struct WaveExec {
     // merged and sorted: the host-side independence test of wave groups.
     std::vector<std::pair<uint64_t, uint64_t>> rd, wr;
     size_t part_floats = 0;  // split-K partials (kgroups * cout * tokens), 0 without split-K
+    // 2-D spatial wave (VALU over the padded-plane tile layout): tile tables, output plane.
+    bool tile2d = false;
+    DevBuf<uint32_t> tile_x, tile_y;
+    k44dev::Plane2D plane{};
+    uint32_t tiles = 0, tiles_per_frame = 0;
+    int masked = 0;
     // MFMA: descriptor of this wave alone (command-by-command execution).
     DevBuf<k44dev::MfmaTileArgs> one_args;
     DevBuf<uint32_t> one_start, one_epi;
@@ -154,7 +161,18 @@ struct AuxExec {
     bool decode = false, has_state = false;
     float eps = 1e-5f;
     DevBuf<__half> table;  // gamma (RMSNORM), mix (TOKEN_SHIFT), embedding table (EMBED)
+    // 2-D spatial commands (S2D, pools, upsample, scatter-upconv): channel count C, planes
+    k44dev::Plane2D pin{}, pout{};
+    uint32_t C = 0, out_channels = 0;
 };
+
+k44dev::Plane2D plane_of(const k44_host::K44ResDesc &L) {
+    return k44dev::Plane2D{L.H, L.W, L.W_pad, L.batch_size, L.single_stride, L.channel_stride};
+}
+
+// Canvas elements allocated past the plan's canvas: the misaligned 2-D gathers read up to 3
+// elements beyond the last one they use.
+constexpr uint64_t kCanvasSlack = 256;
 
 // Tokens per MFMA workgroup: the widest tile that divides the token count (most reuse of each
 // weight fragment; a 64-token workgroup is one wave with a long serial loop, measured slower
@@ -259,9 +277,12 @@ struct K44GpuExecutorState {
     void build_wave(const K44ExecCmd &c, WaveExec &wx) {
         const auto &Lo = plan_meta.res_map.at(c.res_key_out);
         auto itin = plan_meta.res_map.find(c.res_key_in);
-        if (!Lo.is_1d_tokens || itin == plan_meta.res_map.end() || !itin->second.is_1d_tokens)
-            throw std::runtime_error("wave '" + c.name +
-                                     "': 2-D spatial layouts are not supported by this executor");
+        if (itin == plan_meta.res_map.end())
+            throw std::runtime_error("wave '" + c.name + "': unknown input layout");
+        if (!Lo.is_1d_tokens || !itin->second.is_1d_tokens) {
+            build_wave2d(c, wx, Lo, itin->second);
+            return;
+        }
         if (c.h_idx.empty() || c.B == 0u || c.B_raw == 0u || c.h_idx.size() % c.B != 0u)
             throw std::runtime_error("wave '" + c.name + "': missing or malformed index table");
         if (c.h_w_wmma.size() * 8u < (size_t)c.Cout * c.B)
@@ -520,7 +541,174 @@ struct K44GpuExecutorState {
         wx.eff_flops = c.gflops * 1e9;
     }
 
+    // 2-D wave: every 64-token tile of the output layout gathers X at
+    // seg + s*step + tile_x[t] + m (tap-shifted, any alignment) and stores pixels at
+    // y_off + out_j*channel_stride + tile_y[t] + m.
+    void build_wave2d(const K44ExecCmd &c, WaveExec &wx, const K44ResDesc &Lo,
+                      const K44ResDesc &Li) {
+        if (Lo.is_image_token64 || Li.is_image_token64)
+            throw std::runtime_error("wave '" + c.name +
+                                     "': 64-frame interleaved image layouts are not supported");
+        if (Lo.is_1d_tokens || Li.is_1d_tokens || c.res_key_in != c.res_key_out)
+            throw std::runtime_error("wave '" + c.name +
+                                     "': 2-D wave whose input and output layouts differ");
+        if (c.h_idx.empty() || c.B == 0u || c.B_raw == 0u || c.h_idx.size() % c.B != 0u)
+            throw std::runtime_error("wave '" + c.name + "': missing or malformed index table");
+        if (c.h_w_wmma.size() * 8u < (size_t)c.Cout * c.B)
+            throw std::runtime_error("wave '" + c.name + "': weight block smaller than Cout x B");
+        const size_t rows = c.h_idx.size() / c.B;
+        if (rows * c.cluster_size != c.Cout)
+            throw std::runtime_error("wave '" + c.name + "': index rows x cluster != Cout");
+        if (c.has_cout_map && c.h_cout_map.size() < c.Cout)
+            throw std::runtime_error("wave '" + c.name + "': cout_map shorter than Cout");
+        if (Lo.h_tile_off_X.size() != Lo.num_tiles || Lo.h_tile_off_Y.size() != Lo.num_tiles)
+            throw std::runtime_error("wave '" + c.name + "': tile tables missing");
+        wx.tile2d = true;
+        wx.name = c.name;
+        wx.path = "valu_gather_tile";
+        wx.why = "2-D spatial layout: tap-shifted gathers over padded-plane tiles";
+        wx.cout = c.Cout;
+        wx.cluster = c.cluster_size;
+        wx.rows = (uint32_t)rows;
+        wx.step = Li.channel_stride;
+        wx.y_off = c.y_off;
+        wx.res_off = c.res_off;
+        wx.has_res = c.has_residual;
+        wx.act = (int)c.act;
+        if (wx.act < 0 || wx.act > 5)
+            throw std::runtime_error("wave '" + c.name + "': unknown activation id");
+        std::vector<uint64_t> starts;
+        segment_rows(c, wx.step, wx.S, starts);
+        wx.K = c.B_raw / wx.S;
+        wx.plane = plane_of(Lo);
+        wx.masked = Lo.needs_mask ? 1 : 0;
+        wx.tiles = Lo.num_tiles;
+        wx.tiles_per_frame = Lo.tiles_per_frame;
+        wx.tokens = Lo.num_tiles * 64u;
+        wx.out_stride = (uint32_t)Lo.channel_stride;
+        std::vector<uint32_t> tx(Lo.num_tiles), ty(Lo.num_tiles);
+        for (uint32_t t = 0; t < Lo.num_tiles; ++t) {
+            tx[t] = Lo.h_tile_off_X[t];
+            const uint32_t f = t / Lo.tiles_per_frame, tl = t % Lo.tiles_per_frame;
+            ty[t] = Lo.needs_mask ? f * Lo.single_stride + Lo.W_pad + 4u + 64u * tl
+                                  : Lo.h_tile_off_Y[t];
+        }
+        // Host-side bounds check of every element the kernel may touch.
+        const uint64_t n_canvas = plan_meta.canvas_elems;
+        const uint64_t tx_hi = *std::max_element(tx.begin(), tx.end());
+        const uint64_t ty_hi = *std::max_element(ty.begin(), ty.end());
+        uint64_t x_hi = 0;
+        for (uint64_t s0 : starts) x_hi = std::max(x_hi, s0);
+        x_hi += (uint64_t)(wx.S - 1u) * wx.step + tx_hi + 64u + 4u;
+        if (x_hi > n_canvas + kCanvasSlack)
+            throw std::runtime_error("wave '" + c.name + "': gather reaches past the canvas");
+        uint64_t oj_hi = c.Cout - 1u;
+        if (c.has_cout_map) {
+            oj_hi = 0;
+            for (uint32_t j = 0; j < c.Cout; ++j)
+                if (c.h_cout_map[j] != 0xffffu) oj_hi = std::max<uint64_t>(oj_hi, c.h_cout_map[j]);
+        }
+        const uint64_t span = oj_hi * Lo.channel_stride + ty_hi + 64u;
+        if (wx.y_off + span > n_canvas || (wx.has_res && wx.res_off + span > n_canvas) ||
+            wx.y_off + (uint64_t)c.Cout * Lo.channel_stride > n_canvas)
+            throw std::runtime_error("wave '" + c.name + "': output/residual past the canvas");
+        // Weights in synapse order (the gather walks synapses p = k*S + s of the row).
+        std::vector<uint16_t> wraw((size_t)c.Cout * c.B);
+        convert_wmma_to_raw(reinterpret_cast<uint4_host *>(wraw.data()), c.h_w_wmma.data(),
+                            c.Cout, c.B / 8u);
+        std::vector<__half> wh((size_t)c.Cout * c.B_raw);
+        for (size_t j = 0; j < c.Cout; ++j) {
+            for (uint32_t q = c.B_raw; q < c.B; ++q)
+                if (wraw[j * c.B + q] != 0u)
+                    throw std::runtime_error("wave '" + c.name +
+                                             "': non-zero weight on a padded synapse");
+            std::memcpy(&wh[j * c.B_raw], &wraw[j * c.B], (size_t)c.B_raw * 2u);
+        }
+        wx.w.upload(wh);
+        wx.seg.upload(starts);
+        std::vector<__half> bh(c.Cout);
+        for (size_t j = 0; j < c.Cout; ++j) {
+            const uint16_t v = j < c.h_bias.size() ? c.h_bias[j] : 0u;
+            std::memcpy(&bh[j], &v, 2);
+        }
+        if (c.has_bias) wx.bias.upload(bh);
+        if (c.has_cout_map)
+            wx.cmap.upload(std::vector<uint16_t>(c.h_cout_map.begin(), c.h_cout_map.begin() + c.Cout));
+        wx.tile_x.upload(tx);
+        wx.tile_y.upload(ty);
+        wx.flops = 2.0 * (double)c.Cout * c.B_raw * Lo.H * Lo.W * Lo.batch_size;
+        wx.eff_flops = c.gflops * 1e9;
+    }
+
+    // 2-D spatial aux commands (reference k44_wave_executor.cu:480-544).
+    void build_spatial(const K44ExecCmd &c, AuxExec &ax) {
+        const K44ResDesc &Li = plan_meta.res_map.at(c.res_key_in);
+        const K44ResDesc &Lo = plan_meta.res_map.at(c.res_key_out);
+        if (Li.is_1d_tokens || Lo.is_1d_tokens || Li.is_image_token64 || Lo.is_image_token64)
+            throw std::runtime_error("command '" + c.name +
+                                     "': needs 2-D single-frame-interleave layouts");
+        if (Li.batch_size != Lo.batch_size)
+            throw std::runtime_error("command '" + c.name + "': frame counts differ");
+        ax.type = c.type;
+        ax.name = c.name;
+        ax.y_off = c.y_off;
+        ax.src_off = c.src_off;
+        ax.pin = plane_of(Li);
+        ax.pout = plane_of(Lo);
+        uint32_t cin_planes = 0, cout_planes = 0;
+        switch (c.type) {
+        case K44CmdType::S2D_2X2:
+            ax.C = c.Cin;
+            cin_planes = c.Cin;
+            cout_planes = 4u * c.Cin;
+            if (2u * Lo.H > Li.H + 1u || 2u * Lo.W > Li.W + 1u)
+                throw std::runtime_error("command '" + c.name + "': S2D output too large");
+            break;
+        case K44CmdType::MAXPOOL_2X2:
+            ax.C = c.Cin;
+            cin_planes = cout_planes = c.Cin;
+            if (2u * Lo.H > Li.H || 2u * Lo.W > Li.W)
+                throw std::runtime_error("command '" + c.name + "': pool output too large");
+            break;
+        case K44CmdType::MAXPOOL_5X5:
+            ax.C = c.Cin;
+            cin_planes = cout_planes = c.Cin;
+            if (Lo.H != Li.H || Lo.W != Li.W)
+                throw std::runtime_error("command '" + c.name + "': 5x5 pool changes the size");
+            break;
+        case K44CmdType::UPSAMPLE_2X:
+            ax.C = c.Cin;
+            cin_planes = cout_planes = c.Cin;
+            if (Lo.H != 2u * Li.H || Lo.W != 2u * Li.W)
+                throw std::runtime_error("command '" + c.name + "': upsample sizes");
+            break;
+        case K44CmdType::SCATTER_UP2X2:
+            ax.C = c.Cout;
+            ax.D = c.Cin / 4u;  // channels between quad plane groups
+            if (c.Cin % 4u != 0u || ax.D < c.Cout)
+                throw std::runtime_error("command '" + c.name + "': quad tensor channels");
+            cin_planes = c.Cin;
+            cout_planes = c.Cout;
+            if (Lo.H != 2u * Li.H || Lo.W != 2u * Li.W)
+                throw std::runtime_error("command '" + c.name + "': scatter-upconv sizes");
+            break;
+        default:
+            throw std::runtime_error("command '" + c.name + "': not a spatial command");
+        }
+        ax.out_channels = cout_planes;
+        const uint64_t n_canvas = plan_meta.canvas_elems;
+        if (ax.src_off + (uint64_t)cin_planes * Li.channel_stride > n_canvas ||
+            ax.y_off + (uint64_t)cout_planes * Lo.channel_stride > n_canvas)
+            throw std::runtime_error("command '" + c.name + "': tensor past the canvas");
+    }
+
     void build_aux(const K44ExecCmd &c, AuxExec &ax) {
+        if (c.type == K44CmdType::S2D_2X2 || c.type == K44CmdType::MAXPOOL_2X2 ||
+            c.type == K44CmdType::MAXPOOL_5X5 || c.type == K44CmdType::UPSAMPLE_2X ||
+            c.type == K44CmdType::SCATTER_UP2X2) {
+            build_spatial(c, ax);
+            return;
+        }
         const K44ResDesc &L = plan_meta.res_map.at(c.res_key_out);
         if (!L.is_1d_tokens)
             throw std::runtime_error("command '" + c.name + "': needs a 1-D token layout");
@@ -619,6 +807,27 @@ struct K44GpuExecutorState {
             K44_HIP(k44dev::launch_embed(cv + a.y_off, a.table.p, ids.p, a.D, a.vocab, a.stride,
                                          a.tokens, stream));
             break;
+        case K44CmdType::S2D_2X2:
+            K44_HIP(k44dev::launch_s2d(cv + a.y_off, cv + a.src_off, a.C, a.pin, a.pout, stream));
+            K44_HIP(k44dev::launch_halo_clear(cv + a.y_off, a.out_channels, a.pout, stream));
+            break;
+        case K44CmdType::MAXPOOL_2X2:
+            K44_HIP(k44dev::launch_maxpool2(cv + a.y_off, cv + a.src_off, a.C, a.pin, a.pout, stream));
+            K44_HIP(k44dev::launch_halo_clear(cv + a.y_off, a.out_channels, a.pout, stream));
+            break;
+        case K44CmdType::MAXPOOL_5X5:
+            K44_HIP(k44dev::launch_maxpool5(cv + a.y_off, cv + a.src_off, a.C, a.pin, a.pout, stream));
+            K44_HIP(k44dev::launch_halo_clear(cv + a.y_off, a.out_channels, a.pout, stream));
+            break;
+        case K44CmdType::UPSAMPLE_2X:
+            K44_HIP(k44dev::launch_upsample2(cv + a.y_off, cv + a.src_off, a.C, a.pin, a.pout, stream));
+            K44_HIP(k44dev::launch_halo_clear(cv + a.y_off, a.out_channels, a.pout, stream));
+            break;
+        case K44CmdType::SCATTER_UP2X2:
+            K44_HIP(k44dev::launch_scatter_up2(cv + a.y_off, cv + a.src_off, a.C, a.D, a.pin,
+                                               a.pout, stream));
+            K44_HIP(k44dev::launch_halo_clear(cv + a.y_off, a.out_channels, a.pout, stream));
+            break;
         case K44CmdType::ARGMAX_1D:
             K44_HIP(k44dev::launch_argmax(ids.p, hist_steps ? history.p : nullptr, step_ctr.p,
                                           hist_steps, cv + a.src_off, a.D, a.stride, a.tokens,
@@ -661,10 +870,10 @@ struct K44GpuExecutorState {
         K44_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         K44_HIP(hipEventCreate(&ev0));
         K44_HIP(hipEventCreate(&ev1));
-        canvas.alloc(plan.canvas_elems);
+        canvas.alloc(plan.canvas_elems + kCanvasSlack);
         if (scratch_need) scratch.alloc(scratch_need);
         upload_mfma_descriptors();
-        K44_HIP(hipMemsetAsync(canvas.p, 0, plan.canvas_elems * 2u, stream));
+        K44_HIP(hipMemsetAsync(canvas.p, 0, (plan.canvas_elems + kCanvasSlack) * 2u, stream));
         if (id_tokens) {
             ids.alloc(id_tokens);
             step_ctr.alloc(1);
@@ -861,6 +1070,32 @@ struct K44GpuExecutorState {
             launch_mfma(w);
             return;
         }
+        if (w.tile2d) {
+            k44dev::GatherTileArgs a{};
+            a.X = canvas.p;
+            a.seg = w.seg.p;
+            a.W = w.w.p;
+            a.bias = w.bias.p;
+            a.cmap = w.cmap.p;
+            a.Y = canvas.p + w.y_off;
+            a.R = w.has_res ? canvas.p + w.res_off : nullptr;
+            a.tile_x = w.tile_x.p;
+            a.tile_y = w.tile_y.p;
+            a.step = w.step;
+            a.K = w.K;
+            a.S = w.S;
+            a.cluster = w.cluster;
+            a.cout = w.cout;
+            a.tiles = w.tiles;
+            a.out_stride = w.plane.channel_stride;
+            a.act = w.act;
+            a.plane = w.plane;
+            a.tiles_per_frame = w.tiles_per_frame;
+            a.masked = w.masked;
+            K44_HIP(k44dev::launch_gather_tile(a, stream));
+            K44_HIP(k44dev::launch_halo_clear(canvas.p + w.y_off, w.cout, w.plane, stream));
+            return;
+        }
         k44dev::GatherDotArgs a{};
         a.X = canvas.p;
         a.seg = w.seg.p;
@@ -937,7 +1172,9 @@ struct K44GpuExecutorState {
 
     void upload_input_f32(const float *in, size_t n) {
         const K44ResDesc &L = layout(plan_meta.input_res_key);
-        if (!L.is_1d_tokens) throw std::runtime_error("2-D input layouts are not supported");
+        if (L.is_image_token64)
+            throw std::runtime_error("64-frame interleaved image layouts are not supported");
+        // whole planes (zero halos): the region may hold another tensor's data from the last run
         std::vector<uint16_t> pad((size_t)plan_meta.input_c * L.channel_stride, 0u);
         for (uint32_t ch = 0; ch < plan_meta.input_c; ++ch)
             for (uint32_t y = 0; y < plan_meta.input_h; ++y)

@@ -376,6 +376,18 @@ class WaveGraph:
                                            int(pad)), "wavec_add_maxpool")
         return out_blob
 
+    def add_upconv2x2(self, name: str, in_blob: str, out_blob: str, cin: int, cout: int,
+                      weights: np.ndarray, bias: Optional[np.ndarray] = None) -> str:
+        """2x2 stride-2 transposed convolution; weights [cout][cin][2][2] (C ABI
+        wavec_add_upconv2x2, which the reference binds but wraps in no method)."""
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        b = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
+        _check(self._lib.wavec_add_upconv2x2(self._handle, name.encode(), in_blob.encode(),
+                                             out_blob.encode(), int(cin), int(cout),
+                                             _ptr(w, ctypes.c_float), _ptr(b, ctypes.c_float)),
+               "wavec_add_upconv2x2")
+        return out_blob
+
     def add_upsample2x(self, name: str, in_blob: str, out_blob: str) -> str:
         _check(self._lib.wavec_add_upsample2x(self._handle, name.encode(), in_blob.encode(),
                                               out_blob.encode()), "wavec_add_upsample2x")

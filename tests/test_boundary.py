@@ -90,11 +90,11 @@ def test_invalid_sparse_wave_is_rejected(wavec):
 
 def test_unsupported_plans_fail_init_with_message(wavec):
     """The executor refuses what it cannot run instead of silently skipping it."""
-    g = wavec.WaveGraph(kv_cache_max_seq=0)
-    g.add_input("img", 8, 16, 64)  # 2-D image
+    g = wavec.WaveGraph(kv_cache_max_seq=0, batch_size=64)  # 64-frame interleaved image layout
+    g.add_input("img", 8, 16, 64)
     g.add_conv2d("c", "img", "y", 8, 16, 3, 3, np.zeros((16, 8, 3, 3), np.float32), act="relu")
     plan = g.compile()
-    with pytest.raises(RuntimeError, match="2-D"):
+    with pytest.raises(RuntimeError, match="64-frame interleaved"):
         plan.init_gpu()
     g2 = wavec.WaveGraph(kv_cache_max_seq=0)
     g2.add_input("t", 128, 1, 64, is_1d=True)

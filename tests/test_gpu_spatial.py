@@ -1,0 +1,194 @@
+"""2-D (spatial) plans on the GPU: waves over the padded-plane tile layout (3x3 taps shifted by
+one element, masked tiles for widths that are not multiples of 64), the polyphase stride-2
+convolution, pools, upsampling, the 2x2 transposed convolution, halo hygiene and batched frames,
+against the CPU restatement in oracle/cnn_oracle.py."""
+import numpy as np
+import pytest
+
+from oracle import cnn_oracle as co
+from oracle import oracle as orc
+
+from wave_cases import TOL
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def _f16(rng, shape, s=1.0):
+    return (rng.standard_normal(shape) * s).astype(np.float16)
+
+
+def _conv_params(rng, cin, cout, k, s=0.2):
+    return (_f16(rng, (cout, cin, k, k), s / np.sqrt(cin * k * k) * 3),
+            _f16(rng, (cout,), 0.05))
+
+
+def _run(plan, x):
+    """infer_f32 of frame 0 -> fp16-valued float64 array [C][H][W]."""
+    y, _ = plan.infer_f32(x[0].astype(np.float32))
+    return y.astype(np.float64)
+
+
+@pytest.mark.parametrize("H,W", [(8, 64), (7, 20), (5, 30), (3, 130), (6, 192)])
+@pytest.mark.parametrize("act", ["relu", "gelu"])
+def test_conv3x3_same(wavec, H, W, act):
+    rng = np.random.default_rng(H * 1000 + W)
+    cin, cout = 5, 24
+    w, b = _conv_params(rng, cin, cout, 3)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("img", cin, H, W)
+    g.add_conv2d("c", "img", "y", cin, cout, 3, 3, w.astype(np.float32), b.astype(np.float32),
+                 stride=1, pad=1, act=act)
+    plan = g.compile()
+    plan.init_gpu()
+    assert plan.exec_report()["waves"][0]["path"] == "valu_gather_tile"
+    x = _f16(rng, (1, cin, H, W))
+    got = _run(plan, x)
+    ref = co.conv2d_f64(x, w, b, 1, 1, act)[0]
+    err = orc.rel_err(got, ref)
+    _log(f"[conv3x3 {H}x{W} {act}] rel err {err:.3e}")
+    assert err <= TOL
+
+
+def test_conv_residual_1x1_and_stride2(wavec):
+    rng = np.random.default_rng(7)
+    H, W, c0 = 16, 64, 6
+    w1, b1 = _conv_params(rng, c0, c0, 3)
+    w2, b2 = _conv_params(rng, c0, 16, 1)
+    w3, b3 = _conv_params(rng, 16, 12, 3)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("img", c0, H, W)
+    g.add_conv2d("c1", "img", "a", c0, c0, 3, 3, w1.astype(np.float32), b1.astype(np.float32),
+                 stride=1, pad=1, act="silu", res_blob="img")
+    g.add_conv2d("c2", "a", "b", c0, 16, 1, 1, w2.astype(np.float32), b2.astype(np.float32),
+                 stride=1, pad=0, act="relu")
+    g.add_conv2d("c3", "b", "y", 16, 12, 3, 3, w3.astype(np.float32), b3.astype(np.float32),
+                 stride=2, pad=1, act="none")
+    plan = g.compile()
+    assert [c["type"] for c in plan.cmds] == ["K44_WAVE", "K44_WAVE", "S2D_2X2", "K44_WAVE"]
+    plan.init_gpu()
+    x = _f16(rng, (1, c0, H, W))
+    got = _run(plan, x)
+    a = co.conv2d_f64(x, w1, b1, 1, 1, "silu", x).astype(np.float16)
+    bb = co.conv2d_f64(a, w2, b2, 1, 0, "relu").astype(np.float16)
+    ref = co.conv2d_f64(bb, w3, b3, 2, 1)[0]
+    scale = np.abs(ref).max()
+    err = np.abs(got - ref).max() / scale
+    _log(f"[residual/1x1/stride-2 chain] max|d|/max|ref| {err:.3e}")
+    assert got.shape == (12, 8, 32)
+    assert err <= 1e-2  # three layers, one fp16 rounding each (per-layer bound is TOL)
+
+
+@pytest.mark.parametrize("H,W", [(8, 64), (6, 20), (10, 34)])
+def test_pools_and_upsample_exact(wavec, H, W):
+    """Max and nearest copies are exact in fp16: bit-identical to the restatement."""
+    rng = np.random.default_rng(H + W)
+    C = 7
+    for op in ("maxpool2", "maxpool5", "upsample"):
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("img", C, H, W)
+        if op == "maxpool2":
+            g.add_maxpool("p", "img", "y", kernel_size=2, stride=2)
+        elif op == "maxpool5":
+            g.add_maxpool("p", "img", "y", kernel_size=5, stride=1, pad=2)
+        else:
+            g.add_upsample2x("p", "img", "y")
+        plan = g.compile()
+        plan.init_gpu()
+        x = _f16(rng, (1, C, H, W))
+        got = _run(plan, x).astype(np.float16)
+        ref = {"maxpool2": co.maxpool2, "maxpool5": co.maxpool5, "upsample": co.upsample2}[op](x)[0]
+        _log(f"[{op} {H}x{W}] shape {got.shape}")
+        assert got.shape == ref.shape
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("cout", [8, 16])
+def test_upconv2x2(wavec, cout):
+    rng = np.random.default_rng(cout)
+    H, W, cin = 6, 32, 10
+    w = _f16(rng, (cout, cin, 2, 2), 0.3)
+    b = _f16(rng, (cout,), 0.05)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("img", cin, H, W)
+    g.add_upconv2x2("u", "img", "y", cin, cout, w.astype(np.float32), b.astype(np.float32))
+    plan = g.compile()
+    assert [c["type"] for c in plan.cmds] == ["K44_WAVE", "SCATTER_UP2X2"]
+    plan.init_gpu()
+    x = _f16(rng, (1, cin, H, W))
+    got = _run(plan, x)
+    ref = co.upconv2x2_f64(x, w, b)[0]
+    err = orc.rel_err(got, ref)
+    _log(f"[upconv cout={cout}] rel err {err:.3e}")
+    assert got.shape == (cout, 2 * H, 2 * W)
+    assert err <= TOL
+
+
+def test_unet_block_end_to_end_and_halo_hygiene(wavec):
+    """conv -> stride-2 conv -> maxpool -> upsample x2 -> concat with the skip -> conv: run
+    twice, with a different input the second time, so stale canvas data from the first run sits
+    where the second run's halos must read as zero padding."""
+    rng = np.random.default_rng(11)
+    H, W, c0 = 16, 40, 4
+    w1, b1 = _conv_params(rng, c0, 8, 3)
+    w2, b2 = _conv_params(rng, 8, 16, 3)
+    w3, b3 = _conv_params(rng, 24, 8, 3)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("img", c0, H, W)
+    g.add_conv2d("c1", "img", "s", c0, 8, 3, 3, w1.astype(np.float32), b1.astype(np.float32),
+                 stride=1, pad=1, act="relu")
+    g.add_conv2d("c2", "s", "d", 8, 16, 3, 3, w2.astype(np.float32), b2.astype(np.float32),
+                 stride=2, pad=1, act="relu")
+    g.add_maxpool("mp", "d", "p", kernel_size=2, stride=2)
+    g.add_upsample2x("u1", "p", "q")
+    g.add_upsample2x("u2", "q", "r")
+    g.add_concat("cat", ["s", "r"], "k")
+    g.add_conv2d("c3", "k", "y", 24, 8, 3, 3, w3.astype(np.float32), b3.astype(np.float32),
+                 stride=1, pad=1, act="none")
+    plan = g.compile()
+    plan.init_gpu()
+    for run in range(2):
+        x = _f16(rng, (1, c0, H, W), 1.0 + run)
+        got = _run(plan, x)
+        s = co.conv2d_f64(x, w1, b1, 1, 1, "relu").astype(np.float16)
+        d = co.conv2d_f64(s, w2, b2, 2, 1, "relu").astype(np.float16)
+        r = co.upsample2(co.upsample2(co.maxpool2(d)))
+        k = np.concatenate([s, r], axis=1)
+        ref = co.conv2d_f64(k, w3, b3, 1, 1)[0]
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        _log(f"[unet block run {run}] max|d|/max|ref| {err:.3e}")
+        assert err <= 1e-2
+
+
+def test_batched_frames_on_canvas(wavec):
+    """Two frames per channel plane (batch_size 2): both frames written and read on the canvas
+    through the restated layout."""
+    rng = np.random.default_rng(5)
+    H, W, cin, cout, F = 6, 24, 3, 16, 2
+    w, b = _conv_params(rng, cin, cout, 3)
+    g = wavec.WaveGraph(kv_cache_max_seq=0, batch_size=F)
+    g.add_input("img", cin, H, W)
+    g.add_conv2d("c", "img", "y", cin, cout, 3, 3, w.astype(np.float32), b.astype(np.float32),
+                 stride=1, pad=1, act="relu")
+    plan = g.compile()
+    plan.init_gpu()
+    lay = co.Layout2D(H, W, F)
+    c = plan.cmds[0]
+    x = _f16(rng, (F, cin, H, W))
+    region = np.zeros(cin * lay.channel_stride, np.float16)
+    region[lay.offsets(cin).ravel()] = x.ravel()
+    plan.write_canvas(int(c["src_off"]), region)
+    plan.execute(1)
+    out = plan.read_canvas(int(c["y_off"]), cout * lay.channel_stride).view(np.float16)
+    got = out[lay.offsets(cout)].astype(np.float64)
+    ref = co.conv2d_f64(x, w, b, 1, 1, "relu")
+    err = orc.rel_err(got, ref)
+    _log(f"[frames={F}] rel err {err:.3e}")
+    assert err <= TOL
+    # halos of the output planes are zero padding
+    halo = np.ones(cout * lay.channel_stride, bool)
+    halo[lay.offsets(cout).ravel()] = False
+    assert not out[halo].any()

@@ -381,3 +381,26 @@ def test_pruned_wave_rejects_overlap(wavec):
     st = np.array([[0, 16]] * 16, np.uint32)  # clusters of 32 channels overlap
     with pytest.raises(RuntimeError, match="overlap"):
         g.add_pruned_wave("p", "x", "y", st, 32, np.zeros((16, 64), np.float16), tile=16)
+
+
+@pytest.mark.parametrize("H,W,batch", [(8, 64, 1), (5, 30, 1), (7, 20, 2), (4, 128, 3)])
+def test_2d_layout_matches_restatement(wavec, tmp_path, H, W, batch):
+    """The padded-plane layout the compiler writes into each 2-D wave's .tcff geometry tag
+    (W_pad, channel stride) equals the independent restatement oracle.cnn_oracle.Layout2D."""
+    from oracle import cnn_oracle as co
+
+    rng = np.random.default_rng(H * W)
+    g = wavec.WaveGraph(kv_cache_max_seq=0, batch_size=batch)
+    g.add_input("img", 3, H, W)
+    w = (rng.standard_normal((8, 3, 3, 3)) * 0.1).astype(np.float32)
+    g.add_conv2d("c", "img", "y", 3, 8, 3, 3, w, None, stride=1, pad=1, act="relu")
+    plan = g.compile()
+    p = tmp_path / "c.tcff"
+    plan.save_tcff(p, "L")
+    d = p.read_bytes()
+    (ifd,) = _tcff_ifds(d)
+    geo = struct.unpack_from("<10I", d, ifd[0x8444][2])
+    lay = co.Layout2D(H, W, min(batch, 8))
+    assert geo[:5] == (3, 1, 8, H, W)
+    assert geo[6] == lay.channel_stride and geo[7] == lay.W_pad and geo[9] == lay.W_pad + 4
+    assert geo[5] == plan.cmds[0]["Cout"] * lay.channel_stride
