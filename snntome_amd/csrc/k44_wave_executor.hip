@@ -76,12 +76,13 @@ struct DevBuf {
 // Device schedule of one K44_WAVE command.
 struct WaveExec {
     std::string name;
-    std::string path;      // "valu_gather_dot" | "mfma_tile"
+    std::string path;      // "valu_gather_dot" | "mfma_tile" | "mfma_dma" | "mfma_narrow" | ...
     std::string why;
     bool mfma = false;
     uint32_t mt = 0, rows_per_stage = 32, ksteps = 0;  // MFMA tile: tokens, positions/stage
     uint32_t kgroups = 1, stage_chunk = 0;  // MFMA split-K: workgroups per tile, stages each
     bool narrow = false;       // MFMA over <= 16 tokens (decode): k44_mfma_narrow_kernel
+    bool dma = false;          // MFMA over 512-token workgroups: k44_mfma_dma_kernel
     bool lane8 = false;        // VALU: 8 tokens (16-byte loads) per lane
     uint32_t part_tokens = 0;  // row length of split-K partials (16 narrow, tokens wide)
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
@@ -118,6 +119,7 @@ struct WaveExec {
 struct MfmaGroupExec {
     std::vector<size_t> members;  // wave indices, plan order
     uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0;
+    bool dma = false;
     size_t part_floats = 0;
     DevBuf<k44dev::MfmaTileArgs> args;
     DevBuf<uint32_t> start, epi;
@@ -327,15 +329,53 @@ struct K44GpuExecutorState {
         // different rows are read close in time (cache reuse instead of a second HBM read).
         const char *sort_env = std::getenv("K44WAVEC_SORT");
         wx.sorted_segments = wx.K > 1u && !(sort_env && std::string(sort_env) == "0");
+        const bool band_order = sort_env && std::string(sort_env) == "band";
         if (wx.sorted_segments) {
             std::vector<uint32_t> order(wx.K);
             std::vector<uint64_t> st(wx.K);
             std::vector<uint16_t> row_w((size_t)c.B_raw);
+            uint64_t lo = ~0ull, hi = 0;
+            for (uint64_t s0 : starts) {
+                lo = std::min(lo, s0);
+                hi = std::max(hi, s0);
+            }
+            const double span = (double)(hi - lo) + 1.0;
+            std::vector<int> slot_of(wx.K);
+            std::vector<char> used(wx.K);
             for (size_t r = 0; r < rows; ++r) {
                 uint64_t *sr = starts.data() + r * wx.K;
                 for (uint32_t k = 0; k < wx.K; ++k) order[k] = k;
                 std::stable_sort(order.begin(), order.end(),
                                  [&](uint32_t x, uint32_t y) { return sr[x] < sr[y]; });
+                if (band_order) {
+                    // Slot = the segment's address band (K equal bands of the wave's range),
+                    // so concurrently running rows read the same band at the same time;
+                    // collisions go to the nearest free slot.
+                    std::fill(used.begin(), used.end(), 0);
+                    std::vector<uint32_t> left;
+                    for (uint32_t q = 0; q < wx.K; ++q) {
+                        const uint32_t k = order[q];
+                        int b = (int)((double)(sr[k] - lo) * wx.K / span);
+                        b = std::min<int>(b, (int)wx.K - 1);
+                        if (!used[b]) {
+                            used[b] = 1;
+                            slot_of[k] = b;
+                        } else {
+                            left.push_back(k);
+                        }
+                    }
+                    for (uint32_t k : left) {
+                        int b = std::min<int>((int)((double)(sr[k] - lo) * wx.K / span),
+                                              (int)wx.K - 1);
+                        for (int d = 1;; ++d) {
+                            if (b - d >= 0 && !used[b - d]) { b -= d; break; }
+                            if (b + d < (int)wx.K && !used[b + d]) { b += d; break; }
+                        }
+                        used[b] = 1;
+                        slot_of[k] = b;
+                    }
+                    for (uint32_t k = 0; k < wx.K; ++k) order[slot_of[k]] = k;
+                }
                 bool identity = true;
                 for (uint32_t k = 0; k < wx.K; ++k) identity = identity && order[k] == k;
                 if (identity) continue;
@@ -439,6 +479,16 @@ struct K44GpuExecutorState {
             const char *nw_env = std::getenv("K44WAVEC_NARROW");
             wx.narrow = Lo.W <= 16u && !(nw_env && std::string(nw_env) == "0");
             wx.part_tokens = wx.narrow ? 16u : wx.tokens;
+            // 512-token workgroups of 32/64-neuron tiles stream through an LDS ring filled by
+            // direct loads (3 stages in flight per workgroup instead of 1).
+            const char *dma_env = std::getenv("K44WAVEC_DMA");
+            wx.dma = !wx.narrow && wx.mt == 512u && (cl == 32u || cl == 64u) &&
+                     !(dma_env && std::string(dma_env) == "0");
+            if (wx.dma) {
+                wx.path = "mfma_dma";
+                wx.why += " (512-token workgroups: 4-stage LDS ring filled by global_load_lds)";
+                wx.rows_per_stage = 32u;
+            }
             if (wx.narrow) {
                 // Contraction chunks of 8..16 k-steps (<= 512 rows in LDS), ~256 workgroups per
                 // wave when the wave has fewer tiles than that.
@@ -907,7 +957,7 @@ struct K44GpuExecutorState {
             if (grouping && !runs.empty() && runs.back().first == 2) {
                 MfmaGroupExec &g = *groups[runs.back().second];
                 bool ok = g.nt == w.cluster && g.mt == w.mt && g.rows == w.rows_per_stage &&
-                          g.members.size() < 64u;
+                          g.dma == w.dma && g.members.size() < 64u;
                 for (size_t m : g.members) {
                     if (!ok) break;
                     const WaveExec &o = *waves[m];
@@ -926,6 +976,7 @@ struct K44GpuExecutorState {
                 g->nt = w.cluster;
                 g->mt = w.mt;
                 g->rows = w.rows_per_stage;
+                g->dma = w.dma;
                 g->part_floats = w.part_floats;
                 runs.push_back({2, groups.size()});
                 groups.push_back(std::move(g));
@@ -1047,9 +1098,11 @@ struct K44GpuExecutorState {
     }
 
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
-                           uint32_t items, uint32_t epi_items) {
+                           uint32_t items, uint32_t epi_items, bool dma) {
         if (mt == 16u)  // narrow (<= 16 tokens)
             K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream));
+        else if (dma)
+            K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream));
         else
             K44_HIP(k44dev::launch_mfma_tile(d, nt, mt, rows, items, stream));
         if (epi_items) K44_HIP(k44dev::launch_splitk_epilogue(d, epi_items, stream));
@@ -1057,12 +1110,12 @@ struct K44GpuExecutorState {
 
     void launch_mfma(const WaveExec &w) {
         const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, w.one_epi.p, 1u};
-        launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items);
+        launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma);
     }
 
     void launch_group(const MfmaGroupExec &g) {
         const k44dev::MfmaGroup d{g.args.p, g.start.p, g.epi.p, (uint32_t)g.members.size()};
-        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items);
+        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma);
     }
 
     void launch_wave(const WaveExec &w) {

@@ -22,6 +22,10 @@ hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksp
 hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32_t rows_per_stage,
                             uint32_t items, hipStream_t stream);
 
+// LDS-DMA MFMA tile kernel (512 tokens per workgroup, 32-position stages in a 4-deep LDS ring)
+// over a group: `items` workgroups; nt in {32, 64}.
+hipError_t launch_mfma_dma(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream);
+
 // Narrow MFMA kernel (waves of at most 16 tokens) over a group: `items` workgroups (tiles x
 // contraction chunks per wave); nt in {16,32,64,128}.
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream);

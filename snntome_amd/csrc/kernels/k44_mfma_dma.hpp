@@ -1,0 +1,186 @@
+// k44_mfma_dma.hpp — MFMA dense-cluster wave kernel with an LDS ring filled by direct loads.
+//
+// Same contraction and epilogue as k44_mfma_tile_kernel (Y[NT][512 tokens] = W[NT][K*S] x
+// X_gathered[K*S][512] on v_mfma_f32_16x16x32_f16), for the shape that carries the large
+// waves: 512 tokens per workgroup (8 waves x 64 tokens), NT in {32, 64}.
+//
+// What differs is how data reaches LDS.  The register-staged kernel keeps one stage of X in
+// flight per workgroup (its loads must land in registers before they can be stored to LDS), so
+// it is bound by memory latency, not bandwidth.  Here every stage of 32 positions goes straight
+// from memory to LDS with global_load_lds (gfx950): each X row of 512 tokens is one
+// global_load_lds_dwordx4 (64 lanes x 16 bytes = the whole 1 KiB row, written at the row's
+// padded LDS pitch), and the stage's A fragments (64*NT bytes, contiguous in the upload order)
+// are NT/32 global_load_lds_dword per wave.  A ring of 4 stages keeps 3 stages (~113 KiB) of
+// every workgroup in flight while the 4th is multiplied.  No staging registers, no ds_write.
+//
+// Synchronisation per stage i (every wave issues the same D = 4 + NT/32 loads per stage):
+//   s_waitcnt vmcnt(2D) lgkmcnt(0)   own loads of stage i landed; own LDS reads of i-1 done
+//   s_barrier                        every wave's loads of stage i landed; nobody reads i-1
+//   issue stage i+3 into ring slot (i+3)%4 = (i-1)%4
+//   MFMAs of stage i from slot i%4
+// The last three stages drain with vmcnt(2D), vmcnt(D), vmcnt(0).  The waits are explicit
+// because a workgroup barrier with a memory fence (__syncthreads) would wait for every load in
+// flight; compiler barriers keep LDS accesses on their side of each s_barrier.
+#pragma once
+#include "k44_mfma_tile.hpp"
+
+namespace k44dev {
+
+typedef const __attribute__((address_space(1))) void kglobal_void;
+typedef const __attribute__((address_space(4))) uint64_t kconst_u64;
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at bits 15:14,
+// expcnt[6:4] left at its maximum, lgkmcnt[11:8] = 0).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+__device__ __forceinline__ void wg_barrier_no_fence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Byte address of a shared-memory location in the LDS aperture.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+__device__ __forceinline__ h8_t ds_read_b128_at(uint32_t addr) {
+    h8_t v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
+
+// ds_read_b64_tr_b16: 4 x 16-bit, transposed across each 16-lane group (see lds_read_tr16).
+__device__ __forceinline__ h4_t ds_read_tr16_at(uint32_t addr) {
+    h4_t v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
+
+template <int NT>
+__global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
+    static_assert(NT == 32 || NT == 64, "A-fragment stage must be whole dword loads per wave");
+    constexpr int MT = 512, ROWS = 32, NBUF = 4;
+    constexpr int NB = NT / 16;
+    constexpr int PITCH = MT + 16;          // halves; 32-byte skew between rows
+    constexpr int WBYTES = NT * ROWS * 2;   // A fragments of one stage
+    constexpr int WDMA = WBYTES / (8 * 256);  // dword loads per wave per stage (NT / 32)
+    constexpr int XDMA = ROWS / 8;          // row loads per wave per stage
+    constexpr int D = XDMA + WDMA;          // loads per wave per stage
+    __shared__ __attribute__((aligned(16))) _Float16 xl[NBUF][ROWS][PITCH];
+    __shared__ __attribute__((aligned(16))) uint32_t wl[NBUF][WBYTES / 4];
+
+    uint32_t w = 0;
+    while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
+    const MfmaTileArgs a = grp.waves[w];
+    const uint32_t local = blockIdx.x - grp.start[w];
+    const uint32_t tile = local % a.tiles, rest = local / a.tiles;
+    const uint32_t ytile = rest % a.ttiles, zgroup = rest / a.ttiles;
+
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t tok0 = ytile * (uint32_t)MT;
+    // Segment starts are read-only for the kernel's lifetime: scalar loads.
+    const kconst_u64 *segr = (const kconst_u64 *)(a.seg) + (uint64_t)tile * a.K;
+    const uint32_t stages = a.K * a.S / (uint32_t)ROWS;
+    const uint32_t st_begin = zgroup * a.stage_chunk;
+    const uint32_t st_end = min(stages, st_begin + a.stage_chunk);
+    const uint32_t n_st = st_end - st_begin;
+    // A fragments of the tile: [k-step][16-neuron block][lane][8 halves]; one stage = one k-step.
+    const char *wtile = reinterpret_cast<const char *>(a.Wf) + (uint64_t)tile * a.ksteps * WBYTES;
+
+    auto issue = [&](uint32_t st, int buf) {
+        const uint32_t kk = st * (uint32_t)ROWS;
+        const uint32_t k = kk / a.S, s0 = kk - k * a.S;
+        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + tok0 + lane * 8;
+#pragma unroll
+        for (int r = 0; r < XDMA; ++r) {
+            const int row = wave + 8 * r;
+            __builtin_amdgcn_global_load_lds((kglobal_void *)(base + (uint64_t)row * a.step),
+                                             (__attribute__((address_space(3))) void *)&xl[buf][row][0],
+                                             16, 0, 0);
+        }
+        const char *ws = wtile + (uint64_t)st * WBYTES;
+#pragma unroll
+        for (int j = 0; j < WDMA; ++j) {
+            const int q = wave * WDMA + j;  // 256-byte piece of the stage's A fragments
+            __builtin_amdgcn_global_load_lds((kglobal_void *)(ws + q * 256 + lane * 4),
+                                             (__attribute__((address_space(3))) void *)&wl[buf][q * 64],
+                                             4, 0, 0);
+        }
+    };
+
+    f4_t acc[NB][4];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) acc[nb][tb] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int g = lane >> 4;
+    const int tr_row = 8 * g + ((lane & 15) >> 2);  // row read by this lane (first half)
+    const int tr_col = wave * 64 + 4 * (lane & 3);  // token column (+16 per token block)
+    // LDS reads of a stage are inline asm: the compiler would otherwise make every LDS read
+    // wait for all direct loads in flight (it cannot tell the ring slots apart), which would
+    // serialise the ring.  Their completion is awaited explicitly before the MFMAs.
+    const uint32_t xa = lds_addr(&xl[0][tr_row][tr_col]);
+    const uint32_t wa = lds_addr(&wl[0][lane * 4]);
+    constexpr uint32_t XBUF = ROWS * PITCH * 2, WBUF = WBYTES;
+    auto compute = [&](int buf) {
+        const uint32_t x0 = xa + (uint32_t)buf * XBUF, w0 = wa + (uint32_t)buf * WBUF;
+        h8_t af[NB];
+        h4_t lo[4], hi[4];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) af[nb] = ds_read_b128_at(w0 + nb * 1024u);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            lo[tb] = ds_read_tr16_at(x0 + 32u * tb);
+            hi[tb] = ds_read_tr16_at(x0 + 32u * tb + 8u * PITCH);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) asm volatile("" : "+v"(af[nb]));
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            asm volatile("" : "+v"(lo[tb]), "+v"(hi[tb]));
+            const h8_t b = __builtin_shufflevector(lo[tb], hi[tb], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[nb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[nb], b, acc[nb][tb], 0, 0, 0);
+        }
+    };
+
+    issue(st_begin, 0);
+    if (n_st > 1u) issue(st_begin + 1u, 1);
+    if (n_st > 2u) issue(st_begin + 2u, 2);
+    uint32_t i = 0;
+    for (; i + 3u < n_st; ++i) {
+        wait_vm_lgkm0<2 * D>();
+        wg_barrier_no_fence();
+        issue(st_begin + i + 3u, (int)((i + 3u) & 3u));
+        compute((int)(i & 3u));
+    }
+    // Drain: q = n_st - i <= 3 stages left, all issued.
+    if (i + 2u < n_st) {
+        wait_vm_lgkm0<2 * D>();
+        wg_barrier_no_fence();
+        compute((int)(i & 3u));
+        ++i;
+    }
+    if (i + 1u < n_st) {
+        wait_vm_lgkm0<D>();
+        wg_barrier_no_fence();
+        compute((int)(i & 3u));
+        ++i;
+    }
+    wait_vm_lgkm0<0>();
+    wg_barrier_no_fence();
+    compute((int)(i & 3u));
+
+    mfma_tile_epilogue<NT>(a, acc, tile, tok0, zgroup, lane, wave);
+}
+
+}  // namespace k44dev

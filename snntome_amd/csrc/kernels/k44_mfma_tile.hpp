@@ -78,6 +78,49 @@ struct MfmaGroup {
     uint32_t n;
 };
 
+// Epilogue of a 64-token-per-wave MFMA tile: lane holds C[4g + i][lane & 15] of every 16x16
+// accumulator tile.  Split-K stores the fp32 partial; otherwise bias, activation, residual /
+// cout_map and the fp16 (RNE) store.
+template <int NT>
+__device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a, const f4_t (&acc)[NT / 16][4],
+                                                   uint32_t tile, uint32_t tok0, uint32_t zgroup,
+                                                   int lane, int wave) {
+    constexpr int NB = NT / 16;
+    const int g = lane >> 4;
+    const uint32_t n_base = tile * (uint32_t)NT + 4u * (uint32_t)g;
+    const uint32_t t_base = tok0 + (uint32_t)wave * 64u + (uint32_t)(lane & 15);
+    if (a.part) {  // split-K: fp32 partial tile, epilogue in k44_splitk_epilogue_kernel
+        float *pz = a.part + (uint64_t)zgroup * a.cout * a.tokens;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t j = n_base + 16u * nb + (uint32_t)i;
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb)
+                    pz[(uint64_t)j * a.tokens + t_base + 16u * tb] = acc[nb][tb][i];
+            }
+        return;
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t j = n_base + 16u * nb + (uint32_t)i;
+            const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
+            const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
+            if (oj == K44_CMAP_EMPTY) continue;  // empty slot of a pattern-sorted tile
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const uint64_t o = oj * a.out_stride + t_base + 16u * tb;
+                const float r = a.R ? __half2float(a.R[o]) : 0.0f;
+                const float v = acc[nb][tb][i] + b;
+                const float y = a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r;
+                a.Y[o] = __float2half_rn(y);
+            }
+        }
+}
+
 template <int NT, int MT, int ROWS>
 __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
     uint32_t w = 0;
@@ -186,39 +229,7 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
         __syncthreads();
     }
 
-    // Epilogue: lane holds C[4g + i][lane & 15] of every 16x16 tile.
-    const uint32_t n_base = tile * (uint32_t)NT + 4u * (uint32_t)g;
-    const uint32_t t_base = tok0 + (uint32_t)wave * 64u + (uint32_t)(lane & 15);
-    if (a.part) {  // split-K: fp32 partial tile, epilogue in k44_splitk_epilogue_kernel
-        float *pz = a.part + (uint64_t)zgroup * a.cout * a.tokens;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t j = n_base + 16u * nb + (uint32_t)i;
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb)
-                    pz[(uint64_t)j * a.tokens + t_base + 16u * tb] = acc[nb][tb][i];
-            }
-        return;
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t j = n_base + 16u * nb + (uint32_t)i;
-            const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
-            const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-            if (oj == K44_CMAP_EMPTY) continue;  // empty slot of a pattern-sorted tile
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                const uint64_t o = oj * a.out_stride + t_base + 16u * tb;
-                const float r = a.R ? __half2float(a.R[o]) : 0.0f;
-                const float v = acc[nb][tb][i] + b;
-                const float y = a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r;
-                a.Y[o] = __float2half_rn(y);
-            }
-        }
+    mfma_tile_epilogue<NT>(a, acc, tile, tok0, zgroup, lane, wave);
 }
 
 }  // namespace k44dev

@@ -119,7 +119,10 @@ def test_llm_prefill_commandwise_and_end_to_end(wavec, monkeypatch, path):
     plan.init_gpu()
     paths = {w["path"] for w in plan.exec_report()["waves"]}
     _log(f"[llm prefill {path}] wave paths {sorted(paths)}")
-    assert paths == ({"mfma_tile"} if path == "auto" else {"valu_gather_dot"})
+    if path == "auto":
+        assert paths and paths <= {"mfma_tile", "mfma_dma"}
+    else:
+        assert paths == {"valu_gather_dot"}
     rng = np.random.default_rng(1)
     ids = rng.integers(0, TINY.vocab, TINY.requests * TINY.prompt).astype(np.uint32)
     _check_commands(plan, TINY, wts, ids, False, f"llm prefill {path}")
@@ -306,7 +309,7 @@ def test_mfma_split_k_matches_oracle_and_unsplit(wavec, orc, monkeypatch, tokens
         plan = g.compile()
         plan.init_gpu()
         rep = plan.exec_report()["waves"][0]
-        assert rep["path"] == "mfma_tile"
+        assert rep["path"] in ("mfma_tile", "mfma_dma")
         assert (rep["ksplit"] > 1) == (mode == "split"), rep
         plan.fill_input_uniform(3)
         plan.execute(1)

@@ -25,7 +25,7 @@ def test_config3_full_wave_sampled(wavec, orc):
     plan.init_gpu()
     rep = plan.exec_report()["waves"][0]
     _log(f"[c3] path={rep['path']} K={rep['K']} S={rep['S']} tile={rep['cluster']}")
-    assert rep["path"] == "mfma_tile" and (rep["K"], rep["S"]) == (16, 512)
+    assert rep["path"] == "mfma_dma" and (rep["K"], rep["S"]) == (16, 512)
     plan.fill_input_uniform(wl.seed)
     plan.execute(1)
     tiles = [0, 1, 77, 128, 200, 255]
@@ -71,7 +71,8 @@ def test_mfma_tile_shapes(wavec, orc, nt, tokens):
     y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens, rows=cluster_rows(starts, S),
                                    weights=w, bias=b, cluster=nt, act="gelu", seed=13)
     rep = plan.exec_report()["waves"][0]
-    assert rep["path"] == "mfma_tile"
+    dma = tokens % 512 == 0 and nt in (32, 64)
+    assert rep["path"] == ("mfma_dma" if dma else "mfma_tile")
     assert orc.rel_err(y, ref) <= TOL
 
 
@@ -163,3 +164,39 @@ def test_narrow_mfma_decode_sizes(wavec, orc, monkeypatch, tokens, nt):
             assert np.array_equal(again[:, :tokens].view(np.uint16), y.view(np.uint16))
         ys[mode] = y.astype(np.float64)
     assert orc.rel_err(ys["narrow"], ys["wide"]) <= TOL
+
+
+@pytest.mark.parametrize("nt,S,K,tiles,tokens,res", [
+    (64, 32, 1, 2, 512, False),    # one 32-position stage per tile
+    (64, 64, 1, 1, 512, True),     # two stages
+    (32, 96, 1, 1, 512, False),    # three stages (drain only)
+    (32, 160, 3, 2, 1024, True),   # 15 stages, two token tiles
+    (64, 512, 4, 5, 512, False),   # 64 stages
+])
+def test_dma_ring_matches_register_staged(wavec, orc, monkeypatch, nt, S, K, tiles, tokens, res):
+    """512-token workgroups take the LDS-ring kernel (direct loads, 4 stages, explicit waits).
+    Without split-K it accumulates in the same k-step order as the register-staged kernel, so
+    the outputs are bit-identical; with split-K (partial boundaries differ) both are within
+    tolerance of the oracle.  Stage counts 1..3 exercise the drain-only path."""
+    rng = np.random.default_rng(S * 7 + K)
+    C = 16384
+    starts = (rng.integers(0, (C - S) // 8, size=(tiles, K)) * 8).astype(np.uint32)
+    cout = tiles * nt
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    out = {}
+    for split in ("1", "0"):
+        monkeypatch.setenv("K44WAVEC_SPLITK", "" if split == "1" else "0")
+        for dma in ("1", "0"):
+            monkeypatch.setenv("K44WAVEC_DMA", dma)
+            y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
+                                           rows=cluster_rows(starts, S), weights=w, bias=b,
+                                           cluster=nt, act="gelu", residual=res, seed=21)
+            rep = plan.exec_report()["waves"][0]
+            assert rep["path"] == ("mfma_dma" if dma == "1" else "mfma_tile"), rep
+            err = orc.rel_err(y, ref)
+            _log(f"[dma nt={nt} S={S} K={K} tiles={tiles} tokens={tokens} split={split} "
+                 f"dma={dma}] ksplit {rep['ksplit']} rel err {err:.3e}")
+            assert err <= TOL
+            out[(split, dma)] = y
+    assert np.array_equal(out[("0", "1")], out[("0", "0")])

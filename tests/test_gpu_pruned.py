@@ -43,7 +43,7 @@ def test_pruned_wave_matches_per_neuron_oracle(wavec, orc, monkeypatch, path, n_
     if path == "valu":
         assert {r["path"] for r in rep} == {"valu_gather_dot"}
     elif tile >= 16 and S % 32 == 0:
-        assert {r["path"] for r in rep} == {"mfma_tile"}
+        assert {r["path"] for r in rep} <= {"mfma_tile", "mfma_dma"}
     plan.fill_input_uniform(5)
     plan.execute(1)
     st = stride_of(tokens)
