@@ -172,6 +172,38 @@ int wavec_gpu_copy_canvas(void *dst_handle, unsigned long long dst_elem_off, voi
 int wavec_gpu_copy_ids(void *dst_handle, int dst_first, void *src_handle, int src_first,
                        int src_step, int n);
 
+/* ---- stand-alone kernels on caller-owned device memory (asynchronous on `stream`, a hipStream_t
+ * or NULL for the null stream; pointers are device pointers) --------------------------------- */
+/* Device memory for callers of the stand-alone kernels that have no allocator of their own
+ * (the whitepaper benchmark allocates with hipMalloc directly).  No reference counterpart. */
+void *wavec_dev_malloc(unsigned long long bytes);
+int wavec_dev_free(void *p);
+int wavec_dev_upload(void *dst_dev, const void *src_host, unsigned long long bytes);
+int wavec_dev_download(void *dst_host, const void *src_dev, unsigned long long bytes);
+int wavec_dev_synchronize(void);
+/* Synthetic substrate rows pos0 .. pos0+rows-1 (the generator of wavec_gpu_fill_input_uniform) into
+ * dst [rows][stride] fp16; tokens >= valid are 0.  Synchronous. */
+int wavec_dev_fill_uniform(void *dst, unsigned long long rows, unsigned int stride,
+                           unsigned int valid, unsigned long long pos0, unsigned long long seed);
+/* Token64 wave, replaces launch_k44_f16_forward (whitepaper/sparse_wmma_kernel/kernels/
+ * kernel44_immutable.cuh:285-297, kernel :200-259): X [ceil(batch/64)][Cin][64] fp16,
+ * Y [ceil(batch/64)][Cout][64] fp16, cluster_indices [Cout/cluster_size][16*B_vec16] u32 input
+ * positions (neurons j share row j/cluster_size), cluster_weights_wmma [Cout/16][B_vec16][32]
+ * vectors of 8 fp16 (RDNA4 WMMA order, as written by convert_raw_to_wmma), neuron_bias [Cout] fp16
+ * (NULL = 0).  Y[t][j][m] = fp16_rtz(bias[j] + sum_k W[j][k] X[t][idx[j/cluster][k]][m]), fp32
+ * accumulation, every one of the 64 tokens of every tile.  cluster_size: a multiple of 16
+ * dividing Cout.  64-bit addressing for any Cin; an index >= Cin reads as a zero row. */
+int wavec_k44_f16_forward_token64(void *Y, const void *X, const uint32_t *cluster_indices,
+                                  const void *cluster_weights_wmma, const void *neuron_bias,
+                                  uint32_t batch_size, uint32_t Cin, uint32_t Cout,
+                                  uint32_t B_vec16, uint32_t cluster_size, void *stream);
+/* GPU weight interleave, replaces interleave_weights_cluster16_wmma_gpu_kernel
+ * (kernel44_immutable.cuh:261-267, kernels/rocm/kernel44_rocm_pack.cuh:285-290): row-major
+ * [num_output_neurons][8*B_vec8] fp16 (vectors of 8) -> WMMA vector order; neurons % 16 == 0,
+ * B_vec8 even. */
+int wavec_interleave_weights_wmma(void *dst_wmma, const void *src_compact,
+                                  uint32_t num_output_neurons, uint32_t B_vec8, void *stream);
+
 /* JSON: per wave the kernel path taken and why, its segment schedule (K, S, step) and
  * accounting (flops, distinct substrate rows).  "{}" before a successful init. */
 const char *wavec_gpu_exec_report_json(void *handle);

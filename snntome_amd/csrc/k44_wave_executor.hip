@@ -329,53 +329,15 @@ struct K44GpuExecutorState {
         // different rows are read close in time (cache reuse instead of a second HBM read).
         const char *sort_env = std::getenv("K44WAVEC_SORT");
         wx.sorted_segments = wx.K > 1u && !(sort_env && std::string(sort_env) == "0");
-        const bool band_order = sort_env && std::string(sort_env) == "band";
         if (wx.sorted_segments) {
             std::vector<uint32_t> order(wx.K);
             std::vector<uint64_t> st(wx.K);
             std::vector<uint16_t> row_w((size_t)c.B_raw);
-            uint64_t lo = ~0ull, hi = 0;
-            for (uint64_t s0 : starts) {
-                lo = std::min(lo, s0);
-                hi = std::max(hi, s0);
-            }
-            const double span = (double)(hi - lo) + 1.0;
-            std::vector<int> slot_of(wx.K);
-            std::vector<char> used(wx.K);
             for (size_t r = 0; r < rows; ++r) {
                 uint64_t *sr = starts.data() + r * wx.K;
                 for (uint32_t k = 0; k < wx.K; ++k) order[k] = k;
                 std::stable_sort(order.begin(), order.end(),
                                  [&](uint32_t x, uint32_t y) { return sr[x] < sr[y]; });
-                if (band_order) {
-                    // Slot = the segment's address band (K equal bands of the wave's range),
-                    // so concurrently running rows read the same band at the same time;
-                    // collisions go to the nearest free slot.
-                    std::fill(used.begin(), used.end(), 0);
-                    std::vector<uint32_t> left;
-                    for (uint32_t q = 0; q < wx.K; ++q) {
-                        const uint32_t k = order[q];
-                        int b = (int)((double)(sr[k] - lo) * wx.K / span);
-                        b = std::min<int>(b, (int)wx.K - 1);
-                        if (!used[b]) {
-                            used[b] = 1;
-                            slot_of[k] = b;
-                        } else {
-                            left.push_back(k);
-                        }
-                    }
-                    for (uint32_t k : left) {
-                        int b = std::min<int>((int)((double)(sr[k] - lo) * wx.K / span),
-                                              (int)wx.K - 1);
-                        for (int d = 1;; ++d) {
-                            if (b - d >= 0 && !used[b - d]) { b -= d; break; }
-                            if (b + d < (int)wx.K && !used[b + d]) { b += d; break; }
-                        }
-                        used[b] = 1;
-                        slot_of[k] = b;
-                    }
-                    for (uint32_t k = 0; k < wx.K; ++k) order[slot_of[k]] = k;
-                }
                 bool identity = true;
                 for (uint32_t k = 0; k < wx.K; ++k) identity = identity && order[k] == k;
                 if (identity) continue;
@@ -1306,6 +1268,7 @@ int guarded(const char *what, F &&f) {
     } catch (...) {
         set_error(std::string(what) + ": unknown error");
     }
+    (void)hipGetLastError();  // a failed runtime call must not resurface at the next launch
     return -1;
 }
 
@@ -1644,6 +1607,99 @@ int wavec_gpu_fill_input_uniform(void *h, unsigned long long seed) {
                                             L.channel_stride, ex->plan_meta.input_w, 0u,
                                             (uint64_t)seed, ex->stream));
         K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+void *wavec_dev_malloc(unsigned long long bytes) {
+    void *p = nullptr;
+    const int rc = guarded("wavec_dev_malloc", [&] {
+        K44_HIP(hipMalloc(&p, bytes ? bytes : 1u));
+        return 0;
+    });
+    return rc == 0 ? p : nullptr;
+}
+
+int wavec_dev_free(void *p) {
+    return guarded("wavec_dev_free", [&] {
+        if (p) K44_HIP(hipFree(p));
+        return 0;
+    });
+}
+
+int wavec_dev_upload(void *dst, const void *src, unsigned long long bytes) {
+    if (!dst || !src) return -1;
+    return guarded("wavec_dev_upload", [&] {
+        K44_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+        return 0;
+    });
+}
+
+int wavec_dev_download(void *dst, const void *src, unsigned long long bytes) {
+    if (!dst || !src) return -1;
+    return guarded("wavec_dev_download", [&] {
+        K44_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+        return 0;
+    });
+}
+
+int wavec_dev_synchronize(void) {
+    return guarded("wavec_dev_synchronize", [&] {
+        K44_HIP(hipDeviceSynchronize());
+        return 0;
+    });
+}
+
+int wavec_dev_fill_uniform(void *dst, unsigned long long rows, unsigned int stride,
+                           unsigned int valid, unsigned long long pos0, unsigned long long seed) {
+    if (!dst || stride == 0u || valid > stride) return -1;
+    return guarded("wavec_dev_fill_uniform", [&] {
+        K44_HIP(k44dev::launch_fill_uniform(static_cast<__half *>(dst), rows, stride, valid, pos0,
+                                            seed, nullptr));
+        K44_HIP(hipDeviceSynchronize());
+        return 0;
+    });
+}
+
+int wavec_k44_f16_forward_token64(void *Y, const void *X, const uint32_t *cluster_indices,
+                                  const void *cluster_weights_wmma, const void *neuron_bias,
+                                  uint32_t batch_size, uint32_t Cin, uint32_t Cout,
+                                  uint32_t B_vec16, uint32_t cluster_size, void *stream) {
+    return guarded("wavec_k44_f16_forward_token64", [&] {
+        if (!Y || !X || !cluster_indices || !cluster_weights_wmma)
+            throw std::runtime_error("Y, X, cluster_indices and cluster_weights_wmma are required");
+        if (batch_size == 0u || Cin == 0u || B_vec16 == 0u)
+            throw std::runtime_error("batch_size, Cin and B_vec16 must be positive");
+        if (cluster_size < 16u || cluster_size % 16u != 0u || Cout == 0u || Cout % cluster_size != 0u)
+            throw std::runtime_error("cluster_size must be a multiple of 16 that divides Cout");
+        const uint32_t tiles = (batch_size + 63u) / 64u;
+        if ((tiles + 3u) / 4u > 65535u) throw std::runtime_error("batch_size too large");
+        k44dev::Token64Args a{};
+        a.Y = static_cast<__half *>(Y);
+        a.X = static_cast<const __half *>(X);
+        a.idx = cluster_indices;
+        a.w_wmma = static_cast<const uint4 *>(cluster_weights_wmma);
+        a.bias = static_cast<const __half *>(neuron_bias);
+        a.Cin = Cin;
+        a.Cout = Cout;
+        a.B_vec16 = B_vec16;
+        a.cluster = cluster_size;
+        a.tiles = tiles;
+        K44_HIP(k44dev::launch_token64(a, static_cast<hipStream_t>(stream)));
+        return 0;
+    });
+}
+
+int wavec_interleave_weights_wmma(void *dst_wmma, const void *src_compact,
+                                  uint32_t num_output_neurons, uint32_t B_vec8, void *stream) {
+    return guarded("wavec_interleave_weights_wmma", [&] {
+        if (!dst_wmma || !src_compact) throw std::runtime_error("null device pointer");
+        if (num_output_neurons % 16u != 0u || B_vec8 == 0u || B_vec8 % 2u != 0u)
+            throw std::runtime_error("num_output_neurons must be a multiple of 16 and B_vec8 even");
+        K44_HIP(k44dev::launch_interleave_wmma(static_cast<uint4 *>(dst_wmma),
+                                               static_cast<const uint4 *>(src_compact),
+                                               num_output_neurons, B_vec8,
+                                               static_cast<hipStream_t>(stream)));
         return 0;
     });
 }

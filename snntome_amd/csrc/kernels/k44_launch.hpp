@@ -34,6 +34,22 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items, h
 // each wave with kgroups > 1 sums its fp32 partials in z order and runs the epilogue.
 hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_items, hipStream_t stream);
 
+// Stand-alone Token64 wave (X [tiles][Cin][64], Y [tiles][Cout][64], per-cluster index rows,
+// RDNA4-WMMA-ordered weights, bias, round toward zero); see k44_token64.hip.
+struct Token64Args {
+    __half *Y;
+    const __half *X;
+    const uint32_t *idx;   // [Cout / cluster][16 * B_vec16] input positions
+    const uint4 *w_wmma;   // [Cout / 16][B_vec16][32] vectors of 8 fp16
+    const __half *bias;    // [Cout] or nullptr (zero)
+    uint32_t Cin, Cout, B_vec16, cluster, tiles;
+};
+hipError_t launch_token64(const Token64Args &a, hipStream_t stream);
+
+// GPU weight interleave: row-major [neurons][8 * B_vec8] fp16 -> WMMA vector order.
+hipError_t launch_interleave_wmma(uint4 *dst, const uint4 *src, uint32_t neurons, uint32_t B_vec8,
+                                  hipStream_t stream);
+
 // Synthetic substrate fill (see k44_fill_uniform_kernel).
 hipError_t launch_fill_uniform(__half *dst, uint64_t rows, uint32_t stride, uint32_t valid,
                                uint64_t pos0, uint64_t seed, hipStream_t stream);

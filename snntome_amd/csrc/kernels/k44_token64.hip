@@ -1,0 +1,160 @@
+// k44_token64.hip — the stand-alone Token64 wave and the GPU form of the WMMA weight interleave.
+//
+// Token64 wave (semantics of the reference's whitepaper launcher, whitepaper/sparse_wmma_kernel/
+// kernels/kernel44_immutable.cuh:200-297): activations in 64-token tiles,
+//     X[tile][Cin][64], Y[tile][Cout][64] fp16,
+// clusters of `cluster` (a multiple of 16) consecutive neurons share one index row of
+// B = 16*B_vec16 input positions idx[c][k] (any positions, 64-bit addressing throughout), weights in
+// the RDNA4 WMMA vector order (k44_plan_types.hpp convert_raw_to_wmma), bias always added,
+//     Y[t][j][m] = fp16_round_toward_zero(bias[j] + sum_k W[j][k] * X[t][idx[j/cluster][k]][m]).
+//
+// MI355X mapping.  One wave = one 64-token tile x 16*NB neurons of one cluster (NB = 4, 2, 1:
+// the widest that divides the cluster); a workgroup holds 4 waves on 4 consecutive tiles (same
+// neurons, so the A fragments are shared through L1).  Per 32-deep k-step the wave gathers its
+// 32 index rows (128 bytes each, 8 lanes x 16 bytes per row) into a private LDS tile, and the B
+// operand of v_mfma_f32_16x16x32_f16 comes out with ds_read_b64_tr_b16 (8 positions of one
+// token per lane), exactly as in the dense-cluster tile kernel.  A fragments are read straight
+// from the WMMA-ordered weights: MFMA lane l needs row 16*nb + (l & 15), columns 32*ks + 8*(l>>4)
+// .. +8, which is WMMA vector ((nb * B_vec16 + 2*ks + (l >> 5)) * 32 + (l & 31)).  The next
+// k-step's rows and fragments are loaded while the current one is multiplied; the index words
+// are loaded two k-steps ahead.  An odd B_vec16 leaves the last k-step half empty: those rows
+// and fragments are zero.  An index word >= Cin reads as a zero row (the reference would read
+// outside X).
+#include "k44_launch.hpp"
+
+namespace k44dev {
+
+template <int NB>
+__global__ __launch_bounds__(256) void k44_token64_kernel(Token64Args a) {
+    constexpr int PITCH = 72;  // halves per LDS row: 64 tokens + 16-byte skew
+    __shared__ __attribute__((aligned(16))) _Float16 xs[4][32][PITCH];
+    const int lane = (int)(threadIdx.x & 63u), wave = (int)(threadIdx.x >> 6);
+    const uint32_t tile = blockIdx.y * 4u + (uint32_t)wave;
+    if (tile >= a.tiles) return;  // no workgroup barrier in this kernel
+    const uint32_t j0 = blockIdx.x * 16u * NB;
+    const uint32_t B = a.B_vec16 * 16u;
+    const uint32_t ksteps = (a.B_vec16 + 1u) / 2u;
+    const uint32_t *irow = a.idx + (uint64_t)(j0 / a.cluster) * B;
+    const __half *xt = a.X + (uint64_t)tile * a.Cin * 64u;
+    const int gr = lane >> 3, gc = (lane & 7) * 8;  // gather: row gr (+8i), tokens gc..gc+7
+    const uint4 *wrow = a.w_wmma + (uint64_t)(j0 / 16u) * a.B_vec16 * 32u + (lane & 31);
+    const int g = lane >> 4;
+
+    f4_t acc[NB][4];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        f4_t b0 = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (a.bias) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b0[i] = __half2float(a.bias[j0 + 16u * nb + 4u * g + i]);
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) acc[nb][tb] = b0;
+    }
+
+    auto load_idx = [&](uint32_t ks, uint32_t (&ix)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t k = 32u * ks + 8u * i + (uint32_t)gr;
+            const uint32_t v = k < B ? irow[k] : 0xffffffffu;
+            ix[i] = v < a.Cin ? v : 0xffffffffu;  // out-of-range positions read as zero rows
+        }
+    };
+    auto load_x = [&](const uint32_t (&ix)[4], u4_t (&x)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            x[i] = ix[i] != 0xffffffffu
+                       ? *reinterpret_cast<const u4_t *>(xt + (uint64_t)ix[i] * 64u + gc)
+                       : u4_t{0u, 0u, 0u, 0u};
+    };
+    auto load_a = [&](uint32_t ks, h8_t (&af)[NB]) {
+        const uint32_t kb = 2u * ks + (uint32_t)(lane >> 5);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            af[nb] = kb < a.B_vec16
+                         ? __builtin_bit_cast(h8_t, wrow[((uint64_t)nb * a.B_vec16 + kb) * 32u])
+                         : h8_t{};
+    };
+
+    uint32_t ia[4], ib[4];
+    u4_t xr[4];
+    h8_t ar[NB];
+    load_idx(0u, ia);
+    load_idx(min(1u, ksteps - 1u), ib);
+    load_x(ia, xr);
+    load_a(0u, ar);
+    const int tr_row = 8 * g + ((lane & 15) >> 2), tr_col = 4 * (lane & 3);
+    for (uint32_t ks = 0; ks < ksteps; ++ks) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u4_t *>(&xs[wave][8 * i + gr][gc]) = xr[i];
+        h8_t af[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) af[nb] = ar[nb];
+        // Next k-step in flight (clamped at the end: a re-read of the last step, unused).
+        const uint32_t kn = min(ks + 1u, ksteps - 1u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ia[i] = ib[i];
+        load_idx(min(ks + 2u, ksteps - 1u), ib);
+        load_x(ia, xr);
+        load_a(kn, ar);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const _Float16 *p = &xs[wave][tr_row][tr_col + 16 * tb];
+            const h4_t lo = lds_read_tr16(p);
+            const h4_t hi = lds_read_tr16(p + 4 * PITCH);
+            const h8_t b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[nb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[nb], b, acc[nb][tb], 0, 0, 0);
+        }
+    }
+
+    // C layout: lane holds C[4g + i][lane & 15] of every 16x16 tile; round toward zero.
+    __half *yt = a.Y + ((uint64_t)tile * a.Cout + j0) * 64u + (lane & 15);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb)
+                yt[(uint64_t)(16 * nb + 4 * g + i) * 64u + 16u * tb] = __float2half_rz(acc[nb][tb][i]);
+}
+
+hipError_t launch_token64(const Token64Args &a, hipStream_t stream) {
+    const uint32_t c16 = a.cluster / 16u;
+    const int nb = c16 % 4u == 0u ? 4 : (c16 % 2u == 0u ? 2 : 1);
+    const dim3 grid(a.Cout / (16u * (uint32_t)nb), (a.tiles + 3u) / 4u, 1u), block(256u, 1u, 1u);
+    if (nb == 4)
+        hipLaunchKernelGGL(k44_token64_kernel<4>, grid, block, 0, stream, a);
+    else if (nb == 2)
+        hipLaunchKernelGGL(k44_token64_kernel<2>, grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL(k44_token64_kernel<1>, grid, block, 0, stream, a);
+    return hipGetLastError();
+}
+
+// dst[g] = src[((tile / B_vec16) * 16 + (l & 15)) * B_vec8 + 2 * (tile % B_vec16) + (l >> 4)],
+// tile = g / 32, l = g % 32: the WMMA vector order of a row-major [n][8*B_vec8] fp16 matrix
+// (k44_plan_types.hpp:363-394; GPU form kernel44_immutable.cuh:261-267).  Grid-stride, 64-bit.
+__global__ __launch_bounds__(256) void k44_interleave_wmma_kernel(uint4 *dst, const uint4 *src,
+                                                                  uint64_t n_vec, uint32_t B_vec8) {
+    const uint64_t B_vec16 = B_vec8 / 2u;
+    for (uint64_t gi = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; gi < n_vec;
+         gi += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t t = gi >> 5, l = gi & 31u;
+        dst[gi] = src[((t / B_vec16) * 16u + (l & 15u)) * B_vec8 + 2u * (t % B_vec16) + (l >> 4)];
+    }
+}
+
+hipError_t launch_interleave_wmma(uint4 *dst, const uint4 *src, uint32_t neurons, uint32_t B_vec8,
+                                  hipStream_t stream) {
+    const uint64_t n_vec = (uint64_t)(neurons / 16u) * (B_vec8 / 2u) * 32u;
+    if (n_vec == 0u) return hipSuccess;
+    const uint64_t blocks = std::min<uint64_t>((n_vec + 255u) / 256u, 65536u);
+    hipLaunchKernelGGL(k44_interleave_wmma_kernel, dim3((uint32_t)blocks), dim3(256u), 0, stream,
+                       dst, src, n_vec, B_vec8);
+    return hipGetLastError();
+}
+
+}  // namespace k44dev

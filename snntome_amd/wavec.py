@@ -29,6 +29,7 @@ _pu16 = _c.POINTER(_c.c_uint16)
 _pu32 = _c.POINTER(_c.c_uint32)
 _pcp = _c.POINTER(_c.c_char_p)
 _ull = _c.c_ulonglong
+_u32 = _c.c_uint32
 
 # name -> (restype, argtypes)
 _SIGNATURES = {
@@ -84,6 +85,14 @@ _SIGNATURES = {
     "wavec_gpu_copy_canvas": (_i, [_vp, _ull, _vp, _ull, _ull]),
     "wavec_gpu_copy_ids": (_i, [_vp, _i, _vp, _i, _i, _i]),
     "wavec_gpu_exec_report_json": (_cp, [_vp]),
+    "wavec_dev_malloc": (_vp, [_ull]),
+    "wavec_dev_free": (_i, [_vp]),
+    "wavec_dev_upload": (_i, [_vp, _vp, _ull]),
+    "wavec_dev_download": (_i, [_vp, _vp, _ull]),
+    "wavec_dev_synchronize": (_i, []),
+    "wavec_dev_fill_uniform": (_i, [_vp, _ull, _u32, _u32, _ull, _ull]),
+    "wavec_k44_f16_forward_token64": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
+    "wavec_interleave_weights_wmma": (_i, [_vp, _vp, _u32, _u32, _vp]),
 }
 
 REFERENCE_SYMBOLS = tuple(list(_SIGNATURES)[:30])
@@ -512,3 +521,84 @@ class WaveGraph:
         _check(self._lib.wavec_save_tcff_ex(self._handle, str(path).encode(),
                                             model_prefix.encode(), 1,
                                             1 if include_geometry else 0), "wavec_save_tcff_ex")
+
+
+class DeviceBuffer:
+    """Device memory owned through libk44wavec.so (hipMalloc / hipFree), for the stand-alone
+    kernels; `.ptr` is the device address."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self._lib = get_lib()
+        self.ptr = self._lib.wavec_dev_malloc(self.nbytes)
+        if not self.ptr:
+            raise RuntimeError(f"wavec_dev_malloc({self.nbytes}) failed: {last_error()}")
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(a.nbytes)
+        buf.upload(a)
+        return buf
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError("array larger than the device buffer")
+        _check(self._lib.wavec_dev_upload(self.ptr, a.ctypes.data, a.nbytes), "wavec_dev_upload")
+
+    def download(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        if out.nbytes > self.nbytes:
+            raise ValueError("requested more bytes than the device buffer holds")
+        _check(self._lib.wavec_dev_download(out.ctypes.data, self.ptr, out.nbytes),
+               "wavec_dev_download")
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            self._lib.wavec_dev_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def device_synchronize() -> None:
+    _check(get_lib().wavec_dev_synchronize(), "wavec_dev_synchronize")
+
+
+def _dev_ptr(x) -> int:
+    """Device address of a DeviceBuffer (.ptr), an object with data_ptr(), or an integer."""
+    if x is None:
+        return 0
+    if isinstance(x, DeviceBuffer):
+        return int(x.ptr)
+    return int(x.data_ptr()) if hasattr(x, "data_ptr") else int(x)
+
+
+def forward_token64_f16(Y, X, cluster_indices, cluster_weights_wmma, neuron_bias,
+                        batch_size: int, Cin: int, Cout: int, B_vec16: int, cluster_size: int,
+                        stream=None) -> None:
+    """Stand-alone Token64 wave on caller-owned device memory (the whitepaper launcher
+    launch_k44_f16_forward): X [ceil(batch/64)][Cin][64] fp16 -> Y [ceil(batch/64)][Cout][64]
+    fp16, round toward zero.  Arguments are device tensors (anything with data_ptr()) or raw
+    device addresses; `stream` a hipStream_t address or None.  Asynchronous."""
+    lib = get_lib()
+    _check(lib.wavec_k44_f16_forward_token64(
+        _dev_ptr(Y), _dev_ptr(X), _dev_ptr(cluster_indices), _dev_ptr(cluster_weights_wmma),
+        _dev_ptr(neuron_bias) or None, int(batch_size), int(Cin), int(Cout), int(B_vec16),
+        int(cluster_size), _dev_ptr(stream) or None), "wavec_k44_f16_forward_token64")
+
+
+def interleave_weights_wmma(dst_wmma, src_compact, num_output_neurons: int, B_vec8: int,
+                            stream=None) -> None:
+    """GPU weight interleave: row-major [neurons][8*B_vec8] fp16 -> RDNA4 WMMA vector order."""
+    lib = get_lib()
+    _check(lib.wavec_interleave_weights_wmma(_dev_ptr(dst_wmma), _dev_ptr(src_compact),
+                                             int(num_output_neurons), int(B_vec8),
+                                             _dev_ptr(stream) or None),
+           "wavec_interleave_weights_wmma")

@@ -102,3 +102,18 @@ def test_unsupported_plans_fail_init_with_message(wavec):
     plan2 = g2.compile()
     with pytest.raises(RuntimeError, match="ROPE_GQA_ATTN_1D"):
         plan2.init_gpu()
+
+
+def test_token64_and_interleave_validate_before_touching_the_gpu(wavec):
+    """Argument checks of the stand-alone kernels run on the host (no device work on failure)."""
+    lib = wavec.get_lib()
+    assert lib.wavec_k44_f16_forward_token64(None, None, None, None, None, 64, 10, 64, 2, 64,
+                                             None) == -1
+    assert "required" in wavec.last_error()
+    # cluster size 8 (not a multiple of 16) is refused
+    assert lib.wavec_k44_f16_forward_token64(1, 1, 1, 1, None, 64, 10, 64, 2, 8, None) == -1
+    assert "cluster_size" in wavec.last_error()
+    assert lib.wavec_k44_f16_forward_token64(1, 1, 1, 1, None, 0, 10, 64, 2, 64, None) == -1
+    assert lib.wavec_interleave_weights_wmma(1, 1, 20, 4, None) == -1  # 20 neurons
+    assert lib.wavec_interleave_weights_wmma(1, 1, 32, 3, None) == -1  # odd B_vec8
+    assert lib.wavec_interleave_weights_wmma(None, 1, 32, 4, None) == -1

@@ -1,0 +1,110 @@
+"""GPU parity of the stand-alone Token64 wave (wavec_k44_f16_forward_token64, the whitepaper
+launcher's semantics: X [tile][Cin][64], per-cluster index rows, WMMA-ordered weights, bias,
+round toward zero) and of the GPU weight interleave, through the C ABI on device memory
+allocated with wavec_dev_malloc."""
+import numpy as np
+import pytest
+
+from snntome_amd import synth
+
+from wave_cases import TOL
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("neurons,B", [(16, 16), (64, 96), (48, 512)])
+def test_interleave_matches_host_order(wavec, orc, neurons, B):
+    rng = np.random.default_rng(neurons + B)
+    w = rng.integers(0, 1 << 16, size=(neurons, B), dtype=np.uint16)
+    src = wavec.DeviceBuffer.from_array(w)
+    dst = wavec.DeviceBuffer(w.nbytes)
+    wavec.interleave_weights_wmma(dst, src, neurons, B // 8)
+    wavec.device_synchronize()
+    got = dst.download(np.uint16, w.size)
+    assert np.array_equal(got, orc.raw_to_wmma(w).ravel())
+
+
+def _token64_case(wavec, orc, *, Cin, Cout, cluster, B_vec16, batch, seed, bad_index=False):
+    rng = np.random.default_rng(seed)
+    B = 16 * B_vec16
+    tiles = (batch + 63) // 64
+    x = (rng.uniform(-1, 1, size=(tiles, Cin, 64))).astype(np.float16)
+    idx = rng.integers(0, Cin, size=(Cout // cluster, B), dtype=np.int64).astype(np.uint32)
+    if bad_index:
+        idx[0, 3] = Cin + 5  # out of range: reads as a zero row
+    w = (rng.standard_normal((Cout, B)) * 0.05).astype(np.float16)
+    b = (rng.standard_normal(Cout) * 0.05).astype(np.float16)
+    Xd = wavec.DeviceBuffer.from_array(x)
+    Yd = wavec.DeviceBuffer.from_array(np.full((tiles, Cout, 64), 0xFFFF, np.uint16))
+    Id = wavec.DeviceBuffer.from_array(idx)
+    Wd = wavec.DeviceBuffer.from_array(orc.raw_to_wmma(w.view(np.uint16)))
+    Bd = wavec.DeviceBuffer.from_array(b)
+    wavec.forward_token64_f16(Yd, Xd, Id, Wd, Bd, batch, Cin, Cout, B_vec16, cluster)
+    wavec.device_synchronize()
+    y = Yd.download(np.float16, (tiles, Cout, 64)).astype(np.float64)
+    w_eff = w.copy()
+    idx_eff = idx.astype(np.uint64)
+    if bad_index:
+        w_eff[:cluster, 3] = 0  # a zero row contributes nothing
+        idx_eff[0, 3] = 0
+    errs = []
+    for t in range(tiles):
+        canvas = x[t].reshape(-1)
+        seg = (idx_eff * 64).ravel()
+        ref = orc.wave_f64(canvas, seg, w_eff, b, None, B, 1, cluster, 64, 64, 64, "none")
+        errs.append(orc.rel_err(y[t], ref))
+        # round toward zero: never larger in magnitude than the exact sum beyond fp32 noise
+        assert np.all(np.abs(y[t]) <= np.abs(ref) * (1 + 2 ** -12) + 1e-5)
+    return max(errs)
+
+
+@pytest.mark.parametrize("cluster", [16, 32, 48, 64, 128])
+@pytest.mark.parametrize("B_vec16,batch", [(4, 64), (3, 100), (8, 300)])
+def test_token64_matches_oracle(wavec, orc, cluster, B_vec16, batch):
+    """Cluster sizes 16..128 (16/32/64-neuron waves), even and odd B_vec16 (a half-empty last
+    k-step), ragged batches (2 and 5 tiles: workgroups with idle waves)."""
+    err = _token64_case(wavec, orc, Cin=3000, Cout=cluster * max(2, 128 // cluster), cluster=cluster,
+                        B_vec16=B_vec16, batch=batch, seed=cluster * 100 + B_vec16)
+    _log(f"[token64 cluster={cluster} B_vec16={B_vec16} batch={batch}] rel err {err:.3e}")
+    assert err <= TOL
+
+
+def test_token64_out_of_range_index_reads_zero(wavec, orc):
+    err = _token64_case(wavec, orc, Cin=500, Cout=64, cluster=64, B_vec16=2, batch=64, seed=7,
+                        bad_index=True)
+    assert err <= TOL
+
+
+def test_token64_64bit_substrate(wavec, orc):
+    """Cin = 40,000,000 positions (5.12 GB per 64-token tile, beyond 32-bit byte offsets),
+    filled on the device with the synthetic generator; indices spread over the whole range,
+    the last position included."""
+    Cin, Cout, cluster, B_vec16, seed = 40_000_000, 64, 64, 4, 17
+    B = 16 * B_vec16
+    rng = np.random.default_rng(11)
+    idx = rng.integers(0, Cin, size=(1, B), dtype=np.int64)
+    idx[0, :8] = [Cin - 1, (1 << 25) + 1, 1 << 25, 0, 33_554_431, 39_999_000, 12, Cin - 2]
+    idx = idx.astype(np.uint32)
+    _log("[token64 64-bit] filling a 5.12 GB substrate on the device")
+    X = wavec.DeviceBuffer(Cin * 64 * 2)
+    assert wavec.get_lib().wavec_dev_fill_uniform(X.ptr, Cin, 64, 64, 0, seed) == 0
+    w = (rng.standard_normal((Cout, B)) * 0.05).astype(np.float16)
+    b = (rng.standard_normal(Cout) * 0.05).astype(np.float16)
+    Y = wavec.DeviceBuffer(Cout * 64 * 2)
+    Id = wavec.DeviceBuffer.from_array(idx)
+    Wd = wavec.DeviceBuffer.from_array(orc.raw_to_wmma(w.view(np.uint16)))
+    Bd = wavec.DeviceBuffer.from_array(b)
+    wavec.forward_token64_f16(Y, X, Id, Wd, Bd, 64, Cin, Cout, B_vec16, cluster)
+    wavec.device_synchronize()
+    X.free()
+    rows = synth.substrate_rows(seed, idx[0], 64)  # host copy of the rows the wave reads
+    canvas = rows.view(np.uint16).reshape(-1)
+    seg = np.arange(B, dtype=np.uint64) * 64
+    ref = orc.wave_f64(canvas, seg, w, b, None, B, 1, cluster, 64, 64, 64, "none")
+    err = orc.rel_err(Y.download(np.float16, (Cout, 64)).astype(np.float64), ref)
+    _log(f"[token64 64-bit] rel err {err:.3e}")
+    assert err <= TOL
