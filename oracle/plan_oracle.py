@@ -2,9 +2,14 @@
 TEST INFRASTRUCTURE ONLY (used by tests/ to check libk44wavec.so's plans and .tcff bytes).
 
 Scope: 1-D token graphs — Input, linear (1x1 Convolution), the build's sparse waves,
-Concat / Split / Slice views, RMSNorm / SwiGLU nodes (they take canvas space) — i.e. every
-graph a 1-D wave plan is built from.  Restated from the reference's documented behaviour:
-  res descriptors        wavec/k44_plan_types.hpp:491-516 (1-D mode)
+Concat / Split / Slice views, RMSNorm / SwiGLU nodes (they take canvas space) — and 2-D image
+graphs of up to 63 frames — kxk Convolution (stride 1 and the stride-2 polyphase form with its
+S2D scratch), max-pooling, 2x upsampling, 2x2 transposed convolution (quadrant wave + scratch),
+views.  Restated from the reference's documented behaviour:
+  res descriptors        wavec/k44_plan_types.hpp:491-516 (1-D mode), :517-569 (2-D modes)
+  tap offsets            wavec/k44_plan_types.hpp:593-600
+  2-D shapes, layouts    wavec/k44_wave_compiler.hpp:137-210, 315-366
+  conv / deconv waves    wavec/k44_wave_compiler.hpp:609-807
   cluster size           wavec/k44_plan_types.hpp:157-186, 328-343
   WMMA weight order      wavec/k44_plan_types.hpp:363-375
   passes 1, 3, 4, 5      wavec/k44_wave_compiler.hpp:78-223, 315-366, 388-593, 824-988
@@ -18,6 +23,8 @@ import math
 import struct
 
 import numpy as np
+
+from .cnn_oracle import Layout2D
 
 ACT_NAMES = ["NONE", "RELU", "SIGMOID", "SILU", "LEAKY_RELU", "GELU"]
 
@@ -61,6 +68,26 @@ def res_key_1d(w):
     return 0x80000000 | w
 
 
+def res_key(h, w, is_1d):
+    """Layout key of a tensor shape (k44_wave_compiler.hpp:26-29)."""
+    if is_1d:
+        return res_key_1d(w)
+    return h if h == w else (((h << 14) ^ w) & 0xFFFFFFFF)
+
+
+def tiles_per_frame_2d(L) -> int:
+    """64-element tiles of one frame of a 2-D layout (k44_plan_types.hpp:517-569)."""
+    if L.aligned:
+        return L.H * (L.W // 64)
+    return (L.H * L.W_pad + 63) // 64
+
+
+def tap_2d(L, base, dy, dx):
+    """Gather index of tap (dy, dx) of the channel based at `base` (k44_plan_types.hpp:593-600,
+    non-token64 2-D mode: h_tile_off_X is anchored one row and one column before the tile)."""
+    return base + (1 + dy) * L.W_pad + (1 + dx)
+
+
 class Layout1D:
     def __init__(self, w):
         self.W = w
@@ -101,6 +128,9 @@ class Node:
         self.cluster = kw.get("cluster", 1)
         self.seg_len = kw.get("seg_len", 0)
         self.slice_sizes = kw.get("slice_sizes", [])
+        self.kh = kw.get("kh", 1)
+        self.kw = kw.get("kw", 1)
+        self.stride = kw.get("stride", 1)
 
 
 class Graph:
@@ -138,6 +168,22 @@ class Graph:
         self._add(Node("PrunedWave", name, [i], [o], cout=w_bits.shape[0], weights=w_bits,
                        bias=b_bits, rows=np.asarray(starts), cluster=tile, act=act,
                        residual=residual, seg_len=S))
+
+    def conv2d(self, name, i, o, cin, cout, kh, kw, stride, w_bits, b_bits, act=0, residual=""):
+        """w_bits: [cout][cin*kh*kw] fp16 bits (synapse ch*kh*kw + ky*kw + kx)."""
+        self._add(Node("Convolution", name, [i], [o], cin=cin, cout=cout, weights=w_bits,
+                       bias=b_bits, act=act, residual=residual, kh=kh, kw=kw, stride=stride))
+
+    def maxpool(self, name, i, o, k, stride):
+        self._add(Node("Pooling", name, [i], [o], kh=k, kw=k, stride=stride))
+
+    def upsample2x(self, name, i, o):
+        self._add(Node("Interp", name, [i], [o]))
+
+    def upconv2x2(self, name, i, o, cin, cout, w_bits, b_bits):
+        """w_bits: [cout][cin][4] fp16 bits (quadrant 2*ky + kx)."""
+        self._add(Node("Deconvolution", name, [i], [o], cin=cin, cout=cout, weights=w_bits,
+                       bias=b_bits, kh=2, kw=2, stride=2))
 
     def concat(self, name, ins, o):
         self._add(Node("Concat", name, ins, [o]))
@@ -203,53 +249,82 @@ def pruned_parts(starts: np.ndarray, S: int, w: np.ndarray, bias: np.ndarray, ti
 
 def compile_plan(g: Graph) -> dict:
     nodes = g.nodes
-    if nodes and nodes[0].op == "Input" and nodes[0].is_1d and g.batch > 1 and nodes[0].w_out == 1:
+    graph_1d = bool(nodes) and nodes[0].op == "Input" and nodes[0].is_1d
+    if graph_1d and g.batch > 1 and nodes[0].w_out == 1:
         nodes[0].w_in = nodes[0].w_out = g.batch
-    shapes = {}
-    for n in nodes:  # pass 1 (1-D subset)
+    shapes = {}  # tensor -> (c, h, w, is_1d)
+    for n in nodes:  # pass 1
         if n.op == "Input":
-            assert n.is_1d
-            shapes[n.outs[0]] = (n.cout, n.h_out, n.w_out)
+            shapes[n.outs[0]] = (n.cout, n.h_out, n.w_out, n.is_1d)
             plan_in = (n.cout, n.h_out, n.w_out)
         elif n.op in ("Convolution", "SparseWave", "PrunedWave"):
-            c, h, w = shapes[n.ins[0]]
+            c, h, w, d = shapes[n.ins[0]]
             if n.op in ("SparseWave", "PrunedWave"):
+                assert d, "sparse waves take 1-D token inputs"
                 n.cin = c
-            n.h_in, n.w_in, n.h_out, n.w_out = h, w, 1, w
-            shapes[n.outs[0]] = (n.cout, 1, w)
+            elif not d and n.kh == 1 and n.kw == 1 and n.cin == c * h * w and n.cin != c:
+                raise NotImplementedError("implicit flatten of a 2-D tensor")
+            n.is_1d = d
+            n.h_in, n.w_in = h, w
+            n.h_out, n.w_out = (1, w) if d else (h // n.stride, w // n.stride)
+            shapes[n.outs[0]] = (n.cout, n.h_out, n.w_out, d)
+        elif n.op == "Deconvolution":
+            c, h, w, d = shapes[n.ins[0]]
+            n.h_in, n.w_in, n.h_out, n.w_out = h, w, 2 * h, 2 * w
+            shapes[n.outs[0]] = (n.cout, n.h_out, n.w_out, False)
+        elif n.op in ("Pooling", "Interp"):
+            c, h, w, d = shapes[n.ins[0]]
+            n.cin = n.cout = c
+            n.h_in, n.w_in = h, w
+            n.h_out, n.w_out = (h // n.stride, w // n.stride) if n.op == "Pooling" else (2 * h, 2 * w)
+            shapes[n.outs[0]] = (c, n.h_out, n.w_out, False)
         elif n.op == "Concat":
-            c0, h, w = shapes[n.ins[0]]
-            shapes[n.outs[0]] = (sum(shapes[t][0] for t in n.ins), h, w)
+            c0, h, w, d = shapes[n.ins[0]]
+            n.is_1d = d
+            shapes[n.outs[0]] = (sum(shapes[t][0] for t in n.ins), h, w, d)
         elif n.op == "Split":
             for o in n.outs:
                 shapes[o] = shapes[n.ins[0]]
         elif n.op == "Slice":
-            c, h, w = shapes[n.ins[0]]
+            c, h, w, d = shapes[n.ins[0]]
             for k, o in enumerate(n.outs):
                 cc = n.slice_sizes[k] if n.slice_sizes else c // len(n.outs)
-                shapes[o] = (cc, h, w)
+                shapes[o] = (cc, h, w, d)
         elif n.op in ("RMSNorm", "SwiGLU"):
-            c, h, w = shapes[n.ins[0]]
+            c, h, w, d = shapes[n.ins[0]]
+            n.is_1d = d
             n.h_in = n.h_out = h
             n.w_in = n.w_out = w
             if n.op == "SwiGLU":
                 n.cin = n.cout = c
-            shapes[n.outs[0]] = (c, h, w)
-    # pass 3: one layout per token width; wave configs
+            shapes[n.outs[0]] = (c, h, w, d)
+    # pass 3: one layout per shape key (frames per wave: 1 for token graphs, else <= 8); configs
+    if not graph_1d:
+        assert g.batch < 64, "the 64-frame interleaved image layout is not restated"
+    frames = 1 if graph_1d else min(max(1, g.batch), 8)
     res = {}
     for t in sorted(shapes):
-        c, h, w = shapes[t]
-        res.setdefault(res_key_1d(w), Layout1D(w))
+        c, h, w, d = shapes[t]
+        if res_key(h, w, d) not in res:
+            res[res_key(h, w, d)] = Layout1D(w) if d else Layout2D(h, w, frames)
     cfg = {}
     for i, n in enumerate(nodes):
         if n.op == "Convolution":
             cp = round_up_16(n.cout)
-            tiles = max(1, res[res_key_1d(n.w_out)].num_tiles)
+            if n.is_1d:
+                tiles = max(1, res[res_key_1d(n.w_out)].num_tiles)
+            else:
+                tiles = max(1, n.h_out * n.w_out)
             cfg[i] = (choose_cluster_size(cp, tiles, g.force), cp)
         elif n.op == "SparseWave":
             lcm = 16 * n.cluster // math.gcd(16, n.cluster)
             cfg[i] = (n.cluster, (n.cout + lcm - 1) // lcm * lcm)
-    # pass 4: allocation ids, liveness, best-fit placement
+
+    def out_key(n):
+        d = n.is_1d if n.op not in ("Deconvolution", "Pooling", "Interp") else False
+        return res_key(n.h_out, n.w_out, d)
+
+    # pass 4: allocation ids, liveness, best-fit placement, then the S2D / quadrant scratch
     ids, allocs, out_aid = {}, {}, {}
     nxt = 0
     for i, n in enumerate(nodes):
@@ -260,7 +335,7 @@ def compile_plan(g: Graph) -> dict:
             ids[n.outs[0]] = set().union(*[ids[t] for t in n.ins])
         else:
             ch = cfg[i][1] if n.op in ("Convolution", "SparseWave") else n.cout
-            allocs[nxt] = [res_key_1d(n.w_out), ch, 0]
+            allocs[nxt] = [out_key(n), ch, 0]
             ids[n.outs[0]] = {nxt}
             out_aid[i] = nxt
             nxt += 1
@@ -271,6 +346,14 @@ def compile_plan(g: Graph) -> dict:
         for t in n.ins + ([n.residual] if n.residual else []):
             for a in ids.get(t, ()):
                 last[a] = max(last.get(a, 0), i)
+    s2d_ch, quad_ch = {}, {}
+    for n in nodes:
+        if n.op == "Convolution" and n.stride == 2 and not n.is_1d:
+            k = res_key(n.h_out, n.w_out, False)
+            s2d_ch[k] = max(s2d_ch.get(k, 0), 4 * n.cin)
+        elif n.op == "Deconvolution":
+            k = res_key(n.h_in, n.w_in, False)
+            quad_ch[k] = max(quad_ch.get(k, 0), 4 * round_up_16(n.cout))
     free, peak, placed, live = [], 0, {}, []
     for i, n in enumerate(nodes):
         if i in out_aid:
@@ -307,10 +390,23 @@ def compile_plan(g: Graph) -> dict:
                 else:
                     merged.append(f)
             free = merged
-    canvas = (peak + 63) // 64 * 64
-    canvas = (canvas + 127) // 128 * 128 or 128
+    cur = (peak + 63) // 64 * 64
+    s2d_base = {k: cur for k in s2d_ch}
+    cur += (max([s2d_ch[k] * res[k].channel_stride for k in s2d_ch], default=0) + 63) // 64 * 64
+    quad_base = {k: cur for k in quad_ch}
+    cur += (max([quad_ch[k] * res[k].channel_stride for k in quad_ch], default=0) + 63) // 64 * 64
+    canvas = (cur + 127) // 128 * 128 or 128
     plan = {"canvas_elems": canvas, "input_off": allocs[0][2], "cmds": [], "res": res,
             "total_w_bytes": 0, "total_idx_bytes": 0, "input": plan_in}
+
+    def geom_1d(c, Lo):
+        toks = max(1, c["w_out"])
+        return [2 if toks > 1 else 1, toks, c["logical_Cout"], 1, 1, 1, Lo.channel_stride, 1, 1, 0]
+
+    def geom_2d(c, Lo):
+        return [3, 1, c["logical_Cout"], c["h_out"], c["w_out"], c["Cout"] * Lo.channel_stride,
+                Lo.channel_stride, Lo.W_pad, 1, Lo.W_pad + 4]
+
     # pass 5
     chan = {}
     for i, n in enumerate(nodes):
@@ -328,10 +424,91 @@ def compile_plan(g: Graph) -> dict:
                 at += ln
         elif n.op == "Concat":
             chan[n.outs[0]] = [x for t in n.ins for x in chan[t]]
-        elif n.op in ("RMSNorm", "SwiGLU"):
+        elif n.op in ("RMSNorm", "SwiGLU", "Pooling", "Interp"):
             key, ch, at = allocs[out_aid[i]]
             chan[n.outs[0]] = [at + c * res[key].channel_stride for c in range(n.cout)]
-            plan["cmds"].append({"type": 7 if n.op == "RMSNorm" else 8, "name": n.name})
+            plan["cmds"].append({"type": {"RMSNorm": 7, "SwiGLU": 8, "Pooling": 3,
+                                          "Interp": 4}[n.op], "name": n.name})
+        elif n.op == "Deconvolution":
+            key, ch, dst = allocs[out_aid[i]]
+            chan[n.outs[0]] = [dst + c * res[key].channel_stride for c in range(n.cout)]
+            kin = res_key(n.h_in, n.w_in, False)
+            Li = res[kin]
+            in_chs = chan[n.ins[0]]
+            cal = round_up_16(n.cout)
+            cq = 4 * cal
+            cl = choose_cluster_size(cq, tiles_per_frame_2d(Li), g.force)
+            B = round_up_32(n.cin)
+            idx = np.zeros((cq // cl, B), dtype=np.uint64)
+            idx[:, :n.cin] = np.asarray([tap_2d(Li, in_chs[c], 0, 0) for c in range(n.cin)],
+                                        dtype=np.uint64)[None, :]
+            w = np.zeros((cq, B), dtype=np.uint16)
+            bias = np.zeros(cq, dtype=np.uint16)
+            wq = np.asarray(n.weights).reshape(n.cout, n.cin, 4)
+            for q in range(4):
+                w[q * cal:q * cal + n.cout, :n.cin] = wq[:, :, q]
+                bias[q * cal:q * cal + n.cout] = n.bias[:n.cout]
+            cmd = {"type": 0, "name": n.name, "Cin": n.cin, "Cout": cq, "logical_Cout": 4 * n.cout,
+                   "cluster": cl, "B": B, "B_raw": n.cin, "act": 0, "has_res": False,
+                   "h_out": n.h_in, "w_out": n.w_in, "src_off": 0, "y_off": quad_base[kin],
+                   "res_off": 0, "x_base_off": 0, "idx_mode": 0, "idx_stride": 1,
+                   "seg_len": 0, "idx": idx.astype(np.uint32), "w_rows": w, "bias": bias,
+                   "out_stride": Li.channel_stride}
+            cmd["geom"] = geom_2d(cmd, Li)
+            plan["total_w_bytes"] += cq * B * 2
+            plan["total_idx_bytes"] += idx.size * 4 + cq * 2
+            plan["cmds"].append(cmd)
+            plan["cmds"].append({"type": 6, "name": n.name + "_scatter2x2"})
+        elif n.op == "Convolution" and not n.is_1d:
+            key, ch, dst = allocs[out_aid[i]]
+            Lo = res[key]
+            chan[n.outs[0]] = [dst + c * Lo.channel_stride for c in range(n.cout)]
+            in_chs = chan[n.ins[0]]
+            S_cl, cout_pad = cfg[i]
+            has_res = bool(n.residual)
+            res_off = chan[n.residual][0] if has_res else 0
+            if has_res:
+                end = res_off + cout_pad * Lo.channel_stride
+                if end > plan["canvas_elems"]:
+                    plan["canvas_elems"] = (end + 127) // 128 * 128
+            taps = n.kh * n.kw
+            b_raw = taps * n.cin
+            B = round_up_32(b_raw)
+            poly = n.stride == 2
+            if poly:
+                s2d = s2d_base[key]
+                plan["cmds"].append({"type": 5, "name": n.name + "_s2d_2x2"})
+            row = np.zeros(b_raw, dtype=np.uint64)
+            for c in range(n.cin):
+                for ky in range(n.kh):
+                    for kx in range(n.kw):
+                        if poly:  # stride 2 = stride-1 taps over polyphase channel 4c+2py+px
+                            dy, py = (-1, 1) if ky == 0 else (0, 0 if ky == 1 else 1)
+                            dx, px = (-1, 1) if kx == 0 else (0, 0 if kx == 1 else 1)
+                            base = s2d + (4 * c + 2 * py + px) * Lo.channel_stride
+                            v = tap_2d(Lo, base, dy, dx)
+                        else:
+                            v = tap_2d(Lo, in_chs[c], ky - n.kh // 2, kx - n.kw // 2)
+                        row[c * taps + ky * n.kw + kx] = v
+            idx = np.zeros((cout_pad // S_cl, B), dtype=np.uint64)
+            idx[:, :b_raw] = row[None, :]
+            log_c = min(cout_pad, n.cout)
+            w = np.zeros((cout_pad, B), dtype=np.uint16)
+            w[:log_c, :b_raw] = n.weights[:log_c]
+            bias = np.zeros(cout_pad, dtype=np.uint16)
+            bias[:log_c] = n.bias[:log_c]
+            cmd = {"type": 0, "name": n.name, "Cin": n.cin, "Cout": cout_pad,
+                   "logical_Cout": log_c, "cluster": S_cl, "B": B, "B_raw": b_raw,
+                   "act": n.act, "has_res": has_res, "h_out": n.h_out, "w_out": n.w_out,
+                   "src_off": s2d if poly else in_chs[0], "y_off": dst, "res_off": res_off,
+                   "x_base_off": 0, "idx_mode": 0, "idx_stride": 1, "seg_len": 0,
+                   "idx": idx.astype(np.uint32), "w_rows": w, "bias": bias,
+                   "out_stride": Lo.channel_stride}
+            assert int(idx.max()) < 0x70000000
+            cmd["geom"] = geom_2d(cmd, Lo)
+            plan["total_w_bytes"] += cout_pad * B * 2
+            plan["total_idx_bytes"] += idx.size * 4 + cout_pad * 2
+            plan["cmds"].append(cmd)
         elif n.op == "PrunedWave":
             key, ch, dst = allocs[out_aid[i]]
             Lo = res[key]
@@ -433,7 +610,7 @@ def compile_plan(g: Graph) -> dict:
                 "idx": idx.astype(np.uint32), "w_rows": w, "bias": bias,
                 "out_stride": Lo.channel_stride,
             })
-    out_c, out_h, out_w = shapes[g.output]
+    out_c, out_h, out_w, _ = shapes[g.output]
     plan["output"] = (out_c, out_h, out_w)
     plan["output_off"] = chan[g.output][0]
     return plan
@@ -506,9 +683,12 @@ def tcff_bytes(plan: dict, prefix="K44Model", include_geometry=True) -> bytes:
                 (297, 3, 2, wi | (len(waves) << 16)), (339, 3, 1, 3), (0x8440, 4, 1, 0x45564157),
                 (0x8441, 4, 10, par_at), (0x8442, 4, 11, aux_at), (0x8443, 4, 2, h_at)]
         if include_geometry:
-            toks = max(1, c["w_out"])
-            g_at = stash(u32s(2 if toks > 1 else 1, toks, c["logical_Cout"], 1, 1, 1,
-                              c["out_stride"], 1, 1, 0))
+            if "geom" in c:
+                g_at = stash(u32s(*c["geom"]))
+            else:
+                toks = max(1, c["w_out"])
+                g_at = stash(u32s(2 if toks > 1 else 1, toks, c["logical_Cout"], 1, 1, 1,
+                                  c["out_stride"], 1, 1, 0))
             tags.append((0x8444, 4, 10, g_at))
         if ext:
             v = [c["idx_mode"], lo(c["idx_stride"]), c["idx_stride"] >> 32, lo(c["x_base_off"]),

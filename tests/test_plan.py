@@ -404,3 +404,157 @@ def test_2d_layout_matches_restatement(wavec, tmp_path, H, W, batch):
     assert geo[:5] == (3, 1, 8, H, W)
     assert geo[6] == lay.channel_stride and geo[7] == lay.W_pad and geo[9] == lay.W_pad + 4
     assert geo[5] == plan.cmds[0]["Cout"] * lay.channel_stride
+
+
+# ---- 2-D image plans: the padded-plane layouts, tap offsets, stride-2 polyphase (S2D) waves,
+# ---- pooling / upsampling / transposed-convolution scratch, checked the same way.
+
+def _conv(g, pg, name, i, o, cin, cout, k, rng, stride=1, act="silu", res=None):
+    w = (rng.standard_normal((cout, cin, k, k)) * 0.1).astype(np.float32)
+    b = (rng.standard_normal(cout) * 0.1).astype(np.float32)
+    g.add_conv2d(name, i, o, cin, cout, k, k, w, b, stride=stride, pad=k // 2, act=act,
+                 res_blob=res)
+    pg.conv2d(name, i, o, cin, cout, k, k, stride, _f16(w).reshape(cout, cin * k * k), _f16(b),
+              act=po.ACT_NAMES.index(act.upper()) if act else 0, residual=res or "")
+
+
+def _upconv(g, pg, name, i, o, cin, cout, rng):
+    w = (rng.standard_normal((cout, cin, 2, 2)) * 0.1).astype(np.float32)
+    b = (rng.standard_normal(cout) * 0.1).astype(np.float32)
+    g.add_upconv2x2(name, i, o, cin, cout, w, b)
+    pg.upconv2x2(name, i, o, cin, cout, _f16(w).reshape(cout, cin, 4), _f16(b))
+
+
+def _pair2d(wavec, build, batch):
+    g = wavec.WaveGraph(kv_cache_max_seq=0, batch_size=batch)
+    pg = po.Graph(batch_size=batch)
+    build(g, pg)
+    return g, g.compile(), po.compile_plan(pg)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_2d_yolo_like_plan(wavec, tmp_path, batch):
+    """Aligned width (W % 64 == 0): 3x3 stride 1 and 2 (S2D scratch), 5x5 max-pool, 1x1 with a
+    residual, upsample, concat, 2x2 max-pool; 1 and 3 frames per wave."""
+    rng = np.random.default_rng(batch)
+
+    def build(g, pg):
+        g.add_input("img", 3, 64, 64)
+        pg.input("img", 3, 64, 64, False)
+        _conv(g, pg, "c1", "img", "a", 3, 16, 3, rng)
+        _conv(g, pg, "c2", "a", "b", 16, 32, 3, rng, stride=2)
+        for G in (g, pg):
+            (G.add_maxpool if G is g else G.maxpool)("sppf", "b", "p", 5, 1, *([2] if G is g else []))
+        _conv(g, pg, "c3", "p", "r", 32, 32, 1, rng, act="relu", res="b")
+        g.add_upsample2x("up", "r", "u")
+        pg.upsample2x("up", "r", "u")
+        g.add_concat("cat", ["u", "a"], "m")
+        pg.concat("cat", ["u", "a"], "m")
+        _conv(g, pg, "c4", "m", "q", 48, 24, 3, rng, act="gelu")
+        g.add_maxpool("mp", "q", "out", 2, 2, 0)
+        pg.maxpool("mp", "q", "out", 2, 2)
+        g.set_output("out")
+        pg.output = "out"
+
+    g, plan, pplan = _pair2d(wavec, build, batch)
+    _assert_same_plan(plan, pplan)
+    _assert_same_tcff(plan, pplan, tmp_path)
+
+
+def test_2d_unet_like_masked_plan(wavec, tmp_path):
+    """Masked width (W % 64 != 0): pooling down, 2x2 transposed convolution up (quadrant wave
+    into its scratch), skip concatenation, split / slice views of a 2-D tensor."""
+    rng = np.random.default_rng(7)
+
+    def build(g, pg):
+        g.add_input("img", 4, 20, 20)
+        pg.input("img", 4, 20, 20, False)
+        _conv(g, pg, "e1", "img", "s", 4, 16, 3, rng, act="relu")
+        g.add_maxpool("down", "s", "d", 2, 2, 0)
+        pg.maxpool("down", "s", "d", 2, 2)
+        _conv(g, pg, "e2", "d", "e", 16, 32, 3, rng, act="relu")
+        _upconv(g, pg, "up", "e", "u", 32, 16, rng)
+        g.add_concat("cat", ["u", "s"], "m")
+        pg.concat("cat", ["u", "s"], "m")
+        g.add_slice("sl", "m", ["m0", "m1"], [8, 24])
+        pg.slice("sl", "m", ["m0", "m1"], [8, 24])
+        _conv(g, pg, "d1", "m1", "h", 24, 12, 3, rng, act="silu")
+        _conv(g, pg, "head", "h", "out", 12, 5, 1, rng, act=None)
+        g.set_output("out")
+        pg.output = "out"
+
+    g, plan, pplan = _pair2d(wavec, build, 2)
+    _assert_same_plan(plan, pplan)
+    _assert_same_tcff(plan, pplan, tmp_path)
+
+
+def test_2d_rectangular_and_stride2_masked(wavec, tmp_path):
+    """H != W layout keys ((h << 14) ^ w) and a stride-2 convolution on a masked width."""
+    rng = np.random.default_rng(9)
+
+    def build(g, pg):
+        g.add_input("img", 6, 16, 128)
+        pg.input("img", 6, 16, 128, False)
+        _conv(g, pg, "a", "img", "x", 6, 20, 3, rng, stride=2)   # 8 x 64 (aligned)
+        _conv(g, pg, "b", "x", "y", 20, 40, 3, rng, stride=2)    # 4 x 32 (masked)
+        _conv(g, pg, "c", "y", "out", 40, 64, 1, rng, act="leaky_relu")
+        g.set_output("out")
+        pg.output = "out"
+
+    g, plan, pplan = _pair2d(wavec, build, 1)
+    _assert_same_plan(plan, pplan)
+    _assert_same_tcff(plan, pplan, tmp_path)
+
+
+def test_2d_tap_offsets_by_hand():
+    """One 3x3 tap row of the oracle against hand-computed offsets (aligned 64-wide layout):
+    W_pad = 72, channel c of a tensor at base B starts at B + c * 66 * 72; tap (dy, dx) adds
+    (1 + dy) * 72 + (1 + dx)."""
+    pg = po.Graph()
+    pg.input("img", 2, 64, 64, False)
+    w = np.zeros((16, 2 * 9), np.uint16)
+    pg.conv2d("c", "img", "out", 2, 16, 3, 3, 1, w, np.zeros(16, np.uint16))
+    pg.output = "out"
+    p = po.compile_plan(pg)
+    wave = [c for c in p["cmds"] if c["type"] == 0][0]
+    cs = 66 * 72
+    base = p["input_off"]
+    want = [base + c * cs + (1 + dy) * 72 + (1 + dx) for c in range(2) for dy in (-1, 0, 1)
+            for dx in (-1, 0, 1)]
+    assert list(wave["idx"][0, :18]) == want
+    assert wave["geom"] == [3, 1, 16, 64, 64, 16 * cs, cs, 72, 1, 76]
+
+
+@pytest.mark.parametrize("mistake", ["dy_sign", "kernel_transposed", "quad_order"])
+def test_2d_planted_mistakes_are_caught(wavec, tmp_path, monkeypatch, mistake):
+    """The 2-D comparison is sensitive: a flipped tap sign, a transposed 3x3 kernel on the
+    stride-2 polyphase path or a wrong transposed-convolution quadrant order in the oracle each
+    change the .tcff bytes."""
+    rng = np.random.default_rng(3)
+    if mistake == "dy_sign":
+        monkeypatch.setattr(po, "tap_2d", lambda L, b, dy, dx: b + (1 - dy) * L.W_pad + (1 + dx))
+
+    def build(g, pg):
+        g.add_input("img", 4, 20, 20)
+        pg.input("img", 4, 20, 20, False)
+        if mistake == "quad_order":
+            w = (rng.standard_normal((8, 4, 2, 2)) * 0.1).astype(np.float32)
+            b = np.zeros(8, np.float32)
+            g.add_upconv2x2("up", "img", "out", 4, 8, w, b)
+            wq = _f16(w).reshape(8, 4, 4)[:, :, ::-1].copy()  # planted: quadrants reversed
+            pg.upconv2x2("up", "img", "out", 4, 8, wq, _f16(b))
+        else:
+            w = (rng.standard_normal((16, 4, 3, 3)) * 0.1).astype(np.float32)
+            b = np.zeros(16, np.float32)
+            g.add_conv2d("c", "img", "out", 4, 16, 3, 3, w, b, stride=2, pad=1, act="relu")
+            wr = _f16(w).reshape(16, 4, 3, 3)
+            if mistake == "kernel_transposed":  # planted: ky <-> kx
+                wr = wr.transpose(0, 1, 3, 2).copy()
+            pg.conv2d("c", "img", "out", 4, 16, 3, 3, 2, wr.reshape(16, 36), _f16(b), act=1)
+        g.set_output("out")
+        pg.output = "out"
+
+    g, plan, pplan = _pair2d(wavec, build, 1)
+    path = tmp_path / "p.tcff"
+    plan.save_tcff(path, "K44Model")
+    assert path.read_bytes() != po.tcff_bytes(pplan, "K44Model")
