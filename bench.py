@@ -244,6 +244,67 @@ def bench_llm(args):
     print(json.dumps(out), flush=True)
 
 
+def bench_token64(args):
+    """The whitepaper's stand-alone Token64 wave (wavec_k44_f16_forward_token64) at its own
+    benchmark shape (whitepaper/sparse_wmma_kernel/tests/benchmark_whitepaper_k44.cpp:141-197):
+    Cin = 10,000,000 positions, M = 512 tokens (8 tiles of 64), B = 1024 synapses per cluster row,
+    Cout = 8192, cluster size S (--cluster).  Index rows uniform over the substrate; weights and
+    index rows rotate through a pool of >= 1 GiB (as the reference's ring benchmark does) so that
+    every launch streams them from HBM.  TSyn/s = Cout * B * M / t; TFLOP/s = 2 * TSyn/s."""
+    from snntome_amd import wavec
+
+    lib = wavec.get_lib()
+    Cin, M, B, Cout, S = args.t64_cin, 512, 1024, 8192, args.cluster
+    tiles = M // 64
+    rng = np.random.default_rng(44)
+    log(f"[bench] token64: Cin={Cin:,} M={M} B={B} Cout={Cout} S={S}; filling "
+        f"{tiles * Cin * 128 / 1e9:.2f} GB substrate")
+    X = wavec.DeviceBuffer(tiles * Cin * 64 * 2)
+    if lib.wavec_dev_fill_uniform(X.ptr, tiles * Cin, 64, 64, 0, 7) != 0:
+        raise RuntimeError(wavec.last_error())
+    w_bytes = Cout * B * 2
+    idx_bytes = (Cout // S) * B * 4
+    n_sets = max(4, -(-(1 << 30) // (w_bytes + idx_bytes)))
+    W = wavec.DeviceBuffer(n_sets * w_bytes)
+    I = wavec.DeviceBuffer(n_sets * idx_bytes)
+    w0 = wavec.DeviceBuffer.from_array(
+        (rng.standard_normal((Cout, B), dtype=np.float32) * 0.02).astype(np.float16))
+    for k in range(n_sets):  # distinct index rows per set, same weights (bytes are what matter)
+        idx = rng.integers(0, Cin, size=(Cout // S, B), dtype=np.int64).astype(np.uint32)
+        lib.wavec_dev_upload(I.ptr + k * idx_bytes, idx.ctypes.data, idx_bytes)
+        wavec.interleave_weights_wmma(W.ptr + k * w_bytes, w0, Cout, B // 8)  # WMMA order
+    wavec.device_synchronize()
+    bias = wavec.DeviceBuffer.from_array(np.zeros(Cout, np.float16))
+    Y = wavec.DeviceBuffer(tiles * Cout * 64 * 2)
+
+    def launch(k):
+        wavec.forward_token64_f16(Y, X, I.ptr + (k % n_sets) * idx_bytes,
+                                  W.ptr + (k % n_sets) * w_bytes, bias, M, Cin, Cout, B // 16, S)
+
+    for k in range(args.warmup):
+        launch(k)
+    wavec.device_synchronize()
+    ms = __import__("ctypes").c_float()
+    lib.wavec_dev_time_begin()
+    for k in range(args.steps):
+        launch(args.warmup + k)
+    lib.wavec_dev_time_end(__import__("ctypes").byref(ms))
+    t = ms.value * 1e-3 / args.steps
+    tsyn = Cout * B * M / t / 1e12
+    log(f"[bench] token64 S={S}: {t * 1e6:.1f} us/launch, {tsyn:.2f} TSyn/s, {2 * tsyn:.1f} TFLOP/s")
+    out = {
+        "metric": "effective TFLOP/s (2*nnz*batch) + achieved HBM GB/s per wave, 1xMI355X",
+        "value": round(2 * tsyn, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(t * 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16 (fp32 accumulate)",
+        "data": "synthetic (device-generated substrate, uniform index rows, N(0,0.02) weights)",
+        "config": {"workload": "whitepaper_token64", "Cin": Cin, "M": M, "B": B, "Cout": Cout,
+                   "cluster": S, "pool_sets": n_sets},
+        "tsyn_per_s": round(tsyn, 3),
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,6 +314,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="config 5: launch kernel by kernel instead of replaying HIP graphs")
+    ap.add_argument("--token64", action="store_true",
+                    help="the whitepaper's stand-alone Token64 wave at its benchmark shape")
+    ap.add_argument("--cluster", type=int, default=128, help="--token64: cluster size S")
+    ap.add_argument("--t64-cin", type=int, default=10_000_000, help="--token64: Cin")
     ap.add_argument("--copy-probe-gib", type=float, default=0.0,
                     help="only run a plain device copy of this many GiB (PMC calibration)")
     args = ap.parse_args()
@@ -265,6 +330,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.token64:
+        bench_token64(args)
+        return
     if args.config == 5:
         bench_llm(args)
         return

@@ -185,6 +185,10 @@ int wavec_dev_synchronize(void);
  * dst [rows][stride] fp16; tokens >= valid are 0.  Synchronous. */
 int wavec_dev_fill_uniform(void *dst, unsigned long long rows, unsigned int stride,
                            unsigned int valid, unsigned long long pos0, unsigned long long seed);
+/* HIP events on the null stream around stand-alone launches: begin, then end returns the
+ * elapsed milliseconds (waits for the end event). */
+int wavec_dev_time_begin(void);
+int wavec_dev_time_end(float *ms);
 /* Token64 wave, replaces launch_k44_f16_forward (whitepaper/sparse_wmma_kernel/kernels/
  * kernel44_immutable.cuh:285-297, kernel :200-259): X [ceil(batch/64)][Cin][64] fp16,
  * Y [ceil(batch/64)][Cout][64] fp16, cluster_indices [Cout/cluster_size][16*B_vec16] u32 input

@@ -1661,6 +1661,30 @@ int wavec_dev_fill_uniform(void *dst, unsigned long long rows, unsigned int stri
     });
 }
 
+namespace {
+hipEvent_t g_t0 = nullptr, g_t1 = nullptr;  // null-stream timer of the stand-alone kernels
+}
+
+int wavec_dev_time_begin(void) {
+    return guarded("wavec_dev_time_begin", [&] {
+        if (!g_t0) K44_HIP(hipEventCreate(&g_t0));
+        if (!g_t1) K44_HIP(hipEventCreate(&g_t1));
+        K44_HIP(hipEventRecord(g_t0, nullptr));
+        return 0;
+    });
+}
+
+int wavec_dev_time_end(float *ms) {
+    if (!ms) return -1;
+    return guarded("wavec_dev_time_end", [&] {
+        if (!g_t0 || !g_t1) throw std::runtime_error("wavec_dev_time_begin was not called");
+        K44_HIP(hipEventRecord(g_t1, nullptr));
+        K44_HIP(hipEventSynchronize(g_t1));
+        K44_HIP(hipEventElapsedTime(ms, g_t0, g_t1));
+        return 0;
+    });
+}
+
 int wavec_k44_f16_forward_token64(void *Y, const void *X, const uint32_t *cluster_indices,
                                   const void *cluster_weights_wmma, const void *neuron_bias,
                                   uint32_t batch_size, uint32_t Cin, uint32_t Cout,

@@ -26,9 +26,6 @@
 
 namespace k44dev {
 
-typedef const __attribute__((address_space(1))) void kglobal_void;
-typedef const __attribute__((address_space(4))) uint64_t kconst_u64;
-
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at bits 15:14,
 // expcnt[6:4] left at its maximum, lgkmcnt[11:8] = 0).
 template <int N>

@@ -42,30 +42,54 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
     const uint32_t ks_end = min(a.ksteps, ks_begin + a.stage_chunk);
     const uint32_t r0 = ks_begin * 32u, nrows = (ks_end - ks_begin) * 32u;
 
-    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint64_t *segr = a.seg + (uint64_t)tile * a.K;
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
+    // Segment starts are read-only: scalar loads through the constant address space (they wait
+    // on the scalar counter only, not on the A-fragment loads already in flight).
+    const kconst_u64 *segr = (const kconst_u64 *)(a.seg) + (uint64_t)tile * a.K;
     const int blk0 = wave % BL, kw = wave / BL;
     const h8_t *wf = reinterpret_cast<const h8_t *>(a.Wf) + (uint64_t)tile * a.ksteps * NB * 64 +
                      lane;
 
     // The first AB k-steps' A fragments are requested before the X gather, so both are in
-    // flight together (a chunk is a handful of k-steps: the workgroup is latency-bound).
+    // flight together (a chunk is a handful of k-steps: the workgroup is latency-bound).  Loads
+    // past the chunk re-read its last k-step (unused): a fixed load count per wave lets every
+    // later wait be partial.
     h8_t af[AB][BPW];
 #pragma unroll
     for (int u = 0; u < AB; ++u) {
-        const uint32_t k2 = ks_begin + (uint32_t)kw + (uint32_t)u * KW;
-        if (k2 < ks_end) {
+        const uint32_t k2 = min(ks_begin + (uint32_t)kw + (uint32_t)u * KW, ks_end - 1u);
 #pragma unroll
-            for (int i = 0; i < BPW; ++i) af[u][i] = wf[((uint64_t)k2 * NB + blk0 + BL * i) * 64];
-        }
+        for (int i = 0; i < BPW; ++i)
+            af[u][i] = *(const __attribute__((address_space(1))) h8_t *)(
+                wf + ((uint64_t)k2 * NB + blk0 + BL * i) * 64);
     }
 
-    // X rows [r0, r0 + nrows) of the tile's index row, 16 tokens each, into LDS.
-    for (uint32_t q = (uint32_t)tid; q < nrows * 2u; q += 256u) {
-        const uint32_t r = r0 + (q >> 1), k = r / a.S, s = r - k * a.S;
-        const u4_t v = *reinterpret_cast<const u4_t *>(a.X + segr[k] + (uint64_t)s * a.step +
-                                                        (q & 1u) * 8u);
-        *reinterpret_cast<u4_t *>(&xl[q >> 1][(q & 1u) * 8u]) = v;
+    // X rows [r0, r0 + nrows) of the tile's index row, 16 tokens each, into LDS.  Pass q of a
+    // wave covers 32 consecutive rows starting at a multiple of 32, i.e. inside one segment
+    // (S % 32 == 0): its segment start is wave-uniform.  All loads are issued before the first
+    // LDS store.
+    constexpr int XQ = NARROW_MAX_ROWS * 2 / 256;  // 16-byte chunks per thread at most
+    u4_t xv[XQ];
+    // first row of each pass; passes past the chunk re-read its last 32 rows (unused), so the
+    // load count is fixed and the stores below wait only once.  The scalar segment-start loads
+    // of all passes are issued together, then all X loads.
+    uint64_t sb[XQ];
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) {
+        const uint32_t r = r0 + min((uint32_t)(32 * (wave + 4 * q)), nrows - 32u);
+        const uint32_t k = r / a.S;
+        sb[q] = segr[k] + (uint64_t)(r - k * a.S) * a.step;
+    }
+#pragma unroll
+    for (int q = 0; q < XQ; ++q)
+        xv[q] = *(const __attribute__((address_space(1))) u4_t *)(
+            a.X + sb[q] + (uint64_t)(lane >> 1) * a.step + (uint32_t)(lane & 1) * 8u);
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) {
+        const uint32_t rb = (uint32_t)(32 * (wave + 4 * q));
+        if (rb < nrows)
+            *reinterpret_cast<u4_t *>(&xl[rb + (uint32_t)(lane >> 1)][(lane & 1) * 8]) = xv[q];
     }
     __syncthreads();
 
@@ -80,12 +104,11 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
         if (ks != ks_begin + (uint32_t)kw) {  // later batches (chunks longer than AB k-steps)
 #pragma unroll
             for (int u = 0; u < AB; ++u) {
-                const uint32_t k2 = ks + (uint32_t)u * KW;
-                if (k2 < ks_end) {
+                const uint32_t k2 = min(ks + (uint32_t)u * KW, ks_end - 1u);
 #pragma unroll
-                    for (int i = 0; i < BPW; ++i)
-                        af[u][i] = wf[((uint64_t)k2 * NB + blk0 + BL * i) * 64];
-                }
+                for (int i = 0; i < BPW; ++i)
+                    af[u][i] = *(const __attribute__((address_space(1))) h8_t *)(
+                        wf + ((uint64_t)k2 * NB + blk0 + BL * i) * 64);
             }
         }
 #pragma unroll

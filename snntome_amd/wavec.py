@@ -91,6 +91,8 @@ _SIGNATURES = {
     "wavec_dev_download": (_i, [_vp, _vp, _ull]),
     "wavec_dev_synchronize": (_i, []),
     "wavec_dev_fill_uniform": (_i, [_vp, _ull, _u32, _u32, _ull, _ull]),
+    "wavec_dev_time_begin": (_i, []),
+    "wavec_dev_time_end": (_i, [_pf]),
     "wavec_k44_f16_forward_token64": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
     "wavec_interleave_weights_wmma": (_i, [_vp, _vp, _u32, _u32, _vp]),
 }
