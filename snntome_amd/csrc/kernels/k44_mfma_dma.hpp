@@ -40,6 +40,45 @@ __device__ __forceinline__ void wg_barrier_no_fence() {
     asm volatile("" ::: "memory");
 }
 
+// Drain of an LDS ring: R stages left, all issued; each waits for its own loads with the
+// younger ones still in flight.
+template <int R, int NBUF, int D, typename Comp>
+__device__ __forceinline__ void lds_ring_drain(uint32_t left, uint32_t &i, Comp &comp) {
+    if constexpr (R >= 1) {
+        if (left == (uint32_t)R) {
+            wait_vm_lgkm0<(R - 1) * D>();
+            wg_barrier_no_fence();
+            comp((int)(i % NBUF));
+            ++i;
+            --left;
+        }
+        lds_ring_drain<R - 1, NBUF, D>(left, i, comp);
+    }
+}
+
+// Schedule of an LDS ring of NBUF stages with NBUF-1 in flight, D direct loads per wave per
+// stage: load(stage, slot) issues a stage's direct loads into ring slot `slot`, comp(slot)
+// multiplies a landed stage.  Stage i is multiplied after (a) this wave's loads of stage i have
+// landed — the loads of the NBUF-2 younger stages may still be in flight: vmcnt((NBUF-2)·D) —
+// and (b) a barrier, after which every wave's loads of stage i have landed and no wave still
+// reads slot (i-1) % NBUF, which stage i+NBUF-1 then refills.  The last NBUF-1 stages drain
+// with decreasing vmcnt.  n_st >= 1.
+template <int NBUF, int D, typename Load, typename Comp>
+__device__ __forceinline__ void lds_ring(uint32_t n_st, Load &&load, Comp &&comp) {
+    constexpr int AHEAD = NBUF - 1;
+#pragma unroll
+    for (int p = 0; p < AHEAD; ++p)
+        if ((uint32_t)p < n_st) load((uint32_t)p, p);
+    uint32_t i = 0;
+    for (; i + AHEAD < n_st; ++i) {
+        wait_vm_lgkm0<(AHEAD - 1) * D>();
+        wg_barrier_no_fence();
+        load(i + AHEAD, (int)((i + AHEAD) % NBUF));
+        comp((int)(i % NBUF));
+    }
+    lds_ring_drain<AHEAD, NBUF, D>(n_st - i, i, comp);
+}
+
 // Byte address of a shared-memory location in the LDS aperture.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
@@ -150,32 +189,7 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
         }
     };
 
-    issue(st_begin, 0);
-    if (n_st > 1u) issue(st_begin + 1u, 1);
-    if (n_st > 2u) issue(st_begin + 2u, 2);
-    uint32_t i = 0;
-    for (; i + 3u < n_st; ++i) {
-        wait_vm_lgkm0<2 * D>();
-        wg_barrier_no_fence();
-        issue(st_begin + i + 3u, (int)((i + 3u) & 3u));
-        compute((int)(i & 3u));
-    }
-    // Drain: q = n_st - i <= 3 stages left, all issued.
-    if (i + 2u < n_st) {
-        wait_vm_lgkm0<2 * D>();
-        wg_barrier_no_fence();
-        compute((int)(i & 3u));
-        ++i;
-    }
-    if (i + 1u < n_st) {
-        wait_vm_lgkm0<D>();
-        wg_barrier_no_fence();
-        compute((int)(i & 3u));
-        ++i;
-    }
-    wait_vm_lgkm0<0>();
-    wg_barrier_no_fence();
-    compute((int)(i & 3u));
+    lds_ring<NBUF, D>(n_st, [&](uint32_t st, int buf) { issue(st_begin + st, buf); }, compute);
 
     mfma_tile_epilogue<NT>(a, acc, tile, tok0, zgroup, lane, wave);
 }

@@ -20,7 +20,10 @@
 // are loaded two k-steps ahead.  An odd B_vec16 leaves the last k-step half empty: those rows
 // and fragments are zero.  An index word >= Cin reads as a zero row (the reference would read
 // outside X).
+#include <cstdlib>
+
 #include "k44_launch.hpp"
+#include "k44_mfma_dma.hpp"
 
 namespace k44dev {
 
@@ -121,7 +124,146 @@ __global__ __launch_bounds__(256) void k44_token64_kernel(Token64Args a) {
                 yt[(uint64_t)(16 * nb + 4 * g + i) * 64u + 16u * tb] = __float2half_rz(acc[nb][tb][i]);
 }
 
+// ---------------------------------------------------------------------------------------------
+// LDS-ring variant for the large shapes: clusters of a multiple of 64 neurons, batches of whole
+// groups of 4 tiles, even B_vec16 (whole 32-deep k-steps), B <= 4096.  Workgroup = 64 neurons x
+// 4 tiles (4 waves, one tile each).  The cluster's index row is staged in LDS once; then every
+// k-step's 32 gathered rows per tile (128 B each: one global_load_lds_dwordx4 covers 8 rows) and
+// its 64-neuron A fragments (1 KiB per 16-neuron block, contiguous in the WMMA order: one
+// dwordx4 direct load per wave) go memory -> LDS directly, into a ring of 4 stages with 3 in
+// flight (a 6-deep ring measured the same), synchronised exactly as the dense-cluster LDS-ring
+// kernel (lds_ring, k44_mfma_dma.hpp):
+// per stage vmcnt(2D) + bare s_barrier, LDS reads in inline asm with an explicit lgkmcnt wait.
+// Rows of out-of-range indices are read from a zero row in device memory.
+// ---------------------------------------------------------------------------------------------
+__device__ __attribute__((aligned(16))) uint4 k44_t64_zero_row[8];  // 128 zero bytes
+
+constexpr int T64R_IDX_MAX = 4096;
+
+__device__ __forceinline__ uint32_t t64_lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+__global__ __launch_bounds__(256) void k44_token64_ring_kernel(Token64Args a) {
+    constexpr int NB = 4, TW = 4, NBUF = 4;
+    constexpr int XST = 32 * 128;     // bytes of one tile's stage: 32 rows x 64 tokens x fp16
+    constexpr int WST = NB * 64 * 16;  // bytes of one stage's A fragments
+    constexpr int D = 4 + 1;           // direct loads per wave per stage
+    __shared__ __attribute__((aligned(16))) char xr[NBUF][TW][XST];
+    __shared__ __attribute__((aligned(16))) char wr[NBUF][WST];
+    __shared__ uint32_t ix[T64R_IDX_MAX];
+
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t j0 = blockIdx.x * 64u;
+    const uint32_t tile = blockIdx.y * TW + (uint32_t)wave;
+    const uint32_t B = a.B_vec16 * 16u, ksteps = B / 32u;
+    const uint32_t *irow = a.idx + (uint64_t)(j0 / a.cluster) * B;
+    for (uint32_t q = (uint32_t)tid; q < B; q += 256u) {
+        const uint32_t v = irow[q];
+        ix[q] = v < a.Cin ? v : 0xffffffffu;
+    }
+    __syncthreads();
+
+    const char *xt = reinterpret_cast<const char *>(a.X + (uint64_t)tile * a.Cin * 64u);
+    const char *zrow = reinterpret_cast<const char *>(k44_t64_zero_row);
+    const int gr = lane >> 3, gc = (lane & 7) * 16;  // row within an 8-row piece, byte column
+    // A fragments of 16-neuron block `wave`: WMMA vectors (j0/16 + wave, 2 ks .. 2 ks + 1, 0..31)
+    const char *wsrc = reinterpret_cast<const char *>(a.w_wmma) +
+                       ((uint64_t)(j0 / 16u + (uint32_t)wave) * a.B_vec16 * 32u) * 16u;
+    const uint32_t ix_addr = t64_lds_addr(&ix[gr]);
+
+    // Row indices of a k-step for this lane: rows 8i + gr, i = 0..3.
+    auto row_idx = [&](uint32_t ks, uint32_t (&v)[4]) {
+        const uint32_t base = ix_addr + ks * 128u;
+        asm volatile("ds_read_b32 %0, %4\n\tds_read_b32 %1, %4 offset:32\n\t"
+                     "ds_read_b32 %2, %4 offset:64\n\tds_read_b32 %3, %4 offset:96\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=v"(v[0]), "=v"(v[1]), "=v"(v[2]), "=v"(v[3])
+                     : "v"(base)
+                     : "memory");
+    };
+    auto load_stage = [&](uint32_t ks, int buf) {
+        uint32_t v[4];
+        row_idx(ks, v);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const char *src = v[i] != 0xffffffffu ? xt + (uint64_t)v[i] * 128u + gc : zrow + gc;
+            __builtin_amdgcn_global_load_lds((kglobal_void *)src,
+                                             (__attribute__((address_space(3))) void *)&xr[buf][wave][i * 1024],
+                                             16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds((kglobal_void *)(wsrc + (uint64_t)ks * 1024u + lane * 16),
+                                         (__attribute__((address_space(3))) void *)&wr[buf][wave * 1024],
+                                         16, 0, 0);
+    };
+
+    const int g = lane >> 4;
+    f4_t acc[NB][4];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        f4_t b0 = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (a.bias) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b0[i] = __half2float(a.bias[j0 + 16u * nb + 4u * g + i]);
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) acc[nb][tb] = b0;
+    }
+    const int tr_row = 8 * g + ((lane & 15) >> 2), tr_col = 4 * (lane & 3);
+    const uint32_t xa = t64_lds_addr(&xr[0][wave][tr_row * 128 + tr_col * 2]);
+    const uint32_t wa = t64_lds_addr(&wr[0][lane * 16]);
+    auto compute = [&](int buf) {
+        const uint32_t x0 = xa + (uint32_t)buf * (TW * XST), w0 = wa + (uint32_t)buf * WST;
+        h8_t af[NB];
+        h4_t lo[4], hi[4];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            asm volatile("ds_read_b128 %0, %1" : "=v"(af[nb]) : "v"(w0 + nb * 1024u) : "memory");
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo[tb]) : "v"(x0 + 32u * tb) : "memory");
+            asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(hi[tb]) : "v"(x0 + 32u * tb + 512u)
+                         : "memory");
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) asm volatile("" : "+v"(af[nb]));
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            asm volatile("" : "+v"(lo[tb]), "+v"(hi[tb]));
+            const h8_t b = __builtin_shufflevector(lo[tb], hi[tb], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[nb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[nb], b, acc[nb][tb], 0, 0, 0);
+        }
+    };
+
+    lds_ring<NBUF, D>(ksteps, load_stage, compute);
+
+    __half *yt = a.Y + ((uint64_t)tile * a.Cout + j0) * 64u + (lane & 15);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2)
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb)
+                yt[(uint64_t)(16 * nb + 4 * g + i2) * 64u + 16u * tb] =
+                    __float2half_rz(acc[nb][tb][i2]);
+}
+
+bool token64_ring_ok(const Token64Args &a) {
+    return a.cluster % 64u == 0u && a.tiles % 4u == 0u && a.B_vec16 % 2u == 0u &&
+           a.B_vec16 * 16u <= (uint32_t)T64R_IDX_MAX;
+}
+
 hipError_t launch_token64(const Token64Args &a, hipStream_t stream) {
+    const char *env = std::getenv("K44WAVEC_T64_RING");
+    if (token64_ring_ok(a) && !(env && env[0] == '0')) {
+        const dim3 grid(a.Cout / 64u, a.tiles / 4u, 1u), block(256u, 1u, 1u);
+        hipLaunchKernelGGL(k44_token64_ring_kernel, grid, block, 0, stream, a);
+        return hipGetLastError();
+    }
     const uint32_t c16 = a.cluster / 16u;
     const int nb = c16 % 4u == 0u ? 4 : (c16 % 2u == 0u ? 2 : 1);
     const dim3 grid(a.Cout / (16u * (uint32_t)nb), (a.tiles + 3u) / 4u, 1u), block(256u, 1u, 1u);

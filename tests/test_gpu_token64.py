@@ -28,6 +28,9 @@ def test_interleave_matches_host_order(wavec, orc, neurons, B):
     assert np.array_equal(got, orc.raw_to_wmma(w).ravel())
 
 
+_LAST_Y = [None]  # output bits of the last _token64_case call
+
+
 def _token64_case(wavec, orc, *, Cin, Cout, cluster, B_vec16, batch, seed, bad_index=False):
     rng = np.random.default_rng(seed)
     B = 16 * B_vec16
@@ -45,7 +48,9 @@ def _token64_case(wavec, orc, *, Cin, Cout, cluster, B_vec16, batch, seed, bad_i
     Bd = wavec.DeviceBuffer.from_array(b)
     wavec.forward_token64_f16(Yd, Xd, Id, Wd, Bd, batch, Cin, Cout, B_vec16, cluster)
     wavec.device_synchronize()
-    y = Yd.download(np.float16, (tiles, Cout, 64)).astype(np.float64)
+    y16 = Yd.download(np.float16, (tiles, Cout, 64))
+    _LAST_Y[0] = y16.view(np.uint16).copy()
+    y = y16.astype(np.float64)
     w_eff = w.copy()
     idx_eff = idx.astype(np.uint64)
     if bad_index:
@@ -73,38 +78,64 @@ def test_token64_matches_oracle(wavec, orc, cluster, B_vec16, batch):
     assert err <= TOL
 
 
-def test_token64_out_of_range_index_reads_zero(wavec, orc):
-    err = _token64_case(wavec, orc, Cin=500, Cout=64, cluster=64, B_vec16=2, batch=64, seed=7,
+@pytest.mark.parametrize("batch", [64, 256])
+def test_token64_out_of_range_index_reads_zero(wavec, orc, batch):
+    err = _token64_case(wavec, orc, Cin=500, Cout=64, cluster=64, B_vec16=2, batch=batch, seed=7,
                         bad_index=True)
     assert err <= TOL
 
 
-def test_token64_64bit_substrate(wavec, orc):
+@pytest.mark.parametrize("cluster,B_vec16,batch", [(64, 2, 256), (128, 8, 512), (192, 6, 256),
+                                                   (64, 64, 256)])
+def test_token64_ring_matches_oracle_and_fallback(wavec, orc, monkeypatch, cluster, B_vec16,
+                                                  batch):
+    """Shapes the LDS-ring kernel takes (clusters of whole 64-neuron blocks, whole 4-tile
+    groups, even B_vec16): within tolerance of the oracle, and bit-identical to the per-wave
+    kernel (same k-step accumulation order from the bias)."""
+    Cout = cluster * 2
+    ys = {}
+    for ring in ("1", "0"):
+        monkeypatch.setenv("K44WAVEC_T64_RING", ring)
+        err = _token64_case(wavec, orc, Cin=5000, Cout=Cout, cluster=cluster, B_vec16=B_vec16,
+                            batch=batch, seed=cluster + B_vec16)
+        _log(f"[token64 ring={ring} cluster={cluster} B_vec16={B_vec16} batch={batch}] "
+             f"rel err {err:.3e}")
+        assert err <= TOL
+        ys[ring] = _LAST_Y[0]
+    assert np.array_equal(ys["1"], ys["0"])
+
+
+@pytest.mark.parametrize("batch", [64, 256])
+def test_token64_64bit_substrate(wavec, orc, batch):
     """Cin = 40,000,000 positions (5.12 GB per 64-token tile, beyond 32-bit byte offsets),
     filled on the device with the synthetic generator; indices spread over the whole range,
-    the last position included."""
+    the last position included.  Batch 256 takes the LDS-ring kernel (tiles 1..3 at offsets
+    past 5 GB)."""
     Cin, Cout, cluster, B_vec16, seed = 40_000_000, 64, 64, 4, 17
+    tiles = batch // 64
     B = 16 * B_vec16
     rng = np.random.default_rng(11)
     idx = rng.integers(0, Cin, size=(1, B), dtype=np.int64)
     idx[0, :8] = [Cin - 1, (1 << 25) + 1, 1 << 25, 0, 33_554_431, 39_999_000, 12, Cin - 2]
     idx = idx.astype(np.uint32)
     _log("[token64 64-bit] filling a 5.12 GB substrate on the device")
-    X = wavec.DeviceBuffer(Cin * 64 * 2)
-    assert wavec.get_lib().wavec_dev_fill_uniform(X.ptr, Cin, 64, 64, 0, seed) == 0
+    X = wavec.DeviceBuffer(tiles * Cin * 64 * 2)
+    assert wavec.get_lib().wavec_dev_fill_uniform(X.ptr, tiles * Cin, 64, 64, 0, seed) == 0
     w = (rng.standard_normal((Cout, B)) * 0.05).astype(np.float16)
     b = (rng.standard_normal(Cout) * 0.05).astype(np.float16)
-    Y = wavec.DeviceBuffer(Cout * 64 * 2)
+    Y = wavec.DeviceBuffer(tiles * Cout * 64 * 2)
     Id = wavec.DeviceBuffer.from_array(idx)
     Wd = wavec.DeviceBuffer.from_array(orc.raw_to_wmma(w.view(np.uint16)))
     Bd = wavec.DeviceBuffer.from_array(b)
-    wavec.forward_token64_f16(Y, X, Id, Wd, Bd, 64, Cin, Cout, B_vec16, cluster)
+    wavec.forward_token64_f16(Y, X, Id, Wd, Bd, batch, Cin, Cout, B_vec16, cluster)
     wavec.device_synchronize()
     X.free()
-    rows = synth.substrate_rows(seed, idx[0], 64)  # host copy of the rows the wave reads
-    canvas = rows.view(np.uint16).reshape(-1)
+    y = Y.download(np.float16, (tiles, Cout, 64)).astype(np.float64)
     seg = np.arange(B, dtype=np.uint64) * 64
-    ref = orc.wave_f64(canvas, seg, w, b, None, B, 1, cluster, 64, 64, 64, "none")
-    err = orc.rel_err(Y.download(np.float16, (Cout, 64)).astype(np.float64), ref)
-    _log(f"[token64 64-bit] rel err {err:.3e}")
-    assert err <= TOL
+    for t in range(tiles):  # tile t's row p is generator position t * Cin + p
+        rows = synth.substrate_rows(seed, idx[0].astype(np.uint64) + t * Cin, 64)
+        ref = orc.wave_f64(rows.view(np.uint16).reshape(-1), seg, w, b, None, B, 1, cluster, 64,
+                           64, 64, "none")
+        err = orc.rel_err(y[t], ref)
+        _log(f"[token64 64-bit batch={batch} tile {t}] rel err {err:.3e}")
+        assert err <= TOL
