@@ -144,22 +144,30 @@ __device__ __forceinline__ uint32_t t64_lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
-__global__ __launch_bounds__(256) void k44_token64_ring_kernel(Token64Args a) {
-    constexpr int NB = 4, TW = 4, NBUF = 4;
-    constexpr int XST = 32 * 128;     // bytes of one tile's stage: 32 rows x 64 tokens x fp16
-    constexpr int WST = NB * 64 * 16;  // bytes of one stage's A fragments
-    constexpr int D = 4 + 1;           // direct loads per wave per stage
+// NBK 64-neuron blocks of one cluster per workgroup (1, or 2 when the cluster is a multiple of
+// 128 neurons: both blocks then share every gathered row), 4 tiles, 4 * NBK waves: wave w owns
+// tile w % 4 and block w / 4; the NBK waves of a tile split its row loads, every wave loads one
+// 16-neuron block of A fragments per stage.
+template <int NBK, int NBUF>
+__global__ __launch_bounds__(256 * NBK) void k44_token64_ring_kernel(Token64Args a) {
+    constexpr int NB = 4, TW = 4;
+    constexpr int XST = 32 * 128;          // bytes of one tile's stage: 32 rows x 64 tokens x fp16
+    constexpr int WST = NBK * NB * 64 * 16;  // bytes of one stage's A fragments
+    constexpr int XR = 4 / NBK;            // 8-row loads per wave per stage
+    constexpr int D = XR + 1;              // direct loads per wave per stage
     __shared__ __attribute__((aligned(16))) char xr[NBUF][TW][XST];
     __shared__ __attribute__((aligned(16))) char wr[NBUF][WST];
     __shared__ uint32_t ix[T64R_IDX_MAX];
 
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t j0 = blockIdx.x * 64u;
-    const uint32_t tile = blockIdx.y * TW + (uint32_t)wave;
+    const int wt = wave % TW, wb = wave / TW;  // tile and 64-neuron block of this wave
+    const uint32_t jw = blockIdx.x * 64u * NBK;  // first neuron of the workgroup
+    const uint32_t j0 = jw + 64u * (uint32_t)wb;  // first neuron of this wave
+    const uint32_t tile = blockIdx.y * TW + (uint32_t)wt;
     const uint32_t B = a.B_vec16 * 16u, ksteps = B / 32u;
-    const uint32_t *irow = a.idx + (uint64_t)(j0 / a.cluster) * B;
-    for (uint32_t q = (uint32_t)tid; q < B; q += 256u) {
+    const uint32_t *irow = a.idx + (uint64_t)(jw / a.cluster) * B;
+    for (uint32_t q = (uint32_t)tid; q < B; q += 256u * NBK) {
         const uint32_t v = irow[q];
         ix[q] = v < a.Cin ? v : 0xffffffffu;
     }
@@ -168,30 +176,32 @@ __global__ __launch_bounds__(256) void k44_token64_ring_kernel(Token64Args a) {
     const char *xt = reinterpret_cast<const char *>(a.X + (uint64_t)tile * a.Cin * 64u);
     const char *zrow = reinterpret_cast<const char *>(k44_t64_zero_row);
     const int gr = lane >> 3, gc = (lane & 7) * 16;  // row within an 8-row piece, byte column
-    // A fragments of 16-neuron block `wave`: WMMA vectors (j0/16 + wave, 2 ks .. 2 ks + 1, 0..31)
+    // A fragments of 16-neuron block `wave` of the workgroup: WMMA vectors
+    // (jw/16 + wave, 2 ks .. 2 ks + 1, 0..31), 1 KiB contiguous per k-step.
     const char *wsrc = reinterpret_cast<const char *>(a.w_wmma) +
-                       ((uint64_t)(j0 / 16u + (uint32_t)wave) * a.B_vec16 * 32u) * 16u;
-    const uint32_t ix_addr = t64_lds_addr(&ix[gr]);
+                       ((uint64_t)(jw / 16u + (uint32_t)wave) * a.B_vec16 * 32u) * 16u;
+    // This wave loads 8-row pieces p = wb * XR .. wb * XR + XR - 1 of its tile's stage.
+    const uint32_t ix_addr = t64_lds_addr(&ix[8 * wb * XR + gr]);
 
-    // Row indices of a k-step for this lane: rows 8i + gr, i = 0..3.
-    auto row_idx = [&](uint32_t ks, uint32_t (&v)[4]) {
-        const uint32_t base = ix_addr + ks * 128u;
-        asm volatile("ds_read_b32 %0, %4\n\tds_read_b32 %1, %4 offset:32\n\t"
-                     "ds_read_b32 %2, %4 offset:64\n\tds_read_b32 %3, %4 offset:96\n\t"
-                     "s_waitcnt lgkmcnt(0)"
-                     : "=v"(v[0]), "=v"(v[1]), "=v"(v[2]), "=v"(v[3])
-                     : "v"(base)
-                     : "memory");
-    };
     auto load_stage = [&](uint32_t ks, int buf) {
-        uint32_t v[4];
-        row_idx(ks, v);
+        uint32_t v[XR];
+        const uint32_t base = ix_addr + ks * 128u;
+        if constexpr (XR == 4)
+            asm volatile("ds_read_b32 %0, %4\n\tds_read_b32 %1, %4 offset:32\n\t"
+                         "ds_read_b32 %2, %4 offset:64\n\tds_read_b32 %3, %4 offset:96\n\t"
+                         "s_waitcnt lgkmcnt(0)"
+                         : "=v"(v[0]), "=v"(v[1]), "=v"(v[2]), "=v"(v[3]) : "v"(base) : "memory");
+        else
+            asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:32\n\t"
+                         "s_waitcnt lgkmcnt(0)"
+                         : "=v"(v[0]), "=v"(v[1]) : "v"(base) : "memory");
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < XR; ++i) {
             const char *src = v[i] != 0xffffffffu ? xt + (uint64_t)v[i] * 128u + gc : zrow + gc;
-            __builtin_amdgcn_global_load_lds((kglobal_void *)src,
-                                             (__attribute__((address_space(3))) void *)&xr[buf][wave][i * 1024],
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds(
+                (kglobal_void *)src,
+                (__attribute__((address_space(3))) void *)&xr[buf][wt][(wb * XR + i) * 1024], 16, 0,
+                0);
         }
         __builtin_amdgcn_global_load_lds((kglobal_void *)(wsrc + (uint64_t)ks * 1024u + lane * 16),
                                          (__attribute__((address_space(3))) void *)&wr[buf][wave * 1024],
@@ -211,8 +221,8 @@ __global__ __launch_bounds__(256) void k44_token64_ring_kernel(Token64Args a) {
         for (int tb = 0; tb < 4; ++tb) acc[nb][tb] = b0;
     }
     const int tr_row = 8 * g + ((lane & 15) >> 2), tr_col = 4 * (lane & 3);
-    const uint32_t xa = t64_lds_addr(&xr[0][wave][tr_row * 128 + tr_col * 2]);
-    const uint32_t wa = t64_lds_addr(&wr[0][lane * 16]);
+    const uint32_t xa = t64_lds_addr(&xr[0][wt][tr_row * 128 + tr_col * 2]);
+    const uint32_t wa = t64_lds_addr(&wr[0][wb * NB * 1024 + lane * 16]);
     auto compute = [&](int buf) {
         const uint32_t x0 = xa + (uint32_t)buf * (TW * XST), w0 = wa + (uint32_t)buf * WST;
         h8_t af[NB];
@@ -260,8 +270,15 @@ bool token64_ring_ok(const Token64Args &a) {
 hipError_t launch_token64(const Token64Args &a, hipStream_t stream) {
     const char *env = std::getenv("K44WAVEC_T64_RING");
     if (token64_ring_ok(a) && !(env && env[0] == '0')) {
-        const dim3 grid(a.Cout / 64u, a.tiles / 4u, 1u), block(256u, 1u, 1u);
-        hipLaunchKernelGGL(k44_token64_ring_kernel, grid, block, 0, stream, a);
+        // Two 64-neuron blocks sharing every gathered row: half the row traffic but half the
+        // workgroups; measured equal at 128-neuron clusters, slightly faster from 256 on.
+        if (a.cluster % 256u == 0u && !(env && env[0] == '1')) {
+            const dim3 grid(a.Cout / 128u, a.tiles / 4u, 1u), block(512u, 1u, 1u);
+            hipLaunchKernelGGL((k44_token64_ring_kernel<2, 6>), grid, block, 0, stream, a);
+        } else {
+            const dim3 grid(a.Cout / 64u, a.tiles / 4u, 1u), block(256u, 1u, 1u);
+            hipLaunchKernelGGL((k44_token64_ring_kernel<1, 4>), grid, block, 0, stream, a);
+        }
         return hipGetLastError();
     }
     const uint32_t c16 = a.cluster / 16u;
