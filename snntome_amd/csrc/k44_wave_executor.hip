@@ -452,15 +452,26 @@ struct K44GpuExecutorState {
                 wx.rows_per_stage = 32u;
             }
             if (wx.narrow) {
-                // Contraction chunks of 8..16 k-steps (<= 512 rows in LDS), ~256 workgroups per
-                // wave when the wave has fewer tiles than that.
                 wx.path = "mfma_narrow";
                 wx.why += " (at most 16 tokens: weight-streaming narrow tile)";
                 wx.mt = 16u;
                 const uint32_t ksteps = c.B_raw / 32u;
-                uint32_t want = (256u + (uint32_t)rows - 1u) / (uint32_t)rows;
-                want = std::min(want, (ksteps + 7u) / 8u);
-                want = std::max(want, (ksteps + 15u) / 16u);
+                uint32_t want;
+                if (cl >= 64u) {
+                    // Tiles of whole 16-neuron blocks per wave: chunks of any length, streamed
+                    // in 16-k-step sub-chunks.  At most 3 sub-chunks per workgroup; waves of
+                    // >= 32 tiles split no further (fused epilogue, no second kernel), smaller
+                    // ones split into chunks of >= 16 k-steps for parallelism.
+                    want = (ksteps + 47u) / 48u;
+                    if (rows < 32u)
+                        want = std::max(want, std::min((128u + (uint32_t)rows - 1u) / (uint32_t)rows,
+                                                       (ksteps + 15u) / 16u));
+                } else {
+                    // Chunks of 8..16 k-steps (<= 512 rows in LDS), ~256 workgroups per wave.
+                    want = (256u + (uint32_t)rows - 1u) / (uint32_t)rows;
+                    want = std::min(want, (ksteps + 7u) / 8u);
+                    want = std::max(want, (ksteps + 15u) / 16u);
+                }
                 want = std::max(1u, std::min(want, ksteps));
                 wx.stage_chunk = (ksteps + want - 1u) / want;
                 wx.kgroups = (ksteps + wx.stage_chunk - 1u) / wx.stage_chunk;

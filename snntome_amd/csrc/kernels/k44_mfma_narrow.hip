@@ -180,6 +180,141 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
     }
 }
 
+// Tiles of 64 / 128 neurons (every wave owns whole 16-neuron blocks): contraction chunks of any
+// length, taken in sub-chunks of 16 k-steps (512 rows) through two LDS buffers.  While sub-chunk
+// s is multiplied, the X rows of s+1 are in flight to registers, and every A fragment consumed
+// is replaced by its counterpart of s+1 (the weights stream without a gap).  A chunk that
+// covers the whole contraction runs the fused epilogue: waves of up to a few sub-chunks need no
+// split-K partials and no second kernel.
+template <int NT>
+__global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp) {
+    constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16;
+    static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
+    __shared__ __attribute__((aligned(16))) _Float16 xl[2][NARROW_MAX_ROWS][NARROW_PITCH];
+
+    uint32_t w = 0;
+    while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
+    const MfmaTileArgs a = grp.waves[w];
+    const uint32_t local = blockIdx.x - grp.start[w];
+    const uint32_t tile = local % a.tiles, zgroup = local / a.tiles;
+    const uint32_t ks_begin = zgroup * a.stage_chunk;
+    const uint32_t ks_end = min(a.ksteps, ks_begin + a.stage_chunk);
+    const uint32_t nsub = (ks_end - ks_begin + SUBK - 1u) / SUBK;
+
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const kconst_u64 *segr = (const kconst_u64 *)(a.seg) + (uint64_t)tile * a.K;
+    typedef const __attribute__((address_space(1))) h8_t gh8_t;
+    typedef const __attribute__((address_space(1))) u4_t gu4_t;
+    gh8_t *wf = (gh8_t *)(reinterpret_cast<const h8_t *>(a.Wf) +
+                          (uint64_t)tile * a.ksteps * NB * 64 + lane);
+    auto load_a = [&](uint32_t k2, h8_t (&f)[BPW]) {
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) f[i] = wf[((uint64_t)k2 * NB + wave + 4 * i) * 64];
+    };
+
+    // X rows of sub-chunk s: wave pass q covers 32 rows starting at a multiple of 32 (one
+    // segment, S % 32 == 0: wave-uniform start); passes past the sub-chunk re-read its last
+    // 32 rows (fixed load count).
+    constexpr int XQ = NARROW_MAX_ROWS * 2 / 256;
+    auto gather = [&](uint32_t s, u4_t (&xv)[XQ]) {
+        const uint32_t kb = ks_begin + s * SUBK;
+        const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
+        uint64_t sb[XQ];
+#pragma unroll
+        for (int q = 0; q < XQ; ++q) {
+            const uint32_t r = kb * 32u + min((uint32_t)(32 * (wave + 4 * q)), nrows - 32u);
+            const uint32_t k = r / a.S;
+            sb[q] = segr[k] + (uint64_t)(r - k * a.S) * a.step;
+        }
+#pragma unroll
+        for (int q = 0; q < XQ; ++q)
+            xv[q] = *(gu4_t *)(a.X + sb[q] + (uint64_t)(lane >> 1) * a.step +
+                               (uint32_t)(lane & 1) * 8u);
+    };
+    auto store = [&](uint32_t s, int buf, const u4_t (&xv)[XQ]) {
+        const uint32_t kb = ks_begin + s * SUBK;
+        const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
+#pragma unroll
+        for (int q = 0; q < XQ; ++q) {
+            const uint32_t rb = (uint32_t)(32 * (wave + 4 * q));
+            if (rb < nrows)
+                *reinterpret_cast<u4_t *>(&xl[buf][rb + (uint32_t)(lane >> 1)][(lane & 1) * 8]) =
+                    xv[q];
+        }
+    };
+
+    h8_t af[SUBK][BPW];
+#pragma unroll
+    for (int u = 0; u < SUBK; ++u) load_a(min(ks_begin + (uint32_t)u, ks_end - 1u), af[u]);
+    u4_t xv[XQ];
+    gather(0u, xv);
+    store(0u, 0, xv);
+    __syncthreads();
+
+    const int g = lane >> 4;
+    const int tr_row = 8 * g + ((lane & 15) >> 2);
+    const int tr_col = 4 * (lane & 3);
+    f4_t acc[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) acc[i] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (uint32_t s = 0; s < nsub; ++s) {
+        const int buf = (int)(s & 1u);
+        const bool more = s + 1u < nsub;
+        if (more) gather(s + 1u, xv);
+        const uint32_t kb = ks_begin + s * SUBK;
+#pragma unroll
+        for (int u = 0; u < SUBK; ++u) {
+            const uint32_t k2 = kb + (uint32_t)u;
+            if (k2 < ks_end) {
+                const _Float16 *p = &xl[buf][u * 32 + tr_row][tr_col];
+                const h4_t lo = lds_read_tr16(p);
+                const h4_t hi = lds_read_tr16(p + 4 * NARROW_PITCH);
+                const h8_t b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int i = 0; i < BPW; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u][i], b, acc[i], 0, 0, 0);
+            }
+            load_a(min(k2 + (uint32_t)SUBK, ks_end - 1u), af[u]);  // next sub-chunk's fragment
+        }
+        if (more) {
+            store(s + 1u, buf ^ 1, xv);
+            __syncthreads();
+        }
+    }
+
+    // Lane holds C[4g + i][lane & 15]: neuron 16*blk + 4g + i, token lane & 15.
+    const uint32_t t = (uint32_t)(lane & 15);
+    if (!a.part) {
+#pragma unroll
+        for (int bi = 0; bi < BPW; ++bi) {
+            const uint32_t blk = (uint32_t)(wave + 4 * bi);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
+                const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
+                if (oj == K44_CMAP_EMPTY) continue;
+                const uint64_t o = oj * a.out_stride + t;
+                const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
+                const float r = a.R ? __half2float(a.R[o]) : 0.0f;
+                const float v = acc[bi][i] + b;
+                a.Y[o] = __float2half_rn(a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r);
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi) {
+        const uint32_t blk = (uint32_t)(wave + 4 * bi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
+            a.part[((uint64_t)zgroup * a.cout + j) * 16u + t] = acc[bi][i];
+        }
+    }
+}
+
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
                               hipStream_t stream) {
     if (items == 0u) return hipSuccess;
@@ -187,8 +322,8 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
     switch (nt) {
     case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, g); break;
     case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, g); break;
-    case 64u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<64>, grid, block, 0, stream, g); break;
-    case 128u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<128>, grid, block, 0, stream, g); break;
+    case 64u: hipLaunchKernelGGL(k44_mfma_narrow_long_kernel<64>, grid, block, 0, stream, g); break;
+    case 128u: hipLaunchKernelGGL(k44_mfma_narrow_long_kernel<128>, grid, block, 0, stream, g); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -200,3 +200,44 @@ def test_dma_ring_matches_register_staged(wavec, orc, monkeypatch, nt, S, K, til
             assert err <= TOL
             out[(split, dma)] = y
     assert np.array_equal(out[("0", "1")], out[("0", "0")])
+
+
+@pytest.mark.parametrize("K,tokens", [(3, 16), (7, 16), (7, 9), (2, 1)])
+def test_narrow_long_chunks_many_tiles(wavec, orc, monkeypatch, K, tokens):
+    """Waves of >= 32 64-neuron tiles over <= 16 tokens: contraction chunks of several 16-k-step
+    sub-chunks through two LDS buffers, fused epilogue when one chunk covers the contraction
+    (K = 2, 3: 32 / 48 k-steps), split-K partials plus the epilogue kernel otherwise (K = 7:
+    112 k-steps); within tolerance of the oracle and of the wide kernel."""
+    rng = np.random.default_rng(K * 100 + tokens)
+    S, nt, tiles, C = 512, 64, 40, 8192
+    starts = (rng.integers(0, C // S, size=(tiles, K)) * S).astype(np.uint32)
+    cout = tiles * nt
+    w = synth.normal_f16(rng, (cout, K * S), 0.02)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    ys = {}
+    for mode in ("narrow", "wide"):
+        if mode == "wide":
+            monkeypatch.setenv("K44WAVEC_NARROW", "0")
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("x", C, 1, tokens, is_1d=True)
+        g.add_cluster_wave("w", "x", "y", starts, S, w, b, cluster=nt, act="silu", res_blob="x")
+        plan = g.compile()
+        plan.init_gpu()
+        rep = plan.exec_report()["waves"][0]
+        assert rep["path"] == ("mfma_tile" if mode == "wide" else "mfma_narrow"), rep
+        if mode == "narrow":
+            assert (rep["ksplit"] > 1) == (K * S // 32 > 48), rep
+        plan.fill_input_uniform(4)
+        plan.execute(1)
+        st = stride_of(tokens)
+        canvas = plan.read_canvas(0, int(plan.summary["canvas_elems"]))
+        x0 = int(plan.cmds[0]["src_off"])
+        y0 = int(plan.cmds[0]["y_off"])
+        y = canvas[y0:y0 + cout * st].view(np.float16).reshape(cout, st)[:, :tokens]
+        seg = (x0 + starts.astype(np.uint64) * st).ravel()
+        ref = orc.wave_f64(canvas, seg, w, b, None, K, S, nt, st, st, st, "silu", res_off=x0)
+        err = orc.rel_err(y.astype(np.float64), ref[:, :tokens])
+        _log(f"[narrow-long K={K} tok={tokens} {mode}] ksplit {rep['ksplit']} rel err {err:.3e}")
+        assert err <= TOL
+        ys[mode] = y.astype(np.float64)
+    assert orc.rel_err(ys["narrow"], ys["wide"]) <= TOL
