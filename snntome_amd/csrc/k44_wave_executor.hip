@@ -84,6 +84,7 @@ struct WaveExec {
     bool narrow = false;       // MFMA over <= 16 tokens (decode): k44_mfma_narrow_kernel
     bool dma = false;          // MFMA over 512-token workgroups: k44_mfma_dma_kernel
     bool lane8 = false;        // VALU: 8 tokens (16-byte loads) per lane
+    bool stream_loads = false; // VALU: non-temporal X / weight loads (gathered rows >> caches)
     uint32_t part_tokens = 0;  // row length of split-K partials (16 narrow, tokens wide)
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
     uint64_t step = 1;
@@ -119,7 +120,7 @@ struct WaveExec {
 struct MfmaGroupExec {
     std::vector<size_t> members;  // wave indices, plan order
     uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0;
-    bool dma = false;
+    bool dma = false, stream_loads = false;
     size_t part_floats = 0;
     DevBuf<k44dev::MfmaTileArgs> args;
     DevBuf<uint32_t> start, epi;
@@ -274,6 +275,16 @@ struct K44GpuExecutorState {
         for (size_t r = 0; r < rows; ++r)
             for (uint32_t k = 0; k < K; ++k) starts[r * K + k] = off(r, k * S);
         S_out = S;
+    }
+
+    // VALU gathers whose distinct rows are far beyond the caches (>= 512 MiB, twice the MALL)
+    // read their rows and weights with the non-temporal load policy: config 2 (random 8 KiB
+    // segments of a 20 GB substrate) 391 -> 373 us.  Cache-resident substrates keep the default
+    // policy.  K44WAVEC_NT=0/1 forces it.
+    static bool streaming_gather(const WaveExec &wx) {
+        const char *nt = std::getenv("K44WAVEC_NT");
+        if (nt) return std::string(nt) == "1";
+        return wx.unique_rows * (uint64_t)wx.tokens * 2u >= (512ull << 20);
     }
 
     void build_wave(const K44ExecCmd &c, WaveExec &wx) {
@@ -450,6 +461,10 @@ struct K44GpuExecutorState {
                 wx.path = "mfma_dma";
                 wx.why += " (512-token workgroups: 4-stage LDS ring filled by global_load_lds)";
                 wx.rows_per_stage = 32u;
+                // Config 3 measured the same with either load policy (363 TFLOP/s): default
+                // policy unless K44WAVEC_NT=1.
+                const char *nt = std::getenv("K44WAVEC_NT");
+                wx.stream_loads = nt && std::string(nt) == "1";
             }
             if (wx.narrow) {
                 wx.path = "mfma_narrow";
@@ -531,6 +546,7 @@ struct K44GpuExecutorState {
                            wx.res_off % 8u == 0u && wx.step % 8u == 0u;
                 for (uint64_t s0 : starts) ok8 = ok8 && s0 % 8u == 0u;
                 wx.lane8 = want8 && ok8;
+                wx.stream_loads = streaming_gather(wx);
             }
             const char *ks_env = std::getenv("K44WAVEC_KSPLIT");
             wx.ksplit = (wx.K >= 2u && wx.K <= 8u) ? 4u : 1u;
@@ -930,7 +946,8 @@ struct K44GpuExecutorState {
             if (grouping && !runs.empty() && runs.back().first == 2) {
                 MfmaGroupExec &g = *groups[runs.back().second];
                 bool ok = g.nt == w.cluster && g.mt == w.mt && g.rows == w.rows_per_stage &&
-                          g.dma == w.dma && g.members.size() < 64u;
+                          g.dma == w.dma && g.stream_loads == w.stream_loads &&
+                          g.members.size() < 64u;
                 for (size_t m : g.members) {
                     if (!ok) break;
                     const WaveExec &o = *waves[m];
@@ -950,6 +967,7 @@ struct K44GpuExecutorState {
                 g->mt = w.mt;
                 g->rows = w.rows_per_stage;
                 g->dma = w.dma;
+                g->stream_loads = w.stream_loads;
                 g->part_floats = w.part_floats;
                 runs.push_back({2, groups.size()});
                 groups.push_back(std::move(g));
@@ -1046,6 +1064,7 @@ struct K44GpuExecutorState {
               << ", \"ksplit\": " << (w.mfma ? w.kgroups : w.ksplit)
               << ", \"sorted_segments\": " << (w.sorted_segments ? "true" : "false")
               << ", \"tokens_per_lane\": " << (w.mfma ? 0 : (w.lane8 ? 8 : 4))
+              << ", \"stream_loads\": " << (w.stream_loads ? "true" : "false")
               << ", \"flops\": " << (long long)w.flops
               << ", \"effective_flops\": " << (long long)w.eff_flops
               << ", \"mapped\": " << (w.cmap.p ? "true" : "false")
@@ -1071,11 +1090,11 @@ struct K44GpuExecutorState {
     }
 
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
-                           uint32_t items, uint32_t epi_items, bool dma) {
+                           uint32_t items, uint32_t epi_items, bool dma, bool stream_loads) {
         if (mt == 16u)  // narrow (<= 16 tokens)
             K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream));
         else if (dma)
-            K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream));
+            K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream, stream_loads));
         else
             K44_HIP(k44dev::launch_mfma_tile(d, nt, mt, rows, items, stream));
         if (epi_items) K44_HIP(k44dev::launch_splitk_epilogue(d, epi_items, stream));
@@ -1083,12 +1102,13 @@ struct K44GpuExecutorState {
 
     void launch_mfma(const WaveExec &w) {
         const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, w.one_epi.p, 1u};
-        launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma);
+        launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
+                          w.stream_loads);
     }
 
     void launch_group(const MfmaGroupExec &g) {
         const k44dev::MfmaGroup d{g.args.p, g.start.p, g.epi.p, (uint32_t)g.members.size()};
-        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma);
+        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.stream_loads);
     }
 
     void launch_wave(const WaveExec &w) {
@@ -1138,7 +1158,8 @@ struct K44GpuExecutorState {
         a.cout = w.cout;
         a.out_stride = w.out_stride;
         a.act = w.act;
-        K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream, w.lane8));
+        K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream, w.lane8,
+                                          w.stream_loads));
     }
 
     void launch_op(size_t i) {

@@ -13,8 +13,10 @@ namespace k44dev {
 // VALU gather-dot over `cout` neurons x `tokens` tokens with the given slab (64/128/256);
 // ksplit 4 = one neuron per workgroup, its segments split over the 4 waves.
 // lane8: 8 tokens (16-byte loads) per lane instead of 4 (8-byte loads); same weight layout.
+// stream_loads: read X rows and weights with non-temporal loads (substrates far beyond the caches).
 hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
-                             uint32_t tokens, hipStream_t stream, bool lane8 = false);
+                             uint32_t tokens, hipStream_t stream, bool lane8 = false,
+                             bool stream_loads = false);
 
 // MFMA tile kernel over a group of waves (one kernel configuration): `items` workgroups (the
 // group's start[n]), block mt; nt in {16,32,64,128}, mt in {64,128,256,512}, rows_per_stage in
@@ -24,7 +26,8 @@ hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32
 
 // LDS-DMA MFMA tile kernel (512 tokens per workgroup, 32-position stages in a 4-deep LDS ring)
 // over a group: `items` workgroups; nt in {32, 64}.
-hipError_t launch_mfma_dma(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream);
+hipError_t launch_mfma_dma(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream,
+                           bool stream_loads = false);
 
 // Narrow MFMA kernel (waves of at most 16 tokens) over a group: `items` workgroups (tiles x
 // contraction chunks per wave); nt in {16,32,64,128}.

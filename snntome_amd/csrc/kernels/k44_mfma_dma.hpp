@@ -97,7 +97,8 @@ __device__ __forceinline__ h4_t ds_read_tr16_at(uint32_t addr) {
     return v;
 }
 
-template <int NT>
+// NTX: the direct loads use the non-temporal cache policy (substrates far beyond the caches).
+template <int NT, bool NTX>
 __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
     static_assert(NT == 32 || NT == 64, "A-fragment stage must be whole dword loads per wave");
     constexpr int MT = 512, ROWS = 32, NBUF = 4;
@@ -107,6 +108,7 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
     constexpr int WDMA = WBYTES / (8 * 256);  // dword loads per wave per stage (NT / 32)
     constexpr int XDMA = ROWS / 8;          // row loads per wave per stage
     constexpr int D = XDMA + WDMA;          // loads per wave per stage
+    constexpr int CPOL = NTX ? 2 : 0;       // cache-policy operand: 2 = nt
     __shared__ __attribute__((aligned(16))) _Float16 xl[NBUF][ROWS][PITCH];
     __shared__ __attribute__((aligned(16))) uint32_t wl[NBUF][WBYTES / 4];
 
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
             const int row = wave + 8 * r;
             __builtin_amdgcn_global_load_lds((kglobal_void *)(base + (uint64_t)row * a.step),
                                              (__attribute__((address_space(3))) void *)&xl[buf][row][0],
-                                             16, 0, 0);
+                                             16, 0, CPOL);
         }
         const char *ws = wtile + (uint64_t)st * WBYTES;
 #pragma unroll
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
             const int q = wave * WDMA + j;  // 256-byte piece of the stage's A fragments
             __builtin_amdgcn_global_load_lds((kglobal_void *)(ws + q * 256 + lane * 4),
                                              (__attribute__((address_space(3))) void *)&wl[buf][q * 64],
-                                             4, 0, 0);
+                                             4, 0, CPOL);
         }
     };
 

@@ -36,11 +36,6 @@ typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef short s4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u4_t __attribute__((ext_vector_type(4)));
-// Address-space-qualified views: read-only tables through the constant space (scalar loads),
-// data through the global space (a generic pointer loaded from memory would compile to flat
-// loads, which also count against the LDS wait counter).
-typedef const __attribute__((address_space(1))) void kglobal_void;
-typedef const __attribute__((address_space(4))) uint64_t kconst_u64;
 
 // ds_read_b64_tr_b16 on an LDS address: 4 x 16-bit, transposed across each 16-lane group.
 __device__ __forceinline__ h4_t lds_read_tr16(const _Float16 *p) {

@@ -21,16 +21,17 @@ __global__ __launch_bounds__(256) void k44_fill_uniform_kernel(__half *dst, uint
 }
 
 
-hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
-                             uint32_t tokens, hipStream_t stream, bool lane8) {
+template <bool NTX>
+static hipError_t launch_gather_dot_policy(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
+                                           uint32_t tokens, hipStream_t stream, bool lane8) {
     const dim3 grid(ksplit == 4u ? a.cout : (a.cout + 3u) / 4u, tokens / slab, 1u);
     const dim3 block(256u, 1u, 1u);
     if (lane8) {
 #define K44_GD8(SLAB)                                                                           \
     if (ksplit == 4u)                                                                           \
-        hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 4>), grid, block, 0, stream, a);       \
+        hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 4, NTX>), grid, block, 0, stream, a);  \
     else                                                                                        \
-        hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 1>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 1, NTX>), grid, block, 0, stream, a);
         switch (slab) {
         case 256u: K44_GD8(256) break;
         case 128u: K44_GD8(128) break;
@@ -40,11 +41,11 @@ hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksp
 #undef K44_GD8
         return hipGetLastError();
     }
-#define K44_GD(SLAB, U)                                                                        \
-    if (ksplit == 4u)                                                                          \
-        hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 4>), grid, block, 0, stream, a);     \
-    else                                                                                       \
-        hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 1>), grid, block, 0, stream, a);
+#define K44_GD(SLAB, U)                                                                          \
+    if (ksplit == 4u)                                                                            \
+        hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 4, NTX>), grid, block, 0, stream, a);  \
+    else                                                                                         \
+        hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 1, NTX>), grid, block, 0, stream, a);
     switch (slab) {
     case 256u: K44_GD(256, 16) break;
     case 128u: K44_GD(128, 8) break;
@@ -53,6 +54,12 @@ hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksp
     }
 #undef K44_GD
     return hipGetLastError();
+}
+
+hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
+                             uint32_t tokens, hipStream_t stream, bool lane8, bool stream_loads) {
+    return stream_loads ? launch_gather_dot_policy<true>(a, slab, ksplit, tokens, stream, lane8)
+                        : launch_gather_dot_policy<false>(a, slab, ksplit, tokens, stream, lane8);
 }
 
 // Split-K reduction + epilogue: thread = (neuron j, 4 tokens) of the wave that owns the

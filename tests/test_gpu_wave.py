@@ -129,3 +129,29 @@ def test_tcff_roundtrip_on_gpu(wavec, orc, tmp_path):
         cmd = p.cmds[0]
         outs.append(p.read_canvas(int(cmd["y_off"]), cout * stride_of(tokens)))
     assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("lanes", [4, 8])
+@pytest.mark.parametrize("tokens,S", [(256, 32), (256, 24), (100, 16), (512, 40)])
+def test_streaming_loads_bit_identical(wavec, orc, monkeypatch, lanes, tokens, S):
+    """The non-temporal load policy (chosen for substrates far beyond the caches, forced here
+    with K44WAVEC_NT=1) changes the cache policy only: outputs equal the default policy's bit
+    for bit, over whole and partial 16-row batches, both lane widths, residual and bias."""
+    monkeypatch.setenv("K44WAVEC_LANE8", "1" if lanes == 8 else "0")
+    rng = np.random.default_rng(tokens + S)
+    C, cout, K = 4000, 64, 3
+    starts = (rng.integers(0, (C - S) // 8, size=(cout, K)) * 8).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.1)
+    b = synth.normal_f16(rng, (cout,), 0.1)
+    ys = {}
+    for nt in ("0", "1"):
+        monkeypatch.setenv("K44WAVEC_NT", nt)
+        y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
+                                       rows=cluster_rows(starts, S), weights=w, bias=b,
+                                       act="relu", residual=True, seed=11)
+        rep = plan.exec_report()["waves"][0]
+        assert rep["path"] == "valu_gather_dot" and rep["stream_loads"] == (nt == "1"), rep
+        assert rep["tokens_per_lane"] == lanes
+        assert orc.rel_err(y, ref) <= TOL
+        ys[nt] = y
+    assert np.array_equal(ys["0"], ys["1"])
