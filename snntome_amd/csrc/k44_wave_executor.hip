@@ -85,6 +85,7 @@ struct WaveExec {
     bool dma = false;          // MFMA over 512-token workgroups: k44_mfma_dma_kernel
     bool lane8 = false;        // VALU: 8 tokens (16-byte loads) per lane
     bool stream_loads = false; // VALU: non-temporal X / weight loads (gathered rows >> caches)
+    bool stream_kernel = false; // VALU: k44_gather_stream_kernel (output rows staged in LDS)
     uint32_t part_tokens = 0;  // row length of split-K partials (16 narrow, tokens wide)
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
     uint64_t step = 1;
@@ -551,6 +552,20 @@ struct K44GpuExecutorState {
             const char *ks_env = std::getenv("K44WAVEC_KSPLIT");
             wx.ksplit = (wx.K >= 2u && wx.K <= 8u) ? 4u : 1u;
             if (ks_env) wx.ksplit = std::string(ks_env) == "4" ? 4u : 1u;
+            {
+                // Streaming gathers over 256-token slabs with >= 256 workgroups of 256 neurons:
+                // stage the output rows in LDS and write them after the last gather (writes
+                // interleaved with the random reads cost ~15 % on config 2).
+                const char *sk = std::getenv("K44WAVEC_STREAMK");
+                const bool big = (uint64_t)(c.Cout / 256u) * (wx.tokens / 256u) >= 256u;
+                wx.stream_kernel = wx.stream_loads && !wx.lane8 && wx.slab == 256u &&
+                                   !wx.has_res && (sk ? std::string(sk) == "1" : big);
+                if (wx.stream_kernel) {
+                    wx.ksplit = 1u;
+                    wx.why += "; streaming kernel: 256 neurons per workgroup, output rows "
+                              "staged in LDS";
+                }
+            }
             const uint32_t rpi = 256u / wx.slab;
             wx.U = 16u / rpi;
             const uint32_t per_batch = rpi * wx.U;
@@ -1065,6 +1080,7 @@ struct K44GpuExecutorState {
               << ", \"sorted_segments\": " << (w.sorted_segments ? "true" : "false")
               << ", \"tokens_per_lane\": " << (w.mfma ? 0 : (w.lane8 ? 8 : 4))
               << ", \"stream_loads\": " << (w.stream_loads ? "true" : "false")
+              << ", \"stream_kernel\": " << (w.stream_kernel ? "true" : "false")
               << ", \"flops\": " << (long long)w.flops
               << ", \"effective_flops\": " << (long long)w.eff_flops
               << ", \"mapped\": " << (w.cmap.p ? "true" : "false")
@@ -1158,8 +1174,11 @@ struct K44GpuExecutorState {
         a.cout = w.cout;
         a.out_stride = w.out_stride;
         a.act = w.act;
-        K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream, w.lane8,
-                                          w.stream_loads));
+        if (w.stream_kernel)
+            K44_HIP(k44dev::launch_gather_stream(a, w.tokens, stream, w.stream_loads));
+        else
+            K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream, w.lane8,
+                                              w.stream_loads));
     }
 
     void launch_op(size_t i) {

@@ -132,7 +132,7 @@ __device__ __forceinline__ void load_weights(float (&w)[U], const __half *p) {
 // few segments (the ultra-sparse regime), instead of serialising K load-wait-FMA phases.
 // NTX: X rows and weights are read with non-temporal loads (see ld_once).
 template <int SLAB, int U, int KSPLIT, bool NTX>
-__global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k44_gather_dot_kernel(GatherDotArgs a) {
     constexpr int LPR = SLAB / 4;  // lanes per position row
     constexpr int RPI = 64 / LPR;  // rows per load instruction
     const int lane = (int)(threadIdx.x & 63u);
@@ -150,27 +150,47 @@ __global__ __launch_bounds__(256) void k44_gather_dot_kernel(GatherDotArgs a) {
     const __half *wl = a.W + (uint64_t)j * batches * (RPI * U) + g * U;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
+    // Row addresses: a wave-uniform row base (scalar) plus this lane's byte offset, so that each
+    // load is one scalar-base + 32-bit-offset access and no 64-bit address lives in VGPRs.
+    const uint32_t lane_off = 8u * (uint32_t)c;
+    const uint64_t row_bytes = a.step * 2u;
     for (uint32_t k = KSPLIT == 1 ? 0u : (uint32_t)wave; k < a.K; k += KSPLIT) {
-        const __half *xs = a.X + seg[k] + slab0 + 4u * (uint32_t)c;
+        const char *xseg = reinterpret_cast<const char *>(a.X + seg[k] + slab0);
         for (uint32_t b = 0; b < a.n_batch; ++b) {
             const uint32_t s0 = b * (uint32_t)(RPI * U) + (uint32_t)(g * U);
             gd_u2 x[U];
             if ((b + 1u) * (uint32_t)(RPI * U) <= a.S) {  // whole batch inside the segment
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    x[u] = ld_once<NTX>(reinterpret_cast<const gd_u2 *>(xs + (uint64_t)(s0 + u) * a.step));
+                    x[u] = ld_once<NTX>(reinterpret_cast<const gd_u2 *>(
+                        xseg + (uint64_t)(s0 + u) * row_bytes + lane_off));
             } else {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const uint32_t s = s0 + (uint32_t)u;
-                    x[u] = s < a.S ? ld_once<NTX>(reinterpret_cast<const gd_u2 *>(xs + (uint64_t)s * a.step))
+                    x[u] = s < a.S ? ld_once<NTX>(reinterpret_cast<const gd_u2 *>(
+                                         xseg + (uint64_t)s * row_bytes + lane_off))
                                    : gd_u2{0u, 0u};
                 }
             }
-            float w[U];
-            load_weights<U, NTX>(w, wl + ((uint64_t)k * a.n_batch + b) * (RPI * U));
+            const __half *wb = wl + ((uint64_t)k * a.n_batch + b) * (RPI * U);
+            if constexpr (RPI == 1) {
+                // One row per instruction: every lane needs the same U weights — scalar loads,
+                // consumed straight from SGPRs.
+                const kconst_u32 *ww = (const kconst_u32 *)wb;
 #pragma unroll
-            for (int u = 0; u < U; ++u) fma4(acc, w[u], make_uint2(x[u].x, x[u].y));
+                for (int u = 0; u < U; u += 2) {
+                    const uint32_t pair = ww[u / 2];
+                    const float2 wf = __half22float2(*reinterpret_cast<const __half2 *>(&pair));
+                    fma4(acc, wf.x, make_uint2(x[u].x, x[u].y));
+                    fma4(acc, wf.y, make_uint2(x[u + 1].x, x[u + 1].y));
+                }
+            } else {
+                float w[U];
+                load_weights<U, NTX>(w, wb);
+#pragma unroll
+                for (int u = 0; u < U; ++u) fma4(acc, w[u], make_uint2(x[u].x, x[u].y));
+            }
         }
     }
 
@@ -316,6 +336,122 @@ __global__ __launch_bounds__(256) void k44_gather_dot8_kernel(GatherDotArgs a) {
         out[t] = __float2half_rn(y);
     }
     *reinterpret_cast<gd_u4 *>(a.Y + o) = *reinterpret_cast<const gd_u4 *>(out);
+}
+
+// Streaming variant for waves whose gathers come from far beyond the caches (256-token slabs,
+// 4 tokens per lane, no residual).  Measured on config 2's pattern: the write of each neuron's
+// 512-byte output row, interleaved with the random gathers, costs ~15 % of the kernel (HBM
+// read/write turnaround: 308 us of pure gathers, 366 us with the rows written as they are
+// done, 320 us when they are written in one burst at the end).  So a workgroup owns NPW
+// neurons of one slab, keeps their finished fp16 rows in LDS (NPW x 512 B) and writes them
+// after its last gather.  Wave w takes neurons w, w + WAVES, ...; its work is the flat list of
+// (neuron, segment, 16-row batch) steps, two steps in flight (the loads of step t+1 are issued
+// before the FMAs of step t).  Per neuron the accumulation order is that of
+// k44_gather_dot_kernel<256, 16, 1>: segments, batches and rows in order, one FMA chain — the
+// two kernels give bit-identical outputs.  Weights are scalar loads (every lane needs the same
+// 16 per batch).
+template <int NPW, int WAVES, bool NTX>
+__global__ __launch_bounds__(WAVES * 64) void k44_gather_stream_kernel(GatherDotArgs a) {
+    constexpr int U = 16;
+    constexpr int PER = NPW / WAVES;  // neuron slots per wave
+    static_assert(NPW % WAVES == 0, "whole neuron slots per wave");
+    __shared__ gd_u2 orow[NPW][64];
+    const int lane = (int)(threadIdx.x & 63u);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t j0 = blockIdx.x * (uint32_t)NPW;
+    const uint32_t slab0 = blockIdx.y * 256u;
+    const uint32_t lane_off = 8u * (uint32_t)lane;
+    const uint64_t row_bytes = a.step * 2u;
+    // Neurons of this wave: j0 + wave + i*WAVES for i < n_mine (the last workgroup may be short).
+    const uint32_t n_here = min((uint32_t)NPW, a.cout - j0);
+    const uint32_t n_mine = n_here > (uint32_t)wave ? (n_here - (uint32_t)wave + WAVES - 1u) / WAVES : 0u;
+    const uint32_t per_neuron = a.K * a.n_batch;
+    const uint32_t total = n_mine * per_neuron;
+
+    // Step t -> (neuron slot i, segment k, batch b) by running counters, advanced per step.
+    struct Cursor {
+        uint32_t i, k, b;
+    };
+    auto advance = [&](Cursor &c) {
+        if (++c.b == a.n_batch) {
+            c.b = 0;
+            if (++c.k == a.K) {
+                c.k = 0;
+                ++c.i;
+            }
+        }
+    };
+    auto issue = [&](const Cursor &c, gd_u2 (&x)[U]) {
+        const uint32_t j = j0 + (uint32_t)wave + c.i * WAVES;
+        const kconst_u64 *seg = (const kconst_u64 *)a.seg + (uint64_t)(j / a.cluster) * a.K;
+        const char *xseg = reinterpret_cast<const char *>(a.X + seg[c.k] + slab0);
+        const uint32_t s0 = c.b * (uint32_t)U;
+        if (s0 + (uint32_t)U <= a.S) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                x[u] = ld_once<NTX>(reinterpret_cast<const gd_u2 *>(
+                    xseg + (uint64_t)(s0 + u) * row_bytes + lane_off));
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t s = s0 + (uint32_t)u;
+                x[u] = s < a.S ? ld_once<NTX>(reinterpret_cast<const gd_u2 *>(
+                                     xseg + (uint64_t)s * row_bytes + lane_off))
+                               : gd_u2{0u, 0u};
+            }
+        }
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto consume = [&](const Cursor &c, const gd_u2 (&x)[U]) {
+        const uint32_t j = j0 + (uint32_t)wave + c.i * WAVES;
+        const kconst_u32 *ww = (const kconst_u32 *)(a.W + (((uint64_t)j * a.K + c.k) * a.n_batch + c.b) * U);
+#pragma unroll
+        for (int u = 0; u < U; u += 2) {
+            const uint32_t pair = ww[u / 2];
+            const float2 wf = __half22float2(*reinterpret_cast<const __half2 *>(&pair));
+            fma4(acc, wf.x, make_uint2(x[u].x, x[u].y));
+            fma4(acc, wf.y, make_uint2(x[u + 1].x, x[u + 1].y));
+        }
+        if (c.k + 1u == a.K && c.b + 1u == a.n_batch) {  // neuron done: fused epilogue into LDS
+            const float bias =
+                a.bias ? __half2float(__ushort_as_half((unsigned short)half_of(scalar_word16(a.bias, a.W, j), j)))
+                       : 0.0f;
+            __half out[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                out[t] = __float2half_rn(apply_act(acc[t] + bias, a.act));
+                acc[t] = 0.0f;
+            }
+            orow[(uint32_t)wave + c.i * WAVES][lane] = *reinterpret_cast<const gd_u2 *>(out);
+        }
+    };
+
+    gd_u2 xa[U], xb[U];
+    Cursor ca{0u, 0u, 0u};
+    if (total) issue(ca, xa);
+    for (uint32_t t = 0; t < total; t += 2) {
+        Cursor cb = ca;
+        advance(cb);
+        if (t + 1u < total) issue(cb, xb);
+        consume(ca, xa);
+        if (t + 1u >= total) break;
+        ca = cb;
+        advance(ca);
+        if (t + 2u < total) issue(ca, xa);
+        consume(cb, xb);
+    }
+    __syncthreads();
+    // Burst write of the finished rows: wave w writes rows w, w + WAVES, ... (512 B each).
+    for (uint32_t l = (uint32_t)wave; l < n_here; l += WAVES) {
+        const uint32_t j = j0 + l;
+        const uint64_t oj = a.cmap ? (uint64_t)half_of(scalar_word16(a.cmap, a.W, j), j) : (uint64_t)j;
+        if (oj == K44_CMAP_EMPTY) continue;
+        gd_u2 *dst = reinterpret_cast<gd_u2 *>(a.Y + oj * a.out_stride + slab0) + lane;
+        if constexpr (NTX)
+            __builtin_nontemporal_store(orow[l][lane], dst);
+        else
+            *dst = orow[l][lane];
+    }
 }
 
 // Synthetic substrate: X[pos][t] = fp16_rne((int32(h >> 40) - 2^23) * 2^-23) with

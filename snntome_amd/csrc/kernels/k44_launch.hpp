@@ -13,6 +13,10 @@ namespace k44dev {
 // VALU gather-dot over `cout` neurons x `tokens` tokens with the given slab (64/128/256);
 // ksplit 4 = one neuron per workgroup, its segments split over the 4 waves.
 // lane8: 8 tokens (16-byte loads) per lane instead of 4 (8-byte loads); same weight layout.
+// Streaming gather kernel (256-token slabs, no residual): output rows staged in LDS and written
+// after the workgroup's last gather.  tokens: a multiple of 256.
+hipError_t launch_gather_stream(const GatherDotArgs &a, uint32_t tokens, hipStream_t stream,
+                                bool stream_loads);
 // stream_loads: read X rows and weights with non-temporal loads (substrates far beyond the caches).
 hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
                              uint32_t tokens, hipStream_t stream, bool lane8 = false,

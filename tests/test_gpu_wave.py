@@ -155,3 +155,71 @@ def test_streaming_loads_bit_identical(wavec, orc, monkeypatch, lanes, tokens, S
         assert orc.rel_err(y, ref) <= TOL
         ys[nt] = y
     assert np.array_equal(ys["0"], ys["1"])
+
+
+@pytest.mark.parametrize("cout,K,S,tokens,act,cluster", [
+    (300, 3, 24, 256, "gelu", 1),    # two workgroups, the second short; partial 16-row batches
+    (512, 4, 16, 512, "relu", 1),    # two 256-token slabs
+    (256, 1, 40, 256, "silu", 2),    # one segment per neuron, shared index rows
+    (40, 2, 16, 256, "none", 1),     # fewer neurons than waves in the workgroup
+])
+def test_stream_kernel_bit_identical(wavec, orc, monkeypatch, cout, K, S, tokens, act, cluster):
+    """The streaming gather kernel (output rows staged in LDS, written after the last gather;
+    forced with K44WAVEC_STREAMK=1) accumulates each neuron in the order of the one-neuron-per-
+    wave kernel (K44WAVEC_KSPLIT=1): bit-identical outputs, both within tolerance of the oracle."""
+    monkeypatch.setenv("K44WAVEC_NT", "1")
+    monkeypatch.setenv("K44WAVEC_LANE8", "0")
+    rng = np.random.default_rng(cout + K * 10 + S)
+    C = 5000
+    starts = (rng.integers(0, (C - S) // 8, size=(cout // cluster, K)) * 8).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.08)
+    b = synth.normal_f16(rng, (cout,), 0.1)
+    ys = {}
+    for mode in ("stream", "plain"):
+        monkeypatch.setenv("K44WAVEC_STREAMK", "1" if mode == "stream" else "0")
+        monkeypatch.setenv("K44WAVEC_KSPLIT", "1")
+        y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
+                                       rows=cluster_rows(starts, S), weights=w, bias=b,
+                                       cluster=cluster, act=act, seed=13)
+        rep = plan.exec_report()["waves"][0]
+        assert rep["stream_kernel"] == (mode == "stream"), rep
+        err = orc.rel_err(y, ref)
+        _log(f"[stream-kernel cout={cout} K={K} S={S} tok={tokens} {mode}] rel err {err:.3e}")
+        assert err <= TOL
+        ys[mode] = y
+    assert np.array_equal(ys["stream"], ys["plain"])
+
+
+def test_stream_kernel_cout_map(wavec, orc, monkeypatch):
+    """Streaming kernel on a pruned projection (VALU path): cout_map stores and empty slots of
+    the pattern-sorted tiles, against the per-neuron fp64 oracle."""
+    monkeypatch.setenv("K44WAVEC_PATH", "valu")
+    monkeypatch.setenv("K44WAVEC_NT", "1")
+    monkeypatch.setenv("K44WAVEC_LANE8", "0")
+    monkeypatch.setenv("K44WAVEC_STREAMK", "1")
+    rng = np.random.default_rng(77)
+    n_cl, K, S, cout, tokens = 6, 3, 32, 333, 256
+    C = n_cl * S
+    pick = np.argsort(rng.random((cout, n_cl)), axis=1)[:, :K]
+    starts = (pick * S).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", C, 1, tokens, is_1d=True)
+    g.add_pruned_wave("p", "x", "y", starts, S, w, b, tile=32, act="gelu")
+    plan = g.compile()
+    plan.init_gpu()
+    rep = plan.exec_report()["waves"]
+    assert all(r["stream_kernel"] and r["mapped"] for r in rep), rep
+    plan.fill_input_uniform(5)
+    plan.execute(1)
+    st = stride_of(tokens)
+    canvas = plan.read_canvas(0, int(plan.summary["canvas_elems"]))
+    x0 = int(plan.cmds[0]["src_off"])
+    seg = (x0 + starts.astype(np.uint64) * st).ravel()
+    ref = orc.wave_f64(canvas, seg, w, b, None, K, S, 1, st, st, st, "gelu")
+    y0 = int(plan.cmds[0]["y_off"])
+    y = canvas[y0:y0 + cout * st].view(np.float16).reshape(cout, st).astype(np.float64)
+    err = orc.rel_err(y, ref)
+    _log(f"[stream-kernel cout_map] rel err {err:.3e}")
+    assert err <= TOL
