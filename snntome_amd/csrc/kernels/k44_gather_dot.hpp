@@ -47,7 +47,8 @@ __device__ __forceinline__ uint32_t half_of(uint32_t word, uint32_t j) {
 enum : int { ACT_NONE = 0, ACT_RELU = 1, ACT_SIGMOID = 2, ACT_SILU = 3, ACT_LEAKY = 4, ACT_GELU = 5 };
 
 // cout_map entry of an empty slot (a pattern-sorted tile with fewer neurons than slots): the
-// epilogue stores nothing for it.
+// epilogue stores nothing for it.  Only with a cout_map: without one, neuron 65535 of a large
+// wave is an ordinary output channel.
 constexpr uint64_t K44_CMAP_EMPTY = 0xffffu;
 
 __device__ __forceinline__ float apply_act(float v, int act) {
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     const uint64_t oj = a.cmap ? (uint64_t)half_of(cmap_w, j) : (uint64_t)j;
     const float bias =
         a.bias ? __half2float(__ushort_as_half((unsigned short)half_of(bias_w, j))) : 0.0f;
-    if (oj == K44_CMAP_EMPTY) return;  // empty slot of a pattern-sorted tile: no output
+    if (a.cmap && oj == K44_CMAP_EMPTY) return;  // empty slot of a pattern-sorted tile: no output
     const uint64_t o = oj * a.out_stride + slab0 + 4u * (uint32_t)c;
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.R) {
@@ -319,7 +320,7 @@ __global__ __launch_bounds__(256) void k44_gather_dot8_kernel(GatherDotArgs a) {
     const uint64_t oj = a.cmap ? (uint64_t)half_of(cmap_w, j) : (uint64_t)j;
     const float bias =
         a.bias ? __half2float(__ushort_as_half((unsigned short)half_of(bias_w, j))) : 0.0f;
-    if (oj == K44_CMAP_EMPTY) return;
+    if (a.cmap && oj == K44_CMAP_EMPTY) return;
     const uint64_t o = oj * a.out_stride + slab0 + 8u * (uint32_t)c;
     float r[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (a.R) {
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(WAVES * 64) void k44_gather_stream_kernel(GatherDot
     for (uint32_t l = (uint32_t)wave; l < n_here; l += WAVES) {
         const uint32_t j = j0 + l;
         const uint64_t oj = a.cmap ? (uint64_t)half_of(scalar_word16(a.cmap, a.W, j), j) : (uint64_t)j;
-        if (oj == K44_CMAP_EMPTY) continue;
+        if (a.cmap && oj == K44_CMAP_EMPTY) continue;
         gd_u2 *dst = reinterpret_cast<gd_u2 *>(a.Y + oj * a.out_stride + slab0) + lane;
         if constexpr (NTX)
             __builtin_nontemporal_store(orow[l][lane], dst);

@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
             for (int i = 0; i < 4; ++i) {
                 const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
                 const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-                if (oj == K44_CMAP_EMPTY) continue;
+                if (a.cmap && oj == K44_CMAP_EMPTY) continue;
                 const uint64_t o = oj * a.out_stride + t;
                 const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
                 const float r = a.R ? __half2float(a.R[o]) : 0.0f;
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
             for (int i = 0; i < 4; ++i) {
                 const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
                 const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-                if (oj == K44_CMAP_EMPTY) continue;
+                if (a.cmap && oj == K44_CMAP_EMPTY) continue;
                 const uint64_t o = oj * a.out_stride + t;
                 const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
                 const float r = a.R ? __half2float(a.R[o]) : 0.0f;

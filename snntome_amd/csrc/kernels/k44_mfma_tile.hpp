@@ -109,7 +109,7 @@ __device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a, const 
             const uint32_t j = n_base + 16u * nb + (uint32_t)i;
             const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
             const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-            if (oj == K44_CMAP_EMPTY) continue;  // empty slot of a pattern-sorted tile
+            if (a.cmap && oj == K44_CMAP_EMPTY) continue;  // empty slot of a pattern-sorted tile
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
                 const uint64_t o = oj * a.out_stride + t_base + 16u * tb;

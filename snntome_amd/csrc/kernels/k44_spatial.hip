@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) void k44_gather_tile_kernel(GatherTileArgs a) 
         for (int off = 16; off < 64; off <<= 1)
 #pragma unroll
             for (int q = 0; q < 4; ++q) acc[q] += __shfl_xor(acc[q], off, 64);
-        if (g != 0u || oj == K44_CMAP_EMPTY) continue;
+        if (g != 0u || (a.cmap && oj == K44_CMAP_EMPTY)) continue;
         const uint32_t tl = t % a.tiles_per_frame;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {

@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp)
         v.z += u1.z;
         v.w += u1.w;
     }
-    if (oj == K44_CMAP_EMPTY) return;
+    if (a.cmap && oj == K44_CMAP_EMPTY) return;
     const uint64_t o = oj * a.out_stride + t;
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.R) {

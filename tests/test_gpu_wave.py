@@ -8,7 +8,7 @@ import pytest
 
 from snntome_amd import synth
 
-from wave_cases import TOL, cluster_rows, random_rows, run_sparse_case, stride_of
+from wave_cases import TOL, cluster_rows, random_rows, run_sparse_case, sampled_parity, stride_of
 
 pytestmark = pytest.mark.gpu
 
@@ -31,6 +31,32 @@ def test_config1_full_wave(wavec, orc):
     err = orc.rel_err(y, ref)
     _log(f"[c1] rel err {err:.3e}")
     assert err <= TOL
+
+
+def test_config2_full_wave_sampled(wavec, orc):
+    """Config 2 at full size (40,000,000 x 256 substrate = 20.5 GB generated on the device,
+    65,536 neurons x 4 clusters of S=16): the streaming kernel with non-temporal loads; 768
+    neurons (first, middle and last workgroups) against the oracle, and a second execution
+    bit-identical to the first (the kernel's result does not depend on cache state or timing)."""
+    wl = synth.config2()
+    _log(f"[c2] {wl.description}")
+    plan = synth.build_graph(wl, wavec).compile()
+    plan.init_gpu()
+    rep = plan.exec_report()["waves"][0]
+    _log(f"[c2] path={rep['path']} stream_kernel={rep['stream_kernel']} "
+         f"stream_loads={rep['stream_loads']}")
+    assert rep["path"] == "valu_gather_dot" and rep["stream_kernel"] and rep["stream_loads"]
+    plan.fill_input_uniform(wl.seed)
+    plan.execute(1)
+    neurons = np.concatenate([np.arange(0, 256), np.arange(30000, 30256),
+                              np.arange(65280, 65536)])
+    y, ref = sampled_parity(orc, plan, wl, 0, neurons)
+    err = orc.rel_err(y, ref)
+    _log(f"[c2] rel err over {len(neurons)} neurons x 256 tokens: {err:.3e}")
+    assert err <= TOL
+    plan.execute(1)
+    y2, _ = sampled_parity(orc, plan, wl, 0, neurons[:64])
+    assert np.array_equal(y2, y[:64])
 
 
 @pytest.mark.parametrize("lanes", [4, 8])
@@ -223,3 +249,25 @@ def test_stream_kernel_cout_map(wavec, orc, monkeypatch):
     err = orc.rel_err(y, ref)
     _log(f"[stream-kernel cout_map] rel err {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("path,cluster", [("valu", 1), ("mfma", 16)])
+def test_neuron_65535_without_cout_map(wavec, orc, monkeypatch, path, cluster):
+    """Waves of more than 65,536 neurons: channel 65535 equals the 16-bit empty-slot marker of
+    cout_map, which must only mean "no output" when the wave has a cout_map (regression: the
+    last neuron of config 2 was dropped)."""
+    monkeypatch.setenv("K44WAVEC_PATH", path)
+    rng = np.random.default_rng(65535)
+    C, cout, K, S, tokens = 4096, 65536 + 32, 1, 32, 64
+    starts = (rng.integers(0, (C - S) // 16, size=(cout // cluster, K)) * 16).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.1)
+    b = synth.normal_f16(rng, (cout,), 0.1)
+    y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
+                                   rows=cluster_rows(starts, S), weights=w, bias=b,
+                                   cluster=cluster, act="none", seed=21)
+    assert plan.exec_report()["waves"][0]["path"].startswith(path)
+    tail = slice(65536 - 64, cout)
+    err = orc.rel_err(y[tail], ref[tail])
+    _log(f"[65535 {path}] rel err over neurons 65472..{cout - 1}: {err:.3e}")
+    assert err <= TOL
+    assert np.any(y[65535] != 0.0)
