@@ -104,6 +104,16 @@ struct WaveExec {
     // Canvas element ranges read (gather segments, residual rows) and written (output rows),
     // merged and sorted: the host-side independence test of wave groups.
     std::vector<std::pair<uint64_t, uint64_t>> rd, wr;
+    std::vector<std::pair<uint64_t, uint64_t>> xrd, resrd;  // gather segments; residual rows
+    // Element-wise multiplies fused into this wave's gather (whole-plan execution only):
+    // xprod 2 / 3 leaves at element offsets xd relative to the wave's input tensor; rd_fused =
+    // the read ranges of the fused form.
+    uint32_t xprod = 0;
+    int64_t xd[3] = {0, 0, 0};
+    // Whole-plan execution (multiplies folded, operands relocated): output offset and canvas
+    // ranges; equal to y_off / rd / wr unless folding changed them.
+    uint64_t y_off_run = 0;
+    std::vector<std::pair<uint64_t, uint64_t>> rd_run, wr_run;
     size_t part_floats = 0;  // split-K partials (kgroups * cout * tokens), 0 without split-K
     // 2-D spatial wave (VALU over the padded-plane tile layout): tile tables, output plane.
     bool tile2d = false;
@@ -121,7 +131,7 @@ struct WaveExec {
 struct MfmaGroupExec {
     std::vector<size_t> members;  // wave indices, plan order
     uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0;
-    bool dma = false, stream_loads = false;
+    bool dma = false, stream_loads = false, prod = false;
     size_t part_floats = 0;
     DevBuf<k44dev::MfmaTileArgs> args;
     DevBuf<uint32_t> start, epi;
@@ -163,6 +173,7 @@ struct AuxExec {
     uint64_t y_off = 0, src_off = 0, src2_off = 0, state_off = 0;
     uint32_t D = 0, stride = 0, tokens = 0, rf = 0, seq_len = 0, vocab = 0;
     bool decode = false, has_state = false;
+    bool fused = false;  // SWIGLU_MUL_1D folded into its consumers' gathers (not launched)
     float eps = 1e-5f;
     DevBuf<__half> table;  // gamma (RMSNORM), mix (TOKEN_SHIFT), embedding table (EMBED)
     // 2-D spatial commands (S2D, pools, upsample, scatter-upconv): channel count C, planes
@@ -212,6 +223,7 @@ struct K44GpuExecutorState {
     // partials of MFMA waves, per-chunk (value, index) partials of ARGMAX.
     DevBuf<float> scratch;
     size_t scratch_need = 0;  // floats
+    uint64_t fold_elems = 0;  // private region past the canvas for relocated multiply operands
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     hipGraph_t graph = nullptr;
@@ -243,6 +255,7 @@ struct K44GpuExecutorState {
         canvas.reset();
         scratch.reset();
         scratch_need = 0;
+        fold_elems = 0;
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
         if (stream) (void)hipStreamDestroy(stream);
@@ -403,8 +416,25 @@ struct K44GpuExecutorState {
                     rd.push_back({wx.res_off + oj * wx.out_stride,
                                   wx.res_off + oj * wx.out_stride + wx.tokens});
             }
+            Ranges xr;
+            xr.reserve(starts.size());
+            for (uint64_t s0 : starts)
+                xr.push_back({s0, s0 + (uint64_t)(wx.S - 1u) * wx.step + wx.tokens});
+            wx.xrd = merge_ranges(std::move(xr));
+            Ranges rr;
+            if (wx.has_res)
+                for (uint32_t j = 0; j < c.Cout; ++j) {
+                    const uint64_t oj = c.has_cout_map ? (uint64_t)c.h_cout_map[j] : (uint64_t)j;
+                    if (c.has_cout_map && oj == 0xffffu) continue;
+                    rr.push_back({wx.res_off + oj * wx.out_stride,
+                                  wx.res_off + oj * wx.out_stride + wx.tokens});
+                }
+            wx.resrd = merge_ranges(std::move(rr));
             wx.rd = merge_ranges(std::move(rd));
             wx.wr = merge_ranges(std::move(wr));
+            wx.rd_run = wx.rd;
+            wx.wr_run = wx.wr;
+            wx.y_off_run = wx.y_off;
         }
 
         // Distinct substrate positions (compulsory-traffic accounting).
@@ -478,7 +508,9 @@ struct K44GpuExecutorState {
                     // in 16-k-step sub-chunks.  At most 3 sub-chunks per workgroup; waves of
                     // >= 32 tiles split no further (fused epilogue, no second kernel), smaller
                     // ones split into chunks of >= 16 k-steps for parallelism.
-                    want = (ksteps + 47u) / 48u;
+                    const char *ce = std::getenv("K44WAVEC_NARROW_CHUNK");
+                    const uint32_t cmax = ce ? std::max(16, std::atoi(ce)) : 48u;
+                    want = (ksteps + cmax - 1u) / cmax;
                     if (rows < 32u)
                         want = std::max(want, std::min((128u + (uint32_t)rows - 1u) / (uint32_t)rows,
                                                        (ksteps + 15u) / 16u));
@@ -920,14 +952,17 @@ struct K44GpuExecutorState {
                 aux.push_back(std::move(ax));
             }
         }
+        fuse_products();
         form_runs();
         K44_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         K44_HIP(hipEventCreate(&ev0));
         K44_HIP(hipEventCreate(&ev1));
-        canvas.alloc(plan.canvas_elems + kCanvasSlack);
+        canvas.alloc((plan.canvas_elems + kCanvasSlack + 63u) / 64u * 64u + fold_elems);
         if (scratch_need) scratch.alloc(scratch_need);
         upload_mfma_descriptors();
-        K44_HIP(hipMemsetAsync(canvas.p, 0, (plan.canvas_elems + kCanvasSlack) * 2u, stream));
+        K44_HIP(hipMemsetAsync(canvas.p, 0,
+                               ((plan.canvas_elems + kCanvasSlack + 63u) / 64u * 64u + fold_elems) * 2u,
+                               stream));
         if (id_tokens) {
             ids.alloc(id_tokens);
             step_ctr.alloc(1);
@@ -939,6 +974,251 @@ struct K44GpuExecutorState {
         initialized = true;
     }
 
+    // Canvas ranges an aux command reads and writes (the 2-D commands: everything).
+    void aux_ranges(const AuxExec &a, Ranges &rd, Ranges &wr) const {
+        const uint64_t n = (uint64_t)a.D * a.stride;
+        rd.clear();
+        wr.clear();
+        switch (a.type) {
+        case K44CmdType::RMSNORM_1D:
+            rd = {{a.src_off, a.src_off + n}};
+            wr = {{a.y_off, a.y_off + n}};
+            break;
+        case K44CmdType::SWIGLU_MUL_1D:
+            rd = merge_ranges({{a.src_off, a.src_off + n}, {a.src2_off, a.src2_off + n}});
+            wr = {{a.y_off, a.y_off + n}};
+            break;
+        case K44CmdType::TOKEN_SHIFT_1D: {
+            Ranges r = {{a.src_off, a.src_off + n}}, w = {{a.y_off, a.y_off + n}};
+            if (a.has_state) {
+                const uint64_t ns = (uint64_t)a.D * (a.rf - 1u) * 64u;
+                r.push_back({a.state_off, a.state_off + ns});
+                w.push_back({a.state_off, a.state_off + ns});
+            }
+            rd = merge_ranges(std::move(r));
+            wr = merge_ranges(std::move(w));
+            break;
+        }
+        case K44CmdType::EMBED_1D:
+            wr = {{a.y_off, a.y_off + n}};
+            break;
+        case K44CmdType::ARGMAX_1D:
+            rd = {{a.src_off, a.src_off + n}};
+            break;
+        default:
+            rd = wr = {{0u, UINT64_MAX}};
+        }
+    }
+
+    // Element-wise multiplies (SWIGLU_MUL_1D) whose product is read only by narrow MFMA waves
+    // of 64 / 128-neuron tiles are folded into those waves' gathers: the wave loads the
+    // operands' rows and multiplies with the commands' own rounding (y = fp16(a*b); a chain
+    // m = q*(k*v) as fp16(q*fp16(k*v))), so its input and output are bit-identical and two
+    // launches fewer run per chain.  Conditions, from the canvas ranges of the commands in plan
+    // order: the product is not the plan output; every reader until it is overwritten is such a
+    // wave reading it only as gather input (an inner product: exactly one reader, the outer
+    // multiply); every operand stays intact from the first folded multiply through the last
+    // reader — or, when the canvas allocator has reused its range in between (the plan only
+    // needed it until the multiply), the operand is relocated: the MFMA waves that produce it
+    // (the sub-waves of one projection, together covering every row) write it to a private
+    // region past the canvas instead, provided nothing but the folded multiplies reads it.
+    // Whole-plan execution only: execute_range runs every command as compiled.
+    // K44WAVEC_FUSE=0 disables it.
+    void fuse_products() {
+        const char *fe = std::getenv("K44WAVEC_FUSE");
+        if (fe && std::string(fe) == "0") return;
+        const size_t n = ops.size();
+        std::vector<Ranges> rd(n), wr(n);
+        for (size_t i = 0; i < n; ++i) {
+            if (ops[i].first) {
+                rd[i] = waves[ops[i].second]->rd;
+                wr[i] = waves[ops[i].second]->wr;
+            } else {
+                aux_ranges(*aux[ops[i].second], rd[i], wr[i]);
+            }
+        }
+        Ranges out_rng = {{0u, UINT64_MAX}};
+        {
+            auto it = plan_meta.res_map.find(plan_meta.output_res_key);
+            if (it != plan_meta.res_map.end())
+                out_rng = {{plan_meta.output_off,
+                            plan_meta.output_off +
+                                (uint64_t)plan_meta.output_c * it->second.channel_stride}};
+        }
+        typedef std::pair<uint64_t, uint64_t> Rng;
+        auto is_mul = [&](size_t i) {
+            return !ops[i].first && aux[ops[i].second]->type == K44CmdType::SWIGLU_MUL_1D;
+        };
+        auto covers = [](const Ranges &a, const Rng &r) {
+            for (const auto &x : a)
+                if (x.first <= r.first && r.second <= x.second) return true;
+            return false;
+        };
+        auto inside = [](const Ranges &a, const Rng &r) {
+            for (const auto &x : a)
+                if (x.first < r.first || x.second > r.second) return false;
+            return true;
+        };
+        // Readers of the tensor in range R written by op i, up to the first op that writes into
+        // R (the compiler's allocator reuses a range only once its tensor is dead); false if the
+        // tensor is still alive at the end of the plan and overlaps the plan output.
+        auto readers = [&](size_t i, Rng R, std::vector<size_t> &out) {
+            const Ranges rr = {R};
+            for (size_t j = i + 1; j < n; ++j) {
+                if (ranges_overlap(rd[j], rr)) out.push_back(j);
+                if (ranges_overlap(wr[j], rr)) return true;
+            }
+            return !ranges_overlap(rr, out_rng);
+        };
+        auto out_range = [&](size_t i) {
+            const AuxExec &a = *aux[ops[i].second];
+            return Rng(a.y_off, a.y_off + (uint64_t)a.D * a.stride);
+        };
+        auto opnd_range = [&](size_t i, int k) {
+            const AuxExec &a = *aux[ops[i].second];
+            const uint64_t o = k == 0 ? a.src_off : a.src2_off;
+            return Rng(o, o + (uint64_t)a.D * a.stride);
+        };
+        const uint64_t fold_base = (plan_meta.canvas_elems + kCanvasSlack + 63u) / 64u * 64u;
+        const bool dbg = std::getenv("K44WAVEC_FUSE_DEBUG") != nullptr;
+        auto note = [&](size_t i, const char *why) {
+            if (dbg) std::fprintf(stderr, "[fuse] %s: %s\n", aux[ops[i].second]->name.c_str(), why);
+        };
+        for (size_t i = 0; i < n; ++i) {
+            if (!is_mul(i) || aux[ops[i].second]->fused) continue;
+            const auto R = out_range(i);
+            const uint64_t D = aux[ops[i].second]->D, stride = aux[ops[i].second]->stride;
+            std::vector<size_t> rds;
+            if (!readers(i, R, rds) || rds.empty()) {
+                note(i, "product is the plan output or unread");
+                continue;
+            }
+            bool ok = true;
+            for (size_t j : rds) {
+                if (!ops[j].first) {
+                    ok = false;
+                    break;
+                }
+                const WaveExec &w = *waves[ops[j].second];
+                ok = w.mfma && w.narrow && (w.cluster == 64u || w.cluster == 128u) &&
+                     !w.tile2d && !w.xprod;
+                for (const auto &x : w.xrd) ok = ok && R.first <= x.first && x.second <= R.second;
+                // residual rows must not read the product (only the gather is replaced)
+                ok = ok && !ranges_overlap(w.resrd, Ranges{R});
+                if (!ok) break;
+            }
+            if (!ok) {
+                note(i, "a reader is not a narrow 64/128-neuron wave gathering only the product");
+                continue;
+            }
+            // Operands; an operand produced by a multiply read only here is expanded (3 leaves).
+            Rng leaf[3];
+            int nleaf = 2;
+            leaf[0] = opnd_range(i, 0);
+            leaf[1] = opnd_range(i, 1);
+            size_t inner = n;
+            for (int k = 0; k < 2 && inner == n; ++k) {
+                const auto Q = opnd_range(i, k);
+                for (size_t p = i; p-- > 0;) {
+                    if (!ranges_overlap(wr[p], Ranges{Q})) continue;
+                    if (is_mul(p) && !aux[ops[p].second]->fused && out_range(p) == Q) {
+                        std::vector<size_t> r2;
+                        if (readers(p, Q, r2) && r2.size() == 1u && r2[0] == i) {
+                            inner = p;
+                            leaf[0] = opnd_range(i, 1 - k);  // A: the other operand
+                            leaf[1] = opnd_range(p, 0);
+                            leaf[2] = opnd_range(p, 1);
+                            nleaf = 3;
+                        }
+                    }
+                    break;
+                }
+            }
+            const size_t first = inner < n ? inner : i;
+            auto chain_mul = [&](size_t j) { return j == i || j == inner; };
+            // Each operand: intact in place, or relocatable (its producers found and only the
+            // chain's multiplies read it).
+            std::vector<size_t> prods[3];
+            bool move[3] = {false, false, false};
+            for (int k = 0; k < nleaf && ok; ++k) {
+                const Rng L = leaf[k];
+                bool intact = true;
+                for (size_t j = first + 1; j <= rds.back() && intact; ++j)
+                    if (!chain_mul(j)) intact = !ranges_overlap(wr[j], Ranges{L});
+                if (intact) continue;
+                // Producers: MFMA waves writing inside L, back from the chain, until their rows
+                // cover all D rows of L.
+                Ranges cov;
+                bool full = false;
+                for (size_t p = first; p-- > 0 && !full;) {
+                    if (!ranges_overlap(wr[p], Ranges{L})) continue;
+                    if (!ops[p].first) break;
+                    const WaveExec &w = *waves[ops[p].second];
+                    if (!w.mfma || w.tile2d || !inside(w.wr, L)) break;
+                    prods[k].push_back(p);
+                    for (const auto &x : w.wr) cov.push_back(x);
+                    cov = merge_ranges(std::move(cov));
+                    full = true;
+                    for (uint64_t r = 0; r < D && full; ++r)
+                        full = covers(cov, Rng(L.first + r * stride, L.first + r * stride + 1u));
+                }
+                ok = full;
+                if (!ok) {
+                    note(i, "operand overwritten in place and its producers not relocatable");
+                    break;
+                }
+                // Nothing but the producers before the chain and the chain's multiplies after
+                // the last producer reads L while it is alive.
+                const size_t p0 = prods[k].back(), p1 = prods[k].front();
+                for (size_t j = p0; j < first && ok; ++j) {
+                    bool is_prod = false;
+                    for (size_t q : prods[k]) is_prod = is_prod || q == j;
+                    if (!is_prod) ok = !ranges_overlap(rd[j], Ranges{L});
+                }
+                std::vector<size_t> lr;
+                ok = ok && readers(p1, L, lr);
+                for (size_t j : lr) ok = ok && chain_mul(j);
+                if (!ok) note(i, "relocatable operand has other readers");
+                move[k] = true;
+            }
+            if (!ok) continue;
+            note(i, nleaf == 3 ? "folded (3 operands)" : "folded (2 operands)");
+            // Apply: relocate operands, skip the multiplies, point the readers' gathers.
+            uint64_t at[3];
+            for (int k = 0; k < nleaf; ++k) {
+                at[k] = leaf[k].first;
+                if (!move[k]) continue;
+                at[k] = fold_base + fold_elems;
+                fold_elems += D * stride;
+                for (size_t p : prods[k]) {
+                    WaveExec &w = *waves[ops[p].second];
+                    const uint64_t delta = at[k] - leaf[k].first;
+                    w.y_off_run = w.y_off + delta;
+                    Ranges m;
+                    for (const auto &x : w.wr) m.push_back({x.first + delta, x.second + delta});
+                    w.wr_run = merge_ranges(std::move(m));
+                    w.why += "; output relocated for a folded multiply";
+                }
+            }
+            aux[ops[i].second]->fused = true;
+            if (inner < n) aux[ops[inner].second]->fused = true;
+            for (size_t j : rds) {
+                WaveExec &w = *waves[ops[j].second];
+                w.xprod = (uint32_t)nleaf;
+                Ranges fr = w.resrd;
+                for (int k = 0; k < nleaf; ++k) {
+                    w.xd[k] = (int64_t)at[k] - (int64_t)R.first;
+                    for (const auto &x : w.xrd)
+                        fr.push_back({(uint64_t)((int64_t)x.first + w.xd[k]),
+                                      (uint64_t)((int64_t)x.second + w.xd[k])});
+                }
+                w.rd_run = merge_ranges(std::move(fr));
+                w.why += nleaf == 3 ? "; gathers fp16(a*fp16(b*c)) (two multiplies folded)"
+                                    : "; gathers fp16(a*b) (multiply folded)";
+            }
+        }
+    }
+
     // Plan order -> runs: consecutive MFMA waves of one kernel configuration join a group while
     // no member writes what another reads or writes (checked on canvas element ranges).
     void form_runs() {
@@ -948,7 +1228,7 @@ struct K44GpuExecutorState {
         groups.clear();
         for (const auto &op : ops) {
             if (!op.first) {
-                runs.push_back({0, op.second});
+                if (!aux[op.second]->fused) runs.push_back({0, op.second});
                 continue;
             }
             const WaveExec &w = *waves[op.second];
@@ -962,12 +1242,12 @@ struct K44GpuExecutorState {
                 MfmaGroupExec &g = *groups[runs.back().second];
                 bool ok = g.nt == w.cluster && g.mt == w.mt && g.rows == w.rows_per_stage &&
                           g.dma == w.dma && g.stream_loads == w.stream_loads &&
-                          g.members.size() < 64u;
+                          g.prod == (w.xprod != 0u) && g.members.size() < 64u;
                 for (size_t m : g.members) {
                     if (!ok) break;
                     const WaveExec &o = *waves[m];
-                    ok = !ranges_overlap(w.wr, o.rd) && !ranges_overlap(w.rd, o.wr) &&
-                         !ranges_overlap(w.wr, o.wr);
+                    ok = !ranges_overlap(w.wr_run, o.rd_run) && !ranges_overlap(w.rd_run, o.wr_run) &&
+                         !ranges_overlap(w.wr_run, o.wr_run);
                 }
                 if (ok) {
                     g.members.push_back(op.second);
@@ -983,6 +1263,7 @@ struct K44GpuExecutorState {
                 g->rows = w.rows_per_stage;
                 g->dma = w.dma;
                 g->stream_loads = w.stream_loads;
+                g->prod = w.xprod != 0u;
                 g->part_floats = w.part_floats;
                 runs.push_back({2, groups.size()});
                 groups.push_back(std::move(g));
@@ -991,14 +1272,18 @@ struct K44GpuExecutorState {
         for (const auto &g : groups) scratch_need = std::max(scratch_need, g->part_floats);
     }
 
-    k44dev::MfmaTileArgs mfma_args(const WaveExec &w, float *part) const {
+    k44dev::MfmaTileArgs mfma_args(const WaveExec &w, float *part, bool fused) const {
         k44dev::MfmaTileArgs a{};
+        if (fused && w.xprod) {
+            a.xprod = w.xprod;
+            for (int i = 0; i < 3; ++i) a.xd[i] = w.xd[i];
+        }
         a.X = canvas.p;
         a.seg = w.seg.p;
         a.Wf = w.w.p;
         a.bias = w.bias.p;
         a.cmap = w.cmap.p;
-        a.Y = canvas.p + w.y_off;
+        a.Y = canvas.p + (fused ? w.y_off_run : w.y_off);
         a.R = w.has_res ? canvas.p + w.res_off : nullptr;
         a.step = w.step;
         a.K = w.K;
@@ -1031,7 +1316,7 @@ struct K44GpuExecutorState {
             if (!w.mfma) continue;
             w.items = w.rows * (w.narrow ? 1u : w.tokens / w.mt) * w.kgroups;
             w.epi_items = epi_workgroups(w);
-            w.one_args.upload({mfma_args(w, scratch.p)});
+            w.one_args.upload({mfma_args(w, scratch.p, false)});
             w.one_start.upload({0u, w.items});
             w.one_epi.upload({0u, w.epi_items});
         }
@@ -1042,7 +1327,7 @@ struct K44GpuExecutorState {
             size_t off = 0;
             for (size_t m : g.members) {
                 const WaveExec &w = *waves[m];
-                args.push_back(mfma_args(w, scratch.p ? scratch.p + off : nullptr));
+                args.push_back(mfma_args(w, scratch.p ? scratch.p + off : nullptr, true));
                 off += w.part_floats;
                 start.push_back(start.back() + w.items);
                 epi.push_back(epi.back() + w.epi_items);
@@ -1081,6 +1366,7 @@ struct K44GpuExecutorState {
               << ", \"tokens_per_lane\": " << (w.mfma ? 0 : (w.lane8 ? 8 : 4))
               << ", \"stream_loads\": " << (w.stream_loads ? "true" : "false")
               << ", \"stream_kernel\": " << (w.stream_kernel ? "true" : "false")
+              << ", \"xprod\": " << w.xprod
               << ", \"flops\": " << (long long)w.flops
               << ", \"effective_flops\": " << (long long)w.eff_flops
               << ", \"mapped\": " << (w.cmap.p ? "true" : "false")
@@ -1091,6 +1377,7 @@ struct K44GpuExecutorState {
         for (size_t i = 0; i < aux.size(); ++i)
             o << (i ? ", " : "") << "{\"name\": \"" << aux[i]->name << "\", \"type\": \""
               << cmd_type_str(aux[i]->type) << "\", \"channels\": " << aux[i]->D
+              << ", \"fused\": " << (aux[i]->fused ? "true" : "false")
               << ", \"tokens\": " << aux[i]->tokens << "}";
         o << "], \"groups\": [";
         for (size_t i = 0; i < groups.size(); ++i) {
@@ -1106,9 +1393,10 @@ struct K44GpuExecutorState {
     }
 
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
-                           uint32_t items, uint32_t epi_items, bool dma, bool stream_loads) {
+                           uint32_t items, uint32_t epi_items, bool dma, bool stream_loads,
+                           bool prod) {
         if (mt == 16u)  // narrow (<= 16 tokens)
-            K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream));
+            K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream, prod));
         else if (dma)
             K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream, stream_loads));
         else
@@ -1119,12 +1407,13 @@ struct K44GpuExecutorState {
     void launch_mfma(const WaveExec &w) {
         const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, w.one_epi.p, 1u};
         launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
-                          w.stream_loads);
+                          w.stream_loads, false);
     }
 
     void launch_group(const MfmaGroupExec &g) {
         const k44dev::MfmaGroup d{g.args.p, g.start.p, g.epi.p, (uint32_t)g.members.size()};
-        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.stream_loads);
+        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.stream_loads,
+                          g.prod);
     }
 
     void launch_wave(const WaveExec &w) {

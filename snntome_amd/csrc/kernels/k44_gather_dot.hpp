@@ -354,7 +354,6 @@ __global__ __launch_bounds__(256) void k44_gather_dot8_kernel(GatherDotArgs a) {
 template <int NPW, int WAVES, bool NTX>
 __global__ __launch_bounds__(WAVES * 64) void k44_gather_stream_kernel(GatherDotArgs a) {
     constexpr int U = 16;
-    constexpr int PER = NPW / WAVES;  // neuron slots per wave
     static_assert(NPW % WAVES == 0, "whole neuron slots per wave");
     __shared__ gd_u2 orow[NPW][64];
     const int lane = (int)(threadIdx.x & 63u);

@@ -34,8 +34,10 @@ hipError_t launch_mfma_dma(const MfmaGroup &g, uint32_t nt, uint32_t items, hipS
                            bool stream_loads = false);
 
 // Narrow MFMA kernel (waves of at most 16 tokens) over a group: `items` workgroups (tiles x
-// contraction chunks per wave); nt in {16,32,64,128}.
-hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream);
+// contraction chunks per wave); nt in {16,32,64,128}.  prod: the waves gather element-wise
+// products (MfmaTileArgs::xprod; nt 64 / 128 only).
+hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream,
+                              bool prod = false);
 
 // Split-K second pass over the same group: `epi_items` workgroups (the group's epi_start[n]);
 // each wave with kgroups > 1 sums its fp32 partials in z order and runs the epilogue.

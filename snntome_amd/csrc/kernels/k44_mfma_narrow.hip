@@ -186,7 +186,9 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
 // is replaced by its counterpart of s+1 (the weights stream without a gap).  A chunk that
 // covers the whole contraction runs the fused epilogue: waves of up to a few sub-chunks need no
 // split-K partials and no second kernel.
-template <int NT>
+// PROD: the launch's waves gather element-wise products (a.xprod 2 / 3); without it the
+// product registers are not allocated.
+template <int NT, bool PROD>
 __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp) {
     constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16;
     static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
@@ -216,8 +218,11 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
     // X rows of sub-chunk s: wave pass q covers 32 rows starting at a multiple of 32 (one
     // segment, S % 32 == 0: wave-uniform start); passes past the sub-chunk re-read its last
     // 32 rows (fixed load count).
+    // Product gathers (a.xprod = 2 / 3) load the same row chunk of two / three tensors and
+    // multiply with the rounding of the unfused multiply commands: fp16(A*B), fp16(A*fp16(B*C)).
     constexpr int XQ = NARROW_MAX_ROWS * 2 / 256;
-    auto gather = [&](uint32_t s, u4_t (&xv)[XQ]) {
+    const uint32_t xprod = PROD ? a.xprod : 0u;
+    auto gather = [&](uint32_t s, u4_t (&xv)[XQ], u4_t (&xb)[XQ], u4_t (&xc)[XQ]) {
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
         uint64_t sb[XQ];
@@ -225,16 +230,44 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
         for (int q = 0; q < XQ; ++q) {
             const uint32_t r = kb * 32u + min((uint32_t)(32 * (wave + 4 * q)), nrows - 32u);
             const uint32_t k = r / a.S;
-            sb[q] = segr[k] + (uint64_t)(r - k * a.S) * a.step;
+            sb[q] = segr[k] + (uint64_t)(r - k * a.S) * a.step + (uint64_t)(lane >> 1) * a.step +
+                    (uint32_t)(lane & 1) * 8u;
         }
+        if (xprod == 0u) {
 #pragma unroll
-        for (int q = 0; q < XQ; ++q)
-            xv[q] = *(gu4_t *)(a.X + sb[q] + (uint64_t)(lane >> 1) * a.step +
-                               (uint32_t)(lane & 1) * 8u);
+            for (int q = 0; q < XQ; ++q) xv[q] = *(gu4_t *)(a.X + sb[q]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < XQ; ++q) {
+                xv[q] = *(gu4_t *)(a.X + (int64_t)sb[q] + a.xd[0]);
+                xb[q] = *(gu4_t *)(a.X + (int64_t)sb[q] + a.xd[1]);
+            }
+            if (xprod == 3u) {
+#pragma unroll
+                for (int q = 0; q < XQ; ++q) xc[q] = *(gu4_t *)(a.X + (int64_t)sb[q] + a.xd[2]);
+            }
+        }
     };
-    auto store = [&](uint32_t s, int buf, const u4_t (&xv)[XQ]) {
+    auto store = [&](uint32_t s, int buf, u4_t (&xv)[XQ], const u4_t (&xb)[XQ],
+                     const u4_t (&xc)[XQ]) {
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
+        if (xprod != 0u) {
+#pragma unroll
+            for (int q = 0; q < XQ; ++q) {
+                __half *ha = reinterpret_cast<__half *>(&xv[q]);
+                const __half *hb = reinterpret_cast<const __half *>(&xb[q]);
+                const __half *hc = reinterpret_cast<const __half *>(&xc[q]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float bc = xprod == 3u
+                                         ? __half2float(__float2half_rn(__half2float(hb[e]) *
+                                                                        __half2float(hc[e])))
+                                         : __half2float(hb[e]);
+                    ha[e] = __float2half_rn(__half2float(ha[e]) * bc);
+                }
+            }
+        }
 #pragma unroll
         for (int q = 0; q < XQ; ++q) {
             const uint32_t rb = (uint32_t)(32 * (wave + 4 * q));
@@ -247,9 +280,9 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
     h8_t af[SUBK][BPW];
 #pragma unroll
     for (int u = 0; u < SUBK; ++u) load_a(min(ks_begin + (uint32_t)u, ks_end - 1u), af[u]);
-    u4_t xv[XQ];
-    gather(0u, xv);
-    store(0u, 0, xv);
+    u4_t xv[XQ], xb[XQ], xc[XQ];
+    gather(0u, xv, xb, xc);
+    store(0u, 0, xv, xb, xc);
     __syncthreads();
 
     const int g = lane >> 4;
@@ -262,7 +295,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
     for (uint32_t s = 0; s < nsub; ++s) {
         const int buf = (int)(s & 1u);
         const bool more = s + 1u < nsub;
-        if (more) gather(s + 1u, xv);
+        if (more) gather(s + 1u, xv, xb, xc);
         const uint32_t kb = ks_begin + s * SUBK;
 #pragma unroll
         for (int u = 0; u < SUBK; ++u) {
@@ -279,7 +312,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
             load_a(min(k2 + (uint32_t)SUBK, ks_end - 1u), af[u]);  // next sub-chunk's fragment
         }
         if (more) {
-            store(s + 1u, buf ^ 1, xv);
+            store(s + 1u, buf ^ 1, xv, xb, xc);
             __syncthreads();
         }
     }
@@ -316,14 +349,25 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
 }
 
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
-                              hipStream_t stream) {
+                              hipStream_t stream, bool prod) {
+    if (prod && nt != 64u && nt != 128u) return hipErrorInvalidValue;
     if (items == 0u) return hipSuccess;
     const dim3 grid(items), block(256);
     switch (nt) {
     case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, g); break;
     case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, g); break;
-    case 64u: hipLaunchKernelGGL(k44_mfma_narrow_long_kernel<64>, grid, block, 0, stream, g); break;
-    case 128u: hipLaunchKernelGGL(k44_mfma_narrow_long_kernel<128>, grid, block, 0, stream, g); break;
+    case 64u:
+        if (prod)
+            hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<64, true>), grid, block, 0, stream, g);
+        else
+            hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<64, false>), grid, block, 0, stream, g);
+        break;
+    case 128u:
+        if (prod)
+            hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<128, true>), grid, block, 0, stream, g);
+        else
+            hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<128, false>), grid, block, 0, stream, g);
+        break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -66,6 +66,11 @@ struct MfmaTileArgs {
     uint32_t tokens;  // tokens of the wave (partial row length)
     // Work items of the wave: tiles x token tiles x split-K groups (tile index fastest).
     uint32_t tiles, ttiles, kgroups;
+    // Product gather (element-wise multiplies fused into the X gather; narrow kernels of 64 /
+    // 128-neuron tiles only): xprod 0 = the X rows as they are; 2 = fp16(A*B); 3 =
+    // fp16(A*fp16(B*C)), A / B / C the rows at (segment offset + xd[0] / xd[1] / xd[2]).
+    uint32_t xprod;
+    int64_t xd[3];
 };
 
 // A launch covers a group of independent waves of one kernel configuration (the sub-waves of a

@@ -356,3 +356,48 @@ def test_grouped_launches_match_per_wave(wavec, monkeypatch, decode):
         out[mode + "_ids"] = plan.get_ids(n)
     assert np.array_equal(out["grouped"], out["alone"])
     assert np.array_equal(out["grouped_ids"], out["alone_ids"])
+
+
+def test_folded_multiplies_match_unfolded(wavec, monkeypatch):
+    """Decode plans fold the element-wise multiplies (k*v, q*(k*v), g*u) into the gathers of the
+    narrow MFMA waves that read the products; ids and logits of several decode steps are
+    bit-identical to the plan that launches every multiply (K44WAVEC_FUSE=0)."""
+    spec = TINY
+    steps = 4
+    wts = synth.llm_weights(spec)
+    pre = synth.build_llm_graph(spec, wts, decode=False, wavec_mod=wavec).compile()
+    pre.init_gpu()
+    plans = {}
+    for mode in ("folded", "launched"):
+        if mode == "launched":
+            monkeypatch.setenv("K44WAVEC_FUSE", "0")
+        else:
+            monkeypatch.delenv("K44WAVEC_FUSE", raising=False)
+        p = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
+        p.init_gpu()
+        plans[mode] = p
+    rep = plans["folded"].exec_report()
+    fused = [a for a in rep["aux"] if a["fused"]]
+    prods = sorted({w["xprod"] for w in rep["waves"]})
+    _log(f"[fold] {len(fused)} multiplies folded, xprod kinds {prods}, "
+         f"{rep['launches_per_run']} vs {plans['launched'].exec_report()['launches_per_run']} "
+         "launches per run")
+    assert len(fused) == 3 * spec.layers and prods == [0, 2, 3]
+    assert not any(a["fused"] for a in plans["launched"].exec_report()["aux"])
+    R = spec.requests
+    pre.set_ids(np.random.default_rng(5).integers(0, spec.vocab, R * spec.prompt))
+    pre.execute(1)
+    head = next(c for c in pre.cmds if c["name"].split("/")[0] == "head")
+    out = {}
+    for mode, p in plans.items():
+        synth.llm_handoff(spec, pre, p)
+        hd = next(c for c in p.cmds if c["name"].split("/")[0] == "head")
+        ids, logits = [], []
+        for _ in range(steps):
+            p.execute(1)
+            ids.append(p.get_ids(R))
+            logits.append(p.read_canvas(int(hd["y_off"]), spec.vocab * 64))
+        out[mode] = (np.stack(ids), np.stack(logits))
+    assert head is not None
+    assert np.array_equal(out["folded"][0], out["launched"][0])
+    assert np.array_equal(out["folded"][1], out["launched"][1])
