@@ -505,15 +505,16 @@ struct K44GpuExecutorState {
                 uint32_t want;
                 if (cl >= 64u) {
                     // Tiles of whole 16-neuron blocks per wave: chunks of any length, streamed
-                    // in 16-k-step sub-chunks.  At most 3 sub-chunks per workgroup; waves of
-                    // >= 32 tiles split no further (fused epilogue, no second kernel), smaller
-                    // ones split into chunks of >= 16 k-steps for parallelism.
+                    // in 16-k-step sub-chunks.  Chunks of at most 48 k-steps; split further, down
+                    // to 16 k-steps, until the wave has ~128 workgroups.  Measured on config-5
+                    // decode (per step): 1.196 ms, against 1.219 ms when waves of >= 32 tiles
+                    // stay unsplit (fused epilogue), 1.28 ms with 8-k-step chunks, 1.46 ms
+                    // without split.
                     const char *ce = std::getenv("K44WAVEC_NARROW_CHUNK");
                     const uint32_t cmax = ce ? std::max(16, std::atoi(ce)) : 48u;
                     want = (ksteps + cmax - 1u) / cmax;
-                    if (rows < 32u)
-                        want = std::max(want, std::min((128u + (uint32_t)rows - 1u) / (uint32_t)rows,
-                                                       (ksteps + 15u) / 16u));
+                    want = std::max(want, std::min((128u + (uint32_t)rows - 1u) / (uint32_t)rows,
+                                                   (ksteps + 15u) / 16u));
                 } else {
                     // Chunks of 8..16 k-steps (<= 512 rows in LDS), ~256 workgroups per wave.
                     want = (256u + (uint32_t)rows - 1u) / (uint32_t)rows;
@@ -1269,7 +1270,42 @@ struct K44GpuExecutorState {
                 groups.push_back(std::move(g));
             }
         }
+        // Split-K is chosen per wave for parallelism; a group launch has the workgroups of all
+        // its members, so a wide-token group that fills the GPU without splitting (>= 256
+        // workgroups) runs unsplit: no partial planes, no epilogue kernel (config-5 prefill
+        // 29.0 -> 27.0 ms).  Decode groups keep their split: measured 1.22 ms per step against
+        // 1.46 ms unsplit — at 16 tokens the extra workgroups stream weights faster than the
+        // epilogue costs.
+        const char *gs = std::getenv("K44WAVEC_GROUP_SPLIT");
+        if (!(gs && std::string(gs) == "0")) {
+            for (auto &gp : groups) {
+                MfmaGroupExec &g = *gp;
+                if (g.mt == 16u) continue;
+                uint64_t base = 0;
+                for (size_t m : g.members) {
+                    const WaveExec &w = *waves[m];
+                    base += (uint64_t)w.rows * (w.tokens / w.mt);
+                }
+                if (base < 256u) continue;
+                g.part_floats = 0;
+                for (size_t m : g.members) {
+                    WaveExec &w = *waves[m];
+                    set_split(w, 1u);
+                    g.part_floats += w.part_floats;
+                }
+            }
+        }
         for (const auto &g : groups) scratch_need = std::max(scratch_need, g->part_floats);
+    }
+
+    // Contraction split of an MFMA wave into `want` chunks (k-steps for the narrow kernels,
+    // stages of rows_per_stage positions otherwise).
+    static void set_split(WaveExec &w, uint32_t want) {
+        const uint32_t units = w.narrow ? w.ksteps : w.K * w.S / w.rows_per_stage;
+        want = std::max(1u, std::min(want, units));
+        w.stage_chunk = (units + want - 1u) / want;
+        w.kgroups = (units + w.stage_chunk - 1u) / w.stage_chunk;
+        w.part_floats = w.kgroups > 1u ? (size_t)w.kgroups * w.cout * w.part_tokens : 0u;
     }
 
     k44dev::MfmaTileArgs mfma_args(const WaveExec &w, float *part, bool fused) const {

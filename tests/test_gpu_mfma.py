@@ -204,12 +204,12 @@ def test_dma_ring_matches_register_staged(wavec, orc, monkeypatch, nt, S, K, til
 
 @pytest.mark.parametrize("K,tokens", [(3, 16), (7, 16), (7, 9), (2, 1)])
 def test_narrow_long_chunks_many_tiles(wavec, orc, monkeypatch, K, tokens):
-    """Waves of >= 32 64-neuron tiles over <= 16 tokens: contraction chunks of several 16-k-step
+    """Waves of >= 128 64-neuron tiles over <= 16 tokens: contraction chunks of several 16-k-step
     sub-chunks through two LDS buffers, fused epilogue when one chunk covers the contraction
     (K = 2, 3: 32 / 48 k-steps), split-K partials plus the epilogue kernel otherwise (K = 7:
     112 k-steps); within tolerance of the oracle and of the wide kernel."""
     rng = np.random.default_rng(K * 100 + tokens)
-    S, nt, tiles, C = 512, 64, 40, 8192
+    S, nt, tiles, C = 512, 64, 130, 16384  # residual rows: cout <= C
     starts = (rng.integers(0, C // S, size=(tiles, K)) * S).astype(np.uint32)
     cout = tiles * nt
     w = synth.normal_f16(rng, (cout, K * S), 0.02)
