@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256 * NBK) void k44_token64_ring_kernel(Token64Args
     constexpr int D = XR + 1;              // direct loads per wave per stage
     __shared__ __attribute__((aligned(16))) char xr[NBUF][TW][XST];
     __shared__ __attribute__((aligned(16))) char wr[NBUF][WST];
-    __shared__ uint32_t ix[T64R_IDX_MAX];
+    extern __shared__ uint32_t ix[];  // B entries (dynamic: sized by the launch)
 
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -272,12 +272,14 @@ hipError_t launch_token64(const Token64Args &a, hipStream_t stream) {
     if (token64_ring_ok(a) && !(env && env[0] == '0')) {
         // Two 64-neuron blocks sharing every gathered row: half the row traffic but half the
         // workgroups; measured equal at 128-neuron clusters, slightly faster from 256 on.
+        const size_t ix_bytes = (size_t)a.B_vec16 * 16u * 4u;
         if (a.cluster % 256u == 0u && !(env && env[0] == '1')) {
             const dim3 grid(a.Cout / 128u, a.tiles / 4u, 1u), block(512u, 1u, 1u);
-            hipLaunchKernelGGL((k44_token64_ring_kernel<2, 6>), grid, block, 0, stream, a);
+            hipLaunchKernelGGL((k44_token64_ring_kernel<2, 6>), grid, block, ix_bytes, stream, a);
         } else {
+            // (A 3-stage ring, two workgroups per CU, measured 3 % slower at the whitepaper shape.)
             const dim3 grid(a.Cout / 64u, a.tiles / 4u, 1u), block(256u, 1u, 1u);
-            hipLaunchKernelGGL((k44_token64_ring_kernel<1, 4>), grid, block, 0, stream, a);
+            hipLaunchKernelGGL((k44_token64_ring_kernel<1, 4>), grid, block, ix_bytes, stream, a);
         }
         return hipGetLastError();
     }
