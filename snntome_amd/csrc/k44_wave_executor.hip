@@ -18,7 +18,10 @@
 //    readable through wavec_last_error().
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
+#include <cstdio>
+#include <cstdlib>
 #include <memory>
 #include <mutex>
 #include <numeric>

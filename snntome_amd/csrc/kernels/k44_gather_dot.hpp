@@ -51,6 +51,9 @@ enum : int { ACT_NONE = 0, ACT_RELU = 1, ACT_SIGMOID = 2, ACT_SILU = 3, ACT_LEAK
 // wave is an ordinary output channel.
 constexpr uint64_t K44_CMAP_EMPTY = 0xffffu;
 
+// Largest per-neuron weight block (halves) the gather kernels stage in LDS.
+constexpr uint32_t GD_WL_MAX = 2048;
+
 __device__ __forceinline__ float apply_act(float v, int act) {
     switch (act) {
     case ACT_RELU: return fmaxf(v, 0.0f);
@@ -252,14 +255,32 @@ __device__ __forceinline__ void fma8(float (&acc)[8], float w, gd_u4 x) {
     }
 }
 
-template <int SLAB, int KSPLIT, bool NTX>
+// WL: the neuron's weights (K * n_batch * 16 <= GD_WL_MAX halves) are staged in LDS first, so no
+// batch waits on a weight load from HBM (they are read once, never cache resident): cache-
+// resident substrates (configs 1, 4) otherwise pay an HBM round trip per 16-row batch.
+
+template <int SLAB, int KSPLIT, bool NTX, bool WL>
 __global__ __launch_bounds__(256) void k44_gather_dot8_kernel(GatherDotArgs a) {
     constexpr int LPR = SLAB / 8;  // lanes per position row
     constexpr int RPI = 64 / LPR;  // rows per load instruction
     constexpr int U = 16 / RPI;    // loads in flight per lane (16 rows per batch)
+    constexpr int NWL = WL ? (KSPLIT == 1 ? 4 : 1) : 0;
+    __shared__ __attribute__((aligned(16))) __half wlds[NWL ? NWL : 1][NWL ? GD_WL_MAX : 8];
     const int lane = (int)(threadIdx.x & 63u);
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t j = KSPLIT == 1 ? blockIdx.x * 4u + (uint32_t)wave : blockIdx.x;
+    const uint64_t batches = (uint64_t)a.K * a.n_batch;
+    if constexpr (WL) {
+        // copy [batches][16] halves of this wave's (KSPLIT 1) / the workgroup's neuron
+        const uint32_t n16 = (uint32_t)batches * 2u;  // 16-byte chunks
+        const uint32_t jj = j < a.cout ? j : a.cout - 1u;
+        const gd_u4 *src = reinterpret_cast<const gd_u4 *>(a.W + (uint64_t)jj * batches * 16u);
+        gd_u4 *dst = reinterpret_cast<gd_u4 *>(&wlds[KSPLIT == 1 ? wave : 0][0]);
+        const uint32_t t0 = KSPLIT == 1 ? (uint32_t)lane : threadIdx.x;
+        const uint32_t tn = KSPLIT == 1 ? 64u : 256u;
+        for (uint32_t q = t0; q < n16; q += tn) dst[q] = ld_once<NTX>(src + q);
+        __syncthreads();
+    }
     if (j >= a.cout) return;
     const int g = lane / LPR, c = lane % LPR;
     const uint32_t slab0 = blockIdx.y * (uint32_t)SLAB;
@@ -267,8 +288,8 @@ __global__ __launch_bounds__(256) void k44_gather_dot8_kernel(GatherDotArgs a) {
     const uint32_t cmap_w = scalar_word16(a.cmap, a.W, j);
 
     const kconst_u64 *seg = (const kconst_u64 *)a.seg + (uint64_t)(j / a.cluster) * a.K;
-    const uint64_t batches = (uint64_t)a.K * a.n_batch;
-    const __half *wl = a.W + (uint64_t)j * batches * 16u + g * U;
+    const __half *wl = WL ? &wlds[KSPLIT == 1 ? wave : 0][g * U]
+                          : a.W + (uint64_t)j * batches * 16u + g * U;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 
     for (uint32_t k = KSPLIT == 1 ? 0u : (uint32_t)wave; k < a.K; k += KSPLIT) {
@@ -289,7 +310,13 @@ __global__ __launch_bounds__(256) void k44_gather_dot8_kernel(GatherDotArgs a) {
                 }
             }
             float w[U];
-            load_weights<U, NTX>(w, wl + ((uint64_t)k * a.n_batch + b) * 16u);
+            if constexpr (WL) {
+                const __half *wp = wl + ((uint64_t)k * a.n_batch + b) * 16u;
+#pragma unroll
+                for (int u = 0; u < U; ++u) w[u] = __half2float(wp[u]);
+            } else {
+                load_weights<U, NTX>(w, wl + ((uint64_t)k * a.n_batch + b) * 16u);
+            }
 #pragma unroll
             for (int u = 0; u < U; ++u) fma8(acc, w[u], x[u]);
         }

@@ -1,4 +1,6 @@
 // Translation unit of the VALU kernels (gather-dot, substrate fill) and their launchers.
+#include <cstdlib>
+
 #include "k44_launch.hpp"
 
 namespace k44dev {
@@ -27,11 +29,16 @@ static hipError_t launch_gather_dot_policy(const GatherDotArgs &a, uint32_t slab
     const dim3 grid(ksplit == 4u ? a.cout : (a.cout + 3u) / 4u, tokens / slab, 1u);
     const dim3 block(256u, 1u, 1u);
     if (lane8) {
-#define K44_GD8(SLAB)                                                                           \
-    if (ksplit == 4u)                                                                           \
-        hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 4, NTX>), grid, block, 0, stream, a);  \
-    else                                                                                        \
-        hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 1, NTX>), grid, block, 0, stream, a);
+        const char *wle = std::getenv("K44WAVEC_WLDS");
+        const bool wl = (uint64_t)a.K * a.n_batch * 16u <= GD_WL_MAX && !(wle && wle[0] == '0');
+#define K44_GD8(SLAB)                                                                                \
+    if (ksplit == 4u) {                                                                              \
+        if (wl) hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 4, NTX, true>), grid, block, 0, stream, a);  \
+        else hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 4, NTX, false>), grid, block, 0, stream, a);    \
+    } else {                                                                                         \
+        if (wl) hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 1, NTX, true>), grid, block, 0, stream, a);  \
+        else hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 1, NTX, false>), grid, block, 0, stream, a);    \
+    }
         switch (slab) {
         case 256u: K44_GD8(256) break;
         case 128u: K44_GD8(128) break;

@@ -271,3 +271,26 @@ def test_neuron_65535_without_cout_map(wavec, orc, monkeypatch, path, cluster):
     _log(f"[65535 {path}] rel err over neurons 65472..{cout - 1}: {err:.3e}")
     assert err <= TOL
     assert np.any(y[65535] != 0.0)
+
+
+@pytest.mark.parametrize("tokens,K,S", [(128, 16, 128), (64, 8, 64), (256, 3, 40), (100, 12, 24)])
+def test_weights_staged_in_lds_bit_identical(wavec, orc, monkeypatch, tokens, K, S):
+    """The 8-token-per-lane gather kernel stages each neuron's weights in LDS before its gathers
+    (K44WAVEC_WLDS=0 reads them from memory per batch): same values, same FMA order, so the
+    outputs are bit-identical; one neuron per wave (K > 8) and four waves per neuron (K <= 8)."""
+    monkeypatch.setenv("K44WAVEC_LANE8", "1")
+    rng = np.random.default_rng(tokens + K * 3 + S)
+    C, cout = 5000, 96
+    starts = (rng.integers(0, (C - S) // 8, size=(cout, K)) * 8).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.1)
+    ys = {}
+    for mode in ("lds", "memory"):
+        monkeypatch.setenv("K44WAVEC_WLDS", "1" if mode == "lds" else "0")
+        y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
+                                       rows=cluster_rows(starts, S), weights=w, bias=b,
+                                       act="silu", residual=True, seed=23)
+        assert plan.exec_report()["waves"][0]["tokens_per_lane"] == 8
+        assert orc.rel_err(y, ref) <= TOL
+        ys[mode] = y
+    assert np.array_equal(ys["lds"], ys["memory"])
