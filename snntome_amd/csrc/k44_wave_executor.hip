@@ -585,8 +585,11 @@ struct K44GpuExecutorState {
                 wx.lane8 = want8 && ok8;
                 wx.stream_loads = streaming_gather(wx);
             }
+            // Four waves per neuron (segments round-robin) for few-segment neurons gathering from
+            // HBM; one wave per neuron when the rows are cache resident (8 tokens per lane,
+            // weights in LDS): config 1 19.2 us against 23.2 us with four.
             const char *ks_env = std::getenv("K44WAVEC_KSPLIT");
-            wx.ksplit = (wx.K >= 2u && wx.K <= 8u) ? 4u : 1u;
+            wx.ksplit = (!wx.lane8 && wx.K >= 2u && wx.K <= 8u) ? 4u : 1u;
             if (ks_env) wx.ksplit = std::string(ks_env) == "4" ? 4u : 1u;
             {
                 // Streaming gathers over 256-token slabs with >= 256 workgroups of 256 neurons:
