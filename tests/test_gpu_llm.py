@@ -401,3 +401,35 @@ def test_folded_multiplies_match_unfolded(wavec, monkeypatch):
     assert head is not None
     assert np.array_equal(out["folded"][0], out["launched"][0])
     assert np.array_equal(out["folded"][1], out["launched"][1])
+
+
+def test_decode_step_full_width_against_oracle(wavec):
+    """One decode step of the config-5 decoder at its real widths (d 2048, FFN 5632, vocab
+    32,000, 16 requests; 2 of the 16 layers, zero token-shift history): folded multiplies,
+    relocated operands, split-K chunking, union tiles of up to 11 clusters and the 500-tile
+    head, against the fp64-accumulating oracle end to end."""
+    spec = synth.LLMSpec(layers=2)
+    wts = synth.llm_weights(spec)
+    dec = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
+    dec.init_gpu()
+    rep = dec.exec_report()
+    _log(f"[decode full width] {len(rep['waves'])} waves, "
+         f"{sum(a['fused'] for a in rep['aux'])} multiplies folded, "
+         f"{rep['launches_per_run']} launches per step")
+    assert sum(a["fused"] for a in rep["aux"]) == 3 * spec.layers
+    R = spec.requests
+    ids = np.random.default_rng(11).integers(0, spec.vocab, R).astype(np.uint32)
+    dec.set_ids(ids)
+    dec.execute(1)
+    head = next(c for c in dec.cmds if c["name"].split("/")[0] == "head")
+    logits = _read(dec, head["y_off"], head["logical_Cout"], 64)[:, :R].astype(np.float64)
+    zero = [np.zeros((spec.d, spec.rf - 1, 64), np.float16) for _ in range(spec.layers)]
+    ref = lo.llm_forward(spec, wts, ids, decode=True, shift_state=zero)
+    want = ref.tensors["logits"][:, :R].astype(np.float64)
+    scale = np.abs(want).max()
+    err = np.abs(logits - want).max() / scale
+    _log(f"[decode full width] max|d| / max|logit| = {err:.3e} (max|logit| {scale:.2f})")
+    assert err <= E2E_TOL
+    srt = np.sort(want, axis=0)
+    clear = (srt[-1] - srt[-2]) > 0.05
+    assert np.array_equal(dec.get_ids(R)[clear], ref.ids[clear])
