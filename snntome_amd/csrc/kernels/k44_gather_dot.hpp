@@ -408,8 +408,13 @@ __global__ __launch_bounds__(WAVES * 64) void k44_gather_stream_kernel(GatherDot
             }
         }
     };
-    auto issue = [&](const Cursor &c, gd_u2 (&x)[U]) {
+    // issue(): the step's rows and its 16 weights (scalar loads), one step ahead of consume().
+    auto issue = [&](const Cursor &c, gd_u2 (&x)[U], uint32_t (&wv)[U / 2]) {
         const uint32_t j = j0 + (uint32_t)wave + c.i * WAVES;
+        const kconst_u32 *ww =
+            (const kconst_u32 *)(a.W + (((uint64_t)j * a.K + c.k) * a.n_batch + c.b) * U);
+#pragma unroll
+        for (int u = 0; u < U / 2; ++u) wv[u] = ww[u];
         const kconst_u64 *seg = (const kconst_u64 *)a.seg + (uint64_t)(j / a.cluster) * a.K;
         const char *xseg = reinterpret_cast<const char *>(a.X + seg[c.k] + slab0);
         const uint32_t s0 = c.b * (uint32_t)U;
@@ -429,12 +434,11 @@ __global__ __launch_bounds__(WAVES * 64) void k44_gather_stream_kernel(GatherDot
         }
     };
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto consume = [&](const Cursor &c, const gd_u2 (&x)[U]) {
+    auto consume = [&](const Cursor &c, const gd_u2 (&x)[U], const uint32_t (&wv)[U / 2]) {
         const uint32_t j = j0 + (uint32_t)wave + c.i * WAVES;
-        const kconst_u32 *ww = (const kconst_u32 *)(a.W + (((uint64_t)j * a.K + c.k) * a.n_batch + c.b) * U);
 #pragma unroll
         for (int u = 0; u < U; u += 2) {
-            const uint32_t pair = ww[u / 2];
+            const uint32_t pair = wv[u / 2];
             const float2 wf = __half22float2(*reinterpret_cast<const __half2 *>(&pair));
             fma4(acc, wf.x, make_uint2(x[u].x, x[u].y));
             fma4(acc, wf.y, make_uint2(x[u + 1].x, x[u + 1].y));
@@ -454,18 +458,19 @@ __global__ __launch_bounds__(WAVES * 64) void k44_gather_stream_kernel(GatherDot
     };
 
     gd_u2 xa[U], xb[U];
+    uint32_t wa[U / 2], wb[U / 2];
     Cursor ca{0u, 0u, 0u};
-    if (total) issue(ca, xa);
+    if (total) issue(ca, xa, wa);
     for (uint32_t t = 0; t < total; t += 2) {
         Cursor cb = ca;
         advance(cb);
-        if (t + 1u < total) issue(cb, xb);
-        consume(ca, xa);
+        if (t + 1u < total) issue(cb, xb, wb);
+        consume(ca, xa, wa);
         if (t + 1u >= total) break;
         ca = cb;
         advance(ca);
-        if (t + 2u < total) issue(ca, xa);
-        consume(cb, xb);
+        if (t + 2u < total) issue(ca, xa, wa);
+        consume(cb, xb, wb);
     }
     __syncthreads();
     // Burst write of the finished rows: wave w writes rows w, w + WAVES, ... (512 B each).
