@@ -326,7 +326,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(the wave shards by batch columns with no communication; see DESIGN.md)",
+              "(a wave shards by batch columns across GPUs with no communication; this build "
+              "runs and measures the one-GPU share)",
               file=sys.stderr)
         sys.exit(2)
 
