@@ -86,6 +86,7 @@ struct WaveExec {
     uint32_t kgroups = 1, stage_chunk = 0;  // MFMA split-K: workgroups per tile, stages each
     bool narrow = false;       // MFMA over <= 16 tokens (decode): k44_mfma_narrow_kernel
     bool dma = false;          // MFMA over 512-token workgroups: k44_mfma_dma_kernel
+    k44dev::DmaShape dshape;   // dma: ring stages, load policy
     bool lane8 = false;        // VALU: 8 tokens (16-byte loads) per lane
     bool stream_loads = false; // VALU: non-temporal X / weight loads (gathered rows >> caches)
     bool stream_kernel = false; // VALU: k44_gather_stream_kernel (output rows staged in LDS)
@@ -135,6 +136,7 @@ struct MfmaGroupExec {
     std::vector<size_t> members;  // wave indices, plan order
     uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0;
     bool dma = false, stream_loads = false, prod = false;
+    k44dev::DmaShape dshape;
     size_t part_floats = 0;
     DevBuf<k44dev::MfmaTileArgs> args;
     DevBuf<uint32_t> start, epi;
@@ -499,6 +501,16 @@ struct K44GpuExecutorState {
                 // policy unless K44WAVEC_NT=1.
                 const char *nt = std::getenv("K44WAVEC_NT");
                 wx.stream_loads = nt && std::string(nt) == "1";
+                // Ring depth: gathers from inputs that stay in the caches (distinct gathered
+                // bytes <= 256 MB, the last-level cache) take 2-stage rings, two workgroups per
+                // CU — config-5 prefill 26.9 -> 20.9 ms; gathers from HBM keep 4 stages and one
+                // workgroup per CU — config 3: 364 us, against 379 us with 2 stages.
+                const double gathered = (double)wx.unique_rows * wx.tokens * 2.0;
+                wx.dshape.nbuf = gathered <= 256.0 * 1048576.0 ? 2u : 4u;
+                const char *nb = std::getenv("K44WAVEC_DMA_NBUF");
+                if (nb && (std::atoi(nb) == 2 || std::atoi(nb) == 4)) wx.dshape.nbuf = (uint32_t)std::atoi(nb);
+                wx.dshape.stream_loads = wx.stream_loads;
+                wx.why += "; " + std::to_string(wx.dshape.nbuf) + "-stage ring";
             }
             if (wx.narrow) {
                 wx.path = "mfma_narrow";
@@ -1244,22 +1256,32 @@ struct K44GpuExecutorState {
                 runs.push_back({1, op.second});
                 continue;
             }
+            // Join the latest group of the same kernel configuration among the last group
+            // launches before this wave, provided the wave is independent of every member of
+            // that group and of the groups after it: it then runs earlier than in plan order
+            // with the same inputs (the groups in between neither write what it reads nor read
+            // or write what it writes).  Projections whose sub-waves take different kernels
+            // (paired full-pattern tiles, single union tiles) thus still share launches.
             bool joined = false;
-            if (grouping && !runs.empty() && runs.back().first == 2) {
-                MfmaGroupExec &g = *groups[runs.back().second];
-                bool ok = g.nt == w.cluster && g.mt == w.mt && g.rows == w.rows_per_stage &&
-                          g.dma == w.dma && g.stream_loads == w.stream_loads &&
-                          g.prod == (w.xprod != 0u) && g.members.size() < 64u;
+            for (size_t ri = runs.size(), seen = 0; grouping && ri-- > 0 && seen < 8u; ++seen) {
+                if (runs[ri].first != 2) break;
+                MfmaGroupExec &g = *groups[runs[ri].second];
+                bool indep = true;
                 for (size_t m : g.members) {
-                    if (!ok) break;
                     const WaveExec &o = *waves[m];
-                    ok = !ranges_overlap(w.wr_run, o.rd_run) && !ranges_overlap(w.rd_run, o.wr_run) &&
-                         !ranges_overlap(w.wr_run, o.wr_run);
+                    indep = !ranges_overlap(w.wr_run, o.rd_run) &&
+                            !ranges_overlap(w.rd_run, o.wr_run) &&
+                            !ranges_overlap(w.wr_run, o.wr_run);
+                    if (!indep) break;
                 }
-                if (ok) {
+                if (!indep) break;
+                if (g.nt == w.cluster && g.mt == w.mt && g.rows == w.rows_per_stage &&
+                    g.dma == w.dma && g.stream_loads == w.stream_loads && g.dshape == w.dshape &&
+                    g.prod == (w.xprod != 0u) && g.members.size() < 64u) {
                     g.members.push_back(op.second);
                     g.part_floats += w.part_floats;
                     joined = true;
+                    break;
                 }
             }
             if (!joined) {
@@ -1270,6 +1292,7 @@ struct K44GpuExecutorState {
                 g->rows = w.rows_per_stage;
                 g->dma = w.dma;
                 g->stream_loads = w.stream_loads;
+                g->dshape = w.dshape;
                 g->prod = w.xprod != 0u;
                 g->part_floats = w.part_floats;
                 runs.push_back({2, groups.size()});
@@ -1408,6 +1431,7 @@ struct K44GpuExecutorState {
               << ", \"tokens_per_lane\": " << (w.mfma ? 0 : (w.lane8 ? 8 : 4))
               << ", \"stream_loads\": " << (w.stream_loads ? "true" : "false")
               << ", \"stream_kernel\": " << (w.stream_kernel ? "true" : "false")
+              << ", \"ring_stages\": " << (w.dma ? w.dshape.nbuf : 0u)
               << ", \"xprod\": " << w.xprod
               << ", \"flops\": " << (long long)w.flops
               << ", \"effective_flops\": " << (long long)w.eff_flops
@@ -1435,12 +1459,12 @@ struct K44GpuExecutorState {
     }
 
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
-                           uint32_t items, uint32_t epi_items, bool dma, bool stream_loads,
+                           uint32_t items, uint32_t epi_items, bool dma, const k44dev::DmaShape &ds,
                            bool prod) {
         if (mt == 16u)  // narrow (<= 16 tokens)
             K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream, prod));
         else if (dma)
-            K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream, stream_loads));
+            K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream, ds));
         else
             K44_HIP(k44dev::launch_mfma_tile(d, nt, mt, rows, items, stream));
         if (epi_items) K44_HIP(k44dev::launch_splitk_epilogue(d, epi_items, stream));
@@ -1449,12 +1473,12 @@ struct K44GpuExecutorState {
     void launch_mfma(const WaveExec &w) {
         const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, w.one_epi.p, 1u};
         launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
-                          w.stream_loads, false);
+                          w.dshape, false);
     }
 
     void launch_group(const MfmaGroupExec &g) {
         const k44dev::MfmaGroup d{g.args.p, g.start.p, g.epi.p, (uint32_t)g.members.size()};
-        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.stream_loads,
+        launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.dshape,
                           g.prod);
     }
 

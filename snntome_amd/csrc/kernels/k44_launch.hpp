@@ -28,10 +28,20 @@ hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksp
 hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32_t rows_per_stage,
                             uint32_t items, hipStream_t stream);
 
-// LDS-DMA MFMA tile kernel (512 tokens per workgroup, 32-position stages in a 4-deep LDS ring)
-// over a group: `items` workgroups; nt in {32, 64}.
+// Shape of an LDS-DMA MFMA launch: ring stages (4: one workgroup per CU, 3 stages in flight;
+// 2: two workgroups per CU, 1 stage in flight each) and the loads' cache policy.
+struct DmaShape {
+    uint32_t nbuf = 4;
+    bool stream_loads = false;
+    bool operator==(const DmaShape &o) const {
+        return nbuf == o.nbuf && stream_loads == o.stream_loads;
+    }
+};
+
+// LDS-DMA MFMA tile kernel (512 tokens per workgroup, 32-position stages through an LDS ring
+// filled by direct loads) over a group: `items` workgroups; nt in {32, 64}.
 hipError_t launch_mfma_dma(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream,
-                           bool stream_loads = false);
+                           const DmaShape &shape);
 
 // Narrow MFMA kernel (waves of at most 16 tokens) over a group: `items` workgroups (tiles x
 // contraction chunks per wave); nt in {16,32,64,128}.  prod: the waves gather element-wise

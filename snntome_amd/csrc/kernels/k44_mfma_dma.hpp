@@ -10,10 +10,13 @@
 // from memory to LDS with global_load_lds (gfx950): each X row of 512 tokens is one
 // global_load_lds_dwordx4 (64 lanes x 16 bytes = the whole 1 KiB row, written at the row's
 // padded LDS pitch), and the stage's A fragments (64*NT bytes, contiguous in the upload order)
-// are NT/32 global_load_lds_dword per wave.  A ring of 4 stages keeps 3 stages (~113 KiB) of
-// every workgroup in flight while the 4th is multiplied.  No staging registers, no ds_write.
+// are NT/32 global_load_lds_dword per wave.  A ring of NBUF = 4 stages keeps 3 stages
+// (~113 KiB) of the CU's one workgroup in flight while the 4th is multiplied (gathers from
+// HBM); NBUF = 2 (74 KiB of LDS) fits two workgroups per CU, each with one stage in flight
+// (gathers that hit the caches).  No staging registers, no ds_write.
 //
-// Synchronisation per stage i (every wave issues the same D = 4 + NT/32 loads per stage):
+// Synchronisation per stage i (every wave issues the same D = 4 + NT/32 loads per stage;
+// shown for NBUF = 4):
 //   s_waitcnt vmcnt(2D) lgkmcnt(0)   own loads of stage i landed; own LDS reads of i-1 done
 //   s_barrier                        every wave's loads of stage i landed; nobody reads i-1
 //   issue stage i+3 into ring slot (i+3)%4 = (i-1)%4
@@ -98,10 +101,10 @@ __device__ __forceinline__ h4_t ds_read_tr16_at(uint32_t addr) {
 }
 
 // NTX: the direct loads use the non-temporal cache policy (substrates far beyond the caches).
-template <int NT, bool NTX>
+template <int NT, bool NTX, int NBUF = 4>
 __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
     static_assert(NT == 32 || NT == 64, "A-fragment stage must be whole dword loads per wave");
-    constexpr int MT = 512, ROWS = 32, NBUF = 4;
+    constexpr int MT = 512, ROWS = 32;
     constexpr int NB = NT / 16;
     constexpr int PITCH = MT + 16;          // halves; 32-byte skew between rows
     constexpr int WBYTES = NT * ROWS * 2;   // A fragments of one stage
