@@ -127,7 +127,7 @@ struct WaveExec {
     int masked = 0;
     // MFMA: descriptor of this wave alone (command-by-command execution).
     DevBuf<k44dev::MfmaTileArgs> one_args;
-    DevBuf<uint32_t> one_start, one_epi;
+    DevBuf<uint32_t> one_start;
     uint32_t items = 0, epi_items = 0;
 };
 
@@ -139,7 +139,7 @@ struct MfmaGroupExec {
     k44dev::DmaShape dshape;
     size_t part_floats = 0;
     DevBuf<k44dev::MfmaTileArgs> args;
-    DevBuf<uint32_t> start, epi;
+    DevBuf<uint32_t> start;
 };
 
 // Sorted, merged [lo, hi) element ranges.
@@ -1383,25 +1383,24 @@ struct K44GpuExecutorState {
             w.epi_items = epi_workgroups(w);
             w.one_args.upload({mfma_args(w, scratch.p, false)});
             w.one_start.upload({0u, w.items});
-            w.one_epi.upload({0u, w.epi_items});
         }
         for (auto &gp : groups) {
             MfmaGroupExec &g = *gp;
             std::vector<k44dev::MfmaTileArgs> args;
-            std::vector<uint32_t> start = {0u}, epi = {0u};
+            std::vector<uint32_t> start = {0u};
+            uint32_t epi_max = 0;
             size_t off = 0;
             for (size_t m : g.members) {
                 const WaveExec &w = *waves[m];
                 args.push_back(mfma_args(w, scratch.p ? scratch.p + off : nullptr, true));
                 off += w.part_floats;
                 start.push_back(start.back() + w.items);
-                epi.push_back(epi.back() + w.epi_items);
+                epi_max = std::max(epi_max, w.epi_items);
             }
             g.items = start.back();
-            g.epi_items = epi.back();
+            g.epi_items = epi_max;  // epilogue grid: epi_max x members
             g.args.upload(args);
             g.start.upload(start);
-            g.epi.upload(epi);
         }
     }
 
@@ -1471,13 +1470,13 @@ struct K44GpuExecutorState {
     }
 
     void launch_mfma(const WaveExec &w) {
-        const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, w.one_epi.p, 1u};
+        const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, 1u};
         launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
                           w.dshape, false);
     }
 
     void launch_group(const MfmaGroupExec &g) {
-        const k44dev::MfmaGroup d{g.args.p, g.start.p, g.epi.p, (uint32_t)g.members.size()};
+        const k44dev::MfmaGroup d{g.args.p, g.start.p, (uint32_t)g.members.size()};
         launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.dshape,
                           g.prod);
     }

@@ -20,6 +20,17 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
     __shared__ float part[4][OCT * 8];
     const uint32_t oct = threadIdx.x % OCT, lane_c = threadIdx.x / OCT;
     const uint32_t t0 = (blockIdx.x * OCT + oct) * 8u;
+    // Slices of at most one channel per thread (decode): the thread's own channel and its gamma
+    // are loaded with the sum's loads instead of after the reduction.
+    const uint32_t c_end = min(D, (blockIdx.y + 1u) * cslice);
+    const bool one = cslice <= CL;
+    const uint32_t c_own = blockIdx.y * cslice + lane_c;
+    uint4 xo = {0u, 0u, 0u, 0u};
+    float go = 1.0f;
+    if (one && c_own < c_end) {
+        xo = *reinterpret_cast<const uint4 *>(x + (uint64_t)c_own * stride + t0);
+        if (gamma) go = __half2float(gamma[c_own]);
+    }
     float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t c = lane_c;
     for (; c + 7u * CL < D; c += 8u * CL) {
@@ -62,7 +73,17 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
         const uint32_t q = oct * 8u + k;
         inv[k] = rsqrtf((((part[0][q] + part[1][q]) + part[2][q]) + part[3][q]) / (float)D + eps);
     }
-    const uint32_t c_end = min(D, (blockIdx.y + 1u) * cslice);
+    if (one) {
+        if (c_own < c_end) {
+            const __half *h = reinterpret_cast<const __half *>(&xo);
+            uint4 o;
+            __half *oh = reinterpret_cast<__half *>(&o);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) oh[k] = __float2half_rn(__half2float(h[k]) * inv[k] * go);
+            *reinterpret_cast<uint4 *>(y + (uint64_t)c_own * stride + t0) = o;
+        }
+        return;
+    }
     for (c = blockIdx.y * cslice + lane_c; c < c_end; c += CL) {
         const uint4 v = *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0);
         const __half *h = reinterpret_cast<const __half *>(&v);

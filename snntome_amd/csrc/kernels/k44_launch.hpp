@@ -49,9 +49,9 @@ hipError_t launch_mfma_dma(const MfmaGroup &g, uint32_t nt, uint32_t items, hipS
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream,
                               bool prod = false);
 
-// Split-K second pass over the same group: `epi_items` workgroups (the group's epi_start[n]);
-// each wave with kgroups > 1 sums its fp32 partials in z order and runs the epilogue.
-hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_items, hipStream_t stream);
+// Split-K second pass over the same group: grid epi_max x g.n (epi_max = the largest wave's
+// epilogue workgroups, ceil(cout * tokens / 4 / 256); 0: no wave of the group is split).
+hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_max, hipStream_t stream);
 
 // Stand-alone Token64 wave (X [tiles][Cin][64], Y [tiles][Cout][64], per-cluster index rows,
 // RDNA4-WMMA-ordered weights, bias, round toward zero); see k44_token64.hip.

@@ -75,11 +75,11 @@ struct MfmaTileArgs {
 
 // A launch covers a group of independent waves of one kernel configuration (the sub-waves of a
 // pruned projection, projections reading the same input): workgroup i belongs to the wave w with
-// start[w] <= i < start[w+1]; the split-K epilogue workgroups likewise by epi_start.
+// start[w] <= i < start[w+1]; the split-K epilogue runs grid (largest wave's epilogue
+// workgroups) x (waves).
 struct MfmaGroup {
     const MfmaTileArgs *waves;  // [n]
     const uint32_t *start;      // [n+1] prefix sums of tiles * ttiles * kgroups
-    const uint32_t *epi_start;  // [n+1] prefix sums of epilogue workgroups (0 without split-K)
     uint32_t n;
 };
 

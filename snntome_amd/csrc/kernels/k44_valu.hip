@@ -83,15 +83,16 @@ hipError_t launch_gather_stream(const GatherDotArgs &a, uint32_t tokens, hipStre
     return hipGetLastError();
 }
 
-// Split-K reduction + epilogue: thread = (neuron j, 4 tokens) of the wave that owns the
-// workgroup; partials summed in z order.
+// Split-K reduction + epilogue: workgroup (x, w) covers threads x*256.. of wave w of the group
+// (grid.y = the group's waves, grid.x = the largest wave's workgroups: the wave is known without
+// a table lookup); thread = (neuron j, 4 tokens); partials summed in z order.  Waves without
+// split-K have no epilogue.
 __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp) {
-    uint32_t w = 0;
-    while (w + 1u < grp.n && blockIdx.x >= grp.epi_start[w + 1u]) ++w;
-    const MfmaTileArgs a = grp.waves[w];
+    const MfmaTileArgs a = grp.waves[blockIdx.y];
     const uint32_t groups = a.kgroups, cout = a.cout, tokens = a.tokens;
+    if (groups <= 1u) return;
     const uint32_t per_row = tokens / 4u;
-    const uint64_t q = (uint64_t)(blockIdx.x - grp.epi_start[w]) * 256u + threadIdx.x;
+    const uint64_t q = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     if (q >= (uint64_t)cout * per_row) return;
     const uint32_t j = (uint32_t)(q / per_row), t = (uint32_t)(q - (uint64_t)j * per_row) * 4u;
     // cout_map entry, bias and the first partials are independent loads: issue them together.
@@ -139,9 +140,9 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp)
     *reinterpret_cast<gd_u2 *>(a.Y + o) = *reinterpret_cast<const gd_u2 *>(out);
 }
 
-hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_items, hipStream_t stream) {
-    if (epi_items == 0u) return hipSuccess;
-    hipLaunchKernelGGL(k44_splitk_epilogue_kernel, dim3(epi_items), dim3(256), 0, stream, g);
+hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_max, hipStream_t stream) {
+    if (epi_max == 0u) return hipSuccess;
+    hipLaunchKernelGGL(k44_splitk_epilogue_kernel, dim3(epi_max, g.n), dim3(256), 0, stream, g);
     return hipGetLastError();
 }
 
