@@ -167,9 +167,10 @@ __global__ __launch_bounds__(256) void k44_token_shift_prefill_kernel(
 }
 
 // Decode: one token per request (t < tokens <= 64); thread = (channel, token).
+template <uint32_t RF>
 __global__ __launch_bounds__(256) void k44_token_shift_decode_kernel(
     __half *__restrict__ y, const __half *__restrict__ x, const __half *__restrict__ mu,
-    __half *__restrict__ state, uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf) {
+    __half *__restrict__ state, uint32_t D, uint32_t stride, uint32_t tokens) {
     const uint64_t n = (uint64_t)D * stride;
     for (uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x; e < n;
          e += (uint64_t)gridDim.x * 256u) {
@@ -178,14 +179,21 @@ __global__ __launch_bounds__(256) void k44_token_shift_decode_kernel(
             y[e] = __float2half_rn(0.0f);
             continue;
         }
-        const __half *m = mu + (uint64_t)c * rf;
-        float acc = __half2float(m[0]) * __half2float(x[e]);
-        __half *st = state + (uint64_t)c * (rf - 1u) * 64u + t;  // request r = token t
-        float prev[8];
-        for (uint32_t i = 1; i < rf; ++i) prev[i - 1] = __half2float(st[(i - 1u) * 64u]);
-        for (uint32_t i = 1; i < rf; ++i) acc = fmaf(__half2float(m[i]), prev[i - 1], acc);
-        for (uint32_t i = rf - 1u; i > 1u; --i) st[(i - 1u) * 64u] = __float2half_rn(prev[i - 2]);
-        if (rf > 1u) st[0] = x[e];
+        // The receptive field is a template parameter: every load below is issued at once.
+        const __half *m = mu + (uint64_t)c * RF;
+        __half *st = state + (uint64_t)c * (RF - 1u) * 64u + t;  // request r = token t
+        const __half xe = x[e];
+        float mw[RF], prev[RF > 1u ? RF - 1u : 1u];
+#pragma unroll
+        for (uint32_t i = 0; i < RF; ++i) mw[i] = __half2float(m[i]);
+#pragma unroll
+        for (uint32_t i = 1; i < RF; ++i) prev[i - 1] = __half2float(st[(i - 1u) * 64u]);
+        float acc = mw[0] * __half2float(xe);
+#pragma unroll
+        for (uint32_t i = 1; i < RF; ++i) acc = fmaf(mw[i], prev[i - 1], acc);
+#pragma unroll
+        for (uint32_t i = RF - 1u; i > 1u; --i) st[(i - 1u) * 64u] = __float2half_rn(prev[i - 2]);
+        if (RF > 1u) st[0] = xe;
         y[e] = __float2half_rn(acc);
     }
 }
@@ -327,11 +335,21 @@ hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __ha
                               uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf,
                               uint32_t seq_len, int decode, hipStream_t stream) {
     if (rf == 0u || rf > 9u || seq_len == 0u || stride % 64u != 0u ||
-        (decode && (!state || tokens > 64u)))
+        (decode && ((rf > 1u && !state) || tokens > 64u)))
         return hipErrorInvalidValue;
     if (decode) {
-        hipLaunchKernelGGL(k44_token_shift_decode_kernel, dim3(grid_for((uint64_t)D * stride)),
-                           dim3(256), 0, stream, y, x, mu, state, D, stride, tokens, rf);
+        const dim3 grid(grid_for((uint64_t)D * stride));
+        switch (rf) {
+#define K44_TSD(R)                                                                           \
+    case R:                                                                                  \
+        hipLaunchKernelGGL(k44_token_shift_decode_kernel<R>, grid, dim3(256), 0, stream, y, x, \
+                           mu, state, D, stride, tokens);                                    \
+        break;
+            K44_TSD(1) K44_TSD(2) K44_TSD(3) K44_TSD(4) K44_TSD(5) K44_TSD(6) K44_TSD(7)
+            K44_TSD(8) K44_TSD(9)
+#undef K44_TSD
+        default: return hipErrorInvalidValue;
+        }
     } else {
         const uint32_t chunks = stride / 8u;
         const uint32_t gx = (chunks + 255u) / 256u;

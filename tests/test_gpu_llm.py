@@ -238,6 +238,39 @@ def test_token_shift_long_rf_and_many_requests(wavec):
     assert np.array_equal(got_st.view(np.uint16), st.view(np.uint16))
 
 
+@pytest.mark.parametrize("rf", [1, 2, 5, 9])
+def test_token_shift_decode_every_rf(wavec, rf):
+    """Decode token shift (one token per request, state shifted in place) for receptive fields
+    1..9 (one kernel instance per rf) over two steps, against the oracle: outputs within
+    tolerance, state bit-exact."""
+    D, req = 96, 13
+    rng = np.random.default_rng(rf)
+    mu = (rng.standard_normal((D, rf)) * 0.5).astype(np.float16)
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", D, 1, req, is_1d=True)
+    g.add_token_shift("ts", "x", "y", mu, 1, decode=True)
+    plan = g.compile()
+    plan.init_gpu()
+    c = plan.cmds[0]
+    state = np.zeros((D, max(rf - 1, 0), 64), np.float16)
+    if rf > 1:
+        state = (rng.standard_normal(state.shape)).astype(np.float16)
+        plan.write_canvas(int(c["state_off"]), state.reshape(D * (rf - 1), 64))
+    for step in range(2):
+        x = np.zeros((D, 64), np.float16)
+        x[:, :req] = rng.standard_normal((D, req)).astype(np.float16)
+        plan.write_canvas(int(c["src_off"]), x)
+        plan.execute(1)
+        y = _read(plan, c["y_off"], D, 64)
+        ref, state = lo.token_shift_decode(x, mu, state, req, f64=True)
+        assert lo.orc.rel_err(y.astype(np.float64), ref) <= TOL
+        assert not y[:, req:].any()
+        if rf > 1:
+            got = _read(plan, c["state_off"], D * (rf - 1), 64).reshape(D, rf - 1, 64)
+            assert np.array_equal(got[:, :, :req].view(np.uint16),
+                                  state[:, :, :req].view(np.uint16)), step
+
+
 @pytest.mark.parametrize("V,tokens", [(1000, 100), (32000, 64), (300, 1000)])
 def test_argmax_chunks_and_ties(wavec, V, tokens):
     """Two-pass argmax (per-chunk partials, merge in chunk order) against the lowest-index rule,
