@@ -134,7 +134,7 @@ struct WaveExec {
 // A launch of several independent MFMA waves of one kernel configuration.
 struct MfmaGroupExec {
     std::vector<size_t> members;  // wave indices, plan order
-    uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0;
+    uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0, max_items = 0;
     bool dma = false, stream_loads = false, prod = false;
     k44dev::DmaShape dshape;
     size_t part_floats = 0;
@@ -1388,7 +1388,7 @@ struct K44GpuExecutorState {
             MfmaGroupExec &g = *gp;
             std::vector<k44dev::MfmaTileArgs> args;
             std::vector<uint32_t> start = {0u};
-            uint32_t epi_max = 0;
+            uint32_t epi_max = 0, item_max = 0;
             size_t off = 0;
             for (size_t m : g.members) {
                 const WaveExec &w = *waves[m];
@@ -1396,9 +1396,11 @@ struct K44GpuExecutorState {
                 off += w.part_floats;
                 start.push_back(start.back() + w.items);
                 epi_max = std::max(epi_max, w.epi_items);
+                item_max = std::max(item_max, w.items);
             }
             g.items = start.back();
             g.epi_items = epi_max;  // epilogue grid: epi_max x members
+            g.max_items = item_max;
             g.args.upload(args);
             g.start.upload(start);
         }
@@ -1459,9 +1461,9 @@ struct K44GpuExecutorState {
 
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
                            uint32_t items, uint32_t epi_items, bool dma, const k44dev::DmaShape &ds,
-                           bool prod) {
+                           bool prod, uint32_t max_items) {
         if (mt == 16u)  // narrow (<= 16 tokens)
-            K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream, prod));
+            K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream, prod, max_items));
         else if (dma)
             K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream, ds));
         else
@@ -1472,13 +1474,13 @@ struct K44GpuExecutorState {
     void launch_mfma(const WaveExec &w) {
         const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, 1u};
         launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
-                          w.dshape, false);
+                          w.dshape, false, w.items);
     }
 
     void launch_group(const MfmaGroupExec &g) {
         const k44dev::MfmaGroup d{g.args.p, g.start.p, (uint32_t)g.members.size()};
         launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.dshape,
-                          g.prod);
+                          g.prod, g.max_items);
     }
 
     void launch_wave(const WaveExec &w) {

@@ -188,16 +188,24 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
 // split-K partials and no second kernel.
 // PROD: the launch's waves gather element-wise products (a.xprod 2 / 3); without it the
 // product registers are not allocated.
-template <int NT, bool PROD>
+// BYY: grid (largest wave's workgroups) x (waves): the wave is blockIdx.y, known without a
+// lookup in the group's prefix sums; workgroups past a wave's own count exit at once.
+template <int NT, bool PROD, bool BYY>
 __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp) {
     constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16;
     static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][NARROW_MAX_ROWS][NARROW_PITCH];
 
-    uint32_t w = 0;
-    while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
+    uint32_t w = 0, local;
+    if constexpr (BYY) {
+        w = blockIdx.y;
+        local = blockIdx.x;
+    } else {
+        while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
+        local = blockIdx.x - grp.start[w];
+    }
     const MfmaTileArgs a = grp.waves[w];
-    const uint32_t local = blockIdx.x - grp.start[w];
+    if (BYY && local >= a.tiles * a.kgroups) return;
     const uint32_t tile = local % a.tiles, zgroup = local / a.tiles;
     const uint32_t ks_begin = zgroup * a.stage_chunk;
     const uint32_t ks_end = min(a.ksteps, ks_begin + a.stage_chunk);
@@ -349,27 +357,39 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
 }
 
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
-                              hipStream_t stream, bool prod) {
+                              hipStream_t stream, bool prod, uint32_t max_items) {
     if (prod && nt != 64u && nt != 128u) return hipErrorInvalidValue;
     if (items == 0u) return hipSuccess;
     const dim3 grid(items), block(256);
+    // 64/128-neuron tiles: grid (max_items, waves) when it launches at most 1.5x the
+    // workgroups (max_items = the largest wave's workgroups; 0 = not known).
+    const bool byy = max_items != 0u && 2ull * max_items * g.n <= 3ull * items;
+    const dim3 grid_y(max_items, g.n);
+#define K44_NL(N, P)                                                                               \
+    if (byy)                                                                                       \
+        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, true>), grid_y, block, 0, stream, g); \
+    else                                                                                           \
+        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, false>), grid, block, 0, stream, g);
     switch (nt) {
     case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, g); break;
     case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, g); break;
     case 64u:
-        if (prod)
-            hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<64, true>), grid, block, 0, stream, g);
-        else
-            hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<64, false>), grid, block, 0, stream, g);
+        if (prod) {
+            K44_NL(64, true)
+        } else {
+            K44_NL(64, false)
+        }
         break;
     case 128u:
-        if (prod)
-            hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<128, true>), grid, block, 0, stream, g);
-        else
-            hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<128, false>), grid, block, 0, stream, g);
+        if (prod) {
+            K44_NL(128, true)
+        } else {
+            K44_NL(128, false)
+        }
         break;
     default: return hipErrorInvalidValue;
     }
+#undef K44_NL
     return hipGetLastError();
 }
 
