@@ -178,7 +178,9 @@ struct AuxExec {
     uint64_t y_off = 0, src_off = 0, src2_off = 0, state_off = 0;
     uint32_t D = 0, stride = 0, tokens = 0, rf = 0, seq_len = 0, vocab = 0;
     bool decode = false, has_state = false;
-    bool fused = false;  // SWIGLU_MUL_1D folded into its consumers' gathers (not launched)
+    bool fused = false;  // SWIGLU_MUL_1D folded into its consumers' gathers, or TOKEN_SHIFT_1D
+                         // run by the RMSNorm before it (not launched)
+    size_t shift_with = SIZE_MAX;  // RMSNORM_1D: the decode token shift it runs (whole plans)
     float eps = 1e-5f;
     DevBuf<__half> table;  // gamma (RMSNORM), mix (TOKEN_SHIFT), embedding table (EMBED)
     // 2-D spatial commands (S2D, pools, upsample, scatter-upconv): channel count C, planes
@@ -891,12 +893,21 @@ struct K44GpuExecutorState {
         }
     }
 
-    void launch_aux(const AuxExec &a) {
+    // whole: whole-plan execution (folded / fused commands apply).
+    void launch_aux(const AuxExec &a, bool whole = false) {
         __half *cv = canvas.p;
         switch (a.type) {
         case K44CmdType::RMSNORM_1D:
-            K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D, a.stride,
-                                           a.tokens, a.eps, stream));
+            if (whole && a.shift_with != SIZE_MAX) {
+                const AuxExec &t = *aux[a.shift_with];
+                const k44dev::RmsShift sh{cv + t.y_off, t.table.p,
+                                          t.has_state ? cv + t.state_off : nullptr, t.rf, 0u};
+                K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
+                                               a.stride, a.tokens, a.eps, stream, &sh));
+            } else {
+                K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
+                                               a.stride, a.tokens, a.eps, stream));
+            }
             break;
         case K44CmdType::SWIGLU_MUL_1D:
             K44_HIP(k44dev::launch_mul(cv + a.y_off, cv + a.src_off, cv + a.src2_off,
@@ -972,6 +983,7 @@ struct K44GpuExecutorState {
             }
         }
         fuse_products();
+        fuse_norm_shifts();
         form_runs();
         K44_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         K44_HIP(hipEventCreate(&ev0));
@@ -1235,6 +1247,33 @@ struct K44GpuExecutorState {
                 w.why += nleaf == 3 ? "; gathers fp16(a*fp16(b*c)) (two multiplies folded)"
                                     : "; gathers fp16(a*b) (multiply folded)";
             }
+        }
+    }
+
+    // A decode RMSNorm followed directly by the decode token shift of its output runs the shift
+    // in the same kernel (whole-plan execution; bit-identical to the two commands): the norm's
+    // decode form keeps one channel per thread, so the shift of that channel's tokens follows
+    // in place.  K44WAVEC_FUSE=0 keeps both launches.
+    void fuse_norm_shifts() {
+        const char *fe = std::getenv("K44WAVEC_FUSE");
+        if (fe && std::string(fe) == "0") return;
+        for (size_t i = 0; i + 1u < ops.size(); ++i) {
+            if (ops[i].first || ops[i + 1u].first) continue;
+            AuxExec &N = *aux[ops[i].second];
+            AuxExec &T = *aux[ops[i + 1u].second];
+            if (N.type != K44CmdType::RMSNORM_1D || T.type != K44CmdType::TOKEN_SHIFT_1D ||
+                N.fused || T.fused || !T.decode || T.src_off != N.y_off || T.D != N.D ||
+                T.stride != N.stride || T.tokens != N.tokens || N.stride != 64u ||
+                N.tokens == 0u || N.tokens > 64u || T.rf == 0u || T.rf > 9u ||
+                (T.rf > 1u && !T.has_state))
+                continue;
+            // The launcher's decode geometry must give one channel per thread.
+            const uint32_t chunks = (N.tokens + 7u) / 8u;
+            uint32_t slices = (256u + chunks - 1u) / chunks;
+            slices = std::min(slices, (N.D + 255u) / 256u);
+            if ((N.D + slices - 1u) / slices > 256u) continue;
+            N.shift_with = ops[i + 1u].second;
+            T.fused = true;
         }
     }
 
@@ -1548,7 +1587,7 @@ struct K44GpuExecutorState {
     void launch_ops() {
         for (const auto &r : runs) {
             if (r.first == 0)
-                launch_aux(*aux[r.second]);
+                launch_aux(*aux[r.second], true);
             else if (r.first == 1)
                 launch_wave(*waves[r.second]);
             else

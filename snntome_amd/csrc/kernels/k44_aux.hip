@@ -10,12 +10,16 @@ namespace k44dev {
 // reduce (shuffles, then the 4 waves in LDS in a fixed order), and the workgroup writes channel
 // slice blockIdx.y of its tokens.  Small token counts (decode) use OCT = 1 and several slices
 // per token chunk, each recomputing the (cache-resident) sum, so the grid still fills the chip.
-template <int OCT>
+// RF > 0 (decode slices of one channel per thread): the decode token shift of the output
+// follows in the same thread — y2 = mu[c][0]*y + sum_i mu[c][i]*state[c][i-1][t], state shifted
+// in place, with the arithmetic of k44_token_shift_decode_kernel (bit-identical); the grid
+// then covers every octet of the stride, octets without requests writing zeros to y2 only.
+template <int OCT, uint32_t RF>
 __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y,
                                                           const __half *__restrict__ x,
                                                           const __half *__restrict__ gamma,
                                                           uint32_t D, uint32_t stride, float eps,
-                                                          uint32_t cslice) {
+                                                          uint32_t cslice, RmsShift sh) {
     constexpr uint32_t CL = 256u / OCT;  // channel lanes
     __shared__ float part[4][OCT * 8];
     const uint32_t oct = threadIdx.x % OCT, lane_c = threadIdx.x / OCT;
@@ -27,9 +31,30 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
     const uint32_t c_own = blockIdx.y * cslice + lane_c;
     uint4 xo = {0u, 0u, 0u, 0u};
     float go = 1.0f;
+    // Fused token shift: octets without requests only write zeros; the mixing weights and the
+    // state of the thread's channel are loaded here too.
+    if constexpr (RF > 0u) {
+        if (t0 >= sh.tokens) {
+            if (c_own < c_end)
+                *reinterpret_cast<uint4 *>(sh.y2 + (uint64_t)c_own * stride + t0) =
+                    uint4{0u, 0u, 0u, 0u};
+            return;  // uniform: one octet per workgroup
+        }
+    }
+    float mw[RF > 0u ? RF : 1u];
+    uint4 sv[RF > 1u ? RF - 1u : 1u];
     if (one && c_own < c_end) {
         xo = *reinterpret_cast<const uint4 *>(x + (uint64_t)c_own * stride + t0);
         if (gamma) go = __half2float(gamma[c_own]);
+        if constexpr (RF > 0u) {
+            const __half *m = sh.mu + (uint64_t)c_own * RF;
+#pragma unroll
+            for (uint32_t i = 0; i < RF; ++i) mw[i] = __half2float(m[i]);
+            const __half *st = sh.state + (uint64_t)c_own * (RF - 1u) * 64u + t0;
+#pragma unroll
+            for (uint32_t i = 1; i < RF; ++i)
+                sv[i - 1] = *reinterpret_cast<const uint4 *>(st + (i - 1u) * 64u);
+        }
     }
     float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t c = lane_c;
@@ -80,7 +105,37 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
             __half *oh = reinterpret_cast<__half *>(&o);
 #pragma unroll
             for (int k = 0; k < 8; ++k) oh[k] = __float2half_rn(__half2float(h[k]) * inv[k] * go);
-            *reinterpret_cast<uint4 *>(y + (uint64_t)c_own * stride + t0) = o;
+            if (RF == 0u || t0 < sh.tokens)
+                *reinterpret_cast<uint4 *>(y + (uint64_t)c_own * stride + t0) = o;
+            if constexpr (RF > 0u) {
+                __half *st = sh.state + (uint64_t)c_own * (RF - 1u) * 64u + t0;
+                uint4 o2;
+                __half *yh = reinterpret_cast<__half *>(&o2);
+                uint4 nsv[RF > 1u ? RF - 1u : 1u];
+#pragma unroll
+                for (uint32_t i = 1; i < RF; ++i) nsv[i - 1] = sv[i - 1];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    if (t0 + (uint32_t)k >= sh.tokens) {
+                        yh[k] = __float2half_rn(0.0f);
+                        continue;
+                    }
+                    float acc = mw[0] * __half2float(oh[k]);
+#pragma unroll
+                    for (uint32_t i = 1; i < RF; ++i)
+                        acc = fmaf(mw[i], __half2float(reinterpret_cast<const __half *>(&sv[i - 1])[k]), acc);
+                    yh[k] = __float2half_rn(acc);
+#pragma unroll
+                    for (uint32_t i = RF - 1u; i > 1u; --i)
+                        reinterpret_cast<__half *>(&nsv[i - 1])[k] =
+                            reinterpret_cast<const __half *>(&sv[i - 2])[k];
+                    if (RF > 1u) reinterpret_cast<__half *>(&nsv[0])[k] = oh[k];
+                }
+#pragma unroll
+                for (uint32_t i = 1; i < RF; ++i)
+                    *reinterpret_cast<uint4 *>(st + (i - 1u) * 64u) = nsv[i - 1];
+                *reinterpret_cast<uint4 *>(sh.y2 + (uint64_t)c_own * stride + t0) = o2;
+            }
         }
         return;
     }
@@ -300,7 +355,8 @@ static uint32_t grid_for(uint64_t n) {
 }
 
 hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
-                          uint32_t stride, uint32_t tokens, float eps, hipStream_t stream) {
+                          uint32_t stride, uint32_t tokens, float eps, hipStream_t stream,
+                          const RmsShift *shift) {
     if (stride % 64u != 0u || D == 0u || tokens == 0u || tokens > stride)
         return hipErrorInvalidValue;
     // token columns >= tokens are not written; octets per workgroup: the widest that still
@@ -308,18 +364,45 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
     const uint32_t octets = (tokens + 7u) / 8u;
     uint32_t oct = 8u;
     while (oct > 1u && (octets + oct - 1u) / oct < 256u) oct >>= 1;
-    const uint32_t chunks = (octets + oct - 1u) / oct;
+    uint32_t chunks = (octets + oct - 1u) / oct;
     uint32_t slices = (256u + chunks - 1u) / chunks;
     const uint32_t max_slices = (D + 255u) / 256u;
     slices = slices < max_slices ? slices : max_slices;
     const uint32_t cslice = (D + slices - 1u) / slices;
-    const dim3 grid(chunks, (D + cslice - 1u) / cslice);
-    switch (oct) {
-    case 8u: hipLaunchKernelGGL(k44_rmsnorm_kernel<8>, grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice); break;
-    case 4u: hipLaunchKernelGGL(k44_rmsnorm_kernel<4>, grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice); break;
-    case 2u: hipLaunchKernelGGL(k44_rmsnorm_kernel<2>, grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice); break;
-    default: hipLaunchKernelGGL(k44_rmsnorm_kernel<1>, grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice); break;
+    RmsShift sh{};
+    if (shift) {
+        // Fused decode token shift: one channel per thread, every octet of the stride.
+        if (oct != 1u || cslice > 256u || tokens > 64u || stride != 64u || shift->rf == 0u ||
+            shift->rf > 9u || (shift->rf > 1u && !shift->state))
+            return hipErrorInvalidValue;
+        sh = *shift;
+        sh.tokens = tokens;
+        chunks = stride / 8u;
     }
+    const dim3 grid(chunks, (D + cslice - 1u) / cslice);
+#define K44_RMS(O, R) \
+    hipLaunchKernelGGL((k44_rmsnorm_kernel<O, R>), grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice, sh)
+    if (shift) {
+        switch (sh.rf) {
+        case 1u: K44_RMS(1, 1u); break;
+        case 2u: K44_RMS(1, 2u); break;
+        case 3u: K44_RMS(1, 3u); break;
+        case 4u: K44_RMS(1, 4u); break;
+        case 5u: K44_RMS(1, 5u); break;
+        case 6u: K44_RMS(1, 6u); break;
+        case 7u: K44_RMS(1, 7u); break;
+        case 8u: K44_RMS(1, 8u); break;
+        default: K44_RMS(1, 9u); break;
+        }
+    } else {
+        switch (oct) {
+        case 8u: K44_RMS(8, 0u); break;
+        case 4u: K44_RMS(4, 0u); break;
+        case 2u: K44_RMS(2, 0u); break;
+        default: K44_RMS(1, 0u); break;
+        }
+    }
+#undef K44_RMS
     return hipGetLastError();
 }
 

@@ -19,8 +19,18 @@
 
 namespace k44dev {
 
+// Decode token shift fused into an RMSNorm (launch_rmsnorm's `shift`): its output y2, mixing
+// weights mu [D][rf], state [D][rf-1][64]; tokens is filled in by the launcher.
+struct RmsShift {
+    __half *y2;
+    const __half *mu;
+    __half *state;
+    uint32_t rf, tokens;
+};
+
 hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
-                          uint32_t stride, uint32_t tokens, float eps, hipStream_t stream);
+                          uint32_t stride, uint32_t tokens, float eps, hipStream_t stream,
+                          const RmsShift *shift = nullptr);
 hipError_t launch_mul(__half *y, const __half *a, const __half *b, uint64_t n,
                       hipStream_t stream);
 hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __half *state,

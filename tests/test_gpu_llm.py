@@ -410,12 +410,14 @@ def test_folded_multiplies_match_unfolded(wavec, monkeypatch):
         p.init_gpu()
         plans[mode] = p
     rep = plans["folded"].exec_report()
-    fused = [a for a in rep["aux"] if a["fused"]]
+    fused = [a for a in rep["aux"] if a["fused"] and a["type"] == "SWIGLU_MUL_1D"]
+    shifts = [a for a in rep["aux"] if a["fused"] and a["type"] == "TOKEN_SHIFT_1D"]
     prods = sorted({w["xprod"] for w in rep["waves"]})
-    _log(f"[fold] {len(fused)} multiplies folded, xprod kinds {prods}, "
+    _log(f"[fold] {len(fused)} multiplies folded, {len(shifts)} token shifts run by their "
+         f"RMSNorm, xprod kinds {prods}, "
          f"{rep['launches_per_run']} vs {plans['launched'].exec_report()['launches_per_run']} "
          "launches per run")
-    assert len(fused) == 3 * spec.layers and prods == [0, 2, 3]
+    assert len(fused) == 3 * spec.layers and prods == [0, 2, 3] and len(shifts) == spec.layers
     assert not any(a["fused"] for a in plans["launched"].exec_report()["aux"])
     R = spec.requests
     pre.set_ids(np.random.default_rng(5).integers(0, spec.vocab, R * spec.prompt))
@@ -446,10 +448,11 @@ def test_decode_step_full_width_against_oracle(wavec):
     dec = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
     dec.init_gpu()
     rep = dec.exec_report()
-    _log(f"[decode full width] {len(rep['waves'])} waves, "
-         f"{sum(a['fused'] for a in rep['aux'])} multiplies folded, "
-         f"{rep['launches_per_run']} launches per step")
-    assert sum(a["fused"] for a in rep["aux"]) == 3 * spec.layers
+    n_mul = sum(a["fused"] and a["type"] == "SWIGLU_MUL_1D" for a in rep["aux"])
+    n_shift = sum(a["fused"] and a["type"] == "TOKEN_SHIFT_1D" for a in rep["aux"])
+    _log(f"[decode full width] {len(rep['waves'])} waves, {n_mul} multiplies folded, "
+         f"{n_shift} token shifts run by their RMSNorm, {rep['launches_per_run']} launches per step")
+    assert n_mul == 3 * spec.layers and n_shift == spec.layers
     R = spec.requests
     ids = np.random.default_rng(11).integers(0, spec.vocab, R).astype(np.uint32)
     dec.set_ids(ids)
