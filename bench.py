@@ -1,19 +1,27 @@
 #!/usr/bin/env python3
 """Benchmark of the SNNtome wave hot path on one MI355X.
 
-Workload: the ultra-sparse gather-bound wave — substrate of
+Headline workload: the ultra-sparse gather-bound wave — substrate of
 40,000,000 positions x batch 256 fp16 (20.5 GB, generated on the device), 65,536 neurons, each
 reading 4 dendritic clusters of S=16 consecutive positions (16-aligned uniform starts),
 W ~ N(0, 0.05), b ~ N(0, 0.01), ReLU, fp32 accumulation.  One step = one execution of the
 compiled one-wave plan through libk44wavec.so (inputs resident in HBM).
 
-Metric: effective TFLOP/s = 2 * nnz * batch / t  (nnz = 65,536 x 64 synapses, batch = 256),
-reported with the achieved HBM GB/s of the wave kernel against the 8 TB/s roofline, and the
-CPU path (OpenMP fp32 oracle) timed on the host cores on a bounded sample of the same wave.
+Metric: effective TFLOP/s = 2 * nnz * batch / t (nnz = 65,536 x 64 synapses, batch = 256),
+reported with the achieved algorithmic HBM GB/s of the wave kernel against the 8 TB/s roofline,
+and the CPU path (OpenMP fp32 oracle) timed on the host cores on a bounded sample of the wave.
 
-Config 5 (--config 5): the LLM-shaped decoder, prefill + 128 greedy decode steps per step.
+The default run (no --config) prints ONE JSON line: the headline (config 2) at the top level and
+the other BASELINE configurations at their full sizes under "configs" (c1 plumbing, c3 dense
+cluster, c4 8-wave plan, c5 LLM-shaped decoder), each with its own binding roofline:
+  c1, c4  cache-resident gathers: achieved = gathered bytes / kernel time against the aggregate
+          L2 bandwidth (8 XCDs x 16 channels x 128 B/clk x 2.4 GHz = 39.3 TB/s);
+  c2, c3  HBM: compulsory (algorithmic) bytes / kernel time against 8 TB/s;
+  c5      prefill: effective FLOPs / prefill time against 2.5 PFLOP/s fp16 MFMA; decode: weight
+          bytes / step time against HBM.
+--config N runs one configuration alone (its record at the top level).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5] [--no-cpu] [--eager]
 """
 import argparse
 import json
@@ -29,10 +37,28 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
+# Aggregate L2 read bandwidth: 8 XCDs x 16 channels x 128 B per clock at 2.4 GHz.
+L2_PEAK_GBS = 8 * 16 * 128 * 2.4
+METRIC = "effective TFLOP/s (2*nnz*batch) + achieved HBM GB/s per wave, 1xMI355X"
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def under_profiler() -> bool:
+    """rocprofv3 preloads its tool library into the program it profiles."""
+    return "rocprofiler-sdk" in os.environ.get("LD_PRELOAD", "")
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def workload(cfg: int):
@@ -85,6 +111,8 @@ def cpu_baseline(wl, budget_s: float = 12.0, sample_neurons: int = 4096):
         "unit": "TFLOP/s",
         "cores": int(used),
         "kind": "port",
+        "cpu_model": cpu_model(),
+        "host_threads": os.cpu_count(),
         "sample": (f"{n} of {w.cout} neurons of {w.name} ({n * w.K} segments, "
                    f"{n * w.K * w.S} substrate rows x {wl.tokens} tokens), median of "
                    f"{len(times)} passes, fp32 OpenMP oracle/wave_oracle.c:orc_wave_f32_omp"),
@@ -133,13 +161,94 @@ def cpu_baseline_llm(spec, wts, tokens, budget_s: float = 12.0, sample_neurons: 
         "unit": "TFLOP/s",
         "cores": int(used),
         "kind": "port",
+        "cpu_model": cpu_model(),
+        "host_threads": os.cpu_count(),
         "sample": (f"{n} of {p.starts.shape[0]} neurons of layer 0's down projection "
                    f"({K} x {spec.S} inputs each) x {tokens} prefill tokens, median of "
                    f"{len(times)} passes, fp32 OpenMP oracle/wave_oracle.c:orc_wave_f32_omp"),
     }
 
 
-def bench_llm(args):
+def gathered_bytes(wl, w) -> int:
+    """Bytes the wave's gathers read (every segment row of every index row x tokens x 2): what a
+    cache-resident wave moves from L2 / MALL."""
+    stride = (wl.tokens + 63) // 64 * 64
+    return 2 * stride * w.starts.size * w.S
+
+
+def bench_wave(cfg: int, steps: int, warmup: int) -> dict:
+    """One of configs 1-4 at full size: compiled plan, device-generated input, `warmup` untimed
+    then `steps` timed plan executions bracketed by device synchronisation."""
+    from snntome_amd import synth, wavec
+
+    t_start = time.perf_counter()
+    wl = workload(cfg)
+    log(f"[bench] workload {wl.name}: {wl.description}")
+    plan = synth.build_graph(wl, wavec).compile()
+    plan.init_gpu()
+    plan.fill_input_uniform(wl.seed)
+    rep = plan.exec_report()
+    for wv in rep["waves"][:2]:
+        log(f"[bench] {wv['name']}: path={wv['path']} K={wv['K']} S={wv['S']} "
+            f"slab={wv['slab']} tokens={wv['tokens']}")
+    log(f"[bench] setup {time.perf_counter() - t_start:.1f}s; warmup {warmup}")
+    if warmup > 0:
+        plan.execute(warmup)
+    plan.sync()
+    t0 = time.perf_counter()
+    ev_ms = plan.execute(steps)  # HIP events on the executor stream, average per step
+    plan.sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    log(f"[bench] {wl.name} {steps} steps: {wall_ms:.4f} ms/step wall, {ev_ms:.4f} ms/step events")
+    plan.release_gpu()
+
+    flops = wl.flops
+    comp = sum(synth.compulsory_bytes(wl, w) for w in wl.waves)
+    gath = sum(gathered_bytes(wl, w) for w in wl.waves)
+    value = flops / (wall_ms * 1e-3) / 1e12
+    path = rep["waves"][0]["path"]
+    kernel_key = path + "_" + wl.name.split("_")[0]
+    w0 = wl.waves[0]
+    mfma_frac = flops / (ev_ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS
+    if cfg in (1, 4):  # substrate and intermediate tensors stay in the caches
+        achieved = gath / (ev_ms * 1e-3) / 1e9
+        roof = {"bound": "l2", "achieved": round(achieved, 1), "peak": round(L2_PEAK_GBS, 1),
+                "unit": "GB/s", "frac": round(achieved / L2_PEAK_GBS, 4),
+                "traffic": traffic_from_profiles(kernel_key), "gathered_bytes": gath,
+                "algorithmic_hbm_bytes": comp,
+                "hbm_frac_of_algorithmic": round(comp / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "kernel_ms": round(ev_ms, 5),
+                "note": "gathered bytes (every segment row x tokens) from L2/MALL per kernel time "
+                        "against the aggregate L2 read bandwidth"}
+    else:
+        achieved = comp / (ev_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic_from_profiles(kernel_key), "algorithmic_bytes": comp,
+                "kernel_ms": round(ev_ms, 5), "mfma_tflops_frac": round(mfma_frac, 4)}
+    return {
+        "metric": METRIC,
+        "value": round(value, 4),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(wall_ms, 5),
+        "config": {
+            "workload": wl.name,
+            "substrate_positions": wl.substrate,
+            "batch": wl.tokens,
+            "neurons_per_wave": w0.cout,
+            "clusters_per_neuron": w0.K,
+            "S": w0.S,
+            "waves": len(wl.waves),
+            "act": w0.act,
+            "path": path,
+        },
+        "hbm_gbs": round(comp / (ev_ms * 1e-3) / 1e9, 1),
+        "roofline": roof,
+        "_wl": wl,
+    }
+
+
+def bench_llm(steps: int, warmup: int, eager: bool, no_cpu: bool = True) -> dict:
     """Config 5: LLM-shaped decoder, 16 x 512-token prefill + 128 greedy decode steps.  One step =
     prefill of all requests, device-side hand-over (token-shift state, last-token ids), then the
     decode steps as replays of one captured HIP graph (argmax -> embedding chained on the device,
@@ -154,8 +263,8 @@ def bench_llm(args):
     dec = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
     pre.init_gpu()
     dec.init_gpu()
-    pre.use_graph(not args.eager)
-    dec.use_graph(not args.eager)
+    pre.use_graph(not eager)
+    dec.use_graph(not eager)
     R, P, D = spec.requests, spec.prompt, spec.decode_steps
     prompt = np.random.default_rng(spec.seed).integers(0, spec.vocab, R * P).astype(np.uint32)
     rep = pre.exec_report()["waves"]
@@ -163,7 +272,8 @@ def bench_llm(args):
     ex_flops = sum(w["flops"] for w in rep)
     log(f"[bench] config5 setup {time.perf_counter() - t_start:.1f}s: {len(pre.cmds)} prefill "
         f"commands ({len(rep)} waves, paths {paths}), executed/effective flops "
-        f"{ex_flops / (2 * spec.nnz_per_token * R * P):.3f}")
+        f"{ex_flops / (2 * spec.nnz_per_token * R * P):.3f}; "
+        f"{'eager launches' if eager else 'HIP-graph replays'}")
 
     def one_step():
         ms_p = pre.execute(1)
@@ -172,19 +282,19 @@ def bench_llm(args):
         return ms_p, ms_d
 
     pre.set_ids(prompt)
-    for _ in range(max(1, args.warmup)):
+    for _ in range(max(1, warmup)):
         one_step()
     pre.sync()
     dec.sync()
     t0 = time.perf_counter()
     pms, dms = [], []
-    for _ in range(args.steps):
+    for _ in range(steps):
         pre.set_ids(prompt)  # (prompt ids: host input, re-uploaded; 32 KB)
         a, b = one_step()
         pms.append(a)
         dms.append(b)
     dec.sync()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     prefill_ms, decode_ms = float(np.mean(pms)), float(np.mean(dms))
     f_pre = 2.0 * spec.nnz_per_token * R * P
     f_dec = 2.0 * spec.nnz_per_token * R
@@ -193,27 +303,19 @@ def bench_llm(args):
     w_bytes = dec.summary["total_w_bytes"]
     dec_gbs = w_bytes / (decode_ms * 1e-3) / 1e9
     pre_tf = f_pre / (prefill_ms * 1e-3) / 1e12
-    log(f"[bench] {args.steps} steps: {wall_ms:.2f} ms/step wall; prefill {prefill_ms:.3f} ms "
+    log(f"[bench] config5 {steps} steps: {wall_ms:.2f} ms/step wall; prefill {prefill_ms:.3f} ms "
         f"({pre_tf:.1f} TFLOP/s), decode {decode_ms:.4f} ms/step ({dec_gbs:.0f} GB/s weights)")
     out = {
-        "metric": "effective TFLOP/s (2*nnz*batch) + achieved HBM GB/s per wave, 1xMI355X",
+        "metric": METRIC,
         "value": round(value, 4),
         "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
         "ms_per_step": round(wall_ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16 (fp32 accumulate)",
-        "data": "synthetic (random-init fp16 weights, uniform random prompt ids)",
         "config": {
             "workload": "config5_llm_decoder",
             "layers": spec.layers, "d": spec.d, "ffn": spec.ffn, "vocab": spec.vocab,
             "S": spec.S, "clusters_kept": [spec.kept(spec.d), spec.kept(spec.ffn)],
             "tile": spec.tile, "token_shift_rf": spec.rf, "requests": R, "prompt": P,
-            "decode_steps": D, "paths": paths, "hip_graphs": not args.eager,
+            "decode_steps": D, "paths": paths, "hip_graphs": not eager,
         },
         "prefill_ms": round(prefill_ms, 4),
         "prefill_tflops": round(pre_tf, 2),
@@ -237,11 +339,13 @@ def bench_llm(args):
             "scope": "decode step: executed weight bytes / step time",
         },
     }
-    if not args.no_cpu:
+    if not no_cpu:
         log("[bench] cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline_llm(spec, wts, R * P)
         log(f"[bench] cpu baseline {out['cpu_baseline']}")
-    print(json.dumps(out), flush=True)
+    pre.release_gpu()
+    dec.release_gpu()
+    return out
 
 
 def bench_token64(args):
@@ -293,7 +397,7 @@ def bench_token64(args):
     tsyn = Cout * B * M / t / 1e12
     log(f"[bench] token64 S={S}: {t * 1e6:.1f} us/launch, {tsyn:.2f} TSyn/s, {2 * tsyn:.1f} TFLOP/s")
     out = {
-        "metric": "effective TFLOP/s (2*nnz*batch) + achieved HBM GB/s per wave, 1xMI355X",
+        "metric": METRIC,
         "value": round(2 * tsyn, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(t * 1e3, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f16 (fp32 accumulate)",
@@ -305,12 +409,29 @@ def bench_token64(args):
     print(json.dumps(out), flush=True)
 
 
+def _envelope(rec: dict, args, data: str) -> dict:
+    """The driver's contract fields around one configuration record."""
+    out = {
+        "metric": rec["metric"], "value": rec["value"], "unit": rec["unit"], "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": rec["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 (fp32 accumulate)", "data": data,
+    }
+    out.update({k: v for k, v in rec.items() if k not in out and not k.startswith("_")})
+    return out
+
+
+WAVE_DATA = "synthetic (device-generated counter-hash substrate; numpy PCG64 weights)"
+LLM_DATA = "synthetic (random-init fp16 weights, uniform random prompt ids)"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=None, choices=[1, 2, 3, 4, 5],
+                    help="one configuration alone (default: headline config 2 + all others)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="config 5: launch kernel by kernel instead of replaying HIP graphs")
@@ -330,85 +451,40 @@ def main():
               "runs and measures the one-GPU share)",
               file=sys.stderr)
         sys.exit(2)
-
     if args.token64:
         bench_token64(args)
         return
+    # Under rocprofv3 config 5 launches kernel by kernel: a kernel-trace run of its HIP-graph
+    # capture ended in a host segmentation fault inside the profiler's preloaded libraries.
+    eager = args.eager or under_profiler()
+
     if args.config == 5:
-        bench_llm(args)
+        rec = bench_llm(args.steps, args.warmup, eager, no_cpu=args.no_cpu)
+        print(json.dumps(_envelope(rec, args, LLM_DATA)), flush=True)
+        return
+    if args.config is not None:
+        rec = bench_wave(args.config, args.steps, args.warmup)
+        out = _envelope(rec, args, WAVE_DATA)
+        if not args.no_cpu:
+            log("[bench] cpu baseline ...")
+            out["cpu_baseline"] = cpu_baseline(rec["_wl"])
+        print(json.dumps(out), flush=True)
         return
 
-    from snntome_amd import synth, wavec
-
-    t_start = time.perf_counter()
-    wl = workload(args.config)
-    log(f"[bench] workload {wl.name}: {wl.description}")
-    plan = synth.build_graph(wl, wavec).compile()
-    plan.init_gpu()
-    plan.fill_input_uniform(wl.seed)
-    rep = plan.exec_report()
-    for wv in rep["waves"]:
-        log(f"[bench] {wv['name']}: path={wv['path']} K={wv['K']} S={wv['S']} "
-            f"slab={wv['slab']} tokens={wv['tokens']}")
-    log(f"[bench] setup {time.perf_counter() - t_start:.1f}s; warmup {args.warmup}")
-    if args.warmup > 0:
-        plan.execute(args.warmup)
-    plan.sync()
-
-    # Timed region: K plan executions, device synchronised on both sides.
-    t0 = time.perf_counter()
-    ev_ms = plan.execute(args.steps)  # HIP events on the executor stream, average per step
-    plan.sync()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    log(f"[bench] {args.steps} steps: {wall_ms:.4f} ms/step wall, {ev_ms:.4f} ms/step events")
-
-    flops = wl.flops
-    comp = sum(synth.compulsory_bytes(wl, w) for w in wl.waves)
-    value = flops / (wall_ms * 1e-3) / 1e12
-    achieved_gbs = comp / (ev_ms * 1e-3) / 1e9
-    kernel_key = rep["waves"][0]["path"] + "_" + wl.name.split("_")[0]
-    traffic = traffic_from_profiles(kernel_key)
-    w0 = wl.waves[0]
-    out = {
-        "metric": "effective TFLOP/s (2*nnz*batch) + achieved HBM GB/s per wave, 1xMI355X",
-        "value": round(value, 4),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16 (fp32 accumulate)",
-        "data": "synthetic (device-generated counter-hash substrate; numpy PCG64 weights)",
-        "config": {
-            "workload": wl.name,
-            "substrate_positions": wl.substrate,
-            "batch": wl.tokens,
-            "neurons_per_wave": w0.cout,
-            "clusters_per_neuron": w0.K,
-            "S": w0.S,
-            "waves": len(wl.waves),
-            "act": w0.act,
-            "path": rep["waves"][0]["path"],
-        },
-        "hbm_gbs": round(achieved_gbs, 1),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "algorithmic_bytes": comp,
-            "kernel_ms": round(ev_ms, 5),
-            "mfma_tflops_frac": round(flops / (ev_ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4),
-        },
-    }
+    # Default: the headline (config 2) plus every other configuration at its full size.
+    head = bench_wave(2, args.steps, args.warmup)
+    out = _envelope(head, args, WAVE_DATA)
+    configs = {}
+    for cfg in (1, 3, 4):
+        rec = bench_wave(cfg, args.steps, args.warmup)
+        configs[f"c{cfg}"] = {k: v for k, v in rec.items() if not k.startswith("_") and k != "metric"}
+    rec = bench_llm(1, 1, eager)
+    configs["c5"] = {k: v for k, v in rec.items() if k != "metric"}
+    configs["c5"]["steps"], configs["c5"]["warmup"] = 1, 1
+    out["configs"] = configs
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(wl)
+        out["cpu_baseline"] = cpu_baseline(head["_wl"])
         log(f"[bench] cpu baseline {out['cpu_baseline']}")
     print(json.dumps(out), flush=True)
 

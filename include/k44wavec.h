@@ -201,6 +201,13 @@ int wavec_k44_f16_forward_token64(void *Y, const void *X, const uint32_t *cluste
                                   const void *cluster_weights_wmma, const void *neuron_bias,
                                   uint32_t batch_size, uint32_t Cin, uint32_t Cout,
                                   uint32_t B_vec16, uint32_t cluster_size, void *stream);
+/* Stand-alone argmax over caller-owned device memory (the decode plans' ARGMAX_1D op, no
+ * reference counterpart): ids[t] = the lowest channel c with the largest logits[c * stride + t]
+ * (fp16), for t < tokens; logits [vocab][stride], stride a multiple of 64, tokens <= stride.
+ * Two passes; the per-chunk (value, index) partials live in a workspace the library allocates
+ * and frees on `stream` for the call (hipMallocAsync / hipFreeAsync).  Asynchronous. */
+int wavec_argmax_f16(uint32_t *ids, const void *logits, uint32_t vocab, uint32_t stride,
+                     uint32_t tokens, void *stream);
 /* GPU weight interleave, replaces interleave_weights_cluster16_wmma_gpu_kernel
  * (kernel44_immutable.cuh:261-267, kernels/rocm/kernel44_rocm_pack.cuh:285-290): row-major
  * [num_output_neurons][8*B_vec8] fp16 (vectors of 8) -> WMMA vector order; neurons % 16 == 0,
@@ -209,8 +216,39 @@ int wavec_interleave_weights_wmma(void *dst_wmma, const void *src_compact,
                                   uint32_t num_output_neurons, uint32_t B_vec8, void *stream);
 
 /* JSON: per wave the kernel path taken and why, its segment schedule (K, S, step) and
- * accounting (flops, distinct substrate rows).  "{}" before a successful init. */
+ * accounting (flops, distinct substrate rows); per token op whether it was folded; the group
+ * launches; "runs": the whole-plan schedule as lists of plan command indices.  "{}" before a
+ * successful init. */
 const char *wavec_gpu_exec_report_json(void *handle);
+
+/* Runs [first_run, first_run + n_runs) of the whole-plan schedule (the "runs" of the report:
+ * token ops, VALU waves and group launches, with folded multiplies and fused RMSNorm + token
+ * shift exactly as wavec_gpu_execute launches them) and waits for them.  Lets a caller check the
+ * whole-plan execution run by run.  No reference counterpart. */
+int wavec_gpu_execute_runs(void *handle, int first_run, int n_runs);
+/* Strided canvas read: `cols` elements from each of `rows` rows, row r starting at
+ * elem_off + r * row_stride, packed into dst [rows][cols].  The range must lie inside the
+ * canvas allocation. */
+int wavec_gpu_read_canvas_2d(void *handle, unsigned long long elem_off, unsigned long long rows,
+                             unsigned long long row_stride, unsigned long long cols,
+                             uint16_t *dst);
+
+/* Process-wide executor tuning switches, for A/B tests and benchmarks (no reference
+ * counterpart).  Every switch is -1 (the executor's own choice) until set; a value is read when
+ * a plan is initialised.  No switch changes what a plan computes.  Keys:
+ *   "path" 0 VALU for every wave / 1 MFMA (init fails where no MFMA tiling exists);
+ *   "dma" 0 register-staged MFMA tile instead of the LDS ring; "dma_stages" 2 | 4;
+ *   "nt" 0 | 1 non-temporal gather loads; "splitk" 0 no split-K on wide MFMA waves;
+ *   "lane8" 0 | 1 tokens per VALU lane 4 | 8; "ksplit" 1 | 4 waves per neuron (VALU);
+ *   "stream_kernel" 0 | 1; "narrow" 0 no narrow MFMA kernel; "narrow_chunk" >= 16 k-steps;
+ *   "group" 0 no group launches; "group_split" 0 groups keep their members' split-K;
+ *   "fuse" 0 no folded multiplies or RMSNorm + token-shift kernels; "sort" 0 segments in
+ *   index-row order; "wlds" 0 VALU weights read per batch; "t64_ring" 0 | 1 Token64 kernel.
+ * wavec_set_tuning returns -1 for an unknown key or a value < -1; wavec_get_tuning returns the
+ * value or -2 for an unknown key. */
+int wavec_set_tuning(const char *key, int value);
+int wavec_get_tuning(const char *key);
+void wavec_reset_tuning(void);
 
 #ifdef __cplusplus
 }

@@ -101,10 +101,14 @@ def upconv2x2_f64(x: np.ndarray, w: np.ndarray, b) -> np.ndarray:
 
 @dataclass
 class Layout2D:
-    """Padded-plane layout of a 2-D tensor (K44ResDesc::init, non-token64 modes)."""
+    """Padded-plane layout of a 2-D tensor (K44ResDesc::init).  tok64: the 64-frame interleaved
+    image layout (k44_plan_types.hpp:576-598): pixel (y, x) of frame f at c*channel_stride +
+    (f//64)*64*single_stride + ((y+1)*W_pad + x+1)*64 + f%64, frames a multiple of 64 (64-frame
+    blocks 64*single_stride apart)."""
     H: int
     W: int
     frames: int = 1
+    tok64: bool = False
 
     @property
     def aligned(self) -> bool:
@@ -131,4 +135,8 @@ class Layout2D:
         c = np.arange(C)[None, :, None, None]
         y = np.arange(self.H)[None, None, :, None]
         x = np.arange(self.W)[None, None, None, :]
+        if self.tok64:
+            assert self.frames % 64 == 0
+            return (c * self.channel_stride + (f // 64) * 64 * self.single_stride
+                    + ((y + 1) * self.W_pad + x + 1) * 64 + f % 64)
         return (c * self.channel_stride + f * self.single_stride + (y + 1) * self.W_pad + 4 + x)

@@ -12,6 +12,9 @@ Reference citations:
             y = gate * up (SiLU fused into the gate projection's epilogue,
             wavec/k44_wave_compiler.hpp:1024-1049 emits SWIGLU_MUL_1D after it)
   project   the K44 wave of wave_oracle.c (orc_wave_f64) on a compact canvas
+  project_dense_f64
+            the same projection as one float64 matrix product (for full-size checks, where the
+            scalar orc_wave_f64 is too slow); pinned against `project` in tests/test_llm_oracle.py
   token_shift, embed, argmax: build extensions with no reference counterpart; pinned in
             tests/test_llm_oracle.py against brute-force loops and closed forms.
 """
@@ -21,6 +24,7 @@ from typing import Dict, List, Optional
 import numpy as np
 
 from . import oracle as orc
+from .cnn_oracle import act as act_f64
 
 F16 = np.float16
 
@@ -112,6 +116,33 @@ def project(x: np.ndarray, starts: np.ndarray, S: int, tile: int, w: np.ndarray,
     seg = (starts.astype(np.uint64) * np.uint64(T)).ravel()
     out = orc.wave_f64(canvas, seg, w, b, None, K, S, tile, T, T, T, act, res_off=res_off)
     return out if f64 else out.astype(F16)
+
+
+def project_dense_f64(x: np.ndarray, starts: np.ndarray, S: int, w: np.ndarray, b: np.ndarray,
+                      act, res: Optional[np.ndarray] = None, block: int = 4096) -> np.ndarray:
+    """`project` with per-neuron clusters (tile 1), before the fp16 store, computed as one float64
+    matrix product: neuron j's K disjoint clusters are scattered into row j of a dense [cout, D]
+    weight matrix, v = W x + b, y = act(v) [+ res].  Rows are processed in blocks of `block`."""
+    D, T = x.shape
+    cout, K = starts.shape
+    cols = (starts.astype(np.int64)[:, :, None] + np.arange(S, dtype=np.int64)).reshape(cout, K * S)
+    if cols.size and cols.max() >= D:
+        raise ValueError("a cluster reaches past the input rows")
+    srt = np.sort(cols, axis=1)
+    if np.any(srt[:, 1:] == srt[:, :-1]):
+        raise ValueError("a neuron reads one input row twice (clusters overlap)")
+    xf = x.astype(np.float64)
+    out = np.empty((cout, T), dtype=np.float64)
+    for r0 in range(0, cout, block):
+        r1 = min(cout, r0 + block)
+        Wd = np.zeros((r1 - r0, D), dtype=np.float64)
+        np.put_along_axis(Wd, cols[r0:r1], w[r0:r1].astype(np.float64), axis=1)
+        v = Wd @ xf + b[r0:r1].astype(np.float64)[:, None]
+        y = act_f64(v, act)
+        if res is not None:
+            y = y + res[r0:r1].astype(np.float64)
+        out[r0:r1] = y
+    return out
 
 
 @dataclass

@@ -219,31 +219,44 @@ static float orc_act_f32(float v, int act) {
  *   sel      neuron indices to evaluate (n_sel of them); out [n_sel][tokens] fp64, pre-rounding.
  * Returns 0.
  * ------------------------------------------------------------------------------------------- */
+/* Every fp16 bit pattern as a double (orc_f16_to_f32 widened; exact). */
+static double g_f16_f64[65536];
+static int g_f16_f64_ready = 0;
+
+static void f16_table_init(void) {
+    if (g_f16_f64_ready) return;
+    for (uint32_t h = 0; h < 65536u; ++h) g_f16_f64[h] = (double)orc_f16_to_f32((uint16_t)h);
+    g_f16_f64_ready = 1;
+}
+
 int orc_wave_f64(const uint16_t *canvas, const uint64_t *seg, const uint16_t *w,
                  const uint16_t *bias, const uint16_t *cmap, uint32_t K, uint32_t S,
                  uint32_t cluster, uint64_t step, uint32_t tokens, uint64_t out_stride,
                  int act, int has_residual, uint64_t res_off, const uint32_t *sel,
                  uint32_t n_sel, double *out) {
     const uint64_t KS = (uint64_t)K * S;
+    const double *tab = g_f16_f64;
+    f16_table_init();
+    /* Per neuron and token: acc = bias, then + w*x over k (outer) and s (inner), in that order;
+     * the token loop is innermost so that a whole row of X is consumed per synapse. */
 #pragma omp parallel for schedule(dynamic, 4)
     for (int64_t q = 0; q < (int64_t)n_sel; ++q) {
         uint32_t j = sel[q];
         const uint64_t *rs = seg + (uint64_t)(j / cluster) * K;
         const uint16_t *wj = w + (uint64_t)j * KS;
-        double b = bias ? (double)orc_f16_to_f32(bias[j]) : 0.0;
+        double b = bias ? tab[bias[j]] : 0.0;
         uint64_t oj = cmap ? cmap[j] : j;
+        double *acc = out + (uint64_t)q * tokens;
+        for (uint32_t m = 0; m < tokens; ++m) acc[m] = b;
+        for (uint32_t k = 0; k < K; ++k)
+            for (uint32_t s = 0; s < S; ++s) {
+                const double wv = tab[wj[(uint64_t)k * S + s]];
+                const uint16_t *xr = canvas + rs[k] + (uint64_t)s * step;
+                for (uint32_t m = 0; m < tokens; ++m) acc[m] += wv * tab[xr[m]];
+            }
         for (uint32_t m = 0; m < tokens; ++m) {
-            double acc = b;
-            for (uint32_t k = 0; k < K; ++k)
-                for (uint32_t s = 0; s < S; ++s) {
-                    double wv = (double)orc_f16_to_f32(wj[(uint64_t)k * S + s]);
-                    double xv = (double)orc_f16_to_f32(canvas[rs[k] + (uint64_t)s * step + m]);
-                    acc += wv * xv;
-                }
-            double r = has_residual
-                           ? (double)orc_f16_to_f32(canvas[res_off + oj * out_stride + m])
-                           : 0.0;
-            out[(uint64_t)q * tokens + m] = cmap ? orc_act(acc + r, act) : orc_act(acc, act) + r;
+            double r = has_residual ? tab[canvas[res_off + oj * out_stride + m]] : 0.0;
+            acc[m] = cmap ? orc_act(acc[m] + r, act) : orc_act(acc[m], act) + r;
         }
     }
     return 0;

@@ -320,8 +320,10 @@ struct K44ResDesc {
     // fp16 element offset of (channel, y, x, frame) inside a tensor region.
     uint32_t canvas_offset(uint32_t ch, uint32_t y, uint32_t x, uint32_t bf = 0u) const {
         if (is_1d_tokens) return ch * channel_stride + bf * single_stride + x;
+        // 64-frame blocks are 64 * single_stride apart (the reference's (bf / 64) *
+        // single_stride would put block 1 inside block 0's plane; equal for one block).
         if (is_image_token64)
-            return ch * channel_stride + (bf / 64u) * single_stride +
+            return ch * channel_stride + (bf / 64u) * 64u * single_stride +
                    ((y + 1u) * W_pad + x + 1u) * 64u + (bf & 63u);
         return ch * channel_stride + bf * single_stride + (y + 1u) * W_pad + 4u + x;
     }

@@ -1,0 +1,35 @@
+// k44_tuning.hpp — process-wide tuning switches of the wave executor.
+//
+// Every switch defaults to -1: the executor decides from the plan (the measured defaults
+// documented where each decision is made).  Tests and benchmarks force a choice through
+// wavec_set_tuning(key, value) to compare paths that must give identical or tolerance-equal
+// results; the value is read when a plan is initialised (wavec_gpu_init_plan), so a plan keeps
+// the choices it was built with.  No switch changes a plan's semantics, only how it is run.
+#pragma once
+
+namespace k44_host {
+
+enum class Tune : int {
+    Path = 0,      // "path":          0 VALU gather-dot for every wave, 1 MFMA where it applies
+    Dma,           // "dma":           0 = register-staged MFMA tile instead of the LDS ring
+    DmaStages,     // "dma_stages":    2 or 4 LDS ring stages
+    NonTemporal,   // "nt":            0 / 1 non-temporal gather loads
+    SplitK,        // "splitk":        0 = no split-K on wide MFMA waves
+    Lane8,         // "lane8":         0 / 1 eight tokens per lane in the VALU kernels
+    KSplit,        // "ksplit":        1 or 4 waves per neuron in the VALU kernel
+    StreamKernel,  // "stream_kernel": 0 / 1 streaming VALU kernel (output rows staged in LDS)
+    Narrow,        // "narrow":        0 = no narrow (<= 16 token) MFMA kernel
+    NarrowChunk,   // "narrow_chunk":  longest contraction chunk of the narrow kernel, >= 16 k-steps
+    Group,         // "group":         0 = every MFMA wave launched alone
+    GroupSplit,    // "group_split":   0 = group launches keep their members' split-K
+    Fuse,          // "fuse":          0 = no folded multiplies / RMSNorm+token-shift kernels
+    SortSegments,  // "sort":          0 = segments in index-row order (not address order)
+    WeightsInLds,  // "wlds":          0 = 8-token VALU kernel reads weights per batch
+    Token64Ring,   // "t64_ring":      0 per-wave Token64 kernel, 1 64-neuron ring kernel
+    Count
+};
+
+// Current value of a switch (-1 = automatic).
+int tune(Tune t);
+
+}  // namespace k44_host

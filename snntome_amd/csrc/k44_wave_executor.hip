@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -27,10 +28,30 @@
 #include <numeric>
 #include <sstream>
 
+#include "k44_tuning.hpp"
 #include "k44_wave_compiler.hpp"
 #include "k44wavec.h"
 #include "kernels/k44_launch.hpp"
 #include "kernels/k44_spatial.hpp"
+
+namespace k44_host {
+
+namespace {
+// Switch values (-1 = automatic) and their wavec_set_tuning keys, in Tune order.
+std::atomic<int> g_tune[(int)Tune::Count];
+const char *const kTuneKeys[(int)Tune::Count] = {
+    "path", "dma", "dma_stages", "nt", "splitk", "lane8", "ksplit", "stream_kernel", "narrow",
+    "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring"};
+struct TuneInit {
+    TuneInit() {
+        for (auto &v : g_tune) v.store(-1);
+    }
+} g_tune_init;
+}  // namespace
+
+int tune(Tune t) { return g_tune[(int)t].load(std::memory_order_relaxed); }
+
+}  // namespace k44_host
 
 namespace {
 
@@ -90,6 +111,9 @@ struct WaveExec {
     bool lane8 = false;        // VALU: 8 tokens (16-byte loads) per lane
     bool stream_loads = false; // VALU: non-temporal X / weight loads (gathered rows >> caches)
     bool stream_kernel = false; // VALU: k44_gather_stream_kernel (output rows staged in LDS)
+    bool weights_in_lds = true; // VALU 8-token kernel: neuron weights staged in LDS
+    bool misaligned = false;    // segment starts off the 4-element grid (token-shifted taps)
+    bool phase_order = false;   // synapses regrouped by token phase (segment_rows)
     uint32_t part_tokens = 0;  // row length of split-K partials (16 narrow, tokens wide)
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
     uint64_t step = 1;
@@ -181,6 +205,7 @@ struct AuxExec {
     bool fused = false;  // SWIGLU_MUL_1D folded into its consumers' gathers, or TOKEN_SHIFT_1D
                          // run by the RMSNorm before it (not launched)
     size_t shift_with = SIZE_MAX;  // RMSNORM_1D: the decode token shift it runs (whole plans)
+    std::string fuse_note;         // SWIGLU_MUL_1D: why it was or was not folded (report)
     float eps = 1e-5f;
     DevBuf<__half> table;  // gamma (RMSNORM), mix (TOKEN_SHIFT), embedding table (EMBED)
     // 2-D spatial commands (S2D, pools, upsample, scatter-upconv): channel count C, planes
@@ -189,7 +214,8 @@ struct AuxExec {
 };
 
 k44dev::Plane2D plane_of(const k44_host::K44ResDesc &L) {
-    return k44dev::Plane2D{L.H, L.W, L.W_pad, L.batch_size, L.single_stride, L.channel_stride};
+    return k44dev::Plane2D{L.H, L.W, L.W_pad, L.batch_size, L.single_stride, L.channel_stride,
+                           L.is_image_token64 ? 1u : 0u};
 }
 
 // Canvas elements allocated past the plan's canvas: the misaligned 2-D gathers read up to 3
@@ -222,9 +248,11 @@ struct K44GpuExecutorState {
     // wave, or a group of independent MFMA waves (kind 0 / 1 / 2, index).
     std::vector<std::pair<bool, size_t>> ops;
     std::vector<std::pair<int, size_t>> runs;
+    std::vector<size_t> wave_cmd, aux_cmd;  // plan command index of every wave / aux command
     std::vector<std::unique_ptr<MfmaGroupExec>> groups;
     DevBuf<__half> canvas;
     DevBuf<uint32_t> ids, history, step_ctr;  // token ids (EMBED / ARGMAX), greedy history
+    DevBuf<uint16_t> stage;  // packed strided canvas reads (wavec_gpu_read_canvas_2d)
     uint32_t id_tokens = 0, hist_steps = 0;
     // Scratch shared by the commands of the plan (they run in order on one stream): split-K
     // partials of MFMA waves, per-chunk (value, index) partials of ARGMAX.
@@ -249,13 +277,18 @@ struct K44GpuExecutorState {
     }
 
     void free_all() {
+        // Nothing queued on the executor stream may still use the graph or the buffers.
+        if (stream) (void)hipStreamSynchronize(stream);
         drop_graph();
         groups.clear();
         waves.clear();
         aux.clear();
         ops.clear();
         runs.clear();
+        wave_cmd.clear();
+        aux_cmd.clear();
         ids.reset();
+        stage.reset();
         history.reset();
         step_ctr.reset();
         id_tokens = hist_steps = 0;
@@ -274,37 +307,68 @@ struct K44GpuExecutorState {
     // Index rows -> dendritic segments.  Canvas element offsets e[s] of a row are split at
     // every s where e[s] != e[s-1] + step; the segment length S is the gcd of B_raw and all
     // split points, so every row is K = B_raw / S runs of S consecutive positions.
+    // With `reorder`, a row whose synapses in index order give segments shorter than 32
+    // positions is also tried in phase order — synapses sorted by (offset mod step, offset) —
+    // and that order is kept (perm[r * B_raw + s] = index-order synapse of position s) when it
+    // gives longer segments.  A 1-D convolution of kw taps over contiguous channels is such a
+    // row: in index order every synapse is its own segment (channel-major, tap-minor offsets
+    // ch_base + dx), in phase order it is kw segments of cin consecutive channels.
     static void segment_rows(const K44ExecCmd &c, uint64_t step, uint32_t &S_out,
-                             std::vector<uint64_t> &starts) {
+                             std::vector<uint64_t> &starts, std::vector<uint32_t> &perm,
+                             bool reorder) {
         const uint32_t B = c.B, b_raw = c.B_raw;
         const size_t rows = c.h_idx.size() / B;
-        auto off = [&](size_t r, uint32_t s) -> uint64_t {
-            const uint64_t v = c.h_idx[r * B + s];
-            return c.idx_mode == 1u ? c.x_base_off + v * c.idx_stride : c.x_base_off + v;
+        std::vector<uint64_t> off((size_t)rows * b_raw);
+        for (size_t r = 0; r < rows; ++r)
+            for (uint32_t s = 0; s < b_raw; ++s) {
+                const uint64_t v = c.h_idx[r * B + s];
+                off[r * b_raw + s] = c.idx_mode == 1u ? c.x_base_off + v * c.idx_stride
+                                                      : c.x_base_off + v;
+            }
+        auto seg_len = [&](const std::vector<uint64_t> &o) {
+            uint32_t S = b_raw;
+            for (size_t r = 0; r < rows && S > 1u; ++r) {
+                const uint64_t *e = o.data() + r * b_raw;
+                for (uint32_t s = 1; s < b_raw; ++s)
+                    if (e[s] != e[s - 1] + step) S = std::gcd(S, s);
+            }
+            return S;
         };
-        uint32_t S = b_raw;
-        for (size_t r = 0; r < rows && S > 1u; ++r) {
-            uint64_t prev = off(r, 0);
-            for (uint32_t s = 1; s < b_raw; ++s) {
-                const uint64_t e = off(r, s);
-                if (e != prev + step) S = std::gcd(S, s);
-                prev = e;
+        uint32_t S = seg_len(off);
+        perm.clear();
+        if (reorder && S < 32u && b_raw > 1u && step > 1u) {
+            std::vector<uint32_t> pm((size_t)rows * b_raw);
+            std::vector<uint64_t> po(off.size());
+            for (size_t r = 0; r < rows; ++r) {
+                uint32_t *q = pm.data() + r * b_raw;
+                const uint64_t *e = off.data() + r * b_raw;
+                for (uint32_t s = 0; s < b_raw; ++s) q[s] = s;
+                std::stable_sort(q, q + b_raw, [&](uint32_t x, uint32_t y) {
+                    const uint64_t px = e[x] % step, py = e[y] % step;
+                    return px != py ? px < py : e[x] < e[y];
+                });
+                for (uint32_t s = 0; s < b_raw; ++s) po[r * b_raw + s] = e[q[s]];
+            }
+            const uint32_t Sp = seg_len(po);
+            if (Sp > S) {
+                S = Sp;
+                off.swap(po);
+                perm.swap(pm);
             }
         }
         const uint32_t K = b_raw / S;
         starts.resize(rows * K);
         for (size_t r = 0; r < rows; ++r)
-            for (uint32_t k = 0; k < K; ++k) starts[r * K + k] = off(r, k * S);
+            for (uint32_t k = 0; k < K; ++k) starts[r * K + k] = off[r * b_raw + (size_t)k * S];
         S_out = S;
     }
 
     // VALU gathers whose distinct rows are far beyond the caches (>= 512 MiB, twice the MALL)
     // read their rows and weights with the non-temporal load policy: config 2 (random 8 KiB
     // segments of a 20 GB substrate) 391 -> 373 us.  Cache-resident substrates keep the default
-    // policy.  K44WAVEC_NT=0/1 forces it.
+    // policy.  Tuning switch "nt" forces either.
     static bool streaming_gather(const WaveExec &wx) {
-        const char *nt = std::getenv("K44WAVEC_NT");
-        if (nt) return std::string(nt) == "1";
+        if (tune(Tune::NonTemporal) >= 0) return tune(Tune::NonTemporal) == 1;
         return wx.unique_rows * (uint64_t)wx.tokens * 2u >= (512ull << 20);
     }
 
@@ -342,8 +406,10 @@ struct K44GpuExecutorState {
             throw std::runtime_error("wave '" + c.name + "': unknown activation id");
 
         std::vector<uint64_t> starts;
-        segment_rows(c, wx.step, wx.S, starts);
+        std::vector<uint32_t> perm;
+        segment_rows(c, wx.step, wx.S, starts, perm, true);
         wx.K = c.B_raw / wx.S;
+        wx.phase_order = !perm.empty();
 
         // Row-major [Cout][B] weights from the on-disk WMMA order; padded synapses must be 0.
         std::vector<uint16_t> wraw((size_t)c.Cout * c.B);
@@ -354,13 +420,21 @@ struct K44GpuExecutorState {
                 if (wraw[j * c.B + s] != 0u)
                     throw std::runtime_error("wave '" + c.name +
                                              "': non-zero weight on a padded synapse");
+        if (!perm.empty()) {  // synapses in the segment order chosen above
+            std::vector<uint16_t> tmp(c.B_raw);
+            for (size_t j = 0; j < c.Cout; ++j) {
+                const uint32_t *q = perm.data() + (j / c.cluster_size) * c.B_raw;
+                uint16_t *wj = wraw.data() + j * c.B;
+                for (uint32_t s = 0; s < c.B_raw; ++s) tmp[s] = wj[q[s]];
+                std::memcpy(wj, tmp.data(), (size_t)c.B_raw * 2u);
+            }
+        }
 
         // Address-sorted segments: every index row visits its segments in ascending canvas
         // order (weight columns permuted with them; only the fp32 summation order changes), so
         // concurrently running rows sweep the substrate together and overlapping segments of
         // different rows are read close in time (cache reuse instead of a second HBM read).
-        const char *sort_env = std::getenv("K44WAVEC_SORT");
-        wx.sorted_segments = wx.K > 1u && !(sort_env && std::string(sort_env) == "0");
+        wx.sorted_segments = wx.K > 1u && tune(Tune::SortSegments) != 0;
         if (wx.sorted_segments) {
             std::vector<uint32_t> order(wx.K);
             std::vector<uint64_t> st(wx.K);
@@ -385,12 +459,15 @@ struct K44GpuExecutorState {
             }
         }
 
+        // Token-shifted taps: segment starts off the 4-element (8-byte) grid take the funnel-
+        // shift gather, whose second word reads up to 3 elements past a row's last token.
+        for (uint64_t s0 : starts) wx.misaligned = wx.misaligned || s0 % 4u != 0u;
         // Host-side bounds check of every canvas element the kernel may touch.
         const uint64_t n_canvas = plan_meta.canvas_elems;
         uint64_t x_hi = 0;
         for (uint64_t s0 : starts) x_hi = std::max(x_hi, s0);
         x_hi += (uint64_t)(wx.S - 1u) * wx.step + wx.tokens;
-        if (x_hi > n_canvas)
+        if (x_hi > n_canvas + (wx.misaligned ? kCanvasSlack - 4u : 0u))
             throw std::runtime_error("wave '" + c.name + "': gather reaches past the canvas");
         uint64_t oj_hi = c.Cout - 1u;
         if (c.has_cout_map) {
@@ -405,16 +482,13 @@ struct K44GpuExecutorState {
         if (wx.tokens % 64u != 0u || wx.out_stride % 4u != 0u || wx.y_off % 4u != 0u ||
             wx.res_off % 4u != 0u || wx.step % 4u != 0u)
             throw std::runtime_error("wave '" + c.name + "': canvas rows not 8-byte aligned");
-        for (uint64_t s0 : starts)
-            if (s0 % 4u != 0u)
-                throw std::runtime_error("wave '" + c.name +
-                                         "': token-shifted (unaligned) gathers not supported yet");
 
         {
             Ranges rd, wr;
             rd.reserve(starts.size() + c.Cout);
+            const uint64_t over = wx.misaligned ? 4u : 0u;  // funnel-shift words past the row
             for (uint64_t s0 : starts)
-                rd.push_back({s0, s0 + (uint64_t)(wx.S - 1u) * wx.step + wx.tokens});
+                rd.push_back({s0, s0 + (uint64_t)(wx.S - 1u) * wx.step + wx.tokens + over});
             for (uint32_t j = 0; j < c.Cout; ++j) {
                 const uint64_t oj = c.has_cout_map ? (uint64_t)c.h_cout_map[j] : (uint64_t)j;
                 if (c.has_cout_map && oj == 0xffffu) continue;
@@ -469,15 +543,15 @@ struct K44GpuExecutorState {
         // Path selection.  MFMA needs a real dense contraction: >= 16 neurons sharing every
         // index row (tile NT in {16, 32, 64, 128}), segments of whole 32-deep K-steps and
         // 16-byte aligned rows.  Everything else is a batched GEMV: VALU gather-dot.
-        const char *force = std::getenv("K44WAVEC_PATH");
+        const int force = tune(Tune::Path);  // -1 auto, 0 VALU, 1 MFMA
         bool aligned8 = wx.step % 8u == 0u;
         for (uint64_t s0 : starts) aligned8 = aligned8 && s0 % 8u == 0u;
         const uint32_t cl = c.cluster_size;
         const bool nt_ok = cl == 16u || cl == 32u || cl == 64u || cl == 128u;
         const bool mfma_ok = nt_ok && wx.S % 32u == 0u && aligned8 && wx.tokens % 64u == 0u;
-        wx.mfma = mfma_ok && !(force && std::string(force) == "valu");
-        if (force && std::string(force) == "mfma" && !mfma_ok)
-            throw std::runtime_error("wave '" + c.name + "': K44WAVEC_PATH=mfma but the wave has "
+        wx.mfma = mfma_ok && force != 0;
+        if (force == 1 && !mfma_ok)
+            throw std::runtime_error("wave '" + c.name + "': tuning path=mfma but the wave has "
                                      "no dense MFMA tiling (cluster/segment/alignment)");
         if (wx.mfma) {
             wx.path = "mfma_tile";
@@ -487,30 +561,27 @@ struct K44GpuExecutorState {
                      " contraction per tile on v_mfma_f32_16x16x32_f16";
             wx.mt = pick_mt(wx.tokens);
             wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
-            const char *nw_env = std::getenv("K44WAVEC_NARROW");
-            wx.narrow = Lo.W <= 16u && !(nw_env && std::string(nw_env) == "0");
+            wx.narrow = Lo.W <= 16u && tune(Tune::Narrow) != 0;
             wx.part_tokens = wx.narrow ? 16u : wx.tokens;
             // 512-token workgroups of 32/64-neuron tiles stream through an LDS ring filled by
             // direct loads (3 stages in flight per workgroup instead of 1).
-            const char *dma_env = std::getenv("K44WAVEC_DMA");
             wx.dma = !wx.narrow && wx.mt == 512u && (cl == 32u || cl == 64u) &&
-                     !(dma_env && std::string(dma_env) == "0");
+                     tune(Tune::Dma) != 0;
             if (wx.dma) {
                 wx.path = "mfma_dma";
                 wx.why += " (512-token workgroups: 4-stage LDS ring filled by global_load_lds)";
                 wx.rows_per_stage = 32u;
                 // Config 3 measured the same with either load policy (363 TFLOP/s): default
-                // policy unless K44WAVEC_NT=1.
-                const char *nt = std::getenv("K44WAVEC_NT");
-                wx.stream_loads = nt && std::string(nt) == "1";
+                // policy unless tuning switch "nt" is 1.
+                wx.stream_loads = tune(Tune::NonTemporal) == 1;
                 // Ring depth: gathers from inputs that stay in the caches (distinct gathered
                 // bytes <= 256 MB, the last-level cache) take 2-stage rings, two workgroups per
                 // CU — config-5 prefill 26.9 -> 20.9 ms; gathers from HBM keep 4 stages and one
                 // workgroup per CU — config 3: 364 us, against 379 us with 2 stages.
                 const double gathered = (double)wx.unique_rows * wx.tokens * 2.0;
                 wx.dshape.nbuf = gathered <= 256.0 * 1048576.0 ? 2u : 4u;
-                const char *nb = std::getenv("K44WAVEC_DMA_NBUF");
-                if (nb && (std::atoi(nb) == 2 || std::atoi(nb) == 4)) wx.dshape.nbuf = (uint32_t)std::atoi(nb);
+                if (tune(Tune::DmaStages) == 2 || tune(Tune::DmaStages) == 4)
+                    wx.dshape.nbuf = (uint32_t)tune(Tune::DmaStages);
                 wx.dshape.stream_loads = wx.stream_loads;
                 wx.why += "; " + std::to_string(wx.dshape.nbuf) + "-stage ring";
             }
@@ -527,8 +598,8 @@ struct K44GpuExecutorState {
                     // decode (per step): 1.196 ms, against 1.219 ms when waves of >= 32 tiles
                     // stay unsplit (fused epilogue), 1.28 ms with 8-k-step chunks, 1.46 ms
                     // without split.
-                    const char *ce = std::getenv("K44WAVEC_NARROW_CHUNK");
-                    const uint32_t cmax = ce ? std::max(16, std::atoi(ce)) : 48u;
+                    const int ce = tune(Tune::NarrowChunk);
+                    const uint32_t cmax = ce > 0 ? (uint32_t)std::max(16, ce) : 48u;
                     want = (ksteps + cmax - 1u) / cmax;
                     want = std::max(want, std::min((128u + (uint32_t)rows - 1u) / (uint32_t)rows,
                                                    (ksteps + 15u) / 16u));
@@ -545,13 +616,12 @@ struct K44GpuExecutorState {
             } else {
                 const uint32_t stages = c.B_raw / wx.rows_per_stage;
                 const uint64_t wgs = (uint64_t)rows * (wx.tokens / wx.mt);
-                const char *sk_env = std::getenv("K44WAVEC_SPLITK");
                 // Few workgroups: split the contraction.  Each split adds a partial plane of
                 // 4 * cout * tokens bytes, so prefill-sized token counts split at most 8 ways
                 // with >= 4 stages per workgroup; small token counts up to 32 ways.
                 const bool wide_tokens = wx.tokens >= 1024u;
                 uint32_t want = wgs >= 256u ? 1u : (uint32_t)((512u + wgs - 1u) / wgs);
-                if (sk_env && std::string(sk_env) == "0") want = 1u;
+                if (tune(Tune::SplitK) == 0) want = 1u;
                 want = std::min(want, wide_tokens ? 8u : 32u);
                 const uint32_t min_stages = wide_tokens ? 4u : 1u;
                 want = std::max(1u, std::min(want, std::max(1u, stages / min_stages)));
@@ -583,36 +653,39 @@ struct K44GpuExecutorState {
                      : wx.S % 32u != 0u
                          ? "segments of " + std::to_string(wx.S) +
                                " positions do not fill 32-deep MFMA K-steps"
-                         : (force ? std::string("forced by K44WAVEC_PATH")
+                         : (force == 0 ? std::string("forced by tuning switch path=0")
                                   : std::string("segment rows not 16-byte aligned"));
+            if (wx.misaligned)
+                wx.why += "; token-shifted segment starts: funnel-shift gathers, 4 tokens per lane";
+            if (wx.phase_order) wx.why += "; synapses regrouped by token phase";
             wx.slab = pick_slab(wx.tokens);
             {
                 // 8 tokens per lane (16-byte loads) when the rows it gathers fit the 256 MB MALL
                 // (measured: configs 1 and 4 13-28 % faster); 4 tokens per lane for HBM-bound
                 // gathers (config 2: 2.5 % faster).  16-byte accesses need 8-element alignment.
-                const char *l8 = std::getenv("K44WAVEC_LANE8");
-                const bool want8 = l8 ? std::string(l8) == "1"
-                                      : wx.unique_rows * (uint64_t)wx.tokens * 2u < (256ull << 20);
+                const bool want8 = tune(Tune::Lane8) >= 0
+                                       ? tune(Tune::Lane8) == 1
+                                       : wx.unique_rows * (uint64_t)wx.tokens * 2u < (256ull << 20);
                 bool ok8 = wx.out_stride % 8u == 0u && wx.y_off % 8u == 0u &&
-                           wx.res_off % 8u == 0u && wx.step % 8u == 0u;
+                           wx.res_off % 8u == 0u && wx.step % 8u == 0u && !wx.misaligned;
                 for (uint64_t s0 : starts) ok8 = ok8 && s0 % 8u == 0u;
                 wx.lane8 = want8 && ok8;
                 wx.stream_loads = streaming_gather(wx);
+                wx.weights_in_lds = tune(Tune::WeightsInLds) != 0;
             }
             // Four waves per neuron (segments round-robin) for few-segment neurons gathering from
             // HBM; one wave per neuron when the rows are cache resident (8 tokens per lane,
             // weights in LDS): config 1 19.2 us against 23.2 us with four.
-            const char *ks_env = std::getenv("K44WAVEC_KSPLIT");
             wx.ksplit = (!wx.lane8 && wx.K >= 2u && wx.K <= 8u) ? 4u : 1u;
-            if (ks_env) wx.ksplit = std::string(ks_env) == "4" ? 4u : 1u;
+            if (tune(Tune::KSplit) >= 0) wx.ksplit = tune(Tune::KSplit) == 4 ? 4u : 1u;
             {
                 // Streaming gathers over 256-token slabs with >= 256 workgroups of 256 neurons:
                 // stage the output rows in LDS and write them after the last gather (writes
                 // interleaved with the random reads cost ~15 % on config 2).
-                const char *sk = std::getenv("K44WAVEC_STREAMK");
                 const bool big = (uint64_t)(c.Cout / 256u) * (wx.tokens / 256u) >= 256u;
+                const int sk = tune(Tune::StreamKernel);
                 wx.stream_kernel = wx.stream_loads && !wx.lane8 && wx.slab == 256u &&
-                                   !wx.has_res && (sk ? std::string(sk) == "1" : big);
+                                   !wx.has_res && !wx.misaligned && (sk >= 0 ? sk == 1 : big);
                 if (wx.stream_kernel) {
                     wx.ksplit = 1u;
                     wx.why += "; streaming kernel: 256 neurons per workgroup, output rows "
@@ -653,12 +726,20 @@ struct K44GpuExecutorState {
     // y_off + out_j*channel_stride + tile_y[t] + m.
     void build_wave2d(const K44ExecCmd &c, WaveExec &wx, const K44ResDesc &Lo,
                       const K44ResDesc &Li) {
-        if (Lo.is_image_token64 || Li.is_image_token64)
-            throw std::runtime_error("wave '" + c.name +
-                                     "': 64-frame interleaved image layouts are not supported");
-        if (Lo.is_1d_tokens || Li.is_1d_tokens || c.res_key_in != c.res_key_out)
+        const bool tok64 = Lo.is_image_token64;
+        if (Li.is_image_token64 != tok64 || Lo.is_1d_tokens || Li.is_1d_tokens)
+            throw std::runtime_error("wave '" + c.name + "': mixed 2-D layouts");
+        // Input layout: the output's, except for the 64-frame interleaved layout's stride-2
+        // convolutions, which gather the input directly (every output pixel reads the input
+        // pixels around twice its coordinates).
+        const bool stride2 = tok64 && c.res_key_in != c.res_key_out;
+        if (!tok64 && c.res_key_in != c.res_key_out)
             throw std::runtime_error("wave '" + c.name +
                                      "': 2-D wave whose input and output layouts differ");
+        if (stride2 && (Lo.H != (Li.H + 1u) / 2u || Lo.W != (Li.W + 1u) / 2u))
+            throw std::runtime_error("wave '" + c.name + "': stride-2 output size");
+        if (tok64 && (Lo.batch_size % 64u != 0u || Li.batch_size != Lo.batch_size))
+            throw std::runtime_error("wave '" + c.name + "': interleaved frames not whole blocks");
         if (c.h_idx.empty() || c.B == 0u || c.B_raw == 0u || c.h_idx.size() % c.B != 0u)
             throw std::runtime_error("wave '" + c.name + "': missing or malformed index table");
         if (c.h_w_wmma.size() * 8u < (size_t)c.Cout * c.B)
@@ -668,12 +749,15 @@ struct K44GpuExecutorState {
             throw std::runtime_error("wave '" + c.name + "': index rows x cluster != Cout");
         if (c.has_cout_map && c.h_cout_map.size() < c.Cout)
             throw std::runtime_error("wave '" + c.name + "': cout_map shorter than Cout");
-        if (Lo.h_tile_off_X.size() != Lo.num_tiles || Lo.h_tile_off_Y.size() != Lo.num_tiles)
+        if (!tok64 &&
+            (Lo.h_tile_off_X.size() != Lo.num_tiles || Lo.h_tile_off_Y.size() != Lo.num_tiles))
             throw std::runtime_error("wave '" + c.name + "': tile tables missing");
         wx.tile2d = true;
         wx.name = c.name;
         wx.path = "valu_gather_tile";
-        wx.why = "2-D spatial layout: tap-shifted gathers over padded-plane tiles";
+        wx.why = tok64 ? "2-D layout of 64-frame interleaved images: one 64-token tile per pixel "
+                         "(its 64 frames), taps shift whole pixels"
+                       : "2-D spatial layout: tap-shifted gathers over padded-plane tiles";
         wx.cout = c.Cout;
         wx.cluster = c.cluster_size;
         wx.rows = (uint32_t)rows;
@@ -685,21 +769,49 @@ struct K44GpuExecutorState {
         if (wx.act < 0 || wx.act > 5)
             throw std::runtime_error("wave '" + c.name + "': unknown activation id");
         std::vector<uint64_t> starts;
-        segment_rows(c, wx.step, wx.S, starts);
+        std::vector<uint32_t> perm;  // 2-D: index order (the tile kernel handles any alignment)
+        segment_rows(c, wx.step, wx.S, starts, perm, false);
         wx.K = c.B_raw / wx.S;
         wx.plane = plane_of(Lo);
-        wx.masked = Lo.needs_mask ? 1 : 0;
-        wx.tiles = Lo.num_tiles;
-        wx.tiles_per_frame = Lo.tiles_per_frame;
-        wx.tokens = Lo.num_tiles * 64u;
-        wx.out_stride = (uint32_t)Lo.channel_stride;
-        std::vector<uint32_t> tx(Lo.num_tiles), ty(Lo.num_tiles);
-        for (uint32_t t = 0; t < Lo.num_tiles; ++t) {
-            tx[t] = Lo.h_tile_off_X[t];
-            const uint32_t f = t / Lo.tiles_per_frame, tl = t % Lo.tiles_per_frame;
-            ty[t] = Lo.needs_mask ? f * Lo.single_stride + Lo.W_pad + 4u + 64u * tl
-                                  : Lo.h_tile_off_Y[t];
+        std::vector<uint32_t> tx, ty;
+        if (tok64) {
+            // Tile = (64-frame block, output pixel): the pixel's 64 frames at
+            // ((y+1)*W_pad + x+1)*64 of the block; the gather anchor is the input pixel
+            // diagonally before the tap centre, (y-1, x-1) (stride 1) or (2y-1, 2x-1) (stride 2),
+            // to which the index words add ((1+dy)*W_pad + (1+dx))*64.
+            const uint32_t blocks = Lo.batch_size / 64u, f = stride2 ? 2u : 1u;
+            wx.masked = 0;
+            wx.tiles_per_frame = Lo.H * Lo.W;
+            wx.tiles = blocks * wx.tiles_per_frame;
+            const uint64_t hi = (uint64_t)blocks * 64u * std::max(Li.single_stride, Lo.single_stride);
+            if (hi > 0xffffffffull)
+                throw std::runtime_error("wave '" + c.name + "': interleaved plane beyond 32 bits");
+            tx.resize(wx.tiles);
+            ty.resize(wx.tiles);
+            for (uint32_t b = 0; b < blocks; ++b)
+                for (uint32_t y = 0; y < Lo.H; ++y)
+                    for (uint32_t x = 0; x < Lo.W; ++x) {
+                        const size_t t = ((size_t)b * Lo.H + y) * Lo.W + x;
+                        tx[t] = (uint32_t)(b * 64ull * Li.single_stride +
+                                           ((uint64_t)f * y * Li.W_pad + (uint64_t)f * x) * 64u);
+                        ty[t] = (uint32_t)(b * 64ull * Lo.single_stride +
+                                           ((uint64_t)(y + 1u) * Lo.W_pad + x + 1u) * 64u);
+                    }
+        } else {
+            wx.masked = Lo.needs_mask ? 1 : 0;
+            wx.tiles = Lo.num_tiles;
+            wx.tiles_per_frame = Lo.tiles_per_frame;
+            tx.resize(Lo.num_tiles);
+            ty.resize(Lo.num_tiles);
+            for (uint32_t t = 0; t < Lo.num_tiles; ++t) {
+                tx[t] = Lo.h_tile_off_X[t];
+                const uint32_t fr = t / Lo.tiles_per_frame, tl = t % Lo.tiles_per_frame;
+                ty[t] = Lo.needs_mask ? fr * Lo.single_stride + Lo.W_pad + 4u + 64u * tl
+                                      : Lo.h_tile_off_Y[t];
+            }
         }
+        wx.tokens = wx.tiles * 64u;
+        wx.out_stride = (uint32_t)Lo.channel_stride;
         // Host-side bounds check of every element the kernel may touch.
         const uint64_t n_canvas = plan_meta.canvas_elems;
         const uint64_t tx_hi = *std::max_element(tx.begin(), tx.end());
@@ -751,11 +863,13 @@ struct K44GpuExecutorState {
     void build_spatial(const K44ExecCmd &c, AuxExec &ax) {
         const K44ResDesc &Li = plan_meta.res_map.at(c.res_key_in);
         const K44ResDesc &Lo = plan_meta.res_map.at(c.res_key_out);
-        if (Li.is_1d_tokens || Lo.is_1d_tokens || Li.is_image_token64 || Lo.is_image_token64)
-            throw std::runtime_error("command '" + c.name +
-                                     "': needs 2-D single-frame-interleave layouts");
+        if (Li.is_1d_tokens || Lo.is_1d_tokens || Li.is_image_token64 != Lo.is_image_token64)
+            throw std::runtime_error("command '" + c.name + "': needs matching 2-D layouts");
         if (Li.batch_size != Lo.batch_size)
             throw std::runtime_error("command '" + c.name + "': frame counts differ");
+        if (Lo.is_image_token64 && (Lo.batch_size % 64u != 0u || c.type == K44CmdType::S2D_2X2))
+            throw std::runtime_error("command '" + c.name +
+                                     "': not defined on the 64-frame interleaved layout");
         ax.type = c.type;
         ax.name = c.name;
         ax.y_off = c.y_off;
@@ -973,11 +1087,13 @@ struct K44GpuExecutorState {
             if (c.type == K44CmdType::K44_WAVE) {
                 auto wx = std::make_unique<WaveExec>();
                 build_wave(c, *wx);
+                wave_cmd.push_back(ops.size());
                 ops.push_back({true, waves.size()});
                 waves.push_back(std::move(wx));
             } else {
                 auto ax = std::make_unique<AuxExec>();
                 build_aux(c, *ax);
+                aux_cmd.push_back(ops.size());
                 ops.push_back({false, aux.size()});
                 aux.push_back(std::move(ax));
             }
@@ -1054,10 +1170,9 @@ struct K44GpuExecutorState {
     // (the sub-waves of one projection, together covering every row) write it to a private
     // region past the canvas instead, provided nothing but the folded multiplies reads it.
     // Whole-plan execution only: execute_range runs every command as compiled.
-    // K44WAVEC_FUSE=0 disables it.
+    // Tuning switch fuse=0 disables it.
     void fuse_products() {
-        const char *fe = std::getenv("K44WAVEC_FUSE");
-        if (fe && std::string(fe) == "0") return;
+        if (tune(Tune::Fuse) == 0) return;
         const size_t n = ops.size();
         std::vector<Ranges> rd(n), wr(n);
         for (size_t i = 0; i < n; ++i) {
@@ -1111,9 +1226,8 @@ struct K44GpuExecutorState {
             return Rng(o, o + (uint64_t)a.D * a.stride);
         };
         const uint64_t fold_base = (plan_meta.canvas_elems + kCanvasSlack + 63u) / 64u * 64u;
-        const bool dbg = std::getenv("K44WAVEC_FUSE_DEBUG") != nullptr;
         auto note = [&](size_t i, const char *why) {
-            if (dbg) std::fprintf(stderr, "[fuse] %s: %s\n", aux[ops[i].second]->name.c_str(), why);
+            aux[ops[i].second]->fuse_note = why;
         };
         for (size_t i = 0; i < n; ++i) {
             if (!is_mul(i) || aux[ops[i].second]->fused) continue;
@@ -1253,10 +1367,9 @@ struct K44GpuExecutorState {
     // A decode RMSNorm followed directly by the decode token shift of its output runs the shift
     // in the same kernel (whole-plan execution; bit-identical to the two commands): the norm's
     // decode form keeps one channel per thread, so the shift of that channel's tokens follows
-    // in place.  K44WAVEC_FUSE=0 keeps both launches.
+    // in place.  Tuning switch fuse=0 keeps both launches.
     void fuse_norm_shifts() {
-        const char *fe = std::getenv("K44WAVEC_FUSE");
-        if (fe && std::string(fe) == "0") return;
+        if (tune(Tune::Fuse) == 0) return;
         for (size_t i = 0; i + 1u < ops.size(); ++i) {
             if (ops[i].first || ops[i + 1u].first) continue;
             AuxExec &N = *aux[ops[i].second];
@@ -1272,6 +1385,14 @@ struct K44GpuExecutorState {
             uint32_t slices = (256u + chunks - 1u) / chunks;
             slices = std::min(slices, (N.D + 255u) / 256u);
             if ((N.D + slices - 1u) / slices > 256u) continue;
+            // Every workgroup of the fused kernel reads all D rows of the norm's input for its
+            // sums while other workgroups already store shift outputs and state: the canvas
+            // allocator may have given the input's range (dead after the norm) to the shift's
+            // output, so fuse only when the shift writes nothing the norm reads.
+            Ranges rd_n, wr_n, rd_t, wr_t;
+            aux_ranges(N, rd_n, wr_n);
+            aux_ranges(T, rd_t, wr_t);
+            if (ranges_overlap(wr_t, rd_n)) continue;
             N.shift_with = ops[i + 1u].second;
             T.fused = true;
         }
@@ -1280,8 +1401,7 @@ struct K44GpuExecutorState {
     // Plan order -> runs: consecutive MFMA waves of one kernel configuration join a group while
     // no member writes what another reads or writes (checked on canvas element ranges).
     void form_runs() {
-        const char *genv = std::getenv("K44WAVEC_GROUP");
-        const bool grouping = !(genv && std::string(genv) == "0");
+        const bool grouping = tune(Tune::Group) != 0;
         runs.clear();
         groups.clear();
         for (const auto &op : ops) {
@@ -1344,8 +1464,7 @@ struct K44GpuExecutorState {
         // 29.0 -> 27.0 ms).  Decode groups keep their split: measured 1.22 ms per step against
         // 1.46 ms unsplit — at 16 tokens the extra workgroups stream weights faster than the
         // epilogue costs.
-        const char *gs = std::getenv("K44WAVEC_GROUP_SPLIT");
-        if (!(gs && std::string(gs) == "0")) {
+        if (tune(Tune::GroupSplit) != 0) {
             for (auto &gp : groups) {
                 MfmaGroupExec &g = *gp;
                 if (g.mt == 16u) continue;
@@ -1468,6 +1587,8 @@ struct K44GpuExecutorState {
               << ", \"U\": " << (w.mfma ? w.rows_per_stage : w.U)
               << ", \"ksplit\": " << (w.mfma ? w.kgroups : w.ksplit)
               << ", \"sorted_segments\": " << (w.sorted_segments ? "true" : "false")
+              << ", \"misaligned\": " << (w.misaligned ? "true" : "false")
+              << ", \"phase_order\": " << (w.phase_order ? "true" : "false")
               << ", \"tokens_per_lane\": " << (w.mfma ? 0 : (w.lane8 ? 8 : 4))
               << ", \"stream_loads\": " << (w.stream_loads ? "true" : "false")
               << ", \"stream_kernel\": " << (w.stream_kernel ? "true" : "false")
@@ -1477,19 +1598,40 @@ struct K44GpuExecutorState {
               << ", \"effective_flops\": " << (long long)w.eff_flops
               << ", \"mapped\": " << (w.cmap.p ? "true" : "false")
               << ", \"unique_rows\": " << w.unique_rows
-              << ", \"y_off\": " << w.y_off << "}";
+              << ", \"y_off\": " << w.y_off << ", \"y_off_run\": " << w.y_off_run
+              << ", \"xd\": [" << w.xd[0] << ", " << w.xd[1] << ", " << w.xd[2] << "]"
+              << ", \"cmd\": " << wave_cmd[i] << "}";
         }
         o << "], \"aux\": [";
         for (size_t i = 0; i < aux.size(); ++i)
-            o << (i ? ", " : "") << "{\"name\": \"" << aux[i]->name << "\", \"type\": \""
+            o << (i ? ", " : "") << "{\"name\": \"" << aux[i]->name << "\", \"cmd\": " << aux_cmd[i]
+              << ", \"type\": \""
               << cmd_type_str(aux[i]->type) << "\", \"channels\": " << aux[i]->D
               << ", \"fused\": " << (aux[i]->fused ? "true" : "false")
+              << ", \"fuse_note\": \"" << aux[i]->fuse_note << "\""
               << ", \"tokens\": " << aux[i]->tokens << "}";
         o << "], \"groups\": [";
         for (size_t i = 0; i < groups.size(); ++i) {
             o << (i ? ", " : "") << "[";
             for (size_t k = 0; k < groups[i]->members.size(); ++k)
                 o << (k ? ", " : "") << groups[i]->members[k];
+            o << "]";
+        }
+        // Runs of the whole-plan schedule as plan command indices (wavec_gpu_execute_runs).
+        o << "], \"runs\": [";
+        for (size_t r = 0; r < runs.size(); ++r) {
+            std::vector<size_t> cmds;
+            if (runs[r].first == 0) {
+                cmds.push_back(aux_cmd[runs[r].second]);
+                const size_t sw = aux[runs[r].second]->shift_with;
+                if (sw != SIZE_MAX) cmds.push_back(aux_cmd[sw]);
+            } else if (runs[r].first == 1) {
+                cmds.push_back(wave_cmd[runs[r].second]);
+            } else {
+                for (size_t m : groups[runs[r].second]->members) cmds.push_back(wave_cmd[m]);
+            }
+            o << (r ? ", " : "") << "[";
+            for (size_t k = 0; k < cmds.size(); ++k) o << (k ? ", " : "") << cmds[k];
             o << "]";
         }
         o << "], \"launches_per_run\": " << launches_per_run();
@@ -1573,7 +1715,7 @@ struct K44GpuExecutorState {
             K44_HIP(k44dev::launch_gather_stream(a, w.tokens, stream, w.stream_loads));
         else
             K44_HIP(k44dev::launch_gather_dot(a, w.slab, w.ksplit, w.tokens, stream, w.lane8,
-                                              w.stream_loads));
+                                              w.stream_loads, w.weights_in_lds, w.misaligned));
     }
 
     void launch_op(size_t i) {
@@ -1584,8 +1726,10 @@ struct K44GpuExecutorState {
             launch_aux(*aux[op.second]);
     }
 
-    void launch_ops() {
-        for (const auto &r : runs) {
+    void launch_ops(size_t first = 0, size_t n = SIZE_MAX) {
+        const size_t end = n == SIZE_MAX ? runs.size() : std::min(runs.size(), first + n);
+        for (size_t i = first; i < end; ++i) {
+            const auto &r = runs[i];
             if (r.first == 0)
                 launch_aux(*aux[r.second], true);
             else if (r.first == 1)
@@ -1633,8 +1777,6 @@ struct K44GpuExecutorState {
 
     void upload_input_f32(const float *in, size_t n) {
         const K44ResDesc &L = layout(plan_meta.input_res_key);
-        if (L.is_image_token64)
-            throw std::runtime_error("64-frame interleaved image layouts are not supported");
         // whole planes (zero halos): the region may hold another tensor's data from the last run
         std::vector<uint16_t> pad((size_t)plan_meta.input_c * L.channel_stride, 0u);
         for (uint32_t ch = 0; ch < plan_meta.input_c; ++ch)
@@ -2155,7 +2297,29 @@ int wavec_k44_f16_forward_token64(void *Y, const void *X, const uint32_t *cluste
         a.B_vec16 = B_vec16;
         a.cluster = cluster_size;
         a.tiles = tiles;
-        K44_HIP(k44dev::launch_token64(a, static_cast<hipStream_t>(stream)));
+        K44_HIP(k44dev::launch_token64(a, static_cast<hipStream_t>(stream),
+                                       k44_host::tune(k44_host::Tune::Token64Ring)));
+        return 0;
+    });
+}
+
+int wavec_argmax_f16(uint32_t *ids, const void *logits, uint32_t vocab, uint32_t stride,
+                     uint32_t tokens, void *stream) {
+    return guarded("wavec_argmax_f16", [&] {
+        if (!ids || !logits) throw std::runtime_error("ids and logits are required");
+        if (vocab == 0u || stride == 0u || stride % 64u != 0u || tokens == 0u || tokens > stride)
+            throw std::runtime_error("vocab > 0, stride a positive multiple of 64 and "
+                                     "0 < tokens <= stride are required");
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        // Per-chunk (value, index) partials: a stream-ordered workspace for this call.
+        const size_t bytes = k44dev::argmax_scratch_floats(vocab, stride) * sizeof(float);
+        void *work = nullptr;
+        K44_HIP(hipMallocAsync(&work, bytes, st));
+        const hipError_t e = k44dev::launch_argmax(ids, nullptr, nullptr, 0u,
+                                                   static_cast<const __half *>(logits), vocab,
+                                                   stride, tokens, static_cast<float *>(work), st);
+        K44_HIP(hipFreeAsync(work, st));
+        K44_HIP(e);
         return 0;
     });
 }
@@ -2369,6 +2533,68 @@ int wavec_gpu_copy_ids(void *dst_h, int dst_first, void *src_h, int src_first, i
 const char *wavec_gpu_exec_report_json(void *h) {
     k44_host::K44GpuExecutorState *ex = h ? k44_host::find_exec(h) : nullptr;
     return ex ? ex->report_json.c_str() : "{}";
+}
+
+int wavec_gpu_execute_runs(void *h, int first_run, int n_runs) {
+    if (!h || first_run < 0 || n_runs < 0) return -1;
+    return guarded("wavec_gpu_execute_runs", [&] {
+        auto *ex = exec_or_throw(h);
+        if ((size_t)first_run + (size_t)n_runs > ex->runs.size())
+            throw std::runtime_error("run range past the end of the plan's schedule");
+        ex->launch_ops((size_t)first_run, (size_t)n_runs);
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+int wavec_gpu_read_canvas_2d(void *h, unsigned long long off, unsigned long long rows,
+                             unsigned long long row_stride, unsigned long long cols,
+                             uint16_t *dst) {
+    if (!h || (!dst && rows && cols)) return -1;
+    return guarded("wavec_gpu_read_canvas_2d", [&] {
+        auto *ex = exec_or_throw(h);
+        if (!rows || !cols) return 0;
+        // Anything inside the allocation may be read (relocated multiply operands live past
+        // the plan's canvas).
+        const uint64_t n = ex->canvas.n;
+        if (cols > row_stride || off > n || rows - 1u > (n - off) / row_stride ||
+            off + (rows - 1u) * row_stride + cols > n)
+            throw std::runtime_error("2-D range outside the canvas allocation");
+        // Packed on the device first (a staging buffer kept by the executor), then one copy.
+        if (ex->stage.n < rows * cols) ex->stage.alloc(rows * cols);
+        K44_HIP(k44dev::launch_gather_cols(ex->stage.p,
+                                           reinterpret_cast<const uint16_t *>(ex->canvas.p + off),
+                                           rows, row_stride, cols, ex->stream));
+        K44_HIP(hipMemcpyAsync(dst, ex->stage.p, rows * cols * 2u, hipMemcpyDeviceToHost,
+                               ex->stream));
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
+int wavec_set_tuning(const char *key, int value) {
+    if (!key) return -1;
+    return guarded("wavec_set_tuning", [&] {
+        for (int i = 0; i < (int)k44_host::Tune::Count; ++i) {
+            if (std::string(key) != k44_host::kTuneKeys[i]) continue;
+            if (value < -1) throw std::runtime_error("value must be -1 (automatic) or >= 0");
+            k44_host::g_tune[i].store(value);
+            return 0;
+        }
+        throw std::runtime_error(std::string("unknown tuning key '") + key + "'");
+    });
+}
+
+int wavec_get_tuning(const char *key) {
+    if (!key) return -2;
+    for (int i = 0; i < (int)k44_host::Tune::Count; ++i)
+        if (std::string(key) == k44_host::kTuneKeys[i]) return k44_host::g_tune[i].load();
+    set_error(std::string("wavec_get_tuning: unknown tuning key '") + key + "'");
+    return -2;
+}
+
+void wavec_reset_tuning(void) {
+    for (auto &v : k44_host::g_tune) v.store(-1);
 }
 
 }  // extern "C"

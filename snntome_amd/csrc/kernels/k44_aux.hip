@@ -453,6 +453,27 @@ hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uin
 
 __global__ void k44_step_inc_kernel(uint32_t *ctr) { *ctr += 1u; }
 
+// dst[r * cols + c] = src[r * row_stride + c]: `cols` elements of `rows` strided rows, packed
+// (one contiguous copy to the host afterwards instead of a row-by-row 2-D transfer).
+__global__ __launch_bounds__(256) void k44_gather_cols_kernel(uint16_t *__restrict__ dst,
+                                                              const uint16_t *__restrict__ src,
+                                                              uint64_t rows, uint64_t row_stride,
+                                                              uint64_t cols) {
+    const uint64_t n = rows * cols;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * 256u) {
+        const uint64_t r = i / cols, c = i - r * cols;
+        dst[i] = src[r * row_stride + c];
+    }
+}
+
+hipError_t launch_gather_cols(uint16_t *dst, const uint16_t *src, uint64_t rows,
+                              uint64_t row_stride, uint64_t cols, hipStream_t stream) {
+    hipLaunchKernelGGL(k44_gather_cols_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, stream,
+                       dst, src, rows, row_stride, cols);
+    return hipGetLastError();
+}
+
 static uint32_t argmax_chunk_len(uint32_t V, uint32_t stride) {
     const uint32_t tiles = stride / 64u;
     uint32_t chunks = (512u + tiles - 1u) / tiles;  // ~512 workgroups in pass 1

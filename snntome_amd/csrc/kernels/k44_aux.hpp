@@ -47,4 +47,8 @@ hipError_t launch_argmax(uint32_t *ids, uint32_t *history, uint32_t *step_ctr,
                          uint32_t hist_steps, const __half *x, uint32_t V, uint32_t stride,
                          uint32_t tokens, float *scratch, hipStream_t stream);
 
+// Packs `cols` elements of `rows` rows `row_stride` apart into dst [rows][cols] (16-bit words).
+hipError_t launch_gather_cols(uint16_t *dst, const uint16_t *src, uint64_t rows,
+                              uint64_t row_stride, uint64_t cols, hipStream_t stream);
+
 }  // namespace k44dev

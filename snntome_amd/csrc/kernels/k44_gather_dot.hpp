@@ -135,7 +135,11 @@ __device__ __forceinline__ void load_weights(float (&w)[U], const __half *p) {
 // Splitting keeps one short, fully parallel segment stream per wave when a neuron has only a
 // few segments (the ultra-sparse regime), instead of serialising K load-wait-FMA phases.
 // NTX: X rows and weights are read with non-temporal loads (see ld_once).
-template <int SLAB, int U, int KSPLIT, bool NTX>
+// MIS: segment starts may sit at any element (token-shifted taps of 1-D convolutions, the
+// reference's `ch_base + dx`): each lane loads the two aligned 8-byte words around its 4 tokens
+// and funnel-shifts them by the segment's misalignment (uniform per segment).  The second word
+// reaches up to 3 elements past the last token used; the canvas carries slack for it.
+template <int SLAB, int U, int KSPLIT, bool NTX, bool MIS = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k44_gather_dot_kernel(GatherDotArgs a) {
     constexpr int LPR = SLAB / 4;  // lanes per position row
     constexpr int RPI = 64 / LPR;  // rows per load instruction
@@ -159,11 +163,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
     const uint32_t lane_off = 8u * (uint32_t)c;
     const uint64_t row_bytes = a.step * 2u;
     for (uint32_t k = KSPLIT == 1 ? 0u : (uint32_t)wave; k < a.K; k += KSPLIT) {
-        const char *xseg = reinterpret_cast<const char *>(a.X + seg[k] + slab0);
+        uint64_t start = seg[k];
+        uint32_t mis = 0u;  // elements past the 8-byte boundary below the segment start
+        if constexpr (MIS) {
+            mis = (uint32_t)(start & 3u);
+            start -= mis;
+        }
+        const char *xseg = reinterpret_cast<const char *>(a.X + start + slab0);
         for (uint32_t b = 0; b < a.n_batch; ++b) {
             const uint32_t s0 = b * (uint32_t)(RPI * U) + (uint32_t)(g * U);
             gd_u2 x[U];
-            if ((b + 1u) * (uint32_t)(RPI * U) <= a.S) {  // whole batch inside the segment
+            if constexpr (MIS) {
+                gd_u2 hi[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t s = s0 + (uint32_t)u;
+                    const char *p = xseg + (uint64_t)s * row_bytes + lane_off;
+                    const bool in = s < a.S;
+                    x[u] = in ? ld_once<NTX>(reinterpret_cast<const gd_u2 *>(p)) : gd_u2{0u, 0u};
+                    hi[u] = in && mis ? ld_once<NTX>(reinterpret_cast<const gd_u2 *>(p + 8))
+                                      : gd_u2{0u, 0u};
+                }
+                if (mis) {
+                    // words d0..d3 of the lane's 8 elements; keep elements mis .. mis+3
+                    const bool q = mis >= 2u, odd = (mis & 1u) != 0u;
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const uint32_t a0 = q ? x[u].y : x[u].x, a1 = q ? hi[u].x : x[u].y,
+                                       a2 = q ? hi[u].y : hi[u].x;
+                        x[u].x = odd ? __builtin_amdgcn_alignbit(a1, a0, 16u) : a0;
+                        x[u].y = odd ? __builtin_amdgcn_alignbit(a2, a1, 16u) : a1;
+                    }
+                }
+            } else if ((b + 1u) * (uint32_t)(RPI * U) <= a.S) {  // whole batch inside the segment
 #pragma unroll
                 for (int u = 0; u < U; ++u)
                     x[u] = ld_once<NTX>(reinterpret_cast<const gd_u2 *>(

@@ -18,9 +18,13 @@ namespace k44dev {
 hipError_t launch_gather_stream(const GatherDotArgs &a, uint32_t tokens, hipStream_t stream,
                                 bool stream_loads);
 // stream_loads: read X rows and weights with non-temporal loads (substrates far beyond the caches).
+// weights_in_lds: the 8-token kernel stages each neuron's weights in LDS when they fit (false:
+// read per 16-row batch; same values and FMA order).
+// misaligned: segment starts at any element (4-token lanes only; lane8 must be false).
 hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
                              uint32_t tokens, hipStream_t stream, bool lane8 = false,
-                             bool stream_loads = false);
+                             bool stream_loads = false, bool weights_in_lds = true,
+                             bool misaligned = false);
 
 // MFMA tile kernel over a group of waves (one kernel configuration): `items` workgroups (the
 // group's start[n]), block mt; nt in {16,32,64,128}, mt in {64,128,256,512}, rows_per_stage in
@@ -64,7 +68,8 @@ struct Token64Args {
     const __half *bias;    // [Cout] or nullptr (zero)
     uint32_t Cin, Cout, B_vec16, cluster, tiles;
 };
-hipError_t launch_token64(const Token64Args &a, hipStream_t stream);
+// ring_mode: -1 automatic, 0 per-wave kernel, 1 the 64-neuron ring kernel where it applies.
+hipError_t launch_token64(const Token64Args &a, hipStream_t stream, int ring_mode = -1);
 
 // GPU weight interleave: row-major [neurons][8 * B_vec8] fp16 -> WMMA vector order.
 hipError_t launch_interleave_wmma(uint4 *dst, const uint4 *src, uint32_t neurons, uint32_t B_vec8,

@@ -82,6 +82,9 @@ __global__ __launch_bounds__(256) void k44_gather_tile_kernel(GatherTileArgs a) 
 
 __device__ __forceinline__ uint64_t pix(const Plane2D &p, uint32_t c, uint32_t f, uint32_t y,
                                         uint32_t x) {
+    if (p.tok64)
+        return (uint64_t)c * p.channel_stride + (uint64_t)(f >> 6) * 64u * p.single_stride +
+               ((uint64_t)(y + 1u) * p.W_pad + x + 1u) * 64u + (f & 63u);
     return (uint64_t)c * p.channel_stride + (uint64_t)f * p.single_stride +
            (uint64_t)(y + 1u) * p.W_pad + 4u + x;
 }
@@ -100,15 +103,20 @@ __device__ __forceinline__ uint64_t pix(const Plane2D &p, uint32_t c, uint32_t f
     const uint32_t f = (uint32_t)(r2_ % (P).frames);                                              \
     const uint32_t c = (uint32_t)(r2_ / (P).frames);
 
+// Planes: (channel, frame) of single_stride elements, or (channel, 64-frame block) of
+// 64 * single_stride elements in the interleaved layout (element e belongs to pixel e / 64).
 __global__ __launch_bounds__(256) void k44_halo_clear_kernel(__half *base, uint32_t planes,
                                                              Plane2D p) {
+    const uint32_t per_ch = p.tok64 ? p.frames / 64u : p.frames;
+    const uint64_t plane = p.tok64 ? 64u * p.single_stride : p.single_stride;
+    const uint32_t sh = p.tok64 ? 6u : 0u, col0 = p.tok64 ? 1u : 4u;
     for (uint32_t pl = blockIdx.y; pl < planes; pl += gridDim.y) {
-        const uint32_t c = pl / p.frames, f = pl - c * p.frames;
-        __half *pb = base + (uint64_t)c * p.channel_stride + (uint64_t)f * p.single_stride;
-        for (uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x; e < p.single_stride;
+        const uint32_t c = pl / per_ch, f = pl - c * per_ch;
+        __half *pb = base + (uint64_t)c * p.channel_stride + (uint64_t)f * plane;
+        for (uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x; e < plane;
              e += (uint64_t)gridDim.x * 256u) {
-            const uint64_t row = e / p.W_pad, col = e - row * p.W_pad;
-            if (row >= 1u && row <= p.H && col >= 4u && col < 4u + p.W) continue;
+            const uint64_t px = e >> sh, row = px / p.W_pad, col = px - row * p.W_pad;
+            if (row >= 1u && row <= p.H && col >= col0 && col < col0 + p.W) continue;
             pb[e] = __float2half_rn(0.0f);
         }
     }
@@ -191,9 +199,10 @@ hipError_t launch_gather_tile(const GatherTileArgs &a, hipStream_t stream) {
 
 hipError_t launch_halo_clear(__half *base, uint32_t channels, const Plane2D &p,
                              hipStream_t stream) {
-    const uint32_t planes = channels * p.frames;
+    if (p.tok64 && p.frames % 64u != 0u) return hipErrorInvalidValue;
+    const uint32_t planes = channels * (p.tok64 ? p.frames / 64u : p.frames);
     if (planes == 0u) return hipSuccess;
-    const uint64_t bx = (p.single_stride + 255u) / 256u;
+    const uint64_t bx = ((p.tok64 ? 64u : 1u) * p.single_stride + 255u) / 256u;
     const dim3 grid((uint32_t)(bx < 4096u ? bx : 4096u), planes < 65535u ? planes : 65535u);
     hipLaunchKernelGGL(k44_halo_clear_kernel, grid, dim3(256), 0, stream, base, planes, p);
     return hipGetLastError();

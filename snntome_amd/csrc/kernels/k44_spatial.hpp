@@ -6,6 +6,10 @@
 // plane is zero padding ("halo").  Two modes: W % 64 == 0 (W_pad = W + 8, a 64-token tile is 64
 // pixels of one row) and any other W (W_pad = W + 4, a tile is 64 consecutive plane elements
 // from (row 1, column 4), spanning rows and halo columns; only pixels are stored).
+// 64-frame interleaved images (batches of whole 64-frame blocks, k44_plan_types.hpp:576-598):
+// pixel (y, x) of frame f at c*channel_stride + (f/64)*64*single_stride +
+// ((y+1)*W_pad + x+1)*64 + f%64 — a 64-token tile is the 64 frames of one pixel, every tile is
+// 64-element aligned, and a tap (dy, dx) is a shift by whole pixels of 64 elements.
 //
 //  * WAVE (2-D): token m of tile t reads X[seg + s*step + tile_x[t] + m] — seg holds the
 //    reference's tap-shifted channel offsets ((1+dy)*W_pad + (1+dx) relative to the tile
@@ -19,9 +23,10 @@
 //  * SCATTER_UP2X2 (:93-103): out channel c at (y, x) = in channel q*Q + c at (y/2, x/2),
 //    q = 2*(y&1) + (x&1), Q = quad input channels / 4 (the compiler pads each quad plane group
 //    to a multiple of 16 channels; the reference reads q*Cout + c, equal when Cout % 16 == 0).
-//  * HALO CLEAR: zero every non-pixel element of each (channel, frame) plane of a tensor (run
-//    after every command that writes a 2-D tensor: canvas memory is reused between tensors, and
-//    the next 3x3 tap reads the halo as zero padding).
+//  * HALO CLEAR: zero every non-pixel element of each (channel, frame) plane — (channel,
+//    64-frame block) plane of 64 * single_stride elements in the interleaved layout — of a
+//    tensor (run after every command that writes a 2-D tensor: canvas memory is reused between
+//    tensors, and the next 3x3 tap reads the halo as zero padding).
 #pragma once
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -32,6 +37,7 @@ namespace k44dev {
 struct Plane2D {
     uint32_t H, W, W_pad, frames;
     uint64_t single_stride, channel_stride;
+    uint32_t tok64;  // 1: 64-frame interleaved layout (frames a multiple of 64)
 };
 
 struct GatherTileArgs {

@@ -267,13 +267,12 @@ bool token64_ring_ok(const Token64Args &a) {
            a.B_vec16 * 16u <= (uint32_t)T64R_IDX_MAX;
 }
 
-hipError_t launch_token64(const Token64Args &a, hipStream_t stream) {
-    const char *env = std::getenv("K44WAVEC_T64_RING");
-    if (token64_ring_ok(a) && !(env && env[0] == '0')) {
+hipError_t launch_token64(const Token64Args &a, hipStream_t stream, int ring_mode) {
+    if (token64_ring_ok(a) && ring_mode != 0) {
         // Two 64-neuron blocks sharing every gathered row: half the row traffic but half the
         // workgroups; measured equal at 128-neuron clusters, slightly faster from 256 on.
         const size_t ix_bytes = (size_t)a.B_vec16 * 16u * 4u;
-        if (a.cluster % 256u == 0u && !(env && env[0] == '1')) {
+        if (a.cluster % 256u == 0u && ring_mode != 1) {
             const dim3 grid(a.Cout / 128u, a.tiles / 4u, 1u), block(512u, 1u, 1u);
             hipLaunchKernelGGL((k44_token64_ring_kernel<2, 6>), grid, block, ix_bytes, stream, a);
         } else {

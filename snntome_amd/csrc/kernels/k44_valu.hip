@@ -1,6 +1,4 @@
 // Translation unit of the VALU kernels (gather-dot, substrate fill) and their launchers.
-#include <cstdlib>
-
 #include "k44_launch.hpp"
 
 namespace k44dev {
@@ -25,12 +23,13 @@ __global__ __launch_bounds__(256) void k44_fill_uniform_kernel(__half *dst, uint
 
 template <bool NTX>
 static hipError_t launch_gather_dot_policy(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
-                                           uint32_t tokens, hipStream_t stream, bool lane8) {
+                                           uint32_t tokens, hipStream_t stream, bool lane8,
+                                           bool weights_in_lds, bool misaligned) {
     const dim3 grid(ksplit == 4u ? a.cout : (a.cout + 3u) / 4u, tokens / slab, 1u);
     const dim3 block(256u, 1u, 1u);
+    if (lane8 && misaligned) return hipErrorInvalidValue;  // 16-byte loads need aligned rows
     if (lane8) {
-        const char *wle = std::getenv("K44WAVEC_WLDS");
-        const bool wl = (uint64_t)a.K * a.n_batch * 16u <= GD_WL_MAX && !(wle && wle[0] == '0');
+        const bool wl = weights_in_lds && (uint64_t)a.K * a.n_batch * 16u <= GD_WL_MAX;
 #define K44_GD8(SLAB)                                                                                \
     if (ksplit == 4u) {                                                                              \
         if (wl) hipLaunchKernelGGL((k44_gather_dot8_kernel<SLAB, 4, NTX, true>), grid, block, 0, stream, a);  \
@@ -49,7 +48,14 @@ static hipError_t launch_gather_dot_policy(const GatherDotArgs &a, uint32_t slab
         return hipGetLastError();
     }
 #define K44_GD(SLAB, U)                                                                          \
-    if (ksplit == 4u)                                                                            \
+    if (misaligned) {                                                                            \
+        if (ksplit == 4u)                                                                        \
+            hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 4, NTX, true>), grid, block, 0,    \
+                               stream, a);                                                       \
+        else                                                                                     \
+            hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 1, NTX, true>), grid, block, 0,    \
+                               stream, a);                                                       \
+    } else if (ksplit == 4u)                                                                     \
         hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 4, NTX>), grid, block, 0, stream, a);  \
     else                                                                                         \
         hipLaunchKernelGGL((k44_gather_dot_kernel<SLAB, U, 1, NTX>), grid, block, 0, stream, a);
@@ -64,9 +70,12 @@ static hipError_t launch_gather_dot_policy(const GatherDotArgs &a, uint32_t slab
 }
 
 hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksplit,
-                             uint32_t tokens, hipStream_t stream, bool lane8, bool stream_loads) {
-    return stream_loads ? launch_gather_dot_policy<true>(a, slab, ksplit, tokens, stream, lane8)
-                        : launch_gather_dot_policy<false>(a, slab, ksplit, tokens, stream, lane8);
+                             uint32_t tokens, hipStream_t stream, bool lane8, bool stream_loads,
+                             bool weights_in_lds, bool misaligned) {
+    return stream_loads ? launch_gather_dot_policy<true>(a, slab, ksplit, tokens, stream, lane8,
+                                                         weights_in_lds, misaligned)
+                        : launch_gather_dot_policy<false>(a, slab, ksplit, tokens, stream, lane8,
+                                                          weights_in_lds, misaligned);
 }
 
 // Streaming gather kernel: 256 neurons x one 256-token slab per workgroup (16 waves, 128 KiB of

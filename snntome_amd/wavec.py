@@ -1,125 +1,146 @@
-"""wavec.py — ctypes interface of libk44wavec.so, the MI355X (gfx950) wave executor.
+"""Python front end of libk44wavec.so, the gfx950 (MI355X) wave executor.
 
-Same Python API as the reference's wavec/wavec.py (ACT_MAP, get_lib, WavePlan, WaveGraph and
-their methods, argument meaning, RuntimeError on a failed call), bound to this build's
-library, plus the build extensions: sparse / dendritic-cluster waves, device-side input fill,
-timed plan execution, raw canvas access and the per-wave execution report.
+Callers of SNNtome's ``wavec`` module find the same surface here: ``ACT_MAP``, ``get_lib()``,
+``WaveGraph`` and ``WavePlan`` with the method names, argument names, defaults and return values
+of the reference binding (reference wavec/wavec.py:13-16, :135-141, :147-211, :214-344), and a
+``RuntimeError`` whenever the library reports a failure.  The library text of the error
+(``wavec_last_error``) is part of every message.
 
-The library must exist next to this file (build it with ``python -m snntome_amd.build``);
-loading fails loudly otherwise — there is no CPU fallback.
+Beyond that surface this module binds the build's extensions: sparse, dendritic-cluster and
+pruned waves, token ops (token shift, embedding, argmax), device-side input generation, timed
+plan execution, command- and run-wise execution, raw canvas access, the per-wave execution
+report, executor tuning switches, and device buffers for the stand-alone Token64 launcher.
+
+The shared library must sit next to this file (``python -m snntome_amd.build`` makes it).  There
+is no CPU fallback: importing works without it, the first call that needs it raises.
 """
 
 import ctypes
 import json
+import os
 from pathlib import Path
 from typing import List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 
+# Activation names -> the epilogue ids of K44ExecCmd.act.  Ids 0-4 are the reference's; 5 (GELU,
+# erf form) is an extension.
 ACT_MAP = {
     None: 0, "none": 0, "identity": 0, "linear": 0,
     "relu": 1, "sigmoid": 2, "silu": 3, "swish": 3, "leaky_relu": 4,
     "gelu": 5,
 }
 
-_c = ctypes
-_vp, _cp, _i, _f = _c.c_void_p, _c.c_char_p, _c.c_int, _c.c_float
-_pf = _c.POINTER(_c.c_float)
-_pu16 = _c.POINTER(_c.c_uint16)
-_pu32 = _c.POINTER(_c.c_uint32)
-_pcp = _c.POINTER(_c.c_char_p)
-_ull = _c.c_ulonglong
-_u32 = _c.c_uint32
+C = ctypes
+_VOID, _STR, _INT, _FLT = C.c_void_p, C.c_char_p, C.c_int, C.c_float
+_U32, _ULL = C.c_uint32, C.c_ulonglong
+_P_FLT = C.POINTER(C.c_float)
+_P_U16 = C.POINTER(C.c_uint16)
+_P_U32 = C.POINTER(C.c_uint32)
+_P_STR = C.POINTER(C.c_char_p)
 
-# name -> (restype, argtypes)
-_SIGNATURES = {
-    "wavec_create": (_vp, [_i, _i, _i, _i]),
-    "wavec_destroy": (None, [_vp]),
-    "wavec_gpu_release": (_i, [_vp]),
-    "wavec_add_input": (_i, [_vp, _cp, _i, _i, _i, _i]),
-    "wavec_add_flatten": (_i, [_vp, _cp, _cp, _cp]),
-    "wavec_add_conv2d": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _i, _i, _i, _i, _pf, _pf, _cp]),
-    "wavec_add_conv2d_f16": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _i, _i, _i, _i, _pu16, _pf, _cp]),
-    "wavec_add_linear_f32": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _pf, _pf, _cp]),
-    "wavec_add_linear_f16": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _pu16, _pf, _cp]),
-    "wavec_add_linear_bf16": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _pu16, _pf, _cp]),
-    "wavec_add_upconv2x2": (_i, [_vp, _cp, _cp, _cp, _i, _i, _pf, _pf]),
-    "wavec_add_maxpool": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i]),
-    "wavec_add_upsample2x": (_i, [_vp, _cp, _cp, _cp]),
-    "wavec_add_rmsnorm": (_i, [_vp, _cp, _cp, _cp, _i, _f, _pf, _i]),
-    "wavec_add_swiglu": (_i, [_vp, _cp, _cp, _cp, _cp]),
-    "wavec_add_rope_gqa_attn": (_i, [_vp, _cp, _cp, _cp, _cp, _cp, _i, _i, _i, _f, _i]),
-    "wavec_add_split": (_i, [_vp, _cp, _cp, _i, _pcp]),
-    "wavec_add_slice": (_i, [_vp, _cp, _cp, _i, _pcp, _c.POINTER(_i)]),
-    "wavec_add_concat": (_i, [_vp, _cp, _i, _pcp, _cp]),
-    "wavec_set_output": (_i, [_vp, _cp]),
-    "wavec_set_reuse_canvas": (_i, [_vp, _i]),
-    "wavec_set_batch_size": (_i, [_vp, _i]),
-    "wavec_set_target_preset": (_i, [_vp, _cp]),
-    "wavec_compile": (_i, [_vp]),
-    "wavec_get_summary_json": (_cp, [_vp]),
-    "wavec_save_tcff": (_i, [_vp, _cp, _cp]),
-    "wavec_save_tcff_ex": (_i, [_vp, _cp, _cp, _i, _i]),
-    "wavec_load_tcff_weights": (_i, [_vp, _cp]),
-    "wavec_gpu_init_plan": (_i, [_vp]),
-    "wavec_gpu_infer_f32": (_i, [_vp, _pf, _i, _pf, _i, _pf]),
-    # build extensions
-    "wavec_last_error": (_cp, []),
-    "wavec_add_sparse_wave": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _pu32, _pu16, _pu16, _i, _cp]),
-    "wavec_add_cluster_wave": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _i, _pu32, _pu16, _pu16, _i, _cp]),
-    "wavec_add_pruned_wave": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _i, _pu32, _pu16, _pu16, _i, _cp]),
-    "wavec_gpu_fill_input_uniform": (_i, [_vp, _ull]),
-    "wavec_gpu_execute": (_i, [_vp, _i, _pf]),
-    "wavec_gpu_sync": (_i, [_vp]),
-    "wavec_gpu_execute_range": (_i, [_vp, _i, _i]),
-    "wavec_gpu_read_canvas": (_i, [_vp, _ull, _ull, _pu16]),
-    "wavec_gpu_write_canvas": (_i, [_vp, _ull, _ull, _pu16]),
-    "wavec_add_token_shift": (_i, [_vp, _cp, _cp, _cp, _i, _i, _i, _pu16, _i]),
-    "wavec_add_embedding": (_i, [_vp, _cp, _cp, _cp, _i, _i, _pu16]),
-    "wavec_add_argmax": (_i, [_vp, _cp, _cp, _cp]),
-    "wavec_gpu_set_ids": (_i, [_vp, _pu32, _i]),
-    "wavec_gpu_get_ids": (_i, [_vp, _pu32, _i]),
-    "wavec_gpu_set_history": (_i, [_vp, _i]),
-    "wavec_gpu_get_history": (_i, [_vp, _pu32, _i]),
-    "wavec_gpu_use_graph": (_i, [_vp, _i]),
-    "wavec_gpu_copy_canvas": (_i, [_vp, _ull, _vp, _ull, _ull]),
-    "wavec_gpu_copy_ids": (_i, [_vp, _i, _vp, _i, _i, _i]),
-    "wavec_gpu_exec_report_json": (_cp, [_vp]),
-    "wavec_dev_malloc": (_vp, [_ull]),
-    "wavec_dev_free": (_i, [_vp]),
-    "wavec_dev_upload": (_i, [_vp, _vp, _ull]),
-    "wavec_dev_download": (_i, [_vp, _vp, _ull]),
-    "wavec_dev_synchronize": (_i, []),
-    "wavec_dev_fill_uniform": (_i, [_vp, _ull, _u32, _u32, _ull, _ull]),
-    "wavec_dev_time_begin": (_i, []),
-    "wavec_dev_time_end": (_i, [_pf]),
-    "wavec_k44_f16_forward_token64": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
-    "wavec_interleave_weights_wmma": (_i, [_vp, _vp, _u32, _u32, _vp]),
-}
+# Every exported entry point: (name, result type, argument types).  The first 30 rows are the
+# reference's C ABI (wavec/k44_wave_executor.cu:644-986), the rest this build's extensions.
+_ABI = (
+    ("wavec_create", _VOID, (_INT, _INT, _INT, _INT)),
+    ("wavec_destroy", None, (_VOID,)),
+    ("wavec_gpu_release", _INT, (_VOID,)),
+    ("wavec_add_input", _INT, (_VOID, _STR, _INT, _INT, _INT, _INT)),
+    ("wavec_add_flatten", _INT, (_VOID, _STR, _STR, _STR)),
+    ("wavec_add_conv2d", _INT,
+     (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _INT, _INT, _INT, _INT, _P_FLT, _P_FLT, _STR)),
+    ("wavec_add_conv2d_f16", _INT,
+     (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _INT, _INT, _INT, _INT, _P_U16, _P_FLT, _STR)),
+    ("wavec_add_linear_f32", _INT, (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _P_FLT, _P_FLT, _STR)),
+    ("wavec_add_linear_f16", _INT, (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _P_U16, _P_FLT, _STR)),
+    ("wavec_add_linear_bf16", _INT, (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _P_U16, _P_FLT, _STR)),
+    ("wavec_add_upconv2x2", _INT, (_VOID, _STR, _STR, _STR, _INT, _INT, _P_FLT, _P_FLT)),
+    ("wavec_add_maxpool", _INT, (_VOID, _STR, _STR, _STR, _INT, _INT, _INT)),
+    ("wavec_add_upsample2x", _INT, (_VOID, _STR, _STR, _STR)),
+    ("wavec_add_rmsnorm", _INT, (_VOID, _STR, _STR, _STR, _INT, _FLT, _P_FLT, _INT)),
+    ("wavec_add_swiglu", _INT, (_VOID, _STR, _STR, _STR, _STR)),
+    ("wavec_add_rope_gqa_attn", _INT, (_VOID, _STR, _STR, _STR, _STR, _STR, _INT, _INT, _INT, _FLT, _INT)),
+    ("wavec_add_split", _INT, (_VOID, _STR, _STR, _INT, _P_STR)),
+    ("wavec_add_slice", _INT, (_VOID, _STR, _STR, _INT, _P_STR, C.POINTER(_INT))),
+    ("wavec_add_concat", _INT, (_VOID, _STR, _INT, _P_STR, _STR)),
+    ("wavec_set_output", _INT, (_VOID, _STR)),
+    ("wavec_set_reuse_canvas", _INT, (_VOID, _INT)),
+    ("wavec_set_batch_size", _INT, (_VOID, _INT)),
+    ("wavec_set_target_preset", _INT, (_VOID, _STR)),
+    ("wavec_compile", _INT, (_VOID,)),
+    ("wavec_get_summary_json", _STR, (_VOID,)),
+    ("wavec_save_tcff", _INT, (_VOID, _STR, _STR)),
+    ("wavec_save_tcff_ex", _INT, (_VOID, _STR, _STR, _INT, _INT)),
+    ("wavec_load_tcff_weights", _INT, (_VOID, _STR)),
+    ("wavec_gpu_init_plan", _INT, (_VOID,)),
+    ("wavec_gpu_infer_f32", _INT, (_VOID, _P_FLT, _INT, _P_FLT, _INT, _P_FLT)),
+    # ---- extensions
+    ("wavec_last_error", _STR, ()),
+    ("wavec_add_sparse_wave", _INT,
+     (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _P_U32, _P_U16, _P_U16, _INT, _STR)),
+    ("wavec_add_cluster_wave", _INT,
+     (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _INT, _P_U32, _P_U16, _P_U16, _INT, _STR)),
+    ("wavec_add_pruned_wave", _INT,
+     (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _INT, _P_U32, _P_U16, _P_U16, _INT, _STR)),
+    ("wavec_gpu_fill_input_uniform", _INT, (_VOID, _ULL)),
+    ("wavec_gpu_execute", _INT, (_VOID, _INT, _P_FLT)),
+    ("wavec_gpu_sync", _INT, (_VOID,)),
+    ("wavec_gpu_execute_range", _INT, (_VOID, _INT, _INT)),
+    ("wavec_gpu_read_canvas", _INT, (_VOID, _ULL, _ULL, _P_U16)),
+    ("wavec_gpu_write_canvas", _INT, (_VOID, _ULL, _ULL, _P_U16)),
+    ("wavec_add_token_shift", _INT, (_VOID, _STR, _STR, _STR, _INT, _INT, _INT, _P_U16, _INT)),
+    ("wavec_add_embedding", _INT, (_VOID, _STR, _STR, _STR, _INT, _INT, _P_U16)),
+    ("wavec_add_argmax", _INT, (_VOID, _STR, _STR, _STR)),
+    ("wavec_gpu_set_ids", _INT, (_VOID, _P_U32, _INT)),
+    ("wavec_gpu_get_ids", _INT, (_VOID, _P_U32, _INT)),
+    ("wavec_gpu_set_history", _INT, (_VOID, _INT)),
+    ("wavec_gpu_get_history", _INT, (_VOID, _P_U32, _INT)),
+    ("wavec_gpu_use_graph", _INT, (_VOID, _INT)),
+    ("wavec_gpu_copy_canvas", _INT, (_VOID, _ULL, _VOID, _ULL, _ULL)),
+    ("wavec_gpu_copy_ids", _INT, (_VOID, _INT, _VOID, _INT, _INT, _INT)),
+    ("wavec_gpu_exec_report_json", _STR, (_VOID,)),
+    ("wavec_dev_malloc", _VOID, (_ULL,)),
+    ("wavec_dev_free", _INT, (_VOID,)),
+    ("wavec_dev_upload", _INT, (_VOID, _VOID, _ULL)),
+    ("wavec_dev_download", _INT, (_VOID, _VOID, _ULL)),
+    ("wavec_dev_synchronize", _INT, ()),
+    ("wavec_dev_fill_uniform", _INT, (_VOID, _ULL, _U32, _U32, _ULL, _ULL)),
+    ("wavec_dev_time_begin", _INT, ()),
+    ("wavec_dev_time_end", _INT, (_P_FLT,)),
+    ("wavec_k44_f16_forward_token64", _INT,
+     (_VOID, _VOID, _VOID, _VOID, _VOID, _U32, _U32, _U32, _U32, _U32, _VOID)),
+    ("wavec_interleave_weights_wmma", _INT, (_VOID, _VOID, _U32, _U32, _VOID)),
+    ("wavec_argmax_f16", _INT, (_VOID, _VOID, _U32, _U32, _U32, _VOID)),
+    ("wavec_set_tuning", _INT, (_STR, _INT)),
+    ("wavec_get_tuning", _INT, (_STR,)),
+    ("wavec_reset_tuning", None, ()),
+    ("wavec_gpu_execute_runs", _INT, (_VOID, _INT, _INT)),
+    ("wavec_gpu_read_canvas_2d", _INT, (_VOID, _ULL, _ULL, _ULL, _ULL, _P_U16)),
+)
 
-REFERENCE_SYMBOLS = tuple(list(_SIGNATURES)[:30])
-EXTENSION_SYMBOLS = tuple(list(_SIGNATURES)[30:])
+REFERENCE_SYMBOLS = tuple(name for name, _, _ in _ABI[:30])
+EXTENSION_SYMBOLS = tuple(name for name, _, _ in _ABI[30:])
 
 LIB_PATH = Path(__file__).resolve().parent / "libk44wavec.so"
-
-
-def _load_lib() -> ctypes.CDLL:
-    if not LIB_PATH.exists():
-        raise FileNotFoundError(
-            f"Shared library {LIB_PATH} not found. Run `python -m snntome_amd.build` first."
-        )
-    lib = ctypes.CDLL(str(LIB_PATH))
-    for name, (res, args) in _SIGNATURES.items():
-        fn = getattr(lib, name)
-        fn.restype = res
-        fn.argtypes = args
-    return lib
-
 
 _LIB: Optional[ctypes.CDLL] = None
 
 
+def _load_lib() -> ctypes.CDLL:
+    """Opens libk44wavec.so beside this module and declares every entry point's types."""
+    if not LIB_PATH.is_file():
+        raise FileNotFoundError(
+            f"{LIB_PATH.name} is missing from {LIB_PATH.parent}; build it with "
+            "`python -m snntome_amd.build` (there is no CPU fallback)")
+    lib = ctypes.CDLL(os.fspath(LIB_PATH))
+    for name, restype, argtypes in _ABI:
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = restype, list(argtypes)
+    return lib
+
+
 def get_lib() -> ctypes.CDLL:
+    """The process-wide handle of libk44wavec.so (loaded on first use)."""
     global _LIB
     if _LIB is None:
         _LIB = _load_lib()
@@ -127,38 +148,79 @@ def get_lib() -> ctypes.CDLL:
 
 
 def last_error() -> str:
-    msg = get_lib().wavec_last_error()
-    return msg.decode("utf-8", "replace") if msg else ""
+    """Message of the library's last failure on this thread ('' if none)."""
+    raw = get_lib().wavec_last_error()
+    return raw.decode("utf-8", "replace") if raw else ""
 
 
-def _check(rc: int, what: str) -> None:
+def _raise_on(rc: int, action: str) -> None:
     if rc != 0:
-        raise RuntimeError(f"{what} failed: {last_error()}")
+        detail = last_error() or f"return code {rc}"
+        raise RuntimeError(f"{action}: {detail}")
 
 
-def _ptr(a: Optional[np.ndarray], ctype):
-    return None if a is None else a.ctypes.data_as(ctypes.POINTER(ctype))
+def _cstr(s: Optional[str]) -> Optional[bytes]:
+    return None if s is None else os.fspath(s).encode("utf-8")
+
+
+def _pointer(a: Optional[np.ndarray], ctype):
+    return None if a is None else a.ctypes.data_as(C.POINTER(ctype))
+
+
+def _f32(a) -> Optional[np.ndarray]:
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
 
 
 def _f16_bits(a) -> np.ndarray:
+    """fp16 bit patterns (uint16) of an fp16 / uint16 array, or of a float array rounded RNE."""
     a = np.asarray(a)
-    if a.dtype == np.float16:
-        return np.ascontiguousarray(a).view(np.uint16)
     if a.dtype == np.uint16:
         return np.ascontiguousarray(a)
-    return np.ascontiguousarray(a, dtype=np.float32).astype(np.float16).view(np.uint16)
+    if a.dtype != np.float16:
+        a = np.asarray(a, dtype=np.float32).astype(np.float16)
+    return np.ascontiguousarray(a).view(np.uint16)
+
+
+def _opt_f16_bits(a) -> Optional[np.ndarray]:
+    return None if a is None else _f16_bits(a)
+
+
+def _name_array(names: Sequence[str]):
+    return (C.c_char_p * len(names))(*[_cstr(n) for n in names])
+
+
+def set_tuning(key: str, value: int) -> None:
+    """Sets one of the executor's process-wide tuning switches (A/B tests and benchmarks; every
+    switch defaults to -1, the executor's own choice).  Applies to plans initialised afterwards.
+    Keys are listed with wavec_set_tuning in include/k44wavec.h."""
+    _raise_on(get_lib().wavec_set_tuning(_cstr(key), int(value)), f"wavec_set_tuning({key!r})")
+
+
+def get_tuning(key: str) -> int:
+    v = get_lib().wavec_get_tuning(_cstr(key))
+    if v < -1:
+        raise RuntimeError(f"wavec_get_tuning({key!r}): {last_error()}")
+    return int(v)
+
+
+def reset_tuning() -> None:
+    """Every tuning switch back to -1 (automatic)."""
+    get_lib().wavec_reset_tuning()
 
 
 class WavePlan:
-    """Compiled Wave Execution Plan with TCFF v1.0 serialization and GPU execution."""
+    """Result of WaveGraph.compile(): the plan's commands, canvas layout and weights.  It can be
+    written to a .tcff file, have its weights replaced from one, and run on the GPU.  The plan
+    shares the compiler handle of its graph and keeps that graph alive."""
 
     def __init__(self, handle: ctypes.c_void_p, lib: ctypes.CDLL, summary: dict, owner=None):
         self._handle = handle
         self._lib = lib
         self.summary = summary
+        self._owner = owner
         self._gpu_initialized = False
-        self._owner = owner  # the WaveGraph that owns `handle`; kept alive with the plan
 
+    # ------------------------------------------------------------------ summary values
     @property
     def total_gflops(self) -> float:
         return float(self.summary.get("total_gflops", 0.0))
@@ -169,127 +231,162 @@ class WavePlan:
 
     @property
     def num_wave_dispatches(self) -> int:
-        return int(self.summary.get("num_waves", self.summary.get("num_wave_dispatches", 0)))
+        for key in ("num_waves", "num_wave_dispatches"):
+            if key in self.summary:
+                return int(self.summary[key])
+        return 0
 
+    # ------------------------------------------------------------------ .tcff
     def save_tcff(self, tcff_path: Union[str, Path], model_prefix: str = "K44Model") -> int:
-        n = self._lib.wavec_save_tcff(self._handle, str(tcff_path).encode("utf-8"),
-                                      model_prefix.encode("utf-8"))
-        if n < 0:
-            raise RuntimeError(f"Failed to export TCFF v1.0 file: {tcff_path}")
+        """Writes the plan as .tcff v1.0; returns the number of wave commands written."""
+        rc = self._lib.wavec_save_tcff(self._handle, _cstr(tcff_path), _cstr(model_prefix))
+        if rc < 0:
+            raise RuntimeError(f"could not write plan file {os.fspath(tcff_path)!r}: {last_error()}")
         return self.num_wave_dispatches
 
     def load_tcff_weights(self, tcff_path: Union[str, Path]) -> None:
-        rc = self._lib.wavec_load_tcff_weights(self._handle, str(tcff_path).encode("utf-8"))
+        """Replaces weights, indices and biases with those of a .tcff file written for the same
+        plan (every block hash-checked); the GPU state must be initialised again afterwards."""
+        rc = self._lib.wavec_load_tcff_weights(self._handle, _cstr(tcff_path))
         if rc != 0:
-            raise RuntimeError(f"Failed to load TCFF weights from: {tcff_path}")
+            raise RuntimeError(f"plan file {os.fspath(tcff_path)!r} was rejected: {last_error()}")
         self._gpu_initialized = False
 
+    # ------------------------------------------------------------------ GPU
     def init_gpu(self) -> None:
-        if not self._gpu_initialized:
-            rc = self._lib.wavec_gpu_init_plan(self._handle)
-            if rc != 0:
-                raise RuntimeError("Failed to initialize GPU execution state for WavePlan: "
-                                   + last_error())
-            self._gpu_initialized = True
+        """Uploads the plan (device schedules, weights, zeroed canvas); idempotent."""
+        if self._gpu_initialized:
+            return
+        if self._lib.wavec_gpu_init_plan(self._handle) != 0:
+            raise RuntimeError(f"the GPU executor refused this plan: {last_error()}")
+        self._gpu_initialized = True
 
     def infer_f32(self, x: np.ndarray) -> Tuple[np.ndarray, float]:
+        """Host fp32 input -> one plan run -> host fp32 output of shape output_shape (with a
+        leading frame axis when the plan's batch_size > 1; the executor moves frame 0, as the
+        reference's does).  Returns (output, GPU milliseconds of the run)."""
         self.init_gpu()
-        x_f32 = np.ascontiguousarray(x, dtype=np.float32)
-        c, h, w = tuple(self.summary["output_shape"])
-        batch = int(self.summary.get("batch_size", 1))
-        out_elems = batch * c * h * w if batch > 1 else c * h * w
-        out_arr = np.empty((batch, c, h, w) if batch > 1 else (c, h, w), dtype=np.float32)
-        gpu_ms = ctypes.c_float(0.0)
-        rc = self._lib.wavec_gpu_infer_f32(self._handle, _ptr(x_f32, ctypes.c_float),
-                                           int(x_f32.size), _ptr(out_arr, ctypes.c_float),
-                                           int(out_elems), ctypes.byref(gpu_ms))
+        c, h, w = (int(v) for v in self.summary["output_shape"])
+        frames = int(self.summary.get("batch_size", 1))
+        y = np.zeros((frames, c, h, w) if frames > 1 else (c, h, w), dtype=np.float32)
+        xin = np.ascontiguousarray(x, dtype=np.float32)
+        ms = C.c_float(0.0)
+        rc = self._lib.wavec_gpu_infer_f32(self._handle, _pointer(xin, C.c_float), int(xin.size),
+                                           _pointer(y, C.c_float), int(y.size), C.byref(ms))
         if rc != 0:
-            raise RuntimeError("GPU inference failed in wavec_gpu_infer_f32: " + last_error())
-        return out_arr, float(gpu_ms.value)
+            raise RuntimeError(f"wavec_gpu_infer_f32 did not run the plan: {last_error()}")
+        return y, float(ms.value)
 
-    # ---------------------------------------------------------------- build extensions
+    # ------------------------------------------------------------------ extensions
     def fill_input_uniform(self, seed: int) -> None:
-        """Device-side synthetic input (the substrate generator of include/k44wavec.h)."""
+        """Fills the plan input on the device with the synthetic substrate generator."""
         self.init_gpu()
-        _check(self._lib.wavec_gpu_fill_input_uniform(self._handle, int(seed)),
-               "wavec_gpu_fill_input_uniform")
+        _raise_on(self._lib.wavec_gpu_fill_input_uniform(self._handle, int(seed)),
+                  "wavec_gpu_fill_input_uniform")
 
     def execute(self, iters: int = 1) -> float:
-        """Runs the plan `iters` times back to back; returns average ms per run (HIP events)."""
+        """`iters` back-to-back runs of the whole plan; average milliseconds per run."""
         self.init_gpu()
-        ms = ctypes.c_float(0.0)
-        _check(self._lib.wavec_gpu_execute(self._handle, int(iters), ctypes.byref(ms)),
-               "wavec_gpu_execute")
+        ms = C.c_float(0.0)
+        _raise_on(self._lib.wavec_gpu_execute(self._handle, int(iters), C.byref(ms)),
+                  "wavec_gpu_execute")
         return float(ms.value)
 
     def sync(self) -> None:
-        _check(self._lib.wavec_gpu_sync(self._handle), "wavec_gpu_sync")
+        _raise_on(self._lib.wavec_gpu_sync(self._handle), "wavec_gpu_sync")
+
+    def release_gpu(self) -> None:
+        """Frees the plan's device state (canvas, schedules, graphs); init_gpu builds it again."""
+        _raise_on(self._lib.wavec_gpu_release(self._handle), "wavec_gpu_release")
+        self._gpu_initialized = False
 
     def execute_range(self, first_cmd: int, n_cmds: int = 1) -> None:
-        """Runs plan commands [first_cmd, first_cmd + n_cmds) and waits for them."""
+        """Commands [first_cmd, first_cmd + n_cmds), each as compiled and launched alone (no
+        grouping, nothing folded); waits for them."""
         self.init_gpu()
-        _check(self._lib.wavec_gpu_execute_range(self._handle, int(first_cmd), int(n_cmds)),
-               "wavec_gpu_execute_range")
+        _raise_on(self._lib.wavec_gpu_execute_range(self._handle, int(first_cmd), int(n_cmds)),
+                  "wavec_gpu_execute_range")
+
+    def execute_runs(self, first_run: int, n_runs: int = 1) -> None:
+        """Runs [first_run, first_run + n_runs) of the whole-plan schedule (exec_report()['runs']),
+        launched exactly as wavec_gpu_execute launches them; waits for them."""
+        self.init_gpu()
+        _raise_on(self._lib.wavec_gpu_execute_runs(self._handle, int(first_run), int(n_runs)),
+                  "wavec_gpu_execute_runs")
 
     def read_canvas(self, off: int, n: int) -> np.ndarray:
-        out = np.empty(int(n), dtype=np.uint16)
-        _check(self._lib.wavec_gpu_read_canvas(self._handle, int(off), int(n),
-                                               _ptr(out, ctypes.c_uint16)),
-               "wavec_gpu_read_canvas")
-        return out
+        buf = np.empty(int(n), dtype=np.uint16)
+        _raise_on(self._lib.wavec_gpu_read_canvas(self._handle, int(off), int(n),
+                                                  _pointer(buf, C.c_uint16)),
+                  "wavec_gpu_read_canvas")
+        return buf
+
+    def read_canvas_2d(self, off: int, rows: int, row_stride: int, cols: int) -> np.ndarray:
+        """[rows][cols] fp16 bits: `cols` elements from each of `rows` rows `row_stride` apart."""
+        buf = np.empty((int(rows), int(cols)), dtype=np.uint16)
+        _raise_on(self._lib.wavec_gpu_read_canvas_2d(self._handle, int(off), int(rows),
+                                                     int(row_stride), int(cols),
+                                                     _pointer(buf, C.c_uint16)),
+                  "wavec_gpu_read_canvas_2d")
+        return buf
 
     def write_canvas(self, off: int, data: np.ndarray) -> None:
-        d = _f16_bits(data).ravel()
-        _check(self._lib.wavec_gpu_write_canvas(self._handle, int(off), int(d.size),
-                                                _ptr(d, ctypes.c_uint16)),
-               "wavec_gpu_write_canvas")
+        bits = _f16_bits(data).ravel()
+        _raise_on(self._lib.wavec_gpu_write_canvas(self._handle, int(off), int(bits.size),
+                                                   _pointer(bits, C.c_uint16)),
+                  "wavec_gpu_write_canvas")
 
     def exec_report(self) -> dict:
+        """Per-wave path choices, token ops, group launches and runs of the initialised plan."""
         raw = self._lib.wavec_gpu_exec_report_json(self._handle)
-        return json.loads(raw.decode("utf-8")) if raw else {}
+        return json.loads(raw) if raw else {}
 
     @property
     def cmds(self) -> List[dict]:
         return list(self.summary.get("cmds", []))
 
     def set_ids(self, ids) -> None:
-        a = np.ascontiguousarray(ids, dtype=np.uint32)
-        _check(self._lib.wavec_gpu_set_ids(self._handle, _ptr(a, ctypes.c_uint32), int(a.size)),
-               "wavec_gpu_set_ids")
+        v = np.ascontiguousarray(ids, dtype=np.uint32)
+        _raise_on(self._lib.wavec_gpu_set_ids(self._handle, _pointer(v, C.c_uint32), int(v.size)),
+                  "wavec_gpu_set_ids")
 
     def get_ids(self, n: int) -> np.ndarray:
-        out = np.empty(int(n), dtype=np.uint32)
-        _check(self._lib.wavec_gpu_get_ids(self._handle, _ptr(out, ctypes.c_uint32), int(n)),
-               "wavec_gpu_get_ids")
-        return out
+        v = np.empty(int(n), dtype=np.uint32)
+        _raise_on(self._lib.wavec_gpu_get_ids(self._handle, _pointer(v, C.c_uint32), int(n)),
+                  "wavec_gpu_get_ids")
+        return v
 
     def set_history(self, steps: int) -> None:
-        _check(self._lib.wavec_gpu_set_history(self._handle, int(steps)), "wavec_gpu_set_history")
+        _raise_on(self._lib.wavec_gpu_set_history(self._handle, int(steps)),
+                  "wavec_gpu_set_history")
 
     def get_history(self, steps: int, tokens: int) -> np.ndarray:
-        out = np.zeros(int(steps) * int(tokens), dtype=np.uint32)
-        n = self._lib.wavec_gpu_get_history(self._handle, _ptr(out, ctypes.c_uint32), out.size)
-        if n < 0:
-            raise RuntimeError("wavec_gpu_get_history failed: " + last_error())
-        return out.reshape(int(steps), int(tokens))[:n]
+        v = np.zeros((int(steps), int(tokens)), dtype=np.uint32)
+        got = self._lib.wavec_gpu_get_history(self._handle, _pointer(v, C.c_uint32), int(v.size))
+        if got < 0:
+            raise RuntimeError(f"wavec_gpu_get_history: {last_error()}")
+        return v[:got]
 
     def use_graph(self, enable: bool = True) -> None:
-        _check(self._lib.wavec_gpu_use_graph(self._handle, 1 if enable else 0),
-               "wavec_gpu_use_graph")
+        _raise_on(self._lib.wavec_gpu_use_graph(self._handle, int(bool(enable))),
+                  "wavec_gpu_use_graph")
 
     def copy_canvas_from(self, src: "WavePlan", dst_off: int, src_off: int, n: int) -> None:
-        _check(self._lib.wavec_gpu_copy_canvas(self._handle, int(dst_off), src._handle,
-                                               int(src_off), int(n)), "wavec_gpu_copy_canvas")
+        _raise_on(self._lib.wavec_gpu_copy_canvas(self._handle, int(dst_off), src._handle,
+                                                  int(src_off), int(n)),
+                  "wavec_gpu_copy_canvas")
 
     def copy_ids_from(self, src: "WavePlan", dst_first: int, src_first: int, src_step: int,
                       n: int) -> None:
-        _check(self._lib.wavec_gpu_copy_ids(self._handle, int(dst_first), src._handle,
-                                            int(src_first), int(src_step), int(n)),
-               "wavec_gpu_copy_ids")
+        _raise_on(self._lib.wavec_gpu_copy_ids(self._handle, int(dst_first), src._handle,
+                                               int(src_first), int(src_step), int(n)),
+                  "wavec_gpu_copy_ids")
 
 
 class WaveGraph:
-    """5-Pass Wave Graph Builder for Vision (2D Spatial) and LLM (1D Token) Connectomes."""
+    """Graph builder in front of the 5-pass wave compiler: tensors are named blobs, every add_*
+    appends one node (1-D token graphs for LLM-shaped networks, 2-D image graphs for CNNs) and
+    returns its output blob name; compile() lowers the graph to a WavePlan."""
 
     def __init__(
         self,
@@ -303,139 +400,126 @@ class WaveGraph:
     ):
         self._lib = get_lib()
         self._handle = self._lib.wavec_create(int(max_B_per_wave), int(default_S),
-                                              int(kv_cache_max_seq),
-                                              1 if fold_rmsnorm_gamma else 0)
+                                              int(kv_cache_max_seq), int(bool(fold_rmsnorm_gamma)))
         if not self._handle:
-            raise RuntimeError("wavec_create failed")
-        self._lib.wavec_set_reuse_canvas(self._handle, 1 if reuse_canvas else 0)
-        self._lib.wavec_set_batch_size(self._handle, int(batch_size))
-        self._lib.wavec_set_target_preset(self._handle, target.encode("utf-8"))
-        self._keep: list = []
+            raise RuntimeError("wavec_create returned no compiler handle")
+        for fn, arg in ((self._lib.wavec_set_reuse_canvas, int(bool(reuse_canvas))),
+                        (self._lib.wavec_set_batch_size, int(batch_size)),
+                        (self._lib.wavec_set_target_preset, _cstr(target))):
+            _raise_on(fn(self._handle, arg), fn.__name__)
 
     def __del__(self):
-        if getattr(self, "_handle", None):
-            self._lib.wavec_destroy(self._handle)
-            self._handle = None
+        handle, self._handle = getattr(self, "_handle", None), None
+        if handle:
+            self._lib.wavec_destroy(handle)
 
+    def _node(self, fn_name: str, *args) -> None:
+        """Calls wavec_<...>(handle, *args); a failure raises with the library's message."""
+        _raise_on(getattr(self._lib, fn_name)(self._handle, *args), fn_name)
+
+    # ------------------------------------------------------------------ reference API
     def add_input(self, name: str, c: int, h: int = 1, w: int = 1, is_1d: bool = False) -> str:
-        _check(self._lib.wavec_add_input(self._handle, name.encode(), int(c), int(h), int(w),
-                                         1 if is_1d else 0), "wavec_add_input")
+        self._node("wavec_add_input", _cstr(name), int(c), int(h), int(w), int(bool(is_1d)))
         return name
 
     def add_conv2d(self, name: str, in_blob: str, out_blob: str, cin: int, cout: int, kh: int,
                    kw: int, weights: np.ndarray, bias: Optional[np.ndarray] = None,
                    stride: int = 1, pad: int = 0, act: Optional[str] = "silu",
                    res_blob: Optional[str] = None) -> str:
-        w_f32 = np.ascontiguousarray(weights, dtype=np.float32)
-        b_f32 = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
-        _check(self._lib.wavec_add_conv2d(
-            self._handle, name.encode(), in_blob.encode(), out_blob.encode(), int(cin), int(cout),
-            int(kh), int(kw), int(stride), int(pad), ACT_MAP.get(act, 0),
-            _ptr(w_f32, ctypes.c_float), _ptr(b_f32, ctypes.c_float),
-            res_blob.encode() if res_blob else None), "wavec_add_conv2d")
+        """weights: [cout][cin][kh][kw] (fp32 or anything convertible); bias: [cout] or None."""
+        w, b = _f32(weights), _f32(bias)
+        self._node("wavec_add_conv2d", _cstr(name), _cstr(in_blob), _cstr(out_blob), int(cin),
+                   int(cout), int(kh), int(kw), int(stride), int(pad), ACT_MAP.get(act, 0),
+                   _pointer(w, C.c_float), _pointer(b, C.c_float), _cstr(res_blob))
         return out_blob
 
     def add_linear(self, name: str, in_blob: str, out_blob: str, cin: int, cout: int,
                    weights: np.ndarray, bias: Optional[np.ndarray] = None,
                    act: Optional[str] = None, res_blob: Optional[str] = None) -> str:
-        b_f32 = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
-        res_c = res_blob.encode() if res_blob else None
-        if weights.dtype == np.float16 or weights.dtype == np.uint16:
-            w_u16 = np.ascontiguousarray(weights.view(np.uint16), dtype=np.uint16)
-            rc = self._lib.wavec_add_linear_f16(
-                self._handle, name.encode(), in_blob.encode(), out_blob.encode(), int(cin),
-                int(cout), ACT_MAP.get(act, 0), _ptr(w_u16, ctypes.c_uint16),
-                _ptr(b_f32, ctypes.c_float), res_c)
+        """weights [cout][cin]: fp16 / uint16 arrays go through the fp16 entry point unchanged,
+        anything else is passed as fp32 (rounded to fp16 by the compiler)."""
+        b = _f32(bias)
+        if weights.dtype in (np.float16, np.uint16):
+            fn, w = "wavec_add_linear_f16", _f16_bits(weights)
+            wp = _pointer(w, C.c_uint16)
         else:
-            w_f32 = np.ascontiguousarray(weights, dtype=np.float32)
-            rc = self._lib.wavec_add_linear_f32(
-                self._handle, name.encode(), in_blob.encode(), out_blob.encode(), int(cin),
-                int(cout), ACT_MAP.get(act, 0), _ptr(w_f32, ctypes.c_float),
-                _ptr(b_f32, ctypes.c_float), res_c)
-        _check(rc, "wavec_add_linear")
+            fn, w = "wavec_add_linear_f32", _f32(weights)
+            wp = _pointer(w, C.c_float)
+        self._node(fn, _cstr(name), _cstr(in_blob), _cstr(out_blob), int(cin), int(cout),
+                   ACT_MAP.get(act, 0), wp, _pointer(b, C.c_float), _cstr(res_blob))
         return out_blob
 
     def add_rmsnorm(self, name: str, in_blob: str, out_blob: str, dim: int, gamma: np.ndarray,
                     eps: float = 1e-5, pre_folded: bool = False) -> str:
-        g_f32 = np.ascontiguousarray(gamma, dtype=np.float32)
-        _check(self._lib.wavec_add_rmsnorm(
-            self._handle, name.encode(), in_blob.encode(), out_blob.encode(), int(dim),
-            ctypes.c_float(eps), _ptr(g_f32, ctypes.c_float), 1 if pre_folded else 0),
-            "wavec_add_rmsnorm")
+        g = _f32(gamma)
+        self._node("wavec_add_rmsnorm", _cstr(name), _cstr(in_blob), _cstr(out_blob), int(dim),
+                   C.c_float(eps), _pointer(g, C.c_float), int(bool(pre_folded)))
         return out_blob
 
     def add_swiglu(self, name: str, gate_blob: str, up_blob: str, out_blob: str,
                    dim: int = 0) -> str:
-        _check(self._lib.wavec_add_swiglu(self._handle, name.encode(), gate_blob.encode(),
-                                          up_blob.encode(), out_blob.encode()),
-               "wavec_add_swiglu")
+        """Element-wise gate * up (the gate's SiLU is its projection's epilogue); `dim` is
+        accepted for the reference signature and not used (the shapes come from the blobs)."""
+        self._node("wavec_add_swiglu", _cstr(name), _cstr(gate_blob), _cstr(up_blob),
+                   _cstr(out_blob))
         return out_blob
 
     def add_rope_gqa_attn(self, name: str, q_blob: str, k_blob: str, v_blob: str, out_blob: str,
                           h_q: int, h_kv: int, head_dim: int, rope_theta: float = 10000.0,
                           llama3_scaling: bool = False) -> str:
-        _check(self._lib.wavec_add_rope_gqa_attn(
-            self._handle, name.encode(), q_blob.encode(), k_blob.encode(), v_blob.encode(),
-            out_blob.encode(), int(h_q), int(h_kv), int(head_dim), ctypes.c_float(rope_theta),
-            1 if llama3_scaling else 0), "wavec_add_rope_gqa_attn")
+        self._node("wavec_add_rope_gqa_attn", _cstr(name), _cstr(q_blob), _cstr(k_blob),
+                   _cstr(v_blob), _cstr(out_blob), int(h_q), int(h_kv), int(head_dim),
+                   C.c_float(rope_theta), int(bool(llama3_scaling)))
         return out_blob
 
     def add_maxpool(self, name: str, in_blob: str, out_blob: str, kernel_size: int = 5,
                     stride: int = 1, pad: int = 2) -> str:
-        _check(self._lib.wavec_add_maxpool(self._handle, name.encode(), in_blob.encode(),
-                                           out_blob.encode(), int(kernel_size), int(stride),
-                                           int(pad)), "wavec_add_maxpool")
-        return out_blob
-
-    def add_upconv2x2(self, name: str, in_blob: str, out_blob: str, cin: int, cout: int,
-                      weights: np.ndarray, bias: Optional[np.ndarray] = None) -> str:
-        """2x2 stride-2 transposed convolution; weights [cout][cin][2][2] (C ABI
-        wavec_add_upconv2x2, which the reference binds but wraps in no method)."""
-        w = np.ascontiguousarray(weights, dtype=np.float32)
-        b = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
-        _check(self._lib.wavec_add_upconv2x2(self._handle, name.encode(), in_blob.encode(),
-                                             out_blob.encode(), int(cin), int(cout),
-                                             _ptr(w, ctypes.c_float), _ptr(b, ctypes.c_float)),
-               "wavec_add_upconv2x2")
+        self._node("wavec_add_maxpool", _cstr(name), _cstr(in_blob), _cstr(out_blob),
+                   int(kernel_size), int(stride), int(pad))
         return out_blob
 
     def add_upsample2x(self, name: str, in_blob: str, out_blob: str) -> str:
-        _check(self._lib.wavec_add_upsample2x(self._handle, name.encode(), in_blob.encode(),
-                                              out_blob.encode()), "wavec_add_upsample2x")
+        self._node("wavec_add_upsample2x", _cstr(name), _cstr(in_blob), _cstr(out_blob))
         return out_blob
 
     def add_split(self, name: str, in_blob: str, out_blobs: Sequence[str]) -> List[str]:
-        arr = (ctypes.c_char_p * len(out_blobs))(*[b.encode() for b in out_blobs])
-        _check(self._lib.wavec_add_split(self._handle, name.encode(), in_blob.encode(),
-                                         len(out_blobs), arr), "wavec_add_split")
-        return list(out_blobs)
+        names = list(out_blobs)
+        self._node("wavec_add_split", _cstr(name), _cstr(in_blob), len(names), _name_array(names))
+        return names
 
     def add_slice(self, name: str, in_blob: str, out_blobs: Sequence[str],
                   slice_sizes: Sequence[int]) -> List[str]:
-        arr = (ctypes.c_char_p * len(out_blobs))(*[b.encode() for b in out_blobs])
-        sz = (ctypes.c_int * len(slice_sizes))(*[int(s) for s in slice_sizes])
-        _check(self._lib.wavec_add_slice(self._handle, name.encode(), in_blob.encode(),
-                                         len(out_blobs), arr, sz), "wavec_add_slice")
-        return list(out_blobs)
+        names, sizes = list(out_blobs), [int(s) for s in slice_sizes]
+        self._node("wavec_add_slice", _cstr(name), _cstr(in_blob), len(names), _name_array(names),
+                   (C.c_int * len(sizes))(*sizes))
+        return names
 
     def add_concat(self, name: str, in_blobs: Sequence[str], out_blob: str) -> str:
-        arr = (ctypes.c_char_p * len(in_blobs))(*[b.encode() for b in in_blobs])
-        _check(self._lib.wavec_add_concat(self._handle, name.encode(), len(in_blobs), arr,
-                                          out_blob.encode()), "wavec_add_concat")
+        names = list(in_blobs)
+        self._node("wavec_add_concat", _cstr(name), len(names), _name_array(names),
+                   _cstr(out_blob))
         return out_blob
 
     def set_output(self, out_blob: str) -> None:
-        _check(self._lib.wavec_set_output(self._handle, out_blob.encode()), "wavec_set_output")
+        self._node("wavec_set_output", _cstr(out_blob))
 
     def compile(self) -> WavePlan:
-        rc = self._lib.wavec_compile(self._handle)
-        if rc != 0:
-            raise RuntimeError("WaveGraph 5-pass compilation failed: " + last_error())
-        raw_json = self._lib.wavec_get_summary_json(self._handle)
-        summary = json.loads(raw_json.decode("utf-8")) if raw_json else {}
-        return WavePlan(self._handle, self._lib, summary, owner=self)
+        """Runs the five compiler passes and returns the plan with its summary."""
+        if self._lib.wavec_compile(self._handle) != 0:
+            raise RuntimeError(f"the wave compiler rejected this graph: {last_error()}")
+        raw = self._lib.wavec_get_summary_json(self._handle)
+        return WavePlan(self._handle, self._lib, json.loads(raw) if raw else {}, owner=self)
 
-    # ---------------------------------------------------------------- build extensions
+    # ------------------------------------------------------------------ extensions
+    def add_upconv2x2(self, name: str, in_blob: str, out_blob: str, cin: int, cout: int,
+                      weights: np.ndarray, bias: Optional[np.ndarray] = None) -> str:
+        """2x2 stride-2 transposed convolution, weights [cout][cin][2][2] (the reference exports
+        wavec_add_upconv2x2 but its Python module has no method for it)."""
+        w, b = _f32(weights), _f32(bias)
+        self._node("wavec_add_upconv2x2", _cstr(name), _cstr(in_blob), _cstr(out_blob), int(cin),
+                   int(cout), _pointer(w, C.c_float), _pointer(b, C.c_float))
+        return out_blob
+
     def add_sparse_wave(self, name: str, in_blob: str, out_blob: str, rows: np.ndarray,
                         weights: np.ndarray, bias: Optional[np.ndarray] = None,
                         cluster: int = 1, act: Optional[str] = None,
@@ -446,12 +530,11 @@ class WaveGraph:
         r = np.ascontiguousarray(rows, dtype=np.uint32)
         if r.shape != (cout // cluster, fan_in):
             raise ValueError(f"rows must have shape {(cout // cluster, fan_in)}, got {r.shape}")
-        b = _f16_bits(bias) if bias is not None else None
-        _check(self._lib.wavec_add_sparse_wave(
-            self._handle, name.encode(), in_blob.encode(), out_blob.encode(), int(cout),
-            int(fan_in), int(cluster), _ptr(r, ctypes.c_uint32), _ptr(w, ctypes.c_uint16),
-            _ptr(b, ctypes.c_uint16), ACT_MAP.get(act, 0),
-            res_blob.encode() if res_blob else None), "wavec_add_sparse_wave")
+        b = _opt_f16_bits(bias)
+        self._node("wavec_add_sparse_wave", _cstr(name), _cstr(in_blob), _cstr(out_blob),
+                   int(cout), int(fan_in), int(cluster), _pointer(r, C.c_uint32),
+                   _pointer(w, C.c_uint16), _pointer(b, C.c_uint16), ACT_MAP.get(act, 0),
+                   _cstr(res_blob))
         return out_blob
 
     def add_cluster_wave(self, name: str, in_blob: str, out_blob: str, starts: np.ndarray,
@@ -461,17 +544,15 @@ class WaveGraph:
         """starts: [cout/cluster, K] first input channel of each dendritic cluster of seg_len
         consecutive channels; weights [cout, K*seg_len]."""
         w = _f16_bits(weights)
-        cout = w.shape[0]
         st = np.ascontiguousarray(starts, dtype=np.uint32)
-        K = st.shape[1]
+        cout, K = w.shape[0], st.shape[1]
         if st.shape[0] * cluster != cout or w.shape[1] != K * seg_len:
             raise ValueError("starts / weights shapes do not match cout, cluster, K, seg_len")
-        b = _f16_bits(bias) if bias is not None else None
-        _check(self._lib.wavec_add_cluster_wave(
-            self._handle, name.encode(), in_blob.encode(), out_blob.encode(), int(cout), int(K),
-            int(seg_len), int(cluster), _ptr(st, ctypes.c_uint32), _ptr(w, ctypes.c_uint16),
-            _ptr(b, ctypes.c_uint16), ACT_MAP.get(act, 0),
-            res_blob.encode() if res_blob else None), "wavec_add_cluster_wave")
+        b = _opt_f16_bits(bias)
+        self._node("wavec_add_cluster_wave", _cstr(name), _cstr(in_blob), _cstr(out_blob),
+                   int(cout), int(K), int(seg_len), int(cluster), _pointer(st, C.c_uint32),
+                   _pointer(w, C.c_uint16), _pointer(b, C.c_uint16), ACT_MAP.get(act, 0),
+                   _cstr(res_blob))
         return out_blob
 
     def add_pruned_wave(self, name: str, in_blob: str, out_blob: str, starts: np.ndarray,
@@ -485,12 +566,11 @@ class WaveGraph:
         cout, K = st.shape
         if w.shape != (cout, K * seg_len):
             raise ValueError("starts / weights shapes do not match cout, K, seg_len")
-        b = _f16_bits(bias) if bias is not None else None
-        _check(self._lib.wavec_add_pruned_wave(
-            self._handle, name.encode(), in_blob.encode(), out_blob.encode(), int(cout), int(K),
-            int(seg_len), int(tile), _ptr(st, ctypes.c_uint32), _ptr(w, ctypes.c_uint16),
-            _ptr(b, ctypes.c_uint16), ACT_MAP.get(act, 0),
-            res_blob.encode() if res_blob else None), "wavec_add_pruned_wave")
+        b = _opt_f16_bits(bias)
+        self._node("wavec_add_pruned_wave", _cstr(name), _cstr(in_blob), _cstr(out_blob),
+                   int(cout), int(K), int(seg_len), int(tile), _pointer(st, C.c_uint32),
+                   _pointer(w, C.c_uint16), _pointer(b, C.c_uint16), ACT_MAP.get(act, 0),
+                   _cstr(res_blob))
         return out_blob
 
     def add_token_shift(self, name: str, in_blob: str, out_blob: str, mu: np.ndarray,
@@ -498,35 +578,30 @@ class WaveGraph:
         """Causal depth-wise mix over the last rf tokens of each request; mu: [dim, rf]."""
         m = _f16_bits(mu)
         dim, rf = m.shape
-        _check(self._lib.wavec_add_token_shift(self._handle, name.encode(), in_blob.encode(),
-                                               out_blob.encode(), int(dim), int(rf),
-                                               int(seq_len), _ptr(m, ctypes.c_uint16),
-                                               1 if decode else 0), "wavec_add_token_shift")
+        self._node("wavec_add_token_shift", _cstr(name), _cstr(in_blob), _cstr(out_blob),
+                   int(dim), int(rf), int(seq_len), _pointer(m, C.c_uint16), int(bool(decode)))
         return out_blob
 
     def add_embedding(self, name: str, tok_blob: str, out_blob: str, table: np.ndarray) -> str:
         """y[c][t] = table[id[t]][c]; table: [vocab, dim]."""
         t = _f16_bits(table)
         vocab, dim = t.shape
-        _check(self._lib.wavec_add_embedding(self._handle, name.encode(), tok_blob.encode(),
-                                             out_blob.encode(), int(vocab), int(dim),
-                                             _ptr(t, ctypes.c_uint16)), "wavec_add_embedding")
+        self._node("wavec_add_embedding", _cstr(name), _cstr(tok_blob), _cstr(out_blob),
+                   int(vocab), int(dim), _pointer(t, C.c_uint16))
         return out_blob
 
     def add_argmax(self, name: str, in_blob: str, out_blob: str) -> str:
-        _check(self._lib.wavec_add_argmax(self._handle, name.encode(), in_blob.encode(),
-                                          out_blob.encode()), "wavec_add_argmax")
+        self._node("wavec_add_argmax", _cstr(name), _cstr(in_blob), _cstr(out_blob))
         return out_blob
 
     def save_tcff(self, path: Union[str, Path], model_prefix: str = "K44Model",
                   include_geometry: bool = True) -> None:
-        _check(self._lib.wavec_save_tcff_ex(self._handle, str(path).encode(),
-                                            model_prefix.encode(), 1,
-                                            1 if include_geometry else 0), "wavec_save_tcff_ex")
+        self._node("wavec_save_tcff_ex", _cstr(path), _cstr(model_prefix), 1,
+                   int(bool(include_geometry)))
 
 
 class DeviceBuffer:
-    """Device memory owned through libk44wavec.so (hipMalloc / hipFree), for the stand-alone
+    """Device memory allocated by libk44wavec.so (hipMalloc / hipFree) for the stand-alone
     kernels; `.ptr` is the device address."""
 
     def __init__(self, nbytes: int):
@@ -534,7 +609,7 @@ class DeviceBuffer:
         self._lib = get_lib()
         self.ptr = self._lib.wavec_dev_malloc(self.nbytes)
         if not self.ptr:
-            raise RuntimeError(f"wavec_dev_malloc({self.nbytes}) failed: {last_error()}")
+            raise RuntimeError(f"wavec_dev_malloc({self.nbytes}): {last_error()}")
 
     @classmethod
     def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
@@ -546,21 +621,22 @@ class DeviceBuffer:
     def upload(self, a: np.ndarray) -> None:
         a = np.ascontiguousarray(a)
         if a.nbytes > self.nbytes:
-            raise ValueError("array larger than the device buffer")
-        _check(self._lib.wavec_dev_upload(self.ptr, a.ctypes.data, a.nbytes), "wavec_dev_upload")
+            raise ValueError(f"{a.nbytes} bytes do not fit a {self.nbytes}-byte device buffer")
+        _raise_on(self._lib.wavec_dev_upload(self.ptr, a.ctypes.data, a.nbytes),
+                  "wavec_dev_upload")
 
     def download(self, dtype, shape) -> np.ndarray:
         out = np.empty(shape, dtype=dtype)
         if out.nbytes > self.nbytes:
-            raise ValueError("requested more bytes than the device buffer holds")
-        _check(self._lib.wavec_dev_download(out.ctypes.data, self.ptr, out.nbytes),
-               "wavec_dev_download")
+            raise ValueError(f"{out.nbytes} bytes requested from a {self.nbytes}-byte buffer")
+        _raise_on(self._lib.wavec_dev_download(out.ctypes.data, self.ptr, out.nbytes),
+                  "wavec_dev_download")
         return out
 
     def free(self) -> None:
-        if self.ptr:
-            self._lib.wavec_dev_free(self.ptr)
-            self.ptr = None
+        ptr, self.ptr = self.ptr, None
+        if ptr:
+            self._lib.wavec_dev_free(ptr)
 
     def __del__(self):
         try:
@@ -570,7 +646,7 @@ class DeviceBuffer:
 
 
 def device_synchronize() -> None:
-    _check(get_lib().wavec_dev_synchronize(), "wavec_dev_synchronize")
+    _raise_on(get_lib().wavec_dev_synchronize(), "wavec_dev_synchronize")
 
 
 def _dev_ptr(x) -> int:
@@ -589,8 +665,7 @@ def forward_token64_f16(Y, X, cluster_indices, cluster_weights_wmma, neuron_bias
     launch_k44_f16_forward): X [ceil(batch/64)][Cin][64] fp16 -> Y [ceil(batch/64)][Cout][64]
     fp16, round toward zero.  Arguments are device tensors (anything with data_ptr()) or raw
     device addresses; `stream` a hipStream_t address or None.  Asynchronous."""
-    lib = get_lib()
-    _check(lib.wavec_k44_f16_forward_token64(
+    _raise_on(get_lib().wavec_k44_f16_forward_token64(
         _dev_ptr(Y), _dev_ptr(X), _dev_ptr(cluster_indices), _dev_ptr(cluster_weights_wmma),
         _dev_ptr(neuron_bias) or None, int(batch_size), int(Cin), int(Cout), int(B_vec16),
         int(cluster_size), _dev_ptr(stream) or None), "wavec_k44_f16_forward_token64")
@@ -599,8 +674,14 @@ def forward_token64_f16(Y, X, cluster_indices, cluster_weights_wmma, neuron_bias
 def interleave_weights_wmma(dst_wmma, src_compact, num_output_neurons: int, B_vec8: int,
                             stream=None) -> None:
     """GPU weight interleave: row-major [neurons][8*B_vec8] fp16 -> RDNA4 WMMA vector order."""
-    lib = get_lib()
-    _check(lib.wavec_interleave_weights_wmma(_dev_ptr(dst_wmma), _dev_ptr(src_compact),
-                                             int(num_output_neurons), int(B_vec8),
-                                             _dev_ptr(stream) or None),
-           "wavec_interleave_weights_wmma")
+    _raise_on(get_lib().wavec_interleave_weights_wmma(
+        _dev_ptr(dst_wmma), _dev_ptr(src_compact), int(num_output_neurons), int(B_vec8),
+        _dev_ptr(stream) or None), "wavec_interleave_weights_wmma")
+
+
+def argmax_f16(ids, logits, vocab: int, stride: int, tokens: int, stream=None) -> None:
+    """ids[t] = argmax_c logits[c][t] (lowest channel on ties) on caller-owned device memory:
+    logits [vocab][stride] fp16, ids [tokens] uint32.  Asynchronous on `stream`."""
+    _raise_on(get_lib().wavec_argmax_f16(_dev_ptr(ids), _dev_ptr(logits), int(vocab), int(stride),
+                                         int(tokens), _dev_ptr(stream) or None),
+              "wavec_argmax_f16")

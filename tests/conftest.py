@@ -26,3 +26,12 @@ def orc():
 
     oracle.lib()
     return oracle
+
+
+@pytest.fixture
+def tuning(wavec):
+    """wavec.set_tuning for the duration of one test: every executor tuning switch is back to
+    automatic (-1) before and after it."""
+    wavec.reset_tuning()
+    yield wavec.set_tuning
+    wavec.reset_tuning()

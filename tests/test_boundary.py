@@ -90,12 +90,6 @@ def test_invalid_sparse_wave_is_rejected(wavec):
 
 def test_unsupported_plans_fail_init_with_message(wavec):
     """The executor refuses what it cannot run instead of silently skipping it."""
-    g = wavec.WaveGraph(kv_cache_max_seq=0, batch_size=64)  # 64-frame interleaved image layout
-    g.add_input("img", 8, 16, 64)
-    g.add_conv2d("c", "img", "y", 8, 16, 3, 3, np.zeros((16, 8, 3, 3), np.float32), act="relu")
-    plan = g.compile()
-    with pytest.raises(RuntimeError, match="64-frame interleaved"):
-        plan.init_gpu()
     g2 = wavec.WaveGraph(kv_cache_max_seq=0)
     g2.add_input("t", 128, 1, 64, is_1d=True)
     g2.add_rope_gqa_attn("a", "t", "t", "t", "o", 2, 2, 64)
@@ -117,3 +111,93 @@ def test_token64_and_interleave_validate_before_touching_the_gpu(wavec):
     assert lib.wavec_interleave_weights_wmma(1, 1, 20, 4, None) == -1  # 20 neurons
     assert lib.wavec_interleave_weights_wmma(1, 1, 32, 3, None) == -1  # odd B_vec8
     assert lib.wavec_interleave_weights_wmma(None, 1, 32, 4, None) == -1
+
+
+def test_tuning_switches_set_get_reset(wavec):
+    wavec.reset_tuning()
+    for key in ("path", "dma", "fuse", "group", "t64_ring", "narrow_chunk"):
+        assert wavec.get_tuning(key) == -1
+    wavec.set_tuning("fuse", 0)
+    wavec.set_tuning("narrow_chunk", 32)
+    assert wavec.get_tuning("fuse") == 0 and wavec.get_tuning("narrow_chunk") == 32
+    with pytest.raises(RuntimeError, match="unknown tuning key"):
+        wavec.set_tuning("no_such_switch", 1)
+    with pytest.raises(RuntimeError, match="-1"):
+        wavec.set_tuning("fuse", -5)
+    with pytest.raises(RuntimeError, match="unknown tuning key"):
+        wavec.get_tuning("no_such_switch")
+    wavec.reset_tuning()
+    assert wavec.get_tuning("fuse") == -1 and wavec.get_tuning("narrow_chunk") == -1
+
+
+# The reference binding's public methods and their parameters (wavec/wavec.py:147-344): the
+# drop-in contract of snntome_amd.wavec.
+REFERENCE_PY_API = {
+    "WavePlan": {
+        "__init__": ["self", "handle", "lib", "summary"],
+        "save_tcff": ["self", "tcff_path", "model_prefix"],
+        "load_tcff_weights": ["self", "tcff_path"],
+        "init_gpu": ["self"],
+        "infer_f32": ["self", "x"],
+    },
+    "WaveGraph": {
+        "__init__": ["self", "max_B_per_wave", "default_S", "kv_cache_max_seq",
+                     "fold_rmsnorm_gamma", "reuse_canvas", "batch_size", "target"],
+        "add_input": ["self", "name", "c", "h", "w", "is_1d"],
+        "add_conv2d": ["self", "name", "in_blob", "out_blob", "cin", "cout", "kh", "kw",
+                       "weights", "bias", "stride", "pad", "act", "res_blob"],
+        "add_linear": ["self", "name", "in_blob", "out_blob", "cin", "cout", "weights", "bias",
+                       "act", "res_blob"],
+        "add_rmsnorm": ["self", "name", "in_blob", "out_blob", "dim", "gamma", "eps",
+                        "pre_folded"],
+        "add_swiglu": ["self", "name", "gate_blob", "up_blob", "out_blob", "dim"],
+        "add_rope_gqa_attn": ["self", "name", "q_blob", "k_blob", "v_blob", "out_blob", "h_q",
+                              "h_kv", "head_dim", "rope_theta", "llama3_scaling"],
+        "add_maxpool": ["self", "name", "in_blob", "out_blob", "kernel_size", "stride", "pad"],
+        "add_upsample2x": ["self", "name", "in_blob", "out_blob"],
+        "add_split": ["self", "name", "in_blob", "out_blobs"],
+        "add_slice": ["self", "name", "in_blob", "out_blobs", "slice_sizes"],
+        "add_concat": ["self", "name", "in_blobs", "out_blob"],
+        "set_output": ["self", "out_blob"],
+        "compile": ["self"],
+    },
+}
+REFERENCE_PY_DEFAULTS = {
+    ("WaveGraph", "__init__"): (288, 0, 2048, True, False, 1, "auto"),
+    ("WaveGraph", "add_conv2d"): (None, 1, 0, "silu", None),
+    ("WaveGraph", "add_linear"): (None, None, None),
+    ("WaveGraph", "add_rmsnorm"): (1e-5, False),
+    ("WaveGraph", "add_maxpool"): (5, 1, 2),
+    ("WaveGraph", "add_rope_gqa_attn"): (10000.0, False),
+    ("WavePlan", "save_tcff"): ("K44Model",),
+}
+
+
+def test_python_api_keeps_reference_signatures(wavec):
+    import inspect
+
+    assert {k: v for k, v in wavec.ACT_MAP.items() if v <= 4} == {
+        None: 0, "none": 0, "identity": 0, "linear": 0, "relu": 1, "sigmoid": 2, "silu": 3,
+        "swish": 3, "leaky_relu": 4}
+    for cls_name, methods in REFERENCE_PY_API.items():
+        cls = getattr(wavec, cls_name)
+        for m, params in methods.items():
+            sig = inspect.signature(getattr(cls, m))
+            got = list(sig.parameters)
+            assert got[:len(params)] == params, (cls_name, m, got)
+            extra = [p for p in list(sig.parameters.values())[len(params):]]
+            assert all(p.default is not inspect.Parameter.empty for p in extra), (cls_name, m)
+            want = REFERENCE_PY_DEFAULTS.get((cls_name, m))
+            if want is not None:
+                defs = tuple(p.default for p in sig.parameters.values()
+                             if p.default is not inspect.Parameter.empty)
+                assert defs[:len(want)] == want, (cls_name, m, defs)
+
+
+def test_standalone_argmax_validates_before_touching_the_gpu(wavec):
+    lib = wavec.get_lib()
+    assert lib.wavec_argmax_f16(None, 1, 100, 64, 10, None) == -1
+    assert "required" in wavec.last_error()
+    assert lib.wavec_argmax_f16(1, 1, 100, 100, 10, None) == -1  # stride not a multiple of 64
+    assert lib.wavec_argmax_f16(1, 1, 100, 64, 65, None) == -1  # more tokens than the stride
+    assert lib.wavec_argmax_f16(1, 1, 0, 64, 10, None) == -1

@@ -89,3 +89,19 @@ def test_layout_modes():
     o = m.offsets(1)
     assert o[0, 0, 4, 29] == 5 * 34 + 4 + 29  # last pixel: row H, column 4 + W - 1
     assert len(np.unique(o)) == o.size
+
+
+def test_layout_token64_interleaved():
+    """64-frame interleaved layout: pixel-major, 64 frames contiguous, blocks of 64 frames
+    64 * single_stride apart; every pixel element distinct and inside the channel stride."""
+    for H, W in ((6, 10), (8, 64)):
+        L = co.Layout2D(H, W, 128, tok64=True)
+        off = L.offsets(3)  # [F][C][H][W]
+        assert off[0, 0, 0, 0] == (L.W_pad + 1) * 64
+        assert off[63, 0, 0, 0] - off[0, 0, 0, 0] == 63
+        assert off[0, 0, 0, 1] - off[0, 0, 0, 0] == 64
+        assert off[0, 0, 1, 0] - off[0, 0, 0, 0] == 64 * L.W_pad
+        assert off[64, 0, 0, 0] - off[0, 0, 0, 0] == 64 * L.single_stride
+        assert off[0, 1, 0, 0] - off[0, 0, 0, 0] == L.channel_stride == 128 * L.single_stride
+        assert len(np.unique(off)) == off.size
+        assert off[:, 0].max() < L.channel_stride

@@ -8,7 +8,7 @@ import pytest
 from oracle import llm_oracle as lo
 from snntome_amd import synth
 
-from wave_cases import TOL, stride_of
+from wave_cases import PATH_IDS, TOL, stride_of
 
 pytestmark = pytest.mark.gpu
 
@@ -111,9 +111,9 @@ def _check_commands(plan, spec, wts, ids, decode, tag):
 
 
 @pytest.mark.parametrize("path", ["auto", "valu"])
-def test_llm_prefill_commandwise_and_end_to_end(wavec, monkeypatch, path):
+def test_llm_prefill_commandwise_and_end_to_end(wavec, tuning, path):
     if path != "auto":
-        monkeypatch.setenv("K44WAVEC_PATH", path)
+        tuning("path", PATH_IDS[path])
     wts = synth.llm_weights(TINY)
     plan = synth.build_llm_graph(TINY, wts, decode=False, wavec_mod=wavec).compile()
     plan.init_gpu()
@@ -322,7 +322,7 @@ def test_rmsnorm_and_embed_shapes(wavec, D, tokens):
 
 
 @pytest.mark.parametrize("tokens,tiles", [(64, 2), (64, 40), (512, 1), (300, 3)])
-def test_mfma_split_k_matches_oracle_and_unsplit(wavec, orc, monkeypatch, tokens, tiles):
+def test_mfma_split_k_matches_oracle_and_unsplit(wavec, orc, tuning, tokens, tiles):
     """Small tile x token-tile grids run split-K (partials + ordered reduction); the result is
     within tolerance of the oracle and of the single-pass kernel, and identical across runs."""
     rng = np.random.default_rng(tokens + tiles)
@@ -335,7 +335,7 @@ def test_mfma_split_k_matches_oracle_and_unsplit(wavec, orc, monkeypatch, tokens
     outs = {}
     for mode in ("split", "single"):
         if mode == "single":
-            monkeypatch.setenv("K44WAVEC_SPLITK", "0")
+            tuning("splitk", 0)
         g = wavec.WaveGraph(kv_cache_max_seq=0)
         g.add_input("x", C, 1, tokens, is_1d=True)
         g.add_cluster_wave("w", "x", "y", starts, S, w, b, cluster=nt, act="gelu", res_blob="x")
@@ -364,7 +364,7 @@ def test_mfma_split_k_matches_oracle_and_unsplit(wavec, orc, monkeypatch, tokens
 
 
 @pytest.mark.parametrize("decode", [False, True])
-def test_grouped_launches_match_per_wave(wavec, monkeypatch, decode):
+def test_grouped_launches_match_per_wave(wavec, tuning, decode):
     """Independent MFMA waves (sub-waves of a pruned projection, projections of one input) run
     as one grouped launch; the logits are bit-identical to launching every wave alone."""
     wts = synth.llm_weights(TINY)
@@ -374,7 +374,7 @@ def test_grouped_launches_match_per_wave(wavec, monkeypatch, decode):
     out = {}
     for mode in ("grouped", "alone"):
         if mode == "alone":
-            monkeypatch.setenv("K44WAVEC_GROUP", "0")
+            tuning("group", 0)
         plan = synth.build_llm_graph(TINY, wts, decode=decode, wavec_mod=wavec).compile()
         plan.init_gpu()
         rep = plan.exec_report()
@@ -391,10 +391,10 @@ def test_grouped_launches_match_per_wave(wavec, monkeypatch, decode):
     assert np.array_equal(out["grouped_ids"], out["alone_ids"])
 
 
-def test_folded_multiplies_match_unfolded(wavec, monkeypatch):
+def test_folded_multiplies_match_unfolded(wavec, tuning):
     """Decode plans fold the element-wise multiplies (k*v, q*(k*v), g*u) into the gathers of the
     narrow MFMA waves that read the products; ids and logits of several decode steps are
-    bit-identical to the plan that launches every multiply (K44WAVEC_FUSE=0)."""
+    bit-identical to the plan that launches every multiply (tuning switch fuse=0)."""
     spec = TINY
     steps = 4
     wts = synth.llm_weights(spec)
@@ -403,9 +403,9 @@ def test_folded_multiplies_match_unfolded(wavec, monkeypatch):
     plans = {}
     for mode in ("folded", "launched"):
         if mode == "launched":
-            monkeypatch.setenv("K44WAVEC_FUSE", "0")
+            tuning("fuse", 0)
         else:
-            monkeypatch.delenv("K44WAVEC_FUSE", raising=False)
+            tuning("fuse", -1)
         p = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
         p.init_gpu()
         plans[mode] = p
@@ -469,3 +469,126 @@ def test_decode_step_full_width_against_oracle(wavec):
     srt = np.sort(want, axis=0)
     clear = (srt[-1] - srt[-2]) > 0.05
     assert np.array_equal(dec.get_ids(R)[clear], ref.ids[clear])
+
+
+@pytest.mark.parametrize("decode", [False, True])
+@pytest.mark.parametrize("mode", ["commands", "runs"])
+def test_plan_checker_tiny(wavec, decode, mode):
+    """The node-by-node checker of the full-size tests (tests/llm_check.py) on the tiny decoder:
+    command-wise and run-wise (group launches, folded multiplies, fused RMSNorm + token shift),
+    prefill and a decode step after the hand-over."""
+    from llm_check import PlanChecker
+
+    wts = synth.llm_weights(TINY)
+    pre = synth.build_llm_graph(TINY, wts, decode=False, wavec_mod=wavec).compile()
+    pre.init_gpu()
+    R, P = TINY.requests, TINY.prompt
+    ids = np.random.default_rng(21).integers(0, TINY.vocab, R * P).astype(np.uint32)
+    if not decode:
+        PlanChecker(pre, TINY, wts, R * P, False, log=_log).run(mode, ids, f"tiny prefill {mode}")
+        return
+    pre.set_ids(ids)
+    pre.execute(1)
+    dec = synth.build_llm_graph(TINY, wts, decode=True, wavec_mod=wavec).compile()
+    dec.init_gpu()
+    synth.llm_handoff(TINY, pre, dec)
+    chk = PlanChecker(dec, TINY, wts, R, True, log=_log)
+    for step in range(2):
+        chk.run(mode, dec.get_ids(R), f"tiny decode {mode} step {step}")
+
+
+def _norm_shift_graph(wavec, D, req, rf, mu, gamma, dead_input):
+    """tok -> embedding e (dead_input: e is read only by the RMSNorm) or input x (kept alive as
+    the plan input) -> RMSNorm u -> decode token shift s."""
+    g = wavec.WaveGraph(kv_cache_max_seq=0, fold_rmsnorm_gamma=False)
+    if dead_input:
+        table = (np.random.default_rng(rf).standard_normal((50, D)) * 2).astype(np.float16)
+        g.add_input("tok", 1, 1, req, is_1d=True)
+        g.add_embedding("emb", "tok", "x", table)
+    else:
+        table = None
+        g.add_input("x", D, 1, req, is_1d=True)
+    g.add_rmsnorm("n", "x", "u", D, gamma)
+    g.add_token_shift("ts", "u", "s", mu, 1, decode=True)
+    g.set_output("s")
+    return g, table
+
+
+@pytest.mark.parametrize("dead_input", [False, True])
+@pytest.mark.parametrize("rf", [1, 2, 5, 9])
+def test_fused_norm_shift_every_rf(wavec, tuning, rf, dead_input):
+    """Decode RMSNorm -> token shift for receptive fields 1, 2, 5 and 9.  With the norm's input
+    alive after it (the plan input) the two run as one kernel; with an input that dies at the
+    norm, the canvas allocator gives its range to the shift output and the executor must keep
+    two launches (one fused kernel would overwrite rows other workgroups still sum).  Either
+    way: outputs and state bit for bit equal to the plan with fusion off, and within tolerance
+    of the oracle, over two steps."""
+    D, req = 2048, 16
+    rng = np.random.default_rng(100 + rf)
+    mu = (rng.standard_normal((D, rf)) * 0.5).astype(np.float16)
+    gamma = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    outs = {}
+    for mode in ("fused", "unfused"):
+        tuning("fuse", 0 if mode == "unfused" else -1)
+        g, table = _norm_shift_graph(wavec, D, req, rf, mu, gamma, dead_input)
+        plan = g.compile()
+        plan.init_gpu()
+        n_cmd, s_cmd = plan.cmds[-2], plan.cmds[-1]
+        fused = [a for a in plan.exec_report()["aux"] if a["fused"]]
+        overlap = int(s_cmd["y_off"]) == int(n_cmd["src_off"])
+        _log(f"[norm+shift rf={rf} dead_input={dead_input} {mode}] shift output reuses the "
+             f"norm input: {overlap}; fused: {[a['name'] for a in fused]}")
+        if dead_input:
+            assert overlap  # the allocator case the executor must not fuse
+        assert bool(fused) == (mode == "fused" and not overlap)
+        rng2 = np.random.default_rng(7)
+        state = np.zeros((D, max(rf - 1, 0), 64), np.float16)
+        if rf > 1:
+            state = rng2.standard_normal(state.shape).astype(np.float16)
+            plan.write_canvas(int(s_cmd["state_off"]), state.reshape(D * (rf - 1), 64))
+        res = []
+        for step in range(2):
+            if dead_input:
+                ids = rng2.integers(0, 50, req).astype(np.uint32)
+                plan.set_ids(ids)
+                x = lo.embed(table, ids, 64)
+            else:
+                x = np.zeros((D, 64), np.float16)
+                x[:, :req] = rng2.standard_normal((D, req)).astype(np.float16)
+                plan.write_canvas(int(n_cmd["src_off"]), x)
+            plan.execute(1)
+            u = _read(plan, n_cmd["y_off"], D, 64)
+            s = _read(plan, s_cmd["y_off"], D, 64)
+            st = (_read(plan, s_cmd["state_off"], D * (rf - 1), 64).reshape(D, rf - 1, 64)
+                  if rf > 1 else None)
+            u_ref = lo.rmsnorm_f64(x, gamma.astype(np.float16))
+            assert lo.orc.rel_err(u[:, :req].astype(np.float64), u_ref[:, :req]) <= TOL
+            s_ref, state = lo.token_shift_decode(u, mu, state, req, f64=True)
+            assert lo.orc.rel_err(s[:, :req].astype(np.float64), s_ref[:, :req]) <= TOL
+            if rf > 1:
+                assert np.array_equal(st[:, :, :req].view(np.uint16),
+                                      state[:, :, :req].view(np.uint16))
+            res.append((u[:, :req].copy(), s[:, :req].copy(), None if st is None else st.copy()))
+        outs[mode] = res
+    for (ua, sa, ta), (ub, sb, tb) in zip(outs["fused"], outs["unfused"]):
+        assert np.array_equal(ua.view(np.uint16), ub.view(np.uint16))
+        assert np.array_equal(sa.view(np.uint16), sb.view(np.uint16))
+        if ta is not None:
+            assert np.array_equal(ta.view(np.uint16), tb.view(np.uint16))
+
+
+@pytest.mark.parametrize("V,stride,tokens", [(32000, 64, 16), (1000, 128, 100), (300, 1024, 1000)])
+def test_standalone_argmax_on_device_buffers(wavec, V, stride, tokens):
+    """wavec_argmax_f16 (the decode argmax on caller-owned device memory, partials in a
+    stream-ordered workspace) against the lowest-index rule, with planted ties."""
+    rng = np.random.default_rng(V + tokens)
+    x = (rng.standard_normal((V, stride)) * 3).astype(np.float16)
+    for t in range(0, tokens, 5):
+        cs = np.sort(rng.choice(V, size=2, replace=False))
+        x[cs, t] = np.float16(30.0)
+    X = wavec.DeviceBuffer.from_array(x)
+    ids = wavec.DeviceBuffer(tokens * 4)
+    wavec.argmax_f16(ids, X, V, stride, tokens)
+    wavec.device_synchronize()
+    got = ids.download(np.uint32, tokens)
+    assert np.array_equal(got, lo.argmax(x, tokens))

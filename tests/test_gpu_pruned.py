@@ -6,7 +6,7 @@ import pytest
 
 from snntome_amd import synth
 
-from wave_cases import TOL, stride_of
+from wave_cases import PATH_IDS, TOL, stride_of
 
 pytestmark = pytest.mark.gpu
 
@@ -21,10 +21,10 @@ def _log(msg):
     (11, 6, 32, 16, 200, None, True),
     (6, 3, 32, 32, 97, "gelu", False),
 ])
-def test_pruned_wave_matches_per_neuron_oracle(wavec, orc, monkeypatch, path, n_cl, K, S, tile,
+def test_pruned_wave_matches_per_neuron_oracle(wavec, orc, tuning, path, n_cl, K, S, tile,
                                                cout, act, res):
     if path != "auto":
-        monkeypatch.setenv("K44WAVEC_PATH", path)
+        tuning("path", PATH_IDS[path])
     rng = np.random.default_rng(n_cl * 7 + K)
     C, tokens = n_cl * S, 100
     pick = np.argsort(rng.random((cout, n_cl)), axis=1)[:, :K]

@@ -192,3 +192,81 @@ def test_batched_frames_on_canvas(wavec):
     halo = np.ones(cout * lay.channel_stride, bool)
     halo[lay.offsets(cout).ravel()] = False
     assert not out[halo].any()
+
+
+def _t64_write(plan, off, lay, x):
+    """x [F][C][H][W] fp16 -> the tensor region at `off` (halo elements zero)."""
+    C = x.shape[1]
+    buf = np.zeros(C * lay.channel_stride, np.float16)
+    buf[lay.offsets(C).ravel()] = x.ravel()
+    plan.write_canvas(int(off), buf)
+
+
+def _t64_read(plan, off, lay, C):
+    buf = plan.read_canvas(int(off), C * lay.channel_stride).view(np.float16)
+    return buf[lay.offsets(C)]
+
+
+@pytest.mark.parametrize("frames,reuse", [(64, False), (128, True)])
+@pytest.mark.parametrize("H,W", [(6, 10), (8, 64), (5, 7)])
+def test_token64_interleaved_image_plan(wavec, frames, reuse, H, W):
+    """Plans of 64-frame interleaved images (batch 64, and batch 128 held as two 64-frame blocks
+    with reuse_canvas): 3x3 and 1x1 convolutions (residual), 2x2 and 5x5 max pools, nearest
+    upsampling, a stride-2 3x3 convolution gathering its input directly, and a 2x2 transposed
+    convolution — every command against cnn_oracle on the tensors the device read (all frames);
+    pools and copies bit for bit."""
+    rng = np.random.default_rng(frames + 100 * H + W)
+    cin, c1, c3, cu = 5, 16, 8, 16
+    w1, b1 = _conv_params(rng, cin, c1, 3)
+    w2, b2 = _conv_params(rng, c1, c1, 1)
+    w3, b3 = _conv_params(rng, c1, c3, 3)
+    wu, bu = _f16(rng, (cu, c3, 2, 2), 0.3), _f16(rng, (cu,), 0.05)
+    f32 = lambda a: a.astype(np.float32)
+    g = wavec.WaveGraph(kv_cache_max_seq=0, batch_size=frames, reuse_canvas=reuse)
+    g.add_input("img", cin, H, W)
+    g.add_conv2d("c1", "img", "a", cin, c1, 3, 3, f32(w1), f32(b1), stride=1, pad=1, act="relu")
+    g.add_conv2d("c2", "a", "b", c1, c1, 1, 1, f32(w2), f32(b2), stride=1, pad=0, act="silu",
+                 res_blob="a")
+    g.add_maxpool("p", "b", "pb", kernel_size=2, stride=2)
+    g.add_upsample2x("u", "pb", "ub")
+    g.add_conv2d("c3", "ub", "d", c1, c3, 3, 3, f32(w3), f32(b3), stride=2, pad=1, act="none")
+    g.add_maxpool("p5", "d", "e", kernel_size=5, stride=1, pad=2)
+    g.add_upconv2x2("up", "e", "y", c3, cu, f32(wu), f32(bu))
+    plan = g.compile()
+    types = [c["type"] for c in plan.cmds]
+    assert types == ["K44_WAVE", "K44_WAVE", "MAXPOOL_2X2", "UPSAMPLE_2X", "K44_WAVE",
+                     "MAXPOOL_5X5", "K44_WAVE", "SCATTER_UP2X2"], types
+    plan.init_gpu()
+    assert {w["path"] for w in plan.exec_report()["waves"]} == {"valu_gather_tile"}
+    F = frames
+    lay = lambda h, w: co.Layout2D(h, w, F, tok64=True)
+    x = _f16(rng, (F, cin, H, W))
+    _t64_write(plan, plan.cmds[0]["src_off"], lay(H, W), x)
+    Hp, Wp = H // 2, W // 2
+    H3, W3 = (2 * Hp + 1) // 2, (2 * Wp + 1) // 2
+    dev = {"img": x}
+    steps = [  # (command, input tensors, output name, channels, H, W, reference, exact)
+        ("img", "a", c1, H, W, lambda t: co.conv2d_f64(t["img"], w1, b1, 1, 1, "relu"), False),
+        ("a", "b", c1, H, W, lambda t: co.conv2d_f64(t["a"], w2, b2, 1, 0, "silu", t["a"]), False),
+        ("b", "pb", c1, Hp, Wp, lambda t: co.maxpool2(t["b"]), True),
+        ("pb", "ub", c1, 2 * Hp, 2 * Wp, lambda t: co.upsample2(t["pb"]), True),
+        ("ub", "d", c3, H3, W3, lambda t: co.conv2d_f64(t["ub"], w3, b3, 2, 1), False),
+        ("d", "e", c3, H3, W3, lambda t: co.maxpool5(t["d"]), True),
+        (None, None, 0, 0, 0, None, False),  # quadrant wave of the transposed convolution
+        ("e", "y", cu, 2 * H3, 2 * W3, lambda t: co.upconv2x2_f64(t["e"], wu, bu), False),
+    ]
+    for i, (src, out, C, h, w, ref_fn, exact) in enumerate(steps):
+        plan.execute_range(i, 1)
+        if out is None:
+            continue
+        c = plan.cmds[i]
+        assert (c["h_out"], c["w_out"]) == (h, w), (i, c["h_out"], c["w_out"])
+        got = _t64_read(plan, c["y_off"], lay(h, w), C)
+        dev[out] = got
+        ref = ref_fn(dev)
+        if exact:
+            assert np.array_equal(got.view(np.uint16), ref.astype(np.float16).view(np.uint16)), out
+        else:
+            err = orc.rel_err(got.astype(np.float64), ref)
+            _log(f"[token64 F={F} {H}x{W}] {out}: rel err {err:.3e}")
+            assert err <= TOL, out

@@ -87,24 +87,24 @@ def test_token64_out_of_range_index_reads_zero(wavec, orc, batch):
 
 @pytest.mark.parametrize("cluster,B_vec16,batch", [(64, 2, 256), (128, 8, 512), (192, 6, 256),
                                                    (64, 64, 256), (256, 4, 256), (512, 256, 256)])
-def test_token64_ring_matches_oracle_and_fallback(wavec, orc, monkeypatch, cluster, B_vec16,
+def test_token64_ring_matches_oracle_and_fallback(wavec, orc, tuning, cluster, B_vec16,
                                                   batch):
     """Shapes the LDS-ring kernels take (clusters of whole 64-neuron blocks, whole 4-tile
     groups, even B_vec16; 128-neuron workgroups sharing the rows when the cluster allows it):
     within tolerance of the oracle, and bit-identical to the per-wave kernel (same k-step
-    accumulation order from the bias).  K44WAVEC_T64_RING: unset = automatic, 1 = 64-neuron
-    ring only, 0 = per-wave kernel."""
+    accumulation order from the bias).  Tuning switch t64_ring: -1 automatic, 1 64-neuron
+    ring only, 0 per-wave kernel."""
     Cout = cluster * 2
     ys = {}
     for ring in ("auto", "1", "0"):
         if ring == "auto":
-            monkeypatch.delenv("K44WAVEC_T64_RING", raising=False)
+            tuning("t64_ring", -1)
             err = _token64_case(wavec, orc, Cin=5000, Cout=Cout, cluster=cluster,
                                 B_vec16=B_vec16, batch=batch, seed=cluster + B_vec16)
             assert err <= TOL
             ys[ring] = _LAST_Y[0]
             continue
-        monkeypatch.setenv("K44WAVEC_T64_RING", ring)
+        tuning("t64_ring", int(ring))
         err = _token64_case(wavec, orc, Cin=5000, Cout=Cout, cluster=cluster, B_vec16=B_vec16,
                             batch=batch, seed=cluster + B_vec16)
         _log(f"[token64 ring={ring} cluster={cluster} B_vec16={B_vec16} batch={batch}] "

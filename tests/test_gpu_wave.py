@@ -8,7 +8,7 @@ import pytest
 
 from snntome_amd import synth
 
-from wave_cases import TOL, cluster_rows, random_rows, run_sparse_case, sampled_parity, stride_of
+from wave_cases import PATH_IDS, TOL, cluster_rows, random_rows, run_sparse_case, sampled_parity, stride_of
 
 pytestmark = pytest.mark.gpu
 
@@ -62,10 +62,10 @@ def test_config2_full_wave_sampled(wavec, orc):
 @pytest.mark.parametrize("lanes", [4, 8])
 @pytest.mark.parametrize("tokens", [64, 128, 256, 320, 512, 100])
 @pytest.mark.parametrize("act", ["none", "relu", "sigmoid", "silu", "leaky_relu", "gelu"])
-def test_activation_and_slab_shapes(wavec, orc, monkeypatch, tokens, act, lanes):
+def test_activation_and_slab_shapes(wavec, orc, tuning, tokens, act, lanes):
     """Every activation x every slab width (64/128/256 and ragged token counts) x both lane
     widths of the gather kernel (4 tokens / 8-byte loads, 8 tokens / 16-byte loads)."""
-    monkeypatch.setenv("K44WAVEC_LANE8", "1" if lanes == 8 else "0")
+    tuning("lane8", 1 if lanes == 8 else 0)
     acts = ["none", "relu", "sigmoid", "silu", "leaky_relu", "gelu"]
     rng = np.random.default_rng(tokens * 16 + acts.index(act))
     C, cout, K, S = 3000, 48, 3, 24
@@ -159,11 +159,11 @@ def test_tcff_roundtrip_on_gpu(wavec, orc, tmp_path):
 
 @pytest.mark.parametrize("lanes", [4, 8])
 @pytest.mark.parametrize("tokens,S", [(256, 32), (256, 24), (100, 16), (512, 40)])
-def test_streaming_loads_bit_identical(wavec, orc, monkeypatch, lanes, tokens, S):
+def test_streaming_loads_bit_identical(wavec, orc, tuning, lanes, tokens, S):
     """The non-temporal load policy (chosen for substrates far beyond the caches, forced here
-    with K44WAVEC_NT=1) changes the cache policy only: outputs equal the default policy's bit
+    with tuning switch nt=1) changes the cache policy only: outputs equal the default policy's bit
     for bit, over whole and partial 16-row batches, both lane widths, residual and bias."""
-    monkeypatch.setenv("K44WAVEC_LANE8", "1" if lanes == 8 else "0")
+    tuning("lane8", 1 if lanes == 8 else 0)
     rng = np.random.default_rng(tokens + S)
     C, cout, K = 4000, 64, 3
     starts = (rng.integers(0, (C - S) // 8, size=(cout, K)) * 8).astype(np.uint32)
@@ -171,7 +171,7 @@ def test_streaming_loads_bit_identical(wavec, orc, monkeypatch, lanes, tokens, S
     b = synth.normal_f16(rng, (cout,), 0.1)
     ys = {}
     for nt in ("0", "1"):
-        monkeypatch.setenv("K44WAVEC_NT", nt)
+        tuning("nt", int(nt))
         y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
                                        rows=cluster_rows(starts, S), weights=w, bias=b,
                                        act="relu", residual=True, seed=11)
@@ -189,12 +189,12 @@ def test_streaming_loads_bit_identical(wavec, orc, monkeypatch, lanes, tokens, S
     (256, 1, 40, 256, "silu", 2),    # one segment per neuron, shared index rows
     (40, 2, 16, 256, "none", 1),     # fewer neurons than waves in the workgroup
 ])
-def test_stream_kernel_bit_identical(wavec, orc, monkeypatch, cout, K, S, tokens, act, cluster):
+def test_stream_kernel_bit_identical(wavec, orc, tuning, cout, K, S, tokens, act, cluster):
     """The streaming gather kernel (output rows staged in LDS, written after the last gather;
-    forced with K44WAVEC_STREAMK=1) accumulates each neuron in the order of the one-neuron-per-
-    wave kernel (K44WAVEC_KSPLIT=1): bit-identical outputs, both within tolerance of the oracle."""
-    monkeypatch.setenv("K44WAVEC_NT", "1")
-    monkeypatch.setenv("K44WAVEC_LANE8", "0")
+    forced with tuning switch stream_kernel=1) accumulates each neuron in the order of the one-neuron-per-
+    wave kernel (ksplit=1): bit-identical outputs, both within tolerance of the oracle."""
+    tuning("nt", 1)
+    tuning("lane8", 0)
     rng = np.random.default_rng(cout + K * 10 + S)
     C = 5000
     starts = (rng.integers(0, (C - S) // 8, size=(cout // cluster, K)) * 8).astype(np.uint32)
@@ -202,8 +202,8 @@ def test_stream_kernel_bit_identical(wavec, orc, monkeypatch, cout, K, S, tokens
     b = synth.normal_f16(rng, (cout,), 0.1)
     ys = {}
     for mode in ("stream", "plain"):
-        monkeypatch.setenv("K44WAVEC_STREAMK", "1" if mode == "stream" else "0")
-        monkeypatch.setenv("K44WAVEC_KSPLIT", "1")
+        tuning("stream_kernel", 1 if mode == "stream" else 0)
+        tuning("ksplit", 1)
         y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
                                        rows=cluster_rows(starts, S), weights=w, bias=b,
                                        cluster=cluster, act=act, seed=13)
@@ -216,13 +216,13 @@ def test_stream_kernel_bit_identical(wavec, orc, monkeypatch, cout, K, S, tokens
     assert np.array_equal(ys["stream"], ys["plain"])
 
 
-def test_stream_kernel_cout_map(wavec, orc, monkeypatch):
+def test_stream_kernel_cout_map(wavec, orc, tuning):
     """Streaming kernel on a pruned projection (VALU path): cout_map stores and empty slots of
     the pattern-sorted tiles, against the per-neuron fp64 oracle."""
-    monkeypatch.setenv("K44WAVEC_PATH", "valu")
-    monkeypatch.setenv("K44WAVEC_NT", "1")
-    monkeypatch.setenv("K44WAVEC_LANE8", "0")
-    monkeypatch.setenv("K44WAVEC_STREAMK", "1")
+    tuning("path", 0)
+    tuning("nt", 1)
+    tuning("lane8", 0)
+    tuning("stream_kernel", 1)
     rng = np.random.default_rng(77)
     n_cl, K, S, cout, tokens = 6, 3, 32, 333, 256
     C = n_cl * S
@@ -252,11 +252,11 @@ def test_stream_kernel_cout_map(wavec, orc, monkeypatch):
 
 
 @pytest.mark.parametrize("path,cluster", [("valu", 1), ("mfma", 16)])
-def test_neuron_65535_without_cout_map(wavec, orc, monkeypatch, path, cluster):
+def test_neuron_65535_without_cout_map(wavec, orc, tuning, path, cluster):
     """Waves of more than 65,536 neurons: channel 65535 equals the 16-bit empty-slot marker of
     cout_map, which must only mean "no output" when the wave has a cout_map (regression: the
     last neuron of config 2 was dropped)."""
-    monkeypatch.setenv("K44WAVEC_PATH", path)
+    tuning("path", PATH_IDS[path])
     rng = np.random.default_rng(65535)
     C, cout, K, S, tokens = 4096, 65536 + 32, 1, 32, 64
     starts = (rng.integers(0, (C - S) // 16, size=(cout // cluster, K)) * 16).astype(np.uint32)
@@ -274,11 +274,11 @@ def test_neuron_65535_without_cout_map(wavec, orc, monkeypatch, path, cluster):
 
 
 @pytest.mark.parametrize("tokens,K,S", [(128, 16, 128), (64, 8, 64), (256, 3, 40), (100, 12, 24)])
-def test_weights_staged_in_lds_bit_identical(wavec, orc, monkeypatch, tokens, K, S):
+def test_weights_staged_in_lds_bit_identical(wavec, orc, tuning, tokens, K, S):
     """The 8-token-per-lane gather kernel stages each neuron's weights in LDS before its gathers
-    (K44WAVEC_WLDS=0 reads them from memory per batch): same values, same FMA order, so the
+    (tuning switch wlds=0 reads them from memory per batch): same values, same FMA order, so the
     outputs are bit-identical; one neuron per wave (K > 8) and four waves per neuron (K <= 8)."""
-    monkeypatch.setenv("K44WAVEC_LANE8", "1")
+    tuning("lane8", 1)
     rng = np.random.default_rng(tokens + K * 3 + S)
     C, cout = 5000, 96
     starts = (rng.integers(0, (C - S) // 8, size=(cout, K)) * 8).astype(np.uint32)
@@ -286,7 +286,7 @@ def test_weights_staged_in_lds_bit_identical(wavec, orc, monkeypatch, tokens, K,
     b = synth.normal_f16(rng, (cout,), 0.1)
     ys = {}
     for mode in ("lds", "memory"):
-        monkeypatch.setenv("K44WAVEC_WLDS", "1" if mode == "lds" else "0")
+        tuning("wlds", 1 if mode == "lds" else 0)
         y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
                                        rows=cluster_rows(starts, S), weights=w, bias=b,
                                        act="silu", residual=True, seed=23)

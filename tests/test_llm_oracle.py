@@ -164,3 +164,38 @@ def test_llm_spec_accounting():
         assert np.all(p.starts % TINY.S == 0)
         assert p.starts.shape[0] == p.weights.shape[0]  # per-neuron patterns
         assert len({tuple(r) for r in st.tolist()}) > 1
+
+
+@pytest.mark.parametrize("act", [None, "relu", "sigmoid", "silu", "leaky_relu", "gelu"])
+@pytest.mark.parametrize("res", [False, True])
+def test_project_dense_equals_scalar_oracle(orc, act, res):
+    """The dense float64 restatement used by the full-size checks equals the scalar fp64 oracle
+    (orc_wave_f64) to float64 rounding, for every activation, with and without residual; a
+    shifted cluster start or a dropped bias in the dense form is caught."""
+    rng = np.random.default_rng(17 + (act is None) + 2 * res)
+    n_cl, S, K, cout, T = 7, 16, 3, 50, 40
+    D = n_cl * S
+    pick = np.argsort(rng.random((cout, n_cl)), axis=1)[:, :K]
+    starts = (pick * S).astype(np.uint32)
+    w = _f16(rng, (cout, K * S), 0.2)
+    b = _f16(rng, (cout,), 0.3)
+    x = _f16(rng, (D, T))
+    r = _f16(rng, (cout, T)) if res else None
+    want = lo.project(x, starts, S, 1, w, b, act, r, f64=True)
+    got = lo.project_dense_f64(x, starts, S, w, b, act, r, block=16)
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1e-2)) < 1e-12
+    # planted mistakes in the dense form are visible at the tolerance of the device checks
+    bad = starts.copy()
+    bad[0, 0] = S * next(c for c in range(n_cl) if c not in pick[0])  # another cluster
+    moved = lo.project_dense_f64(x, bad, S, w, b, act, r)
+    assert orc.rel_err(moved, want) > 2e-3
+    no_bias = lo.project_dense_f64(x, starts, S, w, np.zeros_like(b), act, r)
+    assert orc.rel_err(no_bias, want) > 2e-3
+
+
+def test_project_dense_rejects_overlapping_clusters():
+    x = np.zeros((64, 8), np.float16)
+    starts = np.array([[0, 8]], np.uint32)  # clusters of 16 overlap on rows 8..15
+    with pytest.raises(ValueError):
+        lo.project_dense_f64(x, starts, 16, np.zeros((1, 32), np.float16), np.zeros(1, np.float16),
+                             None)

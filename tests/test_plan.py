@@ -558,3 +558,121 @@ def test_2d_planted_mistakes_are_caught(wavec, tmp_path, monkeypatch, mistake):
     path = tmp_path / "p.tcff"
     plan.save_tcff(path, "K44Model")
     assert path.read_bytes() != po.tcff_bytes(pplan, "K44Model")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_canvas_allocator_invariants_on_random_graphs(wavec, seed):
+    """The compiler's canvas allocator (reference wavec/k44_wave_compiler.hpp:388-593, restated in
+    pass4) checked by invariants that do not depend on its tie-breaks, on random 1-D graphs of
+    sparse waves, residual waves, RMSNorms and element-wise products reading random earlier
+    tensors.  Liveness is computed here from the graph as built (a tensor lives from the node
+    that writes it through its last reader; the plan input and output to the end):
+      * every tensor starts on a 64-element boundary;
+      * two tensors alive at the same node never share a canvas element (a node's output and
+        its own inputs are alive together);
+      * the canvas is exactly the highest reserved element, rounded up to 128."""
+    rng = np.random.default_rng(1000 + seed)
+    T = int(rng.choice([64, 100, 256]))
+    stride = (T + 63) // 64 * 64
+    g = wavec.WaveGraph(kv_cache_max_seq=0, fold_rmsnorm_gamma=False)
+    C0 = int(rng.integers(40, 200))
+    g.add_input("x", C0, 1, T, is_1d=True)
+    chans = {"x": C0}
+    order = ["x"]
+    reads = {"x": []}  # tensor -> node indices that read it
+    srcs = []  # first input of every node
+    for k in range(int(rng.integers(8, 20))):
+        name = f"t{k}"
+        kind = rng.choice(["wave", "wave", "res", "norm", "mul"])
+        src = order[int(rng.integers(max(0, len(order) - 4), len(order)))]
+        if kind == "norm":
+            g.add_rmsnorm(f"n{k}", src, name, chans[src], np.ones(chans[src], np.float32))
+            chans[name] = chans[src]
+            ins = [src]
+        elif kind == "mul":
+            same = [t for t in order if chans[t] == chans[src] and t != src]
+            if not same:
+                continue
+            other = same[int(rng.integers(0, len(same)))]
+            g.add_swiglu(f"m{k}", src, other, name)
+            chans[name] = chans[src]
+            ins = [src, other]
+        else:
+            cout = int(rng.integers(16, 160))
+            res = None
+            if kind == "res":
+                cands = [t for t in order if chans[t] == cout]
+                if not cands:
+                    cout = chans[src]
+                    cands = [src]
+                res = cands[int(rng.integers(0, len(cands)))]
+            fan = int(rng.integers(1, 5)) * 8
+            rows = rng.integers(0, chans[src], size=(cout, fan)).astype(np.uint32)
+            _w = synth.normal_f16(rng, (cout, fan), 0.05)
+            g.add_sparse_wave(f"w{k}", src, name, rows, _w, None, act="relu", res_blob=res)
+            chans[name] = cout
+            ins = [src] + ([res] if res else [])
+        node = len(order) - 1  # index of this node's command (the input has none)
+        srcs.append(ins[0])
+        for t in ins:
+            reads[t].append(node)
+        reads[name] = []
+        order.append(name)
+    g.set_output(order[-1])
+    plan = g.compile()
+    s = plan.summary
+    cmds = s["cmds"]
+    assert len(cmds) == len(order) - 1
+    end = len(cmds)
+    span = {}  # tensor -> (canvas lo, hi, def node, last node)
+    span["x"] = None
+    for i, (name, c) in enumerate(zip(order[1:], cmds)):
+        reserve = -(-int(c["Cout"]) * stride // 64) * 64
+        lo = int(c["y_off"])
+        last = end if name == order[-1] else max(reads[name], default=i)
+        span[name] = (lo, lo + reserve, i, last)
+    # the plan input is allocated first, at offset 0, and lives to the end
+    span["x"] = (0, -(-C0 * stride // 64) * 64, -1, end)
+    assert _alloc_violations(span, int(s["canvas_elems"])) == []
+    for i in reads["x"]:  # the plan input sits at offset 0
+        if srcs[i] == "x":
+            assert int(cmds[i]["src_off"]) == 0
+    # The check is not vacuous: moving one tensor onto another that is alive at the same time
+    # (what an allocator freeing a tensor too early would do) is reported.
+    pairs = [(a, b) for a in span for b in span if a != b and a != "x" and
+             not (span[a][3] < span[b][2] or span[b][3] < span[a][2])]
+    a, b = pairs[int(rng.integers(0, len(pairs)))]
+    bad = dict(span)
+    lo_a, hi_a, d_a, e_a = span[a]
+    bad[a] = (span[b][0], span[b][0] + hi_a - lo_a, d_a, e_a)
+    assert _alloc_violations(bad, int(s["canvas_elems"]))
+
+
+def _alloc_violations(span, canvas_elems):
+    """Violated allocator invariants of {tensor: (lo, hi, first node, last node)}."""
+    out = []
+    items = list(span.items())
+    for name, (lo, hi, d, l) in items:
+        if lo % 64:
+            out.append(f"{name} not 64-aligned")
+    for a in range(len(items)):
+        na, (la, ha, da, ea) = items[a]
+        for b in range(a + 1, len(items)):
+            nb, (lb, hb, db, eb) = items[b]
+            if not (ea < db or eb < da) and not (ha <= lb or hb <= la):
+                out.append(f"{na} and {nb} alive together share elements")
+    top = max(hi for _, (lo, hi, d, l) in items)
+    if canvas_elems != -(-top // 128) * 128:
+        out.append(f"canvas {canvas_elems} != highest element {top} rounded to 128")
+    return out
+
+
+def test_conv1d_tap_before_the_canvas_is_refused(wavec):
+    """A 1-D convolution applied directly to the plan input (canvas offset 0) would gather its
+    first channel's dx = -1 tap from offset -1; the reference wraps it to 0xFFFFFFFF
+    (k44_plan_types.hpp:593-595), this compiler refuses the plan."""
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", 32, 1, 64, is_1d=True)
+    g.add_conv2d("c", "x", "y", 32, 16, 1, 3, np.zeros((16, 32, 1, 3), np.float32), pad=1)
+    with pytest.raises(RuntimeError, match="32-bit index range"):
+        g.compile()

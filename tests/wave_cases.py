@@ -4,6 +4,8 @@ import numpy as np
 from snntome_amd import synth
 
 TOL = 2e-3  # north_star: max |d| / (|ref| + 1e-2) <= 2e-3 against the fp64 oracle
+# Values of the executor tuning switch "path" (wavec.set_tuning).
+PATH_IDS = {"auto": -1, "valu": 0, "mfma": 1}
 
 
 def stride_of(tokens: int) -> int:
@@ -69,6 +71,8 @@ def sampled_parity(orc, plan, wl, wave_idx, neurons, read_out=True):
     wl_idx = np.concatenate([np.arange(r * w.cluster, (r + 1) * w.cluster) for r in rows])
     ref = orc.wave_f64(compact.ravel(), seg, w.weights[wl_idx], w.bias[wl_idx], None, w.K, w.S,
                        w.cluster, st, st, st, w.act, sel=sel_local)
+    if not read_out:
+        return None, ref
     cmd = plan.cmds[wave_idx]
     y0 = int(cmd["y_off"])
     ys = np.stack([plan.read_canvas(y0 + int(j) * st, st) for j in neurons])
