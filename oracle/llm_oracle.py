@@ -57,11 +57,18 @@ def token_shift(x: np.ndarray, mu: np.ndarray, seq_len: int, valid: int, f64: bo
     xf = x.astype(np.float64)
     m = mu.astype(np.float64)
     y = np.zeros((D, T), dtype=np.float64)
-    t = np.arange(valid)
-    pos = t % seq_len
-    for i in range(rf):
-        ok = pos >= i
-        y[:, t[ok]] += m[:, i:i + 1] * xf[:, t[ok] - i]
+    if valid % seq_len == 0:  # whole requests: tap i shifts every request by i tokens
+        R = valid // seq_len
+        xr = xf[:, :valid].reshape(D, R, seq_len)
+        yr = y[:, :valid].reshape(D, R, seq_len)
+        for i in range(min(rf, seq_len)):
+            yr[:, :, i:] += m[:, i, None, None] * xr[:, :, :seq_len - i]
+    else:
+        t = np.arange(valid)
+        pos = t % seq_len
+        for i in range(rf):
+            ok = pos >= i
+            y[:, t[ok]] += m[:, i:i + 1] * xf[:, t[ok] - i]
     state = np.zeros((D, max(rf - 1, 0), 64), dtype=F16)
     for r in range(valid // seq_len):
         for i in range(min(rf - 1, seq_len)):  # slots before the request start stay 0

@@ -372,6 +372,111 @@ struct K44GpuExecutorState {
         return wx.unique_rows * (uint64_t)wx.tokens * 2u >= (512ull << 20);
     }
 
+    // MFMA configuration of a wave with a dense tiling (tiles of cl = cluster_size neurons
+    // sharing every index row): kernel (narrow <= 16 tokens, LDS ring for 512-token
+    // workgroups, register-staged tile otherwise), ring depth, split-K, and the weights in
+    // A-fragment order.  width: the output's token count per row (1-D waves; 2-D waves pass
+    // UINT32_MAX: they never take the narrow kernel).
+    void configure_mfma(const K44ExecCmd &c, WaveExec &wx, const std::vector<uint16_t> &wraw,
+                        size_t rows, uint32_t width) {
+        const uint32_t cl = c.cluster_size;
+        wx.path = "mfma_tile";
+        wx.why = "neurons share index rows in tiles of " + std::to_string(cl) +
+                 " and segments are whole 32-position K-steps: dense " + std::to_string(cl) +
+                 " x " + std::to_string(c.B_raw) + " x " + std::to_string(wx.tokens) +
+                 " contraction per tile on v_mfma_f32_16x16x32_f16";
+        wx.mt = pick_mt(wx.tokens);
+        wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
+        wx.narrow = width <= 16u && tune(Tune::Narrow) != 0;
+        wx.part_tokens = wx.narrow ? 16u : wx.tokens;
+        // 512-token workgroups of 32/64-neuron tiles stream through an LDS ring filled by
+        // direct loads (3 stages in flight per workgroup instead of 1).
+        wx.dma = !wx.narrow && wx.mt == 512u && (cl == 32u || cl == 64u || cl == 128u) &&
+                 tune(Tune::Dma) != 0;
+        if (wx.dma) {
+            wx.path = "mfma_dma";
+            wx.why += " (512-token workgroups: 4-stage LDS ring filled by global_load_lds)";
+            wx.rows_per_stage = 32u;
+            // Config 3 measured the same with either load policy (363 TFLOP/s): default
+            // policy unless tuning switch "nt" is 1.
+            wx.stream_loads = tune(Tune::NonTemporal) == 1;
+            // Ring depth: gathers from inputs that stay in the caches (distinct gathered
+            // bytes <= 256 MB, the last-level cache) take 2-stage rings, two workgroups per
+            // CU — config-5 prefill 26.9 -> 20.9 ms; gathers from HBM keep 4 stages and one
+            // workgroup per CU — config 3: 364 us, against 379 us with 2 stages.
+            const double gathered = (double)wx.unique_rows * wx.tokens * 2.0;
+            wx.dshape.nbuf = gathered <= 256.0 * 1048576.0 ? 2u : 4u;
+            if (tune(Tune::DmaStages) == 2 || tune(Tune::DmaStages) == 4)
+                wx.dshape.nbuf = (uint32_t)tune(Tune::DmaStages);
+            // 128-neuron tiles: 128 accumulator registers per lane leave one workgroup per
+            // CU, whose LDS holds a 3-stage ring (2 stages in flight).
+            if (cl == 128u) wx.dshape.nbuf = 3u;
+            wx.dshape.stream_loads = wx.stream_loads;
+            wx.why += "; " + std::to_string(wx.dshape.nbuf) + "-stage ring";
+        }
+        if (wx.narrow) {
+            wx.path = "mfma_narrow";
+            wx.why += " (at most 16 tokens: weight-streaming narrow tile)";
+            wx.mt = 16u;
+            const uint32_t ksteps = c.B_raw / 32u;
+            uint32_t want;
+            if (cl >= 64u) {
+                // Tiles of whole 16-neuron blocks per wave: chunks of any length, streamed
+                // in 16-k-step sub-chunks.  Chunks of at most 48 k-steps; split further, down
+                // to 16 k-steps, until the wave has ~128 workgroups.  Measured on config-5
+                // decode (per step): 1.196 ms, against 1.219 ms when waves of >= 32 tiles
+                // stay unsplit (fused epilogue), 1.28 ms with 8-k-step chunks, 1.46 ms
+                // without split.
+                const int ce = tune(Tune::NarrowChunk);
+                const uint32_t cmax = ce > 0 ? (uint32_t)std::max(16, ce) : 48u;
+                want = (ksteps + cmax - 1u) / cmax;
+                want = std::max(want, std::min((128u + (uint32_t)rows - 1u) / (uint32_t)rows,
+                                               (ksteps + 15u) / 16u));
+            } else {
+                // Chunks of 8..16 k-steps (<= 512 rows in LDS), ~256 workgroups per wave.
+                want = (256u + (uint32_t)rows - 1u) / (uint32_t)rows;
+                want = std::min(want, (ksteps + 7u) / 8u);
+                want = std::max(want, (ksteps + 15u) / 16u);
+            }
+            want = std::max(1u, std::min(want, ksteps));
+            wx.stage_chunk = (ksteps + want - 1u) / want;
+            wx.kgroups = (ksteps + wx.stage_chunk - 1u) / wx.stage_chunk;
+            if (wx.kgroups > 1u) wx.part_floats = (size_t)wx.kgroups * c.Cout * 16u;
+        } else {
+            const uint32_t stages = c.B_raw / wx.rows_per_stage;
+            const uint64_t wgs = (uint64_t)rows * (wx.tokens / wx.mt);
+            // Few workgroups: split the contraction.  Each split adds a partial plane of
+            // 4 * cout * tokens bytes, so prefill-sized token counts split at most 8 ways
+            // with >= 4 stages per workgroup; small token counts up to 32 ways.
+            const bool wide_tokens = wx.tokens >= 1024u;
+            uint32_t want = wgs >= 256u ? 1u : (uint32_t)((512u + wgs - 1u) / wgs);
+            if (tune(Tune::SplitK) == 0) want = 1u;
+            want = std::min(want, wide_tokens ? 8u : 32u);
+            const uint32_t min_stages = wide_tokens ? 4u : 1u;
+            want = std::max(1u, std::min(want, std::max(1u, stages / min_stages)));
+            wx.stage_chunk = (stages + want - 1u) / want;
+            wx.kgroups = (stages + wx.stage_chunk - 1u) / wx.stage_chunk;
+            if (wx.kgroups > 1u) wx.part_floats = (size_t)wx.kgroups * c.Cout * wx.tokens;
+        }
+        wx.ksteps = c.B_raw / 32u;
+        const uint32_t nb = cl / 16u;
+        // A fragments: [tile][k-step][16-neuron block][lane][8]; lane l holds neuron
+        // 16*blk + (l & 15), positions 32*ks + 8*(l >> 4) .. +8 of the tile's index row.
+        std::vector<uint16_t> wf((size_t)c.Cout * c.B_raw);
+        for (size_t t = 0; t < rows; ++t)
+            for (uint32_t ks = 0; ks < wx.ksteps; ++ks)
+                for (uint32_t b = 0; b < nb; ++b)
+                    for (uint32_t l = 0; l < 64u; ++l) {
+                        const size_t dst = (((t * wx.ksteps + ks) * nb + b) * 64u + l) * 8u;
+                        const size_t j = t * cl + 16u * b + (l & 15u);
+                        const size_t src = j * c.B + 32u * ks + 8u * (l >> 4);
+                        std::memcpy(&wf[dst], &wraw[src], 16);
+                    }
+        std::vector<__half> wh(wf.size());
+        std::memcpy(wh.data(), wf.data(), wf.size() * 2u);
+        wx.w.upload(wh);
+    }
+
     void build_wave(const K44ExecCmd &c, WaveExec &wx) {
         const auto &Lo = plan_meta.res_map.at(c.res_key_out);
         auto itin = plan_meta.res_map.find(c.res_key_in);
@@ -554,98 +659,7 @@ struct K44GpuExecutorState {
             throw std::runtime_error("wave '" + c.name + "': tuning path=mfma but the wave has "
                                      "no dense MFMA tiling (cluster/segment/alignment)");
         if (wx.mfma) {
-            wx.path = "mfma_tile";
-            wx.why = "neurons share index rows in tiles of " + std::to_string(cl) +
-                     " and segments are whole 32-position K-steps: dense " + std::to_string(cl) +
-                     " x " + std::to_string(c.B_raw) + " x " + std::to_string(wx.tokens) +
-                     " contraction per tile on v_mfma_f32_16x16x32_f16";
-            wx.mt = pick_mt(wx.tokens);
-            wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
-            wx.narrow = Lo.W <= 16u && tune(Tune::Narrow) != 0;
-            wx.part_tokens = wx.narrow ? 16u : wx.tokens;
-            // 512-token workgroups of 32/64-neuron tiles stream through an LDS ring filled by
-            // direct loads (3 stages in flight per workgroup instead of 1).
-            wx.dma = !wx.narrow && wx.mt == 512u && (cl == 32u || cl == 64u) &&
-                     tune(Tune::Dma) != 0;
-            if (wx.dma) {
-                wx.path = "mfma_dma";
-                wx.why += " (512-token workgroups: 4-stage LDS ring filled by global_load_lds)";
-                wx.rows_per_stage = 32u;
-                // Config 3 measured the same with either load policy (363 TFLOP/s): default
-                // policy unless tuning switch "nt" is 1.
-                wx.stream_loads = tune(Tune::NonTemporal) == 1;
-                // Ring depth: gathers from inputs that stay in the caches (distinct gathered
-                // bytes <= 256 MB, the last-level cache) take 2-stage rings, two workgroups per
-                // CU — config-5 prefill 26.9 -> 20.9 ms; gathers from HBM keep 4 stages and one
-                // workgroup per CU — config 3: 364 us, against 379 us with 2 stages.
-                const double gathered = (double)wx.unique_rows * wx.tokens * 2.0;
-                wx.dshape.nbuf = gathered <= 256.0 * 1048576.0 ? 2u : 4u;
-                if (tune(Tune::DmaStages) == 2 || tune(Tune::DmaStages) == 4)
-                    wx.dshape.nbuf = (uint32_t)tune(Tune::DmaStages);
-                wx.dshape.stream_loads = wx.stream_loads;
-                wx.why += "; " + std::to_string(wx.dshape.nbuf) + "-stage ring";
-            }
-            if (wx.narrow) {
-                wx.path = "mfma_narrow";
-                wx.why += " (at most 16 tokens: weight-streaming narrow tile)";
-                wx.mt = 16u;
-                const uint32_t ksteps = c.B_raw / 32u;
-                uint32_t want;
-                if (cl >= 64u) {
-                    // Tiles of whole 16-neuron blocks per wave: chunks of any length, streamed
-                    // in 16-k-step sub-chunks.  Chunks of at most 48 k-steps; split further, down
-                    // to 16 k-steps, until the wave has ~128 workgroups.  Measured on config-5
-                    // decode (per step): 1.196 ms, against 1.219 ms when waves of >= 32 tiles
-                    // stay unsplit (fused epilogue), 1.28 ms with 8-k-step chunks, 1.46 ms
-                    // without split.
-                    const int ce = tune(Tune::NarrowChunk);
-                    const uint32_t cmax = ce > 0 ? (uint32_t)std::max(16, ce) : 48u;
-                    want = (ksteps + cmax - 1u) / cmax;
-                    want = std::max(want, std::min((128u + (uint32_t)rows - 1u) / (uint32_t)rows,
-                                                   (ksteps + 15u) / 16u));
-                } else {
-                    // Chunks of 8..16 k-steps (<= 512 rows in LDS), ~256 workgroups per wave.
-                    want = (256u + (uint32_t)rows - 1u) / (uint32_t)rows;
-                    want = std::min(want, (ksteps + 7u) / 8u);
-                    want = std::max(want, (ksteps + 15u) / 16u);
-                }
-                want = std::max(1u, std::min(want, ksteps));
-                wx.stage_chunk = (ksteps + want - 1u) / want;
-                wx.kgroups = (ksteps + wx.stage_chunk - 1u) / wx.stage_chunk;
-                if (wx.kgroups > 1u) wx.part_floats = (size_t)wx.kgroups * c.Cout * 16u;
-            } else {
-                const uint32_t stages = c.B_raw / wx.rows_per_stage;
-                const uint64_t wgs = (uint64_t)rows * (wx.tokens / wx.mt);
-                // Few workgroups: split the contraction.  Each split adds a partial plane of
-                // 4 * cout * tokens bytes, so prefill-sized token counts split at most 8 ways
-                // with >= 4 stages per workgroup; small token counts up to 32 ways.
-                const bool wide_tokens = wx.tokens >= 1024u;
-                uint32_t want = wgs >= 256u ? 1u : (uint32_t)((512u + wgs - 1u) / wgs);
-                if (tune(Tune::SplitK) == 0) want = 1u;
-                want = std::min(want, wide_tokens ? 8u : 32u);
-                const uint32_t min_stages = wide_tokens ? 4u : 1u;
-                want = std::max(1u, std::min(want, std::max(1u, stages / min_stages)));
-                wx.stage_chunk = (stages + want - 1u) / want;
-                wx.kgroups = (stages + wx.stage_chunk - 1u) / wx.stage_chunk;
-                if (wx.kgroups > 1u) wx.part_floats = (size_t)wx.kgroups * c.Cout * wx.tokens;
-            }
-            wx.ksteps = c.B_raw / 32u;
-            const uint32_t nb = cl / 16u;
-            // A fragments: [tile][k-step][16-neuron block][lane][8]; lane l holds neuron
-            // 16*blk + (l & 15), positions 32*ks + 8*(l >> 4) .. +8 of the tile's index row.
-            std::vector<uint16_t> wf((size_t)c.Cout * c.B_raw);
-            for (size_t t = 0; t < rows; ++t)
-                for (uint32_t ks = 0; ks < wx.ksteps; ++ks)
-                    for (uint32_t b = 0; b < nb; ++b)
-                        for (uint32_t l = 0; l < 64u; ++l) {
-                            const size_t dst = (((t * wx.ksteps + ks) * nb + b) * 64u + l) * 8u;
-                            const size_t j = t * cl + 16u * b + (l & 15u);
-                            const size_t src = j * c.B + 32u * ks + 8u * (l >> 4);
-                            std::memcpy(&wf[dst], &wraw[src], 16);
-                        }
-            std::vector<__half> wh(wf.size());
-            std::memcpy(wh.data(), wf.data(), wf.size() * 2u);
-            wx.w.upload(wh);
+            configure_mfma(c, wx, wraw, rows, Lo.W);
         } else {
             wx.path = "valu_gather_dot";
             wx.why = !nt_ok ? "neurons do not share index rows in tiles of 16..128 (cluster " +
@@ -769,9 +783,10 @@ struct K44GpuExecutorState {
         if (wx.act < 0 || wx.act > 5)
             throw std::runtime_error("wave '" + c.name + "': unknown activation id");
         std::vector<uint64_t> starts;
-        std::vector<uint32_t> perm;  // 2-D: index order (the tile kernel handles any alignment)
-        segment_rows(c, wx.step, wx.S, starts, perm, false);
+        std::vector<uint32_t> perm;  // phase order: a kh x kw conv is kh*kw segments of cin rows
+        segment_rows(c, wx.step, wx.S, starts, perm, true);
         wx.K = c.B_raw / wx.S;
+        wx.phase_order = !perm.empty();
         wx.plane = plane_of(Lo);
         std::vector<uint32_t> tx, ty;
         if (tok64) {
@@ -836,14 +851,38 @@ struct K44GpuExecutorState {
         convert_wmma_to_raw(reinterpret_cast<uint4_host *>(wraw.data()), c.h_w_wmma.data(),
                             c.Cout, c.B / 8u);
         std::vector<__half> wh((size_t)c.Cout * c.B_raw);
+        std::vector<uint16_t> tmp(c.B_raw);
         for (size_t j = 0; j < c.Cout; ++j) {
             for (uint32_t q = c.B_raw; q < c.B; ++q)
                 if (wraw[j * c.B + q] != 0u)
                     throw std::runtime_error("wave '" + c.name +
                                              "': non-zero weight on a padded synapse");
-            std::memcpy(&wh[j * c.B_raw], &wraw[j * c.B], (size_t)c.B_raw * 2u);
+            uint16_t *wj = wraw.data() + j * c.B;
+            if (!perm.empty()) {  // synapses in the segment order chosen above
+                const uint32_t *q = perm.data() + (j / c.cluster_size) * c.B_raw;
+                for (uint32_t s = 0; s < c.B_raw; ++s) tmp[s] = wj[q[s]];
+                std::memcpy(wj, tmp.data(), (size_t)c.B_raw * 2u);
+            }
+            std::memcpy(&wh[j * c.B_raw], wj, (size_t)c.B_raw * 2u);
         }
-        wx.w.upload(wh);
+        // Dense convolutions of 64-frame interleaved images (tiles of >= 16 output channels
+        // sharing every index row, whole 32-channel k-steps): every tile is a pixel's 64
+        // frames, 64-element aligned, so the MFMA kernels gather it through the tile tables.
+        // The single-frame layouts keep the VALU tile kernel (rows off the 16-byte grid).
+        {
+            const uint32_t cl = c.cluster_size;
+            bool ok = tok64 && (cl == 16u || cl == 32u || cl == 64u || cl == 128u) &&
+                      wx.S % 32u == 0u && wx.step % 8u == 0u && tune(Tune::Path) != 0;
+            for (uint64_t s0 : starts) ok = ok && s0 % 8u == 0u;
+            for (uint32_t v : tx) ok = ok && v % 64u == 0u;
+            for (uint32_t v : ty) ok = ok && v % 64u == 0u;
+            if (ok) {
+                wx.mfma = true;
+                configure_mfma(c, wx, wraw, rows, UINT32_MAX);
+                wx.why += "; 64-frame interleaved image: tile tables";
+            }
+        }
+        if (!wx.mfma) wx.w.upload(wh);
         wx.seg.upload(starts);
         std::vector<__half> bh(c.Cout);
         for (size_t j = 0; j < c.Cout; ++j) {
@@ -1411,7 +1450,7 @@ struct K44GpuExecutorState {
             }
             const WaveExec &w = *waves[op.second];
             scratch_need = std::max(scratch_need, w.part_floats);
-            if (!w.mfma) {
+            if (!w.mfma || w.tile2d) {  // 2-D waves: launched alone, halo clear after each
                 runs.push_back({1, op.second});
                 continue;
             }
@@ -1524,6 +1563,10 @@ struct K44GpuExecutorState {
         a.tiles = w.rows;
         a.ttiles = w.narrow ? 1u : w.tokens / w.mt;
         a.kgroups = w.kgroups;
+        if (w.tile2d) {
+            a.tile_x = w.tile_x.p;
+            a.tile_y = w.tile_y.p;
+        }
         return a;
     }
 
@@ -1667,6 +1710,8 @@ struct K44GpuExecutorState {
     void launch_wave(const WaveExec &w) {
         if (w.mfma) {
             launch_mfma(w);
+            if (w.tile2d)
+                K44_HIP(k44dev::launch_halo_clear(canvas.p + w.y_off, w.cout, w.plane, stream));
             return;
         }
         if (w.tile2d) {

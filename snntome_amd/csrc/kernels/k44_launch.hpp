@@ -33,7 +33,8 @@ hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32
                             uint32_t items, hipStream_t stream);
 
 // Shape of an LDS-DMA MFMA launch: ring stages (4: one workgroup per CU, 3 stages in flight;
-// 2: two workgroups per CU, 1 stage in flight each) and the loads' cache policy.
+// 2: two workgroups per CU, 1 stage in flight each; 3: 128-neuron tiles, one workgroup per CU,
+// 2 stages in flight) and the loads' cache policy.
 struct DmaShape {
     uint32_t nbuf = 4;
     bool stream_loads = false;
@@ -43,7 +44,8 @@ struct DmaShape {
 };
 
 // LDS-DMA MFMA tile kernel (512 tokens per workgroup, 32-position stages through an LDS ring
-// filled by direct loads) over a group: `items` workgroups; nt in {32, 64}.
+// filled by direct loads) over a group: `items` workgroups; nt in {32, 64} (2 or 4 stages) or
+// 128 (3 stages).
 hipError_t launch_mfma_dma(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream,
                            const DmaShape &shape);
 

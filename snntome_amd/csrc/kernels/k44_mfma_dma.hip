@@ -1,5 +1,5 @@
-// Translation unit of the LDS-DMA MFMA tile kernel (512 tokens per workgroup, NT 32 / 64,
-// 2- or 4-stage rings).
+// Translation unit of the LDS-DMA MFMA tile kernel (512 tokens per workgroup, NT 32 / 64 with
+// 2- or 4-stage rings, NT 128 with a 3-stage ring).
 #include "k44_launch.hpp"
 #include "k44_mfma_dma.hpp"
 
@@ -21,6 +21,8 @@ hipError_t launch_mfma_dma(const MfmaGroup &a, uint32_t nt, uint32_t items, hipS
         K44_DMA(64, 4)
     } else if (nt == 64u && shape.nbuf == 2u) {
         K44_DMA(64, 2)
+    } else if (nt == 128u && shape.nbuf == 3u) {
+        K44_DMA(128, 3)
     } else {
         return hipErrorInvalidValue;
     }

@@ -2,7 +2,7 @@
 //
 // Same contraction and epilogue as k44_mfma_tile_kernel (Y[NT][512 tokens] = W[NT][K*S] x
 // X_gathered[K*S][512] on v_mfma_f32_16x16x32_f16), for the shape that carries the large
-// waves: 512 tokens per workgroup (8 waves x 64 tokens), NT in {32, 64}.
+// waves: 512 tokens per workgroup (8 waves x 64 tokens), NT in {32, 64, 128}.
 //
 // What differs is how data reaches LDS.  The register-staged kernel keeps one stage of X in
 // flight per workgroup (its loads must land in registers before they can be stored to LDS), so
@@ -101,9 +101,12 @@ __device__ __forceinline__ h4_t ds_read_tr16_at(uint32_t addr) {
 }
 
 // NTX: the direct loads use the non-temporal cache policy (substrates far beyond the caches).
+// NT = 128 (a 128-neuron tile: twice the MFMA work per gathered stage; 128 accumulator registers
+// per lane, so one workgroup per CU) takes a 3-stage ring (125 KiB of LDS, 2 stages in flight).
 template <int NT, bool NTX, int NBUF = 4>
 __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
-    static_assert(NT == 32 || NT == 64, "A-fragment stage must be whole dword loads per wave");
+    static_assert(NT == 32 || NT == 64 || NT == 128,
+                  "A-fragment stage must be whole dword loads per wave");
     constexpr int MT = 512, ROWS = 32;
     constexpr int NB = NT / 16;
     constexpr int PITCH = MT + 16;          // halves; 32-byte skew between rows
@@ -134,10 +137,12 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
     // A fragments of the tile: [k-step][16-neuron block][lane][8 halves]; one stage = one k-step.
     const char *wtile = reinterpret_cast<const char *>(a.Wf) + (uint64_t)tile * a.ksteps * WBYTES;
 
+    // This lane's 8 tokens of every gathered row (the same offset for every stage).
+    const uint64_t lane_x = tok_x(a, tok0 + (uint32_t)lane * 8u);
     auto issue = [&](uint32_t st, int buf) {
         const uint32_t kk = st * (uint32_t)ROWS;
         const uint32_t k = kk / a.S, s0 = kk - k * a.S;
-        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + tok0 + lane * 8;
+        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + lane_x;
 #pragma unroll
         for (int r = 0; r < XDMA; ++r) {
             const int row = wave + 8 * r;

@@ -71,7 +71,19 @@ struct MfmaTileArgs {
     // fp16(A*fp16(B*C)), A / B / C the rows at (segment offset + xd[0] / xd[1] / xd[2]).
     uint32_t xprod;
     int64_t xd[3];
+    // 2-D waves of 64-frame interleaved images: 64-token tile t of the wave gathers at
+    // segment offset + tile_x[t] and stores at tile_y[t] (every entry 64-element aligned);
+    // nullptr: 1-D token rows, tile t at 64 t for both.
+    const uint32_t *tile_x, *tile_y;
 };
+
+// Canvas offset of token t of a wave (relative to a segment row or an output row).
+__device__ __forceinline__ uint64_t tok_x(const MfmaTileArgs &a, uint32_t t) {
+    return a.tile_x ? (uint64_t)a.tile_x[t >> 6] + (t & 63u) : (uint64_t)t;
+}
+__device__ __forceinline__ uint64_t tok_y(const MfmaTileArgs &a, uint32_t t) {
+    return a.tile_y ? (uint64_t)a.tile_y[t >> 6] + (t & 63u) : (uint64_t)t;
+}
 
 // A launch covers a group of independent waves of one kernel configuration (the sub-waves of a
 // pruned projection, projections reading the same input): workgroup i belongs to the wave w with
@@ -117,7 +129,7 @@ __device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a, const 
             if (a.cmap && oj == K44_CMAP_EMPTY) continue;  // empty slot of a pattern-sorted tile
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
-                const uint64_t o = oj * a.out_stride + t_base + 16u * tb;
+                const uint64_t o = oj * a.out_stride + tok_y(a, t_base + 16u * tb);
                 const float r = a.R ? __half2float(a.R[o]) : 0.0f;
                 const float v = acc[nb][tb][i] + b;
                 const float y = a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r;
@@ -161,18 +173,21 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
                      (uint64_t)tile * a.ksteps * NB * 64 + lane;
 
     // Stage st covers index-row positions [st*ROWS, st*ROWS + ROWS) — inside one segment.
-    // Thread chunk i of a stage: row (tid + i*MT) / CPR, tokens ((tid + i*MT) % CPR) * 8 .. +8.
+    // Thread chunk i of a stage: row (tid + i*MT) / CPR, tokens ((tid + i*MT) % CPR) * 8 .. +8,
+    // at canvas offset xo[i] of the segment row (the same for every stage).
+    uint64_t xo[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) xo[i] = tok_x(a, tok0 + ((tid + i * MT) % CPR) * 8u);
     u4_t xr[CPT];  // X of the next stage, in flight during the current stage's MFMAs
     h8_t wn[SUBS][NB], wc[SUBS][NB];  // A fragments: next stage (in flight), current stage
     {
         const uint32_t kk = st_begin * (uint32_t)ROWS;
         const uint32_t k = kk / a.S, s0 = kk - k * a.S;
-        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + tok0;
+        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step;
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = tid + i * MT;
-            xr[i] = *reinterpret_cast<const u4_t *>(base + (uint64_t)(c / CPR) * a.step +
-                                                     (c % CPR) * 8);
+            xr[i] = *reinterpret_cast<const u4_t *>(base + (uint64_t)(c / CPR) * a.step + xo[i]);
         }
 #pragma unroll
         for (int u = 0; u < SUBS; ++u)
@@ -193,12 +208,12 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
         if (more) {  // issue next stage's X and W loads; consumed only after this stage's math
             const uint32_t kk = (st + 1) * (uint32_t)ROWS;
             const uint32_t k = kk / a.S, s0 = kk - k * a.S;
-            const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step + tok0;
+            const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step;
 #pragma unroll
             for (int i = 0; i < CPT; ++i) {
                 const int c = tid + i * MT;
                 xr[i] = *reinterpret_cast<const u4_t *>(base + (uint64_t)(c / CPR) * a.step +
-                                                         (c % CPR) * 8);
+                                                         xo[i]);
             }
 #pragma unroll
             for (int u = 0; u < SUBS; ++u)

@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp)
         v.w += u1.w;
     }
     if (a.cmap && oj == K44_CMAP_EMPTY) return;
-    const uint64_t o = oj * a.out_stride + t;
+    const uint64_t o = oj * a.out_stride + tok_y(a, t);  // 4 tokens never cross a 64-token tile
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.R) {
         const gd_u2 rv = *reinterpret_cast<const gd_u2 *>(a.R + o);

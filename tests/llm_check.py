@@ -114,7 +114,10 @@ class PlanChecker:
             elif t == "RMSNORM_1D":
                 state[i] = self.rows(c["src_off"], c["Cin"])
             elif t == "TOKEN_SHIFT_1D":
-                st = self._state(c) if self.decode else None
+                if not self.decode:  # prefill: the sampled windows and each request's tail
+                    state[i] = self._shift_inputs(c)
+                    continue
+                st = self._state(c)
                 # a shift fused into its norm reads the norm's output, read after the step
                 state[i] = (None if self._shift_fused(i, fused) else self.full(c["src_off"], c["Cin"]), st)
             elif t == "SWIGLU_MUL_1D":
@@ -146,23 +149,19 @@ class PlanChecker:
             elif t == "RMSNORM_1D":
                 y = self.rows(c["y_off"], c["Cin"]).astype(np.float64)
                 self._note(t, lo.orc.rel_err(y, lo.rmsnorm_f64(state[i])), what)
+            elif t == "TOKEN_SHIFT_1D" and not self.decode:
+                self._check_shift_prefill(c, state[i], what)
             elif t == "TOKEN_SHIFT_1D":
                 x, st_in = state[i]
                 if x is None:  # fused: its input is the norm output the step just wrote
                     x = self.full(c["src_off"], c["Cin"])
                 y = self.full(c["y_off"], c["Cin"])
-                if self.decode:
-                    ref, st_ref = lo.token_shift_decode(x, self.mix[name], st_in, self.valid, f64=True)
-                else:
-                    ref, st_ref = lo.token_shift(x, self.mix[name], self.spec.prompt, self.valid,
-                                                 f64=True)
+                ref, st_ref = lo.token_shift_decode(x, self.mix[name], st_in, self.valid, f64=True)
                 st = self._state(c)
-                if self.decode:  # request slots past the batch are not touched
-                    ok = np.array_equal(st[:, :, :self.valid].view(np.uint16),
-                                        st_ref[:, :, :self.valid].view(np.uint16))
-                else:
-                    ok = np.array_equal(st.view(np.uint16), st_ref.view(np.uint16))
-                assert ok, f"{what}: state block differs"
+                # request slots past the batch are not touched
+                assert np.array_equal(st[:, :, :self.valid].view(np.uint16),
+                                      st_ref[:, :, :self.valid].view(np.uint16)), \
+                    f"{what}: state block differs"
                 v = self.valid
                 self._note(t, lo.orc.rel_err(y[:, :v].astype(np.float64), ref[:, :v]), what)
             elif t == "SWIGLU_MUL_1D":
@@ -185,6 +184,49 @@ class PlanChecker:
     def _progress(self, tag: str, mode: str, k: int, n: int):
         if n >= 100 and (k + 1) % 50 == 0:
             self.log(f"[{tag}] {mode}: {k + 1} of {n} steps checked")
+
+    # ------------------------------------------------------------------ prefill token shift
+    def _shift_inputs(self, c):
+        """Input columns a prefill token shift needs for the sampled windows (each window with
+        the rf-1 columns before it) and for the state block (each request's last rf-1)."""
+        rf, seq, D = self.spec.rf, self.spec.prompt, c["Cin"]
+        T = self.T
+        wins = []
+        for a, n in self.windows:
+            lo_ = max(0, a - (rf - 1))
+            wins.append((a, n, lo_, self.plan.read_canvas_2d(int(c["src_off"]) + lo_, D, T,
+                                                             a + n - lo_).view(F16)))
+        tail = min(rf - 1, seq)
+        R = self.valid // seq
+        tails = [self.plan.read_canvas_2d(int(c["src_off"]) + r * seq + seq - tail, D, T,
+                                          tail).view(F16) for r in range(R)] if tail else []
+        return wins, tails
+
+    def _check_shift_prefill(self, c, inputs, what):
+        """y[:, t] = sum_{i < rf, i <= t % seq} mu[:, i] x[:, t - i] on the sampled windows
+        (the window form of llm_oracle.token_shift); state[c][i][r] = x[c][r*seq + seq-1-i]
+        bit for bit (zero beyond the requests)."""
+        wins, tails = inputs
+        mu = self.mix[c["name"]].astype(np.float64)
+        rf, seq = mu.shape[1], self.spec.prompt
+        ys, refs = [], []
+        for a, n, lo_, xw in wins:
+            xf = xw.astype(np.float64)
+            ref = np.zeros((xf.shape[0], n))
+            for k in range(n):
+                t = a + k
+                for i in range(min(rf, t % seq + 1)):
+                    ref[:, k] += mu[:, i] * xf[:, t - i - lo_]
+            refs.append(ref)
+            ys.append(self.plan.read_canvas_2d(int(c["y_off"]) + a, c["Cin"], self.T, n).view(F16))
+        err = lo.orc.rel_err(np.concatenate(ys, 1).astype(np.float64), np.concatenate(refs, 1))
+        want = np.zeros((c["Cin"], max(rf - 1, 0), 64), F16)
+        for r, tail in enumerate(tails):
+            for i in range(tail.shape[1]):
+                want[:, i, r] = tail[:, tail.shape[1] - 1 - i]
+        assert np.array_equal(self._state(c).view(np.uint16), want.view(np.uint16)), \
+            f"{what}: state block differs"
+        self._note("TOKEN_SHIFT_1D", err, what)
 
     # ------------------------------------------------------------------ drivers
     def run(self, mode: str, ids: np.ndarray, tag: str):

@@ -73,10 +73,10 @@ def test_mfma_tile_shapes(wavec, orc, nt, tokens):
     b = synth.normal_f16(rng, (cout,), 0.05)
     y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens, rows=cluster_rows(starts, S),
                                    weights=w, bias=b, cluster=nt, act="gelu", seed=13)
-    rep = plan.exec_report()["waves"][0]
-    dma = tokens % 512 == 0 and nt in (32, 64)
-    assert rep["path"] == ("mfma_dma" if dma else "mfma_tile")
     assert orc.rel_err(y, ref) <= TOL
+    rep = plan.exec_report()["waves"][0]
+    dma = tokens % 512 == 0 and nt in (32, 64, 128)
+    assert rep["path"] == ("mfma_dma" if dma else "mfma_tile")
 
 
 @pytest.mark.parametrize("S", [32, 96, 128, 160])
@@ -248,3 +248,36 @@ def test_narrow_long_chunks_many_tiles(wavec, orc, tuning, K, tokens):
         assert err <= TOL
         ys[mode] = y.astype(np.float64)
     assert orc.rel_err(ys["narrow"], ys["wide"]) <= TOL
+
+
+@pytest.mark.parametrize("S,K,tiles,tokens,res", [
+    (32, 1, 2, 512, False),     # one stage per tile
+    (64, 1, 1, 512, True),      # two stages (drain only)
+    (160, 3, 2, 1024, True),    # 15 stages, two token tiles
+    (512, 4, 3, 512, False),    # 64 stages
+])
+def test_dma_ring_nt128_matches_register_staged(wavec, orc, tuning, S, K, tiles, tokens, res):
+    """128-neuron tiles over 512-token workgroups take the LDS-ring kernel with a 3-stage ring
+    (one workgroup per CU); without split-K bit-identical to the register-staged 128-neuron
+    kernel (same k-step order), both within tolerance of the oracle."""
+    rng = np.random.default_rng(S * 11 + K)
+    C = 16384
+    starts = (rng.integers(0, (C - S) // 8, size=(tiles, K)) * 8).astype(np.uint32)
+    cout = tiles * 128
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    out = {}
+    tuning("splitk", 0)
+    for dma in (1, 0):
+        tuning("dma", dma)
+        y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens, rows=cluster_rows(starts, S),
+                                       weights=w, bias=b, cluster=128, act="silu", residual=res,
+                                       seed=23)
+        rep = plan.exec_report()["waves"][0]
+        assert rep["path"] == ("mfma_dma" if dma else "mfma_tile"), rep
+        assert rep["ring_stages"] == (3 if dma else 0), rep
+        err = orc.rel_err(y, ref)
+        _log(f"[dma nt=128 S={S} K={K} tiles={tiles} tokens={tokens} dma={dma}] rel err {err:.3e}")
+        assert err <= TOL
+        out[dma] = y
+    assert np.array_equal(out[1], out[0])

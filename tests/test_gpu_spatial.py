@@ -270,3 +270,47 @@ def test_token64_interleaved_image_plan(wavec, frames, reuse, H, W):
             err = orc.rel_err(got.astype(np.float64), ref)
             _log(f"[token64 F={F} {H}x{W}] {out}: rel err {err:.3e}")
             assert err <= TOL, out
+
+
+@pytest.mark.parametrize("frames,reuse", [(64, False), (128, True)])
+@pytest.mark.parametrize("H,W", [(6, 10), (8, 16)])
+def test_token64_dense_convs_on_mfma(wavec, tuning, frames, reuse, H, W):
+    """Dense convolutions of 64-frame interleaved images take the MFMA kernels through per-pixel
+    tile tables: a 3x3 convolution over 32 channels (phase-ordered into 9 segments of 32
+    channels), a 1x1 over 64 channels with a residual, a stride-2 3x3 over 64 channels (register-
+    staged and LDS-ring kernels, split-K) — each against cnn_oracle on the tensor the device
+    read."""
+    rng = np.random.default_rng(frames * 7 + H * W)
+    c0, c1 = 32, 64
+    w1, b1 = _conv_params(rng, c0, c1, 3)
+    w2, b2 = _conv_params(rng, c1, c1, 1)
+    w3, b3 = _conv_params(rng, c1, c0, 3)
+    f32 = lambda a: a.astype(np.float32)
+    g = wavec.WaveGraph(kv_cache_max_seq=0, batch_size=frames, reuse_canvas=reuse)
+    g.add_input("img", c0, H, W)
+    g.add_conv2d("c1", "img", "a", c0, c1, 3, 3, f32(w1), f32(b1), stride=1, pad=1, act="relu")
+    g.add_conv2d("c2", "a", "b", c1, c1, 1, 1, f32(w2), f32(b2), stride=1, pad=0, act="silu",
+                 res_blob="a")
+    g.add_conv2d("c3", "b", "y", c1, c0, 3, 3, f32(w3), f32(b3), stride=2, pad=1, act="none")
+    plan = g.compile()
+    plan.init_gpu()
+    rep = plan.exec_report()["waves"]
+    _log(f"[token64 mfma F={frames} {H}x{W}] " + ", ".join(
+        f"{w['path']} K={w['K']} S={w['S']} ksplit={w['ksplit']}" for w in rep))
+    assert all(w["path"].startswith("mfma") for w in rep), rep
+    lay = lambda h, w: co.Layout2D(h, w, frames, tok64=True)
+    x = _f16(rng, (frames, c0, H, W))
+    _t64_write(plan, plan.cmds[0]["src_off"], lay(H, W), x)
+    dev = {"img": x}
+    H3, W3 = (H + 1) // 2, (W + 1) // 2
+    steps = [("a", c1, H, W, lambda t: co.conv2d_f64(t["img"], w1, b1, 1, 1, "relu")),
+             ("b", c1, H, W, lambda t: co.conv2d_f64(t["a"], w2, b2, 1, 0, "silu", t["a"])),
+             ("y", c0, H3, W3, lambda t: co.conv2d_f64(t["b"], w3, b3, 2, 1))]
+    for i, (out, C, h, w, ref_fn) in enumerate(steps):
+        plan.execute_range(i, 1)
+        c = plan.cmds[i]
+        got = _t64_read(plan, c["y_off"], lay(h, w), C)
+        dev[out] = got
+        err = orc.rel_err(got.astype(np.float64), ref_fn(dev))
+        _log(f"[token64 mfma F={frames} {H}x{W}] {out}: rel err {err:.3e}")
+        assert err <= TOL, out
