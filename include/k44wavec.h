@@ -208,6 +208,15 @@ int wavec_k44_f16_forward_token64(void *Y, const void *X, const uint32_t *cluste
  * and frees on `stream` for the call (hipMallocAsync / hipFreeAsync).  Asynchronous. */
 int wavec_argmax_f16(uint32_t *ids, const void *logits, uint32_t vocab, uint32_t stride,
                      uint32_t tokens, void *stream);
+/* wavec_argmax_f16 without any allocation, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The per-chunk partials live in a fixed 4 MiB array inside the
+ * library's device code (one per GPU, held until the process ends; enough for
+ * strides up to 524,288 tokens: sizes that need more return -1 with a message).  Calls that
+ * overlap on one GPU share that array and race; ids, results and arguments otherwise as
+ * wavec_argmax_f16. */
+int wavec_argmax_f16_noalloc(uint32_t *ids, const void *logits, uint32_t vocab, uint32_t stride,
+                             uint32_t tokens, void *stream);
 /* GPU weight interleave, replaces interleave_weights_cluster16_wmma_gpu_kernel
  * (kernel44_immutable.cuh:261-267, kernels/rocm/kernel44_rocm_pack.cuh:285-290): row-major
  * [num_output_neurons][8*B_vec8] fp16 (vectors of 8) -> WMMA vector order; neurons % 16 == 0,

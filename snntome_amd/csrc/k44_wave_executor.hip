@@ -1866,6 +1866,32 @@ struct K44GpuExecutorState {
     }
 };
 
+// Workspace of the allocation-free entry points: an array in the library's device code
+// object, so each GPU the library runs on holds its own copy until the process ends.  Host code
+// never passes the array's name to a kernel (on the host it is only a stand-in for the symbol):
+// scratch_ptr() looks up its address on the current device once (hipGetSymbolAddress) and keeps
+// it per device.  Every call on one GPU shares that GPU's copy: calls that overlap on one GPU
+// (different streams, different threads) race.
+namespace noalloc {
+constexpr size_t kScratchFloats = (size_t)1 << 20;  // 4 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+static std::mutex g_mu;
+static std::map<int, float *> g_ptr;  // device ordinal -> address of `scratch` there
+
+static float *scratch_ptr() {
+    int dev = 0;
+    K44_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_ptr.find(dev);
+    if (it != g_ptr.end()) return it->second;
+    void *p = nullptr;
+    K44_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) throw std::runtime_error("hipGetSymbolAddress returned no address for the workspace");
+    g_ptr[dev] = static_cast<float *>(p);
+    return g_ptr[dev];
+}
+}  // namespace noalloc
+
 static std::mutex g_exec_mu;
 // Executors by graph handle.  Heap-held and never destroyed, so no HIP call runs from a static
 // destructor after the HIP runtime has shut down at process exit.
@@ -2365,6 +2391,27 @@ int wavec_argmax_f16(uint32_t *ids, const void *logits, uint32_t vocab, uint32_t
                                                    stride, tokens, static_cast<float *>(work), st);
         K44_HIP(hipFreeAsync(work, st));
         K44_HIP(e);
+        return 0;
+    });
+}
+
+int wavec_argmax_f16_noalloc(uint32_t *ids, const void *logits, uint32_t vocab,
+                             uint32_t stride, uint32_t tokens, void *stream) {
+    return guarded("wavec_argmax_f16_noalloc", [&] {
+        if (!ids || !logits) throw std::runtime_error("ids and logits are required");
+        if (vocab == 0u || stride == 0u || stride % 64u != 0u || tokens == 0u || tokens > stride)
+            throw std::runtime_error("vocab > 0, stride a positive multiple of 64 and "
+                                     "0 < tokens <= stride are required");
+        const size_t need = k44dev::argmax_scratch_floats(vocab, stride);
+        if (need > k44_host::noalloc::kScratchFloats)
+            throw std::runtime_error("needs " + std::to_string(need) +
+                                     " floats of workspace; the allocation-free form holds " +
+                                     std::to_string(k44_host::noalloc::kScratchFloats) +
+                                     " (use wavec_argmax_f16 for this size)");
+        float *ws = k44_host::noalloc::scratch_ptr();
+        K44_HIP(k44dev::launch_argmax(ids, nullptr, nullptr, 0u,
+                                      static_cast<const __half *>(logits), vocab, stride, tokens,
+                                      ws, static_cast<hipStream_t>(stream)));
         return 0;
     });
 }

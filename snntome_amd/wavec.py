@@ -111,6 +111,7 @@ _ABI = (
      (_VOID, _VOID, _VOID, _VOID, _VOID, _U32, _U32, _U32, _U32, _U32, _VOID)),
     ("wavec_interleave_weights_wmma", _INT, (_VOID, _VOID, _U32, _U32, _VOID)),
     ("wavec_argmax_f16", _INT, (_VOID, _VOID, _U32, _U32, _U32, _VOID)),
+    ("wavec_argmax_f16_noalloc", _INT, (_VOID, _VOID, _U32, _U32, _U32, _VOID)),
     ("wavec_set_tuning", _INT, (_STR, _INT)),
     ("wavec_get_tuning", _INT, (_STR,)),
     ("wavec_reset_tuning", None, ()),
@@ -685,3 +686,12 @@ def argmax_f16(ids, logits, vocab: int, stride: int, tokens: int, stream=None) -
     _raise_on(get_lib().wavec_argmax_f16(_dev_ptr(ids), _dev_ptr(logits), int(vocab), int(stride),
                                          int(tokens), _dev_ptr(stream) or None),
               "wavec_argmax_f16")
+
+
+def argmax_f16_noalloc(ids, logits, vocab: int, stride: int, tokens: int, stream=None) -> None:
+    """argmax_f16 without any allocation: the partials live in a fixed per-GPU array of the
+    library (strides up to 524,288 tokens); calls that overlap on one GPU race."""
+    _raise_on(get_lib().wavec_argmax_f16_noalloc(_dev_ptr(ids), _dev_ptr(logits), int(vocab),
+                                                 int(stride), int(tokens),
+                                                 _dev_ptr(stream) or None),
+              "wavec_argmax_f16_noalloc")
