@@ -41,7 +41,7 @@ namespace {
 std::atomic<int> g_tune[(int)Tune::Count];
 const char *const kTuneKeys[(int)Tune::Count] = {
     "path", "dma", "dma_stages", "nt", "splitk", "lane8", "ksplit", "stream_kernel", "narrow",
-    "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring"};
+    "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring", "xcd_order"};
 struct TuneInit {
     TuneInit() {
         for (auto &v : g_tune) v.store(-1);
@@ -265,6 +265,7 @@ struct K44GpuExecutorState {
     hipGraphExec_t graph_exec = nullptr;
     bool use_graph = false;
     bool initialized = false;
+    uint32_t xcd_order = 1;  // MFMA tile kernels: contiguous item ranges per XCD
     std::string report_json;
 
     ~K44GpuExecutorState() { free_all(); }
@@ -1108,6 +1109,7 @@ struct K44GpuExecutorState {
     }
 
     void init(const K44WavePlan &plan) {
+        xcd_order = tune(Tune::XcdOrder) == 0 ? 0u : 1u;
         free_all();
         plan_meta.res_map = plan.res_map;
         plan_meta.canvas_elems = plan.canvas_elems;
@@ -1696,13 +1698,13 @@ struct K44GpuExecutorState {
     }
 
     void launch_mfma(const WaveExec &w) {
-        const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, 1u};
+        const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, 1u, xcd_order};
         launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
                           w.dshape, false, w.items);
     }
 
     void launch_group(const MfmaGroupExec &g) {
-        const k44dev::MfmaGroup d{g.args.p, g.start.p, (uint32_t)g.members.size()};
+        const k44dev::MfmaGroup d{g.args.p, g.start.p, (uint32_t)g.members.size(), xcd_order};
         launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.dshape,
                           g.prod, g.max_items);
     }

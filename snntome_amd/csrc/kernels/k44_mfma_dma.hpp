@@ -118,10 +118,11 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
     __shared__ __attribute__((aligned(16))) _Float16 xl[NBUF][ROWS][PITCH];
     __shared__ __attribute__((aligned(16))) uint32_t wl[NBUF][WBYTES / 4];
 
+    const uint32_t item = group_item(grp);
     uint32_t w = 0;
-    while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
+    while (w + 1u < grp.n && item >= grp.start[w + 1u]) ++w;
     const MfmaTileArgs a = grp.waves[w];
-    const uint32_t local = blockIdx.x - grp.start[w];
+    const uint32_t local = item - grp.start[w];
     const uint32_t tile = local % a.tiles, rest = local / a.tiles;
     const uint32_t ytile = rest % a.ttiles, zgroup = rest / a.ttiles;
 

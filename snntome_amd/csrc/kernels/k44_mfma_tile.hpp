@@ -93,7 +93,20 @@ struct MfmaGroup {
     const MfmaTileArgs *waves;  // [n]
     const uint32_t *start;      // [n+1] prefix sums of tiles * ttiles * kgroups
     uint32_t n;
+    uint32_t xcd_order;         // 1: contiguous item ranges per XCD (group_item)
 };
+
+// Work item of this workgroup.  Workgroups are handed to the 8 XCDs round-robin (workgroup b
+// runs on XCD b % 8), each XCD with its own L2.  With xcd_order, XCD x runs the contiguous item
+// range [x*q + min(x, r), ...) (n = 8q + r items, a bijection of [0, n)): consecutive tiles of
+// one token tile, whose gathers read the token tile's input rows, share that XCD's L2 instead of
+// every XCD fetching every token tile.
+__device__ __forceinline__ uint32_t group_item(const MfmaGroup &g) {
+    const uint32_t b = blockIdx.x;
+    if (!g.xcd_order) return b;
+    const uint32_t n = gridDim.x, x = b & 7u, s = b >> 3, q = n >> 3, r = n & 7u;
+    return x * q + min(x, r) + s;
+}
 
 // Epilogue of a 64-token-per-wave MFMA tile: lane holds C[4g + i][lane & 15] of every 16x16
 // accumulator tile.  Split-K stores the fp32 partial; otherwise bias, activation, residual /
@@ -140,10 +153,11 @@ __device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a, const 
 
 template <int NT, int MT, int ROWS>
 __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
+    const uint32_t item = group_item(grp);
     uint32_t w = 0;
-    while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
+    while (w + 1u < grp.n && item >= grp.start[w + 1u]) ++w;
     const MfmaTileArgs a = grp.waves[w];
-    const uint32_t local = blockIdx.x - grp.start[w];
+    const uint32_t local = item - grp.start[w];
     const uint32_t tile = local % a.tiles, rest = local / a.tiles;
     const uint32_t ytile = rest % a.ttiles, zgroup = rest / a.ttiles;
     constexpr int NB = NT / 16;              // 16-neuron blocks per tile

@@ -281,3 +281,26 @@ def test_dma_ring_nt128_matches_register_staged(wavec, orc, tuning, S, K, tiles,
         assert err <= TOL
         out[dma] = y
     assert np.array_equal(out[1], out[0])
+
+
+@pytest.mark.parametrize("nt,tokens,tiles", [(64, 512, 13), (32, 1024, 7), (64, 192, 5),
+                                             (128, 512, 3), (16, 256, 9)])
+def test_xcd_item_order_bit_identical(wavec, orc, tuning, nt, tokens, tiles):
+    """Work items taken as contiguous ranges per XCD (xcd_order, the default) or in plain
+    workgroup order are the same items: bit-identical outputs, within tolerance of the oracle;
+    item counts that are not multiples of 8 included (LDS-ring and register-staged kernels)."""
+    rng = np.random.default_rng(nt * 31 + tiles)
+    C, K, S = 8192, 2, 64
+    starts = (rng.integers(0, (C - S) // 8, size=(tiles, K)) * 8).astype(np.uint32)
+    w = synth.normal_f16(rng, (tiles * nt, K * S), 0.05)
+    b = synth.normal_f16(rng, (tiles * nt,), 0.05)
+    out = {}
+    for order in (1, 0):
+        tuning("xcd_order", order)
+        y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
+                                       rows=cluster_rows(starts, S), weights=w, bias=b,
+                                       cluster=nt, act="silu", seed=29)
+        assert plan.exec_report()["waves"][0]["path"] in ("mfma_dma", "mfma_tile")
+        assert orc.rel_err(y, ref) <= TOL
+        out[order] = y
+    assert np.array_equal(out[0], out[1])
