@@ -348,6 +348,54 @@ def bench_llm(steps: int, warmup: int, eager: bool, no_cpu: bool = True) -> dict
     return out
 
 
+def bench_projection(name: str, steps: int, warmup: int, tile: int = 0) -> dict:
+    """One projection of layer 0 of the config-5 prefill, alone, at its real shape (16 x 512
+    tokens, the same pruned weights and pattern-sorted tiles as in the whole plan, input filled
+    on the device): the unit a kernel profile of the prefill's MFMA waves is taken on.  Plain
+    plan executions, no HIP graph."""
+    from snntome_amd import synth, wavec
+
+    spec = synth.LLMSpec()
+    wts = synth.llm_weights(spec)
+    if tile:
+        spec.tile = tile
+    p = wts.head if name == "head" else wts.proj[0][name]
+    fan = spec.ffn if name == "dn" else spec.d
+    act = {"q": "sigmoid", "k": "silu", "g": "silu"}.get(name)
+    T = spec.requests * spec.prompt
+    g = wavec.WaveGraph(kv_cache_max_seq=0)
+    g.add_input("x", fan, 1, T, is_1d=True)
+    g.add_pruned_wave(name, "x", "y", p.starts, spec.S, p.weights, p.bias, tile=spec.tile, act=act)
+    g.set_output("y")
+    plan = g.compile()
+    plan.init_gpu()
+    plan.fill_input_uniform(spec.seed)
+    rep = plan.exec_report()["waves"]
+    if warmup > 0:
+        plan.execute(warmup)
+    plan.sync()
+    ms = plan.execute(steps)
+    plan.sync()
+    plan.release_gpu()
+    eff = 2.0 * p.weights.shape[0] * p.weights.shape[1] * T
+    ex = float(sum(w["flops"] for w in rep))
+    tf = eff / (ms * 1e-3) / 1e12
+    log(f"[bench] projection {name}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s effective, "
+        f"executed x{ex / eff:.3f}, paths {sorted({w['path'] for w in rep})}")
+    return {
+        "metric": METRIC, "value": round(tf, 3), "unit": "TFLOP/s", "ms_per_step": round(ms, 5),
+        "config": {"workload": "config5_prefill_projection", "projection": f"l0.{name}",
+                   "neurons": int(p.weights.shape[0]), "inputs_per_neuron": int(p.weights.shape[1]),
+                   "fan_in": fan, "tokens": T, "tile": spec.tile,
+                   "paths": sorted({w["path"] for w in rep})},
+        "executed_over_effective_flops": round(ex / eff, 4),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP16_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel_ms": round(ms, 5),
+                     "scope": "one projection alone, effective FLOPs"},
+    }
+
+
 def bench_token64(args):
     """The whitepaper's stand-alone Token64 wave (wavec_k44_f16_forward_token64) at its own
     benchmark shape (whitepaper/sparse_wmma_kernel/tests/benchmark_whitepaper_k44.cpp:141-197):
@@ -418,6 +466,8 @@ def _envelope(rec: dict, args, data: str) -> dict:
         "dtype": "f16 (fp32 accumulate)", "data": data,
     }
     out.update({k: v for k, v in rec.items() if k not in out and not k.startswith("_")})
+    if getattr(args, "tune", None):
+        out["tuning"] = {kv.partition("=")[0]: int(kv.partition("=")[2]) for kv in args.tune}
     return out
 
 
@@ -439,6 +489,13 @@ def main():
                     help="the whitepaper's stand-alone Token64 wave at its benchmark shape")
     ap.add_argument("--cluster", type=int, default=128, help="--token64: cluster size S")
     ap.add_argument("--t64-cin", type=int, default=10_000_000, help="--token64: Cin")
+    ap.add_argument("--c5-projection", default=None,
+                    choices=["q", "k", "v", "o", "g", "u", "dn", "head"],
+                    help="one config-5 prefill projection (layer 0) alone, for kernel profiles")
+    ap.add_argument("--c5-tile", type=int, default=0,
+                    help="--c5-projection: neurons per pattern-sorted tile (default: the spec's)")
+    ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
+                    help="executor tuning switch (wavec_set_tuning) for every plan; repeatable")
     ap.add_argument("--copy-probe-gib", type=float, default=0.0,
                     help="only run a plain device copy of this many GiB (PMC calibration)")
     args = ap.parse_args()
@@ -453,6 +510,15 @@ def main():
         sys.exit(2)
     if args.token64:
         bench_token64(args)
+        return
+    if args.tune:
+        from snntome_amd import wavec
+        for kv in args.tune:
+            key, _, val = kv.partition("=")
+            wavec.set_tuning(key, int(val))
+    if args.c5_projection:
+        rec = bench_projection(args.c5_projection, args.steps, args.warmup, args.c5_tile)
+        print(json.dumps(_envelope(rec, args, LLM_DATA)), flush=True)
         return
     # Under rocprofv3 config 5 launches kernel by kernel: a kernel-trace run of its HIP-graph
     # capture ended in a host segmentation fault inside the profiler's preloaded libraries.

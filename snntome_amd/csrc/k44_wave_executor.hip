@@ -1569,6 +1569,14 @@ struct K44GpuExecutorState {
             a.tile_x = w.tile_x.p;
             a.tile_y = w.tile_y.p;
         }
+        // 16-byte epilogue accesses: output, residual and split-K partial rows 16-byte aligned
+        // (2-D tile tables hold 64-element aligned offsets).
+        const uint64_t y0 = fused ? w.y_off_run : w.y_off;
+        a.epi_vec = (y0 % 8u == 0u && a.out_stride % 8u == 0u &&
+                     (!w.has_res || w.res_off % 8u == 0u) &&
+                     (w.kgroups <= 1u || w.part_tokens % 4u == 0u))
+                        ? 1u
+                        : 0u;
         return a;
     }
 

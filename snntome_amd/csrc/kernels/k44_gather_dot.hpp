@@ -54,16 +54,41 @@ constexpr uint64_t K44_CMAP_EMPTY = 0xffffu;
 // Largest per-neuron weight block (halves) the gather kernels stage in LDS.
 constexpr uint32_t GD_WL_MAX = 2048;
 
+// Activation with the id fixed at compile time (epilogues that apply it many times in
+// unrolled code instantiate one activation instead of inlining the whole switch per element,
+// which multiplies the code size past the instruction cache).
+template <int ACT>
+__device__ __forceinline__ float act_c(float v) {
+    if constexpr (ACT == ACT_RELU) return fmaxf(v, 0.0f);
+    else if constexpr (ACT == ACT_SIGMOID) return 1.0f / (1.0f + __expf(-v));
+    else if constexpr (ACT == ACT_SILU) return v / (1.0f + __expf(-v));
+    else if constexpr (ACT == ACT_LEAKY) return fmaxf(v, 0.1f * v);
+    else if constexpr (ACT == ACT_GELU) return 0.5f * v * (1.0f + erff(v * 0.70710678f));
+    else return v;
+}
+
 __device__ __forceinline__ float apply_act(float v, int act) {
     switch (act) {
-    case ACT_RELU: return fmaxf(v, 0.0f);
-    case ACT_SIGMOID: return 1.0f / (1.0f + __expf(-v));
-    case ACT_SILU: return v / (1.0f + __expf(-v));
-    case ACT_LEAKY: return fmaxf(v, 0.1f * v);
-    case ACT_GELU: return 0.5f * v * (1.0f + erff(v * 0.70710678f));
-    default: return v;
+    case ACT_RELU: return act_c<ACT_RELU>(v);
+    case ACT_SIGMOID: return act_c<ACT_SIGMOID>(v);
+    case ACT_SILU: return act_c<ACT_SILU>(v);
+    case ACT_LEAKY: return act_c<ACT_LEAKY>(v);
+    case ACT_GELU: return act_c<ACT_GELU>(v);
+    default: return act_c<ACT_NONE>(v);
     }
 }
+
+// Runs the statement(s) with the activation id of `act` as the compile-time constant A_ (unknown
+// ids as ACT_NONE, like apply_act): one switch per call site instead of one per element.
+#define K44_WITH_ACT(act, ...)                                                                  \
+    switch (act) {                                                                             \
+    case ACT_RELU: { constexpr int A_ = ACT_RELU; __VA_ARGS__; } break;                         \
+    case ACT_SIGMOID: { constexpr int A_ = ACT_SIGMOID; __VA_ARGS__; } break;                   \
+    case ACT_SILU: { constexpr int A_ = ACT_SILU; __VA_ARGS__; } break;                         \
+    case ACT_LEAKY: { constexpr int A_ = ACT_LEAKY; __VA_ARGS__; } break;                       \
+    case ACT_GELU: { constexpr int A_ = ACT_GELU; __VA_ARGS__; } break;                         \
+    default: { constexpr int A_ = ACT_NONE; __VA_ARGS__; } break;                               \
+    }
 
 struct GatherDotArgs {
     const __half *X;         // canvas base

@@ -117,6 +117,7 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
     constexpr int CPOL = NTX ? 2 : 0;       // cache-policy operand: 2 = nt
     __shared__ __attribute__((aligned(16))) _Float16 xl[NBUF][ROWS][PITCH];
     __shared__ __attribute__((aligned(16))) uint32_t wl[NBUF][WBYTES / 4];
+    static_assert(sizeof(xl) >= 8 * EPI_WAVE_FLOATS * sizeof(float), "epilogue LDS regions");
 
     const uint32_t item = group_item(grp);
     uint32_t w = 0;
@@ -202,7 +203,11 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
 
     lds_ring<NBUF, D>(n_st, [&](uint32_t st, int buf) { issue(st_begin + st, buf); }, compute);
 
-    mfma_tile_epilogue<NT>(a, acc, tile, tok0, zgroup, lane, wave);
+    // Every wave is done with the ring (its LDS reads completed) before the LDS-transposed
+    // epilogue reuses the X slots.
+    if (a.epi_vec) wg_barrier_no_fence();
+    mfma_tile_epilogue<NT>(a, acc, tile, tok0, zgroup, lane, wave,
+                           reinterpret_cast<float *>(&xl[0][0][0]) + wave * EPI_WAVE_FLOATS);
 }
 
 }  // namespace k44dev

@@ -75,6 +75,9 @@ struct MfmaTileArgs {
     // segment offset + tile_x[t] and stores at tile_y[t] (every entry 64-element aligned);
     // nullptr: 1-D token rows, tile t at 64 t for both.
     const uint32_t *tile_x, *tile_y;
+    // 1: Y, R and out_stride are multiples of 8 elements (and split-K partial rows of 4), so
+    // the epilogue may use 16-byte accesses (mfma_tile_epilogue_lds).
+    uint32_t epi_vec;
 };
 
 // Canvas offset of token t of a wave (relative to a segment row or an output row).
@@ -109,12 +112,13 @@ __device__ __forceinline__ uint32_t group_item(const MfmaGroup &g) {
 }
 
 // Epilogue of a 64-token-per-wave MFMA tile: lane holds C[4g + i][lane & 15] of every 16x16
-// accumulator tile.  Split-K stores the fp32 partial; otherwise bias, activation, residual /
-// cout_map and the fp16 (RNE) store.
-template <int NT>
-__device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a, const f4_t (&acc)[NT / 16][4],
-                                                   uint32_t tile, uint32_t tok0, uint32_t zgroup,
-                                                   int lane, int wave) {
+// accumulator tile.  Split-K stores the fp32 partial; otherwise bias, activation ACT, residual /
+// cout_map and the fp16 (RNE) store, 2 bytes per lane per access.
+template <int NT, int ACT>
+__device__ __forceinline__ void mfma_epilogue_direct(const MfmaTileArgs &a,
+                                                     const f4_t (&acc)[NT / 16][4], uint32_t tile,
+                                                     uint32_t tok0, uint32_t zgroup, int lane,
+                                                     int wave) {
     constexpr int NB = NT / 16;
     const int g = lane >> 4;
     const uint32_t n_base = tile * (uint32_t)NT + 4u * (uint32_t)g;
@@ -145,10 +149,101 @@ __device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a, const 
                 const uint64_t o = oj * a.out_stride + tok_y(a, t_base + 16u * tb);
                 const float r = a.R ? __half2float(a.R[o]) : 0.0f;
                 const float v = acc[nb][tb][i] + b;
-                const float y = a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r;
+                const float y = a.cmap ? act_c<ACT>(v + r) : act_c<ACT>(v) + r;
                 a.Y[o] = __float2half_rn(y);
             }
         }
+}
+
+// LDS floats one wave needs for mfma_epilogue_lds (16 neurons x 64 tokens, padded rows).
+constexpr int EPI_PITCH = 68;
+constexpr int EPI_WAVE_FLOATS = 16 * EPI_PITCH;
+
+// The same epilogue with the accumulators transposed through LDS, for waves whose output and
+// residual offsets are multiples of 8 elements (MfmaTileArgs::epi_vec).  Each wave writes its
+// accumulators, 16 neurons at a time, to its own LDS region `ws` ([neuron][64 tokens],
+// EPI_WAVE_FLOATS floats) and reads them back as 8 consecutive tokens of one neuron per lane:
+// 16-byte residual loads and 16-byte stores, 8 lanes covering a neuron's 64 tokens (split-K
+// partials: two 16-byte stores).  Bias and, without a cout_map, the activation are applied
+// before the transpose, the rest after it: the same operations in the same order as
+// mfma_epilogue_direct, so the same results.
+template <int NT, int ACT>
+__device__ __forceinline__ void mfma_epilogue_lds(const MfmaTileArgs &a,
+                                                  const f4_t (&acc)[NT / 16][4], uint32_t tile,
+                                                  uint32_t tok0, uint32_t zgroup, int lane,
+                                                  int wave, float *ws) {
+    constexpr int NB = NT / 16;
+    const int g = lane >> 4, c = lane & 15;
+    const bool split = a.part != nullptr, mapped = a.cmap != nullptr;
+    const uint32_t t_wave = tok0 + (uint32_t)wave * 64u;
+    const int ch = lane & 7;  // read side: 8-token chunk of the lane
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        // write: lane holds neurons 4g..4g+3 of block nb, tokens 16 tb + c
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t j = tile * (uint32_t)NT + 16u * nb + 4u * (uint32_t)g + (uint32_t)i;
+            const float b = (!split && a.bias) ? __half2float(a.bias[j]) : 0.0f;
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                float v = acc[nb][tb][i];
+                if (!split) {
+                    v = v + b;
+                    if (!mapped) v = act_c<ACT>(v);
+                }
+                ws[(4 * g + i) * EPI_PITCH + 16 * tb + c] = v;
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // read: neuron n = 8q + lane / 8 of the block, tokens 8 ch .. 8 ch + 7
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int n = 8 * q + (lane >> 3);
+            const f4_t v0 = *reinterpret_cast<const f4_t *>(&ws[n * EPI_PITCH + 8 * ch]);
+            const f4_t v1 = *reinterpret_cast<const f4_t *>(&ws[n * EPI_PITCH + 8 * ch + 4]);
+            const uint32_t j = tile * (uint32_t)NT + 16u * nb + (uint32_t)n;
+            const uint32_t t = t_wave + 8u * (uint32_t)ch;
+            if (split) {
+                float *pz = a.part + ((uint64_t)zgroup * a.cout + j) * a.tokens + t;
+                reinterpret_cast<f4_t *>(pz)[0] = v0;
+                reinterpret_cast<f4_t *>(pz)[1] = v1;
+                continue;
+            }
+            const uint64_t oj = mapped ? (uint64_t)a.cmap[j] : (uint64_t)j;
+            if (mapped && oj == K44_CMAP_EMPTY) continue;  // empty slot of a pattern-sorted tile
+            const uint64_t o = oj * a.out_stride + tok_y(a, t);
+            const float vv[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            u4_t rr = {0u, 0u, 0u, 0u};
+            if (a.R) rr = *reinterpret_cast<const u4_t *>(a.R + o);
+            const __half *rh = reinterpret_cast<const __half *>(&rr);
+            u4_t out;
+            __half *oh = reinterpret_cast<__half *>(&out);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float r = a.R ? __half2float(rh[k]) : 0.0f;
+                const float y = mapped ? act_c<ACT>(vv[k] + r) : vv[k] + r;
+                oh[k] = __float2half_rn(y);
+            }
+            *reinterpret_cast<u4_t *>(a.Y + o) = out;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+}
+
+// Epilogue of the wide MFMA kernels, one activation instance per wave (the unrolled epilogue
+// with the whole activation switch inlined per element outgrows the instruction cache).  With
+// a.epi_vec the LDS-transposed form: `ws` is this wave's region of EPI_WAVE_FLOATS floats, and
+// every wave of the workgroup must be done with the LDS it overlays.
+template <int NT>
+__device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a,
+                                                   const f4_t (&acc)[NT / 16][4], uint32_t tile,
+                                                   uint32_t tok0, uint32_t zgroup, int lane,
+                                                   int wave, float *ws) {
+    if (a.epi_vec) {
+        K44_WITH_ACT(a.act, mfma_epilogue_lds<NT, A_>(a, acc, tile, tok0, zgroup, lane, wave, ws))
+    } else {
+        K44_WITH_ACT(a.act, mfma_epilogue_direct<NT, A_>(a, acc, tile, tok0, zgroup, lane, wave))
+    }
 }
 
 template <int NT, int MT, int ROWS>
@@ -165,6 +260,7 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
     constexpr int CPR = MT / 8;              // 16-byte chunks per position row
     constexpr int CPT = ROWS * CPR / MT;     // chunks per thread per stage (= ROWS / 8)
     __shared__ __attribute__((aligned(16))) _Float16 lds[2][ROWS][PITCH];
+    static_assert(sizeof(lds) >= (MT / 64) * EPI_WAVE_FLOATS * sizeof(float), "epilogue LDS");
 
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t tok0 = ytile * (uint32_t)MT;
@@ -263,7 +359,9 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
         __syncthreads();
     }
 
-    mfma_tile_epilogue<NT>(a, acc, tile, tok0, zgroup, lane, wave);
+    // The last stage ended with a barrier after its LDS reads: the LDS is free for the epilogue.
+    mfma_tile_epilogue<NT>(a, acc, tile, tok0, zgroup, lane, wave,
+                           reinterpret_cast<float *>(&lds[0][0][0]) + wave * EPI_WAVE_FLOATS);
 }
 
 }  // namespace k44dev
