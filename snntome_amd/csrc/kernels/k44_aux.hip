@@ -151,6 +151,72 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
     }
 }
 
+// Wide token counts (prefill): workgroup = 4 token octets (32 tokens, 64-byte row runs) x 256
+// channel lanes (1024 threads), one workgroup per 32 tokens.  A thread loads its CPT channels
+// (lane, lane + 256, ...) once, keeps them in registers for the sum of squares and the scaled
+// store: the input is read once (the narrower kernel above reads it twice).  Sums meet by
+// shuffles within a wave, then across the 16 waves in LDS in wave order.
+template <int CPT>
+__global__ __launch_bounds__(1024) void k44_rmsnorm_regs_kernel(__half *__restrict__ y,
+                                                                const __half *__restrict__ x,
+                                                                const __half *__restrict__ gamma,
+                                                                uint32_t D, uint32_t stride,
+                                                                float eps) {
+    constexpr uint32_t OCT = 4u, CL = 256u;
+    __shared__ float part[16][OCT * 8];
+    __shared__ float inv_s[OCT * 8];
+    const uint32_t oct = threadIdx.x % OCT, lane_c = threadIdx.x / OCT;
+    const uint32_t t0 = (blockIdx.x * OCT + oct) * 8u;
+    uint4 v[CPT];
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const uint32_t c = lane_c + (uint32_t)u * CL;
+        v[u] = c < D ? *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0)
+                     : uint4{0u, 0u, 0u, 0u};
+    }
+    float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const __half *h = reinterpret_cast<const __half *>(&v[u]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float f = __half2float(h[k]);
+            ss[k] = fmaf(f, f, ss[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (uint32_t m = OCT; m < 64u; m <<= 1) ss[k] += __shfl_xor(ss[k], (int)m, 64);
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if (lane < OCT) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) part[wave][lane * 8u + k] = ss[k];
+    }
+    __syncthreads();
+    if (threadIdx.x < OCT * 8u) {  // one total per (octet, token), the waves added in order
+        float t = part[0][threadIdx.x];
+        for (int w = 1; w < 16; ++w) t += part[w][threadIdx.x];
+        inv_s[threadIdx.x] = rsqrtf(t / (float)D + eps);
+    }
+    __syncthreads();
+    float inv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) inv[k] = inv_s[oct * 8u + k];
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const uint32_t c = lane_c + (uint32_t)u * CL;
+        if (c >= D) break;
+        const __half *h = reinterpret_cast<const __half *>(&v[u]);
+        const float g = gamma ? __half2float(gamma[c]) : 1.0f;
+        uint4 o;
+        __half *oh = reinterpret_cast<__half *>(&o);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) oh[k] = __float2half_rn(__half2float(h[k]) * inv[k] * g);
+        *reinterpret_cast<uint4 *>(y + (uint64_t)c * stride + t0) = o;
+    }
+}
+
 __global__ __launch_bounds__(256) void k44_mul_kernel(__half *__restrict__ y,
                                                       const __half *__restrict__ a,
                                                       const __half *__restrict__ b, uint64_t n8) {
@@ -168,56 +234,86 @@ __global__ __launch_bounds__(256) void k44_mul_kernel(__half *__restrict__ y,
     }
 }
 
-// Prefill: thread = (channel c = blockIdx.y + k*gridDim.y, 8 consecutive tokens), with the
-// 8 tokens before them in registers (rf - 1 <= 8), so every tap is a register read.  State
-// block of channel c: state[(c*(rf-1) + i)*64 + r] = input of request r, i+1 tokens back.
+// Prefill: thread = (TS_CPC channels c0 + j, c0 = (blockIdx.y + k*gridDim.y) * TS_CPC, 8
+// consecutive tokens), with the 8 tokens before them in registers (RF - 1 <= 8), so every tap
+// is a register read; the loads of all TS_CPC channels are issued before the first is used.
+// The receptive field is a template parameter (the taps unroll without per-tap tests of rf).
+// Token t is at position pos = t % seq_len of its request; tap i applies when i <= pos.
+// State block of channel c: state[(c*(RF-1) + i)*64 + r] = input of request r, i+1 tokens back.
+constexpr uint32_t TS_CPC = 4;
+template <uint32_t RF>
 __global__ __launch_bounds__(256) void k44_token_shift_prefill_kernel(
     __half *__restrict__ y, const __half *__restrict__ x, const __half *__restrict__ mu,
-    __half *__restrict__ state, uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf,
-    uint32_t seq_len) {
+    __half *__restrict__ state, uint32_t D, uint32_t stride, uint32_t tokens, uint32_t seq_len) {
     const uint32_t chunk = blockIdx.x * 256u + threadIdx.x;
     const uint32_t t0 = chunk * 8u;
     if (t0 >= stride) return;
-    for (uint32_t c = blockIdx.y; c < D; c += gridDim.y) {
-        const __half *xr = x + (uint64_t)c * stride;
-        float m[9];
+    uint32_t pos_k[8];  // request position of each of the 8 tokens
+    {
+        uint32_t pos = t0 % seq_len;
 #pragma unroll
-        for (int i = 0; i < 9; ++i)
-            m[i] = (uint32_t)i < rf ? __half2float(mu[(uint64_t)c * rf + i]) : 0.0f;
-        float w[16];  // w[8 + k] = x[t0 + k], w[k] = x[t0 - 8 + k]
-        {
-            const uint4 cur = *reinterpret_cast<const uint4 *>(xr + t0);
-            const uint4 prv = t0 ? *reinterpret_cast<const uint4 *>(xr + t0 - 8u) : uint4{0, 0, 0, 0};
-            const __half *hc = reinterpret_cast<const __half *>(&cur);
-            const __half *hp = reinterpret_cast<const __half *>(&prv);
+        for (int k = 0; k < 8; ++k) {
+            pos_k[k] = pos;
+            pos = pos + 1u == seq_len ? 0u : pos + 1u;
+        }
+    }
+    // State entries fall in this chunk only near a request's end.
+    bool near_end = false;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) near_end = near_end || pos_k[k] + RF > seq_len;
+    for (uint32_t c0 = blockIdx.y * TS_CPC; c0 < D; c0 += gridDim.y * TS_CPC) {
+        uint4 cur[TS_CPC], prv[TS_CPC];
+        float m[TS_CPC][RF];
+#pragma unroll
+        for (uint32_t j = 0; j < TS_CPC; ++j) {
+            const uint32_t c = c0 + j;
+            cur[j] = prv[j] = uint4{0u, 0u, 0u, 0u};
+            if (c < D) {
+                const __half *xr = x + (uint64_t)c * stride;
+                cur[j] = *reinterpret_cast<const uint4 *>(xr + t0);
+                if (t0) prv[j] = *reinterpret_cast<const uint4 *>(xr + t0 - 8u);
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < RF; ++i)
+                m[j][i] = c < D ? __half2float(mu[(uint64_t)c * RF + i]) : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < TS_CPC; ++j) {
+            const uint32_t c = c0 + j;
+            if (c >= D) break;
+            float w[16];  // w[8 + k] = x[t0 + k], w[k] = x[t0 - 8 + k]
+            const __half *hc = reinterpret_cast<const __half *>(&cur[j]);
+            const __half *hp = reinterpret_cast<const __half *>(&prv[j]);
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 w[8 + k] = __half2float(hc[k]);
                 w[k] = __half2float(hp[k]);
             }
-        }
-        uint4 o;
-        __half *oh = reinterpret_cast<__half *>(&o);
-        uint32_t pos = t0 % seq_len;
+            uint4 o;
+            __half *oh = reinterpret_cast<__half *>(&o);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t t = t0 + (uint32_t)k;
-            float acc = 0.0f;
-            if (t < tokens) {
-                acc = m[0] * w[8 + k];
+            for (int k = 0; k < 8; ++k) {
+                float acc = 0.0f;
+                if (t0 + (uint32_t)k < tokens) {
+                    acc = m[j][0] * w[8 + k];
 #pragma unroll
-                for (int i = 1; i < 9; ++i)  // taps stay in registers: i and k are unrolled
-                    if ((uint32_t)i < rf && (uint32_t)i <= pos) acc = fmaf(m[i], w[8 + k - i], acc);
-                if (state && pos + rf > seq_len) {  // last rf-1 tokens of the request -> state
-                    const uint32_t back = seq_len - 1u - pos;  // 0 = newest
-                    if (back < rf - 1u)
-                        state[((uint64_t)c * (rf - 1u) + back) * 64u + t / seq_len] = xr[t];
+                    for (uint32_t i = 1; i < RF; ++i)
+                        if (i <= pos_k[k]) acc = fmaf(m[j][i], w[8 + k - i], acc);
+                }
+                oh[k] = __float2half_rn(acc);
+            }
+            *reinterpret_cast<uint4 *>(y + (uint64_t)c * stride + t0) = o;
+            if (RF > 1u && state && near_end) {  // last RF-1 tokens of the request -> state
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t t = t0 + (uint32_t)k;
+                    if (t < tokens && pos_k[k] + RF > seq_len) {
+                        const uint32_t back = seq_len - 1u - pos_k[k];  // 0 = newest
+                        state[((uint64_t)c * (RF - 1u) + back) * 64u + t / seq_len] = hc[k];
+                    }
                 }
             }
-            oh[k] = __float2half_rn(acc);
-            pos = pos + 1u == seq_len ? 0u : pos + 1u;
         }
-        *reinterpret_cast<uint4 *>(y + (uint64_t)c * stride + t0) = o;
     }
 }
 
@@ -299,7 +395,22 @@ __global__ __launch_bounds__(256) void k44_argmax_partial_kernel(
     const uint32_t c_begin = blockIdx.y * chunk, c_end = min(V, c_begin + chunk);
     float bv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     uint32_t bi[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
-    for (uint32_t c = c_begin + grp; c < c_end; c += 16u) {
+    // 8 channel rows per thread in flight (the merge rule is order-independent).
+    constexpr uint32_t UNR = 8;
+    uint32_t c = c_begin + grp;
+    for (; c + (UNR - 1u) * 16u < c_end; c += UNR * 16u) {
+        gd_u2 v[UNR];
+#pragma unroll
+        for (uint32_t u = 0; u < UNR; ++u)
+            v[u] = *reinterpret_cast<const gd_u2 *>(x + (uint64_t)(c + u * 16u) * stride + t0);
+#pragma unroll
+        for (uint32_t u = 0; u < UNR; ++u) {
+            const __half *h = reinterpret_cast<const __half *>(&v[u]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) amax_merge(bv[k], bi[k], __half2float(h[k]), c + u * 16u);
+        }
+    }
+    for (; c < c_end; c += 16u) {
         const gd_u2 v = *reinterpret_cast<const gd_u2 *>(x + (uint64_t)c * stride + t0);
         const __half *h = reinterpret_cast<const __half *>(&v);
 #pragma unroll
@@ -379,6 +490,24 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
         sh.tokens = tokens;
         chunks = stride / 8u;
     }
+    // Prefill-sized token counts without a fused shift: the register-resident wide kernel
+    // (32 tokens x all channels per workgroup) when the channels fit 16 per thread.
+    if (!shift && tokens % 32u == 0u && tokens / 32u >= 256u && D <= 16u * 256u) {
+        const dim3 gw(tokens / 32u);
+#define K44_RMSW(C)                                                                            \
+    hipLaunchKernelGGL((k44_rmsnorm_regs_kernel<C>), gw, dim3(1024), 0, stream, y, x, gamma, D, \
+                       stride, eps)
+        const uint32_t cpt = (D + 255u) / 256u;
+        if (cpt <= 4u) {
+            K44_RMSW(4);
+        } else if (cpt <= 8u) {
+            K44_RMSW(8);
+        } else {
+            K44_RMSW(16);
+        }
+#undef K44_RMSW
+        return hipGetLastError();
+    }
     const dim3 grid(chunks, (D + cslice - 1u) / cslice);
 #define K44_RMS(O, R) \
     hipLaunchKernelGGL((k44_rmsnorm_kernel<O, R>), grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice, sh)
@@ -436,9 +565,19 @@ hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __ha
     } else {
         const uint32_t chunks = stride / 8u;
         const uint32_t gx = (chunks + 255u) / 256u;
-        const uint32_t gy = D < 65535u ? D : 65535u;
-        hipLaunchKernelGGL(k44_token_shift_prefill_kernel, dim3(gx, gy), dim3(256), 0, stream, y,
-                           x, mu, state, D, stride, tokens, rf, seq_len);
+        const uint32_t groups = (D + TS_CPC - 1u) / TS_CPC;
+        const uint32_t gy = groups < 65535u ? groups : 65535u;
+        switch (rf) {
+#define K44_TSP(R)                                                                             \
+    case R:                                                                                    \
+        hipLaunchKernelGGL(k44_token_shift_prefill_kernel<R>, dim3(gx, gy), dim3(256), 0,      \
+                           stream, y, x, mu, state, D, stride, tokens, seq_len);               \
+        break;
+            K44_TSP(1) K44_TSP(2) K44_TSP(3) K44_TSP(4) K44_TSP(5) K44_TSP(6) K44_TSP(7)
+            K44_TSP(8) K44_TSP(9)
+#undef K44_TSP
+        default: return hipErrorInvalidValue;
+        }
     }
     return hipGetLastError();
 }
