@@ -159,7 +159,8 @@ struct WaveExec {
 struct MfmaGroupExec {
     std::vector<size_t> members;  // wave indices, plan order
     uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0, max_items = 0;
-    bool dma = false, stream_loads = false, prod = false;
+    bool dma = false, stream_loads = false;
+    uint32_t prod = 0;  // product form (xprod) every member's gathers take
     k44dev::DmaShape dshape;
     size_t part_floats = 0;
     DevBuf<k44dev::MfmaTileArgs> args;
@@ -1477,7 +1478,7 @@ struct K44GpuExecutorState {
                 if (!indep) break;
                 if (g.nt == w.cluster && g.mt == w.mt && g.rows == w.rows_per_stage &&
                     g.dma == w.dma && g.stream_loads == w.stream_loads && g.dshape == w.dshape &&
-                    g.prod == (w.xprod != 0u) && g.members.size() < 64u) {
+                    g.prod == w.xprod && g.members.size() < 64u) {
                     g.members.push_back(op.second);
                     g.part_floats += w.part_floats;
                     joined = true;
@@ -1493,7 +1494,7 @@ struct K44GpuExecutorState {
                 g->dma = w.dma;
                 g->stream_loads = w.stream_loads;
                 g->dshape = w.dshape;
-                g->prod = w.xprod != 0u;
+                g->prod = w.xprod;
                 g->part_floats = w.part_floats;
                 runs.push_back({2, groups.size()});
                 groups.push_back(std::move(g));
@@ -1695,7 +1696,7 @@ struct K44GpuExecutorState {
 
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
                            uint32_t items, uint32_t epi_items, bool dma, const k44dev::DmaShape &ds,
-                           bool prod, uint32_t max_items) {
+                           uint32_t prod, uint32_t max_items) {
         if (mt == 16u)  // narrow (<= 16 tokens)
             K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream, prod, max_items));
         else if (dma)
@@ -1708,7 +1709,7 @@ struct K44GpuExecutorState {
     void launch_mfma(const WaveExec &w) {
         const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, 1u, xcd_order};
         launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
-                          w.dshape, false, w.items);
+                          w.dshape, 0u, w.items);
     }
 
     void launch_group(const MfmaGroupExec &g) {

@@ -186,11 +186,11 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
 // is replaced by its counterpart of s+1 (the weights stream without a gap).  A chunk that
 // covers the whole contraction runs the fused epilogue: waves of up to a few sub-chunks need no
 // split-K partials and no second kernel.
-// PROD: the launch's waves gather element-wise products (a.xprod 2 / 3); without it the
-// product registers are not allocated.
+// PROD: 0, or the product form every wave of the launch gathers (a.xprod 2 / 3: two or three
+// rows multiplied), fixed at compile time.
 // BYY: grid (largest wave's workgroups) x (waves): the wave is blockIdx.y, known without a
 // lookup in the group's prefix sums; workgroups past a wave's own count exit at once.
-template <int NT, bool PROD, bool BYY>
+template <int NT, int PROD, bool BYY>
 __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp) {
     constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16;
     static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
     // Product gathers (a.xprod = 2 / 3) load the same row chunk of two / three tensors and
     // multiply with the rounding of the unfused multiply commands: fp16(A*B), fp16(A*fp16(B*C)).
     constexpr int XQ = NARROW_MAX_ROWS * 2 / 256;
-    const uint32_t xprod = PROD ? a.xprod : 0u;
+    constexpr uint32_t xprod = (uint32_t)PROD;  // every wave of the launch gathers this form
     auto gather = [&](uint32_t s, u4_t (&xv)[XQ], u4_t (&xb)[XQ], u4_t (&xc)[XQ]) {
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
@@ -261,19 +261,20 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
         if (xprod != 0u) {
+            // (as fp16 vectors: element access through pointer casts of the u4 registers would
+            // put them on the stack)
 #pragma unroll
             for (int q = 0; q < XQ; ++q) {
-                __half *ha = reinterpret_cast<__half *>(&xv[q]);
-                const __half *hb = reinterpret_cast<const __half *>(&xb[q]);
-                const __half *hc = reinterpret_cast<const __half *>(&xc[q]);
+                h8_t ha = __builtin_bit_cast(h8_t, xv[q]);
+                const h8_t hb = __builtin_bit_cast(h8_t, xb[q]);
+                const h8_t hc = __builtin_bit_cast(h8_t, xc[q]);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float bc = xprod == 3u
-                                         ? __half2float(__float2half_rn(__half2float(hb[e]) *
-                                                                        __half2float(hc[e])))
-                                         : __half2float(hb[e]);
-                    ha[e] = __float2half_rn(__half2float(ha[e]) * bc);
+                    const float bc = xprod == 3u ? (float)(_Float16)((float)hb[e] * (float)hc[e])
+                                                 : (float)hb[e];
+                    ha[e] = (_Float16)((float)ha[e] * bc);
                 }
+                xv[q] = __builtin_bit_cast(u4_t, ha);
             }
         }
 #pragma unroll
@@ -357,8 +358,9 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
 }
 
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
-                              hipStream_t stream, bool prod, uint32_t max_items) {
-    if (prod && nt != 64u && nt != 128u) return hipErrorInvalidValue;
+                              hipStream_t stream, uint32_t prod, uint32_t max_items) {
+    if (prod != 0u && ((nt != 64u && nt != 128u) || (prod != 2u && prod != 3u)))
+        return hipErrorInvalidValue;
     if (items == 0u) return hipSuccess;
     const dim3 grid(items), block(256);
     // 64/128-neuron tiles: grid (max_items, waves) when it launches at most 1.5x the
@@ -374,17 +376,21 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
     case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, g); break;
     case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, g); break;
     case 64u:
-        if (prod) {
-            K44_NL(64, true)
+        if (prod == 3u) {
+            K44_NL(64, 3)
+        } else if (prod == 2u) {
+            K44_NL(64, 2)
         } else {
-            K44_NL(64, false)
+            K44_NL(64, 0)
         }
         break;
     case 128u:
-        if (prod) {
-            K44_NL(128, true)
+        if (prod == 3u) {
+            K44_NL(128, 3)
+        } else if (prod == 2u) {
+            K44_NL(128, 2)
         } else {
-            K44_NL(128, false)
+            K44_NL(128, 0)
         }
         break;
     default: return hipErrorInvalidValue;
