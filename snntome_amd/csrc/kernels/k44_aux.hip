@@ -4,6 +4,21 @@
 
 namespace k44dev {
 
+// fp16 of an fp32 value, rounded to fp32 first as written: the opaque register move keeps the
+// compiler from fusing the multiply or FMA that produced `v` and the conversion into one
+// mixed-precision FMA (a single rounding) — which it may do at one use of an expression and
+// not at another (a normalised value stored and the same value recomputed for the fused token
+// shift, or a fused and a stand-alone token shift, differed in the last bit).
+__device__ __forceinline__ __half f16_of(float v) {
+    asm volatile("" : "+v"(v));
+    return __float2half_rn(v);
+}
+
+// RMSNorm output fp16(x * inv * gamma), both products in fp32.
+__device__ __forceinline__ __half norm_scale(__half x, float inv, float g) {
+    return f16_of(__half2float(x) * inv * g);
+}
+
 // Workgroup = OCT token octets (8 consecutive tokens = one 16-byte column chunk each) x
 // 256/OCT channel lanes: every lane sums squares down its channel stripe with 8 loads in flight
 // (OCT lanes side by side read 16*OCT contiguous bytes of a channel row), the lanes of an octet
@@ -104,7 +119,7 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
             uint4 o;
             __half *oh = reinterpret_cast<__half *>(&o);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) oh[k] = __float2half_rn(__half2float(h[k]) * inv[k] * go);
+            for (int k = 0; k < 8; ++k) oh[k] = norm_scale(h[k], inv[k], go);
             if (RF == 0u || t0 < sh.tokens)
                 *reinterpret_cast<uint4 *>(y + (uint64_t)c_own * stride + t0) = o;
             if constexpr (RF > 0u) {
@@ -124,7 +139,7 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
 #pragma unroll
                     for (uint32_t i = 1; i < RF; ++i)
                         acc = fmaf(mw[i], __half2float(reinterpret_cast<const __half *>(&sv[i - 1])[k]), acc);
-                    yh[k] = __float2half_rn(acc);
+                    yh[k] = f16_of(acc);
 #pragma unroll
                     for (uint32_t i = RF - 1u; i > 1u; --i)
                         reinterpret_cast<__half *>(&nsv[i - 1])[k] =
@@ -146,7 +161,7 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
         uint4 o;
         __half *oh = reinterpret_cast<__half *>(&o);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) oh[k] = __float2half_rn(__half2float(h[k]) * inv[k] * g);
+        for (int k = 0; k < 8; ++k) oh[k] = norm_scale(h[k], inv[k], g);
         *reinterpret_cast<uint4 *>(y + (uint64_t)c * stride + t0) = o;
     }
 }
@@ -212,7 +227,7 @@ __global__ __launch_bounds__(1024) void k44_rmsnorm_regs_kernel(__half *__restri
         uint4 o;
         __half *oh = reinterpret_cast<__half *>(&o);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) oh[k] = __float2half_rn(__half2float(h[k]) * inv[k] * g);
+        for (int k = 0; k < 8; ++k) oh[k] = norm_scale(h[k], inv[k], g);
         *reinterpret_cast<uint4 *>(y + (uint64_t)c * stride + t0) = o;
     }
 }
@@ -300,7 +315,7 @@ __global__ __launch_bounds__(256) void k44_token_shift_prefill_kernel(
                     for (uint32_t i = 1; i < RF; ++i)
                         if (i <= pos_k[k]) acc = fmaf(m[j][i], w[8 + k - i], acc);
                 }
-                oh[k] = __float2half_rn(acc);
+                oh[k] = f16_of(acc);
             }
             *reinterpret_cast<uint4 *>(y + (uint64_t)c * stride + t0) = o;
             if (RF > 1u && state && near_end) {  // last RF-1 tokens of the request -> state
@@ -345,7 +360,7 @@ __global__ __launch_bounds__(256) void k44_token_shift_decode_kernel(
 #pragma unroll
         for (uint32_t i = RF - 1u; i > 1u; --i) st[(i - 1u) * 64u] = __float2half_rn(prev[i - 2]);
         if (RF > 1u) st[0] = xe;
-        y[e] = __float2half_rn(acc);
+        y[e] = f16_of(acc);
     }
 }
 
