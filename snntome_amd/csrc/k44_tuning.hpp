@@ -26,7 +26,8 @@ enum class Tune : int {
     SortSegments,  // "sort":          0 = segments in index-row order (not address order)
     WeightsInLds,  // "wlds":          0 = 8-token VALU kernel reads weights per batch
     Token64Ring,   // "t64_ring":      0 per-wave Token64 kernel, 1 64-neuron ring kernel
-    XcdOrder,      // "xcd_order":     0 = MFMA tile kernels take items in workgroup order
+    XcdOrder,      // "xcd_order":     0 = MFMA tile kernels take items in workgroup order,
+                   //                  1 = contiguous item ranges per XCD, 2 = per-wave shares
     Count
 };
 

@@ -266,7 +266,7 @@ struct K44GpuExecutorState {
     hipGraphExec_t graph_exec = nullptr;
     bool use_graph = false;
     bool initialized = false;
-    uint32_t xcd_order = 1;  // MFMA tile kernels: contiguous item ranges per XCD
+    uint32_t xcd_order = 2;  // MFMA tile kernels: item order over the XCDs (MfmaGroup)
     std::string report_json;
 
     ~K44GpuExecutorState() { free_all(); }
@@ -1110,7 +1110,10 @@ struct K44GpuExecutorState {
     }
 
     void init(const K44WavePlan &plan) {
-        xcd_order = tune(Tune::XcdOrder) == 0 ? 0u : 1u;
+        {
+            const int xo = tune(Tune::XcdOrder);
+            xcd_order = xo < 0 ? 2u : (uint32_t)std::min(xo, 2);
+        }
         free_all();
         plan_meta.res_map = plan.res_map;
         plan_meta.canvas_elems = plan.canvas_elems;
@@ -1602,7 +1605,14 @@ struct K44GpuExecutorState {
             std::vector<uint32_t> start = {0u};
             uint32_t epi_max = 0, item_max = 0;
             size_t off = 0;
-            for (size_t m : g.members) {
+            // Device order of the members: with per-wave XCD shares, waves with the most stages
+            // per work item first, so that every XCD starts its longest items first.
+            std::vector<size_t> order = g.members;
+            if (xcd_order == 2u && g.mt != 16u)
+                std::stable_sort(order.begin(), order.end(), [&](size_t p, size_t q) {
+                    return item_stages(*waves[p]) > item_stages(*waves[q]);
+                });
+            for (size_t m : order) {
                 const WaveExec &w = *waves[m];
                 args.push_back(mfma_args(w, scratch.p ? scratch.p + off : nullptr, true));
                 off += w.part_floats;
@@ -1613,8 +1623,29 @@ struct K44GpuExecutorState {
             g.items = start.back();
             g.epi_items = epi_max;  // epilogue grid: epi_max x members
             g.max_items = item_max;
+            if (xcd_order == 2u) check_balanced_order(start);
             g.args.upload(args);
             g.start.upload(start);
+        }
+    }
+
+    // Stages (k-steps for the narrow kernels) one work item of an MFMA wave runs.
+    static uint32_t item_stages(const WaveExec &w) {
+        const uint32_t units = w.narrow ? w.ksteps : w.K * w.S / w.rows_per_stage;
+        return (units + w.kgroups - 1u) / w.kgroups;
+    }
+
+    // The per-wave XCD shares must be a bijection of the group's items (every item run by
+    // exactly one workgroup); checked on the host for every group before its first launch.
+    static void check_balanced_order(const std::vector<uint32_t> &start) {
+        const uint32_t n = start.back(), nw = (uint32_t)start.size() - 1u;
+        std::vector<uint8_t> seen(n, 0u);
+        for (uint32_t b = 0; b < n; ++b) {
+            uint32_t w = 0;
+            const uint32_t it = k44dev::balanced_item(b, start.data(), nw, w);
+            if (it >= n || seen[it] || it < start[w] || it >= start[w + 1u])
+                throw std::logic_error("per-wave XCD shares are not a bijection of the items");
+            seen[it] = 1u;
         }
     }
 

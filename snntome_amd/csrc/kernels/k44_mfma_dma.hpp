@@ -119,9 +119,8 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
     __shared__ __attribute__((aligned(16))) uint32_t wl[NBUF][WBYTES / 4];
     static_assert(sizeof(xl) >= 8 * EPI_WAVE_FLOATS * sizeof(float), "epilogue LDS regions");
 
-    const uint32_t item = group_item(grp);
-    uint32_t w = 0;
-    while (w + 1u < grp.n && item >= grp.start[w + 1u]) ++w;
+    uint32_t w;
+    const uint32_t item = group_item_wave(grp, w);
     const MfmaTileArgs a = grp.waves[w];
     const uint32_t local = item - grp.start[w];
     const uint32_t tile = local % a.tiles, rest = local / a.tiles;

@@ -96,19 +96,50 @@ struct MfmaGroup {
     const MfmaTileArgs *waves;  // [n]
     const uint32_t *start;      // [n+1] prefix sums of tiles * ttiles * kgroups
     uint32_t n;
-    uint32_t xcd_order;         // 1: contiguous item ranges per XCD (group_item)
+    uint32_t xcd_order;         // 0 plain, 1 contiguous per XCD, 2 per-wave shares (group_item_wave)
 };
 
-// Work item of this workgroup.  Workgroups are handed to the 8 XCDs round-robin (workgroup b
-// runs on XCD b % 8), each XCD with its own L2.  With xcd_order, XCD x runs the contiguous item
-// range [x*q + min(x, r), ...) (n = 8q + r items, a bijection of [0, n)): consecutive tiles of
-// one token tile, whose gathers read the token tile's input rows, share that XCD's L2 instead of
-// every XCD fetching every token tile.
-__device__ __forceinline__ uint32_t group_item(const MfmaGroup &g) {
+// Per-wave shares of the 8 XCDs (xcd_order 2), host and device.  Workgroup b runs on XCD
+// x = b % 8 as that XCD's s-th workgroup, s = b / 8.  Every wave w of the group (items
+// [start[w], start[w+1]), cnt = 8q + r) gives each XCD a contiguous share of its items: q, plus
+// one of the r leftover items for r XCDs taken cyclically where the previous wave's leftovers
+// stopped (so every XCD gets exactly as many items as workgroups).  XCD x runs its shares in
+// wave order, so waves placed first (the host sorts a group's waves by stages per item,
+// descending) start first on every XCD.  Returns the item and sets w; a bijection of [0, n).
+__host__ __device__ __forceinline__ uint32_t balanced_item(uint32_t b, const uint32_t *start,
+                                                           uint32_t nw, uint32_t &w) {
+    const uint32_t x = b & 7u;
+    uint32_t s = b >> 3, off = 0;
+    for (w = 0; w + 1u < nw; ++w) {
+        const uint32_t cnt = start[w + 1u] - start[w], q = cnt >> 3, r = cnt & 7u;
+        const uint32_t here = q + (((x - off) & 7u) < r ? 1u : 0u);
+        if (s < here) break;
+        s -= here;
+        off = (off + r) & 7u;
+    }
+    const uint32_t cnt = start[w + 1u] - start[w], q = cnt >> 3, r = cnt & 7u;
+    const uint32_t ring = ((1u << r) - 1u) << off;
+    const uint32_t extra = (ring | (ring >> 8)) & 0xffu & ((1u << x) - 1u);  // XCDs y < x
+    return start[w] + x * q + (uint32_t)__builtin_popcount(extra) + s;
+}
+
+// Work item of this workgroup and its wave.  Workgroups are handed to the 8 XCDs round-robin
+// (workgroup b runs on XCD b % 8), each XCD with its own L2.  xcd_order 1: XCD x runs the
+// contiguous item range [x*q + min(x, r), ...) (n = 8q + r items): consecutive tiles of one
+// token tile, whose gathers read the token tile's input rows, share that XCD's L2 instead of
+// every XCD fetching every token tile.  xcd_order 2: per-wave shares (balanced_item), which keep
+// that locality and also spread long and short waves evenly over the XCDs.
+__device__ __forceinline__ uint32_t group_item_wave(const MfmaGroup &g, uint32_t &w) {
     const uint32_t b = blockIdx.x;
-    if (!g.xcd_order) return b;
-    const uint32_t n = gridDim.x, x = b & 7u, s = b >> 3, q = n >> 3, r = n & 7u;
-    return x * q + min(x, r) + s;
+    if (g.xcd_order == 2u) return balanced_item(b, g.start, g.n, w);
+    uint32_t item = b;
+    if (g.xcd_order) {
+        const uint32_t n = gridDim.x, x = b & 7u, s = b >> 3, q = n >> 3, r = n & 7u;
+        item = x * q + min(x, r) + s;
+    }
+    w = 0;
+    while (w + 1u < g.n && item >= g.start[w + 1u]) ++w;
+    return item;
 }
 
 // Epilogue of a 64-token-per-wave MFMA tile: lane holds C[4g + i][lane & 15] of every 16x16
@@ -248,9 +279,8 @@ __device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a,
 
 template <int NT, int MT, int ROWS>
 __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
-    const uint32_t item = group_item(grp);
-    uint32_t w = 0;
-    while (w + 1u < grp.n && item >= grp.start[w + 1u]) ++w;
+    uint32_t w;
+    const uint32_t item = group_item_wave(grp, w);
     const MfmaTileArgs a = grp.waves[w];
     const uint32_t local = item - grp.start[w];
     const uint32_t tile = local % a.tiles, rest = local / a.tiles;

@@ -286,16 +286,17 @@ def test_dma_ring_nt128_matches_register_staged(wavec, orc, tuning, S, K, tiles,
 @pytest.mark.parametrize("nt,tokens,tiles", [(64, 512, 13), (32, 1024, 7), (64, 192, 5),
                                              (128, 512, 3), (16, 256, 9)])
 def test_xcd_item_order_bit_identical(wavec, orc, tuning, nt, tokens, tiles):
-    """Work items taken as contiguous ranges per XCD (xcd_order, the default) or in plain
-    workgroup order are the same items: bit-identical outputs, within tolerance of the oracle;
-    item counts that are not multiples of 8 included (LDS-ring and register-staged kernels)."""
+    """Work items taken as per-wave shares of the XCDs (xcd_order 2, the default), contiguous
+    ranges per XCD (1) or in plain workgroup order (0) are the same items: bit-identical outputs,
+    within tolerance of the oracle; item counts that are not multiples of 8 included (LDS-ring
+    and register-staged kernels)."""
     rng = np.random.default_rng(nt * 31 + tiles)
     C, K, S = 8192, 2, 64
     starts = (rng.integers(0, (C - S) // 8, size=(tiles, K)) * 8).astype(np.uint32)
     w = synth.normal_f16(rng, (tiles * nt, K * S), 0.05)
     b = synth.normal_f16(rng, (tiles * nt,), 0.05)
     out = {}
-    for order in (1, 0):
+    for order in (2, 1, 0):
         tuning("xcd_order", order)
         y, ref, plan = run_sparse_case(wavec, orc, C=C, tokens=tokens,
                                        rows=cluster_rows(starts, S), weights=w, bias=b,
@@ -304,3 +305,51 @@ def test_xcd_item_order_bit_identical(wavec, orc, tuning, nt, tokens, tiles):
         assert orc.rel_err(y, ref) <= TOL
         out[order] = y
     assert np.array_equal(out[0], out[1])
+    assert np.array_equal(out[0], out[2])
+
+
+@pytest.mark.parametrize("n_cl,K,cout,tokens", [(4, 2, 1000, 1024), (7, 3, 700, 512),
+                                                (5, 2, 333, 1536)])
+def test_group_item_orders_pruned_bit_identical(wavec, orc, tuning, n_cl, K, cout, tokens):
+    """A pruned projection compiles to sub-waves of different stage counts (full-pattern tiles,
+    union tiles) launched as one group; per-wave XCD shares with the longest waves first
+    (xcd_order 2), contiguous ranges (1) and plain order (0) run the same items: bit-identical,
+    and the per-neuron fp64 oracle agrees."""
+    rng = np.random.default_rng(n_cl * 13 + cout)
+    S = 256
+    C = n_cl * S
+    pick = np.argsort(rng.random((cout, n_cl)), axis=1)[:, :K]
+    starts = (pick * S).astype(np.uint32)
+    w = synth.normal_f16(rng, (cout, K * S), 0.05)
+    b = synth.normal_f16(rng, (cout,), 0.05)
+    out = {}
+    for order in (2, 1, 0):
+        tuning("xcd_order", order)
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("x", C, 1, tokens, is_1d=True)
+        g.add_pruned_wave("p", "x", "y", starts, S, w, b, tile=64, act="silu")
+        plan = g.compile()
+        plan.init_gpu()
+        rep = plan.exec_report()
+        parts = rep["waves"]
+        assert {r["path"] for r in parts} <= {"mfma_dma", "mfma_tile"}
+        assert len({r["K"] for r in parts}) >= 2, "expected sub-waves of several lengths"
+        assert len(rep["groups"]) == 1 and len(rep["groups"][0]) == len(parts)
+        plan.fill_input_uniform(11)
+        plan.execute(1)
+        st = stride_of(tokens)
+        canvas = plan.read_canvas(0, int(plan.summary["canvas_elems"]))
+        y0 = int(plan.cmds[0]["y_off"])
+        y = canvas[y0:y0 + cout * st].view(np.float16).reshape(cout, st)
+        if order == 2:
+            x0 = int(plan.cmds[0]["src_off"])
+            seg = (x0 + starts.astype(np.uint64) * st).ravel()
+            ref = orc.wave_f64(canvas, seg, w, b, None, K, S, 1, st, st, st, "silu")
+            err = orc.rel_err(y.astype(np.float64), ref)
+            _log(f"[pruned orders {n_cl}/{K} cout={cout} tokens={tokens}] parts "
+                 f"{[(r['path'], r['cout'], r['K']) for r in parts]} rel err {err:.3e}")
+            assert err <= TOL
+        out[order] = y.copy()
+        plan.release_gpu()
+    assert np.array_equal(out[2], out[1])
+    assert np.array_equal(out[2], out[0])
