@@ -253,7 +253,9 @@ int wavec_gpu_read_canvas_2d(void *handle, unsigned long long elem_off, unsigned
  *   "group" 0 no group launches; "group_split" 0 groups keep their members' split-K;
  *   "fuse" 0 no folded multiplies or RMSNorm + token-shift kernels; "sort" 0 segments in
  *   index-row order; "wlds" 0 VALU weights read per batch; "t64_ring" 0 | 1 Token64 kernel;
- *   "xcd_order" 0 MFMA tile kernels take work items in plain workgroup order.
+ *   "xcd_order" 0 | 1 | 2 MFMA tile kernels take work items in plain workgroup order, as
+ *   contiguous ranges per XCD, or as per-wave shares of every XCD, longest waves first (the
+ *   automatic choice).
  * wavec_set_tuning returns -1 for an unknown key or a value < -1; wavec_get_tuning returns the
  * value or -2 for an unknown key. */
 int wavec_set_tuning(const char *key, int value);
