@@ -206,6 +206,10 @@ struct AuxExec {
     bool fused = false;  // SWIGLU_MUL_1D folded into its consumers' gathers, or TOKEN_SHIFT_1D
                          // run by the RMSNorm before it (not launched)
     size_t shift_with = SIZE_MAX;  // RMSNORM_1D: the decode token shift it runs (whole plans)
+    // SWIGLU_MUL_1D y = other * q where q = b * c is an inner multiply only this one reads:
+    // whole plans run both as y = fp16(other * fp16(b * c)) (the inner one is not launched).
+    size_t chain_inner = SIZE_MAX;
+    uint64_t chain_other = 0;
     std::string fuse_note;         // SWIGLU_MUL_1D: why it was or was not folded (report)
     float eps = 1e-5f;
     DevBuf<__half> table;  // gamma (RMSNORM), mix (TOKEN_SHIFT), embedding table (EMBED)
@@ -1065,8 +1069,14 @@ struct K44GpuExecutorState {
             }
             break;
         case K44CmdType::SWIGLU_MUL_1D:
-            K44_HIP(k44dev::launch_mul(cv + a.y_off, cv + a.src_off, cv + a.src2_off,
-                                       (uint64_t)a.D * a.stride, stream));
+            if (whole && a.chain_inner != SIZE_MAX) {
+                const AuxExec &in = *aux[a.chain_inner];
+                K44_HIP(k44dev::launch_mul3(cv + a.y_off, cv + a.chain_other, cv + in.src_off,
+                                            cv + in.src2_off, (uint64_t)a.D * a.stride, stream));
+            } else {
+                K44_HIP(k44dev::launch_mul(cv + a.y_off, cv + a.src_off, cv + a.src2_off,
+                                           (uint64_t)a.D * a.stride, stream));
+            }
             break;
         case K44CmdType::TOKEN_SHIFT_1D:
             K44_HIP(k44dev::launch_token_shift(cv + a.y_off, cv + a.src_off, a.table.p,
@@ -1144,6 +1154,7 @@ struct K44GpuExecutorState {
             }
         }
         fuse_products();
+        fuse_mul_chains();
         fuse_norm_shifts();
         form_runs();
         K44_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
@@ -1405,6 +1416,86 @@ struct K44GpuExecutorState {
                 w.rd_run = merge_ranges(std::move(fr));
                 w.why += nleaf == 3 ? "; gathers fp16(a*fp16(b*c)) (two multiplies folded)"
                                     : "; gathers fp16(a*b) (multiply folded)";
+            }
+        }
+    }
+
+    // Chains of element-wise multiplies left after fuse_products (prefill: m = q*(k*v) whose
+    // readers are wide MFMA waves): an inner multiply whose product only the outer one reads is
+    // not launched; the outer one computes fp16(other * fp16(b * c)) from the inner one's
+    // operands in one pass (bit-identical, one launch and one tensor round trip fewer).
+    // Conditions, from the canvas ranges in plan order: the inner operands stay intact from the
+    // inner multiply through the outer one, and the output is either disjoint from each operand
+    // or exactly one of them (then every element is read before it is written, by one thread).
+    // Whole-plan execution only; tuning switch fuse=0 disables it.
+    void fuse_mul_chains() {
+        if (tune(Tune::Fuse) == 0) return;
+        const size_t n = ops.size();
+        std::vector<Ranges> rd(n), wr(n);
+        for (size_t i = 0; i < n; ++i) {
+            if (ops[i].first) {
+                rd[i] = waves[ops[i].second]->rd_run;
+                wr[i] = waves[ops[i].second]->wr_run;
+            } else if (!aux[ops[i].second]->fused) {
+                aux_ranges(*aux[ops[i].second], rd[i], wr[i]);
+            }
+        }
+        Ranges out_rng = {{0u, UINT64_MAX}};
+        {
+            auto it = plan_meta.res_map.find(plan_meta.output_res_key);
+            if (it != plan_meta.res_map.end())
+                out_rng = {{plan_meta.output_off,
+                            plan_meta.output_off +
+                                (uint64_t)plan_meta.output_c * it->second.channel_stride}};
+        }
+        typedef std::pair<uint64_t, uint64_t> Rng;
+        auto is_mul = [&](size_t i) {
+            return !ops[i].first && aux[ops[i].second]->type == K44CmdType::SWIGLU_MUL_1D &&
+                   !aux[ops[i].second]->fused && aux[ops[i].second]->chain_inner == SIZE_MAX;
+        };
+        auto rng = [&](size_t i, int k) {
+            const AuxExec &a = *aux[ops[i].second];
+            const uint64_t o = k == 0 ? a.src_off : k == 1 ? a.src2_off : a.y_off;
+            return Rng(o, o + (uint64_t)a.D * a.stride);
+        };
+        for (size_t i = 0; i < n; ++i) {
+            if (!is_mul(i)) continue;
+            AuxExec &outer = *aux[ops[i].second];
+            const Rng R = rng(i, 2);
+            for (int k = 0; k < 2; ++k) {
+                const Rng Q = rng(i, k);
+                size_t p = n;
+                for (size_t j = i; j-- > 0;)
+                    if (ranges_overlap(wr[j], Ranges{Q})) {
+                        p = j;
+                        break;
+                    }
+                if (p == n || !is_mul(p) || rng(p, 2) != Q) continue;
+                const AuxExec &in = *aux[ops[p].second];
+                if (in.D != outer.D || in.stride != outer.stride) continue;
+                // the product q: read by the outer multiply only until overwritten, and not the
+                // plan output if nothing overwrites it
+                bool ok = true, overwritten = false;
+                for (size_t j = p + 1; j < n && ok && !overwritten; ++j) {
+                    if (j != i && ranges_overlap(rd[j], Ranges{Q})) ok = false;
+                    overwritten = ranges_overlap(wr[j], Ranges{Q});
+                }
+                ok = ok && (overwritten || !ranges_overlap(Ranges{Q}, out_rng));
+                const Rng A = rng(i, 1 - k), B = rng(p, 0), C = rng(p, 1);
+                for (size_t j = p + 1; j < i && ok; ++j)
+                    ok = !ranges_overlap(wr[j], Ranges{B}) && !ranges_overlap(wr[j], Ranges{C});
+                for (const Rng &X : {A, B, C})
+                    ok = ok && (X == R || !ranges_overlap(Ranges{X}, Ranges{R}));
+                if (!ok) continue;
+                aux[ops[p].second]->fused = true;
+                aux[ops[p].second]->fuse_note = "run by the multiply that reads it (3-operand kernel)";
+                outer.chain_inner = ops[p].second;
+                outer.chain_other = A.first;
+                outer.fuse_note = "runs the inner multiply it reads (3-operand kernel)";
+                rd[p].clear();
+                wr[p].clear();
+                rd[i] = merge_ranges({A, B, C});
+                break;
             }
         }
     }
@@ -1694,6 +1785,12 @@ struct K44GpuExecutorState {
               << cmd_type_str(aux[i]->type) << "\", \"channels\": " << aux[i]->D
               << ", \"fused\": " << (aux[i]->fused ? "true" : "false")
               << ", \"fuse_note\": \"" << aux[i]->fuse_note << "\""
+              << ", \"chain\": " << (aux[i]->chain_inner != SIZE_MAX ? "true" : "false")
+              << ", \"operands\": ["
+              << (aux[i]->chain_inner != SIZE_MAX ? aux[i]->chain_other : aux[i]->src_off) << ", "
+              << (aux[i]->chain_inner != SIZE_MAX ? aux[aux[i]->chain_inner]->src_off : aux[i]->src2_off)
+              << ", "
+              << (aux[i]->chain_inner != SIZE_MAX ? aux[aux[i]->chain_inner]->src2_off : 0u) << "]"
               << ", \"tokens\": " << aux[i]->tokens << "}";
         o << "], \"groups\": [";
         for (size_t i = 0; i < groups.size(); ++i) {

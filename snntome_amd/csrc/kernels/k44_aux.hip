@@ -249,6 +249,31 @@ __global__ __launch_bounds__(256) void k44_mul_kernel(__half *__restrict__ y,
     }
 }
 
+// m = a * (b * c) with the two commands' roundings: fp16(a * fp16(b * c)).  Products of two
+// fp16 values are exact in fp32, so each rounding is the one multiply command's.  No restrict:
+// the output may be one of the operands (same element, same thread).
+__global__ __launch_bounds__(256) void k44_mul3_kernel(__half *y, const __half *a,
+                                                       const __half *b, const __half *c,
+                                                       uint64_t n8) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n8;
+         i += (uint64_t)gridDim.x * 256u) {
+        const uint4 va = reinterpret_cast<const uint4 *>(a)[i];
+        const uint4 vb = reinterpret_cast<const uint4 *>(b)[i];
+        const uint4 vc = reinterpret_cast<const uint4 *>(c)[i];
+        const __half *ha = reinterpret_cast<const __half *>(&va);
+        const __half *hb = reinterpret_cast<const __half *>(&vb);
+        const __half *hc = reinterpret_cast<const __half *>(&vc);
+        uint4 o;
+        __half *ho = reinterpret_cast<__half *>(&o);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const __half bc = __float2half_rn(__half2float(hb[k]) * __half2float(hc[k]));
+            ho[k] = __float2half_rn(__half2float(ha[k]) * __half2float(bc));
+        }
+        reinterpret_cast<uint4 *>(y)[i] = o;
+    }
+}
+
 // Prefill: thread = (TS_CPC channels c0 + j, c0 = (blockIdx.y + k*gridDim.y) * TS_CPC, 8
 // consecutive tokens), with the 8 tokens before them in registers (RF - 1 <= 8), so every tap
 // is a register read; the loads of all TS_CPC channels are issued before the first is used.
@@ -554,6 +579,14 @@ hipError_t launch_mul(__half *y, const __half *a, const __half *b, uint64_t n,
                       hipStream_t stream) {
     if (n % 8u != 0u) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k44_mul_kernel, dim3(grid_for(n / 8u)), dim3(256), 0, stream, y, a, b,
+                       n / 8u);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul3(__half *y, const __half *a, const __half *b, const __half *c, uint64_t n,
+                       hipStream_t stream) {
+    if (n % 8u != 0u) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k44_mul3_kernel, dim3(grid_for(n / 8u)), dim3(256), 0, stream, y, a, b, c,
                        n / 8u);
     return hipGetLastError();
 }

@@ -33,6 +33,10 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
                           const RmsShift *shift = nullptr);
 hipError_t launch_mul(__half *y, const __half *a, const __half *b, uint64_t n,
                       hipStream_t stream);
+// y = fp16(a * fp16(b * c)) element-wise (a chain of two multiplies in one pass); y may be
+// a, b or c exactly (each element is read before it is written, by the same thread).
+hipError_t launch_mul3(__half *y, const __half *a, const __half *b, const __half *c, uint64_t n,
+                       hipStream_t stream);
 hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __half *state,
                               uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf,
                               uint32_t seq_len, int decode, hipStream_t stream);

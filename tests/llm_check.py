@@ -16,7 +16,9 @@ inputs the device itself read:
 Token columns: `windows` — (first column, count) ranges of the plan's token axis; the full
 check of a 16 x 512-token prefill samples three 64-token windows (the first request's start, a
 request boundary, the last tokens).  Waves whose gather multiplies operands (folded multiplies,
-run mode) are checked on the oracle's product of the operand tensors the device read.
+run mode) are checked on the oracle's product of the operand tensors the device read, and a
+multiply that runs its inner multiply (run mode: a * (b * c) in one kernel) on the oracle's
+chain of the three operands it read.
 """
 from typing import Dict, List, Optional, Sequence, Tuple
 
@@ -121,8 +123,12 @@ class PlanChecker:
                 # a shift fused into its norm reads the norm's output, read after the step
                 state[i] = (None if self._shift_fused(i, fused) else self.full(c["src_off"], c["Cin"]), st)
             elif t == "SWIGLU_MUL_1D":
-                state[i] = (self.rows(c["src_off"], c["logical_Cout"]),
-                            self.rows(c["src2_off"], c["logical_Cout"]))
+                if fused and self.aux_rep[i]["chain"]:  # runs its inner multiply: a * (b * c)
+                    state[i] = tuple(self.rows(o, c["logical_Cout"])
+                                     for o in self.aux_rep[i]["operands"])
+                else:
+                    state[i] = (self.rows(c["src_off"], c["logical_Cout"]),
+                                self.rows(c["src2_off"], c["logical_Cout"]))
             elif t == "ARGMAX_1D":
                 state[i] = self.rows(c["src_off"], c["Cin"])
 
@@ -167,9 +173,14 @@ class PlanChecker:
             elif t == "SWIGLU_MUL_1D":
                 if fused and self.aux_rep[i]["fused"]:
                     continue  # folded: checked through its readers' inputs
-                a, b = state[i]
                 y = self.rows(c["y_off"], c["logical_Cout"])
-                assert np.array_equal(y.view(np.uint16), lo.mul(a, b).view(np.uint16)), what
+                if len(state[i]) == 3:
+                    a, b, c3 = state[i]
+                    want = lo.mul(a, lo.mul(b, c3))
+                else:
+                    a, b = state[i]
+                    want = lo.mul(a, b)
+                assert np.array_equal(y.view(np.uint16), want.view(np.uint16)), what
                 self.checked[t] = self.checked.get(t, 0) + 1
             elif t == "EMBED_1D":
                 y = self.rows(c["y_off"], c["logical_Cout"])

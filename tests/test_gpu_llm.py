@@ -438,6 +438,35 @@ def test_folded_multiplies_match_unfolded(wavec, tuning):
     assert np.array_equal(out["folded"][1], out["launched"][1])
 
 
+def test_prefill_multiply_chain_matches_launched(wavec, tuning):
+    """Prefill plans run m = q*(k*v) as one 3-operand multiply (the inner product k*v is not
+    launched); logits and next ids are bit-identical to the plan that launches both multiplies
+    (tuning switch fuse=0)."""
+    wts = synth.llm_weights(TINY)
+    ids = np.random.default_rng(23).integers(0, TINY.vocab, TINY.requests * TINY.prompt)
+    ids = ids.astype(np.uint32)
+    out = {}
+    for mode in ("chained", "launched"):
+        tuning("fuse", -1 if mode == "chained" else 0)
+        p = synth.build_llm_graph(TINY, wts, decode=False, wavec_mod=wavec).compile()
+        p.init_gpu()
+        rep = p.exec_report()
+        chains = [a for a in rep["aux"] if a["chain"]]
+        inner = [a for a in rep["aux"] if a["fused"] and a["type"] == "SWIGLU_MUL_1D"]
+        _log(f"[prefill chain {mode}] {len(chains)} chained multiplies, {len(inner)} not "
+             f"launched, {rep['launches_per_run']} launches per run")
+        assert (len(chains), len(inner)) == ((TINY.layers, TINY.layers) if mode == "chained"
+                                             else (0, 0))
+        p.set_ids(ids)
+        p.execute(1)
+        head = next(c for c in p.cmds if c["name"].split("/")[0] == "head")
+        T = stride_of(ids.size)
+        out[mode] = (p.get_ids(ids.size), _read(p, head["y_off"], head["logical_Cout"], T))
+        p.release_gpu()
+    assert np.array_equal(out["chained"][0], out["launched"][0])
+    assert np.array_equal(out["chained"][1].view(np.uint16), out["launched"][1].view(np.uint16))
+
+
 def test_decode_step_full_width_against_oracle(wavec):
     """One decode step of the config-5 decoder at its real widths (d 2048, FFN 5632, vocab
     32,000, 16 requests; 2 of the 16 layers, zero token-shift history): folded multiplies,
