@@ -1060,7 +1060,8 @@ struct K44GpuExecutorState {
             if (whole && a.shift_with != SIZE_MAX) {
                 const AuxExec &t = *aux[a.shift_with];
                 const k44dev::RmsShift sh{cv + t.y_off, t.table.p,
-                                          t.has_state ? cv + t.state_off : nullptr, t.rf, 0u};
+                                          t.has_state ? cv + t.state_off : nullptr, t.rf, 0u,
+                                          t.decode ? 0u : t.seq_len};
                 K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
                                                a.stride, a.tokens, a.eps, stream, &sh));
             } else {
@@ -1500,10 +1501,12 @@ struct K44GpuExecutorState {
         }
     }
 
-    // A decode RMSNorm followed directly by the decode token shift of its output runs the shift
-    // in the same kernel (whole-plan execution; bit-identical to the two commands): the norm's
+    // An RMSNorm followed directly by the token shift of its output runs the shift in the same
+    // kernel (whole-plan execution; bit-identical to the two commands).  Decode: the norm's
     // decode form keeps one channel per thread, so the shift of that channel's tokens follows
-    // in place.  Tuning switch fuse=0 keeps both launches.
+    // in place.  Prefill (the register-resident 32-token form): each workgroup also normalizes
+    // the 8 tokens before its block and shifts its own tokens (k44_rmsnorm_shift_prefill_kernel).
+    // Tuning switch fuse=0 keeps both launches.
     void fuse_norm_shifts() {
         if (tune(Tune::Fuse) == 0) return;
         for (size_t i = 0; i + 1u < ops.size(); ++i) {
@@ -1511,16 +1514,22 @@ struct K44GpuExecutorState {
             AuxExec &N = *aux[ops[i].second];
             AuxExec &T = *aux[ops[i + 1u].second];
             if (N.type != K44CmdType::RMSNORM_1D || T.type != K44CmdType::TOKEN_SHIFT_1D ||
-                N.fused || T.fused || !T.decode || T.src_off != N.y_off || T.D != N.D ||
-                T.stride != N.stride || T.tokens != N.tokens || N.stride != 64u ||
-                N.tokens == 0u || N.tokens > 64u || T.rf == 0u || T.rf > 9u ||
-                (T.rf > 1u && !T.has_state))
+                N.fused || T.fused || T.src_off != N.y_off || T.D != N.D ||
+                T.stride != N.stride || T.tokens != N.tokens || T.rf == 0u || T.rf > 9u)
                 continue;
-            // The launcher's decode geometry must give one channel per thread.
-            const uint32_t chunks = (N.tokens + 7u) / 8u;
-            uint32_t slices = (256u + chunks - 1u) / chunks;
-            slices = std::min(slices, (N.D + 255u) / 256u);
-            if ((N.D + slices - 1u) / slices > 256u) continue;
+            if (T.decode) {
+                if (N.stride != 64u || N.tokens == 0u || N.tokens > 64u ||
+                    (T.rf > 1u && !T.has_state))
+                    continue;
+                // The launcher's decode geometry must give one channel per thread.
+                const uint32_t chunks = (N.tokens + 7u) / 8u;
+                uint32_t slices = (256u + chunks - 1u) / chunks;
+                slices = std::min(slices, (N.D + 255u) / 256u);
+                if ((N.D + slices - 1u) / slices > 256u) continue;
+            } else if (!k44dev::rmsnorm_shift_prefill_ok(N.D, N.stride, N.tokens, T.rf,
+                                                         T.seq_len)) {
+                continue;
+            }
             // Every workgroup of the fused kernel reads all D rows of the norm's input for its
             // sums while other workgroups already store shift outputs and state: the canvas
             // allocator may have given the input's range (dead after the norm) to the shift's
@@ -1529,6 +1538,9 @@ struct K44GpuExecutorState {
             aux_ranges(N, rd_n, wr_n);
             aux_ranges(T, rd_t, wr_t);
             if (ranges_overlap(wr_t, rd_n)) continue;
+            // The prefill form also reads the 8 tokens before each workgroup's block: the norm
+            // must not write over its own input either.
+            if (!T.decode && ranges_overlap(wr_n, rd_n)) continue;
             N.shift_with = ops[i + 1u].second;
             T.fused = true;
         }

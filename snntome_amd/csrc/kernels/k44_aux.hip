@@ -232,6 +232,159 @@ __global__ __launch_bounds__(1024) void k44_rmsnorm_regs_kernel(__half *__restri
     }
 }
 
+// Prefill RMSNorm with the token shift of its output fused (k44_rmsnorm_regs_kernel followed by
+// k44_token_shift_prefill_kernel, the same operations in the same order, so the same values).
+// The workgroup of 32 tokens also sums the squares of the 8 tokens before its block, reduced in
+// the order of the workgroup that owns them (same channels per thread, same shuffle tree, waves
+// in order), so their norms are that workgroup's; the shift of octets 1..3 takes the previous
+// octet's normalized values from the neighbouring lane (thread = 4 * channel lane + octet),
+// octet 0 from those 8 tokens.  Writes the norm output y, the shift output y2 and the state
+// block (each request's last RF-1 normalized tokens).  Token t of the block is at request
+// position t % seq_len; tap i applies when i <= that position.
+template <int CPT, uint32_t RF>
+__global__ __launch_bounds__(1024) void k44_rmsnorm_shift_prefill_kernel(
+    __half *__restrict__ y, const __half *__restrict__ x, const __half *__restrict__ gamma,
+    uint32_t D, uint32_t stride, float eps, __half *__restrict__ y2,
+    const __half *__restrict__ mu, __half *__restrict__ state, uint32_t seq_len) {
+    constexpr uint32_t OCT = 4u, CL = 256u;
+    // tokens before the block the taps reach: RF - 1, rounded up to a 4-token (8-byte) load
+    static_assert(RF >= 1u && RF <= 5u, "the registers hold the 4 tokens before the block");
+    constexpr uint32_t HK = RF <= 1u ? 0u : 4u;
+    constexpr uint32_t HS = HK ? HK : 1u;
+    __shared__ float part[16][OCT * 8 + HS];
+    __shared__ float inv_s[OCT * 8 + HS];
+    __shared__ __half mus[2048u * RF], gms[2048u];  // mixing weights and gamma (D <= 2048)
+    const uint32_t oct = threadIdx.x % OCT, lane_c = threadIdx.x / OCT;
+    const uint32_t t0 = (blockIdx.x * OCT + oct) * 8u;
+    const bool halo = HK && oct == 0u && t0 >= 8u;
+    uint4 v[CPT];
+    uint32_t hv[CPT][HS / 2];  // the HK tokens before t0 (octet 0 lanes)
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const uint32_t c = lane_c + (uint32_t)u * CL;
+        const __half *xr = x + (uint64_t)c * stride;
+        v[u] = c < D ? *reinterpret_cast<const uint4 *>(xr + t0) : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (uint32_t j = 0; j < HS / 2; ++j) hv[u][j] = 0u;
+        if constexpr (HK == 4u) {
+            if (halo && c < D) {
+                const uint2 hx = *reinterpret_cast<const uint2 *>(xr + t0 - 4u);
+                hv[u][0] = hx.x;
+                hv[u][1] = hx.y;
+            }
+        }
+    }
+    // the channels' mixing weights and gamma, staged in LDS (visible after the barrier below)
+    for (uint32_t e = threadIdx.x; e < D * RF; e += 1024u) mus[e] = mu[e];
+    for (uint32_t e = threadIdx.x; e < D; e += 1024u) gms[e] = gamma ? gamma[e] : __float2half(1.0f);
+    float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0}, sh[HS];
+#pragma unroll
+    for (uint32_t k = 0; k < HS; ++k) sh[k] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const __half *h = reinterpret_cast<const __half *>(&v[u]);
+        const __half *hh = reinterpret_cast<const __half *>(&hv[u][0]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float f = __half2float(h[k]);
+            ss[k] = fmaf(f, f, ss[k]);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < HK; ++k) {
+            const float fh = __half2float(hh[k]);
+            sh[k] = fmaf(fh, fh, sh[k]);
+        }
+    }
+#pragma unroll
+    for (uint32_t m = OCT; m < 64u; m <<= 1) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss[k] += __shfl_xor(ss[k], (int)m, 64);
+#pragma unroll
+        for (uint32_t k = 0; k < HK; ++k) sh[k] += __shfl_xor(sh[k], (int)m, 64);
+    }
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if (lane < OCT) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) part[wave][lane * 8u + k] = ss[k];
+    }
+    if (HK && lane == 0u) {
+#pragma unroll
+        for (uint32_t k = 0; k < HK; ++k) part[wave][OCT * 8u + k] = sh[k];
+    }
+    __syncthreads();
+    if (threadIdx.x < OCT * 8u + HK) {  // one total per token (block octets, then those before)
+        float t = part[0][threadIdx.x];
+        for (int w = 1; w < 16; ++w) t += part[w][threadIdx.x];
+        inv_s[threadIdx.x] = rsqrtf(t / (float)D + eps);
+    }
+    __syncthreads();
+    // requests are multiples of 8 tokens: an octet lies in one request, positions pos0 + k
+    const uint32_t pos0 = t0 % seq_len;
+    const bool near_end = pos0 + 7u + RF > seq_len;
+    const int src_lane = (int)((lane + 63u) & 63u);  // octet - 1, same channel lane
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const uint32_t c = lane_c + (uint32_t)u * CL;
+        const bool live = c < D;
+        const float g = live ? __half2float(gms[c]) : 1.0f;
+        const __half *h = reinterpret_cast<const __half *>(&v[u]);
+        uint4 o;
+        __half *oh = reinterpret_cast<__half *>(&o);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) oh[k] = norm_scale(h[k], inv_s[oct * 8u + k], g);
+        // the 8 tokens before: the neighbouring lane's normalized octet (every lane shuffles);
+        // octet 0: its own HK tokens normalized, the rest unused by the taps
+        uint4 pv;
+        pv.x = (uint32_t)__shfl((int)o.x, src_lane, 64);
+        pv.y = (uint32_t)__shfl((int)o.y, src_lane, 64);
+        pv.z = (uint32_t)__shfl((int)o.z, src_lane, 64);
+        pv.w = (uint32_t)__shfl((int)o.w, src_lane, 64);
+        if (oct == 0u) {
+            pv = uint4{0u, 0u, 0u, 0u};
+            if (halo) {
+                const __half *hh = reinterpret_cast<const __half *>(&hv[u][0]);
+                __half *ph = reinterpret_cast<__half *>(&pv);
+#pragma unroll
+                for (uint32_t k = 0; k < HK; ++k)
+                    ph[8u - HK + k] = norm_scale(hh[k], inv_s[OCT * 8u + k], g);
+            }
+        }
+        if (!live) continue;
+        *reinterpret_cast<uint4 *>(y + (uint64_t)c * stride + t0) = o;
+        float m[RF];
+#pragma unroll
+        for (uint32_t i = 0; i < RF; ++i) m[i] = __half2float(mus[c * RF + i]);
+        float w[16];  // w[8 + k] = u[t0 + k], w[k] = u[t0 - 8 + k]
+        const __half *hp = reinterpret_cast<const __half *>(&pv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            w[8 + k] = __half2float(oh[k]);
+            w[k] = __half2float(hp[k]);
+        }
+        uint4 s;
+        __half *sh2 = reinterpret_cast<__half *>(&s);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            float acc = m[0] * w[8 + k];
+#pragma unroll
+            for (uint32_t i = 1; i < RF; ++i)
+                if (i <= pos0 + (uint32_t)k) acc = fmaf(m[i], w[8 + k - i], acc);
+            sh2[k] = f16_of(acc);
+        }
+        *reinterpret_cast<uint4 *>(y2 + (uint64_t)c * stride + t0) = s;
+        if (RF > 1u && state && near_end) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (pos0 + (uint32_t)k + RF > seq_len) {
+                    const uint32_t back = seq_len - 1u - (pos0 + (uint32_t)k);  // 0 = newest
+                    state[((uint64_t)c * (RF - 1u) + back) * 64u + (t0 + (uint32_t)k) / seq_len] =
+                        oh[k];
+                }
+            }
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void k44_mul_kernel(__half *__restrict__ y,
                                                       const __half *__restrict__ a,
                                                       const __half *__restrict__ b, uint64_t n8) {
@@ -521,6 +674,31 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
     slices = slices < max_slices ? slices : max_slices;
     const uint32_t cslice = (D + slices - 1u) / slices;
     RmsShift sh{};
+    if (shift && shift->seq_len) {
+        // Fused prefill token shift: the register-resident wide kernel with the shift.
+        if (!rmsnorm_shift_prefill_ok(D, stride, tokens, shift->rf, shift->seq_len))
+            return hipErrorInvalidValue;
+        const dim3 gw(tokens / 32u);
+#define K44_RMSP(C, R)                                                                          \
+    hipLaunchKernelGGL((k44_rmsnorm_shift_prefill_kernel<C, R>), gw, dim3(1024), 0, stream, y, x, \
+                       gamma, D, stride, eps, shift->y2, shift->mu, shift->state, shift->seq_len)
+#define K44_RMSP_RF(C)                  \
+    switch (shift->rf) {                \
+    case 1u: K44_RMSP(C, 1u); break;    \
+    case 2u: K44_RMSP(C, 2u); break;    \
+    case 3u: K44_RMSP(C, 3u); break;    \
+    case 4u: K44_RMSP(C, 4u); break;    \
+    default: K44_RMSP(C, 5u); break;    \
+    }
+        if (D <= 1024u) {
+            K44_RMSP_RF(4)
+        } else {
+            K44_RMSP_RF(8)
+        }
+#undef K44_RMSP_RF
+#undef K44_RMSP
+        return hipGetLastError();
+    }
     if (shift) {
         // Fused decode token shift: one channel per thread, every octet of the stride.
         if (oct != 1u || cslice > 256u || tokens > 64u || stride != 64u || shift->rf == 0u ||

@@ -19,14 +19,28 @@
 
 namespace k44dev {
 
-// Decode token shift fused into an RMSNorm (launch_rmsnorm's `shift`): its output y2, mixing
-// weights mu [D][rf], state [D][rf-1][64]; tokens is filled in by the launcher.
+// Token shift fused into an RMSNorm (launch_rmsnorm's `shift`): its output y2, mixing weights
+// mu [D][rf], state [D][rf-1][64] (nullptr: none); tokens is filled in by the launcher.
+// seq_len 0: the decode shift (one token per request); > 0: the prefill shift over requests of
+// seq_len tokens (rmsnorm_shift_prefill_ok must hold).
 struct RmsShift {
     __half *y2;
     const __half *mu;
     __half *state;
     uint32_t rf, tokens;
+    uint32_t seq_len = 0;
 };
+
+// Shapes the fused prefill RMSNorm + token shift kernel takes: 32-token workgroups covering
+// every token column (tokens == stride), D <= 2048 channels, rf 1..5 (its registers hold the 4
+// tokens before each block), requests of a multiple of 8 tokens, and token counts at which the
+// norm alone runs the register-resident kernel too (>= 256 workgroups), whose sums it repeats
+// (so fused and separate launches give the same values).
+inline bool rmsnorm_shift_prefill_ok(uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf,
+                                     uint32_t seq_len) {
+    return D > 0u && D <= 2048u && tokens == stride && tokens % 32u == 0u &&
+           tokens / 32u >= 256u && rf >= 1u && rf <= 5u && seq_len > 0u && seq_len % 8u == 0u;
+}
 
 hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
                           uint32_t stride, uint32_t tokens, float eps, hipStream_t stream,

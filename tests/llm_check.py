@@ -117,7 +117,8 @@ class PlanChecker:
                 state[i] = self.rows(c["src_off"], c["Cin"])
             elif t == "TOKEN_SHIFT_1D":
                 if not self.decode:  # prefill: the sampled windows and each request's tail
-                    state[i] = self._shift_inputs(c)
+                    # a shift fused into its norm reads the norm's output, read after the step
+                    state[i] = None if self._shift_fused(i, fused) else self._shift_inputs(c)
                     continue
                 st = self._state(c)
                 # a shift fused into its norm reads the norm's output, read after the step
@@ -156,7 +157,8 @@ class PlanChecker:
                 y = self.rows(c["y_off"], c["Cin"]).astype(np.float64)
                 self._note(t, lo.orc.rel_err(y, lo.rmsnorm_f64(state[i])), what)
             elif t == "TOKEN_SHIFT_1D" and not self.decode:
-                self._check_shift_prefill(c, state[i], what)
+                inputs = state[i] if state[i] is not None else self._shift_inputs(c)
+                self._check_shift_prefill(c, inputs, what)
             elif t == "TOKEN_SHIFT_1D":
                 x, st_in = state[i]
                 if x is None:  # fused: its input is the norm output the step just wrote

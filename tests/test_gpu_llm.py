@@ -543,6 +543,68 @@ def _norm_shift_graph(wavec, D, req, rf, mu, gamma, dead_input):
     return g, table
 
 
+@pytest.mark.parametrize("D,rf,seq_len,dead_input", [(2048, 4, 512, False), (256, 1, 128, False),
+                                                     (2048, 2, 256, False), (1024, 5, 128, False),
+                                                     (2048, 4, 512, True)])
+def test_fused_prefill_norm_shift(wavec, tuning, D, rf, seq_len, dead_input):
+    """Prefill RMSNorm -> token shift over 8,192 tokens (the register-resident norm's size): run
+    as one kernel (each 32-token workgroup also normalizes the tokens before its block) unless
+    the norm's input dies at the norm and the allocator hands its range to an output.  Norm
+    output, shift output and state block bit for bit equal to the plan with fusion off, and
+    within tolerance of the oracle."""
+    T = 8192
+    rng = np.random.default_rng(D + rf + seq_len)
+    mu = (rng.standard_normal((D, rf)) * 0.5).astype(np.float16)
+    gamma = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    table = (rng.standard_normal((50, D)) * 2).astype(np.float16)
+    ids = rng.integers(0, 50, T).astype(np.uint32)
+    x_in = (rng.standard_normal((D, T)) * 2).astype(np.float16)
+    outs = {}
+    for mode in ("fused", "unfused"):
+        tuning("fuse", 0 if mode == "unfused" else -1)
+        g = wavec.WaveGraph(kv_cache_max_seq=0, fold_rmsnorm_gamma=False)
+        if dead_input:
+            g.add_input("tok", 1, 1, T, is_1d=True)
+            g.add_embedding("emb", "tok", "x", table)
+        else:
+            g.add_input("x", D, 1, T, is_1d=True)
+        g.add_rmsnorm("n", "x", "u", D, gamma)
+        g.add_token_shift("ts", "u", "s", mu, seq_len, decode=False)
+        g.set_output("s")
+        plan = g.compile()
+        plan.init_gpu()
+        n_cmd, s_cmd = plan.cmds[-2], plan.cmds[-1]
+        fused = [a["name"] for a in plan.exec_report()["aux"] if a["fused"]]
+        rd = {int(n_cmd["src_off"])}
+        clash = int(s_cmd["y_off"]) in rd or int(n_cmd["y_off"]) in rd
+        _log(f"[prefill norm+shift D={D} rf={rf} seq={seq_len} dead={dead_input} {mode}] "
+             f"fused {fused}, output reuses the norm input: {clash}")
+        assert bool(fused) == (mode == "fused" and not clash)
+        if dead_input:
+            plan.set_ids(ids)
+            x = lo.embed(table, ids, T)
+        else:
+            x = x_in
+            plan.write_canvas(int(n_cmd["src_off"]), x)
+        plan.execute(1)
+        u = _read(plan, n_cmd["y_off"], D, T)
+        sh = _read(plan, s_cmd["y_off"], D, T)
+        has_state = rf > 1
+        st = (_read(plan, s_cmd["state_off"], D * (rf - 1), 64).reshape(D, rf - 1, 64)
+              if has_state else None)
+        u_ref = lo.rmsnorm_f64(x, gamma.astype(np.float16))
+        assert lo.orc.rel_err(u.astype(np.float64), u_ref) <= TOL
+        s_ref, st_ref = lo.token_shift(u, mu, seq_len, T, f64=True)
+        assert lo.orc.rel_err(sh.astype(np.float64), s_ref) <= TOL
+        if st is not None:
+            assert np.array_equal(st.view(np.uint16), st_ref.view(np.uint16))
+        outs[mode] = (u.copy(), sh.copy(), None if st is None else st.copy())
+        plan.release_gpu()
+    for a, b in zip(outs["fused"], outs["unfused"]):
+        if a is not None:
+            assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
 @pytest.mark.parametrize("dead_input", [False, True])
 @pytest.mark.parametrize("rf", [1, 2, 5, 9])
 def test_fused_norm_shift_every_rf(wavec, tuning, rf, dead_input):
