@@ -201,30 +201,145 @@ class Graph:
         self._add(Node("SwiGLU", name, [g, u], [o]))
 
 
+MAX_PACK_CLUSTERS = 12
+
+
+def pack_union_tiles(pm, nu: int, T: int, max_iter: int):
+    """Tiles of T neurons with small cluster unions (restatement of the build's
+    k44_host::pack_union_tiles); pm[j] = neuron j's cluster set as a bit mask over nu <= 12
+    distinct clusters.  Returns the tiles' neuron lists (each ascending), in creation order.
+
+    1. Greedy, one tile at a time: among the masks containing at least `need` = min(T,
+       unassigned) unassigned patterns (subset-sum transform of the pattern counts), take the one
+       with the fewest clusters, then the most patterns, then the smallest mask value; of its
+       unassigned neurons take the `need` that lie in the fewest other such masks (superset-sum
+       transform), ties by index.
+    2. Swaps: while the first tile W with the largest union can drop one of its clusters c —
+       tried in order of (neurons of W using c, c) — by trading each of its neurons a that use c
+       (ascending order of W's current list) for the first neuron b (tiles in order, each
+       tile's current list in order) not yet traded, not using c, inside W's union, such that
+       b's tile keeps a union below W's: trade them all (a goes to the end of b's tile's list,
+       b to the end of W's) and repeat; at most max_iter rounds."""
+    pm = np.asarray(pm, dtype=np.int64)
+    n, NM = pm.size, 1 << nu
+    idx = np.arange(NM)
+    pop = np.array([bin(m).count("1") for m in range(NM)])
+    left = np.ones(n, dtype=bool)
+    tiles = []
+    while left.any():
+        need = min(T, int(left.sum()))
+        cnt = np.bincount(pm[left], minlength=NM).astype(np.int64)
+        for b in range(nu):  # cnt[m] = unassigned patterns inside m
+            sel = (idx >> b) & 1 == 1
+            cnt[sel] += cnt[idx[sel] ^ (1 << b)]
+        ok = np.nonzero(cnt >= need)[0]
+        best = int(ok[np.lexsort((ok, -cnt[ok], pop[ok]))[0]])
+        v = ((cnt >= need) & (idx != best)).astype(np.int64)
+        for b in range(nu):  # v[m] = other such masks containing m
+            sel = (idx >> b) & 1 == 0
+            v[sel] += v[idx[sel] | (1 << b)]
+        mem = np.nonzero(left & ((pm & ~best) == 0))[0]
+        take = np.sort(mem[np.argsort(v[pm[mem]], kind="stable")[:need]])
+        left[take] = False
+        tiles.append([int(j) for j in take])
+    cc = np.zeros((len(tiles), nu), dtype=np.int64)  # per tile: neurons using each cluster
+    bits = [[c for c in range(nu) if m >> c & 1] for m in range(NM)]
+    for t, js in enumerate(tiles):
+        for j in js:
+            cc[t, bits[pm[j]]] += 1
+    for _ in range(max_iter):
+        sizes = (cc > 0).sum(axis=1)
+        m = int(sizes.max())
+        W = int(np.argmax(sizes))
+        uw = sum(1 << c for c in range(nu) if cc[W, c])
+        done = False
+        for c in sorted((c for c in range(nu) if cc[W, c]), key=lambda c: (cc[W, c], c)):
+            trades, used = [], set()
+            for a in [j for j in tiles[W] if pm[j] >> c & 1]:
+                hit = None
+                for B in range(len(tiles)):
+                    if B == W:
+                        continue
+                    for b in tiles[B]:
+                        if b in used or pm[b] >> c & 1 or pm[b] & ~uw:
+                            continue
+                        after = cc[B].copy()
+                        after[bits[pm[b]]] -= 1
+                        after[bits[pm[a]]] += 1
+                        if (after > 0).sum() <= m - 1:
+                            hit = (B, b)
+                            break
+                    if hit:
+                        break
+                if hit is None:
+                    break
+                B, b = hit
+                cc[B, bits[pm[b]]] -= 1
+                cc[B, bits[pm[a]]] += 1
+                cc[W, bits[pm[a]]] -= 1
+                cc[W, bits[pm[b]]] += 1
+                trades.append((a, B, b))
+                used.add(b)
+            else:
+                for a, B, b in trades:
+                    tiles[W].remove(a)
+                    tiles[W].append(b)
+                    tiles[B].remove(b)
+                    tiles[B].append(a)
+                done = True
+                break
+            for a, B, b in reversed(trades):  # this cluster cannot go: undo
+                cc[B, bits[pm[b]]] += 1
+                cc[B, bits[pm[a]]] -= 1
+                cc[W, bits[pm[a]]] += 1
+                cc[W, bits[pm[b]]] -= 1
+        if not done:
+            break
+    return [sorted(t) for t in tiles]
+
+
 def pruned_parts(starts: np.ndarray, S: int, w: np.ndarray, bias: np.ndarray, tile: int):
-    """Pattern-sorted tiles of a pruned projection (restatement of the build's
-    K44WaveGraphCompiler::add_pruned_wave): neurons grouped by their sorted cluster pattern
-    (groups in lexicographic order), full tiles per group, the groups' remainders packed in order
-    into tiles whose index row is the union of their clusters, one part per union size
-    (ascending).  Returns [(union starts [tiles][U], weights [tiles*tile][U*S] u16,
+    """Tiles of a pruned projection (restatement of the build's
+    K44WaveGraphCompiler::add_pruned_wave).  Pattern-sorted cutting: neurons grouped by their
+    sorted cluster pattern (groups in lexicographic order), full tiles per group, the groups'
+    remainders packed in order.  With at most 12 distinct clusters over all neurons,
+    pack_union_tiles too, and its tiles replace the cutting's unless they have a larger largest
+    union (or the same largest and a larger total).  A tile's index row is the union of its
+    neurons' clusters; one part per union size (ascending).  Returns [(union starts [tiles][U], weights [tiles*tile][U*S] u16,
     bias [tiles*tile] u16, cmap [tiles*tile] u16 (0xFFFF = empty))]."""
     cout, K = starts.shape
     order = np.argsort(starts, axis=1, kind="stable")
     pat = np.take_along_axis(starts, order, axis=1)
+    univ = sorted({int(v) for v in pat.ravel()})
+    # pattern-sorted cutting: full tiles per pattern group, then the groups' remainders
     groups = {}
     for j in range(cout):
         groups.setdefault(tuple(int(v) for v in pat[j]), []).append(j)
-    tiles, rest = [], []
+    cut, rest = [], []
     for key in sorted(groups):
         g = groups[key]
         full = len(g) // tile
         for f in range(full):
-            tiles.append((g[f * tile:(f + 1) * tile], list(key)))
+            cut.append(g[f * tile:(f + 1) * tile])
         rest += g[full * tile:]
     for b in range(0, len(rest), tile):
-        slots = rest[b:b + tile]
-        uni = sorted({int(v) for j in slots for v in pat[j]})
-        tiles.append((slots + [-1] * (tile - len(slots)), uni))
+        cut.append(rest[b:b + tile])
+    chosen = cut
+    if len(univ) <= MAX_PACK_CLUSTERS:
+        pos = {u: i for i, u in enumerate(univ)}
+        pm = [sum(1 << pos[int(v)] for v in pat[j]) for j in range(cout)]
+        packed = pack_union_tiles(pm, len(univ), tile, 4 * (-(-cout // tile)) + 64)
+
+        def cost(ts):  # (largest union, total of unions)
+            us = [bin(int(np.bitwise_or.reduce([pm[j] for j in t]))).count("1") for t in ts]
+            return max(us), sum(us)
+
+        if cost(packed) <= cost(cut):
+            chosen = packed
+    tiles = []
+    for js in chosen:
+        uni = sorted({int(v) for j in js for v in pat[j]})
+        tiles.append((list(js) + [-1] * (tile - len(js)), uni))
     parts = []
     for U in sorted({len(t[1]) for t in tiles}):
         sel = [t for t in tiles if len(t[1]) == U]

@@ -15,6 +15,7 @@
 // whose offsets do not fit the reference's u32 index words is emitted in row-index mode
 // (K44ExecCmd::idx_mode = 1).
 #pragma once
+#include <algorithm>
 #include <map>
 #include <numeric>
 #include <set>
@@ -24,6 +25,157 @@
 #include "k44_tcff_io.hpp"
 
 namespace k44_host {
+
+// Distinct clusters up to which pruned projections take pack_union_tiles (2^12 masks).
+constexpr uint32_t kMaxPackClusters = 12;
+
+// Tiles of T neurons with small cluster unions for a pruned projection: pm[j] = neuron j's
+// cluster set as a bit mask over nu <= kMaxPackClusters distinct clusters.  A tile's MFMA work
+// (and, where all of a launch's work items run at once, the launch's time) grows with its
+// union, so this bounds the largest union first.  Returns the tiles' neuron lists (each
+// ascending), in creation order.
+//  1. Greedy, one tile at a time: among the masks containing at least need = min(T, unassigned)
+//     unassigned patterns (subset-sum transform of the pattern counts), the one with the fewest
+//     clusters, then the most patterns, then the smallest mask value; of its unassigned neurons
+//     the `need` that lie in the fewest other such masks (superset-sum transform), ties by index.
+//  2. Swaps: while the first tile W with the largest union can drop one of its clusters c —
+//     tried in order of (neurons of W using c, c) — by trading each of its neurons a that use c
+//     (W's current list order) for the first neuron b (tiles in order, each tile's current list
+//     in order) not yet traded, not using c, inside W's union, such that b's tile keeps a union
+//     smaller than W's: trade them all (a to the end of b's tile, b to the end of W) and repeat,
+//     at most max_iter times.
+inline std::vector<std::vector<uint32_t>> pack_union_tiles(const std::vector<uint32_t> &pm,
+                                                           uint32_t nu, uint32_t T,
+                                                           uint32_t max_iter) {
+    const uint32_t n = (uint32_t)pm.size(), NM = 1u << nu;
+    std::vector<uint8_t> left(n, 1u);
+    uint32_t n_left = n;
+    std::vector<std::vector<uint32_t>> tiles;
+    std::vector<int64_t> cnt(NM), v(NM);
+    while (n_left) {
+        const uint32_t need = std::min(T, n_left);
+        std::fill(cnt.begin(), cnt.end(), 0);
+        for (uint32_t j = 0; j < n; ++j)
+            if (left[j]) ++cnt[pm[j]];
+        for (uint32_t b = 0; b < nu; ++b)  // cnt[m] = unassigned patterns inside m
+            for (uint32_t m = 0; m < NM; ++m)
+                if (m >> b & 1u) cnt[m] += cnt[m ^ (1u << b)];
+        uint32_t best = NM - 1u;  // the full mask holds every pattern
+        for (uint32_t m = 0; m < NM; ++m) {
+            if (cnt[m] < (int64_t)need) continue;
+            const int pm_ = __builtin_popcount(m), pb = __builtin_popcount(best);
+            if (pm_ < pb || (pm_ == pb && (cnt[m] > cnt[best] || (cnt[m] == cnt[best] && m < best))))
+                best = m;
+        }
+        for (uint32_t m = 0; m < NM; ++m) v[m] = (cnt[m] >= (int64_t)need && m != best) ? 1 : 0;
+        for (uint32_t b = 0; b < nu; ++b)  // v[m] = other such masks containing m
+            for (uint32_t m = 0; m < NM; ++m)
+                if (!(m >> b & 1u)) v[m] += v[m | (1u << b)];
+        std::vector<uint32_t> mem;
+        for (uint32_t j = 0; j < n; ++j)
+            if (left[j] && (pm[j] & ~best) == 0u) mem.push_back(j);
+        std::stable_sort(mem.begin(), mem.end(),
+                         [&](uint32_t a, uint32_t b) { return v[pm[a]] < v[pm[b]]; });
+        mem.resize(need);
+        std::sort(mem.begin(), mem.end());
+        for (uint32_t j : mem) left[j] = 0u;
+        n_left -= need;
+        tiles.push_back(std::move(mem));
+    }
+    const size_t nt = tiles.size();
+    std::vector<std::vector<int64_t>> cc(nt, std::vector<int64_t>(nu, 0));  // neurons per cluster
+    auto add = [&](size_t t, uint32_t mask, int64_t d) {
+        for (uint32_t c = 0; c < nu; ++c)
+            if (mask >> c & 1u) cc[t][c] += d;
+    };
+    auto usize = [&](const std::vector<int64_t> &x) {
+        uint32_t k = 0;
+        for (int64_t e : x) k += e > 0 ? 1u : 0u;
+        return k;
+    };
+    for (size_t t = 0; t < nt; ++t)
+        for (uint32_t j : tiles[t]) add(t, pm[j], 1);
+    for (uint32_t iter = 0; iter < max_iter; ++iter) {
+        size_t W = 0;
+        uint32_t m = 0;
+        for (size_t t = 0; t < nt; ++t)
+            if (usize(cc[t]) > m) {
+                m = usize(cc[t]);
+                W = t;
+            }
+        uint32_t uw = 0;
+        std::vector<uint32_t> cs;
+        for (uint32_t c = 0; c < nu; ++c)
+            if (cc[W][c] > 0) {
+                uw |= 1u << c;
+                cs.push_back(c);
+            }
+        std::stable_sort(cs.begin(), cs.end(),
+                         [&](uint32_t a, uint32_t b) { return cc[W][a] < cc[W][b]; });
+        bool done = false;
+        for (uint32_t c : cs) {
+            std::vector<uint32_t> A;
+            for (uint32_t j : tiles[W])
+                if (pm[j] >> c & 1u) A.push_back(j);
+            struct Trade { uint32_t a; size_t B; uint32_t b; };
+            std::vector<Trade> trades;
+            std::set<uint32_t> used;
+            bool all = true;
+            for (uint32_t a : A) {
+                bool hit = false;
+                Trade tr{a, 0, 0};
+                for (size_t B = 0; B < nt && !hit; ++B) {
+                    if (B == W) continue;
+                    for (uint32_t b : tiles[B]) {
+                        if (used.count(b) || (pm[b] >> c & 1u) || (pm[b] & ~uw)) continue;
+                        std::vector<int64_t> after = cc[B];
+                        for (uint32_t q = 0; q < nu; ++q) {
+                            if (pm[b] >> q & 1u) --after[q];
+                            if (pm[a] >> q & 1u) ++after[q];
+                        }
+                        if (usize(after) + 1u <= m) {
+                            tr.B = B;
+                            tr.b = b;
+                            hit = true;
+                            break;
+                        }
+                    }
+                }
+                if (!hit) {
+                    all = false;
+                    break;
+                }
+                add(tr.B, pm[tr.b], -1);
+                add(tr.B, pm[a], 1);
+                add(W, pm[a], -1);
+                add(W, pm[tr.b], 1);
+                trades.push_back(tr);
+                used.insert(tr.b);
+            }
+            if (all) {
+                for (const Trade &tr : trades) {
+                    auto &tw = tiles[W], &tb = tiles[tr.B];
+                    tw.erase(std::find(tw.begin(), tw.end(), tr.a));
+                    tw.push_back(tr.b);
+                    tb.erase(std::find(tb.begin(), tb.end(), tr.b));
+                    tb.push_back(tr.a);
+                }
+                done = true;
+                break;
+            }
+            for (size_t k = trades.size(); k-- > 0;) {  // this cluster cannot go: undo
+                const Trade &tr = trades[k];
+                add(tr.B, pm[tr.b], 1);
+                add(tr.B, pm[tr.a], -1);
+                add(W, pm[tr.a], 1);
+                add(W, pm[tr.b], -1);
+            }
+        }
+        if (!done) break;
+    }
+    for (auto &t : tiles) std::sort(t.begin(), t.end());
+    return tiles;
+}
 
 class K44WaveGraphCompiler {
   private:
@@ -1273,13 +1425,15 @@ class K44WaveGraphCompiler {
 
     // Build extension: projection whose neurons each keep their own K dendritic clusters of S
     // consecutive input channels (starts: [cout][K], w_f16: [cout][K*S] in the same cluster
-    // order).  Compiled into pattern-sorted tiles of `tile` neurons for dense MFMA tiles:
+    // order).  Compiled into tiles of `tile` neurons for dense MFMA tiles:
     //   1. each neuron's clusters are sorted by start (weight segments move with them);
-    //   2. neurons are grouped by identical cluster pattern, groups in lexicographic pattern
-    //      order, neurons of a group in index order;
-    //   3. every group contributes floor(n / tile) full tiles of its own pattern; the remainders
-    //      of all groups, in group order, are cut into tiles of `tile` slots (the last one
-    //      partly empty), whose index row is the sorted union of their neurons' clusters;
+    //   2. pattern-sorted cutting: neurons are grouped by identical cluster pattern (groups in
+    //      lexicographic order, neurons of a group in index order), every group contributes
+    //      floor(n / tile) full tiles of its own pattern, and the remainders of all groups, in
+    //      group order, are cut into tiles of `tile` slots (the last one partly empty); with at
+    //      most kMaxPackClusters distinct clusters over all neurons, pack_union_tiles' tiles
+    //      replace these unless their largest union (then their total) is larger;
+    //   3. a tile's index row is the sorted union of its neurons' clusters;
     //   4. tiles are gathered into one sub-wave per union size (ascending); a neuron's weights
     //      are zero on the clusters of the union it does not keep; each sub-wave's cout_map
     //      sends slot j to the neuron's own output channel (0xFFFF: empty slot).
@@ -1308,41 +1462,67 @@ class K44WaveGraphCompiler {
                                                 "': clusters of a neuron overlap");
             }
         }
-        // 2. groups by pattern, lexicographic
-        std::map<std::vector<uint32_t>, std::vector<uint32_t>> groups;
-        for (uint32_t j = 0; j < cout; ++j)
-            groups[std::vector<uint32_t>(pat.begin() + (size_t)j * K,
-                                         pat.begin() + (size_t)(j + 1) * K)]
-                .push_back(j);
-        // 3. full tiles, then remainder tiles; each tile = slots (neuron or -1) + union row
+        // 2-3. tiles; each tile = slots (neuron or -1) + union row
         struct Tile {
             std::vector<int64_t> slots;
             std::vector<uint32_t> uni;
         };
         std::vector<Tile> tiles;
-        std::vector<uint32_t> rest;
-        for (const auto &g : groups) {
-            const size_t full = g.second.size() / tile;
-            for (size_t f = 0; f < full; ++f) {
-                Tile t;
-                t.slots.assign(g.second.begin() + f * tile, g.second.begin() + (f + 1) * tile);
-                t.uni = g.first;
-                tiles.push_back(std::move(t));
+        std::vector<uint32_t> univ(pat.begin(), pat.end());
+        std::sort(univ.begin(), univ.end());
+        univ.erase(std::unique(univ.begin(), univ.end()), univ.end());
+        // pattern-sorted cutting: groups by pattern (lexicographic), full tiles per group, then
+        // the groups' remainders in group order
+        std::vector<std::vector<uint32_t>> chosen;
+        {
+            std::map<std::vector<uint32_t>, std::vector<uint32_t>> groups;
+            for (uint32_t j = 0; j < cout; ++j)
+                groups[std::vector<uint32_t>(pat.begin() + (size_t)j * K,
+                                             pat.begin() + (size_t)(j + 1) * K)]
+                    .push_back(j);
+            std::vector<uint32_t> rest;
+            for (const auto &g : groups) {
+                const size_t full = g.second.size() / tile;
+                for (size_t f = 0; f < full; ++f)
+                    chosen.emplace_back(g.second.begin() + f * tile,
+                                        g.second.begin() + (f + 1) * tile);
+                rest.insert(rest.end(), g.second.begin() + full * tile, g.second.end());
             }
-            rest.insert(rest.end(), g.second.begin() + full * tile, g.second.end());
+            for (size_t b = 0; b < rest.size(); b += tile)
+                chosen.emplace_back(rest.begin() + b, rest.begin() + std::min(rest.size(), b + tile));
         }
-        for (size_t b = 0; b < rest.size(); b += tile) {
+        if (univ.size() <= kMaxPackClusters) {
+            // bounded unions over few distinct clusters (pack_union_tiles), unless their largest
+            // union (then their total) is larger than the cutting's
+            std::vector<uint32_t> pm(cout, 0u);
+            for (uint32_t j = 0; j < cout; ++j)
+                for (uint32_t k = 0; k < K; ++k)
+                    pm[j] |= 1u << (std::lower_bound(univ.begin(), univ.end(),
+                                                     pat[(size_t)j * K + k]) -
+                                    univ.begin());
+            const uint32_t n_tiles = (cout + tile - 1u) / tile;
+            auto packed = pack_union_tiles(pm, (uint32_t)univ.size(), tile, 4u * n_tiles + 64u);
+            auto cost = [&](const std::vector<std::vector<uint32_t>> &ts) {
+                uint32_t mx = 0, sum = 0;
+                for (const auto &t : ts) {
+                    uint32_t m = 0;
+                    for (uint32_t j : t) m |= pm[j];
+                    const uint32_t u = (uint32_t)__builtin_popcount(m);
+                    mx = std::max(mx, u);
+                    sum += u;
+                }
+                return std::make_pair(mx, sum);
+            };
+            if (cost(packed) <= cost(chosen)) chosen = std::move(packed);
+        }
+        for (const auto &js : chosen) {
             Tile t;
             std::set<uint32_t> u;
-            for (size_t q = b; q < b + tile; ++q) {
-                if (q < rest.size()) {
-                    t.slots.push_back(rest[q]);
-                    u.insert(pat.begin() + (size_t)rest[q] * K,
-                             pat.begin() + (size_t)(rest[q] + 1) * K);
-                } else {
-                    t.slots.push_back(-1);
-                }
+            for (uint32_t j : js) {
+                t.slots.push_back(j);
+                u.insert(pat.begin() + (size_t)j * K, pat.begin() + (size_t)(j + 1) * K);
             }
+            t.slots.resize(tile, -1);
             t.uni.assign(u.begin(), u.end());
             tiles.push_back(std::move(t));
         }
