@@ -168,9 +168,12 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
 
 // Wide token counts (prefill): workgroup = 4 token octets (32 tokens, 64-byte row runs) x 256
 // channel lanes (1024 threads), one workgroup per 32 tokens.  A thread loads its CPT channels
-// (lane, lane + 256, ...) once, keeps them in registers for the sum of squares and the scaled
-// store: the input is read once (the narrower kernel above reads it twice).  Sums meet by
-// shuffles within a wave, then across the 16 waves in LDS in wave order.
+// (lane, lane + 256, ...) and their gammas once, keeps them in registers for the sum of squares
+// and the scaled store: the input is read once (the narrower kernel above reads it twice).  All
+// loads are issued together, without branches around them (channels >= D read row D - 1 and
+// drop it): a load under a divergent branch, or one placed among the stores, makes the compiler
+// wait for every access before it, stores included.  Sums meet by shuffles within a wave, then
+// across the 16 waves in LDS in wave order.
 template <int CPT>
 __global__ __launch_bounds__(1024) void k44_rmsnorm_regs_kernel(__half *__restrict__ y,
                                                                 const __half *__restrict__ x,
@@ -182,12 +185,19 @@ __global__ __launch_bounds__(1024) void k44_rmsnorm_regs_kernel(__half *__restri
     __shared__ float inv_s[OCT * 8];
     const uint32_t oct = threadIdx.x % OCT, lane_c = threadIdx.x / OCT;
     const uint32_t t0 = (blockIdx.x * OCT + oct) * 8u;
+    // gamma bits one per register (CPT <= 8; 16 channels a thread load theirs at the store);
+    // without gamma x's first row stands in for it, unused
+    constexpr int GR = CPT <= 8 ? CPT : 1;
     uint4 v[CPT];
+    uint32_t gv[GR];
+    const uint16_t *g16 = reinterpret_cast<const uint16_t *>(gamma ? gamma : x);
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
         const uint32_t c = lane_c + (uint32_t)u * CL;
-        v[u] = c < D ? *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0)
-                     : uint4{0u, 0u, 0u, 0u};
+        const uint32_t cc = c < D ? c : D - 1u;
+        const uint4 t = *reinterpret_cast<const uint4 *>(x + (uint64_t)cc * stride + t0);
+        v[u] = c < D ? t : uint4{0u, 0u, 0u, 0u};
+        if constexpr (CPT <= 8) gv[u] = g16[cc];
     }
     float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
@@ -223,7 +233,12 @@ __global__ __launch_bounds__(1024) void k44_rmsnorm_regs_kernel(__half *__restri
         const uint32_t c = lane_c + (uint32_t)u * CL;
         if (c >= D) break;
         const __half *h = reinterpret_cast<const __half *>(&v[u]);
-        const float g = gamma ? __half2float(gamma[c]) : 1.0f;
+        float g = 1.0f;
+        if constexpr (CPT <= 8) {
+            if (gamma) g = __half2float(__ushort_as_half((unsigned short)gv[u]));
+        } else if (gamma) {
+            g = __half2float(gamma[c]);
+        }
         uint4 o;
         __half *oh = reinterpret_cast<__half *>(&o);
 #pragma unroll
@@ -257,26 +272,52 @@ __global__ __launch_bounds__(1024) void k44_rmsnorm_shift_prefill_kernel(
     const uint32_t oct = threadIdx.x % OCT, lane_c = threadIdx.x / OCT;
     const uint32_t t0 = (blockIdx.x * OCT + oct) * 8u;
     const bool halo = HK && oct == 0u && t0 >= 8u;
+    // Every lane issues every load, without branches (a load under a divergent branch makes the
+    // compiler wait for all accesses before it): channels >= D read row D - 1, lanes without a
+    // halo read the 4 tokens at t0, and both are replaced by zeros after the load.
     uint4 v[CPT];
     uint32_t hv[CPT][HS / 2];  // the HK tokens before t0 (octet 0 lanes)
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
         const uint32_t c = lane_c + (uint32_t)u * CL;
-        const __half *xr = x + (uint64_t)c * stride;
-        v[u] = c < D ? *reinterpret_cast<const uint4 *>(xr + t0) : uint4{0u, 0u, 0u, 0u};
+        const bool live = c < D;
+        const __half *xr = x + (uint64_t)(live ? c : D - 1u) * stride;
+        const uint4 t = *reinterpret_cast<const uint4 *>(xr + t0);
+        v[u] = live ? t : uint4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (uint32_t j = 0; j < HS / 2; ++j) hv[u][j] = 0u;
         if constexpr (HK == 4u) {
-            if (halo && c < D) {
-                const uint2 hx = *reinterpret_cast<const uint2 *>(xr + t0 - 4u);
-                hv[u][0] = hx.x;
-                hv[u][1] = hx.y;
-            }
+            const uint2 hx = *reinterpret_cast<const uint2 *>(xr + (halo ? t0 - 4u : t0));
+            hv[u][0] = halo && live ? hx.x : 0u;
+            hv[u][1] = halo && live ? hx.y : 0u;
         }
     }
-    // the channels' mixing weights and gamma, staged in LDS (visible after the barrier below)
-    for (uint32_t e = threadIdx.x; e < D * RF; e += 1024u) mus[e] = mu[e];
-    for (uint32_t e = threadIdx.x; e < D; e += 1024u) gms[e] = gamma ? gamma[e] : __float2half(1.0f);
+    // the channels' mixing weights and gamma, staged in LDS (visible after the barrier below);
+    // all loads issued before the first LDS write, indices clamped rather than branched around
+    constexpr uint32_t NMU = (2048u * RF + 1023u) / 1024u, NGM = 2u;
+    uint32_t mv[NMU], gmv[NGM];
+    const uint16_t *mu16 = reinterpret_cast<const uint16_t *>(mu);
+    const uint16_t *g16 = reinterpret_cast<const uint16_t *>(gamma);
+#pragma unroll
+    for (uint32_t j = 0; j < NMU; ++j) {
+        const uint32_t e = threadIdx.x + j * 1024u;
+        mv[j] = mu16[e < D * RF ? e : 0u];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < NGM; ++j) {
+        const uint32_t e = threadIdx.x + j * 1024u;
+        gmv[j] = g16 ? (uint32_t)g16[e < D ? e : 0u] : 0x3C00u;  // fp16 1.0 without gamma
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < NMU; ++j) {
+        const uint32_t e = threadIdx.x + j * 1024u;
+        if (e < D * RF) mus[e] = __ushort_as_half((unsigned short)mv[j]);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < NGM; ++j) {
+        const uint32_t e = threadIdx.x + j * 1024u;
+        if (e < D) gms[e] = __ushort_as_half((unsigned short)gmv[j]);
+    }
     float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0}, sh[HS];
 #pragma unroll
     for (uint32_t k = 0; k < HS; ++k) sh[k] = 0.0f;
