@@ -45,7 +45,6 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
     const bool one = cslice <= CL;
     const uint32_t c_own = blockIdx.y * cslice + lane_c;
     uint4 xo = {0u, 0u, 0u, 0u};
-    float go = 1.0f;
     // Fused token shift: octets without requests only write zeros; the mixing weights and the
     // state of the thread's channel are loaded here too.
     if constexpr (RF > 0u) {
@@ -56,16 +55,22 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
             return;  // uniform: one octet per workgroup
         }
     }
-    float mw[RF > 0u ? RF : 1u];
+    // Every lane loads (the last channel of the slice stands in for lanes past it, whose
+    // results are not written; slices of several channels per thread do not use these), and
+    // the values are held opaque until after the sum's loads: a load under a branch, or one
+    // converted right away, makes the compiler wait for it before the sum's loads are issued.
+    // Without gamma, x stands in for it (unused).
+    uint32_t gbits, mbits[RF > 0u ? RF : 1u];
     uint4 sv[RF > 1u ? RF - 1u : 1u];
-    if (one && c_own < c_end) {
-        xo = *reinterpret_cast<const uint4 *>(x + (uint64_t)c_own * stride + t0);
-        if (gamma) go = __half2float(gamma[c_own]);
+    {
+        const uint32_t cc = c_own < c_end ? c_own : c_end - 1u;
+        xo = *reinterpret_cast<const uint4 *>(x + (uint64_t)cc * stride + t0);
+        gbits = reinterpret_cast<const uint16_t *>(gamma ? gamma : x)[cc];
         if constexpr (RF > 0u) {
-            const __half *m = sh.mu + (uint64_t)c_own * RF;
+            const uint16_t *m = reinterpret_cast<const uint16_t *>(sh.mu) + (uint64_t)cc * RF;
 #pragma unroll
-            for (uint32_t i = 0; i < RF; ++i) mw[i] = __half2float(m[i]);
-            const __half *st = sh.state + (uint64_t)c_own * (RF - 1u) * 64u + t0;
+            for (uint32_t i = 0; i < RF; ++i) mbits[i] = m[i];
+            const __half *st = sh.state + (uint64_t)cc * (RF - 1u) * 64u + t0;
 #pragma unroll
             for (uint32_t i = 1; i < RF; ++i)
                 sv[i - 1] = *reinterpret_cast<const uint4 *>(st + (i - 1u) * 64u);
@@ -97,6 +102,15 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
             ss[k] = fmaf(f, f, ss[k]);
         }
     }
+    // the own-channel values become visible to the compiler only here
+    asm volatile("" : "+v"(xo.x), "+v"(xo.y), "+v"(xo.z), "+v"(xo.w), "+v"(gbits));
+    if constexpr (RF > 0u) {
+#pragma unroll
+        for (uint32_t i = 0; i < RF; ++i) asm volatile("" : "+v"(mbits[i]));
+#pragma unroll
+        for (uint32_t i = 1; i < RF; ++i)
+            asm volatile("" : "+v"(sv[i - 1].x), "+v"(sv[i - 1].y), "+v"(sv[i - 1].z), "+v"(sv[i - 1].w));
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k)
 #pragma unroll
@@ -118,6 +132,7 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
             const __half *h = reinterpret_cast<const __half *>(&xo);
             uint4 o;
             __half *oh = reinterpret_cast<__half *>(&o);
+            const float go = gamma ? __half2float(__ushort_as_half((unsigned short)gbits)) : 1.0f;
 #pragma unroll
             for (int k = 0; k < 8; ++k) oh[k] = norm_scale(h[k], inv[k], go);
             if (RF == 0u || t0 < sh.tokens)
@@ -135,6 +150,10 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
                         yh[k] = __float2half_rn(0.0f);
                         continue;
                     }
+                    float mw[RF];
+#pragma unroll
+                    for (uint32_t i = 0; i < RF; ++i)
+                        mw[i] = __half2float(__ushort_as_half((unsigned short)mbits[i]));
                     float acc = mw[0] * __half2float(oh[k]);
 #pragma unroll
                     for (uint32_t i = 1; i < RF; ++i)
@@ -609,6 +628,49 @@ __global__ __launch_bounds__(256) void k44_embed_kernel(__half *__restrict__ y,
     }
 }
 
+// The same gather with 16-byte accesses (D % 8 == 0, 16-byte aligned table and output): a
+// thread loads 8 channels of one token's row and stores 8 tokens of one channel, every load
+// issued before the first wait (ids and rows clamped into range, invalid ones zeroed after).
+__global__ __launch_bounds__(256) void k44_embed_vec_kernel(__half *__restrict__ y,
+                                                            const __half *__restrict__ table,
+                                                            const uint32_t *__restrict__ ids,
+                                                            uint32_t D, uint32_t vocab,
+                                                            uint32_t stride, uint32_t tokens) {
+    constexpr uint32_t PITCH = 72u;  // halves per token row: 16-byte rows, spread banks
+    __shared__ __attribute__((aligned(16))) __half tile[64 * PITCH];
+    const uint32_t t0 = blockIdx.x * 64u, c0 = blockIdx.y * 64u;
+    uint4 v[2];
+    bool ok[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const uint32_t q = threadIdx.x + (uint32_t)r * 256u;
+        const uint32_t tt = q >> 3, c = c0 + (q & 7u) * 8u;
+        const uint32_t t = t0 + tt;
+        const uint32_t id = ids[t < tokens ? t : 0u];
+        ok[r] = t < tokens && id < vocab && c < D;
+        const uint64_t row = id < vocab ? id : 0u;
+        v[r] = *reinterpret_cast<const uint4 *>(table + row * D + (c < D ? c : 0u));
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const uint32_t q = threadIdx.x + (uint32_t)r * 256u;
+        *reinterpret_cast<uint4 *>(&tile[(q >> 3) * PITCH + (q & 7u) * 8u]) =
+            ok[r] ? v[r] : uint4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const uint32_t q = threadIdx.x + (uint32_t)r * 256u;
+        const uint32_t cc = q >> 3, tg = (q & 7u) * 8u;  // channel c0 + cc, tokens tg .. tg + 7
+        if (c0 + cc >= D) continue;
+        uint4 o;
+        __half *oh = reinterpret_cast<__half *>(&o);
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; ++j) oh[j] = tile[(tg + j) * PITCH + cc];
+        *reinterpret_cast<uint4 *>(y + (uint64_t)(c0 + cc) * stride + t0 + tg) = o;
+    }
+}
+
 // ARGMAX pass 1: workgroup = 64 tokens x one chunk of channels; lane (16 per channel row) owns
 // 4 tokens, the 16 row groups of the workgroup stride the chunk.  Ties keep the lowest channel
 // (channels are visited in ascending order per thread, and merged lowest-index-first).
@@ -660,6 +722,59 @@ __global__ __launch_bounds__(256) void k44_argmax_partial_kernel(
         float v = sv[0][threadIdx.x];
         uint32_t i = si[0][threadIdx.x];
         for (int g2 = 1; g2 < 16; ++g2) amax_merge(v, i, sv[g2][threadIdx.x], si[g2][threadIdx.x]);
+        const uint64_t o = (uint64_t)blockIdx.y * (gridDim.x * 64u) + blockIdx.x * 64u + threadIdx.x;
+        pval[o] = v;
+        pidx[o] = i;
+    }
+}
+
+// Pass 1 with 16-byte loads (16-byte aligned logits): 8 lanes per 64-token row, each owning 8
+// tokens; the 32 row groups of the workgroup stride the chunk, 8 rows in flight per thread.
+__global__ __launch_bounds__(256) void k44_argmax_partial16_kernel(
+    float *__restrict__ pval, uint32_t *__restrict__ pidx, const __half *__restrict__ x,
+    uint32_t V, uint32_t stride, uint32_t chunk) {
+    __shared__ float sv[32][64];
+    __shared__ uint32_t si[32][64];
+    const uint32_t grp = threadIdx.x >> 3, q = threadIdx.x & 7u;
+    const uint32_t t0 = blockIdx.x * 64u + q * 8u;
+    const uint32_t c_begin = blockIdx.y * chunk, c_end = min(V, c_begin + chunk);
+    float bv[8];
+    uint32_t bi[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        bv[k] = -INFINITY;
+        bi[k] = 0xffffffffu;
+    }
+    constexpr uint32_t UNR = 8;
+    uint32_t c = c_begin + grp;
+    for (; c + (UNR - 1u) * 32u < c_end; c += UNR * 32u) {
+        uint4 v[UNR];
+#pragma unroll
+        for (uint32_t u = 0; u < UNR; ++u)
+            v[u] = *reinterpret_cast<const uint4 *>(x + (uint64_t)(c + u * 32u) * stride + t0);
+#pragma unroll
+        for (uint32_t u = 0; u < UNR; ++u) {
+            const __half *h = reinterpret_cast<const __half *>(&v[u]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) amax_merge(bv[k], bi[k], __half2float(h[k]), c + u * 32u);
+        }
+    }
+    for (; c < c_end; c += 32u) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0);
+        const __half *h = reinterpret_cast<const __half *>(&v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) amax_merge(bv[k], bi[k], __half2float(h[k]), c);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        sv[grp][q * 8u + k] = bv[k];
+        si[grp][q * 8u + k] = bi[k];
+    }
+    __syncthreads();
+    if (threadIdx.x < 64u) {
+        float v = sv[0][threadIdx.x];
+        uint32_t i = si[0][threadIdx.x];
+        for (int g2 = 1; g2 < 32; ++g2) amax_merge(v, i, sv[g2][threadIdx.x], si[g2][threadIdx.x]);
         const uint64_t o = (uint64_t)blockIdx.y * (gridDim.x * 64u) + blockIdx.x * 64u + threadIdx.x;
         pval[o] = v;
         pidx[o] = i;
@@ -852,8 +967,14 @@ hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __ha
 hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uint32_t D,
                         uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream) {
     if (stride % 64u != 0u || D == 0u) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k44_embed_kernel, dim3(stride / 64u, (D + 63u) / 64u), dim3(256), 0,
-                       stream, y, table, ids, D, vocab, stride, tokens);
+    const dim3 grid(stride / 64u, (D + 63u) / 64u);
+    if (tokens > 0u && D % 8u == 0u && reinterpret_cast<uintptr_t>(table) % 16u == 0u &&
+        reinterpret_cast<uintptr_t>(y) % 16u == 0u)
+        hipLaunchKernelGGL(k44_embed_vec_kernel, grid, dim3(256), 0, stream, y, table, ids, D,
+                           vocab, stride, tokens);
+    else
+        hipLaunchKernelGGL(k44_embed_kernel, grid, dim3(256), 0, stream, y, table, ids, D, vocab,
+                           stride, tokens);
     return hipGetLastError();
 }
 
@@ -902,8 +1023,12 @@ hipError_t launch_argmax(uint32_t *ids, uint32_t *history, uint32_t *step_ctr,
     const uint32_t used = (V + chunk - 1u) / chunk;
     float *pval = scratch;
     uint32_t *pidx = reinterpret_cast<uint32_t *>(scratch + (uint64_t)used * stride);
-    hipLaunchKernelGGL(k44_argmax_partial_kernel, dim3(stride / 64u, used), dim3(256), 0, stream,
-                       pval, pidx, x, V, stride, chunk);
+    if (reinterpret_cast<uintptr_t>(x) % 16u == 0u)
+        hipLaunchKernelGGL(k44_argmax_partial16_kernel, dim3(stride / 64u, used), dim3(256), 0,
+                           stream, pval, pidx, x, V, stride, chunk);
+    else
+        hipLaunchKernelGGL(k44_argmax_partial_kernel, dim3(stride / 64u, used), dim3(256), 0,
+                           stream, pval, pidx, x, V, stride, chunk);
     hipLaunchKernelGGL(k44_argmax_final_kernel, dim3(tokens), dim3(64), 0, stream, ids, history,
                        step_ctr, hist_steps, tokens, pval, pidx, used, stride);
     if (history) hipLaunchKernelGGL(k44_step_inc_kernel, dim3(1), dim3(1), 0, stream, step_ctr);

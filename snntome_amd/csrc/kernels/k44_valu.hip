@@ -95,58 +95,75 @@ hipError_t launch_gather_stream(const GatherDotArgs &a, uint32_t tokens, hipStre
 // Split-K reduction + epilogue: workgroup (x, w) covers threads x*256.. of wave w of the group
 // (grid.y = the group's waves, grid.x = the largest wave's workgroups: the wave is known without
 // a table lookup); thread = (neuron j, 4 tokens); partials summed in z order.  Waves without
-// split-K have no epilogue.
+// split-K have no epilogue.  Every access goes through the global address space (pointers read
+// from the descriptor would otherwise compile to flat accesses), and the cout_map entry, bias
+// and the first 8 partial planes are loaded together, unconditionally (the partial buffer stands
+// in for a null table; planes past the split re-read plane 0, unused), kept as raw bits until all
+// are in flight: a load under a branch makes the compiler wait for it before the next.
 __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp) {
+    typedef const __attribute__((address_space(1))) f4_t gf4;
+    typedef const __attribute__((address_space(1))) uint16_t gu16;
+    typedef const __attribute__((address_space(1))) gd_u2 gu2;
+    typedef __attribute__((address_space(1))) gd_u2 gu2w;
     const MfmaTileArgs a = grp.waves[blockIdx.y];
     const uint32_t groups = a.kgroups, cout = a.cout, tokens = a.tokens;
     if (groups <= 1u) return;
     const uint32_t per_row = tokens / 4u;
     const uint64_t q = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-    if (q >= (uint64_t)cout * per_row) return;
-    const uint32_t j = (uint32_t)(q / per_row), t = (uint32_t)(q - (uint64_t)j * per_row) * 4u;
-    // cout_map entry, bias and the first partials are independent loads: issue them together.
+    const uint64_t nq = (uint64_t)cout * per_row;
+    if (q >= nq) return;
+    uint32_t j, t;
+    if (nq <= 0xffffffffull) {  // 32-bit division (uniform)
+        j = (uint32_t)q / per_row;
+        t = ((uint32_t)q - j * per_row) * 4u;
+    } else {
+        j = (uint32_t)(q / per_row);
+        t = (uint32_t)(q - (uint64_t)j * per_row) * 4u;
+    }
     const uint64_t plane4 = (uint64_t)cout * tokens / 4u;
-    const float4 *p = reinterpret_cast<const float4 *>(a.part + (uint64_t)j * tokens + t);
-    const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-    const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
-    float4 v = p[0];
-    uint32_t z = 1;
-    for (; z + 8u <= groups; z += 8u) {  // 8 partial loads in flight, summed in z order
-        float4 u8[8];
+    gf4 *p = (gf4 *)(a.part + (uint64_t)j * tokens + t);
+    gu16 *cm = (gu16 *)(a.cmap ? (const void *)a.cmap : (const void *)a.part);
+    gu16 *bs = (gu16 *)(a.bias ? (const void *)a.bias : (const void *)a.part);
+    uint32_t cbits = cm[j], bbits = bs[j];
+    constexpr uint32_t U = 8u;
+    f4_t u8[U];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) u8[u] = p[(uint64_t)(z + u) * plane4];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            v.x += u8[u].x;
-            v.y += u8[u].y;
-            v.z += u8[u].z;
-            v.w += u8[u].w;
-        }
+    for (uint32_t u = 0; u < U; ++u) u8[u] = p[(uint64_t)(u < groups ? u : 0u) * plane4];
+    asm volatile("" : "+v"(cbits), "+v"(bbits));
+    f4_t v = u8[0];
+    const uint32_t first = groups < U ? groups : U;
+    for (uint32_t u = 1; u < first; ++u) {  // z order
+        v[0] += u8[u][0];
+        v[1] += u8[u][1];
+        v[2] += u8[u][2];
+        v[3] += u8[u][3];
     }
-    for (; z < groups; ++z) {
-        const float4 u1 = p[(uint64_t)z * plane4];
-        v.x += u1.x;
-        v.y += u1.y;
-        v.z += u1.z;
-        v.w += u1.w;
+    for (uint32_t z = U; z < groups; ++z) {
+        const f4_t u1 = p[(uint64_t)z * plane4];
+        v[0] += u1[0];
+        v[1] += u1[1];
+        v[2] += u1[2];
+        v[3] += u1[3];
     }
+    const uint64_t oj = a.cmap ? (uint64_t)cbits : (uint64_t)j;
+    const float b = a.bias ? __half2float(__ushort_as_half((unsigned short)bbits)) : 0.0f;
     if (a.cmap && oj == K44_CMAP_EMPTY) return;
     const uint64_t o = oj * a.out_stride + tok_y(a, t);  // 4 tokens never cross a 64-token tile
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.R) {
-        const gd_u2 rv = *reinterpret_cast<const gd_u2 *>(a.R + o);
+        const gd_u2 rv = *(gu2 *)(a.R + o);
         const __half *rh = reinterpret_cast<const __half *>(&rv);
 #pragma unroll
         for (int k = 0; k < 4; ++k) r[k] = __half2float(rh[k]);
     }
-    const float acc[4] = {v.x, v.y, v.z, v.w};
+    const float acc[4] = {v[0], v[1], v[2], v[3]};
     __half out[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const float s = acc[k] + b;
         out[k] = __float2half_rn(a.cmap ? apply_act(s + r[k], a.act) : apply_act(s, a.act) + r[k]);
     }
-    *reinterpret_cast<gd_u2 *>(a.Y + o) = *reinterpret_cast<const gd_u2 *>(out);
+    *(gu2w *)(a.Y + o) = *reinterpret_cast<const gd_u2 *>(out);
 }
 
 hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_max, hipStream_t stream) {
