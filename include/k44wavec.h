@@ -255,7 +255,8 @@ int wavec_gpu_read_canvas_2d(void *handle, unsigned long long elem_off, unsigned
  *   index-row order; "wlds" 0 VALU weights read per batch; "t64_ring" 0 | 1 Token64 kernel;
  *   "xcd_order" 0 | 1 | 2 MFMA tile kernels take work items in plain workgroup order, as
  *   contiguous ranges per XCD, or as per-wave shares of every XCD, longest waves first (the
- *   automatic choice).
+ *   automatic choice); "narrow_wgs" >= 1 workgroups a narrow wave of 64/128-neuron tiles is
+ *   split to reach (contraction chunks of >= 16 k-steps).
  * wavec_set_tuning returns -1 for an unknown key or a value < -1; wavec_get_tuning returns the
  * value or -2 for an unknown key. */
 int wavec_set_tuning(const char *key, int value);

@@ -28,6 +28,8 @@ enum class Tune : int {
     Token64Ring,   // "t64_ring":      0 per-wave Token64 kernel, 1 64-neuron ring kernel
     XcdOrder,      // "xcd_order":     0 = MFMA tile kernels take items in workgroup order,
                    //                  1 = contiguous item ranges per XCD, 2 = per-wave shares
+    NarrowWgs,     // "narrow_wgs":    workgroups a narrow wave of >= 64-neuron tiles is split to
+                   //                  reach (>= 1; contraction chunks of >= 16 k-steps)
     Count
 };
 

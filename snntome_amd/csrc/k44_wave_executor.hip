@@ -41,7 +41,8 @@ namespace {
 std::atomic<int> g_tune[(int)Tune::Count];
 const char *const kTuneKeys[(int)Tune::Count] = {
     "path", "dma", "dma_stages", "nt", "splitk", "lane8", "ksplit", "stream_kernel", "narrow",
-    "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring", "xcd_order"};
+    "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring", "xcd_order",
+    "narrow_wgs"};
 struct TuneInit {
     TuneInit() {
         for (auto &v : g_tune) v.store(-1);
@@ -433,10 +434,11 @@ struct K44GpuExecutorState {
                 // decode (per step): 1.196 ms, against 1.219 ms when waves of >= 32 tiles
                 // stay unsplit (fused epilogue), 1.28 ms with 8-k-step chunks, 1.46 ms
                 // without split.
-                const int ce = tune(Tune::NarrowChunk);
+                const int ce = tune(Tune::NarrowChunk), cw = tune(Tune::NarrowWgs);
                 const uint32_t cmax = ce > 0 ? (uint32_t)std::max(16, ce) : 48u;
+                const uint32_t wgs = cw > 0 ? (uint32_t)cw : 128u;
                 want = (ksteps + cmax - 1u) / cmax;
-                want = std::max(want, std::min((128u + (uint32_t)rows - 1u) / (uint32_t)rows,
+                want = std::max(want, std::min((wgs + (uint32_t)rows - 1u) / (uint32_t)rows,
                                                (ksteps + 15u) / 16u));
             } else {
                 // Chunks of 8..16 k-steps (<= 512 rows in LDS), ~256 workgroups per wave.

@@ -23,6 +23,58 @@ namespace k44dev {
 constexpr int NARROW_MAX_ROWS = 512;  // rows of one chunk held in LDS
 constexpr int NARROW_PITCH = 24;      // halves per LDS row (16 tokens + 8 skew)
 
+// Fused epilogue of a whole-contraction chunk: lane holds C[4g + i][t] of BPW 16-neuron blocks,
+// neuron j = j0[bi] + i.  The cout_map entries and biases of all 4 * BPW outputs are loaded in
+// one batch, then the residuals they address in a second, all through the global address space
+// (pointers read from the descriptor would compile to flat accesses, and a load per output under
+// the branch for empty slots makes the compiler wait for each in turn).  Null tables are stood
+// in for by buffers the index is valid in (weights for cout_map / bias, the output for the
+// residual), their values unused.  Arithmetic as in k44_splitk_epilogue_kernel.
+template <int BPW>
+__device__ __forceinline__ void narrow_fused_epilogue(const MfmaTileArgs &a, const f4_t (&acc)[BPW],
+                                                      const uint32_t (&j0)[BPW], uint32_t t) {
+    typedef const __attribute__((address_space(1))) uint16_t gu16;
+    typedef __attribute__((address_space(1))) uint16_t gu16w;
+    gu16 *cm = (gu16 *)(a.cmap ? (const void *)a.cmap : (const void *)a.Wf);
+    gu16 *bs = (gu16 *)(a.bias ? (const void *)a.bias : (const void *)a.Wf);
+    gu16 *rs = (gu16 *)(a.R ? (const void *)a.R : (const void *)a.Y);
+    uint32_t cb[BPW][4], bb[BPW][4], rb[BPW][4];
+    uint64_t o[BPW][4];
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            cb[bi][i] = cm[j0[bi] + (uint32_t)i];
+            bb[bi][i] = bs[j0[bi] + (uint32_t)i];
+        }
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint64_t oj = a.cmap ? (uint64_t)cb[bi][i] : (uint64_t)(j0[bi] + (uint32_t)i);
+            o[bi][i] = (a.cmap && oj == K44_CMAP_EMPTY) ? ~0ull : oj * a.out_stride + t;
+            rb[bi][i] = rs[o[bi][i] == ~0ull ? (uint64_t)t : o[bi][i]];
+        }
+    // every value formed before the first store (a store between a residual load and its use
+    // would be waited for with it: both count on the same counter)
+    uint16_t out[BPW][4];
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float b = a.bias ? __half2float(__ushort_as_half((unsigned short)bb[bi][i])) : 0.0f;
+            const float r = a.R ? __half2float(__ushort_as_half((unsigned short)rb[bi][i])) : 0.0f;
+            const float v = acc[bi][i] + b;
+            out[bi][i] = __half_as_ushort(
+                __float2half_rn(a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r));
+        }
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (o[bi][i] != ~0ull) ((gu16w *)a.Y)[o[bi][i]] = out[bi][i];  // not an empty slot
+}
+
 template <int NT>
 __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
     constexpr int NB = NT / 16;                // 16-neuron blocks per tile
@@ -148,21 +200,11 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
     const uint32_t t = (uint32_t)(lane & 15);
     if (!a.part) {  // whole contraction in this workgroup: fused epilogue
         if (!writer) return;
+        uint32_t j0[BPW];
 #pragma unroll
-        for (int bi = 0; bi < BPW; ++bi) {
-            const uint32_t blk = (uint32_t)(blk0 + BL * bi);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
-                const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-                if (a.cmap && oj == K44_CMAP_EMPTY) continue;
-                const uint64_t o = oj * a.out_stride + t;
-                const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
-                const float r = a.R ? __half2float(a.R[o]) : 0.0f;
-                const float v = acc[bi][i] + b;
-                a.Y[o] = __float2half_rn(a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r);
-            }
-        }
+        for (int bi = 0; bi < BPW; ++bi)
+            j0[bi] = tile * (uint32_t)NT + 16u * (uint32_t)(blk0 + BL * bi) + 4u * (uint32_t)g;
+        narrow_fused_epilogue<BPW>(a, acc, j0, t);
         return;
     }
 
@@ -329,21 +371,11 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
     // Lane holds C[4g + i][lane & 15]: neuron 16*blk + 4g + i, token lane & 15.
     const uint32_t t = (uint32_t)(lane & 15);
     if (!a.part) {
+        uint32_t j0[BPW];
 #pragma unroll
-        for (int bi = 0; bi < BPW; ++bi) {
-            const uint32_t blk = (uint32_t)(wave + 4 * bi);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t j = tile * (uint32_t)NT + 16u * blk + 4u * (uint32_t)g + (uint32_t)i;
-                const uint64_t oj = a.cmap ? (uint64_t)a.cmap[j] : (uint64_t)j;
-                if (a.cmap && oj == K44_CMAP_EMPTY) continue;
-                const uint64_t o = oj * a.out_stride + t;
-                const float b = a.bias ? __half2float(a.bias[j]) : 0.0f;
-                const float r = a.R ? __half2float(a.R[o]) : 0.0f;
-                const float v = acc[bi][i] + b;
-                a.Y[o] = __float2half_rn(a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r);
-            }
-        }
+        for (int bi = 0; bi < BPW; ++bi)
+            j0[bi] = tile * (uint32_t)NT + 16u * (uint32_t)(wave + 4 * bi) + 4u * (uint32_t)g;
+        narrow_fused_epilogue<BPW>(a, acc, j0, t);
         return;
     }
 #pragma unroll
