@@ -198,23 +198,65 @@ constexpr int EPI_WAVE_FLOATS = 16 * EPI_PITCH;
 // partials: two 16-byte stores).  Bias and, without a cout_map, the activation are applied
 // before the transpose, the rest after it: the same operations in the same order as
 // mfma_epilogue_direct, so the same results.
+// Memory accesses go through the global address space (the descriptor's pointers would
+// otherwise compile to flat accesses, which also count on the LDS counter: every LDS wait of the
+// transpose would wait for the stores before it).  The cout_map entries of all blocks load in
+// one batch up front, each block's biases and residual rows together before its transpose (null
+// tables stood in for by the weights or the output, unused).
 template <int NT, int ACT>
 __device__ __forceinline__ void mfma_epilogue_lds(const MfmaTileArgs &a,
                                                   const f4_t (&acc)[NT / 16][4], uint32_t tile,
                                                   uint32_t tok0, uint32_t zgroup, int lane,
                                                   int wave, float *ws) {
+    typedef const __attribute__((address_space(1))) uint16_t gu16;
+    typedef const __attribute__((address_space(1))) gd_u2 gu2;
+    typedef const __attribute__((address_space(1))) u4_t gu4;
+    typedef __attribute__((address_space(1))) u4_t gu4w;
+    typedef __attribute__((address_space(1))) f4_t gf4w;
     constexpr int NB = NT / 16;
     const int g = lane >> 4, c = lane & 15;
     const bool split = a.part != nullptr, mapped = a.cmap != nullptr;
     const uint32_t t_wave = tok0 + (uint32_t)wave * 64u;
     const int ch = lane & 7;  // read side: 8-token chunk of the lane
+    const uint32_t t = t_wave + 8u * (uint32_t)ch;
+    const uint32_t j_tile = tile * (uint32_t)NT;
+    // cout_map entries of the read side (neurons 8q + lane / 8 of each block), all blocks
+    uint32_t cb[NB][2];
+    {
+        gu16 *cm = (gu16 *)(mapped ? (const void *)a.cmap : (const void *)a.Wf);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                cb[nb][q] = cm[j_tile + 16u * nb + 8u * q + (uint32_t)(lane >> 3)];
+    }
+    const uint16_t *bsrc = (const uint16_t *)(a.bias ? (const void *)a.bias : (const void *)a.Wf);
+    const uint64_t ty = split ? 0u : tok_y(a, t);
+    // output offset of read-side row q of block nb, ~0 for an empty slot of a pattern-sorted tile
+    auto out_off = [&](int nb, int q) -> uint64_t {
+        const uint32_t j = j_tile + 16u * nb + 8u * q + (uint32_t)(lane >> 3);
+        const uint64_t oj = mapped ? (uint64_t)cb[nb][q] : (uint64_t)j;
+        return (mapped && oj == K44_CMAP_EMPTY) ? ~0ull : oj * a.out_stride + ty;
+    };
+    const __half *rbase = a.R ? a.R : a.Y;  // without a residual: the output stands in (unused)
+    auto res_load = [&](int nb, u4_t (&r)[2]) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint64_t o = out_off(nb, q);
+            r[q] = *(gu4 *)(rbase + (o == ~0ull ? 0u : o));
+        }
+    };
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
+        // this block's biases (neurons 4g .. 4g+3: one 8-byte load) and residual rows, together
+        const gd_u2 bb = *(gu2 *)(bsrc + j_tile + 16u * nb + 4u * (uint32_t)g);
+        u4_t rcur[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        if (!split && a.R) res_load(nb, rcur);  // in flight during the transpose
         // write: lane holds neurons 4g..4g+3 of block nb, tokens 16 tb + c
+        const __half *bh = reinterpret_cast<const __half *>(&bb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t j = tile * (uint32_t)NT + 16u * nb + 4u * (uint32_t)g + (uint32_t)i;
-            const float b = (!split && a.bias) ? __half2float(a.bias[j]) : 0.0f;
+            const float b = (!split && a.bias) ? __half2float(bh[i]) : 0.0f;
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
                 float v = acc[nb][tb][i];
@@ -232,21 +274,17 @@ __device__ __forceinline__ void mfma_epilogue_lds(const MfmaTileArgs &a,
             const int n = 8 * q + (lane >> 3);
             const f4_t v0 = *reinterpret_cast<const f4_t *>(&ws[n * EPI_PITCH + 8 * ch]);
             const f4_t v1 = *reinterpret_cast<const f4_t *>(&ws[n * EPI_PITCH + 8 * ch + 4]);
-            const uint32_t j = tile * (uint32_t)NT + 16u * nb + (uint32_t)n;
-            const uint32_t t = t_wave + 8u * (uint32_t)ch;
             if (split) {
-                float *pz = a.part + ((uint64_t)zgroup * a.cout + j) * a.tokens + t;
-                reinterpret_cast<f4_t *>(pz)[0] = v0;
-                reinterpret_cast<f4_t *>(pz)[1] = v1;
+                const uint32_t j = j_tile + 16u * nb + (uint32_t)n;
+                gf4w *pz = (gf4w *)(a.part + ((uint64_t)zgroup * a.cout + j) * a.tokens + t);
+                pz[0] = v0;
+                pz[1] = v1;
                 continue;
             }
-            const uint64_t oj = mapped ? (uint64_t)a.cmap[j] : (uint64_t)j;
-            if (mapped && oj == K44_CMAP_EMPTY) continue;  // empty slot of a pattern-sorted tile
-            const uint64_t o = oj * a.out_stride + tok_y(a, t);
+            const uint64_t o = out_off(nb, q);
+            if (o == ~0ull) continue;  // empty slot of a pattern-sorted tile
             const float vv[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            u4_t rr = {0u, 0u, 0u, 0u};
-            if (a.R) rr = *reinterpret_cast<const u4_t *>(a.R + o);
-            const __half *rh = reinterpret_cast<const __half *>(&rr);
+            const __half *rh = reinterpret_cast<const __half *>(&rcur[q]);
             u4_t out;
             __half *oh = reinterpret_cast<__half *>(&out);
 #pragma unroll
@@ -255,7 +293,7 @@ __device__ __forceinline__ void mfma_epilogue_lds(const MfmaTileArgs &a,
                 const float y = mapped ? act_c<ACT>(vv[k] + r) : vv[k] + r;
                 oh[k] = __float2half_rn(y);
             }
-            *reinterpret_cast<u4_t *>(a.Y + o) = out;
+            *(gu4w *)(a.Y + o) = out;
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
