@@ -162,7 +162,18 @@ __global__ __launch_bounds__(256 * NBK) void k44_token64_ring_kernel(Token64Args
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wt = wave % TW, wb = wave / TW;  // tile and 64-neuron block of this wave
-    const uint32_t jw = blockIdx.x * 64u * NBK;  // first neuron of the workgroup
+    // Workgroup p runs on XCD p % 8.  The workgroups of one cluster gather the same rows: when
+    // the grid allows, they are placed 8 apart (p = 8 * (bpc * q + h) + r holds block h of
+    // cluster 8q + r), so they share one XCD's L2 instead of each XCD fetching the rows.
+    uint32_t bx = blockIdx.x;
+    {
+        const uint32_t bpc = a.cluster / (64u * NBK);  // workgroups per cluster
+        if (bpc > 1u && gridDim.x % (8u * bpc) == 0u) {
+            const uint32_t r = bx & 7u, rest = bx >> 3, h = rest % bpc, q = rest / bpc;
+            bx = bpc * (8u * q + r) + h;
+        }
+    }
+    const uint32_t jw = bx * 64u * NBK;  // first neuron of the workgroup
     const uint32_t j0 = jw + 64u * (uint32_t)wb;  // first neuron of this wave
     const uint32_t tile = blockIdx.y * TW + (uint32_t)wt;
     const uint32_t B = a.B_vec16 * 16u, ksteps = B / 32u;
