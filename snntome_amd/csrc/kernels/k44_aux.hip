@@ -515,32 +515,37 @@ __global__ __launch_bounds__(256) void k44_token_shift_prefill_kernel(
 #pragma unroll
     for (int k = 0; k < 8; ++k) near_end = near_end || pos_k[k] + RF > seq_len;
     for (uint32_t c0 = blockIdx.y * TS_CPC; c0 < D; c0 += gridDim.y * TS_CPC) {
+        // Every load of the channel block is issued before any value is used, without
+        // branches around them (the first octet reads its own tokens as the "previous" ones and
+        // drops them, channels past D read row D - 1): a load under a divergent branch, or one
+        // converted right away, would be waited for before the next is issued.
         uint4 cur[TS_CPC], prv[TS_CPC];
-        float m[TS_CPC][RF];
+        uint32_t mb[TS_CPC][RF];
+        const uint16_t *mu16 = reinterpret_cast<const uint16_t *>(mu);
 #pragma unroll
         for (uint32_t j = 0; j < TS_CPC; ++j) {
-            const uint32_t c = c0 + j;
-            cur[j] = prv[j] = uint4{0u, 0u, 0u, 0u};
-            if (c < D) {
-                const __half *xr = x + (uint64_t)c * stride;
-                cur[j] = *reinterpret_cast<const uint4 *>(xr + t0);
-                if (t0) prv[j] = *reinterpret_cast<const uint4 *>(xr + t0 - 8u);
-            }
+            const uint32_t c = c0 + j < D ? c0 + j : D - 1u;
+            const __half *xr = x + (uint64_t)c * stride;
+            cur[j] = *reinterpret_cast<const uint4 *>(xr + t0);
+            prv[j] = *reinterpret_cast<const uint4 *>(xr + (t0 ? t0 - 8u : t0));
 #pragma unroll
-            for (uint32_t i = 0; i < RF; ++i)
-                m[j][i] = c < D ? __half2float(mu[(uint64_t)c * RF + i]) : 0.0f;
+            for (uint32_t i = 0; i < RF; ++i) mb[j][i] = mu16[(uint64_t)c * RF + i];
         }
 #pragma unroll
         for (uint32_t j = 0; j < TS_CPC; ++j) {
             const uint32_t c = c0 + j;
             if (c >= D) break;
-            float w[16];  // w[8 + k] = x[t0 + k], w[k] = x[t0 - 8 + k]
+            float m[RF];
+#pragma unroll
+            for (uint32_t i = 0; i < RF; ++i)
+                m[i] = __half2float(__ushort_as_half((unsigned short)mb[j][i]));
+            float w[16];  // w[8 + k] = x[t0 + k], w[k] = x[t0 - 8 + k] (zero before the stride)
             const __half *hc = reinterpret_cast<const __half *>(&cur[j]);
             const __half *hp = reinterpret_cast<const __half *>(&prv[j]);
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 w[8 + k] = __half2float(hc[k]);
-                w[k] = __half2float(hp[k]);
+                w[k] = t0 ? __half2float(hp[k]) : 0.0f;
             }
             uint4 o;
             __half *oh = reinterpret_cast<__half *>(&o);
@@ -548,10 +553,10 @@ __global__ __launch_bounds__(256) void k44_token_shift_prefill_kernel(
             for (int k = 0; k < 8; ++k) {
                 float acc = 0.0f;
                 if (t0 + (uint32_t)k < tokens) {
-                    acc = m[j][0] * w[8 + k];
+                    acc = m[0] * w[8 + k];
 #pragma unroll
                     for (uint32_t i = 1; i < RF; ++i)
-                        if (i <= pos_k[k]) acc = fmaf(m[j][i], w[8 + k - i], acc);
+                        if (i <= pos_k[k]) acc = fmaf(m[i], w[8 + k - i], acc);
                 }
                 oh[k] = f16_of(acc);
             }

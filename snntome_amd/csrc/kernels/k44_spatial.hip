@@ -44,17 +44,17 @@ __global__ __launch_bounds__(256) void k44_gather_tile_kernel(GatherTileArgs a) 
         for (uint32_t p0 = g; p0 < P; p0 += 16u) {
             uint64_t v[4];
             float w[4];
+            // every lane loads (positions past the row read its last position, replaced by zero
+            // after the load): a load under the divergent branch would be waited for alone
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const uint32_t p = p0 + 4u * (uint32_t)u;
-                if (p < P) {
-                    const uint32_t k = p / a.S, s = p - k * a.S;
-                    v[u] = load4_any(a.X, seg[k] + (uint64_t)s * a.step + tx);
-                    w[u] = __half2float(wj[p]);
-                } else {
-                    v[u] = 0u;
-                    w[u] = 0.0f;
-                }
+                const uint32_t pc = p < P ? p : P - 1u;
+                const uint32_t k = pc / a.S, s = pc - k * a.S;
+                const uint64_t vl = load4_any(a.X, seg[k] + (uint64_t)s * a.step + tx);
+                const float wl = __half2float(wj[pc]);
+                v[u] = p < P ? vl : 0u;
+                w[u] = p < P ? wl : 0.0f;
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) fma4_u64(acc, w[u], v[u]);
