@@ -683,3 +683,21 @@ def test_standalone_argmax_on_device_buffers(wavec, V, stride, tokens):
     wavec.device_synchronize()
     got = ids.download(np.uint32, tokens)
     assert np.array_equal(got, lo.argmax(x, tokens))
+
+
+@pytest.mark.parametrize("V,stride,tokens", [(32000, 64, 16), (1000, 128, 100)])
+def test_standalone_argmax_unaligned_logits(wavec, V, stride, tokens):
+    """Logits 8 bytes past a 16-byte boundary take the 8-byte-load pass: same ids (lowest
+    index on ties) as for aligned logits."""
+    rng = np.random.default_rng(V + 7 * tokens)
+    x = (rng.standard_normal((V, stride)) * 3).astype(np.float16)
+    for t in range(0, tokens, 3):
+        cs = np.sort(rng.choice(V, size=3, replace=False))
+        x[cs, t] = np.float16(25.0)
+    padded = np.concatenate([np.zeros(4, np.float16), x.ravel()])  # 4 halves = 8 bytes
+    X = wavec.DeviceBuffer.from_array(padded)
+    ids = wavec.DeviceBuffer(tokens * 4)
+    wavec.argmax_f16(ids, X.ptr + 8, V, stride, tokens)
+    wavec.device_synchronize()
+    got = ids.download(np.uint32, tokens)
+    assert np.array_equal(got, lo.argmax(x, tokens))
