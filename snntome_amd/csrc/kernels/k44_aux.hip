@@ -734,7 +734,11 @@ __global__ __launch_bounds__(256) void k44_argmax_partial_kernel(
 }
 
 // Pass 1 with 16-byte loads (16-byte aligned logits): 8 lanes per 64-token row, each owning 8
-// tokens; the 32 row groups of the workgroup stride the chunk, 8 rows in flight per thread.
+// tokens; the 32 row groups of the workgroup stride the chunk, UNR rows in flight per thread.
+// Measured on the config-5 prefill logits (32,000 x 8,192, 512 workgroups): 4 rows in flight
+// 85 us, 8 rows 102 us, 16 rows 115 us; a decode chunk (8 rows per thread) takes 8 (one round
+// trip).
+template <uint32_t UNR>
 __global__ __launch_bounds__(256) void k44_argmax_partial16_kernel(
     float *__restrict__ pval, uint32_t *__restrict__ pidx, const __half *__restrict__ x,
     uint32_t V, uint32_t stride, uint32_t chunk) {
@@ -750,7 +754,6 @@ __global__ __launch_bounds__(256) void k44_argmax_partial16_kernel(
         bv[k] = -INFINITY;
         bi[k] = 0xffffffffu;
     }
-    constexpr uint32_t UNR = 8;
     uint32_t c = c_begin + grp;
     for (; c + (UNR - 1u) * 32u < c_end; c += UNR * 32u) {
         uint4 v[UNR];
@@ -1028,8 +1031,11 @@ hipError_t launch_argmax(uint32_t *ids, uint32_t *history, uint32_t *step_ctr,
     const uint32_t used = (V + chunk - 1u) / chunk;
     float *pval = scratch;
     uint32_t *pidx = reinterpret_cast<uint32_t *>(scratch + (uint64_t)used * stride);
-    if (reinterpret_cast<uintptr_t>(x) % 16u == 0u)
-        hipLaunchKernelGGL(k44_argmax_partial16_kernel, dim3(stride / 64u, used), dim3(256), 0,
+    if (reinterpret_cast<uintptr_t>(x) % 16u == 0u && chunk <= 8u * 32u)
+        hipLaunchKernelGGL(k44_argmax_partial16_kernel<8>, dim3(stride / 64u, used), dim3(256), 0,
+                           stream, pval, pidx, x, V, stride, chunk);
+    else if (reinterpret_cast<uintptr_t>(x) % 16u == 0u)
+        hipLaunchKernelGGL(k44_argmax_partial16_kernel<4>, dim3(stride / 64u, used), dim3(256), 0,
                            stream, pval, pidx, x, V, stride, chunk);
     else
         hipLaunchKernelGGL(k44_argmax_partial_kernel, dim3(stride / 64u, used), dim3(256), 0,
