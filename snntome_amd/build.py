@@ -22,6 +22,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-result",
     # Packed fp32 (v_pk_*_f32) code generation stays off on this pool.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading scalar and pointer kernel arguments arrive preloaded in SGPRs (gfx950 kernarg
+    # preload), so a kernel's first dependent load does not wait for a kernarg-segment read.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     f"-I{CSRC}",
     f"-I{HERE.parent / 'include'}",
 ]

@@ -10,9 +10,9 @@ hipError_t launch_mfma_dma(const MfmaGroup &a, uint32_t nt, uint32_t items, hipS
     const dim3 grid(items, 1u, 1u), block(512u, 1u, 1u);
 #define K44_DMA(NT, B)                                                                          \
     if (shape.stream_loads)                                                                     \
-        hipLaunchKernelGGL((k44_mfma_dma_kernel<NT, true, B>), grid, block, 0, stream, a);      \
+        hipLaunchKernelGGL((k44_mfma_dma_kernel<NT, true, B>), grid, block, 0, stream, K44_GROUP_ARGS(a));      \
     else                                                                                        \
-        hipLaunchKernelGGL((k44_mfma_dma_kernel<NT, false, B>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((k44_mfma_dma_kernel<NT, false, B>), grid, block, 0, stream, K44_GROUP_ARGS(a));
     if (nt == 32u && shape.nbuf == 4u) {
         K44_DMA(32, 4)
     } else if (nt == 32u && shape.nbuf == 2u) {

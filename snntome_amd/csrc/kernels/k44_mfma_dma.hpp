@@ -104,7 +104,8 @@ __device__ __forceinline__ h4_t ds_read_tr16_at(uint32_t addr) {
 // NT = 128 (a 128-neuron tile: twice the MFMA work per gathered stage; 128 accumulator registers
 // per lane, so one workgroup per CU) takes a 3-stage ring (125 KiB of LDS, 2 stages in flight).
 template <int NT, bool NTX, int NBUF = 4>
-__global__ __launch_bounds__(512) void k44_mfma_dma_kernel(MfmaGroup grp) {
+__global__ __launch_bounds__(512) void k44_mfma_dma_kernel(K44_GROUP_PARAMS) {
+    K44_GROUP_BIND;
     static_assert(NT == 32 || NT == 64 || NT == 128,
                   "A-fragment stage must be whole dword loads per wave");
     constexpr int MT = 512, ROWS = 32;

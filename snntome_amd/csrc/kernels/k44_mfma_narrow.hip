@@ -76,7 +76,8 @@ __device__ __forceinline__ void narrow_fused_epilogue(const MfmaTileArgs &a, con
 }
 
 template <int NT>
-__global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
+__global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(K44_GROUP_PARAMS) {
+    K44_GROUP_BIND;
     constexpr int NB = NT / 16;                // 16-neuron blocks per tile
     constexpr int BL = NB < 4 ? NB : 4;        // distinct blocks handled at once by the 4 waves
     constexpr int KW = 4 / BL;                 // waves sharing a block (split k-steps)
@@ -113,8 +114,8 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
         const uint32_t k2 = min(ks_begin + (uint32_t)kw + (uint32_t)u * KW, ks_end - 1u);
 #pragma unroll
         for (int i = 0; i < BPW; ++i)
-            af[u][i] = *(const __attribute__((address_space(1))) h8_t *)(
-                wf + ((uint64_t)k2 * NB + blk0 + BL * i) * 64);
+            af[u][i] = __builtin_nontemporal_load((const __attribute__((address_space(1))) h8_t *)(
+                wf + ((uint64_t)k2 * NB + blk0 + BL * i) * 64));
     }
 
     // X rows [r0, r0 + nrows) of the tile's index row, 16 tokens each, into LDS.  Pass q of a
@@ -159,8 +160,9 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
                 const uint32_t k2 = min(ks + (uint32_t)u * KW, ks_end - 1u);
 #pragma unroll
                 for (int i = 0; i < BPW; ++i)
-                    af[u][i] = *(const __attribute__((address_space(1))) h8_t *)(
-                        wf + ((uint64_t)k2 * NB + blk0 + BL * i) * 64);
+                    af[u][i] = __builtin_nontemporal_load(
+                        (const __attribute__((address_space(1))) h8_t *)(
+                            wf + ((uint64_t)k2 * NB + blk0 + BL * i) * 64));
             }
         }
 #pragma unroll
@@ -233,7 +235,8 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(MfmaGroup grp) {
 // BYY: grid (largest wave's workgroups) x (waves): the wave is blockIdx.y, known without a
 // lookup in the group's prefix sums; workgroups past a wave's own count exit at once.
 template <int NT, int PROD, bool BYY>
-__global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp) {
+__global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PARAMS) {
+    K44_GROUP_BIND;
     constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16;
     static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][NARROW_MAX_ROWS][NARROW_PITCH];
@@ -262,7 +265,8 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(MfmaGroup grp
                           (uint64_t)tile * a.ksteps * NB * 64 + lane);
     auto load_a = [&](uint32_t k2, h8_t (&f)[BPW]) {
 #pragma unroll
-        for (int i = 0; i < BPW; ++i) f[i] = wf[((uint64_t)k2 * NB + wave + 4 * i) * 64];
+        for (int i = 0; i < BPW; ++i)
+            f[i] = __builtin_nontemporal_load(&wf[((uint64_t)k2 * NB + wave + 4 * i) * 64]);
     };
 
     // X rows of sub-chunk s: wave pass q covers 32 rows starting at a multiple of 32 (one
@@ -401,12 +405,12 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
     const dim3 grid_y(max_items, g.n);
 #define K44_NL(N, P)                                                                               \
     if (byy)                                                                                       \
-        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, true>), grid_y, block, 0, stream, g); \
+        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, true>), grid_y, block, 0, stream, K44_GROUP_ARGS(g)); \
     else                                                                                           \
-        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, false>), grid, block, 0, stream, g);
+        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, false>), grid, block, 0, stream, K44_GROUP_ARGS(g));
     switch (nt) {
-    case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, g); break;
-    case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, g); break;
+    case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, K44_GROUP_ARGS(g)); break;
+    case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, K44_GROUP_ARGS(g)); break;
     case 64u:
         if (prod == 3u) {
             K44_NL(64, 3)

@@ -10,7 +10,7 @@ hipError_t launch_mfma_tile_nt128(const MfmaGroup &a, uint32_t mt, uint32_t rows
 #define K44_MFMA_CASE(MT)                                                                       \
     case MT:                                                                                    \
         if (rows_per_stage != 32u) return hipErrorInvalidValue;                                 \
-        hipLaunchKernelGGL((k44_mfma_tile_kernel<128, MT, 32>), grid, block, 0, stream, a);     \
+        hipLaunchKernelGGL((k44_mfma_tile_kernel<128, MT, 32>), grid, block, 0, stream, K44_GROUP_ARGS(a));     \
         break;
     switch (mt) {
         K44_MFMA_CASE(512u)

@@ -9,9 +9,9 @@ hipError_t launch_mfma_tile_nt64(const MfmaGroup &a, uint32_t mt, uint32_t rows_
 #define K44_MFMA_CASE(MT)                                                                       \
     case MT:                                                                                    \
         if (rows_per_stage == 64u)                                                              \
-            hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 64>), grid, block, 0, stream, a); \
+            hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 64>), grid, block, 0, stream, K44_GROUP_ARGS(a)); \
         else                                                                                    \
-            hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 32>), grid, block, 0, stream, a); \
+            hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 32>), grid, block, 0, stream, K44_GROUP_ARGS(a)); \
         break;
     switch (mt) {
         K44_MFMA_CASE(512u)

@@ -99,6 +99,15 @@ struct MfmaGroup {
     uint32_t xcd_order;         // 0 plain, 1 contiguous per XCD, 2 per-wave shares (group_item_wave)
 };
 
+// Group kernels take the four MfmaGroup fields as separate scalar parameters: the build preloads
+// leading scalar kernel arguments into SGPRs at dispatch (-amdgpu-kernarg-preload-count), while
+// an aggregate parameter is read from the kernel-argument segment by a load every wave of the
+// launch waits for before its first dependent (descriptor) load.
+#define K44_GROUP_PARAMS \
+    const MfmaTileArgs *grp_waves, const uint32_t *grp_start, uint32_t grp_n, uint32_t grp_xcd
+#define K44_GROUP_ARGS(g) (g).waves, (g).start, (g).n, (g).xcd_order
+#define K44_GROUP_BIND const MfmaGroup grp{grp_waves, grp_start, grp_n, grp_xcd}
+
 // Per-wave shares of the 8 XCDs (xcd_order 2), host and device.  Workgroup b runs on XCD
 // x = b % 8 as that XCD's s-th workgroup, s = b / 8.  Every wave w of the group (items
 // [start[w], start[w+1]), cnt = 8q + r) gives each XCD a contiguous share of its items: q, plus
@@ -316,7 +325,8 @@ __device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a,
 }
 
 template <int NT, int MT, int ROWS>
-__global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(MfmaGroup grp) {
+__global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(K44_GROUP_PARAMS) {
+    K44_GROUP_BIND;
     uint32_t w;
     const uint32_t item = group_item_wave(grp, w);
     const MfmaTileArgs a = grp.waves[w];

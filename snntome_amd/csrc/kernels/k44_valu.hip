@@ -100,7 +100,8 @@ hipError_t launch_gather_stream(const GatherDotArgs &a, uint32_t tokens, hipStre
 // and the first 8 partial planes are loaded together, unconditionally (the partial buffer stands
 // in for a null table; planes past the split re-read plane 0, unused), kept as raw bits until all
 // are in flight: a load under a branch makes the compiler wait for it before the next.
-__global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp) {
+__global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(K44_GROUP_PARAMS) {
+    K44_GROUP_BIND;
     typedef const __attribute__((address_space(1))) f4_t gf4;
     typedef const __attribute__((address_space(1))) uint16_t gu16;
     typedef const __attribute__((address_space(1))) gd_u2 gu2;
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(MfmaGroup grp)
 
 hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_max, hipStream_t stream) {
     if (epi_max == 0u) return hipSuccess;
-    hipLaunchKernelGGL(k44_splitk_epilogue_kernel, dim3(epi_max, g.n), dim3(256), 0, stream, g);
+    hipLaunchKernelGGL(k44_splitk_epilogue_kernel, dim3(epi_max, g.n), dim3(256), 0, stream, K44_GROUP_ARGS(g));
     return hipGetLastError();
 }
 
