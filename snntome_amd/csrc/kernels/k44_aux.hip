@@ -48,6 +48,8 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
     // Fused token shift: octets without requests only write zeros; the mixing weights and the
     // state of the thread's channel are loaded here too.
     if constexpr (RF > 0u) {
+        // the shift's kernel arguments are read before the branch (one round trip, not two)
+        asm volatile("" ::"s"(sh.tokens), "s"(sh.y2), "s"(sh.mu), "s"(sh.state));
         if (t0 >= sh.tokens) {
             if (c_own < c_end)
                 *reinterpret_cast<uint4 *>(sh.y2 + (uint64_t)c_own * stride + t0) =

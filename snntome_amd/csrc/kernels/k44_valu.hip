@@ -107,6 +107,11 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(K44_GROUP_PARA
     typedef const __attribute__((address_space(1))) gd_u2 gu2;
     typedef __attribute__((address_space(1))) gd_u2 gu2w;
     const MfmaTileArgs a = grp.waves[blockIdx.y];
+    // Every descriptor field the kernel reads is loaded before its first branch: a scalar load
+    // placed after a uniform branch is issued only once the branch resolves, one round trip
+    // to the descriptor per branch.
+    asm volatile("" ::"s"(a.kgroups), "s"(a.cout), "s"(a.tokens), "s"(a.part), "s"(a.cmap),
+                 "s"(a.bias), "s"(a.R), "s"(a.Y), "s"(a.out_stride), "s"(a.act), "s"(a.tile_y));
     const uint32_t groups = a.kgroups, cout = a.cout, tokens = a.tokens;
     if (groups <= 1u) return;
     const uint32_t per_row = tokens / 4u;
