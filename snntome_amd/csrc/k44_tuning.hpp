@@ -30,6 +30,8 @@ enum class Tune : int {
                    //                  1 = contiguous item ranges per XCD, 2 = per-wave shares
     NarrowWgs,     // "narrow_wgs":    workgroups a narrow wave of >= 64-neuron tiles is split to
                    //                  reach (>= 1; contraction chunks of >= 16 k-steps)
+    NarrowReduce,  // "narrow_reduce": 0 = split narrow waves reduce in k44_splitk_epilogue_kernel,
+                   //                  1 = the last workgroup of each tile reduces in the launch
     Count
 };
 

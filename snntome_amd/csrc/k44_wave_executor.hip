@@ -42,7 +42,36 @@ std::atomic<int> g_tune[(int)Tune::Count];
 const char *const kTuneKeys[(int)Tune::Count] = {
     "path", "dma", "dma_stages", "nt", "splitk", "lane8", "ksplit", "stream_kernel", "narrow",
     "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring", "xcd_order",
-    "narrow_wgs"};
+    "narrow_wgs", "narrow_reduce"};
+// Values each switch honours besides -1: a set of small values (bit v of `set`), or every
+// value >= `min` when `set` is 0.  Anything else is refused, so an A/B run cannot measure a
+// configuration other than the one it asked for.
+struct TuneValues {
+    uint32_t set;
+    int min;
+};
+constexpr uint32_t V01 = 0x3u;
+const TuneValues kTuneValues[(int)Tune::Count] = {
+    {V01, 0},          // path 0 | 1
+    {V01, 0},          // dma
+    {0x14u, 0},        // dma_stages 2 | 4
+    {V01, 0},          // nt
+    {V01, 0},          // splitk
+    {V01, 0},          // lane8
+    {0x12u, 0},        // ksplit 1 | 4
+    {V01, 0},          // stream_kernel
+    {V01, 0},          // narrow
+    {0u, 16},          // narrow_chunk >= 16
+    {V01, 0},          // group
+    {V01, 0},          // group_split
+    {V01, 0},          // fuse
+    {V01, 0},          // sort
+    {V01, 0},          // wlds
+    {V01, 0},          // t64_ring
+    {0x7u, 0},         // xcd_order 0 | 1 | 2
+    {0u, 1},           // narrow_wgs >= 1
+    {V01, 0},          // narrow_reduce
+};
 struct TuneInit {
     TuneInit() {
         for (auto &v : g_tune) v.store(-1);
@@ -144,6 +173,11 @@ struct WaveExec {
     uint64_t y_off_run = 0;
     std::vector<std::pair<uint64_t, uint64_t>> rd_run, wr_run;
     size_t part_floats = 0;  // split-K partials (kgroups * cout * tokens), 0 without split-K
+    // Narrow 64/128-neuron waves with split-K: whole-plan launches reduce the partials in the
+    // last workgroup of each tile (per-tile arrival counters at arrive + arrive_off) instead of
+    // a second kernel; command-by-command launches keep the epilogue kernel.
+    bool reduce_in_kernel = false;
+    size_t arrive_off = 0;
     // 2-D spatial wave (VALU over the padded-plane tile layout): tile tables, output plane.
     bool tile2d = false;
     DevBuf<uint32_t> tile_x, tile_y;
@@ -264,6 +298,9 @@ struct K44GpuExecutorState {
     // partials of MFMA waves, per-chunk (value, index) partials of ARGMAX.
     DevBuf<float> scratch;
     size_t scratch_need = 0;  // floats
+    // Per-tile arrival counters of the waves that reduce split-K in the launch (zeroed at init;
+    // each launch leaves them at zero).
+    DevBuf<uint32_t> arrive;
     uint64_t fold_elems = 0;  // private region past the canvas for relocated multiply operands
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -302,6 +339,7 @@ struct K44GpuExecutorState {
         canvas.reset();
         scratch.reset();
         scratch_need = 0;
+        arrive.reset();
         fold_elems = 0;
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
@@ -430,13 +468,15 @@ struct K44GpuExecutorState {
             if (cl >= 64u) {
                 // Tiles of whole 16-neuron blocks per wave: chunks of any length, streamed
                 // in 16-k-step sub-chunks.  Chunks of at most 48 k-steps; split further, down
-                // to 16 k-steps, until the wave has ~128 workgroups.  Measured on config-5
-                // decode (per step): 1.196 ms, against 1.219 ms when waves of >= 32 tiles
-                // stay unsplit (fused epilogue), 1.28 ms with 8-k-step chunks, 1.46 ms
-                // without split.
+                // to 16 k-steps, until the wave has ~64 workgroups (~128 when a second kernel
+                // reduces the partials).  Measured on config-5 decode (ms per step, graph
+                // replays, alternated in one process): partials reduced by the tile's last
+                // workgroup 0.869 at 64 workgroups, 0.889 at 32, 0.941 at 128, 0.968 unsplit
+                // beyond 48 k-steps; reduced by the epilogue kernel 0.928 at 128 or 64.
                 const int ce = tune(Tune::NarrowChunk), cw = tune(Tune::NarrowWgs);
                 const uint32_t cmax = ce > 0 ? (uint32_t)std::max(16, ce) : 48u;
-                const uint32_t wgs = cw > 0 ? (uint32_t)cw : 128u;
+                const uint32_t wgs =
+                    cw > 0 ? (uint32_t)cw : (tune(Tune::NarrowReduce) != 0 ? 64u : 128u);
                 want = (ksteps + cmax - 1u) / cmax;
                 want = std::max(want, std::min((wgs + (uint32_t)rows - 1u) / (uint32_t)rows,
                                                (ksteps + 15u) / 16u));
@@ -450,6 +490,8 @@ struct K44GpuExecutorState {
             wx.stage_chunk = (ksteps + want - 1u) / want;
             wx.kgroups = (ksteps + wx.stage_chunk - 1u) / wx.stage_chunk;
             if (wx.kgroups > 1u) wx.part_floats = (size_t)wx.kgroups * c.Cout * 16u;
+            // Split 64/128-neuron tiles: the tile's last workgroup reduces (no epilogue kernel).
+            wx.reduce_in_kernel = cl >= 64u && wx.kgroups > 1u && tune(Tune::NarrowReduce) != 0;
         } else {
             const uint32_t stages = c.B_raw / wx.rows_per_stage;
             const uint64_t wgs = (uint64_t)rows * (wx.tokens / wx.mt);
@@ -1165,6 +1207,18 @@ struct K44GpuExecutorState {
         K44_HIP(hipEventCreate(&ev1));
         canvas.alloc((plan.canvas_elems + kCanvasSlack + 63u) / 64u * 64u + fold_elems);
         if (scratch_need) scratch.alloc(scratch_need);
+        {
+            size_t n_arrive = 0;
+            for (auto &wp : waves)
+                if (wp->reduce_in_kernel) {
+                    wp->arrive_off = n_arrive;
+                    n_arrive += wp->rows;
+                }
+            if (n_arrive) {
+                arrive.alloc(n_arrive);
+                K44_HIP(hipMemsetAsync(arrive.p, 0, n_arrive * sizeof(uint32_t), stream));
+            }
+        }
         upload_mfma_descriptors();
         K44_HIP(hipMemsetAsync(canvas.p, 0,
                                ((plan.canvas_elems + kCanvasSlack + 63u) / 64u * 64u + fold_elems) * 2u,
@@ -1669,6 +1723,7 @@ struct K44GpuExecutorState {
         else  // chunk in stages of rows_per_stage positions
             a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : a.K * a.S / w.rows_per_stage;
         a.part = w.kgroups > 1u ? part : nullptr;
+        if (fused && w.reduce_in_kernel) a.arrive = arrive.p + w.arrive_off;
         a.cout = w.cout;
         a.tokens = w.part_tokens;
         a.tiles = w.rows;
@@ -1722,7 +1777,7 @@ struct K44GpuExecutorState {
                 args.push_back(mfma_args(w, scratch.p ? scratch.p + off : nullptr, true));
                 off += w.part_floats;
                 start.push_back(start.back() + w.items);
-                epi_max = std::max(epi_max, w.epi_items);
+                if (!w.reduce_in_kernel) epi_max = std::max(epi_max, w.epi_items);
                 item_max = std::max(item_max, w.items);
             }
             g.items = start.back();
@@ -1784,6 +1839,7 @@ struct K44GpuExecutorState {
               << ", \"stream_kernel\": " << (w.stream_kernel ? "true" : "false")
               << ", \"ring_stages\": " << (w.dma ? w.dshape.nbuf : 0u)
               << ", \"xprod\": " << w.xprod
+              << ", \"reduce_in_kernel\": " << (w.reduce_in_kernel ? "true" : "false")
               << ", \"flops\": " << (long long)w.flops
               << ", \"effective_flops\": " << (long long)w.eff_flops
               << ", \"mapped\": " << (w.cmap.p ? "true" : "false")
@@ -2822,7 +2878,21 @@ int wavec_set_tuning(const char *key, int value) {
     return guarded("wavec_set_tuning", [&] {
         for (int i = 0; i < (int)k44_host::Tune::Count; ++i) {
             if (std::string(key) != k44_host::kTuneKeys[i]) continue;
-            if (value < -1) throw std::runtime_error("value must be -1 (automatic) or >= 0");
+            const k44_host::TuneValues &tv = k44_host::kTuneValues[i];
+            const bool ok = value == -1 || (tv.set ? (value >= 0 && value < 32 &&
+                                                      ((tv.set >> value) & 1u))
+                                                   : value >= tv.min);
+            if (!ok) {
+                std::string allowed;
+                if (tv.set) {
+                    for (int v = 0; v < 32; ++v)
+                        if ((tv.set >> v) & 1u) allowed += (allowed.empty() ? "" : " | ") + std::to_string(v);
+                } else {
+                    allowed = ">= " + std::to_string(tv.min);
+                }
+                throw std::runtime_error(std::string("value ") + std::to_string(value) +
+                                         " is not honoured by '" + key + "' (-1 or " + allowed + ")");
+            }
             k44_host::g_tune[i].store(value);
             return 0;
         }

@@ -11,10 +11,12 @@
 //    waves of a block take its k-steps round-robin and meet in LDS in a fixed order;
 //  * A fragments (host-arranged [tile][k-step][16-block][lane][8]) stream from HBM with 8 k-steps
 //    of loads in flight per wave before the first MFMA that needs them;
-//  * one chunk: fused epilogue; several: fp32 partials [z][cout][16], summed in chunk order
-//    (bit-reproducible) by k44_splitk_epilogue_kernel.  (Reducing them in the kernel through a
-//    per-tile arrival counter needs a device-scope release per workgroup — an L2 write-back on
-//    this GPU — and measured 4x slower on decode-sized waves.)
+//  * one chunk: fused epilogue; several: fp32 partials, summed in chunk order (bit-
+//    reproducible) by the last workgroup of the tile to arrive (64 / 128-neuron tiles in
+//    whole-plan runs, narrow_reduce_last) or by k44_splitk_epilogue_kernel.  The in-launch
+//    reduction publishes its partials as device-coherent stores instead of through a release
+//    fence: an agent-scope release is an L2 write-back on this GPU (an earlier design with one
+//    per workgroup measured 4x slower on decode-sized waves).
 // Columns 16..stride-1 of the output rows are not written.
 #include "k44_launch.hpp"
 
@@ -22,6 +24,7 @@ namespace k44dev {
 
 constexpr int NARROW_MAX_ROWS = 512;  // rows of one chunk held in LDS
 constexpr int NARROW_PITCH = 24;      // halves per LDS row (16 tokens + 8 skew)
+typedef float f2_t __attribute__((ext_vector_type(2)));
 
 // Fused epilogue of a whole-contraction chunk: lane holds C[4g + i][t] of BPW 16-neuron blocks,
 // neuron j = j0[bi] + i.  The cout_map entries and biases of all 4 * BPW outputs are loaded in
@@ -30,31 +33,43 @@ constexpr int NARROW_PITCH = 24;      // halves per LDS row (16 tokens + 8 skew)
 // the branch for empty slots makes the compiler wait for each in turn).  Null tables are stood
 // in for by buffers the index is valid in (weights for cout_map / bias, the output for the
 // residual), their values unused.  Arithmetic as in k44_splitk_epilogue_kernel.
+// narrow_epi_load issues the loads (split-K waves issue them before their reduction, so they
+// complete under it), narrow_epi_store forms and stores the outputs.
 template <int BPW>
-__device__ __forceinline__ void narrow_fused_epilogue(const MfmaTileArgs &a, const f4_t (&acc)[BPW],
-                                                      const uint32_t (&j0)[BPW], uint32_t t) {
+struct NarrowEpi {
+    uint32_t bb[BPW][4], rb[BPW][4];
+    uint64_t o[BPW][4];  // output element, ~0 for an empty cout_map slot
+};
+
+template <int BPW>
+__device__ __forceinline__ void narrow_epi_load(const MfmaTileArgs &a, const uint32_t (&j0)[BPW],
+                                                uint32_t t, NarrowEpi<BPW> &e) {
     typedef const __attribute__((address_space(1))) uint16_t gu16;
-    typedef __attribute__((address_space(1))) uint16_t gu16w;
     gu16 *cm = (gu16 *)(a.cmap ? (const void *)a.cmap : (const void *)a.Wf);
     gu16 *bs = (gu16 *)(a.bias ? (const void *)a.bias : (const void *)a.Wf);
     gu16 *rs = (gu16 *)(a.R ? (const void *)a.R : (const void *)a.Y);
-    uint32_t cb[BPW][4], bb[BPW][4], rb[BPW][4];
-    uint64_t o[BPW][4];
+    uint32_t cb[BPW][4];
 #pragma unroll
     for (int bi = 0; bi < BPW; ++bi)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             cb[bi][i] = cm[j0[bi] + (uint32_t)i];
-            bb[bi][i] = bs[j0[bi] + (uint32_t)i];
+            e.bb[bi][i] = bs[j0[bi] + (uint32_t)i];
         }
 #pragma unroll
     for (int bi = 0; bi < BPW; ++bi)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint64_t oj = a.cmap ? (uint64_t)cb[bi][i] : (uint64_t)(j0[bi] + (uint32_t)i);
-            o[bi][i] = (a.cmap && oj == K44_CMAP_EMPTY) ? ~0ull : oj * a.out_stride + t;
-            rb[bi][i] = rs[o[bi][i] == ~0ull ? (uint64_t)t : o[bi][i]];
+            e.o[bi][i] = (a.cmap && oj == K44_CMAP_EMPTY) ? ~0ull : oj * a.out_stride + t;
+            e.rb[bi][i] = rs[e.o[bi][i] == ~0ull ? (uint64_t)t : e.o[bi][i]];
         }
+}
+
+template <int BPW>
+__device__ __forceinline__ void narrow_epi_store(const MfmaTileArgs &a, const f4_t (&acc)[BPW],
+                                                 const NarrowEpi<BPW> &e) {
+    typedef __attribute__((address_space(1))) uint16_t gu16w;
     // every value formed before the first store (a store between a residual load and its use
     // would be waited for with it: both count on the same counter)
     uint16_t out[BPW][4];
@@ -62,8 +77,8 @@ __device__ __forceinline__ void narrow_fused_epilogue(const MfmaTileArgs &a, con
     for (int bi = 0; bi < BPW; ++bi)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float b = a.bias ? __half2float(__ushort_as_half((unsigned short)bb[bi][i])) : 0.0f;
-            const float r = a.R ? __half2float(__ushort_as_half((unsigned short)rb[bi][i])) : 0.0f;
+            const float b = a.bias ? __half2float(__ushort_as_half((unsigned short)e.bb[bi][i])) : 0.0f;
+            const float r = a.R ? __half2float(__ushort_as_half((unsigned short)e.rb[bi][i])) : 0.0f;
             const float v = acc[bi][i] + b;
             out[bi][i] = __half_as_ushort(
                 __float2half_rn(a.cmap ? apply_act(v + r, a.act) : apply_act(v, a.act) + r));
@@ -72,7 +87,101 @@ __device__ __forceinline__ void narrow_fused_epilogue(const MfmaTileArgs &a, con
     for (int bi = 0; bi < BPW; ++bi)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            if (o[bi][i] != ~0ull) ((gu16w *)a.Y)[o[bi][i]] = out[bi][i];  // not an empty slot
+            if (e.o[bi][i] != ~0ull) ((gu16w *)a.Y)[e.o[bi][i]] = out[bi][i];  // not an empty slot
+}
+
+template <int BPW>
+__device__ __forceinline__ void narrow_fused_epilogue(const MfmaTileArgs &a, const f4_t (&acc)[BPW],
+                                                      const uint32_t (&j0)[BPW], uint32_t t) {
+    NarrowEpi<BPW> e;
+    narrow_epi_load<BPW>(a, j0, t, e);
+    narrow_epi_store<BPW>(a, acc, e);
+}
+
+// Split-K reduced inside the launch (a.arrive set; 64 / 128-neuron tiles).  Every workgroup of
+// a tile stores its chunk's partial, then counts itself in at the tile's arrival counter; the
+// workgroup that arrives last sums the kgroups partials in chunk order (the order of
+// k44_splitk_epilogue_kernel, so the outputs are the same bits) and runs the fused epilogue.
+// Visibility without an L2 write-back: the partials are stored and read as agent-scope relaxed
+// atomics (stores and loads marked device-coherent: the other XCDs' L2 caches are not
+// consulted), each wave waits for its stores to complete (vmcnt 0) before the barrier that
+// precedes the counter increment, and the last workgroup reads only after the increment has
+// returned.  An agent-scope release fence would instead write back the whole L2 of the XCD.
+// The last workgroup resets the counter to zero for the next launch (no clearing kernel or
+// memset, so HIP-graph replays need no extra node).  Lane (g, t) holds C[4g + i][t] of BPW
+// 16-neuron blocks; its 4 values of block bi are contiguous in the partial layout
+// [z][cout/4][16][4]: index ((z * cout + j0) * 16 + 4 t + i).
+template <int BPW>
+__device__ __forceinline__ bool narrow_reduce_last(const MfmaTileArgs &a, f4_t (&acc)[BPW],
+                                                   const uint32_t (&j0)[BPW], uint32_t t,
+                                                   uint32_t tile, uint32_t z) {
+    typedef unsigned long long u64;
+    typedef __attribute__((address_space(1))) u64 gu64;
+    typedef __attribute__((address_space(1))) uint32_t gu32;
+    __shared__ uint32_t last;
+    gu64 *pp = (gu64 *)(a.part);
+    gu32 *cnt = (gu32 *)(a.arrive) + tile;
+    auto slot = [&](uint32_t zz, int bi) -> uint64_t {
+        return (((uint64_t)zz * a.cout + j0[bi]) * 16u + 4u * t) >> 1;
+    };
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi) {
+        const uint64_t s = slot(z, bi);
+        __hip_atomic_store(pp + s, __builtin_bit_cast(u64, __builtin_shufflevector(acc[bi], acc[bi], 0, 1)),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + s + 1, __builtin_bit_cast(u64, __builtin_shufflevector(acc[bi], acc[bi], 2, 3)),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores performed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               a.kgroups - 1u;
+    __syncthreads();
+    if (!last) return false;
+    const uint32_t kg = a.kgroups;
+    f4_t sum[BPW];
+    constexpr uint32_t ZB = 8u;  // planes loaded together
+    for (uint32_t z0 = 0; z0 < kg; z0 += ZB) {
+        u64 lo[ZB][BPW], hi[ZB][BPW];
+#pragma unroll
+        for (uint32_t u = 0; u < ZB; ++u) {
+            const uint32_t zz = min(z0 + u, kg - 1u);
+#pragma unroll
+            for (int bi = 0; bi < BPW; ++bi) {
+                const uint64_t s = slot(zz, bi);
+                lo[u][bi] = __hip_atomic_load(pp + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                hi[u][bi] = __hip_atomic_load(pp + s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < ZB; ++u) {
+            const uint32_t zz = z0 + u;
+            if (zz < kg) {
+#pragma unroll
+                for (int bi = 0; bi < BPW; ++bi) {
+                    // this workgroup's own chunk from its registers (the same bits it stored)
+                    const f4_t p = zz == z ? acc[bi]
+                                           : __builtin_shufflevector(
+                                                 __builtin_bit_cast(f2_t, lo[u][bi]),
+                                                 __builtin_bit_cast(f2_t, hi[u][bi]), 0, 1, 2, 3);
+                    if (zz == 0u) {
+                        sum[bi] = p;
+                    } else {
+                        sum[bi][0] += p[0];
+                        sum[bi][1] += p[1];
+                        sum[bi][2] += p[2];
+                        sum[bi][3] += p[3];
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi) acc[bi] = sum[bi];
+    // every workgroup of the tile has arrived: the counter is zero again for the next launch
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
 }
 
 template <int NT>
@@ -380,6 +489,17 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
         for (int bi = 0; bi < BPW; ++bi)
             j0[bi] = tile * (uint32_t)NT + 16u * (uint32_t)(wave + 4 * bi) + 4u * (uint32_t)g;
         narrow_fused_epilogue<BPW>(a, acc, j0, t);
+        return;
+    }
+    if (a.arrive) {  // split-K reduced by the tile's last workgroup, then the fused epilogue
+        uint32_t j0[BPW];
+#pragma unroll
+        for (int bi = 0; bi < BPW; ++bi)
+            j0[bi] = tile * (uint32_t)NT + 16u * (uint32_t)(wave + 4 * bi) + 4u * (uint32_t)g;
+        NarrowEpi<BPW> e;
+        narrow_epi_load<BPW>(a, j0, t, e);  // completes under the reduction's round trips
+        if (!narrow_reduce_last<BPW>(a, acc, j0, t, tile, zgroup)) return;
+        narrow_epi_store<BPW>(a, acc, e);
         return;
     }
 #pragma unroll

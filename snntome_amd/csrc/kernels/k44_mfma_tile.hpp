@@ -78,6 +78,11 @@ struct MfmaTileArgs {
     // 1: Y, R and out_stride are multiples of 8 elements (and split-K partial rows of 4), so
     // the epilogue may use 16-byte accesses (mfma_tile_epilogue_lds).
     uint32_t epi_vec;
+    // Narrow kernels of 64 / 128-neuron tiles with split-K: per-tile arrival counters (zero
+    // between launches).  The last workgroup of a tile to arrive sums the partials in chunk order
+    // and runs the epilogue; partials are then laid out [z][cout/4][16 tokens][4 neurons].
+    // nullptr: partials [z][cout][16] for k44_splitk_epilogue_kernel.
+    uint32_t *arrive;
 };
 
 // Canvas offset of token t of a wave (relative to a segment row or an output row).

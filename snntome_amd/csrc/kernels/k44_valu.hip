@@ -110,10 +110,10 @@ __global__ __launch_bounds__(256) void k44_splitk_epilogue_kernel(K44_GROUP_PARA
     // Every descriptor field the kernel reads is loaded before its first branch: a scalar load
     // placed after a uniform branch is issued only once the branch resolves, one round trip
     // to the descriptor per branch.
-    asm volatile("" ::"s"(a.kgroups), "s"(a.cout), "s"(a.tokens), "s"(a.part), "s"(a.cmap),
+    asm volatile("" ::"s"(a.kgroups), "s"(a.arrive), "s"(a.cout), "s"(a.tokens), "s"(a.part), "s"(a.cmap),
                  "s"(a.bias), "s"(a.R), "s"(a.Y), "s"(a.out_stride), "s"(a.act), "s"(a.tile_y));
     const uint32_t groups = a.kgroups, cout = a.cout, tokens = a.tokens;
-    if (groups <= 1u) return;
+    if (groups <= 1u || a.arrive) return;  // unsplit, or reduced in its own launch
     const uint32_t per_row = tokens / 4u;
     const uint64_t q = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     const uint64_t nq = (uint64_t)cout * per_row;

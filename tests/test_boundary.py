@@ -126,6 +126,16 @@ def test_tuning_switches_set_get_reset(wavec):
         wavec.set_tuning("fuse", -5)
     with pytest.raises(RuntimeError, match="unknown tuning key"):
         wavec.get_tuning("no_such_switch")
+    # values a switch does not honour are refused (the old value stays)
+    wavec.reset_tuning()
+    for key, bad in (("dma_stages", 3), ("ksplit", 2), ("xcd_order", 7), ("path", 2),
+                     ("narrow_chunk", 15), ("narrow_wgs", 0), ("narrow_reduce", 2)):
+        with pytest.raises(RuntimeError, match="not honoured"):
+            wavec.set_tuning(key, bad)
+        assert wavec.get_tuning(key) == -1
+    for key, good in (("dma_stages", 4), ("ksplit", 4), ("xcd_order", 2), ("narrow_reduce", 0)):
+        wavec.set_tuning(key, good)
+        assert wavec.get_tuning(key) == good
     wavec.reset_tuning()
     assert wavec.get_tuning("fuse") == -1 and wavec.get_tuning("narrow_chunk") == -1
 

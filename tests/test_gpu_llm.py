@@ -438,6 +438,51 @@ def test_folded_multiplies_match_unfolded(wavec, tuning):
     assert np.array_equal(out["folded"][1], out["launched"][1])
 
 
+def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
+    """Split narrow waves of 64-neuron tiles reduce their chunk partials in the last workgroup
+    of each tile (per-tile arrival counters, device-coherent partial stores and loads); ids and
+    logits of several decode steps, eager and HIP-graph replays, are bit-identical to the plan
+    whose partials are reduced by the split-K epilogue kernel (narrow_reduce=0), and every
+    counter is back at zero between launches (a later launch sums the right chunks)."""
+    # contractions of 32 k-steps (d-input: 4 of 8 clusters of 256) and 40 (FFN input: 5 of 10):
+    # 2 and 3 chunks of <= 16 k-steps, the last one ragged
+    spec = synth.LLMSpec(layers=2, d=2048, ffn=2560, vocab=1024, S=256, requests=4, prompt=64,
+                         decode_steps=5, seed=13)
+    steps = 5
+    wts = synth.llm_weights(spec)
+    pre = synth.build_llm_graph(spec, wts, decode=False, wavec_mod=wavec).compile()
+    pre.init_gpu()
+    R = spec.requests
+    pre.set_ids(np.random.default_rng(31).integers(0, spec.vocab, R * spec.prompt))
+    pre.execute(1)
+    out = {}
+    for mode in ("kernel", "in_launch"):
+        tuning("narrow_reduce", 0 if mode == "kernel" else 1)
+        tuning("narrow_wgs", 512)  # many chunks per tile: every narrow wave splits
+        p = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
+        p.init_gpu()
+        rep = p.exec_report()
+        split = [w for w in rep["waves"] if w["path"] == "mfma_narrow" and w["ksplit"] > 1]
+        inl = [w for w in split if w["reduce_in_kernel"]]
+        _log(f"[narrow reduce {mode}] {len(split)} split narrow waves, {len(inl)} reduced in "
+             f"their launch, chunks {sorted({w['ksplit'] for w in split})}, "
+             f"{rep['launches_per_run']} launches per run")
+        assert split and len(inl) == (len(split) if mode == "in_launch" else 0)
+        synth.llm_handoff(spec, pre, p)
+        hd = next(c for c in p.cmds if c["name"].split("/")[0] == "head")
+        ids, logits = [], []
+        for s in range(steps):
+            if s == 2:
+                p.use_graph(True)  # steps 2.. as replays of one captured graph
+            p.execute(1)
+            ids.append(p.get_ids(R))
+            logits.append(p.read_canvas(int(hd["y_off"]), spec.vocab * 64))
+        out[mode] = (np.stack(ids), np.stack(logits))
+        p.release_gpu()
+    assert np.array_equal(out["kernel"][0], out["in_launch"][0])
+    assert np.array_equal(out["kernel"][1], out["in_launch"][1])
+
+
 def test_prefill_multiply_chain_matches_launched(wavec, tuning):
     """Prefill plans run m = q*(k*v) as one 3-operand multiply (the inner product k*v is not
     launched); logits and next ids are bit-identical to the plan that launches both multiplies
