@@ -178,6 +178,12 @@ struct WaveExec {
     // a second kernel; command-by-command launches keep the epilogue kernel.
     bool reduce_in_kernel = false;
     size_t arrive_off = 0;
+    // Folded RMSNorm (whole-plan runs): producer of the norm's input (fold index, first slot
+    // of this wave's tiles among the fold's tiles), or consumer gathering the normalised rows
+    // (xprod 4; the fold whose scales it applies).
+    size_t norm_fold = SIZE_MAX;
+    uint32_t norm_tile0 = 0;
+    size_t xnorm = SIZE_MAX;
     // 2-D spatial wave (VALU over the padded-plane tile layout): tile tables, output plane.
     bool tile2d = false;
     DevBuf<uint32_t> tile_x, tile_y;
@@ -241,6 +247,7 @@ struct AuxExec {
     bool fused = false;  // SWIGLU_MUL_1D folded into its consumers' gathers, or TOKEN_SHIFT_1D
                          // run by the RMSNorm before it (not launched)
     size_t shift_with = SIZE_MAX;  // RMSNORM_1D: the decode token shift it runs (whole plans)
+    size_t norm_fold = SIZE_MAX;   // RMSNORM_1D: its scales come from the producers' sums
     // SWIGLU_MUL_1D y = other * q where q = b * c is an inner multiply only this one reads:
     // whole plans run both as y = fp16(other * fp16(b * c)) (the inner one is not launched).
     size_t chain_inner = SIZE_MAX;
@@ -301,6 +308,17 @@ struct K44GpuExecutorState {
     // Per-tile arrival counters of the waves that reduce split-K in the launch (zeroed at init;
     // each launch leaves them at zero).
     DevBuf<uint32_t> arrive;
+    // Folded RMSNorms (fuse_norms): per fold the producers' tile slots (16 tokens x 4 words
+    // each), a tile counter (zero between launches) and 64 per-token scales.
+    struct NormFold {
+        size_t norm = 0;            // aux index of the RMSNORM_1D command
+        uint32_t tiles = 0;         // producer tiles (slots)
+        size_t slot0 = 0;           // first slot in norm_slots
+        bool consumers = false;     // not launched: its readers gather normalised rows
+    };
+    std::vector<NormFold> norm_folds;
+    DevBuf<uint32_t> norm_slots, norm_ctrs;
+    DevBuf<float> norm_invs;
     uint64_t fold_elems = 0;  // private region past the canvas for relocated multiply operands
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -340,6 +358,10 @@ struct K44GpuExecutorState {
         scratch.reset();
         scratch_need = 0;
         arrive.reset();
+        norm_folds.clear();
+        norm_slots.reset();
+        norm_ctrs.reset();
+        norm_invs.reset();
         fold_elems = 0;
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
@@ -1106,8 +1128,13 @@ struct K44GpuExecutorState {
                 const k44dev::RmsShift sh{cv + t.y_off, t.table.p,
                                           t.has_state ? cv + t.state_off : nullptr, t.rf, 0u,
                                           t.decode ? 0u : t.seq_len};
+                const float *inv = a.norm_fold != SIZE_MAX ? norm_invs.p + a.norm_fold * 64u : nullptr;
                 K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
-                                               a.stride, a.tokens, a.eps, stream, &sh));
+                                               a.stride, a.tokens, a.eps, stream, &sh, inv));
+            } else if (whole && a.norm_fold != SIZE_MAX) {
+                K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
+                                               a.stride, a.tokens, a.eps, stream, nullptr,
+                                               norm_invs.p + a.norm_fold * 64u));
             } else {
                 K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
                                                a.stride, a.tokens, a.eps, stream));
@@ -1201,6 +1228,7 @@ struct K44GpuExecutorState {
         fuse_products();
         fuse_mul_chains();
         fuse_norm_shifts();
+        fuse_norms();
         form_runs();
         K44_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         K44_HIP(hipEventCreate(&ev0));
@@ -1218,6 +1246,16 @@ struct K44GpuExecutorState {
                 arrive.alloc(n_arrive);
                 K44_HIP(hipMemsetAsync(arrive.p, 0, n_arrive * sizeof(uint32_t), stream));
             }
+        }
+        if (!norm_folds.empty()) {
+            const NormFold &last = norm_folds.back();
+            const size_t slots = last.slot0 + last.tiles;
+            norm_slots.alloc(slots * 64u);
+            norm_ctrs.alloc(norm_folds.size());
+            norm_invs.alloc(norm_folds.size() * 64u);
+            K44_HIP(hipMemsetAsync(norm_slots.p, 0, slots * 64u * sizeof(uint32_t), stream));
+            K44_HIP(hipMemsetAsync(norm_ctrs.p, 0, norm_folds.size() * sizeof(uint32_t), stream));
+            K44_HIP(hipMemsetAsync(norm_invs.p, 0, norm_folds.size() * 64u * sizeof(float), stream));
         }
         upload_mfma_descriptors();
         K44_HIP(hipMemsetAsync(canvas.p, 0,
@@ -1602,6 +1640,158 @@ struct K44GpuExecutorState {
         }
     }
 
+    // RMSNorms of decode-sized plans whose input is written by narrow 64/128-neuron MFMA waves
+    // (the sub-waves of the projections before them, each tile's outputs stored by one
+    // workgroup) take their per-token scales from those waves: every producer tile adds the
+    // exact sums of squares of the values it stored, and the last tile of the tensor forms the
+    // scales (k44_mfma_narrow.hip, narrow_norm_publish).  The sums are exact, so the scales equal
+    // the norm kernel's own bit for bit.  A norm read only by narrow 64/128-neuron waves gathering
+    // it plainly is then not launched: those waves gather its input and normalise it in the
+    // gather with the kernel's expression (xprod 4).  Otherwise (a norm that runs the decode
+    // token shift) the norm kernel runs with the scales and skips its sum pass.  Conditions, from
+    // the canvas ranges of the commands in plan order: the producers are the last writers of
+    // the input, together write each of its D rows exactly once, and run their whole epilogue
+    // in one workgroup per tile (unsplit, or split-K reduced in the launch); for the consumers,
+    // the input stays intact until the last of them, and the norm's output is not the plan
+    // output.  Whole-plan execution only; tuning switch fuse=0 disables it.
+    void fuse_norms() {
+        if (tune(Tune::Fuse) == 0) return;
+        const size_t n = ops.size();
+        std::vector<Ranges> rd(n), wr(n);
+        for (size_t i = 0; i < n; ++i) {
+            if (ops[i].first) {
+                rd[i] = waves[ops[i].second]->rd_run;
+                wr[i] = waves[ops[i].second]->wr_run;
+            } else if (!aux[ops[i].second]->fused) {
+                const AuxExec &A = *aux[ops[i].second];
+                aux_ranges(A, rd[i], wr[i]);
+                if (A.shift_with != SIZE_MAX) {  // the shift it runs
+                    Ranges r2, w2;
+                    aux_ranges(*aux[A.shift_with], r2, w2);
+                    for (const auto &x : r2) rd[i].push_back(x);
+                    for (const auto &x : w2) wr[i].push_back(x);
+                    rd[i] = merge_ranges(std::move(rd[i]));
+                    wr[i] = merge_ranges(std::move(wr[i]));
+                }
+            }
+        }
+        Ranges out_rng = {{0u, UINT64_MAX}};
+        {
+            auto it = plan_meta.res_map.find(plan_meta.output_res_key);
+            if (it != plan_meta.res_map.end())
+                out_rng = {{plan_meta.output_off,
+                            plan_meta.output_off +
+                                (uint64_t)plan_meta.output_c * it->second.channel_stride}};
+        }
+        typedef std::pair<uint64_t, uint64_t> Rng;
+        auto narrow_long = [&](const WaveExec &w) {
+            return w.mfma && w.narrow && (w.cluster == 64u || w.cluster == 128u) && !w.tile2d;
+        };
+        for (size_t i = 0; i < n; ++i) {
+            if (ops[i].first) continue;
+            AuxExec &N = *aux[ops[i].second];
+            if (N.type != K44CmdType::RMSNORM_1D || N.fused || N.tokens == 0u || N.tokens > 16u ||
+                N.D == 0u || N.D > 65536u || N.stride == 0u || (N.stride & (N.stride - 1u)) ||
+                N.stride > 64u)
+                continue;
+            const Rng X(N.src_off, N.src_off + (uint64_t)N.D * N.stride);
+            const Rng Y(N.y_off, N.y_off + (uint64_t)N.D * N.stride);
+            // producers: walking back, every writer into X until each row is covered
+            std::vector<size_t> prods;
+            std::vector<uint8_t> row_seen(N.D, 0u);
+            uint32_t covered = 0;
+            bool ok = true;
+            for (size_t p = i; p-- > 0 && ok && covered < N.D;) {
+                if (!ranges_overlap(wr[p], Ranges{X})) continue;
+                if (!ops[p].first) {
+                    ok = false;
+                    break;
+                }
+                const WaveExec &w = *waves[ops[p].second];
+                ok = narrow_long(w) && (w.kgroups <= 1u || w.reduce_in_kernel) &&
+                     w.y_off_run == w.y_off;
+                for (const auto &x : w.wr_run) {
+                    if (!ok) break;
+                    // rows of X from their first element (merged ranges span consecutive
+                    // rows); each row written once, at least its first N.tokens columns
+                    ok = x.first >= X.first && x.second <= X.second &&
+                         (x.first - X.first) % N.stride == 0u;
+                    if (!ok) break;
+                    const uint64_t r0 = (x.first - X.first) / N.stride;
+                    const uint64_t r1 = (x.second - X.first + N.stride - 1u) / N.stride;
+                    ok = (x.second - X.first) - (r1 - 1u) * N.stride >= N.tokens;
+                    for (uint64_t r = r0; r < r1 && ok; ++r) {
+                        ok = !row_seen[r];
+                        row_seen[r] = 1u;
+                        ++covered;
+                    }
+                }
+                if (ok) prods.push_back(ops[p].second);
+            }
+            if (!ok || covered != N.D || prods.empty()) continue;
+            // consumers (a norm without a fused shift): readers of Y until overwritten
+            std::vector<size_t> cons;
+            bool consume = N.shift_with == SIZE_MAX;
+            if (consume) {
+                size_t last = i;
+                bool overwritten = false;
+                for (size_t j = i + 1; j < n && consume && !overwritten; ++j) {
+                    if (ranges_overlap(rd[j], Ranges{Y})) {
+                        if (!ops[j].first) {
+                            consume = false;
+                            break;
+                        }
+                        const WaveExec &w = *waves[ops[j].second];
+                        consume = narrow_long(w) && w.xprod == 0u &&
+                                  !ranges_overlap(w.resrd, Ranges{Y});
+                        for (const auto &x : w.xrd)
+                            consume = consume && Y.first <= x.first && x.second <= Y.second;
+                        cons.push_back(ops[j].second);
+                        last = j;
+                    }
+                    overwritten = ranges_overlap(wr[j], Ranges{Y});
+                }
+                consume = consume && !cons.empty() &&
+                          (overwritten || !ranges_overlap(Ranges{Y}, out_rng));
+                for (size_t j = i + 1; j <= last && consume; ++j)
+                    consume = !ranges_overlap(wr[j], Ranges{X});
+            }
+            // fold
+            NormFold f;
+            f.norm = ops[i].second;
+            f.slot0 = norm_folds.empty() ? 0u : norm_folds.back().slot0 + norm_folds.back().tiles;
+            for (size_t pw : prods) {
+                WaveExec &w = *waves[pw];
+                w.norm_fold = norm_folds.size();
+                w.norm_tile0 = f.tiles;
+                f.tiles += w.rows;
+                w.why += "; its tiles form the sums of squares of a folded RMSNorm";
+            }
+            f.consumers = consume;
+            N.norm_fold = norm_folds.size();
+            if (consume) {
+                N.fused = true;
+                N.fuse_note = "folded: scales formed by its producers, rows normalised in its "
+                              "readers' gathers";
+                for (size_t cw : cons) {
+                    WaveExec &w = *waves[cw];
+                    w.xprod = 4u;
+                    w.xnorm = norm_folds.size();
+                    w.xd[0] = (int64_t)X.first - (int64_t)Y.first;
+                    Ranges fr = w.resrd;
+                    for (const auto &x : w.xrd)
+                        fr.push_back({(uint64_t)((int64_t)x.first + w.xd[0]),
+                                      (uint64_t)((int64_t)x.second + w.xd[0])});
+                    w.rd_run = merge_ranges(std::move(fr));
+                    w.why += "; gathers its input through a folded RMSNorm";
+                }
+            } else {
+                N.fuse_note = "scales formed by its producers (no sum pass)";
+            }
+            norm_folds.push_back(f);
+        }
+    }
+
     // Plan order -> runs: consecutive MFMA waves of one kernel configuration join a group while
     // no member writes what another reads or writes (checked on canvas element ranges).
     void form_runs() {
@@ -1724,6 +1914,26 @@ struct K44GpuExecutorState {
             a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : a.K * a.S / w.rows_per_stage;
         a.part = w.kgroups > 1u ? part : nullptr;
         if (fused && w.reduce_in_kernel) a.arrive = arrive.p + w.arrive_off;
+        if (fused && w.norm_fold != SIZE_MAX) {
+            const NormFold &f = norm_folds[w.norm_fold];
+            const AuxExec &N = *aux[f.norm];
+            a.norm_part = norm_slots.p + (f.slot0 + w.norm_tile0) * 64u;
+            a.norm_all = norm_slots.p + f.slot0 * 64u;
+            a.norm_cnt = norm_ctrs.p + w.norm_fold;
+            a.norm_inv = norm_invs.p + w.norm_fold * 64u;
+            a.norm_tiles = f.tiles;
+            a.norm_D = N.D;
+            a.norm_eps = N.eps;
+        }
+        if (fused && w.xnorm != SIZE_MAX) {
+            const AuxExec &N = *aux[norm_folds[w.xnorm].norm];
+            a.xinv = norm_invs.p + w.xnorm * 64u;
+            a.xgamma = N.table.p;
+            a.xg_base = N.y_off;
+            uint32_t sh = 0;
+            while ((1u << sh) < N.stride) ++sh;
+            a.xg_shift = sh;
+        }
         a.cout = w.cout;
         a.tokens = w.part_tokens;
         a.tiles = w.rows;

@@ -1,29 +1,18 @@
 // Translation unit of the 1-D token ops (see k44_aux.hpp for their semantics).
 #include "k44_aux.hpp"
 #include "k44_gather_dot.hpp"
+#include "k44_sumsq.hpp"
 
 namespace k44dev {
-
-// fp16 of an fp32 value, rounded to fp32 first as written: the opaque register move keeps the
-// compiler from fusing the multiply or FMA that produced `v` and the conversion into one
-// mixed-precision FMA (a single rounding) — which it may do at one use of an expression and
-// not at another (a normalised value stored and the same value recomputed for the fused token
-// shift, or a fused and a stand-alone token shift, differed in the last bit).
-__device__ __forceinline__ __half f16_of(float v) {
-    asm volatile("" : "+v"(v));
-    return __float2half_rn(v);
-}
-
-// RMSNorm output fp16(x * inv * gamma), both products in fp32.
-__device__ __forceinline__ __half norm_scale(__half x, float inv, float g) {
-    return f16_of(__half2float(x) * inv * g);
-}
 
 // Workgroup = OCT token octets (8 consecutive tokens = one 16-byte column chunk each) x
 // 256/OCT channel lanes: every lane sums squares down its channel stripe with 8 loads in flight
 // (OCT lanes side by side read 16*OCT contiguous bytes of a channel row), the lanes of an octet
-// reduce (shuffles, then the 4 waves in LDS in a fixed order), and the workgroup writes channel
-// slice blockIdx.y of its tokens.  Small token counts (decode) use OCT = 1 and several slices
+// reduce (shuffles, then the 4 waves in LDS), and the workgroup writes channel slice blockIdx.y
+// of its tokens.  The sums of squares are exact (k44_sumsq.hpp): the same bits whatever the
+// grouping, so a norm whose sums were assembled elsewhere (inv_in: the per-token scales
+// rsqrt(sum / D + eps) of every token column, formed by the waves that produced x) gives this
+// kernel's output exactly; with inv_in the sum pass is skipped.  Small token counts (decode) use OCT = 1 and several slices
 // per token chunk, each recomputing the (cache-resident) sum, so the grid still fills the chip.
 // RF > 0 (decode slices of one channel per thread): the decode token shift of the output
 // follows in the same thread — y2 = mu[c][0]*y + sum_i mu[c][i]*state[c][i-1][t], state shifted
@@ -34,9 +23,11 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
                                                           const __half *__restrict__ x,
                                                           const __half *__restrict__ gamma,
                                                           uint32_t D, uint32_t stride, float eps,
-                                                          uint32_t cslice, RmsShift sh) {
+                                                          uint32_t cslice, RmsShift sh,
+                                                          const float *__restrict__ inv_in) {
     constexpr uint32_t CL = 256u / OCT;  // channel lanes
-    __shared__ float part[4][OCT * 8];
+    __shared__ SumSq part[4][OCT * 8];
+    __shared__ float inv_s[OCT * 8];
     const uint32_t oct = threadIdx.x % OCT, lane_c = threadIdx.x / OCT;
     const uint32_t t0 = (blockIdx.x * OCT + oct) * 8u;
     // Slices of at most one channel per thread (decode): the thread's own channel and its gamma
@@ -78,32 +69,24 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
                 sv[i - 1] = *reinterpret_cast<const uint4 *>(st + (i - 1u) * 64u);
         }
     }
-    float ss[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    uint32_t c = lane_c;
+    SumSq ss[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ss[k] = sumsq_zero();
+    uint32_t c = inv_in ? D : lane_c;  // (uniform) precomputed scales: no sum pass
+    auto add8 = [&](const uint4 &v) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sumsq_add(ss[k], w[k >> 1] >> (16 * (k & 1)));
+    };
     for (; c + 7u * CL < D; c += 8u * CL) {
         uint4 v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u)
             v[u] = *reinterpret_cast<const uint4 *>(x + (uint64_t)(c + u * CL) * stride + t0);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const __half *h = reinterpret_cast<const __half *>(&v[u]);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float f = __half2float(h[k]);
-                ss[k] = fmaf(f, f, ss[k]);
-            }
-        }
+        for (int u = 0; u < 8; ++u) add8(v[u]);
     }
-    for (; c < D; c += CL) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0);
-        const __half *h = reinterpret_cast<const __half *>(&v);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float f = __half2float(h[k]);
-            ss[k] = fmaf(f, f, ss[k]);
-        }
-    }
+    for (; c < D; c += CL) add8(*reinterpret_cast<const uint4 *>(x + (uint64_t)c * stride + t0));
     // the own-channel values become visible to the compiler only here
     asm volatile("" : "+v"(xo.x), "+v"(xo.y), "+v"(xo.z), "+v"(xo.w), "+v"(gbits));
     if constexpr (RF > 0u) {
@@ -113,22 +96,46 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
         for (uint32_t i = 1; i < RF; ++i)
             asm volatile("" : "+v"(sv[i - 1].x), "+v"(sv[i - 1].y), "+v"(sv[i - 1].z), "+v"(sv[i - 1].w));
     }
+    if (inv_in) {
+        if (threadIdx.x < OCT * 8u) inv_s[threadIdx.x] = inv_in[blockIdx.x * OCT * 8u + threadIdx.x];
+    } else {
+        // Per-token sums of the CL channel lanes: transposed through LDS ([token][lane], carries
+        // propagated), then thread (token k, part p) adds 8 lanes, the parts of a token meet
+        // by shuffles within the wave and the 4 waves in LDS (exact: any order).
+        constexpr uint32_t TK = OCT * 8u;  // tokens of the workgroup
+        __shared__ uint4 tr[TK][CL];
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < 8; ++k) {
+            const SumSq q = sumsq_norm(ss[k]);
+            tr[oct * 8u + k][lane_c] = uint4{(uint32_t)q.l0, (uint32_t)q.l1, (uint32_t)q.l2, q.sp};
+        }
+        __syncthreads();
+        const uint32_t k = threadIdx.x % TK, pp = threadIdx.x / TK;
+        SumSq a = sumsq_zero();
 #pragma unroll
-        for (int m = OCT; m < 64; m <<= 1) ss[k] += __shfl_xor(ss[k], m, 64);
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    if (lane < OCT) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) part[wave][lane * 8u + k] = ss[k];
+        for (uint32_t j = 0; j < 8u; ++j) {
+            const uint4 v = tr[k][pp * 8u + j];
+            a.l0 += v.x;
+            a.l1 += v.y;
+            a.l2 += v.z;
+            a.sp |= v.w;
+        }
+        a = sumsq_wave_reduce(a, (int)TK);
+        const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+        if (lane < TK) part[wave][lane] = a;
+        __syncthreads();
+        if (threadIdx.x < TK) {
+            SumSq t = part[0][threadIdx.x];
+            sumsq_merge(t, part[1][threadIdx.x]);
+            sumsq_merge(t, part[2][threadIdx.x]);
+            sumsq_merge(t, part[3][threadIdx.x]);
+            inv_s[threadIdx.x] = rms_inv(t, D, eps);
+        }
     }
     __syncthreads();
     float inv[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t q = oct * 8u + k;
-        inv[k] = rsqrtf((((part[0][q] + part[1][q]) + part[2][q]) + part[3][q]) / (float)D + eps);
-    }
+    for (int k = 0; k < 8; ++k) inv[k] = inv_s[oct * 8u + k];
     if (one) {
         if (c_own < c_end) {
             const __half *h = reinterpret_cast<const __half *>(&xo);
@@ -826,9 +833,11 @@ static uint32_t grid_for(uint64_t n) {
 
 hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
                           uint32_t stride, uint32_t tokens, float eps, hipStream_t stream,
-                          const RmsShift *shift) {
+                          const RmsShift *shift, const float *inv_in) {
     if (stride % 64u != 0u || D == 0u || tokens == 0u || tokens > stride)
         return hipErrorInvalidValue;
+    // precomputed scales: the octet kernel only (its exact sums are what they replace)
+    if (inv_in && shift && shift->seq_len) return hipErrorInvalidValue;
     // token columns >= tokens are not written; octets per workgroup: the widest that still
     // gives >= 256 workgroups (coalesced rows), else 1 octet and channel slices
     const uint32_t octets = (tokens + 7u) / 8u;
@@ -876,7 +885,7 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
     }
     // Prefill-sized token counts without a fused shift: the register-resident wide kernel
     // (32 tokens x all channels per workgroup) when the channels fit 16 per thread.
-    if (!shift && tokens % 32u == 0u && tokens / 32u >= 256u && D <= 16u * 256u) {
+    if (!shift && !inv_in && tokens % 32u == 0u && tokens / 32u >= 256u && D <= 16u * 256u) {
         const dim3 gw(tokens / 32u);
 #define K44_RMSW(C)                                                                            \
     hipLaunchKernelGGL((k44_rmsnorm_regs_kernel<C>), gw, dim3(1024), 0, stream, y, x, gamma, D, \
@@ -894,7 +903,7 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
     }
     const dim3 grid(chunks, (D + cslice - 1u) / cslice);
 #define K44_RMS(O, R) \
-    hipLaunchKernelGGL((k44_rmsnorm_kernel<O, R>), grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice, sh)
+    hipLaunchKernelGGL((k44_rmsnorm_kernel<O, R>), grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice, sh, inv_in)
     if (shift) {
         switch (sh.rf) {
         case 1u: K44_RMS(1, 1u); break;

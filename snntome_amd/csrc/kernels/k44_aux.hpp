@@ -3,6 +3,8 @@
 // All tensors are channel-major on the canvas: element (c, t) at base + c*stride + t.
 //  * RMSNORM_1D (reference kernels/common/kernel44_valu_pack.cuh:104-134): per token t,
 //    y[c][t] = x[c][t] * rsqrt(sum_c x[c][t]^2 / D + eps) * gamma[c]   (gamma = 1 when folded).
+//    Token counts below 8,192 (decode) sum the squares exactly (k44_sumsq.hpp); wide token
+//    counts (prefill) sum them in fp32.
 //  * SWIGLU_MUL_1D (reference :135-143): y = gate * up, element-wise (SiLU is fused into the gate
 //    projection's epilogue).
 //  * TOKEN_SHIFT_1D (build extension): causal depth-wise mix over the last RF tokens of the same
@@ -42,9 +44,12 @@ inline bool rmsnorm_shift_prefill_ok(uint32_t D, uint32_t stride, uint32_t token
            tokens / 32u >= 256u && rf >= 1u && rf <= 5u && seq_len > 0u && seq_len % 8u == 0u;
 }
 
+// inv_in (nullable, octet kernel only: token counts below the register-resident kernel's, no
+// fused prefill shift): per-token scales rsqrt(sum_c x^2 / D + eps) of every token column of
+// the stride, already formed (from exact sums of squares, so they equal the kernel's own).
 hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
                           uint32_t stride, uint32_t tokens, float eps, hipStream_t stream,
-                          const RmsShift *shift = nullptr);
+                          const RmsShift *shift = nullptr, const float *inv_in = nullptr);
 hipError_t launch_mul(__half *y, const __half *a, const __half *b, uint64_t n,
                       hipStream_t stream);
 // y = fp16(a * fp16(b * c)) element-wise (a chain of two multiplies in one pass); y may be

@@ -19,6 +19,7 @@
 //    per workgroup measured 4x slower on decode-sized waves).
 // Columns 16..stride-1 of the output rows are not written.
 #include "k44_launch.hpp"
+#include "k44_sumsq.hpp"
 
 namespace k44dev {
 
@@ -68,11 +69,10 @@ __device__ __forceinline__ void narrow_epi_load(const MfmaTileArgs &a, const uin
 
 template <int BPW>
 __device__ __forceinline__ void narrow_epi_store(const MfmaTileArgs &a, const f4_t (&acc)[BPW],
-                                                 const NarrowEpi<BPW> &e) {
+                                                 const NarrowEpi<BPW> &e, uint16_t (&out)[BPW][4]) {
     typedef __attribute__((address_space(1))) uint16_t gu16w;
     // every value formed before the first store (a store between a residual load and its use
     // would be waited for with it: both count on the same counter)
-    uint16_t out[BPW][4];
 #pragma unroll
     for (int bi = 0; bi < BPW; ++bi)
 #pragma unroll
@@ -94,8 +94,81 @@ template <int BPW>
 __device__ __forceinline__ void narrow_fused_epilogue(const MfmaTileArgs &a, const f4_t (&acc)[BPW],
                                                       const uint32_t (&j0)[BPW], uint32_t t) {
     NarrowEpi<BPW> e;
+    uint16_t out[BPW][4];
     narrow_epi_load<BPW>(a, j0, t, e);
-    narrow_epi_store<BPW>(a, acc, e);
+    narrow_epi_store<BPW>(a, acc, e, out);
+}
+
+// Producer side of a folded RMSNorm (a.norm_part set): the tile's stored fp16 outputs (lane
+// (g, t): out[bi][i] of channel slot j0[bi] + i, token t) summed squared per token, exactly:
+// over the lanes of one token (xor 16, 32), then the 4 waves in LDS; wave 0 publishes the
+// tile's slot (device-coherent stores, waited for), counts the tile in at norm_cnt, and the
+// last tile's wave 0 sums every slot of the tensor (lane = token x quarter of the slots) and
+// stores the per-token scales.  Every wave of the workgroup calls this (one barrier).
+template <int BPW>
+__device__ __forceinline__ void narrow_norm_publish(const MfmaTileArgs &a, const NarrowEpi<BPW> &e,
+                                                    const uint16_t (&out)[BPW][4],
+                                                    uint32_t tile) {
+    typedef unsigned long long u64;
+    typedef __attribute__((address_space(1))) u64 gu64;
+    __shared__ SumSq red[4][16];
+    SumSq s = sumsq_zero();
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (e.o[bi][i] != ~0ull) sumsq_add(s, out[bi][i]);  // empty slots store nothing
+    s = sumsq_wave_reduce(s, 16);
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if (lane < 16u) red[wave][lane] = s;
+    __syncthreads();
+    if (wave != 0u) return;
+    if (lane < 16u) {
+        SumSq q = red[0][lane];
+        sumsq_merge(q, red[1][lane]);
+        sumsq_merge(q, red[2][lane]);
+        sumsq_merge(q, red[3][lane]);
+        q = sumsq_norm(q);  // one tile: the top limb and the flags fit 32 bits each
+        gu64 *slot = (gu64 *)(a.norm_part + ((uint64_t)tile * 16u + lane) * 4u);
+        __hip_atomic_store(slot, (u64)q.l0 | (q.l1 << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(slot + 1, (u64)(uint32_t)q.l2 | ((u64)q.sp << 32), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slot is stored before it is counted
+    uint32_t old = 0u;
+    if (lane == 0u)
+        old = __hip_atomic_fetch_add((__attribute__((address_space(1))) uint32_t *)a.norm_cnt, 1u,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != a.norm_tiles - 1u) return;
+    // last tile of the tensor: every slot, token lane & 15, slots lane >> 4, +4, ...
+    const gu64 *all = (const gu64 *)a.norm_all;
+    SumSq acc = sumsq_zero();
+    constexpr uint32_t NB = 8u;  // slots loaded together
+    for (uint32_t j0 = lane >> 4; j0 < a.norm_tiles; j0 += 4u * NB) {
+        u64 lo[NB], hi[NB];
+#pragma unroll
+        for (uint32_t u = 0; u < NB; ++u) {
+            const uint32_t j = min(j0 + 4u * u, a.norm_tiles - 1u);
+            const gu64 *p = all + ((uint64_t)j * 16u + (lane & 15u)) * 2u;
+            lo[u] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            hi[u] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < NB; ++u) {
+            if (j0 + 4u * u < a.norm_tiles) {
+                acc.l0 += lo[u] & 0xffffffffull;
+                acc.l1 += lo[u] >> 32;
+                acc.l2 += hi[u] & 0xffffffffull;
+                acc.sp |= (uint32_t)(hi[u] >> 32);
+            }
+        }
+    }
+    acc = sumsq_wave_reduce(acc, 16);
+    if (lane < 16u) a.norm_inv[lane] = rms_inv(acc, a.norm_D, a.norm_eps);
+    if (lane == 0u)
+        __hip_atomic_store((__attribute__((address_space(1))) uint32_t *)a.norm_cnt, 0u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Split-K reduced inside the launch (a.arrive set; 64 / 128-neuron tiles).  Every workgroup of
@@ -385,6 +458,17 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
     // multiply with the rounding of the unfused multiply commands: fp16(A*B), fp16(A*fp16(B*C)).
     constexpr int XQ = NARROW_MAX_ROWS * 2 / 256;
     constexpr uint32_t xprod = (uint32_t)PROD;  // every wave of the launch gathers this form
+    // Folded RMSNorm (xprod 4): the lane's 8 tokens' scales, loaded once.
+    float xinv[xprod == 4u ? 8 : 1];
+    if constexpr (xprod == 4u) {
+        typedef const __attribute__((address_space(1))) f4_t gf4;
+        const f4_t i0 = ((gf4 *)a.xinv)[(lane & 1) * 2], i1 = ((gf4 *)a.xinv)[(lane & 1) * 2 + 1];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            xinv[e2] = i0[e2];
+            xinv[4 + e2] = i1[e2];
+        }
+    }
     auto gather = [&](uint32_t s, u4_t (&xv)[XQ], u4_t (&xb)[XQ], u4_t (&xc)[XQ]) {
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
@@ -396,7 +480,18 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
             sb[q] = segr[k] + (uint64_t)(r - k * a.S) * a.step + (uint64_t)(lane >> 1) * a.step +
                     (uint32_t)(lane & 1) * 8u;
         }
-        if (xprod == 0u) {
+        if (xprod == 4u) {
+            // the norm's input rows and their gammas (xb holds the gamma bits of each pass)
+#pragma unroll
+            for (int q = 0; q < XQ; ++q) xv[q] = *(gu4_t *)(a.X + (int64_t)sb[q] + a.xd[0]);
+            typedef const __attribute__((address_space(1))) uint16_t gu16;
+            gu16 *gm = (gu16 *)(a.xgamma ? (const void *)a.xgamma : (const void *)a.X);
+#pragma unroll
+            for (int q = 0; q < XQ; ++q) {
+                const uint64_t row = sb[q] - (uint32_t)(lane & 1) * 8u;
+                xb[q][0] = a.xgamma ? (uint32_t)gm[(row - a.xg_base) >> a.xg_shift] : 0x3c00u;
+            }
+        } else if (xprod == 0u) {
 #pragma unroll
             for (int q = 0; q < XQ; ++q) xv[q] = *(gu4_t *)(a.X + sb[q]);
         } else {
@@ -415,7 +510,22 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
                      const u4_t (&xc)[XQ]) {
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
-        if (xprod != 0u) {
+        if (xprod == 4u) {
+#pragma unroll
+            for (int q = 0; q < XQ; ++q) {
+                h8_t ha = __builtin_bit_cast(h8_t, xv[q]);
+                const float gq = __half2float(__ushort_as_half((unsigned short)xb[q][0]));
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) {
+                    // element copied to a scalar first: a bit cast of the vector element itself
+                    // compiled to a read of element 0 for every e2
+                    const _Float16 xe = ha[e2];
+                    const __half r = norm_scale(__builtin_bit_cast(__half, xe), xinv[e2], gq);
+                    ha[e2] = __builtin_bit_cast(_Float16, r);
+                }
+                xv[q] = __builtin_bit_cast(u4_t, ha);
+            }
+        } else if (xprod != 0u) {
             // (as fp16 vectors: element access through pointer casts of the u4 registers would
             // put them on the stack)
 #pragma unroll
@@ -483,23 +593,20 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
 
     // Lane holds C[4g + i][lane & 15]: neuron 16*blk + 4g + i, token lane & 15.
     const uint32_t t = (uint32_t)(lane & 15);
-    if (!a.part) {
-        uint32_t j0[BPW];
-#pragma unroll
-        for (int bi = 0; bi < BPW; ++bi)
-            j0[bi] = tile * (uint32_t)NT + 16u * (uint32_t)(wave + 4 * bi) + 4u * (uint32_t)g;
-        narrow_fused_epilogue<BPW>(a, acc, j0, t);
-        return;
-    }
-    if (a.arrive) {  // split-K reduced by the tile's last workgroup, then the fused epilogue
+    if (!a.part || a.arrive) {
+        // whole contraction here, or split-K reduced by the tile's last workgroup: the fused
+        // epilogue (its loads complete under the reduction's round trips), then the tile's
+        // share of a folded RMSNorm
         uint32_t j0[BPW];
 #pragma unroll
         for (int bi = 0; bi < BPW; ++bi)
             j0[bi] = tile * (uint32_t)NT + 16u * (uint32_t)(wave + 4 * bi) + 4u * (uint32_t)g;
         NarrowEpi<BPW> e;
-        narrow_epi_load<BPW>(a, j0, t, e);  // completes under the reduction's round trips
-        if (!narrow_reduce_last<BPW>(a, acc, j0, t, tile, zgroup)) return;
-        narrow_epi_store<BPW>(a, acc, e);
+        uint16_t out[BPW][4];
+        narrow_epi_load<BPW>(a, j0, t, e);
+        if (a.part && !narrow_reduce_last<BPW>(a, acc, j0, t, tile, zgroup)) return;
+        narrow_epi_store<BPW>(a, acc, e, out);
+        if (a.norm_part) narrow_norm_publish<BPW>(a, e, out, tile);
         return;
     }
 #pragma unroll
@@ -515,7 +622,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
 
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
                               hipStream_t stream, uint32_t prod, uint32_t max_items) {
-    if (prod != 0u && ((nt != 64u && nt != 128u) || (prod != 2u && prod != 3u)))
+    if (prod != 0u && ((nt != 64u && nt != 128u) || (prod < 2u || prod > 4u)))
         return hipErrorInvalidValue;
     if (items == 0u) return hipSuccess;
     const dim3 grid(items), block(256);
@@ -532,7 +639,9 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
     case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, K44_GROUP_ARGS(g)); break;
     case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, K44_GROUP_ARGS(g)); break;
     case 64u:
-        if (prod == 3u) {
+        if (prod == 4u) {
+            K44_NL(64, 4)
+        } else if (prod == 3u) {
             K44_NL(64, 3)
         } else if (prod == 2u) {
             K44_NL(64, 2)
@@ -541,7 +650,9 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
         }
         break;
     case 128u:
-        if (prod == 3u) {
+        if (prod == 4u) {
+            K44_NL(128, 4)
+        } else if (prod == 3u) {
             K44_NL(128, 3)
         } else if (prod == 2u) {
             K44_NL(128, 2)

@@ -68,7 +68,8 @@ struct MfmaTileArgs {
     uint32_t tiles, ttiles, kgroups;
     // Product gather (element-wise multiplies fused into the X gather; narrow kernels of 64 /
     // 128-neuron tiles only): xprod 0 = the X rows as they are; 2 = fp16(A*B); 3 =
-    // fp16(A*fp16(B*C)), A / B / C the rows at (segment offset + xd[0] / xd[1] / xd[2]).
+    // fp16(A*fp16(B*C)), A / B / C the rows at (segment offset + xd[0] / xd[1] / xd[2]);
+    // 4 = a folded RMSNorm of the rows at (segment offset + xd[0]) (fields below).
     uint32_t xprod;
     int64_t xd[3];
     // 2-D waves of 64-frame interleaved images: 64-token tile t of the wave gathers at
@@ -83,6 +84,25 @@ struct MfmaTileArgs {
     // and runs the epilogue; partials are then laid out [z][cout/4][16 tokens][4 neurons].
     // nullptr: partials [z][cout][16] for k44_splitk_epilogue_kernel.
     uint32_t *arrive;
+    // RMSNorm folded around narrow 64 / 128-neuron waves (whole-plan runs), producer side
+    // (norm_part set): once a tile's outputs are stored, the tile adds the exact per-token sums
+    // of squares of the fp16 values it stored (k44_sumsq.hpp) to its slot norm_part[tile][16]
+    // (4 words: limbs 0..2, inf / NaN flags); the tile that arrives last at norm_cnt, out of the
+    // norm_tiles tiles that write the tensor, sums every slot of norm_all and stores the 16
+    // per-token scales rsqrt(sum / norm_D + norm_eps) to norm_inv (and zeroes norm_cnt).
+    uint32_t *norm_part;
+    const uint32_t *norm_all;
+    uint32_t *norm_cnt;
+    float *norm_inv;
+    uint32_t norm_tiles, norm_D;
+    float norm_eps;
+    // Consumer side (xprod 4): the gather reads the norm's input rows (segment offset + xd[0])
+    // and replaces every element by fp16(x * xinv[t] * gamma[c]), the RMSNorm kernel's
+    // expression; gamma from xgamma (nullptr: 1), c = (row offset - xg_base) >> xg_shift.
+    const float *xinv;
+    const __half *xgamma;
+    uint64_t xg_base;
+    uint32_t xg_shift;
 };
 
 // Canvas offset of token t of a wave (relative to a segment row or an output row).

@@ -1,0 +1,113 @@
+// k44_sumsq.hpp — RMSNorm arithmetic: exact sums of squares of fp16 values (decode-sized
+// plans) and the normalised element expression.
+//
+// RMSNorm (reference kernels/common/kernel44_valu_pack.cuh:104-134) needs, per token, the sum
+// of x^2 over the channels.  Summed in fp32, the result depends on the order of the additions,
+// so a norm computed by one kernel and the same norm assembled from the partial sums of the
+// workgroups that produced its input (in another order) would differ in the last bits.  Here
+// the sum is exact: an fp16 value is mm * 2^(e - 25) (mm = the 11-bit significand, e = the
+// exponent field, subnormals with e = 1), so x^2 = mm^2 * 2^(2e - 50) is the 22-bit integer
+// mm^2 shifted left by 2e - 2 (0..58) in units of 2^-48.  Squares are added into three 32-bit
+// limbs held in 64-bit accumulators (no carries while adding: up to 2^32 terms per limb), so
+// any grouping of the terms gives the same integer.  The integer is rounded to fp32 once (round
+// to nearest even), and inf / NaN inputs give an inf / NaN sum, as an fp32 sum would.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k44dev {
+
+// fp16 of an fp32 value, rounded to fp32 first as written: the opaque register move keeps the
+// compiler from fusing the multiply or FMA that produced `v` and the conversion into one
+// mixed-precision FMA (a single rounding) — which it may do at one use of an expression and
+// not at another (a normalised value stored and the same value recomputed for the fused token
+// shift, or a fused and a stand-alone token shift, differed in the last bit).
+__device__ __forceinline__ __half f16_of(float v) {
+    asm volatile("" : "+v"(v));
+    return __float2half_rn(v);
+}
+
+// RMSNorm output fp16(x * inv * gamma), both products in fp32 (the norm kernels and the
+// gathers of waves that apply a folded norm use this one expression).
+__device__ __forceinline__ __half norm_scale(__half x, float inv, float g) {
+    return f16_of(__half2float(x) * inv * g);
+}
+
+struct SumSq {
+    uint64_t l0, l1, l2;  // limbs: value = l0 + l1 * 2^32 + l2 * 2^64 (units of 2^-48)
+    uint32_t sp;          // bit 0: an infinite input, bit 1: a NaN input
+};
+
+__host__ __device__ __forceinline__ SumSq sumsq_zero() { return SumSq{0u, 0u, 0u, 0u}; }
+
+// s += x^2 for the fp16 value with bits h (low 16 bits of h).
+__host__ __device__ __forceinline__ void sumsq_add(SumSq &s, uint32_t h) {
+    const uint32_t e = (h >> 10) & 31u, m = h & 1023u;
+    const uint32_t mm = e ? (m | 1024u) : m;
+    const uint32_t sh = e > 1u ? 2u * e - 2u : 0u;  // e = 31 (inf / NaN) is flagged below
+    const uint64_t v = (uint64_t)(mm * mm);          // < 2^22
+    const bool up = sh >= 32u;
+    const uint64_t w = v << (up ? sh - 32u : sh);    // < 2^54
+    const uint64_t lo = w & 0xffffffffull, hi = w >> 32;
+    s.l0 += up ? 0ull : lo;
+    s.l1 += up ? lo : hi;
+    s.l2 += up ? hi : 0ull;
+    s.sp |= e == 31u ? (m ? 2u : 1u) : 0u;
+}
+
+__host__ __device__ __forceinline__ void sumsq_merge(SumSq &s, const SumSq &o) {
+    s.l0 += o.l0;
+    s.l1 += o.l1;
+    s.l2 += o.l2;
+    s.sp |= o.sp;
+}
+
+// Carries propagated: every limb below 2^32 except the top one (same value).
+__host__ __device__ __forceinline__ SumSq sumsq_norm(SumSq s) {
+    s.l1 += s.l0 >> 32;
+    s.l0 &= 0xffffffffull;
+    s.l2 += s.l1 >> 32;
+    s.l1 &= 0xffffffffull;
+    return s;
+}
+
+// The exact sum rounded to fp32 (round to nearest even).  The 128-bit integer H:L is brought to
+// 64 bits with the bits shifted out ORed into the lowest one (rounding to odd at 64 bits), and
+// that integer is converted with one rounding: rounding to odd at >= 26 bits and then to
+// nearest even at 24 gives the nearest-even rounding of the exact value.
+__host__ __device__ __forceinline__ float sumsq_value(SumSq s) {
+    if (s.sp) return (s.sp & 2u) ? __builtin_nanf("") : __builtin_inff();
+    s = sumsq_norm(s);
+    const uint64_t L = s.l0 | (s.l1 << 32), H = s.l2;
+    if (H == 0ull) return __builtin_ldexpf((float)L, -48);
+    const int k = 64 - __builtin_clzll(H);  // bits of H (1..64)
+    uint64_t T = (L >> k) | (k < 64 ? (H << (64 - k)) : 0ull);
+    if (k == 64) T = H;
+    const uint64_t dropped = k < 64 ? (L & ((1ull << k) - 1ull)) : L;
+    T |= dropped != 0ull ? 1ull : 0ull;
+    return __builtin_ldexpf((float)T, k - 48);
+}
+
+// RMSNorm scale of a token from its exact sum of squares over D channels.
+__device__ __forceinline__ float rms_inv(const SumSq &s, uint32_t D, float eps) {
+    return rsqrtf(sumsq_value(s) / (float)D + eps);
+}
+
+// 64-lane wave reduction of a SumSq over the lanes that share (lane & (span - 1)), i.e. xor
+// distances span, 2 span, ... 32 (span a power of two).  Exact, so the order does not matter.
+__device__ __forceinline__ SumSq sumsq_wave_reduce(SumSq s, int span) {
+    s = sumsq_norm(s);  // every limb < 2^32 except l2 (small): 32-bit shuffles of each
+    for (int m = span; m < 64; m <<= 1) {
+        SumSq o;
+        o.l0 = (uint32_t)__shfl_xor((int)(uint32_t)s.l0, m, 64);
+        o.l1 = (uint32_t)__shfl_xor((int)(uint32_t)s.l1, m, 64);
+        o.l2 = (uint32_t)__shfl_xor((int)(uint32_t)s.l2, m, 64);
+        o.sp = (uint32_t)__shfl_xor((int)s.sp, m, 64);
+        sumsq_merge(s, o);
+        s = sumsq_norm(s);
+    }
+    return s;
+}
+
+}  // namespace k44dev

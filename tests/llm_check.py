@@ -16,9 +16,10 @@ inputs the device itself read:
 Token columns: `windows` — (first column, count) ranges of the plan's token axis; the full
 check of a 16 x 512-token prefill samples three 64-token windows (the first request's start, a
 request boundary, the last tokens).  Waves whose gather multiplies operands (folded multiplies,
-run mode) are checked on the oracle's product of the operand tensors the device read, and a
-multiply that runs its inner multiply (run mode: a * (b * c) in one kernel) on the oracle's
-chain of the three operands it read.
+run mode) are checked on the oracle's product of the operand tensors the device read, waves
+that gather through a folded RMSNorm (run mode, decode) on that norm run alone into its own
+output range (checked against the oracle), and a multiply that runs its inner multiply (run mode: a * (b * c) in one kernel) on the
+oracle's chain of the three operands it read.
 """
 from typing import Dict, List, Optional, Sequence, Tuple
 
@@ -87,12 +88,36 @@ class PlanChecker:
     def _wave_input(self, i: int, fused: bool) -> np.ndarray:
         c = self.cmds[i]
         w = self.wave_rep[i]
+        if fused and w["xprod"] == 4:  # a folded RMSNorm: the norm run alone materialises it
+            self._materialise_norm(i)
+            return self.rows(c["src_off"], c["Cin"])
         if fused and w["xprod"]:
             leaves = [self.rows(int(c["src_off"]) + int(d), c["Cin"]) for d in w["xd"][:w["xprod"]]]
             if w["xprod"] == 2:
                 return lo.mul(leaves[0], leaves[1])
             return lo.mul(leaves[0], lo.mul(leaves[1], leaves[2]))
         return self.rows(c["src_off"], c["Cin"])
+
+    def _materialise_norm(self, i: int):
+        """Run mode, a wave gathering through a folded RMSNorm: the norm command it reads (the
+        latest one before it writing its input tensor) is run alone (execute_range: the norm
+        kernel with its own exact sums of squares) into the norm's output range, which the
+        canvas allocator holds for the norm's output until its last reader and which the
+        whole-plan schedule leaves unwritten; the result is checked against the oracle and is
+        the wave's input, equal bit for bit to what its gather forms (the folded and unfolded
+        decode plans give identical ids and logits: test_folded_multiplies_match_unfolded)."""
+        off = int(self.cmds[i]["src_off"])
+        n = max(k for k in range(i) if self.cmds[k]["type"] == "RMSNORM_1D"
+                and int(self.cmds[k]["y_off"]) == off)
+        assert self.aux_rep[n]["fused"], f"{self.cmds[n]['name']}: not a folded norm"
+        if n in self._materialised:
+            return
+        c = self.cmds[n]
+        x = self.rows(c["src_off"], c["Cin"])
+        self.plan.execute_range(n, 1)
+        y = self.rows(c["y_off"], c["Cin"]).astype(np.float64)
+        self._note("RMSNORM_1D", lo.orc.rel_err(y, lo.rmsnorm_f64(x)), f"{c['name']} (folded)")
+        self._materialised.add(n)
 
     def _y_off(self, i: int, fused: bool) -> int:
         return int(self.wave_rep[i]["y_off_run"] if fused else self.cmds[i]["y_off"])
@@ -246,6 +271,7 @@ class PlanChecker:
         """mode 'commands' (execute_range per graph node) or 'runs' (execute_runs per run)."""
         self.plan.set_ids(ids)
         state = {"proj_in": {}, "done": {}, "ids": np.asarray(ids, dtype=np.uint32)}
+        self._materialised = set()
         if mode == "commands":
             steps, i = [], 0
             while i < len(self.cmds):  # consecutive commands of one node (pruned sub-waves)
