@@ -51,6 +51,23 @@ def under_profiler() -> bool:
     return "rocprofiler-sdk" in os.environ.get("LD_PRELOAD", "")
 
 
+def under_counter_collection() -> bool:
+    """rocprofv3 --pmc / -i passes the requested counters to its tool through the environment."""
+    return under_profiler() and any(
+        os.environ.get(k) for k in ("ROCPROF_COUNTER_COLLECTION", "ROCPROF_COUNTERS",
+                                    "ROCPROFILER_COUNTERS"))
+
+
+# Untimed warm-up: the requested warm-up steps, then more until at least this long has passed
+# (the reference's sustained warm-up, whitepaper/sparse_wmma_kernel/tests/benchmark_common.cuh:
+# 135-161: clocks and caches in their steady state before the timed region).
+WARMUP_MIN_S = 0.2
+# Config 4 is also timed over this many copies of its plan in rotation (weights and segment
+# tables of 4 x 134 MB, beyond the 256 MB last-level cache), as the reference rotates its
+# weight and index pools (benchmark_common.cuh:182-190).
+C4_POOLS = 4
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -191,16 +208,27 @@ def bench_wave(cfg: int, steps: int, warmup: int) -> dict:
     for wv in rep["waves"][:2]:
         log(f"[bench] {wv['name']}: path={wv['path']} K={wv['K']} S={wv['S']} "
             f"slab={wv['slab']} tokens={wv['tokens']}")
-    log(f"[bench] setup {time.perf_counter() - t_start:.1f}s; warmup {warmup}")
+    log(f"[bench] setup {time.perf_counter() - t_start:.1f}s; warmup {warmup} steps, "
+        f">= {WARMUP_MIN_S * 1e3:.0f} ms")
+    tw = time.perf_counter()
+    warm_runs = 0
     if warmup > 0:
         plan.execute(warmup)
+        warm_runs += warmup
     plan.sync()
+    while time.perf_counter() - tw < WARMUP_MIN_S:
+        plan.execute(max(1, warmup))
+        warm_runs += max(1, warmup)
+        plan.sync()
+    warm_ms = (time.perf_counter() - tw) * 1e3
     t0 = time.perf_counter()
     ev_ms = plan.execute(steps)  # HIP events on the executor stream, average per step
     plan.sync()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    log(f"[bench] {wl.name} {steps} steps: {wall_ms:.4f} ms/step wall, {ev_ms:.4f} ms/step events")
+    log(f"[bench] {wl.name} {steps} steps: {wall_ms:.4f} ms/step wall, {ev_ms:.4f} ms/step events "
+        f"(after {warm_runs} warm-up runs, {warm_ms:.0f} ms)")
     plan.release_gpu()
+    rotated = rotated_pools(wl, steps) if cfg == 4 else None
 
     flops = wl.flops
     comp = sum(synth.compulsory_bytes(wl, w) for w in wl.waves)
@@ -226,11 +254,14 @@ def bench_wave(cfg: int, steps: int, warmup: int) -> dict:
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic_from_profiles(kernel_key), "algorithmic_bytes": comp,
                 "kernel_ms": round(ev_ms, 5), "mfma_tflops_frac": round(mfma_frac, 4)}
-    return {
+    out = {
         "metric": METRIC,
         "value": round(value, 4),
         "unit": "TFLOP/s",
         "ms_per_step": round(wall_ms, 5),
+        "warmup_ms": round(warm_ms, 1),
+        "warmup_runs": warm_runs,
+        "residency": RESIDENCY[cfg],
         "config": {
             "workload": wl.name,
             "substrate_positions": wl.substrate,
@@ -246,6 +277,50 @@ def bench_wave(cfg: int, steps: int, warmup: int) -> dict:
         "roofline": roof,
         "_wl": wl,
     }
+    if rotated is not None:
+        out["rotated_pools"] = rotated
+    return out
+
+
+# What stays in the caches across the timed steps of each configuration (one plan replayed).
+RESIDENCY = {
+    1: "weights (4 MB), segment tables (0.3 MB) and substrate (8 MB) stay cache-resident "
+       "across steps: the plumbing configuration measures the L2/MALL-bound gather",
+    2: "weights (8 MB) and segment tables (2 MB) may stay in the 256 MB MALL; the 20.5 GB "
+       "substrate, 99 % of the algorithmic bytes, streams from HBM every step",
+    3: "weights (268 MB) exceed the 256 MB MALL; substrate rows are re-read by ~2.3 tiles",
+    4: "weights (134 MB) and segment tables stay in the 256 MB MALL across steps of one plan; "
+       "rotated_pools times 4 copies of the plan in rotation (536 MB)",
+}
+
+
+def rotated_pools(wl, steps: int) -> dict:
+    """Config 4 over C4_POOLS separately compiled copies of its plan (own weights, segment
+    tables and canvas), one run of each in turn: no copy's weights are in the caches when it
+    runs again.  Kernel time per run from HIP events on each plan's stream (the runs are
+    launched one at a time, so host waits between them are not counted)."""
+    from snntome_amd import synth, wavec
+
+    plans = []
+    for _ in range(C4_POOLS):
+        p = synth.build_graph(wl, wavec).compile()
+        p.init_gpu()
+        p.fill_input_uniform(wl.seed)
+        plans.append(p)
+    tw = time.perf_counter()
+    while time.perf_counter() - tw < WARMUP_MIN_S:
+        for p in plans:
+            p.execute(1)
+    ms = []
+    for k in range(max(steps, 2 * C4_POOLS)):
+        ms.append(plans[k % C4_POOLS].execute(1))
+    for p in plans:
+        p.release_gpu()
+    t = float(np.mean(ms))
+    log(f"[bench] {wl.name} over {C4_POOLS} rotated plan copies: {t:.4f} ms/run (events)")
+    return {"pools": C4_POOLS, "runs": len(ms), "kernel_ms": round(t, 5),
+            "value": round(wl.flops / (t * 1e-3) / 1e12, 4), "unit": "TFLOP/s",
+            "gathered_gbs": round(sum(gathered_bytes(wl, w) for w in wl.waves) / (t * 1e-3) / 1e9, 1)}
 
 
 def bench_llm(steps: int, warmup: int, eager: bool, no_cpu: bool = True) -> dict:
@@ -282,10 +357,16 @@ def bench_llm(steps: int, warmup: int, eager: bool, no_cpu: bool = True) -> dict
         return ms_p, ms_d
 
     pre.set_ids(prompt)
-    for _ in range(max(1, warmup)):
+    tw = time.perf_counter()
+    warm_steps = 0
+    while warm_steps < max(1, warmup) or time.perf_counter() - tw < WARMUP_MIN_S:
+        pre.set_ids(prompt)
         one_step()
+        warm_steps += 1
+        dec.sync()
     pre.sync()
     dec.sync()
+    warm_ms = (time.perf_counter() - tw) * 1e3
     t0 = time.perf_counter()
     pms, dms = [], []
     for _ in range(steps):
@@ -317,6 +398,8 @@ def bench_llm(steps: int, warmup: int, eager: bool, no_cpu: bool = True) -> dict
             "tile": spec.tile, "token_shift_rf": spec.rf, "requests": R, "prompt": P,
             "decode_steps": D, "paths": paths, "hip_graphs": not eager,
         },
+        "warmup_ms": round(warm_ms, 1),
+        "warmup_runs": warm_steps,
         "prefill_ms": round(prefill_ms, 4),
         "prefill_tflops": round(pre_tf, 2),
         "decode_ms_per_step": round(decode_ms, 5),
@@ -523,6 +606,15 @@ def main():
     # Under rocprofv3 config 5 launches kernel by kernel: a kernel-trace run of its HIP-graph
     # capture ended in a host segmentation fault inside the profiler's preloaded libraries.
     eager = args.eager or under_profiler()
+    # Config 5's two-plan workload (alone or in the default run) is not run under counter
+    # collection: one such run ended in a host segmentation fault in a thread of the profiling
+    # runtime reading a device address, cause unknown.  Counters of config 5 are taken per
+    # projection (--c5-projection), configs 1-4 with --config N.
+    if (args.config in (None, 5)) and under_counter_collection():
+        print("bench.py: config 5 (alone or in the default run) is not run under rocprofv3 "
+              "counter collection; take its counters with --c5-projection NAME, and those of "
+              "configs 1-4 with --config N", file=sys.stderr)
+        sys.exit(3)
 
     if args.config == 5:
         rec = bench_llm(args.steps, args.warmup, eager, no_cpu=args.no_cpu)

@@ -6,8 +6,10 @@
  * (0 = success, -1 = failure; pointers NULL on failure).  They are what the reference's ctypes
  * binding (wavec/wavec.py:28-132) binds.  Differences in behaviour, all on error paths:
  *   - a HIP runtime error returns -1 (the reference calls exit(EXIT_FAILURE));
- *   - a plan the executor cannot run (2-D spatial layouts and their aux commands, RoPE/GQA
- *     attention) fails wavec_gpu_init_plan with -1 instead of silently skipping commands;
+ *   - a plan the executor cannot run (RoPE/GQA attention, the one command kind outside this
+ *     build) fails wavec_gpu_init_plan with -1 instead of silently skipping commands; 1-D token
+ *     plans and 2-D spatial plans (padded-plane and 64-frame interleaved layouts, with their
+ *     pools, upsampling, stride-2 and transposed convolutions) run;
  *   - the message of the last failure on the calling thread is available from wavec_last_error().
  *
  * The entry points after "build extensions" have no counterpart in the reference.
@@ -203,7 +205,9 @@ int wavec_k44_f16_forward_token64(void *Y, const void *X, const uint32_t *cluste
                                   uint32_t B_vec16, uint32_t cluster_size, void *stream);
 /* Stand-alone argmax over caller-owned device memory (the decode plans' ARGMAX_1D op, no
  * reference counterpart): ids[t] = the lowest channel c with the largest logits[c * stride + t]
- * (fp16), for t < tokens; logits [vocab][stride], stride a multiple of 64, tokens <= stride.
+ * (fp16), for t < tokens; logits [vocab][stride], stride a multiple of 64, tokens <= stride;
+ * logits 8-byte aligned (a multiple of 4 fp16 elements from an allocation's start) and ids
+ * 4-byte aligned, else -1 before any launch.
  * Two passes; the per-chunk (value, index) partials live in a workspace the library allocates
  * and frees on `stream` for the call (hipMallocAsync / hipFreeAsync).  Asynchronous. */
 int wavec_argmax_f16(uint32_t *ids, const void *logits, uint32_t vocab, uint32_t stride,

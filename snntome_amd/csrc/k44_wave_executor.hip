@@ -1599,7 +1599,8 @@ struct K44GpuExecutorState {
     // kernel (whole-plan execution; bit-identical to the two commands).  Decode: the norm's
     // decode form keeps one channel per thread, so the shift of that channel's tokens follows
     // in place.  Prefill (the register-resident 32-token form): each workgroup also normalizes
-    // the 8 tokens before its block and shifts its own tokens (k44_rmsnorm_shift_prefill_kernel).
+    // the 4 tokens before its block (RF - 1 <= 4) and shifts its own tokens
+    // (k44_rmsnorm_shift_prefill_kernel).
     // Tuning switch fuse=0 keeps both launches.
     void fuse_norm_shifts() {
         if (tune(Tune::Fuse) == 0) return;
@@ -1632,7 +1633,7 @@ struct K44GpuExecutorState {
             aux_ranges(N, rd_n, wr_n);
             aux_ranges(T, rd_t, wr_t);
             if (ranges_overlap(wr_t, rd_n)) continue;
-            // The prefill form also reads the 8 tokens before each workgroup's block: the norm
+            // The prefill form also reads the 4 tokens before each workgroup's block: the norm
             // must not write over its own input either.
             if (!T.decode && ranges_overlap(wr_n, rd_n)) continue;
             N.shift_with = ops[i + 1u].second;
@@ -2793,10 +2794,20 @@ int wavec_k44_f16_forward_token64(void *Y, const void *X, const uint32_t *cluste
     });
 }
 
+// The argmax kernels read logits with 8- or 16-byte loads (16 when the pointer allows) and
+// store 4-byte ids: a pointer off those boundaries is refused before anything is launched.
+static void check_argmax_alignment(const uint32_t *ids, const void *logits) {
+    if (reinterpret_cast<uintptr_t>(logits) % 8u != 0u)
+        throw std::runtime_error("logits must be 8-byte aligned (a multiple of 4 fp16 elements)");
+    if (reinterpret_cast<uintptr_t>(ids) % 4u != 0u)
+        throw std::runtime_error("ids must be 4-byte aligned");
+}
+
 int wavec_argmax_f16(uint32_t *ids, const void *logits, uint32_t vocab, uint32_t stride,
                      uint32_t tokens, void *stream) {
     return guarded("wavec_argmax_f16", [&] {
         if (!ids || !logits) throw std::runtime_error("ids and logits are required");
+        check_argmax_alignment(ids, logits);
         if (vocab == 0u || stride == 0u || stride % 64u != 0u || tokens == 0u || tokens > stride)
             throw std::runtime_error("vocab > 0, stride a positive multiple of 64 and "
                                      "0 < tokens <= stride are required");
@@ -2818,6 +2829,7 @@ int wavec_argmax_f16_noalloc(uint32_t *ids, const void *logits, uint32_t vocab,
                              uint32_t stride, uint32_t tokens, void *stream) {
     return guarded("wavec_argmax_f16_noalloc", [&] {
         if (!ids || !logits) throw std::runtime_error("ids and logits are required");
+        check_argmax_alignment(ids, logits);
         if (vocab == 0u || stride == 0u || stride % 64u != 0u || tokens == 0u || tokens > stride)
             throw std::runtime_error("vocab > 0, stride a positive multiple of 64 and "
                                      "0 < tokens <= stride are required");

@@ -277,11 +277,11 @@ __global__ __launch_bounds__(1024) void k44_rmsnorm_regs_kernel(__half *__restri
 
 // Prefill RMSNorm with the token shift of its output fused (k44_rmsnorm_regs_kernel followed by
 // k44_token_shift_prefill_kernel, the same operations in the same order, so the same values).
-// The workgroup of 32 tokens also sums the squares of the 8 tokens before its block, reduced in
-// the order of the workgroup that owns them (same channels per thread, same shuffle tree, waves
-// in order), so their norms are that workgroup's; the shift of octets 1..3 takes the previous
-// octet's normalized values from the neighbouring lane (thread = 4 * channel lane + octet),
-// octet 0 from those 8 tokens.  Writes the norm output y, the shift output y2 and the state
+// The workgroup of 32 tokens also sums the squares of the HK = 4 tokens before its block (the
+// taps reach RF - 1 <= 4 tokens back), reduced in the order of the workgroup that owns them
+// (same channels per thread, same shuffle tree, waves in order), so their norms are that
+// workgroup's; the shift of octets 1..3 takes the previous octet's normalized values from the
+// neighbouring lane (thread = 4 * channel lane + octet), octet 0 from those 4 tokens.  Writes the norm output y, the shift output y2 and the state
 // block (each request's last RF-1 normalized tokens).  Token t of the block is at request
 // position t % seq_len; tap i applies when i <= that position.
 template <int CPT, uint32_t RF>

@@ -98,6 +98,14 @@ def test_unsupported_plans_fail_init_with_message(wavec):
         plan2.init_gpu()
 
 
+# Host-side argument checks are tested with stand-in pointers (1, 2, ...) that no device could
+# dereference: such a test runs only where no GPU is present (no /dev/kfd), so a check that
+# ever stopped rejecting could not send them to a GPU.
+host_only = pytest.mark.skipif(Path("/dev/kfd").exists(),
+                               reason="stand-in device pointers: host-only test")
+
+
+@host_only
 def test_token64_and_interleave_validate_before_touching_the_gpu(wavec):
     """Argument checks of the stand-alone kernels run on the host (no device work on failure)."""
     lib = wavec.get_lib()
@@ -204,10 +212,19 @@ def test_python_api_keeps_reference_signatures(wavec):
                 assert defs[:len(want)] == want, (cls_name, m, defs)
 
 
+@host_only
 def test_standalone_argmax_validates_before_touching_the_gpu(wavec):
     lib = wavec.get_lib()
+    # logits must be 8-byte aligned and ids 4-byte aligned (the kernels' load / store widths),
+    # in both argmax entry points, refused before any launch
+    for fn in ("wavec_argmax_f16", "wavec_argmax_f16_noalloc"):
+        for logits in (2, 4, 6, 0x1002):
+            assert getattr(lib, fn)(64, logits, 100, 64, 10, None) == -1
+            assert "8-byte aligned" in wavec.last_error()
+        assert getattr(lib, fn)(66, 64, 100, 64, 10, None) == -1
+        assert "4-byte aligned" in wavec.last_error()
     assert lib.wavec_argmax_f16(None, 1, 100, 64, 10, None) == -1
     assert "required" in wavec.last_error()
-    assert lib.wavec_argmax_f16(1, 1, 100, 100, 10, None) == -1  # stride not a multiple of 64
-    assert lib.wavec_argmax_f16(1, 1, 100, 64, 65, None) == -1  # more tokens than the stride
-    assert lib.wavec_argmax_f16(1, 1, 0, 64, 10, None) == -1
+    assert lib.wavec_argmax_f16(64, 64, 100, 100, 10, None) == -1  # stride not a multiple of 64
+    assert lib.wavec_argmax_f16(64, 64, 100, 64, 65, None) == -1  # more tokens than the stride
+    assert lib.wavec_argmax_f16(64, 64, 0, 64, 10, None) == -1

@@ -42,6 +42,11 @@ def test_noalloc_argmax_matches_allocating_entry_point(wavec):
 
 def test_noalloc_argmax_refuses_sizes_beyond_its_workspace(wavec):
     lib = wavec.get_lib()
-    # stride 2^20: 2 * 1 chunk * 2^20 partial floats > the 2^20 the array holds
-    assert lib.wavec_argmax_f16_noalloc(1, 1, 1000, 1 << 20, 64, None) == -1
+    # V = 1, stride 2^20: 2 * 1 chunk * 2^20 partial floats > the 2^20 the array holds.  Real
+    # buffers of that size: were the size check ever to let the call through, the kernels
+    # would compute a valid argmax instead of touching unmapped memory.
+    stride = 1 << 20
+    X = wavec.DeviceBuffer.from_array(np.zeros((1, stride), np.float16))
+    ids = wavec.DeviceBuffer(64 * 4)
+    assert lib.wavec_argmax_f16_noalloc(ids.ptr, X.ptr, 1, stride, 64, None) == -1
     assert "workspace" in wavec.last_error()
