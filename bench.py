@@ -540,6 +540,93 @@ def bench_token64(args):
     print(json.dumps(out), flush=True)
 
 
+def bench_conv(args):
+    """Dense convolutions of reference-compiled plans whose rows sit off the 16-byte grid: a
+    token-shifted 1-D convolution (kw 3 over 512 channels, 4,096 tokens, after a 1x1 so its
+    input is not at canvas offset 0) and single-frame 3x3 / 1x1 image convolutions (batch 1,
+    128 x 128 padded planes, tiles and taps at any element offset).  Each plan is timed on the
+    MFMA tile kernel (rows shifted into place) and with every wave forced to the VALU gathers
+    (tuning switch path=0); HIP events on the executor stream, >= 200 ms of warm-up."""
+    from snntome_amd import wavec
+
+    rng = np.random.default_rng(31)
+
+    def f16(shape, s):
+        return (rng.standard_normal(shape) * s).astype(np.float32)
+
+    def conv1d():
+        cin, W = 512, 4096
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("x", cin, 1, W, is_1d=True)
+        g.add_linear("pre", "x", "h", cin, cin, f16((cin, cin), 0.04), f16((cin,), 0.05),
+                     act="relu")
+        g.add_conv2d("conv", "h", "y", cin, cin, 1, 3, f16((cin, cin, 1, 3), 0.03),
+                     f16((cin,), 0.05), stride=1, pad=1, act="silu")
+        return g, 2.0 * cin * cin * W * (1 + 3)
+
+    def conv2d(k, c, H, W):
+        g = wavec.WaveGraph(kv_cache_max_seq=0)
+        g.add_input("img", c, H, W)
+        g.add_conv2d("conv", "img", "y", c, c, k, k, f16((c, c, k, k), 0.2 / (c * k * k) ** 0.5),
+                     f16((c,), 0.05), stride=1, pad=k // 2, act="relu")
+        return g, 2.0 * c * c * k * k * H * W
+
+    def fill(plan):
+        """Random fp16 input: 1-D plans from the device generator; an image's interior pixels
+        through the padded-plane layout (reference K44ResDesc::init: W_pad = W + 8 for widths
+        that are multiples of 64, else W + 4; pixel (y, x) of channel c at
+        c * channel_stride + (y + 1) * W_pad + 4 + x), halos left zero."""
+        c0 = plan.cmds[0]
+        if int(c0["h_out"]) <= 1:  # a 1-D token input
+            plan.fill_input_uniform(7)
+            return
+        C, H, W = int(c0["Cin"]), int(c0["h_out"]), int(c0["w_out"])
+        aligned = W % 64 == 0
+        wp = W + 8 if aligned else W + 4
+        ss = (H + 2) * wp if aligned else (2 * wp + (H * wp + 63) // 64 * 64 + 63) & ~63
+        off = (np.arange(C)[:, None, None] * ss + (np.arange(H)[None, :, None] + 1) * wp + 4
+               + np.arange(W)[None, None, :])
+        buf = np.zeros(C * ss, np.float16)
+        buf[off.ravel()] = rng.standard_normal(off.size).astype(np.float16)
+        plan.write_canvas(int(c0["src_off"]), buf)
+
+    cases = {"conv1d_k3_512ch_4096tok (1x1 + kw3)": conv1d,
+             "conv2d_3x3_64ch_128x128_batch1": lambda: conv2d(3, 64, 128, 128),
+             "conv2d_1x1_256ch_128x128_batch1": lambda: conv2d(1, 256, 128, 128)}
+    out = {}
+    for name, make in cases.items():
+        rec = {}
+        for mode, path in (("mfma", -1), ("valu", 0)):
+            wavec.reset_tuning()
+            wavec.set_tuning("path", path)
+            g, flops = make()
+            plan = g.compile()
+            plan.init_gpu()
+            fill(plan)
+            paths = [w["path"] for w in plan.exec_report()["waves"]]
+            tw = time.perf_counter()
+            while time.perf_counter() - tw < WARMUP_MIN_S:
+                plan.execute(max(1, args.warmup))
+            ms = plan.execute(args.steps)
+            plan.release_gpu()
+            rec[mode] = {"ms_per_plan": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                         "paths": paths}
+            log(f"[bench] {name} {mode}: {ms:.4f} ms/plan, {flops / (ms * 1e-3) / 1e12:.1f} "
+                f"TFLOP/s, waves {paths}")
+        rec["flops"] = flops
+        rec["mfma_over_valu"] = round(rec["valu"]["ms_per_plan"] / rec["mfma"]["ms_per_plan"], 2)
+        out[name] = rec
+    wavec.reset_tuning()
+    first = next(iter(out.values()))
+    print(json.dumps({
+        "metric": METRIC, "value": first["mfma"]["tflops"], "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": first["mfma"]["ms_per_plan"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16 (fp32 accumulate)",
+        "data": "synthetic (device-generated substrate, normal weights)",
+        "config": {"workload": "misaligned_dense_convolutions"}, "cases": out}), flush=True)
+
+
 def _envelope(rec: dict, args, data: str) -> dict:
     """The driver's contract fields around one configuration record."""
     out = {
@@ -568,6 +655,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="config 5: launch kernel by kernel instead of replaying HIP graphs")
+    ap.add_argument("--conv", action="store_true",
+                    help="dense convolutions with rows off the 16-byte grid, MFMA vs VALU")
     ap.add_argument("--token64", action="store_true",
                     help="the whitepaper's stand-alone Token64 wave at its benchmark shape")
     ap.add_argument("--cluster", type=int, default=128, help="--token64: cluster size S")
@@ -593,6 +682,9 @@ def main():
         sys.exit(2)
     if args.token64:
         bench_token64(args)
+        return
+    if args.conv:
+        bench_conv(args)
         return
     if args.tune:
         from snntome_amd import wavec

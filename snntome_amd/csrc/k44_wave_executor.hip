@@ -143,6 +143,10 @@ struct WaveExec {
     bool stream_kernel = false; // VALU: k44_gather_stream_kernel (output rows staged in LDS)
     bool weights_in_lds = true; // VALU 8-token kernel: neuron weights staged in LDS
     bool misaligned = false;    // segment starts off the 4-element grid (token-shifted taps)
+    // MFMA tile kernel over rows off the 16-byte grid (token-shifted taps, single-frame 2-D
+    // planes): aligned loads shifted into place before the LDS store (MIS variant)
+    bool mis = false;
+    bool epi_scalar = false;    // 2-byte epilogue stores (single-frame 2-D tile offsets)
     bool phase_order = false;   // synapses regrouped by token phase (segment_rows)
     uint32_t part_tokens = 0;  // row length of split-K partials (16 narrow, tokens wide)
     uint32_t cout = 0, K = 0, S = 0, cluster = 1, rows = 0;
@@ -200,7 +204,7 @@ struct WaveExec {
 struct MfmaGroupExec {
     std::vector<size_t> members;  // wave indices, plan order
     uint32_t nt = 0, mt = 0, rows = 0, items = 0, epi_items = 0, max_items = 0;
-    bool dma = false, stream_loads = false;
+    bool dma = false, stream_loads = false, mis = false;
     uint32_t prod = 0;  // product form (xprod) every member's gathers take
     k44dev::DmaShape dshape;
     size_t part_floats = 0;
@@ -453,13 +457,19 @@ struct K44GpuExecutorState {
                  " x " + std::to_string(c.B_raw) + " x " + std::to_string(wx.tokens) +
                  " contraction per tile on v_mfma_f32_16x16x32_f16";
         wx.mt = pick_mt(wx.tokens);
-        wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u) ? 64u : 32u;
-        wx.narrow = width <= 16u && tune(Tune::Narrow) != 0;
+        wx.rows_per_stage = (wx.S % 64u == 0u && cl <= 64u && !wx.mis) ? 64u : 32u;
+        // Rows off the 16-byte grid take the register-staged tile kernel (its loads pass
+        // through registers, where they are shifted into place); the narrow and LDS-ring
+        // kernels gather aligned rows only.
+        wx.narrow = width <= 16u && tune(Tune::Narrow) != 0 && !wx.mis;
         wx.part_tokens = wx.narrow ? 16u : wx.tokens;
         // 512-token workgroups of 32/64-neuron tiles stream through an LDS ring filled by
         // direct loads (3 stages in flight per workgroup instead of 1).
-        wx.dma = !wx.narrow && wx.mt == 512u && (cl == 32u || cl == 64u || cl == 128u) &&
-                 tune(Tune::Dma) != 0;
+        wx.dma = !wx.narrow && !wx.mis && wx.mt == 512u &&
+                 (cl == 32u || cl == 64u || cl == 128u) && tune(Tune::Dma) != 0;
+        if (wx.mis)
+            wx.why += " (rows off the 16-byte grid: aligned loads shifted into place, 32-row "
+                      "stages)";
         if (wx.dma) {
             wx.path = "mfma_dma";
             wx.why += " (512-token workgroups: 4-stage LDS ring filled by global_load_lds)";
@@ -644,7 +654,11 @@ struct K44GpuExecutorState {
         uint64_t x_hi = 0;
         for (uint64_t s0 : starts) x_hi = std::max(x_hi, s0);
         x_hi += (uint64_t)(wx.S - 1u) * wx.step + wx.tokens;
-        if (x_hi > n_canvas + (wx.misaligned ? kCanvasSlack - 4u : 0u))
+        // Rows off the 16-byte grid are read as the aligned 16-byte chunks around them: up to 16
+        // elements past a row's last token, inside the canvas's slack.
+        bool off16 = false;
+        for (uint64_t s0 : starts) off16 = off16 || s0 % 8u != 0u;
+        if (x_hi + (off16 ? 16u : 0u) > n_canvas + (off16 ? kCanvasSlack : 0u))
             throw std::runtime_error("wave '" + c.name + "': gather reaches past the canvas");
         uint64_t oj_hi = c.Cout - 1u;
         if (c.has_cout_map) {
@@ -725,8 +739,12 @@ struct K44GpuExecutorState {
         for (uint64_t s0 : starts) aligned8 = aligned8 && s0 % 8u == 0u;
         const uint32_t cl = c.cluster_size;
         const bool nt_ok = cl == 16u || cl == 32u || cl == 64u || cl == 128u;
-        const bool mfma_ok = nt_ok && wx.S % 32u == 0u && aligned8 && wx.tokens % 64u == 0u;
+        // Segment starts off the 16-byte grid (token-shifted taps): the MIS tile kernel, as long
+        // as consecutive positions of a segment stay 16 bytes apart (step % 8 == 0).
+        const bool mfma_ok =
+            nt_ok && wx.S % 32u == 0u && wx.step % 8u == 0u && wx.tokens % 64u == 0u;
         wx.mfma = mfma_ok && force != 0;
+        wx.mis = wx.mfma && !aligned8;
         if (force == 1 && !mfma_ok)
             throw std::runtime_error("wave '" + c.name + "': tuning path=mfma but the wave has "
                                      "no dense MFMA tiling (cluster/segment/alignment)");
@@ -740,7 +758,7 @@ struct K44GpuExecutorState {
                          ? "segments of " + std::to_string(wx.S) +
                                " positions do not fill 32-deep MFMA K-steps"
                          : (force == 0 ? std::string("forced by tuning switch path=0")
-                                  : std::string("segment rows not 16-byte aligned"));
+                                  : std::string("positions of a segment not 16 bytes apart"));
             if (wx.misaligned)
                 wx.why += "; token-shifted segment starts: funnel-shift gathers, 4 tokens per lane";
             if (wx.phase_order) wx.why += "; synapses regrouped by token phase";
@@ -905,7 +923,7 @@ struct K44GpuExecutorState {
         const uint64_t ty_hi = *std::max_element(ty.begin(), ty.end());
         uint64_t x_hi = 0;
         for (uint64_t s0 : starts) x_hi = std::max(x_hi, s0);
-        x_hi += (uint64_t)(wx.S - 1u) * wx.step + tx_hi + 64u + 4u;
+        x_hi += (uint64_t)(wx.S - 1u) * wx.step + tx_hi + 64u + 16u;  // + the shifted chunks
         if (x_hi > n_canvas + kCanvasSlack)
             throw std::runtime_error("wave '" + c.name + "': gather reaches past the canvas");
         uint64_t oj_hi = c.Cout - 1u;
@@ -937,21 +955,31 @@ struct K44GpuExecutorState {
             }
             std::memcpy(&wh[j * c.B_raw], wj, (size_t)c.B_raw * 2u);
         }
-        // Dense convolutions of 64-frame interleaved images (tiles of >= 16 output channels
-        // sharing every index row, whole 32-channel k-steps): every tile is a pixel's 64
-        // frames, 64-element aligned, so the MFMA kernels gather it through the tile tables.
-        // The single-frame layouts keep the VALU tile kernel (rows off the 16-byte grid).
+        // Dense convolutions (tiles of >= 16 output channels sharing every index row, whole
+        // 32-channel k-steps) run on MFMA through the tile tables.  64-frame interleaved
+        // images: every tile is a pixel's 64 frames, 64-element aligned.  Single-frame planes:
+        // tiles and tap shifts sit at any element offset (rows shifted into place, the MIS
+        // tile kernel), halo columns of masked tiles are not stored (MfmaTileArgs::mask_w),
+        // and the stores are 2-byte (tile offsets off the 8-byte grid), so these waves run
+        // unsplit (the split-K epilogue stores 4 tokens at a time).
         {
             const uint32_t cl = c.cluster_size;
-            bool ok = tok64 && (cl == 16u || cl == 32u || cl == 64u || cl == 128u) &&
-                      wx.S % 32u == 0u && wx.step % 8u == 0u && tune(Tune::Path) != 0;
-            for (uint64_t s0 : starts) ok = ok && s0 % 8u == 0u;
-            for (uint32_t v : tx) ok = ok && v % 64u == 0u;
-            for (uint32_t v : ty) ok = ok && v % 64u == 0u;
-            if (ok) {
+            const bool ok = (cl == 16u || cl == 32u || cl == 64u || cl == 128u) &&
+                            wx.S % 32u == 0u && wx.step % 8u == 0u && tune(Tune::Path) != 0;
+            bool al = tok64;
+            for (uint64_t s0 : starts) al = al && s0 % 8u == 0u;
+            for (uint32_t v : tx) al = al && v % 64u == 0u;
+            for (uint32_t v : ty) al = al && v % 64u == 0u;
+            if (ok && (al || !tok64)) {
                 wx.mfma = true;
+                wx.mis = !al;
+                wx.epi_scalar = !tok64;
                 configure_mfma(c, wx, wraw, rows, UINT32_MAX);
-                wx.why += "; 64-frame interleaved image: tile tables";
+                if (wx.epi_scalar) set_split(wx, 1u);
+                wx.why += tok64 ? std::string("; 64-frame interleaved image: tile tables")
+                                : std::string("; single-frame image: tile tables, rows shifted "
+                                              "into place") +
+                                      (wx.masked ? ", halo columns not stored" : "");
             }
         }
         if (!wx.mfma) wx.w.upload(wh);
@@ -1831,7 +1859,7 @@ struct K44GpuExecutorState {
                 if (!indep) break;
                 if (g.nt == w.cluster && g.mt == w.mt && g.rows == w.rows_per_stage &&
                     g.dma == w.dma && g.stream_loads == w.stream_loads && g.dshape == w.dshape &&
-                    g.prod == w.xprod && g.members.size() < 64u) {
+                    g.prod == w.xprod && g.mis == w.mis && g.members.size() < 64u) {
                     g.members.push_back(op.second);
                     g.part_floats += w.part_floats;
                     joined = true;
@@ -1845,6 +1873,7 @@ struct K44GpuExecutorState {
                 g->mt = w.mt;
                 g->rows = w.rows_per_stage;
                 g->dma = w.dma;
+                g->mis = w.mis;
                 g->stream_loads = w.stream_loads;
                 g->dshape = w.dshape;
                 g->prod = w.xprod;
@@ -1949,9 +1978,15 @@ struct K44GpuExecutorState {
         const uint64_t y0 = fused ? w.y_off_run : w.y_off;
         a.epi_vec = (y0 % 8u == 0u && a.out_stride % 8u == 0u &&
                      (!w.has_res || w.res_off % 8u == 0u) &&
-                     (w.kgroups <= 1u || w.part_tokens % 4u == 0u))
+                     (w.kgroups <= 1u || w.part_tokens % 4u == 0u) && !w.epi_scalar)
                         ? 1u
                         : 0u;
+        if (w.tile2d && w.masked) {
+            a.mask_w = w.plane.W;
+            a.mask_h = w.plane.H;
+            a.mask_wpad = w.plane.W_pad;
+            a.mask_tpf = w.tiles_per_frame;
+        }
         return a;
     }
 
@@ -2105,26 +2140,26 @@ struct K44GpuExecutorState {
 
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
                            uint32_t items, uint32_t epi_items, bool dma, const k44dev::DmaShape &ds,
-                           uint32_t prod, uint32_t max_items) {
+                           uint32_t prod, uint32_t max_items, bool mis) {
         if (mt == 16u)  // narrow (<= 16 tokens)
             K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream, prod, max_items));
         else if (dma)
             K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream, ds));
         else
-            K44_HIP(k44dev::launch_mfma_tile(d, nt, mt, rows, items, stream));
+            K44_HIP(k44dev::launch_mfma_tile(d, nt, mt, rows, items, stream, mis));
         if (epi_items) K44_HIP(k44dev::launch_splitk_epilogue(d, epi_items, stream));
     }
 
     void launch_mfma(const WaveExec &w) {
         const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, 1u, xcd_order};
         launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
-                          w.dshape, 0u, w.items);
+                          w.dshape, 0u, w.items, w.mis);
     }
 
     void launch_group(const MfmaGroupExec &g) {
         const k44dev::MfmaGroup d{g.args.p, g.start.p, (uint32_t)g.members.size(), xcd_order};
         launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.dshape,
-                          g.prod, g.max_items);
+                          g.prod, g.max_items, g.mis);
     }
 
     void launch_wave(const WaveExec &w) {

@@ -28,9 +28,9 @@ hipError_t launch_gather_dot(const GatherDotArgs &a, uint32_t slab, uint32_t ksp
 
 // MFMA tile kernel over a group of waves (one kernel configuration): `items` workgroups (the
 // group's start[n]), block mt; nt in {16,32,64,128}, mt in {64,128,256,512}, rows_per_stage in
-// {32,64}.
+// {32,64}.  mis: segment rows at any element offset (shifted into place; rows_per_stage 32).
 hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32_t rows_per_stage,
-                            uint32_t items, hipStream_t stream);
+                            uint32_t items, hipStream_t stream, bool mis = false);
 
 // Shape of an LDS-DMA MFMA launch: ring stages (4: one workgroup per CU, 3 stages in flight;
 // 2: two workgroups per CU, 1 stage in flight each; 3: 128-neuron tiles, one workgroup per CU,

@@ -5,12 +5,15 @@
 namespace k44dev {
 
 hipError_t launch_mfma_tile_nt128(const MfmaGroup &a, uint32_t mt, uint32_t rows_per_stage,
-                                  uint32_t items, hipStream_t stream) {
+                                  uint32_t items, hipStream_t stream, bool mis) {
     const dim3 grid(items, 1u, 1u), block(mt, 1u, 1u);
 #define K44_MFMA_CASE(MT)                                                                       \
     case MT:                                                                                    \
         if (rows_per_stage != 32u) return hipErrorInvalidValue;                                 \
-        hipLaunchKernelGGL((k44_mfma_tile_kernel<128, MT, 32>), grid, block, 0, stream, K44_GROUP_ARGS(a));     \
+        if (mis)                                                                                \
+            hipLaunchKernelGGL((k44_mfma_tile_kernel<128, MT, 32, true>), grid, block, 0, stream, K44_GROUP_ARGS(a)); \
+        else                                                                                    \
+            hipLaunchKernelGGL((k44_mfma_tile_kernel<128, MT, 32>), grid, block, 0, stream, K44_GROUP_ARGS(a)); \
         break;
     switch (mt) {
         K44_MFMA_CASE(512u)

@@ -4,11 +4,13 @@
 namespace k44dev {
 
 hipError_t launch_mfma_tile_nt64(const MfmaGroup &a, uint32_t mt, uint32_t rows_per_stage,
-                                 uint32_t items, hipStream_t stream) {
+                                 uint32_t items, hipStream_t stream, bool mis) {
     const dim3 grid(items, 1u, 1u), block(mt, 1u, 1u);
 #define K44_MFMA_CASE(MT)                                                                       \
     case MT:                                                                                    \
-        if (rows_per_stage == 64u)                                                              \
+        if (mis)                                                                                \
+            hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 32, true>), grid, block, 0, stream, K44_GROUP_ARGS(a)); \
+        else if (rows_per_stage == 64u)                                                         \
             hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 64>), grid, block, 0, stream, K44_GROUP_ARGS(a)); \
         else                                                                                    \
             hipLaunchKernelGGL((k44_mfma_tile_kernel<64, MT, 32>), grid, block, 0, stream, K44_GROUP_ARGS(a)); \

@@ -103,7 +103,37 @@ struct MfmaTileArgs {
     const __half *xgamma;
     uint64_t xg_base;
     uint32_t xg_shift;
+    // Single-frame 2-D outputs whose 64-token tiles span plane rows (padded-plane layout, W not
+    // a multiple of 64): token t of tile tl of its frame is pixel rel = 64 tl + (t & 63) of the
+    // padded rows, stored only when rel / mask_wpad < mask_h and rel % mask_wpad < mask_w (the
+    // halo columns stay as they are).  mask_w == 0: every token is stored.
+    uint32_t mask_w, mask_h, mask_wpad, mask_tpf;
 };
+
+// Whether token t of a wave is stored (see MfmaTileArgs::mask_w).
+__device__ __forceinline__ bool tok_stored(const MfmaTileArgs &a, uint32_t t) {
+    if (!a.mask_w) return true;
+    const uint32_t rel = 64u * ((t >> 6) % a.mask_tpf) + (t & 63u);
+    const uint32_t row = rel / a.mask_wpad;
+    return row < a.mask_h && rel - row * a.mask_wpad < a.mask_w;
+}
+
+// Eight consecutive fp16 elements m .. m+7 (m in 0..7) of the 16 held in lo:hi (two aligned
+// 16-byte chunks): the dwords selected by m / 2 and, for odd m, funnel-shifted by 16 bits.
+// Used for rows that start off the 16-byte grid (token-shifted taps), each lane with its own m.
+__device__ __forceinline__ u4_t shift_elems(const u4_t &lo, const u4_t &hi, uint32_t m) {
+    const uint32_t A[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const uint32_t q = m >> 1;
+    uint32_t d[5];
+#pragma unroll
+    for (int j = 0; j < 5; ++j)
+        d[j] = q == 0u ? A[j] : q == 1u ? A[j + 1] : q == 2u ? A[j + 2] : A[j + 3];
+    u4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        r[j] = (m & 1u) ? __builtin_amdgcn_alignbit(d[j + 1], d[j], 16u) : d[j];
+    return r;
+}
 
 // Canvas offset of token t of a wave (relative to a segment row or an output row).
 __device__ __forceinline__ uint64_t tok_x(const MfmaTileArgs &a, uint32_t t) {
@@ -211,6 +241,7 @@ __device__ __forceinline__ void mfma_epilogue_direct(const MfmaTileArgs &a,
             if (a.cmap && oj == K44_CMAP_EMPTY) continue;  // empty slot of a pattern-sorted tile
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
+                if (!tok_stored(a, t_base + 16u * tb)) continue;  // halo column of a plane row
                 const uint64_t o = oj * a.out_stride + tok_y(a, t_base + 16u * tb);
                 const float r = a.R ? __half2float(a.R[o]) : 0.0f;
                 const float v = acc[nb][tb][i] + b;
@@ -349,8 +380,12 @@ __device__ __forceinline__ void mfma_tile_epilogue(const MfmaTileArgs &a,
     }
 }
 
-template <int NT, int MT, int ROWS>
+// MIS: segment rows may start at any element (token-shifted taps, single-frame 2-D planes):
+// each lane loads the two aligned 16-byte chunks around its 8 tokens and shifts them into
+// place (shift_elems) before the LDS store; needs 32-row stages.
+template <int NT, int MT, int ROWS, bool MIS = false>
 __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(K44_GROUP_PARAMS) {
+    static_assert(!MIS || ROWS == 32, "misaligned rows: 32-row stages");
     K44_GROUP_BIND;
     uint32_t w;
     const uint32_t item = group_item_wave(grp, w);
@@ -392,26 +427,44 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(K44_GROUP_PARAMS) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) xo[i] = tok_x(a, tok0 + ((tid + i * MT) % CPR) * 8u);
     u4_t xr[CPT];  // X of the next stage, in flight during the current stage's MFMAs
+    u4_t xh[MIS ? CPT : 1];        // MIS: the aligned chunk after xr's
+    uint32_t xm[MIS ? CPT : 1];    // MIS: element offset of the lane's tokens in xr:xh
     h8_t wn[SUBS][NB], wc[SUBS][NB];  // A fragments: next stage (in flight), current stage
-    {
-        const uint32_t kk = st_begin * (uint32_t)ROWS;
+    auto load_x = [&](uint32_t st) {
+        const uint32_t kk = st * (uint32_t)ROWS;
         const uint32_t k = kk / a.S, s0 = kk - k * a.S;
-        const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step;
+        const uint64_t e0 = segr[k] + (uint64_t)s0 * a.step;
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = tid + i * MT;
-            xr[i] = *reinterpret_cast<const u4_t *>(base + (uint64_t)(c / CPR) * a.step + xo[i]);
+            const uint64_t e = e0 + (uint64_t)(c / CPR) * a.step + xo[i];
+            if constexpr (MIS) {
+                const __half *p = a.X + (e & ~7ull);
+                xr[i] = *reinterpret_cast<const u4_t *>(p);
+                xh[i] = *reinterpret_cast<const u4_t *>(p + 8);
+                xm[i] = (uint32_t)(e & 7u);
+            } else {
+                xr[i] = *reinterpret_cast<const u4_t *>(a.X + e);
+            }
         }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * MT;
+            u4_t v = xr[i];
+            if constexpr (MIS) v = shift_elems(xr[i], xh[i], xm[i]);
+            *reinterpret_cast<u4_t *>(&lds[buf][c / CPR][(c % CPR) * 8]) = v;
+        }
+    };
+    {
+        load_x(st_begin);
 #pragma unroll
         for (int u = 0; u < SUBS; ++u)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
                 wc[u][nb] = wf[((uint64_t)(st_begin * SUBS + u) * NB + nb) * 64];
-#pragma unroll
-        for (int i = 0; i < CPT; ++i) {
-            const int c = tid + i * MT;
-            *reinterpret_cast<u4_t *>(&lds[0][c / CPR][(c % CPR) * 8]) = xr[i];
-        }
+        store_x(0);
     }
     __syncthreads();
 
@@ -419,15 +472,7 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(K44_GROUP_PARAMS) {
         const int buf = (int)((st - st_begin) & 1u);
         const bool more = st + 1 < st_end;
         if (more) {  // issue next stage's X and W loads; consumed only after this stage's math
-            const uint32_t kk = (st + 1) * (uint32_t)ROWS;
-            const uint32_t k = kk / a.S, s0 = kk - k * a.S;
-            const __half *base = a.X + segr[k] + (uint64_t)s0 * a.step;
-#pragma unroll
-            for (int i = 0; i < CPT; ++i) {
-                const int c = tid + i * MT;
-                xr[i] = *reinterpret_cast<const u4_t *>(base + (uint64_t)(c / CPR) * a.step +
-                                                         xo[i]);
-            }
+            load_x(st + 1);
 #pragma unroll
             for (int u = 0; u < SUBS; ++u)
 #pragma unroll
@@ -449,11 +494,7 @@ __global__ __launch_bounds__(MT) void k44_mfma_tile_kernel(K44_GROUP_PARAMS) {
             }
         }
         if (more) {
-#pragma unroll
-            for (int i = 0; i < CPT; ++i) {
-                const int c = tid + i * MT;
-                *reinterpret_cast<u4_t *>(&lds[buf ^ 1][c / CPR][(c % CPR) * 8]) = xr[i];
-            }
+            store_x(buf ^ 1);
 #pragma unroll
             for (int u = 0; u < SUBS; ++u)
 #pragma unroll

@@ -65,3 +65,49 @@ def test_token_shifted_conv1d_matches_oracle(wavec, orc, kw, W, residual):
     err = orc.rel_err(y[:, :lim].astype(np.float64), ref[:, :lim])
     _log(f"[conv1d kw={kw} W={W} res={residual}] rel err {err:.3e} over {cout} x {lim}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("cout", [64, 128])
+@pytest.mark.parametrize("W", [100, 256])
+@pytest.mark.parametrize("residual", [False, True])
+def test_token_shifted_conv1d_on_mfma(wavec, orc, tuning, cout, W, residual):
+    """A dense token-shifted 1-D convolution (cin 256, kw 3: 3 segments of 256 channels, two of
+    them off the 16-byte grid by one element) runs on the matrix cores: the register-staged MFMA
+    tile kernel loads the aligned 16-byte chunks around each lane's tokens and shifts them into
+    place.  Both this path and the VALU funnel-shift gather (tuning path=0) are checked against
+    the fp64 oracle with tap offsets from the reference formula."""
+    rng = np.random.default_rng(cout + W + 7 * residual)
+    cin, kw = 256, 3
+    cout = cin if residual else cout
+    act = "gelu"
+    for mode in ("mfma", "valu"):
+        tuning("path", -1 if mode == "mfma" else 0)
+        plan, wc, bc = _conv1d_plan(wavec, np.random.default_rng(cout + W + 7 * residual), cin,
+                                    cout, kw, W, act, residual)
+        plan.init_gpu()
+        rep = plan.exec_report()["waves"][1]
+        _log(f"[conv1d mfma cin={cin} cout={cout} W={W} res={residual} {mode}] "
+             f"path={rep['path']} K={rep['K']} S={rep['S']} ksplit={rep['ksplit']}")
+        if mode == "mfma":
+            assert rep["path"] == "mfma_tile" and "shifted into place" in rep["why"], rep
+        else:
+            assert rep["path"] == "valu_gather_dot" and rep["misaligned"], rep
+        assert (rep["K"], rep["S"]) == (kw, cin)
+        plan.fill_input_uniform(23)
+        plan.execute_range(0, 1)
+        canvas = plan.read_canvas(0, int(plan.summary["canvas_elems"]))
+        plan.execute_range(1, 1)
+        c = plan.cmds[1]
+        st = stride_of(W)
+        h_off = int(c["src_off"])
+        syn = np.array([h_off + ch * st + (kx - kw // 2) for ch in range(cin) for kx in range(kw)],
+                       dtype=np.uint64)
+        w16 = wc.reshape(cout, cin * kw).astype(np.float16)
+        ref = orc.wave_f64(canvas, syn, w16, bc.astype(np.float16), None, cin * kw, 1, cout, st,
+                           st, st, act, res_off=h_off if residual else None)
+        y = plan.read_canvas(int(c["y_off"]), cout * st).view(np.float16).reshape(cout, st)
+        lim = W if W + kw // 2 <= st else W - kw // 2
+        err = orc.rel_err(y[:, :lim].astype(np.float64), ref[:, :lim])
+        _log(f"[conv1d mfma cin={cin} cout={cout} W={W} res={residual} {mode}] rel err {err:.3e}")
+        assert err <= TOL
+        plan.release_gpu()

@@ -314,3 +314,64 @@ def test_token64_dense_convs_on_mfma(wavec, tuning, frames, reuse, H, W):
         err = orc.rel_err(got.astype(np.float64), ref_fn(dev))
         _log(f"[token64 mfma F={frames} {H}x{W}] {out}: rel err {err:.3e}")
         assert err <= TOL, out
+
+
+@pytest.mark.parametrize("frames", [1, 3])
+@pytest.mark.parametrize("H,W", [(8, 64), (7, 20), (5, 130)])
+def test_single_frame_dense_convs_on_mfma(wavec, frames, H, W):
+    """Dense convolutions of single-frame images (batch 1..63, the padded-plane layout: tiles
+    and 3x3 tap shifts at any element offset, masked tiles spanning plane rows for widths that
+    are not multiples of 64) take the MFMA tile kernel with rows shifted into place: a 3x3
+    convolution over 64 channels (9 segments of 64) and a 1x1 with a residual; a stride-2 3x3
+    follows.  Every command against cnn_oracle on the tensor the device read; the output halos
+    stay zero padding."""
+    rng = np.random.default_rng(frames * 11 + H * W)
+    c0, c1 = 64, 64
+    w1, b1 = _conv_params(rng, c0, c1, 3)
+    w2, b2 = _conv_params(rng, c1, c1, 1)
+    w3, b3 = _conv_params(rng, c1, 32, 3)
+    f32 = lambda a: a.astype(np.float32)
+    g = wavec.WaveGraph(kv_cache_max_seq=0, batch_size=frames)
+    g.add_input("img", c0, H, W)
+    g.add_conv2d("c1", "img", "a", c0, c1, 3, 3, f32(w1), f32(b1), stride=1, pad=1, act="relu")
+    g.add_conv2d("c2", "a", "b", c1, c1, 1, 1, f32(w2), f32(b2), stride=1, pad=0, act="silu",
+                 res_blob="a")
+    g.add_conv2d("c3", "b", "y", c1, 32, 3, 3, f32(w3), f32(b3), stride=2, pad=1, act="none")
+    plan = g.compile()
+    plan.init_gpu()
+    rep = plan.exec_report()["waves"]
+    _log(f"[single-frame mfma F={frames} {H}x{W}] " + ", ".join(
+        f"{w['path']} K={w['K']} S={w['S']} ksplit={w['ksplit']}" for w in rep))
+    # the 3x3 and the 1x1 (dense index rows); the stride-2 convolution's index rows compile to
+    # one-position segments (no dense tiling: the VALU tile kernel), checked all the same
+    assert all(w["path"] == "mfma_tile" and "single-frame image" in w["why"] for w in rep[:2]), rep
+    lay = lambda h, w: co.Layout2D(h, w, frames)
+    x = _f16(rng, (frames, c0, H, W))
+    region = np.zeros(c0 * lay(H, W).channel_stride, np.float16)
+    region[lay(H, W).offsets(c0).ravel()] = x.ravel()
+    plan.write_canvas(int(plan.cmds[0]["src_off"]), region)
+    dev = {"img": x}
+    # the stride-2 convolution (S2D polyphase planes, as the reference compiles it) produces
+    # floor(H/2) x floor(W/2) pixels: the textbook output's first rows and columns
+    checks = {"a": (c1, lambda t: co.conv2d_f64(t["img"], w1, b1, 1, 1, "relu")),
+              "b": (c1, lambda t: co.conv2d_f64(t["a"], w2, b2, 1, 0, "silu", t["a"])),
+              "y": (32, lambda t: co.conv2d_f64(t["b"], w3, b3, 2, 1))}
+    order = iter(["a", "b", "y"])
+    for i, c in enumerate(plan.cmds):
+        plan.execute_range(i, 1)
+        if c["type"] != "K44_WAVE":
+            continue
+        out = next(order)
+        C, ref_fn = checks[out]
+        h, w = int(c["h_out"]), int(c["w_out"])
+        assert (h, w) == ((H, W) if out != "y" else (H // 2, W // 2)), (out, h, w)
+        L = lay(h, w)
+        buf = plan.read_canvas(int(c["y_off"]), C * L.channel_stride).view(np.float16)
+        got = buf[L.offsets(C)]
+        dev[out] = got
+        err = orc.rel_err(got.astype(np.float64), ref_fn(dev)[:, :, :h, :w])
+        _log(f"[single-frame mfma F={frames} {H}x{W}] {out}: rel err {err:.3e}")
+        assert err <= TOL, out
+        halo = np.ones(C * L.channel_stride, bool)
+        halo[L.offsets(C).ravel()] = False
+        assert not buf[halo].any(), f"{out}: halo written"
