@@ -256,7 +256,8 @@ int wavec_gpu_read_canvas_2d(void *handle, unsigned long long elem_off, unsigned
  *   "stream_kernel" 0 | 1; "narrow" 0 no narrow MFMA kernel; "narrow_chunk" >= 16 k-steps;
  *   "group" 0 no group launches; "group_split" 0 groups keep their members' split-K;
  *   "fuse" 0 no folded multiplies or RMSNorm + token-shift kernels; "sort" 0 segments in
- *   index-row order; "wlds" 0 VALU weights read per batch; "t64_ring" 0 | 1 Token64 kernel;
+ *   index-row order; "wlds" 0 VALU weights read per batch; "t64_ring" 0 | 1 | 2 Token64
+ *   per-wave kernel, 64-neuron x 4-tile or 128-neuron x 2-tile ring kernel only;
  *   "xcd_order" 0 | 1 | 2 MFMA tile kernels take work items in plain workgroup order, as
  *   contiguous ranges per XCD, or as per-wave shares of every XCD, longest waves first (the
  *   automatic choice); "narrow_wgs" >= 1 workgroups a narrow wave of 64/128-neuron tiles is

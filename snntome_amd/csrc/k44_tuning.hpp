@@ -25,7 +25,7 @@ enum class Tune : int {
     Fuse,          // "fuse":          0 = no folded multiplies / RMSNorm+token-shift kernels
     SortSegments,  // "sort":          0 = segments in index-row order (not address order)
     WeightsInLds,  // "wlds":          0 = 8-token VALU kernel reads weights per batch
-    Token64Ring,   // "t64_ring":      0 per-wave Token64 kernel, 1 64-neuron ring kernel
+    Token64Ring,   // "t64_ring":      0 per-wave Token64 kernel, 1 / 2 64- / 128-neuron ring kernel
     XcdOrder,      // "xcd_order":     0 = MFMA tile kernels take items in workgroup order,
                    //                  1 = contiguous item ranges per XCD, 2 = per-wave shares
     NarrowWgs,     // "narrow_wgs":    workgroups a narrow wave of >= 64-neuron tiles is split to

@@ -67,7 +67,7 @@ const TuneValues kTuneValues[(int)Tune::Count] = {
     {V01, 0},          // fuse
     {V01, 0},          // sort
     {V01, 0},          // wlds
-    {V01, 0},          // t64_ring
+    {0x7u, 0},         // t64_ring 0 | 1 | 2
     {0x7u, 0},         // xcd_order 0 | 1 | 2
     {0u, 1},           // narrow_wgs >= 1
     {V01, 0},          // narrow_reduce

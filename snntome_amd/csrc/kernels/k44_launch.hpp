@@ -71,7 +71,8 @@ struct Token64Args {
     const __half *bias;    // [Cout] or nullptr (zero)
     uint32_t Cin, Cout, B_vec16, cluster, tiles;
 };
-// ring_mode: -1 automatic, 0 per-wave kernel, 1 the 64-neuron ring kernel where it applies.
+// ring_mode: -1 automatic, 0 per-wave kernel, 1 only the 64-neuron x 4-tile ring kernel, 2 only
+// the 128-neuron x 2-tile ring kernel (each where the shape allows it, else the per-wave kernel).
 hipError_t launch_token64(const Token64Args &a, hipStream_t stream, int ring_mode = -1);
 
 // GPU weight interleave: row-major [neurons][8 * B_vec8] fp16 -> WMMA vector order.

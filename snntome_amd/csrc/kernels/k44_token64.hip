@@ -125,16 +125,24 @@ __global__ __launch_bounds__(256) void k44_token64_kernel(Token64Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// LDS-ring variant for the large shapes: clusters of a multiple of 64 neurons, batches of whole
-// groups of 4 tiles, even B_vec16 (whole 32-deep k-steps), B <= 4096.  Workgroup = 64 neurons x
-// 4 tiles (4 waves, one tile each).  The cluster's index row is staged in LDS once; then every
+// LDS-ring kernel for the large shapes: clusters of a multiple of 64 neurons, batches of whole
+// groups of TW tiles, even B_vec16 (whole 32-deep k-steps), B <= 4096.  Workgroup = 64*NBK
+// neurons of one cluster x TW tiles.  The cluster's index row is staged in LDS once; then every
 // k-step's 32 gathered rows per tile (128 B each: one global_load_lds_dwordx4 covers 8 rows) and
-// its 64-neuron A fragments (1 KiB per 16-neuron block, contiguous in the WMMA order: one
-// dwordx4 direct load per wave) go memory -> LDS directly, into a ring of 4 stages with 3 in
-// flight (a 6-deep ring measured the same), synchronised exactly as the dense-cluster LDS-ring
-// kernel (lds_ring, k44_mfma_dma.hpp):
-// per stage vmcnt(2D) + bare s_barrier, LDS reads in inline asm with an explicit lgkmcnt wait.
-// Rows of out-of-range indices are read from a zero row in device memory.
+// its A fragments (1 KiB per 16-neuron block, contiguous in the WMMA order) go memory -> LDS
+// directly, into a ring of NBUF stages with NBUF-1 in flight, synchronised as the dense-cluster
+// LDS-ring kernel (lds_ring, k44_mfma_dma.hpp): per stage a vmcnt wait + bare s_barrier, LDS reads
+// in inline asm with an explicit lgkmcnt wait.  Rows of out-of-range indices are read from a
+// zero row in device memory.
+//
+// Producer and consumer waves.  NBK*TW consumer waves each own one 64-neuron x 64-token output
+// block and only read LDS and multiply; P producer waves issue every direct load of a stage
+// (rows first, then weight blocks, spread evenly).  A wave that both issues a stage's loads and
+// multiplies serialises the two: issuing stalls while the memory pipeline is full, and the
+// MFMAs of that SIMD wait behind it.  With separate producer waves (one per SIMD for P = 4) the
+// multiplies of stage i run while the loads of stage i+NBUF-1 issue.  Both kinds of wave pass
+// the same barrier per stage: a producer refills slot (i-1) % NBUF only after every consumer
+// finished reading it (its reads end with lgkmcnt(0) before the consumer reaches barrier i).
 // ---------------------------------------------------------------------------------------------
 __device__ __attribute__((aligned(16))) uint4 k44_t64_zero_row[8];  // 128 zero bytes
 
@@ -144,27 +152,26 @@ __device__ __forceinline__ uint32_t t64_lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
-// NBK 64-neuron blocks of one cluster per workgroup (1, or 2 when the cluster is a multiple of
-// 128 neurons: both blocks then share every gathered row), 4 tiles, 4 * NBK waves: wave w owns
-// tile w % 4 and block w / 4; the NBK waves of a tile split its row loads, every wave loads one
-// 16-neuron block of A fragments per stage.
-template <int NBK, int NBUF>
-__global__ __launch_bounds__(256 * NBK) void k44_token64_ring_kernel(Token64Args a) {
-    constexpr int NB = 4, TW = 4;
-    constexpr int XST = 32 * 128;          // bytes of one tile's stage: 32 rows x 64 tokens x fp16
-    constexpr int WST = NBK * NB * 64 * 16;  // bytes of one stage's A fragments
-    constexpr int XR = 4 / NBK;            // 8-row loads per wave per stage
-    constexpr int D = XR + 1;              // direct loads per wave per stage
-    __shared__ __attribute__((aligned(16))) char xr[NBUF][TW][XST];
-    __shared__ __attribute__((aligned(16))) char wr[NBUF][WST];
+template <int NBK, int TW, int NBUF, int P>
+__global__ __launch_bounds__(64 * (NBK * TW + P)) void k44_token64_ring_kernel(Token64Args a) {
+    constexpr int NB = 4;                       // 16-neuron blocks per consumer wave
+    constexpr int NC = NBK * TW;                // consumer waves
+    constexpr int XST = 32 * 128;               // bytes of one tile's stage: 32 rows x 64 tokens
+    constexpr int WST = NBK * NB * 1024;        // bytes of one stage's A fragments
+    constexpr int SLOT = TW * XST + WST;
+    constexpr int RP = 4 * TW / P, WP = 4 * NBK / P;  // row / weight loads per producer per stage
+    static_assert(RP * P == 4 * TW && WP * P == 4 * NBK, "P divides the row and weight loads");
+    constexpr int DP = RP + WP;
+    __shared__ __attribute__((aligned(16))) char ring[NBUF][SLOT];
     extern __shared__ uint32_t ix[];  // B entries (dynamic: sized by the launch)
 
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wt = wave % TW, wb = wave / TW;  // tile and 64-neuron block of this wave
     // Workgroup p runs on XCD p % 8.  The workgroups of one cluster gather the same rows: when
     // the grid allows, they are placed 8 apart (p = 8 * (bpc * q + h) + r holds block h of
-    // cluster 8q + r), so they share one XCD's L2 instead of each XCD fetching the rows.
+    // cluster 8q + r), so they share one XCD's L2 instead of each XCD fetching the rows.  The
+    // tile groups of one block (blockIdx.y) are gridDim.x apart: the same XCD whenever gridDim.x
+    // is a multiple of 8, so they share the block's weights through that L2.
     uint32_t bx = blockIdx.x;
     {
         const uint32_t bpc = a.cluster / (64u * NBK);  // workgroups per cluster
@@ -174,51 +181,66 @@ __global__ __launch_bounds__(256 * NBK) void k44_token64_ring_kernel(Token64Args
         }
     }
     const uint32_t jw = bx * 64u * NBK;  // first neuron of the workgroup
-    const uint32_t j0 = jw + 64u * (uint32_t)wb;  // first neuron of this wave
-    const uint32_t tile = blockIdx.y * TW + (uint32_t)wt;
     const uint32_t B = a.B_vec16 * 16u, ksteps = B / 32u;
     const uint32_t *irow = a.idx + (uint64_t)(jw / a.cluster) * B;
-    for (uint32_t q = (uint32_t)tid; q < B; q += 256u * NBK) {
+    for (uint32_t q = (uint32_t)tid; q < B; q += 64u * (NC + P)) {
         const uint32_t v = irow[q];
         ix[q] = v < a.Cin ? v : 0xffffffffu;
     }
     __syncthreads();
-
-    const char *xt = reinterpret_cast<const char *>(a.X + (uint64_t)tile * a.Cin * 64u);
-    const char *zrow = reinterpret_cast<const char *>(k44_t64_zero_row);
     const int gr = lane >> 3, gc = (lane & 7) * 16;  // row within an 8-row piece, byte column
-    // A fragments of 16-neuron block `wave` of the workgroup: WMMA vectors
-    // (jw/16 + wave, 2 ks .. 2 ks + 1, 0..31), 1 KiB contiguous per k-step.
-    const char *wsrc = reinterpret_cast<const char *>(a.w_wmma) +
-                       ((uint64_t)(jw / 16u + (uint32_t)wave) * a.B_vec16 * 32u) * 16u;
-    // This wave loads 8-row pieces p = wb * XR .. wb * XR + XR - 1 of its tile's stage.
-    const uint32_t ix_addr = t64_lds_addr(&ix[8 * wb * XR + gr]);
 
-    auto load_stage = [&](uint32_t ks, int buf) {
-        uint32_t v[XR];
-        const uint32_t base = ix_addr + ks * 128u;
-        if constexpr (XR == 4)
-            asm volatile("ds_read_b32 %0, %4\n\tds_read_b32 %1, %4 offset:32\n\t"
-                         "ds_read_b32 %2, %4 offset:64\n\tds_read_b32 %3, %4 offset:96\n\t"
-                         "s_waitcnt lgkmcnt(0)"
-                         : "=v"(v[0]), "=v"(v[1]), "=v"(v[2]), "=v"(v[3]) : "v"(base) : "memory");
-        else
-            asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:32\n\t"
-                         "s_waitcnt lgkmcnt(0)"
-                         : "=v"(v[0]), "=v"(v[1]) : "v"(base) : "memory");
+    if (wave >= NC) {
+        // Producer pw: row loads r = pw + P*m (piece r % 4 of tile r / 4 of the group), weight
+        // blocks b = pw + P*m.
+        const int pw = wave - NC;
+        const char *zrow = reinterpret_cast<const char *>(k44_t64_zero_row) + gc;
+        const uint64_t wblk = (uint64_t)a.B_vec16 * 32u * 16u;  // bytes of one 16-neuron block
+        const char *xrow[RP];
+        uint32_t ldsx[RP], ixa[RP];
 #pragma unroll
-        for (int i = 0; i < XR; ++i) {
-            const char *src = v[i] != 0xffffffffu ? xt + (uint64_t)v[i] * 128u + gc : zrow + gc;
-            __builtin_amdgcn_global_load_lds(
-                (kglobal_void *)src,
-                (__attribute__((address_space(3))) void *)&xr[buf][wt][(wb * XR + i) * 1024], 16, 0,
-                0);
+        for (int m = 0; m < RP; ++m) {
+            const int r = pw + P * m;
+            const uint32_t t = blockIdx.y * TW + (uint32_t)(r / 4);
+            xrow[m] = reinterpret_cast<const char *>(a.X + (uint64_t)t * a.Cin * 64u) + gc;
+            ldsx[m] = (uint32_t)((r / 4) * XST + (r % 4) * 1024);
+            ixa[m] = t64_lds_addr(&ix[8 * (r % 4) + gr]);
         }
-        __builtin_amdgcn_global_load_lds((kglobal_void *)(wsrc + (uint64_t)ks * 1024u + lane * 16),
-                                         (__attribute__((address_space(3))) void *)&wr[buf][wave * 1024],
-                                         16, 0, 0);
-    };
+        const char *wsrc = reinterpret_cast<const char *>(a.w_wmma) +
+                           (uint64_t)(jw / 16u + (uint32_t)pw) * wblk + lane * 16;
+        auto load_stage = [&](uint32_t ks, int buf) {
+            uint32_t v[RP];
+#pragma unroll
+            for (int m = 0; m < RP; ++m)
+                asm volatile("ds_read_b32 %0, %1" : "=v"(v[m]) : "v"(ixa[m] + ks * 128u) : "memory");
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            // The index words are used only after the wait (inline-asm reads are invisible to
+            // the compiler's own wait insertion: without this it may compute addresses first).
+#pragma unroll
+            for (int m = 0; m < RP; ++m) asm volatile("" : "+v"(v[m]));
+#pragma unroll
+            for (int m = 0; m < RP; ++m) {
+                const char *src = v[m] != 0xffffffffu ? xrow[m] + (uint64_t)v[m] * 128u : zrow;
+                __builtin_amdgcn_global_load_lds(
+                    (kglobal_void *)src, (__attribute__((address_space(3))) void *)&ring[buf][ldsx[m]],
+                    16, 0, 2);  // non-temporal: gathered rows are not read again
+            }
+#pragma unroll
+            for (int m = 0; m < WP; ++m) {
+                const int b = pw + P * m;
+                __builtin_amdgcn_global_load_lds(
+                    (kglobal_void *)(wsrc + (uint64_t)(P * m) * wblk + (uint64_t)ks * 1024u),
+                    (__attribute__((address_space(3))) void *)&ring[buf][TW * XST + b * 1024], 16, 0,
+                    0);
+            }
+        };
+        lds_ring<NBUF, DP>(ksteps, load_stage, [](int) {});
+        return;
+    }
 
+    const int wt = wave % TW, wb = wave / TW;  // tile and 64-neuron block of this consumer
+    const uint32_t j0 = jw + 64u * (uint32_t)wb;
+    const uint32_t tile = blockIdx.y * TW + (uint32_t)wt;
     const int g = lane >> 4;
     f4_t acc[NB][4];
 #pragma unroll
@@ -232,10 +254,10 @@ __global__ __launch_bounds__(256 * NBK) void k44_token64_ring_kernel(Token64Args
         for (int tb = 0; tb < 4; ++tb) acc[nb][tb] = b0;
     }
     const int tr_row = 8 * g + ((lane & 15) >> 2), tr_col = 4 * (lane & 3);
-    const uint32_t xa = t64_lds_addr(&xr[0][wt][tr_row * 128 + tr_col * 2]);
-    const uint32_t wa = t64_lds_addr(&wr[0][wb * NB * 1024 + lane * 16]);
+    const uint32_t xa = t64_lds_addr(&ring[0][wt * XST + tr_row * 128 + tr_col * 2]);
+    const uint32_t wa = t64_lds_addr(&ring[0][TW * XST + wb * NB * 1024 + lane * 16]);
     auto compute = [&](int buf) {
-        const uint32_t x0 = xa + (uint32_t)buf * (TW * XST), w0 = wa + (uint32_t)buf * WST;
+        const uint32_t x0 = xa + (uint32_t)buf * SLOT, w0 = wa + (uint32_t)buf * SLOT;
         h8_t af[NB];
         h4_t lo[4], hi[4];
 #pragma unroll
@@ -259,9 +281,9 @@ __global__ __launch_bounds__(256 * NBK) void k44_token64_ring_kernel(Token64Args
                 acc[nb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[nb], b, acc[nb][tb], 0, 0, 0);
         }
     };
+    lds_ring<NBUF, 1>(ksteps, [](uint32_t, int) {}, compute);
 
-    lds_ring<NBUF, D>(ksteps, load_stage, compute);
-
+    // C layout: lane holds C[4g + i][lane & 15] of every 16x16 tile; round toward zero.
     __half *yt = a.Y + ((uint64_t)tile * a.Cout + j0) * 64u + (lane & 15);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -273,24 +295,30 @@ __global__ __launch_bounds__(256 * NBK) void k44_token64_ring_kernel(Token64Args
                     __float2half_rz(acc[nb][tb][i2]);
 }
 
-bool token64_ring_ok(const Token64Args &a) {
-    return a.cluster % 64u == 0u && a.tiles % 4u == 0u && a.B_vec16 % 2u == 0u &&
-           a.B_vec16 * 16u <= (uint32_t)T64R_IDX_MAX;
+static bool token64_ring_base_ok(const Token64Args &a) {
+    return a.B_vec16 % 2u == 0u && a.B_vec16 * 16u <= (uint32_t)T64R_IDX_MAX;
+}
+// 128-neuron x 2-tile workgroups (both 64-neuron blocks share every gathered row).
+static bool token64_ring128_ok(const Token64Args &a) {
+    return token64_ring_base_ok(a) && a.cluster % 128u == 0u && a.tiles % 2u == 0u;
+}
+// 64-neuron x 4-tile workgroups.
+static bool token64_ring_ok(const Token64Args &a) {
+    return token64_ring_base_ok(a) && a.cluster % 64u == 0u && a.tiles % 4u == 0u;
 }
 
 hipError_t launch_token64(const Token64Args &a, hipStream_t stream, int ring_mode) {
-    if (token64_ring_ok(a) && ring_mode != 0) {
-        // Two 64-neuron blocks sharing every gathered row: half the row traffic but half the
-        // workgroups; measured equal at 128-neuron clusters, slightly faster from 256 on.
-        const size_t ix_bytes = (size_t)a.B_vec16 * 16u * 4u;
-        if (a.cluster % 256u == 0u && ring_mode != 1) {
-            const dim3 grid(a.Cout / 128u, a.tiles / 4u, 1u), block(512u, 1u, 1u);
-            hipLaunchKernelGGL((k44_token64_ring_kernel<2, 6>), grid, block, ix_bytes, stream, a);
-        } else {
-            // (A 3-stage ring, two workgroups per CU, measured 3 % slower at the whitepaper shape.)
-            const dim3 grid(a.Cout / 64u, a.tiles / 4u, 1u), block(256u, 1u, 1u);
-            hipLaunchKernelGGL((k44_token64_ring_kernel<1, 4>), grid, block, ix_bytes, stream, a);
-        }
+    const size_t ix_bytes = (size_t)a.B_vec16 * 16u * 4u;
+    // One producer wave per SIMD (P = 4): one, two and eight producers measured 25.7, 21.9 and
+    // 21.7 us against 21.4 at the whitepaper shape; a 6-stage ring 21.8-22.0.
+    if (ring_mode != 0 && ring_mode != 1 && token64_ring128_ok(a)) {
+        const dim3 grid(a.Cout / 128u, a.tiles / 2u, 1u), block(64u * (4u + 4u), 1u, 1u);
+        hipLaunchKernelGGL((k44_token64_ring_kernel<2, 2, 4, 4>), grid, block, ix_bytes, stream, a);
+        return hipGetLastError();
+    }
+    if (ring_mode != 0 && ring_mode != 2 && token64_ring_ok(a)) {
+        const dim3 grid(a.Cout / 64u, a.tiles / 4u, 1u), block(64u * (4u + 4u), 1u, 1u);
+        hipLaunchKernelGGL((k44_token64_ring_kernel<1, 4, 4, 4>), grid, block, ix_bytes, stream, a);
         return hipGetLastError();
     }
     const uint32_t c16 = a.cluster / 16u;

@@ -78,40 +78,36 @@ def test_token64_matches_oracle(wavec, orc, cluster, B_vec16, batch):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("batch", [64, 256])
-def test_token64_out_of_range_index_reads_zero(wavec, orc, batch):
-    err = _token64_case(wavec, orc, Cin=500, Cout=64, cluster=64, B_vec16=2, batch=batch, seed=7,
-                        bad_index=True)
+@pytest.mark.parametrize("cluster,batch", [(64, 64), (64, 256), (128, 128)])
+def test_token64_out_of_range_index_reads_zero(wavec, orc, cluster, batch):
+    """Per-wave kernel (one tile), 64-neuron and 128-neuron ring kernels."""
+    err = _token64_case(wavec, orc, Cin=500, Cout=cluster, cluster=cluster, B_vec16=2,
+                        batch=batch, seed=7, bad_index=True)
     assert err <= TOL
 
 
 @pytest.mark.parametrize("cluster,B_vec16,batch", [(64, 2, 256), (128, 8, 512), (192, 6, 256),
-                                                   (64, 64, 256), (256, 4, 256), (512, 256, 256)])
+                                                   (64, 64, 256), (256, 4, 256), (512, 256, 256),
+                                                   (128, 4, 128), (256, 2, 384)])
 def test_token64_ring_matches_oracle_and_fallback(wavec, orc, tuning, cluster, B_vec16,
                                                   batch):
     """Shapes the LDS-ring kernels take (clusters of whole 64-neuron blocks, whole 4-tile
-    groups, even B_vec16; 128-neuron workgroups sharing the rows when the cluster allows it):
-    within tolerance of the oracle, and bit-identical to the per-wave kernel (same k-step
-    accumulation order from the bias).  Tuning switch t64_ring: -1 automatic, 1 64-neuron
-    ring only, 0 per-wave kernel."""
+    groups for 64-neuron workgroups, whole 2-tile groups for 128-neuron workgroups, even
+    B_vec16): within tolerance of the oracle, and bit-identical to the per-wave kernel (same
+    k-step accumulation order from the bias).  Tuning switch t64_ring: -1 automatic, 1 the
+    64-neuron ring only, 2 the 128-neuron ring only, 0 per-wave kernel."""
     Cout = cluster * 2
     ys = {}
-    for ring in ("auto", "1", "0"):
-        if ring == "auto":
-            tuning("t64_ring", -1)
-            err = _token64_case(wavec, orc, Cin=5000, Cout=Cout, cluster=cluster,
-                                B_vec16=B_vec16, batch=batch, seed=cluster + B_vec16)
-            assert err <= TOL
-            ys[ring] = _LAST_Y[0]
-            continue
-        tuning("t64_ring", int(ring))
+    for ring in ("auto", "1", "2", "0"):
+        tuning("t64_ring", -1 if ring == "auto" else int(ring))
         err = _token64_case(wavec, orc, Cin=5000, Cout=Cout, cluster=cluster, B_vec16=B_vec16,
                             batch=batch, seed=cluster + B_vec16)
         _log(f"[token64 ring={ring} cluster={cluster} B_vec16={B_vec16} batch={batch}] "
              f"rel err {err:.3e}")
         assert err <= TOL
         ys[ring] = _LAST_Y[0]
-    assert np.array_equal(ys["1"], ys["0"]) and np.array_equal(ys["auto"], ys["0"])
+    for ring in ("auto", "1", "2"):
+        assert np.array_equal(ys[ring], ys["0"]), ring
 
 
 @pytest.mark.parametrize("batch", [64, 256])
