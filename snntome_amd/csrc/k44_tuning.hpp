@@ -32,6 +32,8 @@ enum class Tune : int {
                    //                  reach (>= 1; contraction chunks of >= 16 k-steps)
     NarrowReduce,  // "narrow_reduce": 0 = split narrow waves reduce in k44_splitk_epilogue_kernel,
                    //                  1 = the last workgroup of each tile reduces in the launch
+    DmaProd,       // "dma_prod":      0 = LDS-ring MFMA waves load and multiply in every wave,
+                   //                  1 = producer waves issue the loads (4-stage ring)
     Count
 };
 

@@ -42,7 +42,7 @@ std::atomic<int> g_tune[(int)Tune::Count];
 const char *const kTuneKeys[(int)Tune::Count] = {
     "path", "dma", "dma_stages", "nt", "splitk", "lane8", "ksplit", "stream_kernel", "narrow",
     "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring", "xcd_order",
-    "narrow_wgs", "narrow_reduce"};
+    "narrow_wgs", "narrow_reduce", "dma_prod"};
 // Values each switch honours besides -1: a set of small values (bit v of `set`), or every
 // value >= `min` when `set` is 0.  Anything else is refused, so an A/B run cannot measure a
 // configuration other than the one it asked for.
@@ -71,6 +71,7 @@ const TuneValues kTuneValues[(int)Tune::Count] = {
     {0x7u, 0},         // xcd_order 0 | 1 | 2
     {0u, 1},           // narrow_wgs >= 1
     {V01, 0},          // narrow_reduce
+    {V01, 0},          // dma_prod
 };
 struct TuneInit {
     TuneInit() {
@@ -488,8 +489,16 @@ struct K44GpuExecutorState {
             // 128-neuron tiles: 128 accumulator registers per lane leave one workgroup per
             // CU, whose LDS holds a 3-stage ring (2 stages in flight).
             if (cl == 128u) wx.dshape.nbuf = 3u;
+            // Producer waves issue every load of a stage, the 8 other waves only multiply:
+            // a 4-stage ring, one workgroup of 8 + P waves per CU (32/64-neuron tiles).
+            if (tune(Tune::DmaProd) == 1 && cl != 128u) {
+                wx.dshape.prod = cl == 32u ? 2u : 4u;
+                wx.dshape.nbuf = 4u;
+            }
             wx.dshape.stream_loads = wx.stream_loads;
             wx.why += "; " + std::to_string(wx.dshape.nbuf) + "-stage ring";
+            if (wx.dshape.prod)
+                wx.why += ", " + std::to_string(wx.dshape.prod) + " producer waves";
         }
         if (wx.narrow) {
             wx.path = "mfma_narrow";
@@ -2084,6 +2093,7 @@ struct K44GpuExecutorState {
               << ", \"stream_loads\": " << (w.stream_loads ? "true" : "false")
               << ", \"stream_kernel\": " << (w.stream_kernel ? "true" : "false")
               << ", \"ring_stages\": " << (w.dma ? w.dshape.nbuf : 0u)
+              << ", \"ring_producers\": " << (w.dma ? w.dshape.prod : 0u)
               << ", \"xprod\": " << w.xprod
               << ", \"reduce_in_kernel\": " << (w.reduce_in_kernel ? "true" : "false")
               << ", \"flops\": " << (long long)w.flops

@@ -38,8 +38,9 @@ hipError_t launch_mfma_tile(const MfmaGroup &g, uint32_t nt, uint32_t mt, uint32
 struct DmaShape {
     uint32_t nbuf = 4;
     bool stream_loads = false;
+    uint32_t prod = 0;  // producer waves (0: every wave loads and multiplies)
     bool operator==(const DmaShape &o) const {
-        return nbuf == o.nbuf && stream_loads == o.stream_loads;
+        return nbuf == o.nbuf && stream_loads == o.stream_loads && prod == o.prod;
     }
 };
 

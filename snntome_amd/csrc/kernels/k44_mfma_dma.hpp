@@ -103,11 +103,23 @@ __device__ __forceinline__ h4_t ds_read_tr16_at(uint32_t addr) {
 // NTX: the direct loads use the non-temporal cache policy (substrates far beyond the caches).
 // NT = 128 (a 128-neuron tile: twice the MFMA work per gathered stage; 128 accumulator registers
 // per lane, so one workgroup per CU) takes a 3-stage ring (125 KiB of LDS, 2 stages in flight).
-template <int NT, bool NTX, int NBUF = 4>
-__global__ __launch_bounds__(512) void k44_mfma_dma_kernel(K44_GROUP_PARAMS) {
+//
+// P > 0: producer and consumer waves.  The 8 waves above stop issuing loads and only read LDS,
+// multiply and run the epilogue (consumers); P more waves (producers) issue every direct load of
+// a stage: ROWS / P row loads and NT / (16 P) A-fragment loads of 1 KiB (dwordx4) each.  A wave
+// that both issues a stage's loads and multiplies serialises the two (issuing stalls while the
+// memory pipeline is full, and its SIMD's MFMAs wait behind it); with the roles split the
+// multiplies of stage i run while the loads of stage i+NBUF-1 issue.  Both roles pass the same
+// barrier per stage (a producer refills a slot only after every consumer's reads of it
+// completed); the producers then end, and the epilogue's barrier waits for the consumers only
+// (s_barrier counts the waves of the workgroup that have not ended).
+template <int NT, bool NTX, int NBUF = 4, int P = 0>
+__global__ __launch_bounds__(512 + 64 * P) void k44_mfma_dma_kernel(K44_GROUP_PARAMS) {
     K44_GROUP_BIND;
     static_assert(NT == 32 || NT == 64 || NT == 128,
                   "A-fragment stage must be whole dword loads per wave");
+    static_assert(P == 0 || ((32 % P) == 0 && ((NT / 16) % P) == 0),
+                  "producers split the row and A-fragment loads evenly");
     constexpr int MT = 512, ROWS = 32;
     constexpr int NB = NT / 16;
     constexpr int PITCH = MT + 16;          // halves; 32-byte skew between rows
@@ -201,7 +213,37 @@ __global__ __launch_bounds__(512) void k44_mfma_dma_kernel(K44_GROUP_PARAMS) {
         }
     };
 
-    lds_ring<NBUF, D>(n_st, [&](uint32_t st, int buf) { issue(st_begin + st, buf); }, compute);
+    if constexpr (P == 0) {
+        lds_ring<NBUF, D>(n_st, [&](uint32_t st, int buf) { issue(st_begin + st, buf); }, compute);
+    } else if (wave >= 8) {
+        // Producer pw: rows pw + P*r of every stage, A-fragment blocks pw + P*j.
+        constexpr int RP = ROWS / P, WP = NB / P;
+        const int pw = wave - 8;
+        const __half *xlane = a.X + lane_x;
+        const char *wlane = wtile + (uint64_t)pw * 1024u + (uint32_t)lane * 16u;
+        auto pissue = [&](uint32_t st, int buf) {
+            const uint32_t kk = st * (uint32_t)ROWS;
+            const uint32_t k = kk / a.S, s0 = kk - k * a.S;
+            const __half *base = xlane + segr[k] + (uint64_t)(s0 + (uint32_t)pw) * a.step;
+#pragma unroll
+            for (int r = 0; r < RP; ++r)
+                __builtin_amdgcn_global_load_lds(
+                    (kglobal_void *)(base + (uint64_t)(P * r) * a.step),
+                    (__attribute__((address_space(3))) void *)&xl[buf][pw + P * r][0], 16, 0, CPOL);
+            const char *ws = wlane + (uint64_t)st * WBYTES;
+#pragma unroll
+            for (int j = 0; j < WP; ++j)
+                __builtin_amdgcn_global_load_lds(
+                    (kglobal_void *)(ws + (uint32_t)(P * j) * 1024u),
+                    (__attribute__((address_space(3))) void *)&wl[buf][(pw + P * j) * 256], 16, 0,
+                    CPOL);
+        };
+        lds_ring<NBUF, RP + WP>(n_st, [&](uint32_t st, int buf) { pissue(st_begin + st, buf); },
+                                [](int) {});
+        return;
+    } else {
+        lds_ring<NBUF, 1>(n_st, [](uint32_t, int) {}, compute);
+    }
 
     // Every wave is done with the ring (its LDS reads completed) before the LDS-transposed
     // epilogue reuses the X slots.

@@ -176,14 +176,18 @@ def test_narrow_mfma_decode_sizes(wavec, orc, tuning, tokens, nt):
     (32, 160, 3, 2, 1024, True),   # 15 stages, two token tiles
     (64, 512, 4, 5, 512, False),   # 64 stages
 ])
-@pytest.mark.parametrize("nbuf", ["2", "4"])
+@pytest.mark.parametrize("nbuf", ["2", "4", "4p"])
 def test_dma_ring_matches_register_staged(wavec, orc, tuning, nt, S, K, tiles, tokens, res,
                                           nbuf):
     """512-token workgroups take the LDS-ring kernel (direct loads, 2- or 4-stage ring, explicit
-    waits).  Without split-K it accumulates in the same k-step order as the register-staged
-    kernel, so the outputs are bit-identical; with split-K (partial boundaries differ) both are
-    within tolerance of the oracle.  Stage counts 1..3 exercise the drain-only path."""
+    waits; "4p": 4 stages with producer waves issuing every load).  Without split-K it
+    accumulates in the same k-step order as the register-staged kernel, so the outputs are
+    bit-identical; with split-K (partial boundaries differ) both are within tolerance of the
+    oracle.  Stage counts 1..3 exercise the drain-only path."""
+    prod = nbuf.endswith("p")
+    nbuf = nbuf.rstrip("p")
     tuning("dma_stages", int(nbuf))
+    tuning("dma_prod", 1 if prod else 0)
     rng = np.random.default_rng(S * 7 + K)
     C = 16384
     starts = (rng.integers(0, (C - S) // 8, size=(tiles, K)) * 8).astype(np.uint32)
@@ -201,9 +205,12 @@ def test_dma_ring_matches_register_staged(wavec, orc, tuning, nt, S, K, tiles, t
             rep = plan.exec_report()["waves"][0]
             assert rep["path"] == ("mfma_dma" if dma == "1" else "mfma_tile"), rep
             assert rep["ring_stages"] == (int(nbuf) if dma == "1" else 0), rep
+            want_prod = (2 if nt == 32 else 4) if (prod and dma == "1") else 0
+            assert rep["ring_producers"] == want_prod, rep
             err = orc.rel_err(y, ref)
             _log(f"[dma nt={nt} S={S} K={K} tiles={tiles} tokens={tokens} split={split} "
-                 f"dma={dma} ring={nbuf}] ksplit {rep['ksplit']} rel err {err:.3e}")
+                 f"dma={dma} ring={nbuf} producers={want_prod}] ksplit {rep['ksplit']} "
+                 f"rel err {err:.3e}")
             assert err <= TOL
             out[(split, dma)] = y
     assert np.array_equal(out[("0", "1")], out[("0", "0")])
