@@ -132,9 +132,21 @@ int wavec_add_pruned_wave(void *handle, const char *name, const char *in_tensor,
  * h = splitmix64(((pos << 20) | t) ^ splitmix64(seed)); padding tokens are 0. */
 int wavec_gpu_fill_input_uniform(void *handle, unsigned long long seed);
 
-/* Runs the whole plan `iters` times on the executor stream; average ms per run (HIP events). */
+/* Runs the whole plan `iters` times on the executor stream; average ms per run (HIP events).
+ * With tuning program=1, decode-sized plans (every run a narrow projection, decode RMSNorm +
+ * token shift, embedding or argmax) run each execution as one persistent launch whose stages
+ * wait on device-scope completion counters (kernels/k44_program.hpp); a stage wait past its
+ * limit (tuning prog_spin_ms) ends that launch early and this call (or the next
+ * wavec_gpu_sync) returns -1 naming the stage.  The report's "program" says whether a plan
+ * takes it and why not. */
 int wavec_gpu_execute(void *handle, int iters, float *out_ms_per_iter);
 int wavec_gpu_sync(void *handle);
+/* Per-item timestamps of the last persistent launch of a plan initialised with tuning
+ * prog_trace=1: 8 words per work item in stage order (item start, wait released, completion
+ * signalled, in ticks of the 100 MHz device real-time counter; the workgroup that ran it;
+ * projection items: inputs arrived, MFMAs done; stores performed).  No reference counterpart
+ * (a measurement aid). */
+int wavec_gpu_program_trace(void *handle, unsigned long long *dst, unsigned long long n_words);
 /* Runs plan commands [first_cmd, first_cmd + n_cmds) kernel by kernel and waits for them: lets a
  * caller inspect every intermediate tensor before the canvas allocator reuses its memory. */
 int wavec_gpu_execute_range(void *handle, int first_cmd, int n_cmds);

@@ -33,7 +33,7 @@ HIPCC_FLAGS = [
 SOURCES = ["k44_wave_executor.hip", "kernels/k44_valu.hip", "kernels/k44_aux.hip", "kernels/k44_mfma_dispatch.hip",
            "kernels/k44_mfma_nt16.hip", "kernels/k44_mfma_nt32.hip", "kernels/k44_mfma_nt64.hip",
            "kernels/k44_mfma_nt128.hip", "kernels/k44_mfma_narrow.hip", "kernels/k44_mfma_dma.hip", "kernels/k44_token64.hip",
-           "kernels/k44_spatial.hip"]
+           "kernels/k44_spatial.hip", "kernels/k44_program.hip"]
 BUILD_DIR = HERE / "_build"
 
 
@@ -41,13 +41,26 @@ def _clean(stderr: str) -> str:
     return "\n".join(l for l in stderr.splitlines() if "packed-fp32-ops" not in l)
 
 
-def build(verbose: bool = True) -> Path:
-    """Compiles every translation unit for gfx950 (in parallel) and links libk44wavec.so."""
+def _stale(obj: Path, src: Path) -> bool:
+    """The object is older than its source or than any header of the tree."""
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    heads = [*CSRC.rglob("*.hpp"), *(HERE.parent / "include").glob("*.h")]
+    return any(f.stat().st_mtime > t for f in [src, *heads])
+
+
+def build(verbose: bool = True, changed_only: bool = False) -> Path:
+    """Compiles every translation unit for gfx950 (in parallel) and links libk44wavec.so.
+    changed_only: recompile only objects older than their source or a header."""
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     BUILD_DIR.mkdir(exist_ok=True)
     objs, procs = [], []
     for src in SOURCES:
         obj = BUILD_DIR / (Path(src).stem + ".o")
+        if changed_only and not _stale(obj, CSRC / src):
+            objs.append(obj)
+            continue
         cmd = [hipcc, *[f for f in HIPCC_FLAGS if f != "-shared"], "-c", str(CSRC / src),
                "-o", str(obj)]
         if verbose:
@@ -79,4 +92,4 @@ def build(verbose: bool = True) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(changed_only="--changed" in sys.argv)

@@ -34,6 +34,13 @@ enum class Tune : int {
                    //                  1 = the last workgroup of each tile reduces in the launch
     DmaProd,       // "dma_prod":      0 = LDS-ring MFMA waves load and multiply in every wave,
                    //                  1 = producer waves issue the loads (4-stage ring)
+    Program,       // "program":       1 = decode-sized plans run each whole-plan execution as one
+                   //                  persistent launch (k44_program.hpp); automatic and 0:
+                   //                  kernel by kernel (measured faster on config-5 decode)
+    ProgSpinMs,    // "prog_spin_ms":  wait limit of the persistent launch's stage waits (ms, >= 0;
+                   //                  automatic: 1000), past which the launch is abandoned
+    ProgTrace,     // "prog_trace":    1 = the persistent launch records per-item timestamps
+                   //                  (wavec_gpu_program_trace)
     Count
 };
 

@@ -32,6 +32,7 @@
 #include "k44_wave_compiler.hpp"
 #include "k44wavec.h"
 #include "kernels/k44_launch.hpp"
+#include "kernels/k44_program.hpp"
 #include "kernels/k44_spatial.hpp"
 
 namespace k44_host {
@@ -42,7 +43,7 @@ std::atomic<int> g_tune[(int)Tune::Count];
 const char *const kTuneKeys[(int)Tune::Count] = {
     "path", "dma", "dma_stages", "nt", "splitk", "lane8", "ksplit", "stream_kernel", "narrow",
     "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring", "xcd_order",
-    "narrow_wgs", "narrow_reduce", "dma_prod"};
+    "narrow_wgs", "narrow_reduce", "dma_prod", "program", "prog_spin_ms", "prog_trace"};
 // Values each switch honours besides -1: a set of small values (bit v of `set`), or every
 // value >= `min` when `set` is 0.  Anything else is refused, so an A/B run cannot measure a
 // configuration other than the one it asked for.
@@ -72,6 +73,9 @@ const TuneValues kTuneValues[(int)Tune::Count] = {
     {0u, 1},           // narrow_wgs >= 1
     {V01, 0},          // narrow_reduce
     {V01, 0},          // dma_prod
+    {V01, 0},          // program
+    {0u, 0},           // prog_spin_ms >= 0
+    {V01, 0},          // prog_trace
 };
 struct TuneInit {
     TuneInit() {
@@ -333,6 +337,22 @@ struct K44GpuExecutorState {
     bool initialized = false;
     uint32_t xcd_order = 2;  // MFMA tile kernels: item order over the XCDs (MfmaGroup)
     std::string report_json;
+    // Decode-sized plans whose runs are all narrow projections, decode RMSNorms (with their
+    // token shifts), embeddings and argmaxes run whole-plan executions as one persistent launch
+    // (kernels/k44_program.hpp); `prog_why` says why a plan does not.
+    bool prog_active = false;
+    std::string prog_why = "not built";
+    uint32_t prog_grid = 0;
+    std::vector<k44dev::ProgStage> prog_stages_h;
+    DevBuf<k44dev::ProgStage> prog_stages;
+    DevBuf<k44dev::ProgWave> prog_waves;
+    DevBuf<k44dev::ProgAux> prog_aux;
+    DevBuf<uint32_t> prog_ctrs;  // [nstages] completion counters, exit counter, abort word
+    DevBuf<uint64_t> prog_zero;  // 64 argmax keys (zero between launches)
+    DevBuf<uint64_t> prog_slots; // folded RMSNorms: per producer item 16 tokens x 2 sum words
+    DevBuf<__half> prog_shadow;  // per stage the span of canvas it writes (read by later stages)
+    DevBuf<uint64_t> prog_trace; // tuning prog_trace=1: 4 words per item of the last launch
+    k44dev::ProgArgs prog_args{};
 
     ~K44GpuExecutorState() { free_all(); }
 
@@ -341,6 +361,400 @@ struct K44GpuExecutorState {
         if (graph) (void)hipGraphDestroy(graph);
         graph_exec = nullptr;
         graph = nullptr;
+    }
+
+    void drop_program(const std::string &why) {
+        prog_active = false;
+        prog_why = why;
+        prog_grid = 0;
+        prog_stages_h.clear();
+        prog_stages.reset();
+        prog_waves.reset();
+        prog_aux.reset();
+        prog_ctrs.reset();
+        prog_zero.reset();
+        prog_slots.reset();
+        prog_shadow.reset();
+        prog_trace.reset();
+        prog_args = k44dev::ProgArgs{};
+    }
+
+    // The persistent decode program of a whole-plan run (kernels/k44_program.hpp), when every
+    // run is one of: a launch of narrow 64 / 128-neuron MFMA waves (<= 16 tokens, gather forms
+    // 0 / 2 / 3 / 4, 4-element aligned outputs and residuals), a decode RMSNorm with or without
+    // its decode token shift (rf <= 5), an embedding, an argmax.  Runs become stages in plan
+    // order; folded RMSNorms keep their producers and consumers: the producing launch's items
+    // store their sums of squares in slots, and the consumers add the slots.
+    void build_program() {
+        drop_program("not built");
+        if (tune(Tune::Program) != 1) {
+            // config-5 decode measured 1.54 ms per step as one persistent launch against 0.85
+            // kernel by kernel: each stage waits for its slowest item, whose stores and
+            // completion signal queue behind the other workgroups' weight prefetches
+            prog_why = "off (kernel-by-kernel launches measured faster; tuning program=1 builds it)";
+            return;
+        }
+        const size_t nfold = norm_folds.size();
+        // the stage whose items produce each folded norm's input (all its waves, one stage)
+        std::vector<size_t> fold_stage(nfold, SIZE_MAX);
+        std::vector<size_t> aux_fold;  // per ProgAux: the fold of a NORM run with its scales
+        std::vector<size_t> wave_fold_in;  // per ProgWave: the fold a gather form 4 applies
+        std::vector<size_t> prog_wave_src;  // per ProgWave: its WaveExec
+        // Shadows: canvas ranges each stage writes; per ProgWave its gather operands' and
+        // residual's canvas ranges, per ProgAux the range it reads (resolved to the shadow of
+        // the stage that wrote them last, or the canvas).
+        std::vector<Ranges> st_wr;
+        std::vector<std::vector<Ranges>> pw_ops;
+        std::vector<Ranges> pw_res;
+        std::vector<Ranges> pa_rd;
+        std::vector<k44dev::ProgStage> st;
+        std::vector<k44dev::ProgWave> pw;
+        std::vector<k44dev::ProgAux> pa;
+        auto fail = [&](const std::string &why) {
+            prog_why = why;
+            return;
+        };
+        auto al = [](uint64_t off, uint64_t m) { return off % m == 0u; };
+        bool has_argmax = false;
+        for (const auto &r : runs) {
+            k44dev::ProgStage g{};
+            if (r.first == 0) {
+                const AuxExec &A = *aux[r.second];
+                k44dev::ProgAux x{};
+                Ranges rdr, wrr;
+                x.D = A.D;
+                x.stride = A.stride;
+                x.tokens = A.tokens;
+                x.eps = A.eps;
+                if (A.stride != 64u || A.tokens == 0u || A.tokens > 16u)
+                    return fail("command '" + A.name + "' is not decode-sized");
+                switch (A.type) {
+                case K44CmdType::RMSNORM_1D: {
+                    if (!al(A.src_off, 8u) || !al(A.y_off, 8u))
+                        return fail("RMSNorm '" + A.name + "' rows are not 16-byte aligned");
+                    x.y = canvas.p + A.y_off;
+                    x.x = canvas.p + A.src_off;
+                    x.table = A.table.p;
+                    rdr = {{A.src_off, A.src_off + (uint64_t)A.D * A.stride}};
+                    wrr = {{A.y_off, A.y_off + (uint64_t)A.D * A.stride}};
+                    if (A.shift_with != SIZE_MAX) {
+                        const AuxExec &T = *aux[A.shift_with];
+                        if (!T.decode || T.rf == 0u || T.rf > 5u || (T.rf > 1u && !T.has_state) ||
+                            !al(T.y_off, 8u) || (T.has_state && !al(T.state_off, 8u)))
+                            return fail("token shift '" + T.name + "' has no program form");
+                        x.y2 = canvas.p + T.y_off;
+                        wrr.push_back({T.y_off, T.y_off + (uint64_t)T.D * T.stride});
+                        x.mu = T.table.p;
+                        x.state = T.has_state ? canvas.p + T.state_off : nullptr;
+                        x.rf = T.rf;
+                    }
+                    g.type = k44dev::PROG_NORM;
+                    g.items = k44dev::prog_channel_items(A.D);
+                    break;
+                }
+                case K44CmdType::EMBED_1D:
+                    if (A.D % 8u != 0u || !al(A.y_off, 8u) || !ids.p)
+                        return fail("embedding '" + A.name + "' has no program form");
+                    x.y = canvas.p + A.y_off;
+                    x.table = A.table.p;
+                    x.ids_in = ids.p;
+                    wrr = {{A.y_off, A.y_off + (uint64_t)A.D * A.stride}};
+                    x.vocab = A.vocab;
+                    g.type = k44dev::PROG_EMBED;
+                    g.items = k44dev::prog_channel_items(A.D);
+                    break;
+                case K44CmdType::ARGMAX_1D:
+                    if (!al(A.src_off, 8u) || has_argmax || !ids.p)
+                        return fail("argmax '" + A.name + "' has no program form");
+                    has_argmax = true;
+                    x.x = canvas.p + A.src_off;
+                    x.ids_out = ids.p;
+                    rdr = {{A.src_off, A.src_off + (uint64_t)A.D * A.stride}};
+                    x.history = hist_steps ? history.p : nullptr;
+                    x.step_ctr = step_ctr.p;
+                    x.hist_steps = hist_steps;
+                    g.type = k44dev::PROG_ARGMAX;
+                    g.items = k44dev::prog_channel_items(A.D);
+                    break;
+                default:
+                    return fail("command '" + A.name + "' (" + cmd_type_str(A.type) +
+                                ") has no program form");
+                }
+                g.first = (uint32_t)pa.size();
+                g.count = 1u;
+                aux_fold.push_back(A.type == K44CmdType::RMSNORM_1D ? A.norm_fold : SIZE_MAX);
+                pa.push_back(x);
+                pa_rd.push_back(rdr);
+                st.push_back(g);
+                st_wr.push_back(merge_ranges(wrr));
+                if (A.type == K44CmdType::ARGMAX_1D) {
+                    k44dev::ProgStage f{};
+                    f.type = k44dev::PROG_ARGMAX_FINAL;
+                    f.items = 1u;
+                    f.first = g.first;
+                    f.count = 1u;
+                    st.push_back(f);
+                    st_wr.push_back({});
+                }
+                continue;
+            }
+            std::vector<size_t> members;
+            if (r.first == 1) members = {r.second};
+            else members = groups[r.second]->members;
+            g.type = k44dev::PROG_WAVES;
+            g.first = (uint32_t)pw.size();
+            g.count = (uint32_t)members.size();
+            uint32_t items = 0, kq_max = 0;
+            Ranges wrs;
+            for (size_t m : members) {
+                const WaveExec &w = *waves[m];
+                if (!w.mfma || !w.narrow || (w.cluster != 64u && w.cluster != 128u) || w.tile2d ||
+                    w.mis || w.S % 32u != 0u)
+                    return fail("wave '" + w.name + "' is not a narrow wave of 64 / 128-neuron "
+                                "tiles over whole 32-position k-steps");
+                if (w.out_stride % 4u != 0u || !al(w.y_off_run, 4u) ||
+                    (w.has_res && !al(w.res_off, 4u)))
+                    return fail("wave '" + w.name + "': output or residual rows are not 8-byte "
+                                "aligned");
+                if (w.xprod != 0u && w.xprod != 2u && w.xprod != 3u && w.xprod != 4u)
+                    return fail("wave '" + w.name + "': gather form " + std::to_string(w.xprod));
+                k44dev::ProgWave v{};
+                prog_wave_src.push_back(m);
+                v.Xo[0] = v.Xo[1] = v.Xo[2] = canvas.p;
+                v.seg = w.seg.p;
+                v.Wf = w.w.p;
+                v.bias = w.bias.p;
+                v.cmap = w.cmap.p;
+                v.Y = canvas.p + w.y_off_run;
+                v.R = w.has_res ? canvas.p + w.res_off : nullptr;
+                {
+                    const uint32_t nops = w.xprod == 3u ? 3u : w.xprod == 2u ? 2u : 1u;
+                    std::vector<Ranges> ops;
+                    for (uint32_t k = 0; k < nops; ++k) {
+                        const int64_t d = w.xprod ? w.xd[k] : 0;
+                        Ranges r;
+                        for (const auto &x : w.xrd)
+                            r.push_back({(uint64_t)((int64_t)x.first + d),
+                                         (uint64_t)((int64_t)x.second + d)});
+                        ops.push_back(r);
+                    }
+                    pw_ops.push_back(ops);
+                    pw_res.push_back(w.has_res ? w.resrd : Ranges{});
+                    for (const auto &x : w.wr_run) wrs.push_back(x);
+                }
+                v.step = w.step;
+                v.K = w.K;
+                v.S = w.S;
+                v.ksteps = w.ksteps;
+                v.nb = w.cluster / 16u;
+                v.tiles = w.rows;
+                v.out_stride = w.out_stride;
+                v.act = w.act;
+                if (w.norm_fold != SIZE_MAX) {
+                    const size_t f = w.norm_fold;
+                    if (fold_stage[f] != SIZE_MAX && fold_stage[f] != st.size())
+                        return fail("the producers of a folded RMSNorm span several launches");
+                    fold_stage[f] = st.size();
+                }
+                wave_fold_in.push_back(w.xnorm);
+                if (w.xnorm != SIZE_MAX) {
+                    const AuxExec &N = *aux[norm_folds[w.xnorm].norm];
+                    v.xgamma = N.table.p;
+                    v.xg_base = N.y_off;
+                    uint32_t sh = 0;
+                    while ((1u << sh) < N.stride) ++sh;
+                    v.xg_shift = sh;
+                    v.norm_D = N.D;
+                    v.norm_eps = N.eps;
+                }
+                kq_max = std::max(kq_max, (w.ksteps + 3u) / 4u);
+                pw.push_back(v);
+                g.prod = w.xprod;
+            }
+            g.kreg = ((kq_max + 7u) / 8u > 1u && (g.prod == 0u || g.prod == 2u)) ? 2u : 1u;
+            const uint32_t bpb = k44dev::prog_bpb(g.prod, g.kreg);
+            for (uint32_t k = 0; k < g.count; ++k) {
+                k44dev::ProgWave &v = pw[g.first + k];
+                v.item0 = items;
+                items += v.tiles * v.nb / bpb;
+            }
+            for (size_t m : members) {
+                if (waves[m]->xprod != g.prod)
+                    return fail("a launch of waves with different gather forms");
+                if (waves[m]->norm_fold != waves[members[0]]->norm_fold)
+                    return fail("a launch whose waves feed different folded RMSNorms");
+            }
+            g.items = items;
+            st.push_back(g);
+            st_wr.push_back(merge_ranges(wrs));
+        }
+        if (st.empty()) return fail("empty plan");
+        uint32_t grid = 0;
+        K44_HIP(k44dev::prog_grid(grid));
+        uint64_t cum = 0;
+        for (auto &g : st) {
+            g.rot = (uint32_t)(cum % grid);
+            g.base = (uint32_t)cum;
+            cum += g.items;
+        }
+        if (tune(Tune::ProgTrace) == 1) {
+            prog_trace.alloc(8u * cum);
+            K44_HIP(hipMemsetAsync(prog_trace.p, 0, prog_trace.n * sizeof(uint64_t), stream));
+        }
+        // Shadow layout: stage t's written span [lo, hi) at shadow element base[t].
+        std::vector<uint64_t> sh_lo(st.size(), 0), sh_base(st.size(), 0);
+        uint64_t sh_total = 0;
+        for (size_t t = 0; t < st.size(); ++t) {
+            if (st_wr[t].empty()) continue;
+            sh_lo[t] = st_wr[t].front().first;
+            sh_base[t] = sh_total;
+            sh_total += (st_wr[t].back().second - sh_lo[t] + 63u) / 64u * 64u;
+        }
+        prog_shadow.alloc(sh_total + 64u);
+        // the last stage before `before` that wrote any of `rs`: it must have written all of
+        // them (-1: none did, the canvas holds them); -2: no single producer
+        auto writer_of = [&](const Ranges &rs, size_t before) -> long {
+            long w_all = -3;
+            for (const auto &r : rs) {
+                long w = -1;
+                for (size_t t = before; t-- > 0;)
+                    if (ranges_overlap(st_wr[t], Ranges{r})) {
+                        w = (long)t;
+                        break;
+                    }
+                if (w >= 0) {
+                    bool inside = false;
+                    for (const auto &x : st_wr[(size_t)w])
+                        inside = inside || (x.first <= r.first && r.second <= x.second);
+                    if (!inside) return -2;
+                }
+                if (w_all == -3) w_all = w;
+                else if (w_all != w) return -2;
+            }
+            return w_all == -3 ? -1 : w_all;
+        };
+        // element pointer to canvas element offsets of stage w's outputs (shadow or canvas)
+        auto base_of = [&](long w) -> __half * {
+            if (w < 0) return canvas.p;
+            return reinterpret_cast<__half *>(
+                reinterpret_cast<uintptr_t>(prog_shadow.p) +
+                2u * (uintptr_t)(int64_t)((int64_t)sh_base[(size_t)w] - (int64_t)sh_lo[(size_t)w]));
+        };
+        for (size_t t = 0; t < st.size(); ++t) {
+            const k44dev::ProgStage &g = st[t];
+            if (g.type == k44dev::PROG_WAVES) {
+                for (uint32_t k = 0; k < g.count; ++k) {
+                    const size_t i = g.first + k;
+                    k44dev::ProgWave &v = pw[i];
+                    const WaveExec &w = *waves[prog_wave_src[i]];
+                    for (size_t o = 0; o < pw_ops[i].size(); ++o) {
+                        const long wr = writer_of(pw_ops[i][o], t);
+                        if (wr == -2) return fail("wave '" + w.name + "' gathers rows of several producers");
+                        v.Xo[o] = base_of(wr) + (w.xprod ? w.xd[o] : 0);
+                    }
+                    if (w.has_res) {
+                        const long wr = writer_of(pw_res[i], t);
+                        if (wr == -2) return fail("wave '" + w.name + "' adds rows of several producers");
+                        v.R = base_of(wr) + w.res_off;
+                    }
+                    v.Ys = base_of((long)t) + w.y_off_run;
+                }
+            } else if (g.type != k44dev::PROG_ARGMAX_FINAL) {
+                k44dev::ProgAux &x = pa[g.first];
+                if (!pa_rd[g.first].empty()) {
+                    const long wr = writer_of(pa_rd[g.first], t);
+                    if (wr == -2) return fail("a token op reads rows of several producers");
+                    x.x = base_of(wr) + pa_rd[g.first].front().first;
+                }
+                if (x.y) x.ys = base_of((long)t) + (uint64_t)(x.y - canvas.p);
+                if (x.y2) x.y2s = base_of((long)t) + (uint64_t)(x.y2 - canvas.p);
+            }
+        }
+        prog_zero.alloc(64u);
+        K44_HIP(hipMemsetAsync(prog_zero.p, 0, prog_zero.n * sizeof(uint64_t), stream));
+        for (auto &x : pa) x.keys = prog_zero.p;
+        // slots of the folded norms: 32 words per item of each producing stage
+        std::vector<size_t> slot_off(nfold, 0);
+        size_t nslot = 0;
+        for (size_t f = 0; f < nfold; ++f) {
+            if (fold_stage[f] == SIZE_MAX) continue;
+            const k44dev::ProgStage &g = st[fold_stage[f]];
+            slot_off[f] = nslot;
+            nslot += 32u * (size_t)g.items * k44dev::prog_bpb(g.prod, g.kreg);
+        }
+        if (nslot) prog_slots.alloc(nslot);
+        auto slots_of = [&](size_t f, uint32_t &n) -> uint64_t * {
+            if (f == SIZE_MAX || fold_stage[f] == SIZE_MAX) return nullptr;
+            const k44dev::ProgStage &g = st[fold_stage[f]];
+            n = g.items * k44dev::prog_bpb(g.prod, g.kreg);  // one slot per 16-neuron block
+            return prog_slots.p + slot_off[f];
+        };
+        for (size_t i = 0; i < pa.size(); ++i) {
+            uint32_t n = 0;
+            pa[i].slot_in = slots_of(aux_fold[i], n);
+            pa[i].slot_n = n;
+            if (aux_fold[i] != SIZE_MAX && !pa[i].slot_in)
+                return fail("a folded RMSNorm whose producers are not in the program");
+        }
+        {
+            size_t i = 0;
+            for (const auto &g : st) {
+                if (g.type != k44dev::PROG_WAVES) continue;
+                for (uint32_t k = 0; k < g.count; ++k, ++i) {
+                    k44dev::ProgWave &v = pw[g.first + k];
+                    const WaveExec &w = *waves[prog_wave_src[g.first + k]];
+                    uint32_t n = 0, dummy = 0;
+                    v.slot_out = w.norm_fold != SIZE_MAX ? slots_of(w.norm_fold, dummy) : nullptr;
+                    v.slot_in = slots_of(wave_fold_in[g.first + k], n);
+                    v.slot_n = n;
+                    if (wave_fold_in[g.first + k] != SIZE_MAX && !v.slot_in)
+                        return fail("a folded RMSNorm whose producers are not in the program");
+                }
+            }
+        }
+        prog_stages_h = st;
+        prog_stages.upload(st);
+        prog_waves.upload(pw);
+        prog_aux.upload(pa);
+        prog_ctrs.alloc(st.size() + 2u);
+        K44_HIP(hipMemsetAsync(prog_ctrs.p, 0, prog_ctrs.n * sizeof(uint32_t), stream));
+        int rate_khz = 0, dev = 0;
+        K44_HIP(hipGetDevice(&dev));
+        K44_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev));
+        const int spin_ms = tune(Tune::ProgSpinMs) < 0 ? 1000 : tune(Tune::ProgSpinMs);
+        prog_args = k44dev::ProgArgs{};
+        prog_args.stages = prog_stages.p;
+        prog_args.waves = prog_waves.p;
+        prog_args.aux = prog_aux.p;
+        prog_args.done = prog_ctrs.p;
+        prog_args.exit_ctr = prog_ctrs.p + st.size();
+        prog_args.abort = prog_ctrs.p + st.size() + 1u;
+        prog_args.zero_base = prog_zero.p;
+        prog_args.zero_words = (uint32_t)prog_zero.n;
+        prog_args.spin_ticks = (uint64_t)std::max(rate_khz, 1) * (uint64_t)spin_ms;
+        prog_args.nstages = (uint32_t)st.size();
+        prog_args.trace = prog_trace.p;
+        K44_HIP(hipStreamSynchronize(stream));
+        prog_grid = grid;
+        prog_active = true;
+        prog_why = "persistent launch: " + std::to_string(st.size()) + " stages, " +
+                   std::to_string(grid) + " workgroups";
+    }
+
+    // A persistent launch that gave up on a stage wait left a nonzero abort word: report it
+    // (and clear it) at the next host synchronisation.
+    void check_program() {
+        if (!prog_active) return;
+        uint32_t ab = 0;
+        K44_HIP(hipMemcpyAsync(&ab, prog_args.abort, sizeof(ab), hipMemcpyDeviceToHost, stream));
+        K44_HIP(hipStreamSynchronize(stream));
+        if (!ab) return;
+        K44_HIP(hipMemsetAsync(prog_args.abort, 0, sizeof(uint32_t), stream));
+        K44_HIP(hipStreamSynchronize(stream));
+        throw std::runtime_error("persistent decode launch abandoned: the wait for stage " +
+                                 std::to_string(ab - 1u) + " exceeded its time limit (" +
+                                 std::to_string(prog_args.spin_ticks) + " ticks); outputs of "
+                                 "that run are incomplete");
     }
 
     void free_all() {
@@ -368,6 +782,7 @@ struct K44GpuExecutorState {
         norm_ctrs.reset();
         norm_invs.reset();
         fold_elems = 0;
+        drop_program("not built");
         if (ev0) (void)hipEventDestroy(ev0);
         if (ev1) (void)hipEventDestroy(ev1);
         if (stream) (void)hipStreamDestroy(stream);
@@ -1305,6 +1720,7 @@ struct K44GpuExecutorState {
             K44_HIP(hipMemsetAsync(step_ctr.p, 0, 4u, stream));
         }
         K44_HIP(hipStreamSynchronize(stream));
+        build_program();
         build_report();
         initialized = true;
     }
@@ -2142,7 +2558,16 @@ struct K44GpuExecutorState {
             for (size_t k = 0; k < cmds.size(); ++k) o << (k ? ", " : "") << cmds[k];
             o << "]";
         }
-        o << "], \"launches_per_run\": " << launches_per_run();
+        o << "], \"launches_per_run\": " << (prog_active ? (size_t)1u : launches_per_run());
+        o << ", \"program\": {\"active\": " << (prog_active ? "true" : "false")
+          << ", \"why\": \"" << prog_why << "\", \"stages\": " << prog_stages_h.size()
+          << ", \"grid\": " << prog_grid << ", \"items\": "
+          << (prog_stages_h.empty() ? 0u : prog_stages_h.back().base + prog_stages_h.back().items)
+          << ", \"stage_items\": [";
+        for (size_t i = 0; i < prog_stages_h.size(); ++i)
+            o << (i ? ", " : "") << "[" << prog_stages_h[i].type << ", " << prog_stages_h[i].items
+              << "]";
+        o << "]}";
         o << ", \"canvas_elems\": " << plan_meta.canvas_elems << ", \"id_tokens\": " << id_tokens
           << "}";
         report_json = o.str();
@@ -2252,6 +2677,10 @@ struct K44GpuExecutorState {
     // One plan run on the executor stream: kernel by kernel, or as one replay of a HIP graph
     // captured from the same launches (no memset/memcpy nodes in it).
     void execute_plan() {
+        if (prog_active) {  // one launch: nothing to capture
+            K44_HIP(k44dev::launch_program(prog_args, prog_grid, stream));
+            return;
+        }
         if (!use_graph) {
             launch_ops();
             return;
@@ -2281,6 +2710,7 @@ struct K44GpuExecutorState {
         K44_HIP(hipMemsetAsync(history.p, 0, history.n * 4u, stream));
         K44_HIP(hipMemsetAsync(step_ctr.p, 0, 4u, stream));
         K44_HIP(hipStreamSynchronize(stream));
+        if (prog_active) build_program();  // the history pointer is in its argmax stage
     }
 
     const K44ResDesc &layout(uint32_t key) const { return plan_meta.res_map.at(key); }
@@ -2915,6 +3345,7 @@ int wavec_gpu_execute(void *h, int iters, float *out_ms_per_iter) {
         for (int i = 0; i < iters; ++i) ex->execute_plan();
         K44_HIP(hipEventRecord(ex->ev1, ex->stream));
         K44_HIP(hipEventSynchronize(ex->ev1));
+        ex->check_program();
         float ms = 0.0f;
         K44_HIP(hipEventElapsedTime(&ms, ex->ev0, ex->ev1));
         if (out_ms_per_iter) *out_ms_per_iter = ms / (float)iters;
@@ -2935,12 +3366,28 @@ int wavec_gpu_execute_range(void *h, int first_cmd, int n_cmds) {
     });
 }
 
+int wavec_gpu_program_trace(void *h, unsigned long long *dst, unsigned long long n_words) {
+    if (!h || !dst) return -1;
+    return guarded("wavec_gpu_program_trace", [&] {
+        k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
+        if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
+        if (!ex->prog_trace.p)
+            throw std::runtime_error("no program trace (a persistent launch built with prog_trace=1)");
+        if (n_words > ex->prog_trace.n) throw std::runtime_error("more words than the trace holds");
+        K44_HIP(hipMemcpyAsync(dst, ex->prog_trace.p, n_words * 8u, hipMemcpyDeviceToHost,
+                               ex->stream));
+        K44_HIP(hipStreamSynchronize(ex->stream));
+        return 0;
+    });
+}
+
 int wavec_gpu_sync(void *h) {
     if (!h) return -1;
     return guarded("wavec_gpu_sync", [&] {
         k44_host::K44GpuExecutorState *ex = k44_host::find_exec(h);
         if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
         K44_HIP(hipStreamSynchronize(ex->stream));
+        ex->check_program();
         return 0;
     });
 }

@@ -85,6 +85,7 @@ _ABI = (
     ("wavec_gpu_fill_input_uniform", _INT, (_VOID, _ULL)),
     ("wavec_gpu_execute", _INT, (_VOID, _INT, _P_FLT)),
     ("wavec_gpu_sync", _INT, (_VOID,)),
+    ("wavec_gpu_program_trace", _INT, (_VOID, C.POINTER(C.c_ulonglong), C.c_ulonglong)),
     ("wavec_gpu_execute_range", _INT, (_VOID, _INT, _INT)),
     ("wavec_gpu_read_canvas", _INT, (_VOID, _ULL, _ULL, _P_U16)),
     ("wavec_gpu_write_canvas", _INT, (_VOID, _ULL, _ULL, _P_U16)),
@@ -295,6 +296,18 @@ class WavePlan:
 
     def sync(self) -> None:
         _raise_on(self._lib.wavec_gpu_sync(self._handle), "wavec_gpu_sync")
+
+    def program_trace(self) -> np.ndarray:
+        """[items][8] records of the last persistent launch (tuning prog_trace=1): item start, wait
+        released, completion signalled (100 MHz device ticks), workgroup, inputs arrived and
+        MFMAs done (projection items), stores performed."""
+        rep = self.exec_report()["program"]
+        n = int(rep.get("items", 0))
+        out = np.zeros((n, 8), np.uint64)
+        _raise_on(self._lib.wavec_gpu_program_trace(
+            self._handle, out.ctypes.data_as(C.POINTER(C.c_ulonglong)), n * 8),
+            "wavec_gpu_program_trace")
+        return out
 
     def release_gpu(self) -> None:
         """Frees the plan's device state (canvas, schedules, graphs); init_gpu builds it again."""

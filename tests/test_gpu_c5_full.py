@@ -70,15 +70,21 @@ def test_c5_prefill_full_size_runwise_equals_whole_plan(c5):
 @pytest.fixture(scope="module")
 def c5_decode(c5, wavec):
     """Decode plans handed over from one whole-plan prefill run: 'cmd' and 'run' (defaults),
-    'graph' (defaults, HIP-graph replay) and 'unfused' (tuning switch fuse=0)."""
+    'graph' (kernel by kernel, HIP-graph replay), 'unfused' (tuning switch fuse=0), 'prog'
+    (tuning program=1: whole-plan runs as the persistent decode launch) and 'prog_ref' (kernel by
+    kernel, compared with 'prog' only)."""
     wts, pre, ids = c5
     pre.set_ids(ids)
     pre.execute(1)
     plans = {}
-    for name in ("cmd", "run", "graph", "unfused"):
+    for name in ("cmd", "run", "graph", "unfused", "prog", "prog_ref"):
         wavec.reset_tuning()
         if name == "unfused":
             wavec.set_tuning("fuse", 0)
+        if name in ("graph", "prog_ref"):
+            wavec.set_tuning("program", 0)
+        if name == "prog":
+            wavec.set_tuning("program", 1)
         p = synth.build_llm_graph(FULL, wts, decode=True, wavec_mod=wavec).compile()
         p.init_gpu()
         synth.llm_handoff(FULL, pre, p)
@@ -130,3 +136,38 @@ def test_c5_decode_graph_folded_matches_unfused_full_size(c5_decode):
         assert np.array_equal(ids_g, ids_u), step
         # logits of the batch's token columns (columns past it are unspecified)
         assert np.array_equal(lg.reshape(FULL.vocab, 64)[:, :R], lu.reshape(FULL.vocab, 64)[:, :R]), step
+
+
+def test_c5_decode_program_matches_runwise_full_size(c5_decode):
+    """The persistent decode launch at full size (16 layers) against the kernel-by-kernel plan
+    that the run-wise checker verifies node by node: both start from the same hand-over and
+    take the same ids every step; logits agree to a few fp16 ulps of the largest logit (the
+    projections sum their contractions in another order), ids wherever the top two logits are
+    clearly apart."""
+    _, plans = c5_decode
+    p, u = plans["prog"], plans["prog_ref"]
+    rep = p.exec_report()["program"]
+    _log(f"[c5 decode program] {rep}")
+    assert rep["active"], rep["why"]
+    R = FULL.requests
+    hp, hu = _head(p), _head(u)
+    ids = p.get_ids(R)
+    assert np.array_equal(ids, u.get_ids(R))
+    for step in range(DECODE_STEPS):
+        p.set_ids(ids)
+        u.set_ids(ids)
+        p.execute(1)
+        u.execute(1)
+        lp = p.read_canvas(int(hp["y_off"]), FULL.vocab * 64).view(np.float16)
+        lu = u.read_canvas(int(hu["y_off"]), FULL.vocab * 64).view(np.float16)
+        lp = lp.reshape(FULL.vocab, 64)[:, :R].astype(np.float64)
+        lu = lu.reshape(FULL.vocab, 64)[:, :R].astype(np.float64)
+        scale = np.abs(lu).max()
+        err = np.abs(lp - lu).max() / scale
+        srt = np.sort(lu, axis=0)
+        clear = (srt[-1] - srt[-2]) > 0.05 * scale
+        _log(f"[c5 decode program] step {step}: max|d| / max|logit| = {err:.3e}, "
+             f"{int(clear.sum())} of {R} ids with a clear margin")
+        assert err <= 1e-2, step
+        assert np.array_equal(p.get_ids(R)[clear], u.get_ids(R)[clear]), step
+        ids = u.get_ids(R)

@@ -403,6 +403,7 @@ def test_folded_multiplies_match_unfolded(wavec, tuning):
     pre = synth.build_llm_graph(spec, wts, decode=False, wavec_mod=wavec).compile()
     pre.init_gpu()
     plans = {}
+    tuning("program", 0)  # both plans launch kernel by kernel (the folds are what is compared)
     for mode in ("folded", "launched"):
         if mode == "launched":
             tuning("fuse", 0)
@@ -467,6 +468,7 @@ def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
     pre.set_ids(np.random.default_rng(31).integers(0, spec.vocab, R * spec.prompt))
     pre.execute(1)
     out = {}
+    tuning("program", 0)  # split narrow waves exist only in kernel-by-kernel launches
     for mode in ("kernel", "in_launch"):
         tuning("narrow_reduce", 0 if mode == "kernel" else 1)
         tuning("narrow_wgs", 512)  # many chunks per tile: every narrow wave splits
