@@ -30,7 +30,7 @@ HIPCC_FLAGS = [
 ]
 
 
-SOURCES = ["k44_wave_executor.hip", "kernels/k44_valu.hip", "kernels/k44_aux.hip", "kernels/k44_mfma_dispatch.hip",
+SOURCES = ["k44_wave_executor.hip", "k44_exec_build.hip", "k44_exec_schedule.hip", "k44_exec_launch.hip", "kernels/k44_valu.hip", "kernels/k44_aux.hip", "kernels/k44_mfma_dispatch.hip",
            "kernels/k44_mfma_nt16.hip", "kernels/k44_mfma_nt32.hip", "kernels/k44_mfma_nt64.hip",
            "kernels/k44_mfma_nt128.hip", "kernels/k44_mfma_narrow.hip", "kernels/k44_mfma_dma.hip", "kernels/k44_token64.hip",
            "kernels/k44_spatial.hip", "kernels/k44_program.hip"]

@@ -80,7 +80,7 @@ static inline bool tcff_wave_needs_ext(const K44ExecCmd &c) {
            c.res_off >= big;
 }
 
-static bool save_plan_to_tcff(const K44WavePlan &plan, const char *tcff_path,
+inline bool save_plan_to_tcff(const K44WavePlan &plan, const char *tcff_path,
                               const char *model_prefix = "K44Model", bool include_canvas = true,
                               bool include_geometry = true,
                               const uint16_t *live_canvas_f16 = nullptr) {
@@ -247,7 +247,7 @@ static inline uint64_t read_u64_le(const uint8_t *p) {
 // Loads weights, biases and (when the plan is single-frame and the canvas size matches the
 // header) gather indices of every K44_WAVE command from a TCFF file into an already compiled
 // plan, after verifying the header hash and every per-wave hash.
-static bool load_weights_from_tcff(K44WavePlan &plan, const char *tcff_path) {
+inline bool load_weights_from_tcff(K44WavePlan &plan, const char *tcff_path) {
     FILE *fp = std::fopen(tcff_path, "rb");
     if (!fp) {
         std::fprintf(stderr, "Failed to open TCFF file: %s\n", tcff_path);
