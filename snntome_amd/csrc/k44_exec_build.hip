@@ -32,8 +32,6 @@ void K44GpuExecutorState::free_all() {
     arrive.reset();
     norm_folds.clear();
     norm_slots.reset();
-    norm_ctrs.reset();
-    norm_invs.reset();
     fold_elems = 0;
     drop_program("not built");
     if (ev0) (void)hipEventDestroy(ev0);
@@ -883,11 +881,7 @@ void K44GpuExecutorState::init(const K44WavePlan &plan) {
         const NormFold &last = norm_folds.back();
         const size_t slots = last.slot0 + last.tiles;
         norm_slots.alloc(slots * 64u);
-        norm_ctrs.alloc(norm_folds.size());
-        norm_invs.alloc(norm_folds.size() * 64u);
         K44_HIP(hipMemsetAsync(norm_slots.p, 0, slots * 64u * sizeof(uint32_t), stream));
-        K44_HIP(hipMemsetAsync(norm_ctrs.p, 0, norm_folds.size() * sizeof(uint32_t), stream));
-        K44_HIP(hipMemsetAsync(norm_invs.p, 0, norm_folds.size() * 64u * sizeof(float), stream));
     }
     upload_mfma_descriptors();
     K44_HIP(hipMemsetAsync(canvas.p, 0,
@@ -942,18 +936,15 @@ k44dev::MfmaTileArgs K44GpuExecutorState::mfma_args(const WaveExec &w, float *pa
     if (fused && w.reduce_in_kernel) a.arrive = arrive.p + w.arrive_off;
     if (fused && w.norm_fold != SIZE_MAX) {
         const NormFold &f = norm_folds[w.norm_fold];
-        const AuxExec &N = *aux[f.norm];
         a.norm_part = norm_slots.p + (f.slot0 + w.norm_tile0) * 64u;
-        a.norm_all = norm_slots.p + f.slot0 * 64u;
-        a.norm_cnt = norm_ctrs.p + w.norm_fold;
-        a.norm_inv = norm_invs.p + w.norm_fold * 64u;
-        a.norm_tiles = f.tiles;
-        a.norm_D = N.D;
-        a.norm_eps = N.eps;
     }
     if (fused && w.xnorm != SIZE_MAX) {
-        const AuxExec &N = *aux[norm_folds[w.xnorm].norm];
-        a.xinv = norm_invs.p + w.xnorm * 64u;
+        const NormFold &f = norm_folds[w.xnorm];
+        const AuxExec &N = *aux[f.norm];
+        a.xslots = norm_slots.p + f.slot0 * 64u;
+        a.xslots_n = f.tiles;
+        a.norm_D = N.D;
+        a.norm_eps = N.eps;
         a.xgamma = N.table.p;
         a.xg_base = N.y_off;
         uint32_t sh = 0;

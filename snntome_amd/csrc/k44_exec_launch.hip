@@ -13,13 +13,14 @@ void K44GpuExecutorState::launch_aux(const AuxExec &a, bool whole) {
             const k44dev::RmsShift sh{cv + t.y_off, t.table.p,
                                       t.has_state ? cv + t.state_off : nullptr, t.rf, 0u,
                                       t.decode ? 0u : t.seq_len};
-            const float *inv = a.norm_fold != SIZE_MAX ? norm_invs.p + a.norm_fold * 64u : nullptr;
+            const uint64_t *sl = a.norm_fold != SIZE_MAX ? fold_slots(a.norm_fold) : nullptr;
+            const uint32_t n = a.norm_fold != SIZE_MAX ? norm_folds[a.norm_fold].tiles : 0u;
             K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
-                                           a.stride, a.tokens, a.eps, stream, &sh, inv));
+                                           a.stride, a.tokens, a.eps, stream, &sh, sl, n));
         } else if (whole && a.norm_fold != SIZE_MAX) {
             K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
                                            a.stride, a.tokens, a.eps, stream, nullptr,
-                                           norm_invs.p + a.norm_fold * 64u));
+                                           fold_slots(a.norm_fold), norm_folds[a.norm_fold].tiles));
         } else {
             K44_HIP(k44dev::launch_rmsnorm(cv + a.y_off, cv + a.src_off, a.table.p, a.D,
                                            a.stride, a.tokens, a.eps, stream));

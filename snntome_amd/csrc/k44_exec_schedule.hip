@@ -769,10 +769,11 @@ void K44GpuExecutorState::fuse_norm_shifts() {
 
 // RMSNorms of decode-sized plans whose input is written by narrow 64/128-neuron MFMA waves
 // (the sub-waves of the projections before them, each tile's outputs stored by one
-// workgroup) take their per-token scales from those waves: every producer tile adds the
-// exact sums of squares of the values it stored, and the last tile of the tensor forms the
-// scales (k44_mfma_narrow.hip, narrow_norm_publish).  The sums are exact, so the scales equal
-// the norm kernel's own bit for bit.  A norm read only by narrow 64/128-neuron waves gathering
+// workgroup) take their per-token scales from those waves: every producer tile stores the
+// exact sums of squares of the values it stored in a slot of its own (k44_mfma_narrow.hip,
+// narrow_norm_publish), and each reader of the norm, in a later launch, adds all slots at its
+// start, while its weight stream is in flight (rms_inv_from_slots).  The sums are exact, so
+// the scales equal the norm kernel's own bit for bit.  A norm read only by narrow 64/128-neuron waves gathering
 // it plainly is then not launched: those waves gather its input and normalise it in the
 // gather with the kernel's expression (xprod 4).  Otherwise (a norm that runs the decode
 // token shift) the norm kernel runs with the scales and skips its sum pass.  Conditions, from
@@ -898,8 +899,8 @@ void K44GpuExecutorState::fuse_norms() {
         N.norm_fold = norm_folds.size();
         if (consume) {
             N.fused = true;
-            N.fuse_note = "folded: scales formed by its producers, rows normalised in its "
-                          "readers' gathers";
+            N.fuse_note = "folded: sums of squares stored by its producers, rows normalised "
+                          "in its readers' gathers";
             for (size_t cw : cons) {
                 WaveExec &w = *waves[cw];
                 w.xprod = 4u;
@@ -913,7 +914,7 @@ void K44GpuExecutorState::fuse_norms() {
                 w.why += "; gathers its input through a folded RMSNorm";
             }
         } else {
-            N.fuse_note = "scales formed by its producers (no sum pass)";
+            N.fuse_note = "sums of squares stored by its producers (no sum pass)";
         }
         norm_folds.push_back(f);
     }

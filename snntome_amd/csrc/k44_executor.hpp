@@ -255,7 +255,7 @@ struct K44GpuExecutorState {
     // each launch leaves them at zero).
     DevBuf<uint32_t> arrive;
     // Folded RMSNorms (fuse_norms): per fold the producers' tile slots (16 tokens x 4 words
-    // each), a tile counter (zero between launches) and 64 per-token scales.
+    // each: the exact sums of squares of the values the tile stored).
     struct NormFold {
         size_t norm = 0;            // aux index of the RMSNORM_1D command
         uint32_t tiles = 0;         // producer tiles (slots)
@@ -263,8 +263,10 @@ struct K44GpuExecutorState {
         bool consumers = false;     // not launched: its readers gather normalised rows
     };
     std::vector<NormFold> norm_folds;
-    DevBuf<uint32_t> norm_slots, norm_ctrs;
-    DevBuf<float> norm_invs;
+    DevBuf<uint32_t> norm_slots;
+    const uint64_t *fold_slots(size_t fold) const {
+        return reinterpret_cast<const uint64_t *>(norm_slots.p + norm_folds[fold].slot0 * 64u);
+    }
     uint64_t fold_elems = 0;  // private region past the canvas for relocated multiply operands
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;

@@ -10,9 +10,9 @@ namespace k44dev {
 // (OCT lanes side by side read 16*OCT contiguous bytes of a channel row), the lanes of an octet
 // reduce (shuffles, then the 4 waves in LDS), and the workgroup writes channel slice blockIdx.y
 // of its tokens.  The sums of squares are exact (k44_sumsq.hpp): the same bits whatever the
-// grouping, so a norm whose sums were assembled elsewhere (inv_in: the per-token scales
-// rsqrt(sum / D + eps) of every token column, formed by the waves that produced x) gives this
-// kernel's output exactly; with inv_in the sum pass is skipped.  Small token counts (decode) use OCT = 1 and several slices
+// grouping, so a norm whose sums were assembled elsewhere (slots: the per-tile sums of the waves
+// that produced x, added here) gives this kernel's output exactly; with slots the sum pass over
+// all D channels is skipped.  Small token counts (decode) use OCT = 1 and several slices
 // per token chunk, each recomputing the (cache-resident) sum, so the grid still fills the chip.
 // RF > 0 (decode slices of one channel per thread): the decode token shift of the output
 // follows in the same thread — y2 = mu[c][0]*y + sum_i mu[c][i]*state[c][i-1][t], state shifted
@@ -24,7 +24,8 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
                                                           const __half *__restrict__ gamma,
                                                           uint32_t D, uint32_t stride, float eps,
                                                           uint32_t cslice, RmsShift sh,
-                                                          const float *__restrict__ inv_in) {
+                                                          const uint64_t *__restrict__ slots,
+                                                          uint32_t n_slots) {
     constexpr uint32_t CL = 256u / OCT;  // channel lanes
     __shared__ SumSq part[4][OCT * 8];
     __shared__ float inv_s[OCT * 8];
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
     SumSq ss[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) ss[k] = sumsq_zero();
-    uint32_t c = inv_in ? D : lane_c;  // (uniform) precomputed scales: no sum pass
+    uint32_t c = slots ? D : lane_c;  // (uniform) scales from the producers' sums: no sum pass
     auto add8 = [&](const uint4 &v) {
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -96,8 +97,12 @@ __global__ __launch_bounds__(256) void k44_rmsnorm_kernel(__half *__restrict__ y
         for (uint32_t i = 1; i < RF; ++i)
             asm volatile("" : "+v"(sv[i - 1].x), "+v"(sv[i - 1].y), "+v"(sv[i - 1].z), "+v"(sv[i - 1].w));
     }
-    if (inv_in) {
-        if (threadIdx.x < OCT * 8u) inv_s[threadIdx.x] = inv_in[blockIdx.x * OCT * 8u + threadIdx.x];
+    if (slots) {
+        // one octet per workgroup (decode): its 8 tokens' scales from the producers' slots
+        __shared__ uint4 spart[4][8];
+        __shared__ float sinv[8];
+        rms_inv_from_slots<8u>(slots, n_slots, blockIdx.x * 8u, D, eps, spart, sinv);
+        if (threadIdx.x < 8u) inv_s[threadIdx.x] = sinv[threadIdx.x];
     } else {
         // Per-token sums of the CL channel lanes: transposed through LDS ([token][lane], carries
         // propagated), then thread (token k, part p) adds 8 lanes, the parts of a token meet
@@ -833,11 +838,13 @@ static uint32_t grid_for(uint64_t n) {
 
 hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
                           uint32_t stride, uint32_t tokens, float eps, hipStream_t stream,
-                          const RmsShift *shift, const float *inv_in) {
+                          const RmsShift *shift, const uint64_t *slots, uint32_t n_slots) {
     if (stride % 64u != 0u || D == 0u || tokens == 0u || tokens > stride)
         return hipErrorInvalidValue;
-    // precomputed scales: the octet kernel only (its exact sums are what they replace)
-    if (inv_in && shift && shift->seq_len) return hipErrorInvalidValue;
+    // producers' slots: the decode octet kernel only (16 tokens per slot; its exact sums are
+    // what they replace)
+    if (slots && ((shift && shift->seq_len) || tokens > 16u || n_slots == 0u))
+        return hipErrorInvalidValue;
     // token columns >= tokens are not written; octets per workgroup: the widest that still
     // gives >= 256 workgroups (coalesced rows), else 1 octet and channel slices
     const uint32_t octets = (tokens + 7u) / 8u;
@@ -885,7 +892,7 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
     }
     // Prefill-sized token counts without a fused shift: the register-resident wide kernel
     // (32 tokens x all channels per workgroup) when the channels fit 16 per thread.
-    if (!shift && !inv_in && tokens % 32u == 0u && tokens / 32u >= 256u && D <= 16u * 256u) {
+    if (!shift && !slots && tokens % 32u == 0u && tokens / 32u >= 256u && D <= 16u * 256u) {
         const dim3 gw(tokens / 32u);
 #define K44_RMSW(C)                                                                            \
     hipLaunchKernelGGL((k44_rmsnorm_regs_kernel<C>), gw, dim3(1024), 0, stream, y, x, gamma, D, \
@@ -903,7 +910,7 @@ hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint3
     }
     const dim3 grid(chunks, (D + cslice - 1u) / cslice);
 #define K44_RMS(O, R) \
-    hipLaunchKernelGGL((k44_rmsnorm_kernel<O, R>), grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice, sh, inv_in)
+    hipLaunchKernelGGL((k44_rmsnorm_kernel<O, R>), grid, dim3(256), 0, stream, y, x, gamma, D, stride, eps, cslice, sh, slots, n_slots)
     if (shift) {
         switch (sh.rf) {
         case 1u: K44_RMS(1, 1u); break;

@@ -44,12 +44,14 @@ inline bool rmsnorm_shift_prefill_ok(uint32_t D, uint32_t stride, uint32_t token
            tokens / 32u >= 256u && rf >= 1u && rf <= 5u && seq_len > 0u && seq_len % 8u == 0u;
 }
 
-// inv_in (nullable, octet kernel only: token counts below the register-resident kernel's, no
-// fused prefill shift): per-token scales rsqrt(sum_c x^2 / D + eps) of every token column of
-// the stride, already formed (from exact sums of squares, so they equal the kernel's own).
+// slots (nullable, decode octet kernel only: at most 16 tokens, no fused prefill shift): the
+// n_slots per-tile exact sums of squares of x stored by the waves that produced it (16 tokens x
+// 2 words each, k44_sumsq.hpp); the kernel adds them instead of summing all D channels (the
+// same scales bit for bit).
 hipError_t launch_rmsnorm(__half *y, const __half *x, const __half *gamma, uint32_t D,
                           uint32_t stride, uint32_t tokens, float eps, hipStream_t stream,
-                          const RmsShift *shift = nullptr, const float *inv_in = nullptr);
+                          const RmsShift *shift = nullptr, const uint64_t *slots = nullptr,
+                          uint32_t n_slots = 0);
 hipError_t launch_mul(__half *y, const __half *a, const __half *b, uint64_t n,
                       hipStream_t stream);
 // y = fp16(a * fp16(b * c)) element-wise (a chain of two multiplies in one pass); y may be

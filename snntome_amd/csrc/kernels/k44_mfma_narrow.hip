@@ -101,10 +101,9 @@ __device__ __forceinline__ void narrow_fused_epilogue(const MfmaTileArgs &a, con
 
 // Producer side of a folded RMSNorm (a.norm_part set): the tile's stored fp16 outputs (lane
 // (g, t): out[bi][i] of channel slot j0[bi] + i, token t) summed squared per token, exactly:
-// over the lanes of one token (xor 16, 32), then the 4 waves in LDS; wave 0 publishes the
-// tile's slot (device-coherent stores, waited for), counts the tile in at norm_cnt, and the
-// last tile's wave 0 sums every slot of the tensor (lane = token x quarter of the slots) and
-// stores the per-token scales.  Every wave of the workgroup calls this (one barrier).
+// over the lanes of one token (xor 16, 32), then the 4 waves in LDS; wave 0 stores the tile's
+// slot (16 tokens x 2 words).  The readers of the norm, in later launches, add every slot
+// themselves (rms_inv_from_slots).  Every wave of the workgroup calls this (one barrier).
 template <int BPW>
 __device__ __forceinline__ void narrow_norm_publish(const MfmaTileArgs &a, const NarrowEpi<BPW> &e,
                                                     const uint16_t (&out)[BPW][4],
@@ -122,53 +121,15 @@ __device__ __forceinline__ void narrow_norm_publish(const MfmaTileArgs &a, const
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     if (lane < 16u) red[wave][lane] = s;
     __syncthreads();
-    if (wave != 0u) return;
-    if (lane < 16u) {
-        SumSq q = red[0][lane];
-        sumsq_merge(q, red[1][lane]);
-        sumsq_merge(q, red[2][lane]);
-        sumsq_merge(q, red[3][lane]);
-        q = sumsq_norm(q);  // one tile: the top limb and the flags fit 32 bits each
-        gu64 *slot = (gu64 *)(a.norm_part + ((uint64_t)tile * 16u + lane) * 4u);
-        __hip_atomic_store(slot, (u64)q.l0 | (q.l1 << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(slot + 1, (u64)(uint32_t)q.l2 | ((u64)q.sp << 32), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slot is stored before it is counted
-    uint32_t old = 0u;
-    if (lane == 0u)
-        old = __hip_atomic_fetch_add((__attribute__((address_space(1))) uint32_t *)a.norm_cnt, 1u,
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old != a.norm_tiles - 1u) return;
-    // last tile of the tensor: every slot, token lane & 15, slots lane >> 4, +4, ...
-    const gu64 *all = (const gu64 *)a.norm_all;
-    SumSq acc = sumsq_zero();
-    constexpr uint32_t NB = 8u;  // slots loaded together
-    for (uint32_t j0 = lane >> 4; j0 < a.norm_tiles; j0 += 4u * NB) {
-        u64 lo[NB], hi[NB];
-#pragma unroll
-        for (uint32_t u = 0; u < NB; ++u) {
-            const uint32_t j = min(j0 + 4u * u, a.norm_tiles - 1u);
-            const gu64 *p = all + ((uint64_t)j * 16u + (lane & 15u)) * 2u;
-            lo[u] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            hi[u] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < NB; ++u) {
-            if (j0 + 4u * u < a.norm_tiles) {
-                acc.l0 += lo[u] & 0xffffffffull;
-                acc.l1 += lo[u] >> 32;
-                acc.l2 += hi[u] & 0xffffffffull;
-                acc.sp |= (uint32_t)(hi[u] >> 32);
-            }
-        }
-    }
-    acc = sumsq_wave_reduce(acc, 16);
-    if (lane < 16u) a.norm_inv[lane] = rms_inv(acc, a.norm_D, a.norm_eps);
-    if (lane == 0u)
-        __hip_atomic_store((__attribute__((address_space(1))) uint32_t *)a.norm_cnt, 0u,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wave != 0u || lane >= 16u) return;
+    SumSq q = red[0][lane];
+    sumsq_merge(q, red[1][lane]);
+    sumsq_merge(q, red[2][lane]);
+    sumsq_merge(q, red[3][lane]);
+    q = sumsq_norm(q);  // one tile: the top limb and the flags fit 32 bits each
+    gu64 *slot = (gu64 *)(a.norm_part + ((uint64_t)tile * 16u + lane) * 4u);
+    slot[0] = (u64)q.l0 | (q.l1 << 32);
+    slot[1] = (u64)(uint32_t)q.l2 | ((u64)q.sp << 32);
 }
 
 // Split-K reduced inside the launch (a.arrive set; 64 / 128-neuron tiles).  Every workgroup of
@@ -458,17 +419,9 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
     // multiply with the rounding of the unfused multiply commands: fp16(A*B), fp16(A*fp16(B*C)).
     constexpr int XQ = NARROW_MAX_ROWS * 2 / 256;
     constexpr uint32_t xprod = (uint32_t)PROD;  // every wave of the launch gathers this form
-    // Folded RMSNorm (xprod 4): the lane's 8 tokens' scales, loaded once.
+    // Folded RMSNorm (xprod 4): the lane's 8 tokens' scales, formed from the producers' slots
+    // after the first sub-chunk's loads are issued.
     float xinv[xprod == 4u ? 8 : 1];
-    if constexpr (xprod == 4u) {
-        typedef const __attribute__((address_space(1))) f4_t gf4;
-        const f4_t i0 = ((gf4 *)a.xinv)[(lane & 1) * 2], i1 = ((gf4 *)a.xinv)[(lane & 1) * 2 + 1];
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-            xinv[e2] = i0[e2];
-            xinv[4 + e2] = i1[e2];
-        }
-    }
     auto gather = [&](uint32_t s, u4_t (&xv)[XQ], u4_t (&xb)[XQ], u4_t (&xc)[XQ]) {
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
@@ -556,6 +509,14 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
     for (int u = 0; u < SUBK; ++u) load_a(min(ks_begin + (uint32_t)u, ks_end - 1u), af[u]);
     u4_t xv[XQ], xb[XQ], xc[XQ];
     gather(0u, xv, xb, xc);
+    if constexpr (xprod == 4u) {
+        __shared__ uint4 ipart[4][16];
+        __shared__ float sinv[16];
+        rms_inv_from_slots<16u>(reinterpret_cast<const uint64_t *>(a.xslots), a.xslots_n, 0u,
+                                a.norm_D, a.norm_eps, ipart, sinv);
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) xinv[e2] = sinv[(lane & 1) * 8 + e2];
+    }
     store(0u, 0, xv, xb, xc);
     __syncthreads();
 

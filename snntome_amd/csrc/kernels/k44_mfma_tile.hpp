@@ -85,21 +85,18 @@ struct MfmaTileArgs {
     // nullptr: partials [z][cout][16] for k44_splitk_epilogue_kernel.
     uint32_t *arrive;
     // RMSNorm folded around narrow 64 / 128-neuron waves (whole-plan runs), producer side
-    // (norm_part set): once a tile's outputs are stored, the tile adds the exact per-token sums
-    // of squares of the fp16 values it stored (k44_sumsq.hpp) to its slot norm_part[tile][16]
-    // (4 words: limbs 0..2, inf / NaN flags); the tile that arrives last at norm_cnt, out of the
-    // norm_tiles tiles that write the tensor, sums every slot of norm_all and stores the 16
-    // per-token scales rsqrt(sum / norm_D + norm_eps) to norm_inv (and zeroes norm_cnt).
+    // (norm_part set): once a tile's outputs are stored, the tile stores the exact per-token sums
+    // of squares of the fp16 values it stored (k44_sumsq.hpp) in its slot norm_part[tile]
+    // (16 tokens x 2 words: limbs 0 | 1, limb 2 | inf / NaN flags).
     uint32_t *norm_part;
-    const uint32_t *norm_all;
-    uint32_t *norm_cnt;
-    float *norm_inv;
-    uint32_t norm_tiles, norm_D;
+    uint32_t norm_D;  // consumer side: channels and epsilon of the norm
     float norm_eps;
     // Consumer side (xprod 4): the gather reads the norm's input rows (segment offset + xd[0])
-    // and replaces every element by fp16(x * xinv[t] * gamma[c]), the RMSNorm kernel's
-    // expression; gamma from xgamma (nullptr: 1), c = (row offset - xg_base) >> xg_shift.
-    const float *xinv;
+    // and replaces every element by fp16(x * inv[t] * gamma[c]), the RMSNorm kernel's
+    // expression; inv[t] = rsqrt(sum / norm_D + norm_eps) from the xslots_n producer slots at
+    // xslots; gamma from xgamma (nullptr: 1), c = (row offset - xg_base) >> xg_shift.
+    const uint32_t *xslots;
+    uint32_t xslots_n;
     const __half *xgamma;
     uint64_t xg_base;
     uint32_t xg_shift;

@@ -110,4 +110,56 @@ __device__ __forceinline__ SumSq sumsq_wave_reduce(SumSq s, int span) {
     return s;
 }
 
+// Per-token RMSNorm scales of TK tokens (t0 .. t0 + TK - 1) from the exact sums of squares
+// that the n producer tiles of the norm's input stored, one slot of 16 tokens x 2 words per
+// tile (limbs 0 | 1 << 32, limb 2 | flags << 32).  Called by the whole 256-thread workgroup:
+// thread (token tid % TK, part tid / TK) adds slots part, part + 256 / TK, ... (exact: any
+// order gives the same integer), the parts of a token meet by shuffles within the wave and
+// across the 4 waves in LDS; inv[k] holds token t0 + k's scale after the call's last barrier.
+template <uint32_t TK>
+__device__ __forceinline__ void rms_inv_from_slots(const uint64_t *slots, uint32_t n,
+                                                   uint32_t t0, uint32_t D, float eps,
+                                                   uint4 (&part)[4][TK], float (&inv)[TK]) {
+    static_assert(TK == 8u || TK == 16u, "tokens per pass");
+    constexpr uint32_t PARTS = 256u / TK;
+    typedef const __attribute__((address_space(1))) uint64_t gu64c;
+    const uint32_t tk = threadIdx.x % TK, pt = threadIdx.x / TK;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    SumSq q = sumsq_zero();
+    for (uint32_t i0 = pt; i0 < n; i0 += 4u * PARTS) {
+        uint64_t lo[4], hi[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) {
+            const uint32_t i = min(i0 + PARTS * u, n - 1u);
+            const gu64c *w = (const gu64c *)slots + ((uint64_t)i * 16u + t0 + tk) * 2u;
+            lo[u] = w[0];
+            hi[u] = w[1];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u)
+            if (i0 + PARTS * u < n) {
+                q.l0 += lo[u] & 0xffffffffull;
+                q.l1 += lo[u] >> 32;
+                q.l2 += hi[u] & 0xffffffffull;
+                q.sp |= (uint32_t)(hi[u] >> 32);
+            }
+    }
+    q = sumsq_wave_reduce(q, (int)TK);  // the lanes of one token in this wave
+    if (lane < TK) part[wave][lane] = uint4{(uint32_t)q.l0, (uint32_t)q.l1, (uint32_t)q.l2, q.sp};
+    __syncthreads();
+    if (threadIdx.x < TK) {
+        SumSq t = sumsq_zero();
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 x = part[v][threadIdx.x];
+            t.l0 += x.x;
+            t.l1 += x.y;
+            t.l2 += x.z;
+            t.sp |= x.w;
+        }
+        inv[threadIdx.x] = rms_inv(t, D, eps);
+    }
+    __syncthreads();
+}
+
 }  // namespace k44dev

@@ -417,7 +417,7 @@ def test_folded_multiplies_match_unfolded(wavec, tuning):
     shifts = [a for a in rep["aux"] if a["fused"] and a["type"] == "TOKEN_SHIFT_1D"]
     norms = [a for a in rep["aux"] if a["type"] == "RMSNORM_1D"]
     norm_folded = [a for a in norms if a["fused"]]
-    norm_scaled = [a for a in norms if not a["fused"] and "scales formed" in a["fuse_note"]]
+    norm_scaled = [a for a in norms if not a["fused"] and "sums of squares stored" in a["fuse_note"]]
     prods = sorted({w["xprod"] for w in rep["waves"]})
     _log(f"[fold] {len(fused)} multiplies folded, {len(shifts)} token shifts run by their "
          f"RMSNorm, {len(norm_folded)} RMSNorms folded into their readers, "
