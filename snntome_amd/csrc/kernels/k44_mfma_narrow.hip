@@ -42,14 +42,16 @@ struct NarrowEpi {
     uint64_t o[BPW][4];  // output element, ~0 for an empty cout_map slot
 };
 
+// The two batches separately: cout_map entries and biases (narrow_epi_maps), then the
+// residuals at the output rows they name (narrow_epi_res).  The long kernel issues the first
+// with its first X gather and the second once that gather has arrived, so neither round trip
+// follows the contraction.
 template <int BPW>
-__device__ __forceinline__ void narrow_epi_load(const MfmaTileArgs &a, const uint32_t (&j0)[BPW],
-                                                uint32_t t, NarrowEpi<BPW> &e) {
+__device__ __forceinline__ void narrow_epi_maps(const MfmaTileArgs &a, const uint32_t (&j0)[BPW],
+                                                uint32_t (&cb)[BPW][4], NarrowEpi<BPW> &e) {
     typedef const __attribute__((address_space(1))) uint16_t gu16;
     gu16 *cm = (gu16 *)(a.cmap ? (const void *)a.cmap : (const void *)a.Wf);
     gu16 *bs = (gu16 *)(a.bias ? (const void *)a.bias : (const void *)a.Wf);
-    gu16 *rs = (gu16 *)(a.R ? (const void *)a.R : (const void *)a.Y);
-    uint32_t cb[BPW][4];
 #pragma unroll
     for (int bi = 0; bi < BPW; ++bi)
 #pragma unroll
@@ -57,6 +59,14 @@ __device__ __forceinline__ void narrow_epi_load(const MfmaTileArgs &a, const uin
             cb[bi][i] = cm[j0[bi] + (uint32_t)i];
             e.bb[bi][i] = bs[j0[bi] + (uint32_t)i];
         }
+}
+
+template <int BPW>
+__device__ __forceinline__ void narrow_epi_res(const MfmaTileArgs &a, const uint32_t (&j0)[BPW],
+                                               uint32_t t, const uint32_t (&cb)[BPW][4],
+                                               NarrowEpi<BPW> &e) {
+    typedef const __attribute__((address_space(1))) uint16_t gu16;
+    gu16 *rs = (gu16 *)(a.R ? (const void *)a.R : (const void *)a.Y);
 #pragma unroll
     for (int bi = 0; bi < BPW; ++bi)
 #pragma unroll
@@ -65,6 +75,14 @@ __device__ __forceinline__ void narrow_epi_load(const MfmaTileArgs &a, const uin
             e.o[bi][i] = (a.cmap && oj == K44_CMAP_EMPTY) ? ~0ull : oj * a.out_stride + t;
             e.rb[bi][i] = rs[e.o[bi][i] == ~0ull ? (uint64_t)t : e.o[bi][i]];
         }
+}
+
+template <int BPW>
+__device__ __forceinline__ void narrow_epi_load(const MfmaTileArgs &a, const uint32_t (&j0)[BPW],
+                                                uint32_t t, NarrowEpi<BPW> &e) {
+    uint32_t cb[BPW][4];
+    narrow_epi_maps<BPW>(a, j0, cb, e);
+    narrow_epi_res<BPW>(a, j0, t, cb, e);
 }
 
 template <int BPW>
@@ -377,10 +395,18 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(K44_GROUP_PARAMS) 
 // rows multiplied), fixed at compile time.
 // BYY: grid (largest wave's workgroups) x (waves): the wave is blockIdx.y, known without a
 // lookup in the group's prefix sums; workgroups past a wave's own count exit at once.
+// The weights are read through a buffer resource bounded by the workgroup's chunk: every
+// MFMA's operand slot is refilled with the fragment one sub-chunk ahead, and refills past the
+// chunk are out-of-range loads, which return zeros without a memory access (the load count
+// stays fixed, so every wait is partial, and no request past the chunk delays the split-K
+// reduction's wait or the workgroup's end).  Measured on config-5 decode: 0.836 -> 0.8225
+// ms/step against refills clamped to the chunk's last k-step (re-reads of it); two sub-chunks
+// of fragments in flight per wave instead of one: 0.869 ms/step (each wave's first gather then
+// waits behind twice the weight bytes).
 template <int NT, int PROD, bool BYY>
 __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PARAMS) {
     K44_GROUP_BIND;
-    constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16;
+    constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16, AF = SUBK;
     static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][NARROW_MAX_ROWS][NARROW_PITCH];
 
@@ -402,14 +428,21 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const kconst_u64 *segr = (const kconst_u64 *)(a.seg) + (uint64_t)tile * a.K;
-    typedef const __attribute__((address_space(1))) h8_t gh8_t;
     typedef const __attribute__((address_space(1))) u4_t gu4_t;
-    gh8_t *wf = (gh8_t *)(reinterpret_cast<const h8_t *>(a.Wf) +
-                          (uint64_t)tile * a.ksteps * NB * 64 + lane);
-    auto load_a = [&](uint32_t k2, h8_t (&f)[BPW]) {
+    // the chunk's A fragments [k-step - ks_begin][16-block][lane][8]: 1 KiB per k-step and block
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(reinterpret_cast<const h8_t *>(a.Wf) +
+                 ((uint64_t)tile * a.ksteps + ks_begin) * NB * 64u),
+        (short)0, (int)((ks_end - ks_begin) * (uint32_t)NB * 1024u), 0x00020000);
+    // k-step kk of the chunk (relative to ks_begin; past the chunk: zeros, no access), read
+    // nontemporally (weights are read once per step)
+    auto load_a = [&](uint32_t kk, h8_t (&f)[BPW]) {
 #pragma unroll
         for (int i = 0; i < BPW; ++i)
-            f[i] = __builtin_nontemporal_load(&wf[((uint64_t)k2 * NB + wave + 4 * i) * 64]);
+            f[i] = __builtin_bit_cast(
+                h8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                          wr, ((kk * (uint32_t)NB + (uint32_t)(wave + 4 * i)) * 64u + (uint32_t)lane) * 16u,
+                          0, 2));
     };
 
     // X rows of sub-chunk s: wave pass q covers 32 rows starting at a multiple of 32 (one
@@ -504,11 +537,25 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
         }
     };
 
-    h8_t af[SUBK][BPW];
+    h8_t af[AF][BPW];
 #pragma unroll
-    for (int u = 0; u < SUBK; ++u) load_a(min(ks_begin + (uint32_t)u, ks_end - 1u), af[u]);
+    for (int u = 0; u < AF; ++u) load_a((uint32_t)u, af[u]);
     u4_t xv[XQ], xb[XQ], xc[XQ];
     gather(0u, xv, xb, xc);
+    // Lane holds C[4g + i][lane & 15]: neuron 16*blk + 4g + i, token lane & 15.  A workgroup
+    // that may run the epilogue (whole contraction here, or split-K reduced by the tile's last
+    // workgroup) issues its epilogue loads now: cout_map and biases with the first gather, the
+    // residuals they address after it (all read-only or written only by this lane's store).
+    const int g = lane >> 4;
+    const uint32_t t = (uint32_t)(lane & 15);
+    const bool epi = !a.part || a.arrive;
+    uint32_t j0[BPW];
+#pragma unroll
+    for (int bi = 0; bi < BPW; ++bi)
+        j0[bi] = tile * (uint32_t)NT + 16u * (uint32_t)(wave + 4 * bi) + 4u * (uint32_t)g;
+    NarrowEpi<BPW> e;
+    uint32_t cb[BPW][4];
+    if (epi) narrow_epi_maps<BPW>(a, j0, cb, e);
     if constexpr (xprod == 4u) {
         __shared__ uint4 ipart[4][16];
         __shared__ float sinv[16];
@@ -518,9 +565,9 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
         for (int e2 = 0; e2 < 8; ++e2) xinv[e2] = sinv[(lane & 1) * 8 + e2];
     }
     store(0u, 0, xv, xb, xc);
+    if (epi) narrow_epi_res<BPW>(a, j0, t, cb, e);
     __syncthreads();
 
-    const int g = lane >> 4;
     const int tr_row = 8 * g + ((lane & 15) >> 2);
     const int tr_col = 4 * (lane & 3);
     f4_t acc[BPW];
@@ -544,7 +591,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
                 for (int i = 0; i < BPW; ++i)
                     acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u][i], b, acc[i], 0, 0, 0);
             }
-            load_a(min(k2 + (uint32_t)SUBK, ks_end - 1u), af[u]);  // next sub-chunk's fragment
+            load_a(k2 - ks_begin + (uint32_t)AF, af[u]);  // next sub-chunk's fragment (or none)
         }
         if (more) {
             store(s + 1u, buf ^ 1, xv, xb, xc);
@@ -552,19 +599,9 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
         }
     }
 
-    // Lane holds C[4g + i][lane & 15]: neuron 16*blk + 4g + i, token lane & 15.
-    const uint32_t t = (uint32_t)(lane & 15);
-    if (!a.part || a.arrive) {
-        // whole contraction here, or split-K reduced by the tile's last workgroup: the fused
-        // epilogue (its loads complete under the reduction's round trips), then the tile's
-        // share of a folded RMSNorm
-        uint32_t j0[BPW];
-#pragma unroll
-        for (int bi = 0; bi < BPW; ++bi)
-            j0[bi] = tile * (uint32_t)NT + 16u * (uint32_t)(wave + 4 * bi) + 4u * (uint32_t)g;
-        NarrowEpi<BPW> e;
+    if (epi) {
+        // the fused epilogue (loads issued above), then the tile's share of a folded RMSNorm
         uint16_t out[BPW][4];
-        narrow_epi_load<BPW>(a, j0, t, e);
         if (a.part && !narrow_reduce_last<BPW>(a, acc, j0, t, tile, zgroup)) return;
         narrow_epi_store<BPW>(a, acc, e, out);
         if (a.norm_part) narrow_norm_publish<BPW>(a, e, out, tile);
