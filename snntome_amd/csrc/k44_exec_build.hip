@@ -32,6 +32,9 @@ void K44GpuExecutorState::free_all() {
     arrive.reset();
     norm_folds.clear();
     norm_slots.reset();
+    shift_next.reset();
+    shift_mix.reset();
+    shift_next_elems = 0;
     fold_elems = 0;
     drop_program("not built");
     if (ev0) (void)hipEventDestroy(ev0);
@@ -487,6 +490,7 @@ void K44GpuExecutorState::build_wave(const K44ExecCmd &c, WaveExec &wx) {
         std::memcpy(wh.data(), wk.data(), wk.size() * 2u);
         wx.w.upload(wh);
     }
+    if (wx.narrow) wx.seg_h = starts;
     wx.seg.upload(starts);
     std::vector<__half> bh(c.Cout);
     for (size_t j = 0; j < c.Cout; ++j) {
@@ -882,6 +886,29 @@ void K44GpuExecutorState::init(const K44WavePlan &plan) {
         const size_t slots = last.slot0 + last.tiles;
         norm_slots.alloc(slots * 64u);
         K44_HIP(hipMemsetAsync(norm_slots.p, 0, slots * 64u * sizeof(uint32_t), stream));
+        if (shift_next_elems) {
+            shift_next.alloc(shift_next_elems);
+            K44_HIP(hipMemsetAsync(shift_next.p, 0, shift_next_elems * sizeof(__half), stream));
+            // per folded token shift: [D][8] = mu[c][0..rf-1], 0 .., the norm's gamma at 4
+            std::vector<__half> mix;
+            for (NormFold &f : norm_folds) {
+                if (f.shift == SIZE_MAX) continue;
+                const AuxExec &T = *aux[f.shift], &N = *aux[f.norm];
+                std::vector<uint16_t> mu((size_t)T.D * T.rf), gm(N.D, 0x3c00u);
+                K44_HIP(hipMemcpy(mu.data(), T.table.p, mu.size() * 2u, hipMemcpyDeviceToHost));
+                if (N.table.p)
+                    K44_HIP(hipMemcpy(gm.data(), N.table.p, gm.size() * 2u, hipMemcpyDeviceToHost));
+                f.mix0 = mix.size();
+                std::vector<uint16_t> rows((size_t)T.D * 8u, 0u);
+                for (size_t c = 0; c < T.D; ++c) {
+                    for (uint32_t i = 0; i < T.rf; ++i) rows[c * 8u + i] = mu[c * T.rf + i];
+                    rows[c * 8u + 4u] = gm[c];
+                }
+                mix.resize(mix.size() + rows.size());
+                std::memcpy(mix.data() + f.mix0, rows.data(), rows.size() * 2u);
+            }
+            shift_mix.upload(mix);
+        }
     }
     upload_mfma_descriptors();
     K44_HIP(hipMemsetAsync(canvas.p, 0,
@@ -950,6 +977,32 @@ k44dev::MfmaTileArgs K44GpuExecutorState::mfma_args(const WaveExec &w, float *pa
         uint32_t sh = 0;
         while ((1u << sh) < N.stride) ++sh;
         a.xg_shift = sh;
+        if (w.xprod == 5u) {  // rows of the shift's output; its mixing weights and state
+            const AuxExec &T = *aux[f.shift];
+            a.xg_base = T.y_off;
+            a.mixg = shift_mix.p + f.mix0;
+            a.state = shift_next.p + f.cur0;
+            a.state_next = shift_next.p + f.next0;
+            a.own = w.own.p;
+            a.rf = T.rf;
+            a.sh_tokens = T.tokens;
+        }
+    }
+    if (fused && w.cp_fold != SIZE_MAX) {  // a folded token shift's state copy (16 tokens)
+        const NormFold &f = norm_folds[w.cp_fold];
+        const AuxExec &T = *aux[f.shift];
+        a.cp_rows = T.D * (T.rf - 1u);
+        if (w.cp_refresh) {  // the plan's state into the readers' compact copy
+            a.cp_src = canvas.p + T.state_off;
+            a.cp_sstride = 64u;
+            a.cp_dst = shift_next.p + f.cur0;
+            a.cp_dstride = 16u;
+        } else {  // the shifted state back into the plan's
+            a.cp_src = shift_next.p + f.next0;
+            a.cp_sstride = 16u;
+            a.cp_dst = canvas.p + T.state_off;
+            a.cp_dstride = 64u;
+        }
     }
     a.cout = w.cout;
     a.tokens = w.part_tokens;

@@ -767,6 +767,119 @@ void K44GpuExecutorState::fuse_norm_shifts() {
     }
 }
 
+// A decode RMSNorm that runs its token shift (fuse_norm_shifts) and whose producers store the
+// sums of squares is not launched either when every reader of the shift's output is a narrow
+// 64/128-neuron wave gathering it plainly: those waves gather the norm's input and apply the
+// norm and the shift in their gather (gather form 5, the norm and shift kernel's expressions).
+// The state update cannot happen there in place (other workgroups of the same launch read the
+// old state): for every channel one reading workgroup stores the shifted state in a private
+// buffer (shift_next), and the workgroups of the next narrow launch after the last reader (the
+// carrier) copy it back.  Conditions: a decode shift with 2 <= rf <= 4 and a state; the norm's
+// output read by nothing else and the shift's output only by such waves (segments inside it, at
+// the canvas step of its rows) until overwritten, neither the plan output; the norm's input
+// intact until the last reader; nothing from the norm to the carrier touching the state; every
+// channel gathered by some reader; contraction chunks of at most 4 sub-chunks (64 k-steps).
+// Returns the readers, the carrier (index into ops) and per reader the ownership bits of its
+// work items (MfmaTileArgs::own).
+bool K44GpuExecutorState::fold_shift(size_t i, const std::pair<uint64_t, uint64_t> &X,
+                                     const std::pair<uint64_t, uint64_t> &Y,
+                                     const std::vector<Ranges> &rd, const std::vector<Ranges> &wr,
+                                     const Ranges &out_rng, std::vector<size_t> &cons,
+                                     size_t &refresher, size_t &carrier,
+                                     std::vector<std::vector<uint64_t>> &owns) {
+    typedef std::pair<uint64_t, uint64_t> Rng;
+    const AuxExec &N = *aux[ops[i].second];
+    const AuxExec &T = *aux[N.shift_with];
+    if (!T.decode || T.rf < 2u || T.rf > 4u || !T.has_state || T.tokens != N.tokens ||
+        T.stride != N.stride || T.D != N.D || T.tokens > 16u)
+        return false;
+    const uint64_t D = N.D, stride = N.stride;
+    const Rng Sg(T.y_off, T.y_off + D * stride);
+    const Rng St(T.state_off, T.state_off + D * (T.rf - 1u) * 64u);
+    auto narrow_long = [&](const WaveExec &w) {
+        return w.mfma && w.narrow && (w.cluster == 64u || w.cluster == 128u) && !w.tile2d;
+    };
+    const size_t n = ops.size();
+    cons.clear();
+    size_t last = i;
+    bool ow_y = false, ow_s = false;
+    for (size_t j = i + 1; j < n && !(ow_y && ow_s); ++j) {
+        if (!ow_y && ranges_overlap(rd[j], Ranges{Y})) return false;
+        if (!ow_s && ranges_overlap(rd[j], Ranges{Sg})) {
+            if (!ops[j].first) return false;
+            const WaveExec &w = *waves[ops[j].second];
+            bool ok = narrow_long(w) && w.xprod == 0u && w.step == stride && w.S % 32u == 0u &&
+                      !ranges_overlap(w.resrd, Ranges{Sg}) &&
+                      (w.kgroups > 1u ? w.stage_chunk : w.ksteps) <= 64u &&
+                      w.seg_h.size() == (size_t)w.rows * w.K;
+            for (const auto &x : w.xrd) ok = ok && Sg.first <= x.first && x.second <= Sg.second;
+            if (!ok) return false;
+            cons.push_back(ops[j].second);
+            last = j;
+        }
+        ow_y = ow_y || ranges_overlap(wr[j], Ranges{Y});
+        ow_s = ow_s || ranges_overlap(wr[j], Ranges{Sg});
+    }
+    if (cons.empty() || (!ow_y && ranges_overlap(Ranges{Y}, out_rng)) ||
+        (!ow_s && ranges_overlap(Ranges{Sg}, out_rng)))
+        return false;
+    for (size_t j = i + 1; j <= last; ++j)
+        if (ranges_overlap(wr[j], Ranges{X})) return false;
+    carrier = SIZE_MAX;
+    for (size_t j = last + 1; j < n && carrier == SIZE_MAX; ++j)
+        if (ops[j].first && narrow_long(*waves[ops[j].second]) &&
+            waves[ops[j].second]->cp_fold == SIZE_MAX)
+            carrier = j;
+    if (carrier == SIZE_MAX) return false;
+    for (size_t j = i + 1; j <= carrier; ++j)
+        if (ranges_overlap(rd[j], Ranges{St}) || ranges_overlap(wr[j], Ranges{St})) return false;
+    // the refresher: the last narrow launch before the norm, with nothing after it writing the
+    // state before the readers
+    refresher = SIZE_MAX;
+    for (size_t j = i; j-- > 0 && refresher == SIZE_MAX;)
+        if (ops[j].first && narrow_long(*waves[ops[j].second]) &&
+            waves[ops[j].second]->cp_fold == SIZE_MAX)
+            refresher = j;
+    if (refresher == SIZE_MAX) return false;
+    for (size_t j = refresher; j < i; ++j)
+        if (ranges_overlap(wr[j], Ranges{St})) return false;
+    // ownership: the first work item (readers in plan order, items in launch order) gathering a
+    // channel not yet covered stores the shifted state of its pass (a channel stored twice gets
+    // the same bits twice)
+    std::vector<uint8_t> cov(D, 0u);
+    uint64_t ncov = 0;
+    owns.assign(cons.size(), {});
+    for (size_t k = 0; k < cons.size(); ++k) {
+        const WaveExec &w = *waves[cons[k]];
+        std::vector<uint64_t> &own = owns[k];
+        own.assign((size_t)w.rows * w.kgroups, 0u);
+        const uint32_t chunk = w.kgroups > 1u ? w.stage_chunk : w.ksteps;
+        for (uint32_t z = 0; z < w.kgroups; ++z)
+            for (uint32_t tl = 0; tl < w.rows; ++tl) {
+                const uint32_t kb0 = z * chunk, ke = std::min(w.ksteps, kb0 + chunk);
+                for (uint32_t s = 0; kb0 + 16u * s < ke; ++s) {
+                    const uint32_t kb = kb0 + 16u * s, nr = (std::min(ke, kb + 16u) - kb) * 32u;
+                    for (uint32_t p = 0; p < 16u && 32u * p < nr; ++p) {
+                        const uint32_t r = kb * 32u + 32u * p, kk = r / w.S;
+                        const uint64_t off = w.seg_h[(size_t)tl * w.K + kk] +
+                                             (uint64_t)(r - kk * w.S) * w.step;
+                        if (off < Sg.first || (off - Sg.first) % stride != 0u) return false;
+                        const uint64_t c0 = (off - Sg.first) / stride;
+                        bool fresh = false;
+                        for (uint64_t c = c0; c < c0 + 32u && c < D; ++c)
+                            if (!cov[c]) {
+                                cov[c] = 1u;
+                                ++ncov;
+                                fresh = true;
+                            }
+                        if (fresh) own[(size_t)z * w.rows + tl] |= 1ull << (s * 16u + p);
+                    }
+                }
+            }
+    }
+    return ncov == D;
+}
+
 // RMSNorms of decode-sized plans whose input is written by narrow 64/128-neuron MFMA waves
 // (the sub-waves of the projections before them, each tile's outputs stored by one
 // workgroup) take their per-token scales from those waves: every producer tile stores the
@@ -860,6 +973,12 @@ void K44GpuExecutorState::fuse_norms() {
         // consumers (a norm without a fused shift): readers of Y until overwritten
         std::vector<size_t> cons;
         bool consume = N.shift_with == SIZE_MAX;
+        // a norm with its decode token shift: the shift's readers (fold_shift below)
+        size_t refresher = SIZE_MAX, carrier = SIZE_MAX;
+        std::vector<std::vector<uint64_t>> owns;
+        const bool shifted =
+            !consume && tune(Tune::Program) != 1 &&
+            fold_shift(i, X, Y, rd, wr, out_rng, cons, refresher, carrier, owns);
         if (consume) {
             size_t last = i;
             bool overwritten = false;
@@ -895,9 +1014,45 @@ void K44GpuExecutorState::fuse_norms() {
             f.tiles += w.rows;
             w.why += "; its tiles form the sums of squares of a folded RMSNorm";
         }
-        f.consumers = consume;
+        f.consumers = consume || shifted;
         N.norm_fold = norm_folds.size();
-        if (consume) {
+        if (shifted) {
+            const AuxExec &T = *aux[N.shift_with];
+            const Rng Sg(T.y_off, T.y_off + (uint64_t)T.D * T.stride);
+            const Rng St(T.state_off, T.state_off + (uint64_t)T.D * (T.rf - 1u) * 64u);
+            f.shift = N.shift_with;
+            f.next0 = shift_next_elems;
+            f.cur0 = f.next0 + (size_t)T.D * (T.rf - 1u) * 16u;
+            shift_next_elems += 2u * (size_t)T.D * (T.rf - 1u) * 16u;
+            N.fused = true;
+            N.fuse_note = "folded with its token shift: sums of squares stored by its producers, "
+                          "rows normalised and shifted in its readers' gathers";
+            for (size_t k = 0; k < cons.size(); ++k) {
+                WaveExec &w = *waves[cons[k]];
+                w.xprod = 5u;
+                w.xnorm = norm_folds.size();
+                w.xd[0] = (int64_t)X.first - (int64_t)Sg.first;
+                w.own.upload(owns[k]);
+                Ranges fr = w.resrd;
+                for (const auto &x : w.xrd)
+                    fr.push_back({(uint64_t)((int64_t)x.first + w.xd[0]),
+                                  (uint64_t)((int64_t)x.second + w.xd[0])});
+                fr.push_back(St);
+                w.rd_run = merge_ranges(std::move(fr));
+                w.why += "; gathers its input through a folded RMSNorm and decode token shift";
+            }
+            // the compact copy is refreshed by the refresher's launch and the state written back
+            // by the carrier's (neither grouped with a reader)
+            WaveExec &rw = *waves[ops[refresher].second];
+            rw.cp_fold = norm_folds.size();
+            rw.cp_refresh = true;
+            rw.carry_rng = {St};
+            rw.why += "; its workgroups refresh the compact state copy of a later token shift";
+            WaveExec &cw = *waves[ops[carrier].second];
+            cw.cp_fold = norm_folds.size();
+            cw.carry_rng = {St};
+            cw.why += "; its workgroups copy back the shifted state of an earlier token shift";
+        } else if (consume) {
             N.fused = true;
             N.fuse_note = "folded: sums of squares stored by its producers, rows normalised "
                           "in its readers' gathers";
@@ -950,9 +1105,14 @@ void K44GpuExecutorState::form_runs() {
             bool indep = true;
             for (size_t m : g.members) {
                 const WaveExec &o = *waves[m];
+                // (a carried state copy writes carry_rng)
                 indep = !ranges_overlap(w.wr_run, o.rd_run) &&
                         !ranges_overlap(w.rd_run, o.wr_run) &&
-                        !ranges_overlap(w.wr_run, o.wr_run);
+                        !ranges_overlap(w.wr_run, o.wr_run) &&
+                        !ranges_overlap(w.carry_rng, o.rd_run) &&
+                        !ranges_overlap(w.carry_rng, o.wr_run) &&
+                        !ranges_overlap(w.rd_run, o.carry_rng) &&
+                        !ranges_overlap(w.wr_run, o.carry_rng);
                 if (!indep) break;
             }
             if (!indep) break;
@@ -1046,6 +1206,16 @@ void K44GpuExecutorState::build_report() {
           << ", \"unique_rows\": " << w.unique_rows
           << ", \"y_off\": " << w.y_off << ", \"y_off_run\": " << w.y_off_run
           << ", \"xd\": [" << w.xd[0] << ", " << w.xd[1] << ", " << w.xd[2] << "]"
+          // gather form 5: the token-shift command it applies; a carrier: the token-shift
+          // command whose shifted state its launch copies back (-1: none)
+          << ", \"shift_cmd\": "
+          << (w.xprod == 5u ? (long long)aux_cmd[norm_folds[w.xnorm].shift] : -1LL)
+          << ", \"copies_state_of\": "
+          << (w.cp_fold != SIZE_MAX && !w.cp_refresh
+                  ? (long long)aux_cmd[norm_folds[w.cp_fold].shift] : -1LL)
+          << ", \"refreshes_state_of\": "
+          << (w.cp_fold != SIZE_MAX && w.cp_refresh
+                  ? (long long)aux_cmd[norm_folds[w.cp_fold].shift] : -1LL)
           << ", \"cmd\": " << wave_cmd[i] << "}";
     }
     o << "], \"aux\": [";

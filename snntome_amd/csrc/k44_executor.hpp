@@ -130,6 +130,18 @@ struct WaveExec {
     size_t norm_fold = SIZE_MAX;
     uint32_t norm_tile0 = 0;
     size_t xnorm = SIZE_MAX;
+    // Narrow waves: segment starts as uploaded ([rows][K], host copy).  Gather form 5 (a folded
+    // RMSNorm + decode token shift): per work item the 32-row passes whose channels' shifted
+    // state it stores (bit sub-chunk * 16 + pass).  cp_fold: the fold whose state copy this
+    // wave's launch carries: the plan's state into the compact copy before the readers
+    // (cp_refresh), or the shifted state back into the plan's state after them.
+    std::vector<uint64_t> seg_h;
+    DevBuf<uint64_t> own;
+    size_t cp_fold = SIZE_MAX;
+    bool cp_refresh = false;
+    // the state range of a carried copy, counted as written when launches are grouped (so the
+    // launch never joins one of the fold's readers)
+    std::vector<std::pair<uint64_t, uint64_t>> carry_rng;
     // 2-D spatial wave (VALU over the padded-plane tile layout): tile tables, output plane.
     bool tile2d = false;
     DevBuf<uint32_t> tile_x, tile_y;
@@ -261,9 +273,17 @@ struct K44GpuExecutorState {
         uint32_t tiles = 0;         // producer tiles (slots)
         size_t slot0 = 0;           // first slot in norm_slots
         bool consumers = false;     // not launched: its readers gather normalised rows
+        // The decode token shift run with the norm (its readers gather shifted rows, gather
+        // form 5), and the fold's regions of shift_next ([D][rf-1][16] each): the shifted
+        // state (next0) and the compact copy of the state its readers read (cur0).
+        size_t shift = SIZE_MAX;
+        size_t next0 = 0, cur0 = 0;
+        size_t mix0 = 0;  // its [D][8] table in shift_mix (MfmaTileArgs::mixg)
     };
     std::vector<NormFold> norm_folds;
     DevBuf<uint32_t> norm_slots;
+    DevBuf<__half> shift_next, shift_mix;
+    size_t shift_next_elems = 0;
     const uint64_t *fold_slots(size_t fold) const {
         return reinterpret_cast<const uint64_t *>(norm_slots.p + norm_folds[fold].slot0 * 64u);
     }
@@ -328,6 +348,12 @@ struct K44GpuExecutorState {
     void fuse_products();
     void fuse_mul_chains();
     void fuse_norm_shifts();
+    bool fold_shift(size_t i, const std::pair<uint64_t, uint64_t> &X,
+                    const std::pair<uint64_t, uint64_t> &Y, const std::vector<Ranges> &rd,
+                    const std::vector<Ranges> &wr, const Ranges &out_rng,
+                    std::vector<size_t> &cons, size_t &refresher, size_t &carrier,
+                    std::vector<std::vector<uint64_t>> &owns);
+
     void fuse_norms();
     void form_runs();
     size_t launches_per_run() const;

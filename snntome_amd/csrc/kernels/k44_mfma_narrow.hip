@@ -452,9 +452,15 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
     // multiply with the rounding of the unfused multiply commands: fp16(A*B), fp16(A*fp16(B*C)).
     constexpr int XQ = NARROW_MAX_ROWS * 2 / 256;
     constexpr uint32_t xprod = (uint32_t)PROD;  // every wave of the launch gathers this form
-    // Folded RMSNorm (xprod 4): the lane's 8 tokens' scales, formed from the producers' slots
-    // after the first sub-chunk's loads are issued.
-    float xinv[xprod == 4u ? 8 : 1];
+    // Folded RMSNorm (xprod 4, 5): the lane's 8 tokens' scales, formed from the producers'
+    // slots after the first sub-chunk's loads are issued.
+    constexpr bool NORM = xprod == 4u || xprod == 5u;
+    float xinv[NORM ? 8 : 1];
+    // xprod 5: state rows 1 and 2 of each pass (row 0 in xc), and the passes this workgroup
+    // stores the shifted state of
+    u4_t xs1[XQ], xs2[XQ];
+    uint64_t ownb = 0;
+    if constexpr (xprod == 5u) ownb = ((const kconst_u64 *)a.own)[local];
     auto gather = [&](uint32_t s, u4_t (&xv)[XQ], u4_t (&xb)[XQ], u4_t (&xc)[XQ]) {
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
@@ -466,16 +472,35 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
             sb[q] = segr[k] + (uint64_t)(r - k * a.S) * a.step + (uint64_t)(lane >> 1) * a.step +
                     (uint32_t)(lane & 1) * 8u;
         }
-        if (xprod == 4u) {
+        if (NORM) {
             // the norm's input rows and their gammas (xb holds the gamma bits of each pass)
 #pragma unroll
             for (int q = 0; q < XQ; ++q) xv[q] = *(gu4_t *)(a.X + (int64_t)sb[q] + a.xd[0]);
             typedef const __attribute__((address_space(1))) uint16_t gu16;
-            gu16 *gm = (gu16 *)(a.xgamma ? (const void *)a.xgamma : (const void *)a.X);
+            if (xprod == 4u) {
+                gu16 *gm = (gu16 *)(a.xgamma ? (const void *)a.xgamma : (const void *)a.X);
 #pragma unroll
-            for (int q = 0; q < XQ; ++q) {
-                const uint64_t row = sb[q] - (uint32_t)(lane & 1) * 8u;
-                xb[q][0] = a.xgamma ? (uint32_t)gm[(row - a.xg_base) >> a.xg_shift] : 0x3c00u;
+                for (int q = 0; q < XQ; ++q) {
+                    const uint64_t row = sb[q] - (uint32_t)(lane & 1) * 8u;
+                    xb[q][0] = a.xgamma ? (uint32_t)gm[(row - a.xg_base) >> a.xg_shift] : 0x3c00u;
+                }
+            } else {
+                // the channel's mixing weights and gamma (xb[0..2], one 16-byte load), its
+                // state rows (xc, xs1, xs2; rows past rf - 2 repeat the last) and the channel
+                // itself (xb[3])
+                const uint32_t rf = a.rf;
+#pragma unroll
+                for (int q = 0; q < XQ; ++q) {
+                    const uint32_t c =
+                        (uint32_t)((sb[q] - (uint32_t)(lane & 1) * 8u - a.xg_base) >> a.xg_shift);
+                    xb[q] = *(gu4_t *)(a.mixg + (uint64_t)c * 8u);
+                    xb[q][3] = c;
+                    const __half *st = a.state + (uint64_t)c * (rf - 1u) * 16u +
+                                       (uint32_t)(lane & 1) * 8u;
+                    xc[q] = *(gu4_t *)st;
+                    xs1[q] = *(gu4_t *)(st + min(1u, rf - 2u) * 16u);
+                    xs2[q] = *(gu4_t *)(st + min(2u, rf - 2u) * 16u);
+                }
             }
         } else if (xprod == 0u) {
 #pragma unroll
@@ -496,11 +521,12 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
                      const u4_t (&xc)[XQ]) {
         const uint32_t kb = ks_begin + s * SUBK;
         const uint32_t nrows = (min(ks_end, kb + SUBK) - kb) * 32u;
-        if (xprod == 4u) {
+        if (NORM) {
 #pragma unroll
             for (int q = 0; q < XQ; ++q) {
                 h8_t ha = __builtin_bit_cast(h8_t, xv[q]);
-                const float gq = __half2float(__ushort_as_half((unsigned short)xb[q][0]));
+                const float gq = __half2float(
+                    __ushort_as_half((unsigned short)(xb[q][xprod == 5u ? 2 : 0] & 0xffffu)));
 #pragma unroll
                 for (int e2 = 0; e2 < 8; ++e2) {
                     // element copied to a scalar first: a bit cast of the vector element itself
@@ -508,6 +534,45 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
                     const _Float16 xe = ha[e2];
                     const __half r = norm_scale(__builtin_bit_cast(__half, xe), xinv[e2], gq);
                     ha[e2] = __builtin_bit_cast(_Float16, r);
+                }
+                if (xprod == 5u) {
+                    // decode token shift of the normalised values (k44_rmsnorm_kernel's
+                    // expression and order), and the shifted state for an owned pass
+                    const uint32_t rf = a.rf;
+                    float mw[4];
+                    mw[0] = __half2float(__ushort_as_half((unsigned short)(xb[q][0] & 0xffffu)));
+                    mw[1] = __half2float(__ushort_as_half((unsigned short)(xb[q][0] >> 16)));
+                    mw[2] = __half2float(__ushort_as_half((unsigned short)(xb[q][1] & 0xffffu)));
+                    mw[3] = __half2float(__ushort_as_half((unsigned short)(xb[q][1] >> 16)));
+                    const h8_t s0 = __builtin_bit_cast(h8_t, xc[q]);
+                    const h8_t s1 = __builtin_bit_cast(h8_t, xs1[q]);
+                    const h8_t s2 = __builtin_bit_cast(h8_t, xs2[q]);
+                    h8_t y2, n0 = s0, n1 = s1, n2 = s2;
+#pragma unroll
+                    for (int e2 = 0; e2 < 8; ++e2) {
+                        const uint32_t t = (uint32_t)(lane & 1) * 8u + (uint32_t)e2;
+                        const _Float16 ne = ha[e2], e0 = s0[e2], e1 = s1[e2], e3 = s2[e2];
+                        float acc = mw[0] * (float)ne;
+                        acc = fmaf(mw[1], (float)e0, acc);
+                        if (rf > 2u) acc = fmaf(mw[2], (float)e1, acc);
+                        if (rf > 3u) acc = fmaf(mw[3], (float)e3, acc);
+                        const _Float16 yv = __builtin_bit_cast(_Float16, f16_of(acc));
+                        const bool live = t < a.sh_tokens;
+                        y2[e2] = live ? yv : (_Float16)0.0f;
+                        n0[e2] = live ? ne : e0;
+                        n1[e2] = live ? e0 : e1;
+                        n2[e2] = live ? e1 : e3;
+                    }
+                    const uint32_t rb = (uint32_t)(32 * (wave + 4 * q));
+                    if (rb < nrows && ((ownb >> (s * 16u + (uint32_t)(wave + 4 * q))) & 1u)) {
+                        typedef __attribute__((address_space(1))) u4_t gu4w;
+                        gu4w *sn = (gu4w *)(a.state_next + (uint64_t)xb[q][3] * (rf - 1u) * 16u +
+                                            (uint32_t)(lane & 1) * 8u);
+                        sn[0] = __builtin_bit_cast(u4_t, n0);
+                        if (rf > 2u) sn[2] = __builtin_bit_cast(u4_t, n1);
+                        if (rf > 3u) sn[4] = __builtin_bit_cast(u4_t, n2);
+                    }
+                    ha = y2;
                 }
                 xv[q] = __builtin_bit_cast(u4_t, ha);
             }
@@ -537,6 +602,11 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
         }
     };
 
+    // a folded norm's producer slots first: they arrive ahead of the weights and the gather
+    // (loads complete in issue order), so the scales are formed while those are in flight
+    SlotLoads<16u> slp;
+    if constexpr (NORM)
+        rms_slots_issue<16u>(reinterpret_cast<const uint64_t *>(a.xslots), a.xslots_n, 0u, slp);
     h8_t af[AF][BPW];
 #pragma unroll
     for (int u = 0; u < AF; ++u) load_a((uint32_t)u, af[u]);
@@ -556,11 +626,20 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
     NarrowEpi<BPW> e;
     uint32_t cb[BPW][4];
     if (epi) narrow_epi_maps<BPW>(a, j0, cb, e);
-    if constexpr (xprod == 4u) {
+    // A copy carried for an earlier launch (cp_rows): the thread's first 16 bytes loaded now,
+    // stored after the contraction.
+    const uint32_t cpn = a.cp_rows * 2u, cpstep = a.tiles * a.kgroups * 256u;
+    const uint32_t cpe = local * 256u + (uint32_t)tid;
+    auto cp_at = [&](const __half *base, uint32_t stride, uint32_t i) {
+        return base + (uint64_t)(i >> 1) * stride + (i & 1u) * 8u;
+    };
+    u4_t cpv = {0u, 0u, 0u, 0u};
+    if (cpn) cpv = *(gu4_t *)cp_at(a.cp_src, a.cp_sstride, min(cpe, cpn - 1u));
+    if constexpr (NORM) {
         __shared__ uint4 ipart[4][16];
         __shared__ float sinv[16];
-        rms_inv_from_slots<16u>(reinterpret_cast<const uint64_t *>(a.xslots), a.xslots_n, 0u,
-                                a.norm_D, a.norm_eps, ipart, sinv);
+        rms_slots_finish<16u>(slp, reinterpret_cast<const uint64_t *>(a.xslots), a.xslots_n, 0u,
+                              a.norm_D, a.norm_eps, ipart, sinv);
 #pragma unroll
         for (int e2 = 0; e2 < 8; ++e2) xinv[e2] = sinv[(lane & 1) * 8 + e2];
     }
@@ -599,6 +678,13 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
         }
     }
 
+    if (cpn) {
+        typedef __attribute__((address_space(1))) u4_t gu4w;
+        auto dst = [&](uint32_t i) { return (gu4w *)cp_at(a.cp_dst, a.cp_dstride, i); };
+        if (cpe < cpn) *dst(cpe) = cpv;
+        for (uint32_t i = cpe + cpstep; i < cpn; i += cpstep)
+            *dst(i) = *(gu4_t *)cp_at(a.cp_src, a.cp_sstride, i);
+    }
     if (epi) {
         // the fused epilogue (loads issued above), then the tile's share of a folded RMSNorm
         uint16_t out[BPW][4];
@@ -620,7 +706,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
 
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
                               hipStream_t stream, uint32_t prod, uint32_t max_items) {
-    if (prod != 0u && ((nt != 64u && nt != 128u) || (prod < 2u || prod > 4u)))
+    if (prod != 0u && ((nt != 64u && nt != 128u) || (prod < 2u || prod > 5u)))
         return hipErrorInvalidValue;
     if (items == 0u) return hipSuccess;
     const dim3 grid(items), block(256);
@@ -637,7 +723,9 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
     case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, K44_GROUP_ARGS(g)); break;
     case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, K44_GROUP_ARGS(g)); break;
     case 64u:
-        if (prod == 4u) {
+        if (prod == 5u) {
+            K44_NL(64, 5)
+        } else if (prod == 4u) {
             K44_NL(64, 4)
         } else if (prod == 3u) {
             K44_NL(64, 3)
@@ -648,7 +736,9 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
         }
         break;
     case 128u:
-        if (prod == 4u) {
+        if (prod == 5u) {
+            K44_NL(128, 5)
+        } else if (prod == 4u) {
             K44_NL(128, 4)
         } else if (prod == 3u) {
             K44_NL(128, 3)

@@ -69,7 +69,8 @@ struct MfmaTileArgs {
     // Product gather (element-wise multiplies fused into the X gather; narrow kernels of 64 /
     // 128-neuron tiles only): xprod 0 = the X rows as they are; 2 = fp16(A*B); 3 =
     // fp16(A*fp16(B*C)), A / B / C the rows at (segment offset + xd[0] / xd[1] / xd[2]);
-    // 4 = a folded RMSNorm of the rows at (segment offset + xd[0]) (fields below).
+    // 4 = a folded RMSNorm of the rows at (segment offset + xd[0]) (fields below); 5 = the
+    // same followed by the decode token shift of the normalised rows (fields below).
     uint32_t xprod;
     int64_t xd[3];
     // 2-D waves of 64-frame interleaved images: 64-token tile t of the wave gathers at
@@ -100,6 +101,29 @@ struct MfmaTileArgs {
     const __half *xgamma;
     uint64_t xg_base;
     uint32_t xg_shift;
+    // xprod 5: each normalised element n of channel c, token t becomes the decode token shift's
+    // output fp16(mu[c][0] n + sum_{i=1}^{rf-1} mu[c][i] state[c][i-1][t]) (the shift kernel's
+    // expression) for t < sh_tokens, and 0 beyond.  The state is read from a compact copy
+    // ([c][rf-1][16 tokens], refreshed from the plan's state by an earlier launch: 32 of every
+    // 128 bytes of the plan's [c][rf-1][64] rows are the tokens).  The shifted state ([n,
+    // state[c][0], .., state[c][rf-3]] for t < sh_tokens, unchanged beyond) cannot be stored in
+    // place (other workgroups of the launch read the old state): the workgroup whose bit
+    // own[item] has for a 32-row pass (bit sub-chunk * 16 + pass) stores it for the pass's
+    // channels in state_next [c][rf-1][16], and a later launch copies it back (cp_* below).
+    // 2 <= rf <= 4.
+    const __half *mixg;        // [D][8]: mixing weights mu[c][0..rf-1] (0 past rf), the
+                               // norm's gamma[c] (1 without one) at 4, 0 at 5..7
+    const __half *state;       // [D][rf-1][16] (compact copy)
+    __half *state_next;        // [D][rf-1][16]
+    const uint64_t *own;       // [tiles * kgroups]
+    uint32_t rf, sh_tokens;
+    // Copy carried by this wave's workgroups (cp_rows 0: none): cp_rows rows of 16 fp16 from
+    // cp_src + cp_sstride r to cp_dst + cp_dstride r (strides in elements): a folded token
+    // shift's state refreshed into its compact copy before its readers, or its shifted state
+    // copied back after them.
+    const __half *cp_src;
+    __half *cp_dst;
+    uint32_t cp_rows, cp_sstride, cp_dstride;
     // Single-frame 2-D outputs whose 64-token tiles span plane rows (padded-plane layout, W not
     // a multiple of 64): token t of tile tl of its frame is pixel rel = 64 tl + (t & 63) of the
     // padded rows, stored only when rel / mask_wpad < mask_h and rel % mask_wpad < mask_w (the

@@ -116,25 +116,40 @@ __device__ __forceinline__ SumSq sumsq_wave_reduce(SumSq s, int span) {
 // thread (token tid % TK, part tid / TK) adds slots part, part + 256 / TK, ... (exact: any
 // order gives the same integer), the parts of a token meet by shuffles within the wave and
 // across the 4 waves in LDS; inv[k] holds token t0 + k's scale after the call's last barrier.
+// In two steps, so that a kernel can issue the slot loads before its other loads and add them
+// once they have arrived: rms_slots_issue loads the thread's first 4 slots (up to 4 x 256 / TK
+// slots in all), rms_slots_finish adds them (and loads any further slots itself).
 template <uint32_t TK>
-__device__ __forceinline__ void rms_inv_from_slots(const uint64_t *slots, uint32_t n,
-                                                   uint32_t t0, uint32_t D, float eps,
-                                                   uint4 (&part)[4][TK], float (&inv)[TK]) {
+struct SlotLoads {
+    uint64_t lo[4], hi[4];
+};
+
+template <uint32_t TK>
+__device__ __forceinline__ void rms_slots_issue(const uint64_t *slots, uint32_t n, uint32_t t0,
+                                                SlotLoads<TK> &p) {
     static_assert(TK == 8u || TK == 16u, "tokens per pass");
+    constexpr uint32_t PARTS = 256u / TK;
+    typedef const __attribute__((address_space(1))) uint64_t gu64c;
+    const uint32_t tk = threadIdx.x % TK, pt = threadIdx.x / TK;
+#pragma unroll
+    for (uint32_t u = 0; u < 4u; ++u) {
+        const uint32_t i = min(pt + PARTS * u, n - 1u);
+        const gu64c *w = (const gu64c *)slots + ((uint64_t)i * 16u + t0 + tk) * 2u;
+        p.lo[u] = w[0];
+        p.hi[u] = w[1];
+    }
+}
+
+template <uint32_t TK>
+__device__ __forceinline__ void rms_slots_finish(const SlotLoads<TK> &p, const uint64_t *slots,
+                                                 uint32_t n, uint32_t t0, uint32_t D, float eps,
+                                                 uint4 (&part)[4][TK], float (&inv)[TK]) {
     constexpr uint32_t PARTS = 256u / TK;
     typedef const __attribute__((address_space(1))) uint64_t gu64c;
     const uint32_t tk = threadIdx.x % TK, pt = threadIdx.x / TK;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     SumSq q = sumsq_zero();
-    for (uint32_t i0 = pt; i0 < n; i0 += 4u * PARTS) {
-        uint64_t lo[4], hi[4];
-#pragma unroll
-        for (uint32_t u = 0; u < 4u; ++u) {
-            const uint32_t i = min(i0 + PARTS * u, n - 1u);
-            const gu64c *w = (const gu64c *)slots + ((uint64_t)i * 16u + t0 + tk) * 2u;
-            lo[u] = w[0];
-            hi[u] = w[1];
-        }
+    auto add4 = [&](uint32_t i0, const uint64_t (&lo)[4], const uint64_t (&hi)[4]) {
 #pragma unroll
         for (uint32_t u = 0; u < 4u; ++u)
             if (i0 + PARTS * u < n) {
@@ -143,6 +158,18 @@ __device__ __forceinline__ void rms_inv_from_slots(const uint64_t *slots, uint32
                 q.l2 += hi[u] & 0xffffffffull;
                 q.sp |= (uint32_t)(hi[u] >> 32);
             }
+    };
+    add4(pt, p.lo, p.hi);
+    for (uint32_t i0 = pt + 4u * PARTS; i0 < n; i0 += 4u * PARTS) {
+        uint64_t lo[4], hi[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4u; ++u) {
+            const uint32_t i = min(i0 + PARTS * u, n - 1u);
+            const gu64c *w = (const gu64c *)slots + ((uint64_t)i * 16u + t0 + tk) * 2u;
+            lo[u] = w[0];
+            hi[u] = w[1];
+        }
+        add4(i0, lo, hi);
     }
     q = sumsq_wave_reduce(q, (int)TK);  // the lanes of one token in this wave
     if (lane < TK) part[wave][lane] = uint4{(uint32_t)q.l0, (uint32_t)q.l1, (uint32_t)q.l2, q.sp};
@@ -160,6 +187,15 @@ __device__ __forceinline__ void rms_inv_from_slots(const uint64_t *slots, uint32
         inv[threadIdx.x] = rms_inv(t, D, eps);
     }
     __syncthreads();
+}
+
+template <uint32_t TK>
+__device__ __forceinline__ void rms_inv_from_slots(const uint64_t *slots, uint32_t n,
+                                                   uint32_t t0, uint32_t D, float eps,
+                                                   uint4 (&part)[4][TK], float (&inv)[TK]) {
+    SlotLoads<TK> p;
+    rms_slots_issue<TK>(slots, n, t0, p);
+    rms_slots_finish<TK>(p, slots, n, t0, D, eps, part, inv);
 }
 
 }  // namespace k44dev

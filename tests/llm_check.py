@@ -91,6 +91,9 @@ class PlanChecker:
         if fused and w["xprod"] == 4:  # a folded RMSNorm: the norm run alone materialises it
             self._materialise_norm(i)
             return self.rows(c["src_off"], c["Cin"])
+        if fused and w["xprod"] == 5:  # folded RMSNorm + token shift: both run alone
+            self._materialise_norm_shift(i, int(w["shift_cmd"]))
+            return self.rows(c["src_off"], c["Cin"])
         if fused and w["xprod"]:
             leaves = [self.rows(int(c["src_off"]) + int(d), c["Cin"]) for d in w["xd"][:w["xprod"]]]
             if w["xprod"] == 2:
@@ -118,6 +121,42 @@ class PlanChecker:
         y = self.rows(c["y_off"], c["Cin"]).astype(np.float64)
         self._note("RMSNORM_1D", lo.orc.rel_err(y, lo.rmsnorm_f64(x)), f"{c['name']} (folded)")
         self._materialised.add(n)
+
+    def _materialise_norm_shift(self, i: int, t: int):
+        """Run mode, a wave gathering through a folded RMSNorm and decode token shift (gather
+        form 5): the norm and the shift commands are run alone (execute_range) into their own
+        output ranges — the place and order of the unfolded plan, whose schedule is the same up
+        to this run — and checked against the oracle; the shift's state update is then undone
+        (the gathers read the old state), and the state the shift computed is what the launch
+        that copies back the folded state must leave (checked in _after)."""
+        c = self.cmds[t]
+        assert int(c["y_off"]) == int(self.cmds[i]["src_off"]), f"{c['name']}: not the wave's input"
+        n = max(k for k in range(t) if self.cmds[k]["type"] == "RMSNORM_1D"
+                and int(self.cmds[k]["y_off"]) == int(c["src_off"]))
+        assert self.aux_rep[n]["fused"], f"{self.cmds[n]['name']}: not a folded norm"
+        if t in self._materialised:
+            return
+        cn = self.cmds[n]
+        x = self.rows(cn["src_off"], cn["Cin"])
+        st_raw = self.plan.read_canvas(int(c["state_off"]), self.spec.d * (self.spec.rf - 1) * 64)
+        self.plan.execute_range(n, 1)
+        y = self.rows(cn["y_off"], cn["Cin"]).astype(np.float64)
+        self._note("RMSNORM_1D", lo.orc.rel_err(y, lo.rmsnorm_f64(x)), f"{cn['name']} (folded)")
+        xs = self.full(c["src_off"], c["Cin"])
+        st_in = st_raw.view(F16).reshape(self.spec.d, self.spec.rf - 1, 64)
+        self.plan.execute_range(t, 1)
+        ys = self.full(c["y_off"], c["Cin"])
+        ref, st_ref = lo.token_shift_decode(xs, self.mix[c["name"]], st_in, self.valid, f64=True)
+        st = self._state(c)
+        assert np.array_equal(st[:, :, :self.valid].view(np.uint16),
+                              st_ref[:, :, :self.valid].view(np.uint16)), \
+            f"{c['name']} (folded): state block differs"
+        v = self.valid
+        self._note("TOKEN_SHIFT_1D", lo.orc.rel_err(ys[:, :v].astype(np.float64), ref[:, :v]),
+                   f"{c['name']} (folded)")
+        self._pending_state[t] = st.copy()
+        self.plan.write_canvas(int(c["state_off"]), st_raw)
+        self._materialised.add(t)
 
     def _y_off(self, i: int, fused: bool) -> int:
         return int(self.wave_rep[i]["y_off_run"] if fused else self.cmds[i]["y_off"])
@@ -168,6 +207,13 @@ class PlanChecker:
             what = f"{tag} {name}"
             if t == "K44_WAVE":
                 node = _base(name)
+                cp = int(self.wave_rep[i].get("copies_state_of", -1)) if fused else -1
+                if cp >= 0:  # this launch copied back a folded token shift's state
+                    want = self._pending_state.pop(cp)
+                    assert np.array_equal(self._state(self.cmds[cp]).view(np.uint16),
+                                          want.view(np.uint16)), \
+                        f"{what}: state copied back for {self.cmds[cp]['name']} differs"
+                    self.checked["state copy"] = self.checked.get("state copy", 0) + 1
                 state["done"].setdefault(node, set()).add(i)
                 if state["done"][node] != set(self.subwaves[node]):
                     continue  # the node's other sub-waves have not run yet
@@ -272,6 +318,7 @@ class PlanChecker:
         self.plan.set_ids(ids)
         state = {"proj_in": {}, "done": {}, "ids": np.asarray(ids, dtype=np.uint32)}
         self._materialised = set()
+        self._pending_state = {}
         if mode == "commands":
             steps, i = [], 0
             while i < len(self.cmds):  # consecutive commands of one node (pruned sub-waves)
@@ -292,6 +339,7 @@ class PlanChecker:
                 self._after(members, True, state, tag)
                 self._progress(tag, mode, r, len(self.runs))
         assert not state["proj_in"], f"projections never completed: {sorted(state['proj_in'])}"
+        assert not self._pending_state, f"folded states never copied back: {sorted(self._pending_state)}"
         self.log(f"[{tag}] {mode}: checked " + ", ".join(
             f"{k} x{n}" + (f" (worst {self.worst[k]:.2e})" if k in self.worst else "")
             for k, n in sorted(self.checked.items())))

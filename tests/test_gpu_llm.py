@@ -394,9 +394,11 @@ def test_grouped_launches_match_per_wave(wavec, tuning, decode):
 def test_folded_multiplies_match_unfolded(wavec, tuning):
     """Decode plans fold the element-wise multiplies (k*v, q*(k*v), g*u) into the gathers of the
     narrow MFMA waves that read the products, and the RMSNorms after projections into their
-    producers (exact sums of squares per tile) and readers (normalising gathers); ids and logits
-    of several decode steps are bit-identical to the plan that launches every multiply and
-    norm (tuning switch fuse=0)."""
+    producers (exact sums of squares per tile) and readers (normalising gathers; for the norms
+    that run the decode token shift, normalising and shifting gathers whose shifted state is
+    copied back by the next launch); ids, logits and token-shift states of several decode steps
+    are bit-identical to the plan that launches every multiply and norm (tuning switch
+    fuse=0)."""
     spec = TINY
     steps = 4
     wts = synth.llm_weights(spec)
@@ -417,17 +419,20 @@ def test_folded_multiplies_match_unfolded(wavec, tuning):
     shifts = [a for a in rep["aux"] if a["fused"] and a["type"] == "TOKEN_SHIFT_1D"]
     norms = [a for a in rep["aux"] if a["type"] == "RMSNORM_1D"]
     norm_folded = [a for a in norms if a["fused"]]
+    norm_shifted = [a for a in norm_folded if "token shift" in a["fuse_note"]]
     norm_scaled = [a for a in norms if not a["fused"] and "sums of squares stored" in a["fuse_note"]]
     prods = sorted({w["xprod"] for w in rep["waves"]})
     _log(f"[fold] {len(fused)} multiplies folded, {len(shifts)} token shifts run by their "
-         f"RMSNorm, {len(norm_folded)} RMSNorms folded into their readers, "
+         f"RMSNorm, {len(norm_folded)} RMSNorms folded into their readers "
+         f"({len(norm_shifted)} with their token shift), "
          f"{len(norm_scaled)} run with their producers' scales, xprod kinds {prods}, "
          f"{rep['launches_per_run']} vs {plans['launched'].exec_report()['launches_per_run']} "
          "launches per run")
-    assert len(fused) == 3 * spec.layers and prods == [0, 2, 3, 4] and len(shifts) == spec.layers
-    # every layer's second norm and the final norm fold; the first norm of layers 1.. (after a
-    # projection; layer 0's follows the embedding) takes its scales from the producers
-    assert len(norm_folded) == spec.layers + 1 and len(norm_scaled) == spec.layers - 1
+    assert len(fused) == 3 * spec.layers and prods == [0, 2, 3, 4, 5] and len(shifts) == spec.layers
+    # every layer's second norm and the final norm fold; so does the first norm of layers 1..
+    # (after a projection; layer 0's follows the embedding) with its token shift
+    assert len(norm_folded) == 2 * spec.layers and len(norm_shifted) == spec.layers - 1
+    assert not norm_scaled
     assert not any(a["fused"] for a in plans["launched"].exec_report()["aux"])
     R = spec.requests
     pre.set_ids(np.random.default_rng(5).integers(0, spec.vocab, R * spec.prompt))
@@ -437,17 +442,23 @@ def test_folded_multiplies_match_unfolded(wavec, tuning):
     for mode, p in plans.items():
         synth.llm_handoff(spec, pre, p)
         hd = next(c for c in p.cmds if c["name"].split("/")[0] == "head")
-        ids, logits = [], []
+        ids, logits, states = [], [], []
+        shifts_of = [c for c in p.cmds if c["type"] == "TOKEN_SHIFT_1D"]
         for _ in range(steps):
             p.execute(1)
             ids.append(p.get_ids(R))
             # token columns past the plan's token count are unspecified (the narrow kernels
             # compute 16 columns; a folded norm scales all 16, the norm kernel whole octets)
             logits.append(p.read_canvas(int(hd["y_off"]), spec.vocab * 64).reshape(-1, 64)[:, :R])
-        out[mode] = (np.stack(ids), np.stack(logits))
+            states.append(np.stack([
+                p.read_canvas(int(c["state_off"]), spec.d * (spec.rf - 1) * 64).reshape(-1, 64)
+                for c in shifts_of]))
+        out[mode] = (np.stack(ids), np.stack(logits), np.stack(states))
     assert head is not None
     assert np.array_equal(out["folded"][0], out["launched"][0])
     assert np.array_equal(out["folded"][1], out["launched"][1])
+    # the whole state rows (columns past R are carried unchanged by both)
+    assert np.array_equal(out["folded"][2], out["launched"][2])
 
 
 def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
