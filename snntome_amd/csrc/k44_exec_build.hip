@@ -177,14 +177,18 @@ void K44GpuExecutorState::configure_mfma(const K44ExecCmd &c, WaveExec &wx, cons
         uint32_t want;
         if (cl >= 64u) {
             // Tiles of whole 16-neuron blocks per wave: chunks of any length, streamed
-            // in 16-k-step sub-chunks.  Chunks of at most 48 k-steps; split further, down
+            // in 16-k-step sub-chunks.  Chunks of at most 32 k-steps; split further, down
             // to 16 k-steps, until the wave has ~64 workgroups (~128 when a second kernel
             // reduces the partials).  Measured on config-5 decode (ms per step, graph
             // replays, alternated in one process): partials reduced by the tile's last
             // workgroup 0.869 at 64 workgroups, 0.889 at 32, 0.941 at 128, 0.968 unsplit
-            // beyond 48 k-steps; reduced by the epilogue kernel 0.928 at 128 or 64.
+            // beyond 48 k-steps; reduced by the epilogue kernel 0.928 at 128 or 64.  With
+            // the folded norms and token shifts, at most 32 k-steps per chunk: 0.7685 against
+            // 0.7896 at 48, 0.787 at 40, 0.829 at 24, 0.841 at 16 (the down projections'
+            // 96-k-step contractions in 3 chunks instead of 2: each workgroup's weights two
+            // 16-k-step round trips instead of three).
             const int ce = tune(Tune::NarrowChunk), cw = tune(Tune::NarrowWgs);
-            const uint32_t cmax = ce > 0 ? (uint32_t)std::max(16, ce) : 48u;
+            const uint32_t cmax = ce > 0 ? (uint32_t)std::max(16, ce) : 32u;
             const uint32_t wgs =
                 cw > 0 ? (uint32_t)cw : (tune(Tune::NarrowReduce) != 0 ? 64u : 128u);
             want = (ksteps + cmax - 1u) / cmax;

@@ -220,8 +220,9 @@ def test_dma_ring_matches_register_staged(wavec, orc, tuning, nt, S, K, tiles, t
 def test_narrow_long_chunks_many_tiles(wavec, orc, tuning, K, tokens):
     """Waves of >= 128 64-neuron tiles over <= 16 tokens: contraction chunks of several 16-k-step
     sub-chunks through two LDS buffers, fused epilogue when one chunk covers the contraction
-    (K = 2, 3: 32 / 48 k-steps), split-K partials plus the epilogue kernel otherwise (K = 7:
-    112 k-steps); within tolerance of the oracle and of the wide kernel."""
+    (K = 2: 32 k-steps), split-K partials reduced by each tile's last workgroup otherwise
+    (K = 3, 7: 48 / 112 k-steps in chunks of at most 32); within tolerance of the oracle and of
+    the wide kernel."""
     rng = np.random.default_rng(K * 100 + tokens)
     S, nt, tiles, C = 512, 64, 130, 16384  # residual rows: cout <= C
     starts = (rng.integers(0, C // S, size=(tiles, K)) * S).astype(np.uint32)
@@ -240,7 +241,7 @@ def test_narrow_long_chunks_many_tiles(wavec, orc, tuning, K, tokens):
         rep = plan.exec_report()["waves"][0]
         assert rep["path"] == ("mfma_tile" if mode == "wide" else "mfma_narrow"), rep
         if mode == "narrow":
-            assert (rep["ksplit"] > 1) == (K * S // 32 > 48), rep
+            assert (rep["ksplit"] > 1) == (K * S // 32 > 32), rep
         plan.fill_input_uniform(4)
         plan.execute(1)
         st = stride_of(tokens)
