@@ -2,6 +2,7 @@
 against the CPU restatement on the inputs the device itself read, the whole prefill against the
 oracle run end to end, prefill -> decode hand-over, decode steps, and HIP-graph replay with the
 device-side id history."""
+import dataclasses
 import numpy as np
 import pytest
 
@@ -391,15 +392,16 @@ def test_grouped_launches_match_per_wave(wavec, tuning, decode):
     assert np.array_equal(out["grouped_ids"], out["alone_ids"])
 
 
-def test_folded_multiplies_match_unfolded(wavec, tuning):
+@pytest.mark.parametrize("rf,requests", [(4, 2), (3, 9), (2, 16)])
+def test_folded_multiplies_match_unfolded(wavec, tuning, rf, requests):
     """Decode plans fold the element-wise multiplies (k*v, q*(k*v), g*u) into the gathers of the
     narrow MFMA waves that read the products, and the RMSNorms after projections into their
     producers (exact sums of squares per tile) and readers (normalising gathers; for the norms
     that run the decode token shift, normalising and shifting gathers whose shifted state is
     copied back by the next launch); ids, logits and token-shift states of several decode steps
     are bit-identical to the plan that launches every multiply and norm (tuning switch
-    fuse=0)."""
-    spec = TINY
+    fuse=0).  Receptive fields 2-4 (state rows 1-3) and batches of 2, 9 and 16 requests."""
+    spec = dataclasses.replace(TINY, rf=rf, requests=requests)
     steps = 4
     wts = synth.llm_weights(spec)
     pre = synth.build_llm_graph(spec, wts, decode=False, wavec_mod=wavec).compile()
