@@ -43,8 +43,12 @@ void K44GpuExecutorState::launch_aux(const AuxExec &a, bool whole) {
                                            a.decode ? 1 : 0, stream));
         break;
     case K44CmdType::EMBED_1D:
-        K44_HIP(k44dev::launch_embed(cv + a.y_off, a.table.p, ids.p, a.D, a.vocab, a.stride,
-                                     a.tokens, stream));
+        K44_HIP(k44dev::launch_embed(
+            cv + a.y_off, a.table.p, ids.p, a.D, a.vocab, a.stride, a.tokens, stream,
+            whole && a.slot_fold != SIZE_MAX
+                ? reinterpret_cast<uint64_t *>(norm_slots.p) +
+                      (norm_folds[a.slot_fold].slot0 + a.slot_tile0) * 32u
+                : nullptr));
         break;
     case K44CmdType::S2D_2X2:
         K44_HIP(k44dev::launch_s2d(cv + a.y_off, cv + a.src_off, a.C, a.pin, a.pout, stream));

@@ -939,13 +939,24 @@ void K44GpuExecutorState::fuse_norms() {
         const Rng Y(N.y_off, N.y_off + (uint64_t)N.D * N.stride);
         // producers: walking back, every writer into X until each row is covered
         std::vector<size_t> prods;
+        size_t prod_embed = SIZE_MAX;  // or the decode embedding that writes all of X
         std::vector<uint8_t> row_seen(N.D, 0u);
         uint32_t covered = 0;
         bool ok = true;
         for (size_t p = i; p-- > 0 && ok && covered < N.D;) {
             if (!ranges_overlap(wr[p], Ranges{X})) continue;
             if (!ops[p].first) {
-                ok = false;
+                const AuxExec &E = *aux[ops[p].second];
+                // (k44_embed_vec_kernel's slot form: one 64-token block of <= 16 tokens, 64-
+                // channel blocks, 16-byte rows; not with the persistent launch)
+                ok = covered == 0u && E.type == K44CmdType::EMBED_1D && !E.fused &&
+                     E.y_off == X.first && E.D == N.D && E.stride == 64u && N.stride == 64u &&
+                     E.tokens <= 16u && E.tokens > 0u && E.D % 64u == 0u && E.y_off % 8u == 0u &&
+                     E.slot_fold == SIZE_MAX && tune(Tune::Program) != 1;
+                if (ok) {
+                    prod_embed = ops[p].second;
+                    covered = N.D;
+                }
                 break;
             }
             const WaveExec &w = *waves[ops[p].second];
@@ -969,7 +980,7 @@ void K44GpuExecutorState::fuse_norms() {
             }
             if (ok) prods.push_back(ops[p].second);
         }
-        if (!ok || covered != N.D || prods.empty()) continue;
+        if (!ok || covered != N.D || (prods.empty() && prod_embed == SIZE_MAX)) continue;
         // consumers (a norm without a fused shift): readers of Y until overwritten
         std::vector<size_t> cons;
         bool consume = N.shift_with == SIZE_MAX;
@@ -978,6 +989,7 @@ void K44GpuExecutorState::fuse_norms() {
         std::vector<std::vector<uint64_t>> owns;
         const bool shifted =
             !consume && tune(Tune::Program) != 1 &&
+            prod_embed == SIZE_MAX &&
             fold_shift(i, X, Y, rd, wr, out_rng, cons, refresher, carrier, owns);
         if (consume) {
             size_t last = i;
@@ -1013,6 +1025,12 @@ void K44GpuExecutorState::fuse_norms() {
             w.norm_tile0 = f.tiles;
             f.tiles += w.rows;
             w.why += "; its tiles form the sums of squares of a folded RMSNorm";
+        }
+        if (prod_embed != SIZE_MAX) {
+            AuxExec &E = *aux[prod_embed];
+            E.slot_fold = norm_folds.size();
+            E.slot_tile0 = f.tiles;
+            f.tiles += E.D / 64u;
         }
         f.consumers = consume || shifted;
         N.norm_fold = norm_folds.size();

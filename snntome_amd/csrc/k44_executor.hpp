@@ -206,6 +206,10 @@ struct AuxExec {
                          // run by the RMSNorm before it (not launched)
     size_t shift_with = SIZE_MAX;  // RMSNORM_1D: the decode token shift it runs (whole plans)
     size_t norm_fold = SIZE_MAX;   // RMSNORM_1D: its scales come from the producers' sums
+    // EMBED_1D (decode): the fold whose producer it is (it stores the sums of squares of its
+    // 64-channel blocks from slot slot_tile0 of the fold on)
+    size_t slot_fold = SIZE_MAX;
+    uint32_t slot_tile0 = 0;
     // SWIGLU_MUL_1D y = other * q where q = b * c is an inner multiply only this one reads:
     // whole plans run both as y = fp16(other * fp16(b * c)) (the inner one is not launched).
     size_t chain_inner = SIZE_MAX;

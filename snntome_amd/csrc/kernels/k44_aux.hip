@@ -650,11 +650,14 @@ __global__ __launch_bounds__(256) void k44_embed_kernel(__half *__restrict__ y,
 // The same gather with 16-byte accesses (D % 8 == 0, 16-byte aligned table and output): a
 // thread loads 8 channels of one token's row and stores 8 tokens of one channel, every load
 // issued before the first wait (ids and rows clamped into range, invalid ones zeroed after).
+// slots (decode, see launch_embed): tokens 0..15 of the workgroup's 64 channels summed
+// squared exactly by the 8 threads of each token (threads 0..127), over lanes xor 1, 2, 4.
 __global__ __launch_bounds__(256) void k44_embed_vec_kernel(__half *__restrict__ y,
                                                             const __half *__restrict__ table,
                                                             const uint32_t *__restrict__ ids,
                                                             uint32_t D, uint32_t vocab,
-                                                            uint32_t stride, uint32_t tokens) {
+                                                            uint32_t stride, uint32_t tokens,
+                                                            uint64_t *__restrict__ slots) {
     constexpr uint32_t PITCH = 72u;  // halves per token row: 16-byte rows, spread banks
     __shared__ __attribute__((aligned(16))) __half tile[64 * PITCH];
     const uint32_t t0 = blockIdx.x * 64u, c0 = blockIdx.y * 64u;
@@ -675,6 +678,29 @@ __global__ __launch_bounds__(256) void k44_embed_vec_kernel(__half *__restrict__
         const uint32_t q = threadIdx.x + (uint32_t)r * 256u;
         *reinterpret_cast<uint4 *>(&tile[(q >> 3) * PITCH + (q & 7u) * 8u]) =
             ok[r] ? v[r] : uint4{0u, 0u, 0u, 0u};
+    }
+    if (slots && threadIdx.x < 128u) {  // waves 0, 1: tokens 0..15 (uniform per wave)
+        const uint4 o = ok[0] ? v[0] : uint4{0u, 0u, 0u, 0u};
+        SumSq s = sumsq_zero();
+        const uint32_t w4[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sumsq_add(s, w4[k >> 1] >> (16 * (k & 1)));
+        s = sumsq_norm(s);
+#pragma unroll
+        for (int m = 1; m < 8; m <<= 1) {
+            SumSq x;
+            x.l0 = (uint32_t)__shfl_xor((int)(uint32_t)s.l0, m, 64);
+            x.l1 = (uint32_t)__shfl_xor((int)(uint32_t)s.l1, m, 64);
+            x.l2 = (uint32_t)__shfl_xor((int)(uint32_t)s.l2, m, 64);
+            x.sp = (uint32_t)__shfl_xor((int)s.sp, m, 64);
+            sumsq_merge(s, x);
+            s = sumsq_norm(s);
+        }
+        if ((threadIdx.x & 7u) == 0u) {
+            uint64_t *sl = slots + ((uint64_t)blockIdx.y * 16u + (threadIdx.x >> 3)) * 2u;
+            sl[0] = s.l0 | (s.l1 << 32);
+            sl[1] = (uint64_t)(uint32_t)s.l2 | ((uint64_t)s.sp << 32);
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -991,13 +1017,18 @@ hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __ha
 }
 
 hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uint32_t D,
-                        uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream) {
+                        uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream,
+                        uint64_t *slots) {
     if (stride % 64u != 0u || D == 0u) return hipErrorInvalidValue;
     const dim3 grid(stride / 64u, (D + 63u) / 64u);
-    if (tokens > 0u && D % 8u == 0u && reinterpret_cast<uintptr_t>(table) % 16u == 0u &&
-        reinterpret_cast<uintptr_t>(y) % 16u == 0u)
+    const bool vec = tokens > 0u && D % 8u == 0u && reinterpret_cast<uintptr_t>(table) % 16u == 0u &&
+                     reinterpret_cast<uintptr_t>(y) % 16u == 0u;
+    // slots: the vector kernel over one 64-token block with at most 16 tokens
+    if (slots && (!vec || stride != 64u || tokens > 16u || D % 64u != 0u))
+        return hipErrorInvalidValue;
+    if (vec)
         hipLaunchKernelGGL(k44_embed_vec_kernel, grid, dim3(256), 0, stream, y, table, ids, D,
-                           vocab, stride, tokens);
+                           vocab, stride, tokens, slots);
     else
         hipLaunchKernelGGL(k44_embed_kernel, grid, dim3(256), 0, stream, y, table, ids, D, vocab,
                            stride, tokens);

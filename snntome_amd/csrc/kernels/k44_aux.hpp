@@ -61,8 +61,13 @@ hipError_t launch_mul3(__half *y, const __half *a, const __half *b, const __half
 hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __half *state,
                               uint32_t D, uint32_t stride, uint32_t tokens, uint32_t rf,
                               uint32_t seq_len, int decode, hipStream_t stream);
+// slots (nullable; decode: at most 16 tokens, D % 64 == 0, 16-byte aligned table and output):
+// every 64-channel block b of the output also stores the exact per-token sums of squares of
+// the values it stored (k44_sumsq.hpp) at slots[(b * 16 + t) * 2 + 0 / 1] (limbs 0 | 1, limb 2
+// | inf / NaN flags), the producer side of an RMSNorm folded into the readers of y.
 hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uint32_t D,
-                        uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream);
+                        uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream,
+                        uint64_t *slots = nullptr);
 // history (nullable): ids are also stored at history[*step_ctr][t] while *step_ctr <
 // hist_steps, and *step_ctr is incremented after the argmax (device-side, graph-safe).
 // Two passes: per-chunk (value, index) partials in `scratch` (argmax_scratch_floats(V, stride)

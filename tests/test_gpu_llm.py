@@ -432,9 +432,10 @@ def test_folded_multiplies_match_unfolded(wavec, tuning, rf, requests):
          "launches per run")
     assert len(fused) == 3 * spec.layers and prods == [0, 2, 3, 4, 5] and len(shifts) == spec.layers
     # every layer's second norm and the final norm fold; so does the first norm of layers 1..
-    # (after a projection; layer 0's follows the embedding) with its token shift
+    # (after a projection) with its token shift; layer 0's (after the embedding, which stores
+    # the sums of squares) runs with those sums
     assert len(norm_folded) == 2 * spec.layers and len(norm_shifted) == spec.layers - 1
-    assert not norm_scaled
+    assert len(norm_scaled) == 1
     assert not any(a["fused"] for a in plans["launched"].exec_report()["aux"])
     R = spec.requests
     pre.set_ids(np.random.default_rng(5).integers(0, spec.vocab, R * spec.prompt))
