@@ -277,10 +277,14 @@ int wavec_gpu_read_canvas_2d(void *handle, unsigned long long elem_off, unsigned
  *   waves of 64/128-neuron tiles reduce their partials in a second kernel / in the last
  *   workgroup of each tile (the automatic choice); "dma_prod" 0 | 1 LDS-ring MFMA waves of
  *   32/64-neuron tiles load and multiply in every wave / issue their loads from producer waves
- *   (4-stage ring).
+ *   (4-stage ring); "program" 0 | 1 kernel-by-kernel (automatic) / one persistent launch per
+ *   decode-sized execution; "prog_spin_ms" >= 0 that launch's wait limit; "prog_trace" 0 | 1
+ *   its per-item timestamps; "narrow_pre" 0 | 1 narrow waves read their weights' address and
+ *   geometry from their descriptors / from preloaded kernel arguments (automatic).
  * wavec_set_tuning returns -1 (with a message) for an unknown key or a value the key does not
  * honour: -1 is always accepted; "dma_stages" takes 2 | 4, "ksplit" 1 | 4, "xcd_order" 0..2,
- * "t64_ring" 0..2, "narrow_chunk" >= 16, "narrow_wgs" >= 1, every other key 0 | 1.  wavec_get_tuning returns the
+ * "t64_ring" 0..2, "narrow_chunk" >= 16, "narrow_wgs" >= 1, "prog_spin_ms" >= 0, every
+ * other key 0 | 1.  wavec_get_tuning returns the
  * value or -2 for an unknown key. */
 int wavec_set_tuning(const char *key, int value);
 int wavec_get_tuning(const char *key);

@@ -1046,8 +1046,10 @@ void K44GpuExecutorState::upload_mfma_descriptors() {
         if (!w.mfma) continue;
         w.items = w.rows * (w.narrow ? 1u : w.tokens / w.mt) * w.kgroups;
         w.epi_items = epi_workgroups(w);
-        w.one_args.upload({mfma_args(w, scratch.p, false)});
+        const k44dev::MfmaTileArgs one = mfma_args(w, scratch.p, false);
+        w.one_args.upload({one});
         w.one_start.upload({0u, w.items});
+        w.one_pre = narrow_pre({one});
     }
     for (auto &gp : groups) {
         MfmaGroupExec &g = *gp;
@@ -1076,7 +1078,20 @@ void K44GpuExecutorState::upload_mfma_descriptors() {
         if (xcd_order == 2u) check_balanced_order(start);
         g.args.upload(args);
         g.start.upload(start);
+        g.pre = narrow_pre(args);
     }
+}
+
+// The first three descriptors' weights and geometry for the narrow kernels' preloaded
+// arguments (tuning key narrow_pre 0: none, every wave reads its descriptor).
+k44dev::NarrowPre K44GpuExecutorState::narrow_pre(const std::vector<k44dev::MfmaTileArgs> &args) {
+    k44dev::NarrowPre p;
+    if (tune(Tune::NarrowPre) == 0) return p;
+    for (size_t i = 0; i < args.size() && i < 3u; ++i) {
+        p.w[i] = args[i].Wf;
+        p.geo[i] = k44dev::narrow_geo(args[i]);
+    }
+    return p;
 }
 
 // Stages (k-steps for the narrow kernels) one work item of an MFMA wave runs.

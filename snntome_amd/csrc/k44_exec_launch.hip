@@ -83,9 +83,10 @@ void K44GpuExecutorState::launch_aux(const AuxExec &a, bool whole) {
 
 void K44GpuExecutorState::launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
                        uint32_t items, uint32_t epi_items, bool dma, const k44dev::DmaShape &ds,
-                       uint32_t prod, uint32_t max_items, bool mis) {
+                       uint32_t prod, uint32_t max_items, bool mis,
+                       const k44dev::NarrowPre &pre) {
     if (mt == 16u)  // narrow (<= 16 tokens)
-        K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream, prod, max_items));
+        K44_HIP(k44dev::launch_mfma_narrow(d, nt, items, stream, prod, max_items, pre));
     else if (dma)
         K44_HIP(k44dev::launch_mfma_dma(d, nt, items, stream, ds));
     else
@@ -96,13 +97,13 @@ void K44GpuExecutorState::launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t
 void K44GpuExecutorState::launch_mfma(const WaveExec &w) {
     const k44dev::MfmaGroup d{w.one_args.p, w.one_start.p, 1u, xcd_order};
     launch_mfma_group(d, w.cluster, w.mt, w.rows_per_stage, w.items, w.epi_items, w.dma,
-                      w.dshape, 0u, w.items, w.mis);
+                      w.dshape, 0u, w.items, w.mis, w.one_pre);
 }
 
 void K44GpuExecutorState::launch_group(const MfmaGroupExec &g) {
     const k44dev::MfmaGroup d{g.args.p, g.start.p, (uint32_t)g.members.size(), xcd_order};
     launch_mfma_group(d, g.nt, g.mt, g.rows, g.items, g.epi_items, g.dma, g.dshape,
-                      g.prod, g.max_items, g.mis);
+                      g.prod, g.max_items, g.mis, g.pre);
 }
 
 void K44GpuExecutorState::launch_wave(const WaveExec &w) {

@@ -151,6 +151,7 @@ struct WaveExec {
     // MFMA: descriptor of this wave alone (command-by-command execution).
     DevBuf<k44dev::MfmaTileArgs> one_args;
     DevBuf<uint32_t> one_start;
+    k44dev::NarrowPre one_pre;  // narrow kernels: weights and geometry as kernel arguments
     uint32_t items = 0, epi_items = 0;
 };
 
@@ -164,6 +165,7 @@ struct MfmaGroupExec {
     size_t part_floats = 0;
     DevBuf<k44dev::MfmaTileArgs> args;
     DevBuf<uint32_t> start;
+    k44dev::NarrowPre pre;  // narrow kernels: the first three members' weights and geometry
 };
 
 // Sorted, merged [lo, hi) element ranges.
@@ -343,6 +345,7 @@ struct K44GpuExecutorState {
     static uint32_t epi_workgroups(const WaveExec &w);
     void upload_mfma_descriptors();
     static uint32_t item_stages(const WaveExec &w);
+    static k44dev::NarrowPre narrow_pre(const std::vector<k44dev::MfmaTileArgs> &args);
     static void check_balanced_order(const std::vector<uint32_t> &start);
 
     // Fusion and scheduling (k44_exec_schedule.hip): folded multiplies and RMSNorms, the
@@ -370,7 +373,8 @@ struct K44GpuExecutorState {
     void launch_aux(const AuxExec &a, bool whole = false);
     void launch_mfma_group(const k44dev::MfmaGroup &d, uint32_t nt, uint32_t mt, uint32_t rows,
                            uint32_t items, uint32_t epi_items, bool dma, const k44dev::DmaShape &ds,
-                           uint32_t prod, uint32_t max_items, bool mis);
+                           uint32_t prod, uint32_t max_items, bool mis,
+                           const k44dev::NarrowPre &pre);
     void launch_mfma(const WaveExec &w);
     void launch_group(const MfmaGroupExec &g);
     void launch_wave(const WaveExec &w);

@@ -41,6 +41,9 @@ enum class Tune : int {
                    //                  automatic: 1000), past which the launch is abandoned
     ProgTrace,     // "prog_trace":    1 = the persistent launch records per-item timestamps
                    //                  (wavec_gpu_program_trace)
+    NarrowPre,     // "narrow_pre":    0 = narrow waves read their weights' address and geometry
+                   //                  from their descriptors; automatic and 1: the first three
+                   //                  waves of a launch take them as preloaded kernel arguments
     Count
 };
 

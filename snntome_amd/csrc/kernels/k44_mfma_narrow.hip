@@ -403,9 +403,13 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(K44_GROUP_PARAMS) 
 // ms/step against refills clamped to the chunk's last k-step (re-reads of it); two sub-chunks
 // of fragments in flight per wave instead of one: 0.869 ms/step (each wave's first gather then
 // waits behind twice the weight bytes).
+// geo0..2 / pw0..2: NarrowPre (the first three waves' geometry and weights).  The parameters
+// fill the 14 SGPRs that gfx950 preloads (the group's XCD order is not used here).
 template <int NT, int PROD, bool BYY>
-__global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PARAMS) {
-    K44_GROUP_BIND;
+__global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
+    const MfmaTileArgs *grp_waves, const uint32_t *grp_start, uint32_t grp_n, uint32_t geo0,
+    uint32_t geo1, uint32_t geo2, const void *pw0, const void *pw1, const void *pw2) {
+    const MfmaGroup grp{grp_waves, grp_start, grp_n, 0u};
     constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16, AF = SUBK;
     static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][NARROW_MAX_ROWS][NARROW_PITCH];
@@ -414,26 +418,33 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
     if constexpr (BYY) {
         w = blockIdx.y;
         local = blockIdx.x;
+    } else if (grp.n == 1u) {
+        local = blockIdx.x;
     } else {
         while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
         local = blockIdx.x - grp.start[w];
     }
-    const MfmaTileArgs a = grp.waves[w];
-    if (BYY && local >= a.tiles * a.kgroups) return;
-    const uint32_t tile = local % a.tiles, zgroup = local / a.tiles;
-    const uint32_t ks_begin = zgroup * a.stage_chunk;
-    const uint32_t ks_end = min(a.ksteps, ks_begin + a.stage_chunk);
-    const uint32_t nsub = (ks_end - ks_begin + SUBK - 1u) / SUBK;
-
+    // The wave's weights and geometry from the preloaded arguments where the launch gives them:
+    // its first weight loads are then issued before the descriptor is read (the scheduling
+    // barrier below keeps the descriptor's scalar loads, and their waits, after them).
+    const uint32_t geo = w == 0u ? geo0 : w == 1u ? geo1 : w == 2u ? geo2 : 0u;
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const kconst_u64 *segr = (const kconst_u64 *)(a.seg) + (uint64_t)tile * a.K;
-    typedef const __attribute__((address_space(1))) u4_t gu4_t;
+    uint32_t tiles, ksteps, chunk, kgroups, tile, zgroup, ks_begin, ks_end;
+    __amdgpu_buffer_rsrc_t wr;
     // the chunk's A fragments [k-step - ks_begin][16-block][lane][8]: 1 KiB per k-step and block
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(reinterpret_cast<const h8_t *>(a.Wf) +
-                 ((uint64_t)tile * a.ksteps + ks_begin) * NB * 64u),
-        (short)0, (int)((ks_end - ks_begin) * (uint32_t)NB * 1024u), 0x00020000);
+    auto geometry = [&](const void *wbase) {
+        if (BYY && local >= tiles * kgroups) return false;
+        tile = local % tiles;
+        zgroup = local / tiles;
+        ks_begin = zgroup * chunk;
+        ks_end = min(ksteps, ks_begin + chunk);
+        wr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(reinterpret_cast<const h8_t *>(wbase) +
+                     ((uint64_t)tile * ksteps + ks_begin) * NB * 64u),
+            (short)0, (int)((ks_end - ks_begin) * (uint32_t)NB * 1024u), 0x00020000);
+        return true;
+    };
     // k-step kk of the chunk (relative to ks_begin; past the chunk: zeros, no access), read
     // nontemporally (weights are read once per step)
     auto load_a = [&](uint32_t kk, h8_t (&f)[BPW]) {
@@ -444,6 +455,28 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
                           wr, ((kk * (uint32_t)NB + (uint32_t)(wave + 4 * i)) * 64u + (uint32_t)lane) * 16u,
                           0, 2));
     };
+    h8_t af[AF][BPW];
+    if (geo != 0u) {
+        tiles = geo & 0x7ffu;
+        ksteps = (geo >> 11) & 0xffu;
+        chunk = (geo >> 19) & 0xffu;
+        kgroups = geo >> 27;
+        if (!geometry(w == 0u ? pw0 : w == 1u ? pw1 : pw2)) return;
+#pragma unroll
+        for (int u = 0; u < AF; ++u) load_a((uint32_t)u, af[u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const MfmaTileArgs a = grp.waves[w];
+    if (geo == 0u) {
+        tiles = a.tiles;
+        ksteps = a.ksteps;
+        chunk = a.stage_chunk;
+        kgroups = a.kgroups;
+        if (!geometry(a.Wf)) return;
+    }
+    const uint32_t nsub = (ks_end - ks_begin + SUBK - 1u) / SUBK;
+    const kconst_u64 *segr = (const kconst_u64 *)(a.seg) + (uint64_t)tile * a.K;
+    typedef const __attribute__((address_space(1))) u4_t gu4_t;
 
     // X rows of sub-chunk s: wave pass q covers 32 rows starting at a multiple of 32 (one
     // segment, S % 32 == 0: wave-uniform start); passes past the sub-chunk re-read its last
@@ -604,12 +637,14 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
 
     // a folded norm's producer slots first: they arrive ahead of the weights and the gather
     // (loads complete in issue order), so the scales are formed while those are in flight
+    // (after the weights where those were issued from the preloaded arguments)
     SlotLoads<16u> slp;
     if constexpr (NORM)
         rms_slots_issue<16u>(reinterpret_cast<const uint64_t *>(a.xslots), a.xslots_n, 0u, slp);
-    h8_t af[AF][BPW];
+    if (geo == 0u) {
 #pragma unroll
-    for (int u = 0; u < AF; ++u) load_a((uint32_t)u, af[u]);
+        for (int u = 0; u < AF; ++u) load_a((uint32_t)u, af[u]);
+    }
     u4_t xv[XQ], xb[XQ], xc[XQ];
     gather(0u, xv, xb, xc);
     // Lane holds C[4g + i][lane & 15]: neuron 16*blk + 4g + i, token lane & 15.  A workgroup
@@ -628,7 +663,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
     if (epi) narrow_epi_maps<BPW>(a, j0, cb, e);
     // A copy carried for an earlier launch (cp_rows): the thread's first 16 bytes loaded now,
     // stored after the contraction.
-    const uint32_t cpn = a.cp_rows * 2u, cpstep = a.tiles * a.kgroups * 256u;
+    const uint32_t cpn = a.cp_rows * 2u, cpstep = tiles * kgroups * 256u;
     const uint32_t cpe = local * 256u + (uint32_t)tid;
     auto cp_at = [&](const __half *base, uint32_t stride, uint32_t i) {
         return base + (uint64_t)(i >> 1) * stride + (i & 1u) * 8u;
@@ -705,7 +740,8 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(K44_GROUP_PAR
 }
 
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
-                              hipStream_t stream, uint32_t prod, uint32_t max_items) {
+                              hipStream_t stream, uint32_t prod, uint32_t max_items,
+                              const NarrowPre &pre) {
     if (prod != 0u && ((nt != 64u && nt != 128u) || (prod < 2u || prod > 5u)))
         return hipErrorInvalidValue;
     if (items == 0u) return hipSuccess;
@@ -714,11 +750,17 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
     // workgroups (max_items = the largest wave's workgroups; 0 = not known).
     const bool byy = max_items != 0u && 2ull * max_items * g.n <= 3ull * items;
     const dim3 grid_y(max_items, g.n);
+    // a wave past the group's count never selects its preloaded entry
+    NarrowPre p = pre;
+    for (uint32_t i = g.n; i < 3u; ++i) p.geo[i] = 0u;
+#define K44_PRE_ARGS g.waves, g.start, g.n, p.geo[0], p.geo[1], p.geo[2], p.w[0], p.w[1], p.w[2]
 #define K44_NL(N, P)                                                                               \
     if (byy)                                                                                       \
-        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, true>), grid_y, block, 0, stream, K44_GROUP_ARGS(g)); \
+        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, true>), grid_y, block, 0, stream, \
+                           K44_PRE_ARGS);                                                          \
     else                                                                                           \
-        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, false>), grid, block, 0, stream, K44_GROUP_ARGS(g));
+        hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, false>), grid, block, 0, stream,     \
+                           K44_PRE_ARGS);
     switch (nt) {
     case 16u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<16>, grid, block, 0, stream, K44_GROUP_ARGS(g)); break;
     case 32u: hipLaunchKernelGGL(k44_mfma_narrow_kernel<32>, grid, block, 0, stream, K44_GROUP_ARGS(g)); break;
@@ -751,6 +793,7 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
     default: return hipErrorInvalidValue;
     }
 #undef K44_NL
+#undef K44_PRE_ARGS
     return hipGetLastError();
 }
 

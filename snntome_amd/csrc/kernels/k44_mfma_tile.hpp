@@ -184,6 +184,22 @@ struct MfmaGroup {
 #define K44_GROUP_ARGS(g) (g).waves, (g).start, (g).n, (g).xcd_order
 #define K44_GROUP_BIND const MfmaGroup grp{grp_waves, grp_start, grp_n, grp_xcd}
 
+// Weights and contraction geometry of the first three waves of a narrow launch, passed as
+// scalar kernel arguments (preloaded into SGPRs like the group fields), so that a workgroup
+// issues its weight stream before its descriptor load has returned.  geo packs tiles (11
+// bits), ksteps (8), stage_chunk (8) and kgroups (5); 0 = the wave reads them from its
+// descriptor (more members, larger shapes, or the switch off).
+struct NarrowPre {
+    const void *w[3] = {nullptr, nullptr, nullptr};
+    uint32_t geo[3] = {0u, 0u, 0u};
+};
+inline uint32_t narrow_geo(const MfmaTileArgs &a) {
+    if (a.tiles == 0u || a.tiles >= 2048u || a.ksteps >= 256u || a.stage_chunk >= 256u ||
+        a.kgroups == 0u || a.kgroups >= 32u)
+        return 0u;
+    return a.tiles | (a.ksteps << 11) | (a.stage_chunk << 19) | (a.kgroups << 27);
+}
+
 // Per-wave shares of the 8 XCDs (xcd_order 2), host and device.  Workgroup b runs on XCD
 // x = b % 8 as that XCD's s-th workgroup, s = b / 8.  Every wave w of the group (items
 // [start[w], start[w+1]), cnt = 8q + r) gives each XCD a contiguous share of its items: q, plus
