@@ -359,9 +359,24 @@ def bench_llm(steps: int, warmup: int, eager: bool, no_cpu: bool = True) -> dict
     pre.set_ids(prompt)
     tw = time.perf_counter()
     warm_steps = 0
+    xcd_fallback = False
     while warm_steps < max(1, warmup) or time.perf_counter() - tw < WARMUP_MIN_S:
         pre.set_ids(prompt)
-        one_step()
+        try:
+            one_step()
+        except RuntimeError as e:
+            # XCD-local split-K meetings that found their chunks on different XCDs (the
+            # executor checks after every run): rebuild the decode plan without them.
+            if "narrow_local=0" not in str(e) or xcd_fallback:
+                raise
+            log(f"[bench] {e}; decode plan rebuilt with tuning narrow_local=0")
+            wavec.set_tuning("narrow_local", 0)
+            dec = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
+            dec.init_gpu()
+            dec.use_graph(not eager)
+            wavec.set_tuning("narrow_local", -1)
+            xcd_fallback = True
+            continue
         warm_steps += 1
         dec.sync()
     pre.sync()
@@ -397,6 +412,7 @@ def bench_llm(steps: int, warmup: int, eager: bool, no_cpu: bool = True) -> dict
             "S": spec.S, "clusters_kept": [spec.kept(spec.d), spec.kept(spec.ffn)],
             "tile": spec.tile, "token_shift_rf": spec.rf, "requests": R, "prompt": P,
             "decode_steps": D, "paths": paths, "hip_graphs": not eager,
+            "xcd_local_splitk": not xcd_fallback,
         },
         "warmup_ms": round(warm_ms, 1),
         "warmup_runs": warm_steps,

@@ -874,11 +874,19 @@ void K44GpuExecutorState::init(const K44WavePlan &plan) {
     canvas.alloc((plan.canvas_elems + kCanvasSlack + 63u) / 64u * 64u + fold_elems);
     if (scratch_need) scratch.alloc(scratch_need);
     {
-        size_t n_arrive = 0;
+        // Meetings through one XCD's L2 (the chunks of a tile 8 workgroups apart in launch
+        // order; partial offsets below 2 GiB), their counters one 128-byte line per tile.
+        bool need = false;
+        for (auto &wp : waves) need = need || wp->reduce_in_kernel;
+        if (need && tune(Tune::NarrowLocal) != 0) probe_xcd_placement();
+        n_arrive = 0;
         for (auto &wp : waves)
             if (wp->reduce_in_kernel) {
+                wp->red_local = xcd_local_ok &&
+                                (uint64_t)wp->kgroups * wp->cout * 64u < (1ull << 31);
+                any_local = any_local || wp->red_local;
                 wp->arrive_off = n_arrive;
-                n_arrive += wp->rows;
+                n_arrive += (size_t)wp->rows * (wp->red_local ? 32u : 1u);
             }
         if (n_arrive) {
             arrive.alloc(n_arrive);
@@ -964,7 +972,10 @@ k44dev::MfmaTileArgs K44GpuExecutorState::mfma_args(const WaveExec &w, float *pa
     else  // chunk in stages of rows_per_stage positions
         a.stage_chunk = w.kgroups > 1u ? w.stage_chunk : a.K * a.S / w.rows_per_stage;
     a.part = w.kgroups > 1u ? part : nullptr;
-    if (fused && w.reduce_in_kernel) a.arrive = arrive.p + w.arrive_off;
+    if (fused && w.reduce_in_kernel) {
+        a.arrive = arrive.p + w.arrive_off;
+        a.red_local = w.red_local ? 1u : 0u;
+    }
     if (fused && w.norm_fold != SIZE_MAX) {
         const NormFold &f = norm_folds[w.norm_fold];
         a.norm_part = norm_slots.p + (f.slot0 + w.norm_tile0) * 64u;
@@ -1064,13 +1075,20 @@ void K44GpuExecutorState::upload_mfma_descriptors() {
             std::stable_sort(order.begin(), order.end(), [&](size_t p, size_t q) {
                 return item_stages(*waves[p]) > item_stages(*waves[q]);
             });
+        // Narrow waves meeting XCD-locally number their items in groups of 8 tiles; with one in
+        // the group, every wave's items start at a multiple of 8 (positions past a wave's own
+        // items are idle).
+        bool local = false;
+        for (size_t m : order) local = local || waves[m]->red_local;
         for (size_t m : order) {
             const WaveExec &w = *waves[m];
             args.push_back(mfma_args(w, scratch.p ? scratch.p + off : nullptr, true));
             off += w.part_floats;
-            start.push_back(start.back() + w.items);
+            uint32_t it = w.narrow ? k44dev::narrow_items(w.rows, w.kgroups, w.red_local) : w.items;
+            if (local) it = (it + 7u) / 8u * 8u;
+            start.push_back(start.back() + it);
             if (!w.reduce_in_kernel) epi_max = std::max(epi_max, w.epi_items);
-            item_max = std::max(item_max, w.items);
+            item_max = std::max(item_max, it);
         }
         g.items = start.back();
         g.epi_items = epi_max;  // epilogue grid: epi_max x members
@@ -1080,6 +1098,43 @@ void K44GpuExecutorState::upload_mfma_descriptors() {
         g.start.upload(start);
         g.pre = narrow_pre(args);
     }
+}
+
+// Where workgroups run: probe launches of 4,096 and 1,001 workgroups record the XCD of each.
+// The XCD-local split-K meeting needs workgroups a multiple of 8 apart in one launch to share an
+// XCD (the round-robin dispatch over the 8 XCDs, or fewer in a partitioned mode).
+void K44GpuExecutorState::probe_xcd_placement() {
+    constexpr uint32_t n0 = 4096u, n1 = 1001u;
+    DevBuf<uint32_t> out;
+    out.alloc(n0 + n1);
+    K44_HIP(k44dev::launch_xcd_probe(out.p, n0, stream));
+    K44_HIP(k44dev::launch_xcd_probe(out.p + n0, n1, stream));
+    std::vector<uint32_t> h(n0 + n1);
+    K44_HIP(hipMemcpyAsync(h.data(), out.p, h.size() * 4u, hipMemcpyDeviceToHost, stream));
+    K44_HIP(hipStreamSynchronize(stream));
+    bool ok = true;
+    for (uint32_t b = 8; b < n0 && ok; ++b) ok = h[b] == h[b % 8u];
+    for (uint32_t b = 8; b < n1 && ok; ++b) ok = h[n0 + b] == h[n0 + b % 8u];
+    xcd_local_ok = ok;
+}
+
+// Every XCD-local meeting leaves its tile's arrival counter at zero; a counter left nonzero
+// means chunks of a tile ran on different XCDs and met no one.  Checked at each host
+// synchronisation of a whole-plan run (the counters are then zeroed again).
+void K44GpuExecutorState::check_placement() {
+    if (!any_local || !n_arrive) return;
+    std::vector<uint32_t> h(n_arrive);
+    K44_HIP(hipMemcpyAsync(h.data(), arrive.p, n_arrive * 4u, hipMemcpyDeviceToHost, stream));
+    K44_HIP(hipStreamSynchronize(stream));
+    size_t bad = 0;
+    for (uint32_t v : h) bad += v != 0u;
+    if (!bad) return;
+    K44_HIP(hipMemsetAsync(arrive.p, 0, n_arrive * 4u, stream));
+    K44_HIP(hipStreamSynchronize(stream));
+    throw std::runtime_error(std::to_string(bad) + " split-K arrival counters of XCD-local "
+                             "reductions were left nonzero (chunks of a tile ran on different "
+                             "XCDs); the outputs of that run are unreliable (tuning "
+                             "narrow_local=0 avoids these reductions)");
 }
 
 // The first three descriptors' weights and geometry for the narrow kernels' preloaded

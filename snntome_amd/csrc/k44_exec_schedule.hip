@@ -1218,6 +1218,7 @@ void K44GpuExecutorState::build_report() {
           << ", \"ring_producers\": " << (w.dma ? w.dshape.prod : 0u)
           << ", \"xprod\": " << w.xprod
           << ", \"reduce_in_kernel\": " << (w.reduce_in_kernel ? "true" : "false")
+          << ", \"reduce_xcd_local\": " << (w.red_local ? "true" : "false")
           << ", \"flops\": " << (long long)w.flops
           << ", \"effective_flops\": " << (long long)w.eff_flops
           << ", \"mapped\": " << (w.cmap.p ? "true" : "false")

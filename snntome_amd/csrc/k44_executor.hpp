@@ -123,6 +123,7 @@ struct WaveExec {
     // last workgroup of each tile (per-tile arrival counters at arrive + arrive_off) instead of
     // a second kernel; command-by-command launches keep the epilogue kernel.
     bool reduce_in_kernel = false;
+    bool red_local = false;  // that reduction through one XCD's L2 (MfmaTileArgs::red_local)
     size_t arrive_off = 0;
     // Folded RMSNorm (whole-plan runs): producer of the norm's input (fold index, first slot
     // of this wave's tiles among the fold's tiles), or consumer gathering the normalised rows
@@ -272,6 +273,10 @@ struct K44GpuExecutorState {
     // Per-tile arrival counters of the waves that reduce split-K in the launch (zeroed at init;
     // each launch leaves them at zero).
     DevBuf<uint32_t> arrive;
+    // XCD-local split-K meetings: set-up found workgroups 8 apart in launch order sharing an
+    // XCD; any_local: some wave meets that way (its counters are checked after each run).
+    bool xcd_local_ok = false, any_local = false;
+    size_t n_arrive = 0;
     // Folded RMSNorms (fuse_norms): per fold the producers' tile slots (16 tokens x 4 words
     // each: the exact sums of squares of the values the tile stored).
     struct NormFold {
@@ -346,6 +351,8 @@ struct K44GpuExecutorState {
     void upload_mfma_descriptors();
     static uint32_t item_stages(const WaveExec &w);
     static k44dev::NarrowPre narrow_pre(const std::vector<k44dev::MfmaTileArgs> &args);
+    void probe_xcd_placement();
+    void check_placement();
     static void check_balanced_order(const std::vector<uint32_t> &start);
 
     // Fusion and scheduling (k44_exec_schedule.hip): folded multiplies and RMSNorms, the

@@ -44,6 +44,11 @@ enum class Tune : int {
     NarrowPre,     // "narrow_pre":    0 = narrow waves read their weights' address and geometry
                    //                  from their descriptors; automatic and 1: the first three
                    //                  waves of a launch take them as preloaded kernel arguments
+    NarrowLocal,   // "narrow_local":  0 = split narrow waves reduced in the launch meet through
+                   //                  device-coherent memory; automatic and 1: through the L2 of
+                   //                  the XCD all chunks of a tile run on (items renumbered so
+                   //                  they are 8 workgroups apart), where set-up finds that
+                   //                  workgroups 8 apart share an XCD
     Count
 };
 

@@ -19,7 +19,7 @@ const char *const kTuneKeys[(int)Tune::Count] = {
     "path", "dma", "dma_stages", "nt", "splitk", "lane8", "ksplit", "stream_kernel", "narrow",
     "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring", "xcd_order",
     "narrow_wgs", "narrow_reduce", "dma_prod", "program", "prog_spin_ms", "prog_trace",
-    "narrow_pre"};
+    "narrow_pre", "narrow_local"};
 // Values each switch honours besides -1: a set of small values (bit v of `set`), or every
 // value >= `min` when `set` is 0.  Anything else is refused, so an A/B run cannot measure a
 // configuration other than the one it asked for.
@@ -53,6 +53,7 @@ const TuneValues kTuneValues[(int)Tune::Count] = {
     {0u, 0},           // prog_spin_ms >= 0
     {V01, 0},          // prog_trace
     {V01, 0},          // narrow_pre
+    {V01, 0},          // narrow_local
 };
 struct TuneInit {
     TuneInit() {
@@ -663,6 +664,7 @@ int wavec_gpu_execute(void *h, int iters, float *out_ms_per_iter) {
         K44_HIP(hipEventRecord(ex->ev1, ex->stream));
         K44_HIP(hipEventSynchronize(ex->ev1));
         ex->check_program();
+        ex->check_placement();
         float ms = 0.0f;
         K44_HIP(hipEventElapsedTime(&ms, ex->ev0, ex->ev1));
         if (out_ms_per_iter) *out_ms_per_iter = ms / (float)iters;
@@ -705,6 +707,7 @@ int wavec_gpu_sync(void *h) {
         if (!ex) throw std::runtime_error("wavec_gpu_init_plan has not succeeded for this handle");
         K44_HIP(hipStreamSynchronize(ex->stream));
         ex->check_program();
+        ex->check_placement();
         return 0;
     });
 }

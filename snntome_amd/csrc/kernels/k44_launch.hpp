@@ -60,6 +60,10 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items, h
                               uint32_t prod = 0, uint32_t max_items = 0,
                               const NarrowPre &pre = NarrowPre{});
 
+// out[b] = the XCD workgroup b of an n-workgroup launch ran on (set-up check of the narrow
+// kernels' XCD-local split-K meeting).
+hipError_t launch_xcd_probe(uint32_t *out, uint32_t n, hipStream_t stream);
+
 // Split-K second pass over the same group: grid epi_max x g.n (epi_max = the largest wave's
 // epilogue workgroups, ceil(cout * tokens / 4 / 256); 0: no wave of the group is split).
 hipError_t launch_splitk_epilogue(const MfmaGroup &g, uint32_t epi_max, hipStream_t stream);

@@ -163,6 +163,11 @@ __device__ __forceinline__ void narrow_norm_publish(const MfmaTileArgs &a, const
 // memset, so HIP-graph replays need no extra node).  Lane (g, t) holds C[4g + i][t] of BPW
 // 16-neuron blocks; its 4 values of block bi are contiguous in the partial layout
 // [z][cout/4][16][4]: index ((z * cout + j0) * 16 + 4 t + i).
+// XCD-local form (a.red_local): the same steps through the L2 of the one XCD every chunk of
+// the tile runs on: plain stores (written through L1 into L2), an L2 atomic for the counter
+// and loads that miss in L1 (sc0); no access leaves the XCD.  (Were the chunks ever placed on
+// different XCDs, no workgroup would count last and the tile's counter would stay nonzero:
+// the host checks the counters after each run.)
 template <int BPW>
 __device__ __forceinline__ bool narrow_reduce_last(const MfmaTileArgs &a, f4_t (&acc)[BPW],
                                                    const uint32_t (&j0)[BPW], uint32_t t,
@@ -171,27 +176,43 @@ __device__ __forceinline__ bool narrow_reduce_last(const MfmaTileArgs &a, f4_t (
     typedef __attribute__((address_space(1))) u64 gu64;
     typedef __attribute__((address_space(1))) uint32_t gu32;
     __shared__ uint32_t last;
+    const bool xl = a.red_local != 0u;
     gu64 *pp = (gu64 *)(a.part);
-    gu32 *cnt = (gu32 *)(a.arrive) + tile;
+    // (XCD-local counters one 128-byte line apart: tiles of one line run on different XCDs)
+    gu32 *cnt = (gu32 *)(a.arrive) + tile * (xl ? 32u : 1u);
     auto slot = [&](uint32_t zz, int bi) -> uint64_t {
         return (((uint64_t)zz * a.cout + j0[bi]) * 16u + 4u * t) >> 1;
     };
 #pragma unroll
     for (int bi = 0; bi < BPW; ++bi) {
         const uint64_t s = slot(z, bi);
-        __hip_atomic_store(pp + s, __builtin_bit_cast(u64, __builtin_shufflevector(acc[bi], acc[bi], 0, 1)),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(pp + s + 1, __builtin_bit_cast(u64, __builtin_shufflevector(acc[bi], acc[bi], 2, 3)),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const u64 v0 = __builtin_bit_cast(u64, __builtin_shufflevector(acc[bi], acc[bi], 0, 1));
+        const u64 v1 = __builtin_bit_cast(u64, __builtin_shufflevector(acc[bi], acc[bi], 2, 3));
+        if (xl) {
+            pp[s] = v0;
+            pp[s + 1] = v1;
+        } else {
+            __hip_atomic_store(pp + s, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + s + 1, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores performed
     __syncthreads();
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               a.kgroups - 1u;
+    if (threadIdx.x == 0) {
+        uint32_t before;
+        if (xl) {
+            before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else {
+            before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        last = before == a.kgroups - 1u;
+    }
     __syncthreads();
     if (!last) return false;
     const uint32_t kg = a.kgroups;
+    // (XCD-local: byte offsets from the partial buffer, below 2 GiB by the host's check)
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(a.part, (short)0, 0x7fffffff, 0x00020000);
     f4_t sum[BPW];
     constexpr uint32_t ZB = 8u;  // planes loaded together
     for (uint32_t z0 = 0; z0 < kg; z0 += ZB) {
@@ -202,8 +223,14 @@ __device__ __forceinline__ bool narrow_reduce_last(const MfmaTileArgs &a, f4_t (
 #pragma unroll
             for (int bi = 0; bi < BPW; ++bi) {
                 const uint64_t s = slot(zz, bi);
-                lo[u][bi] = __hip_atomic_load(pp + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                hi[u][bi] = __hip_atomic_load(pp + s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (xl) {
+                    const uint32_t off = (uint32_t)(s * 8u);
+                    lo[u][bi] = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(prs, off, 0, 1));
+                    hi[u][bi] = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(prs, off + 8u, 0, 1));
+                } else {
+                    lo[u][bi] = __hip_atomic_load(pp + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    hi[u][bi] = __hip_atomic_load(pp + s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
         }
 #pragma unroll
@@ -232,7 +259,12 @@ __device__ __forceinline__ bool narrow_reduce_last(const MfmaTileArgs &a, f4_t (
 #pragma unroll
     for (int bi = 0; bi < BPW; ++bi) acc[bi] = sum[bi];
     // every workgroup of the tile has arrived: the counter is zero again for the next launch
-    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) {
+        if (xl)
+            __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else
+            __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     return true;
 }
 
@@ -414,15 +446,15 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
     static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][NARROW_MAX_ROWS][NARROW_PITCH];
 
-    uint32_t w = 0, local;
+    uint32_t w = 0, pos;  // the wave, and the workgroup's position among its work items
     if constexpr (BYY) {
         w = blockIdx.y;
-        local = blockIdx.x;
+        pos = blockIdx.x;
     } else if (grp.n == 1u) {
-        local = blockIdx.x;
+        pos = blockIdx.x;
     } else {
         while (w + 1u < grp.n && blockIdx.x >= grp.start[w + 1u]) ++w;
-        local = blockIdx.x - grp.start[w];
+        pos = blockIdx.x - grp.start[w];
     }
     // The wave's weights and geometry from the preloaded arguments where the launch gives them:
     // its first weight loads are then issued before the descriptor is read (the scheduling
@@ -430,13 +462,24 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
     const uint32_t geo = w == 0u ? geo0 : w == 1u ? geo1 : w == 2u ? geo2 : 0u;
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    uint32_t tiles, ksteps, chunk, kgroups, tile, zgroup, ks_begin, ks_end;
+    uint32_t tiles, ksteps, chunk, kgroups, tile, zgroup, ks_begin, ks_end, local;
+    bool xlocal;
     __amdgpu_buffer_rsrc_t wr;
-    // the chunk's A fragments [k-step - ks_begin][16-block][lane][8]: 1 KiB per k-step and block
+    // the work item at pos (idle past the wave's own), its dense index local = z * tiles + tile,
+    // and the chunk's A fragments [k-step - ks_begin][16-block][lane][8] (1 KiB per k-step and
+    // block)
     auto geometry = [&](const void *wbase) {
-        if (BYY && local >= tiles * kgroups) return false;
-        tile = local % tiles;
-        zgroup = local / tiles;
+        if (xlocal) {
+            const uint32_t g8 = pos / (8u * kgroups), r = pos - g8 * 8u * kgroups;
+            zgroup = r >> 3;
+            tile = g8 * 8u + (r & 7u);
+            if (tile >= tiles) return false;
+        } else {
+            if (pos >= tiles * kgroups) return false;
+            tile = pos % tiles;
+            zgroup = pos / tiles;
+        }
+        local = zgroup * tiles + tile;
         ks_begin = zgroup * chunk;
         ks_end = min(ksteps, ks_begin + chunk);
         wr = __builtin_amdgcn_make_buffer_rsrc(
@@ -457,7 +500,8 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
     };
     h8_t af[AF][BPW];
     if (geo != 0u) {
-        tiles = geo & 0x7ffu;
+        tiles = geo & 0x3ffu;
+        xlocal = ((geo >> 10) & 1u) != 0u;
         ksteps = (geo >> 11) & 0xffu;
         chunk = (geo >> 19) & 0xffu;
         kgroups = geo >> 27;
@@ -469,6 +513,7 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
     const MfmaTileArgs a = grp.waves[w];
     if (geo == 0u) {
         tiles = a.tiles;
+        xlocal = a.red_local != 0u;
         ksteps = a.ksteps;
         chunk = a.stage_chunk;
         kgroups = a.kgroups;
@@ -737,6 +782,17 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
             a.part[((uint64_t)zgroup * a.cout + j) * 16u + t] = acc[bi][i];
         }
     }
+}
+
+// Set-up probe of the XCD-local split-K meeting: workgroup b records the XCD it runs on.
+__global__ __launch_bounds__(64) void k44_xcd_probe_kernel(uint32_t *out) {
+    if (threadIdx.x == 0u) out[blockIdx.x] = k44_xcc_id();
+}
+
+hipError_t launch_xcd_probe(uint32_t *out, uint32_t n, hipStream_t stream) {
+    if (n == 0u) return hipSuccess;
+    hipLaunchKernelGGL(k44_xcd_probe_kernel, dim3(n), dim3(64), 0, stream, out);
+    return hipGetLastError();
 }
 
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,

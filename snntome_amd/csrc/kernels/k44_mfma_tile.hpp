@@ -124,6 +124,13 @@ struct MfmaTileArgs {
     const __half *cp_src;
     __half *cp_dst;
     uint32_t cp_rows, cp_sstride, cp_dstride;
+    // Split-K reduced inside the launch through one XCD's L2 (red_local 1; arrive set): the
+    // wave's work items are numbered so that the chunks of a tile are 8 apart in launch order
+    // (position p: tile 8 (p / 8kg) + p % 8, chunk (p % 8kg) / 8; positions of tiles past the
+    // wave's are idle), which the round-robin dispatch over the XCDs places on one XCD (set-up
+    // checks it); the partials are then plain stores, the arrival counter an L2 atomic and the
+    // reads L1-bypassing loads, instead of device-coherent accesses.
+    uint32_t red_local;
     // Single-frame 2-D outputs whose 64-token tiles span plane rows (padded-plane layout, W not
     // a multiple of 64): token t of tile tl of its frame is pixel rel = 64 tl + (t & 63) of the
     // padded rows, stored only when rel / mask_wpad < mask_h and rel % mask_wpad < mask_w (the
@@ -184,20 +191,32 @@ struct MfmaGroup {
 #define K44_GROUP_ARGS(g) (g).waves, (g).start, (g).n, (g).xcd_order
 #define K44_GROUP_BIND const MfmaGroup grp{grp_waves, grp_start, grp_n, grp_xcd}
 
+// XCD (accelerator complex die) this wave runs on.
+__device__ __forceinline__ uint32_t k44_xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xfu;
+}
+
 // Weights and contraction geometry of the first three waves of a narrow launch, passed as
 // scalar kernel arguments (preloaded into SGPRs like the group fields), so that a workgroup
-// issues its weight stream before its descriptor load has returned.  geo packs tiles (11
-// bits), ksteps (8), stage_chunk (8) and kgroups (5); 0 = the wave reads them from its
-// descriptor (more members, larger shapes, or the switch off).
+// issues its weight stream before its descriptor load has returned.  geo packs tiles (10
+// bits), red_local (1), ksteps (8), stage_chunk (8) and kgroups (5); 0 = the wave reads them
+// from its descriptor (more members, larger shapes, or the switch off).
 struct NarrowPre {
     const void *w[3] = {nullptr, nullptr, nullptr};
     uint32_t geo[3] = {0u, 0u, 0u};
 };
 inline uint32_t narrow_geo(const MfmaTileArgs &a) {
-    if (a.tiles == 0u || a.tiles >= 2048u || a.ksteps >= 256u || a.stage_chunk >= 256u ||
+    if (a.tiles == 0u || a.tiles >= 1024u || a.ksteps >= 256u || a.stage_chunk >= 256u ||
         a.kgroups == 0u || a.kgroups >= 32u)
         return 0u;
-    return a.tiles | (a.ksteps << 11) | (a.stage_chunk << 19) | (a.kgroups << 27);
+    return a.tiles | ((a.red_local ? 1u : 0u) << 10) | (a.ksteps << 11) | (a.stage_chunk << 19) |
+           (a.kgroups << 27);
+}
+// Work items of a narrow wave in launch order (XCD-local waves: whole groups of 8 tiles).
+__host__ __device__ inline uint32_t narrow_items(uint32_t tiles, uint32_t kgroups, bool local) {
+    return (local ? (tiles + 7u) / 8u * 8u : tiles) * kgroups;
 }
 
 // Per-wave shares of the 8 XCDs (xcd_order 2), host and device.  Workgroup b runs on XCD
