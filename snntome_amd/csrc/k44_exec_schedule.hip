@@ -1275,7 +1275,8 @@ void K44GpuExecutorState::build_report() {
         for (size_t k = 0; k < cmds.size(); ++k) o << (k ? ", " : "") << cmds[k];
         o << "]";
     }
-    o << "], \"launches_per_run\": " << (prog_active ? (size_t)1u : launches_per_run());
+    o << "], \"launches_per_run\": " << (prog_active ? (size_t)1u : launches_per_run())
+      << ", \"xcd_local_ok\": " << (xcd_local_ok ? "true" : "false");
     o << ", \"program\": {\"active\": " << (prog_active ? "true" : "false")
       << ", \"why\": \"" << prog_why << "\", \"stages\": " << prog_stages_h.size()
       << ", \"grid\": " << prog_grid << ", \"items\": "

@@ -138,12 +138,12 @@ def test_tuning_switches_set_get_reset(wavec):
     wavec.reset_tuning()
     for key, bad in (("dma_stages", 3), ("ksplit", 2), ("xcd_order", 7), ("path", 2),
                      ("narrow_chunk", 15), ("narrow_wgs", 0), ("narrow_reduce", 2),
-                     ("t64_ring", 3), ("dma_prod", 2)):
+                     ("t64_ring", 3), ("dma_prod", 2), ("narrow_pre", 2), ("narrow_local", 2)):
         with pytest.raises(RuntimeError, match="not honoured"):
             wavec.set_tuning(key, bad)
         assert wavec.get_tuning(key) == -1
     for key, good in (("dma_stages", 4), ("ksplit", 4), ("xcd_order", 2), ("narrow_reduce", 0),
-                      ("t64_ring", 2), ("dma_prod", 1)):
+                      ("t64_ring", 2), ("dma_prod", 1), ("narrow_pre", 0), ("narrow_local", 0)):
         wavec.set_tuning(key, good)
         assert wavec.get_tuning(key) == good
     wavec.reset_tuning()

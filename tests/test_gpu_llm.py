@@ -466,10 +466,12 @@ def test_folded_multiplies_match_unfolded(wavec, tuning, rf, requests):
 
 def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
     """Split narrow waves of 64-neuron tiles reduce their chunk partials in the last workgroup
-    of each tile (per-tile arrival counters, device-coherent partial stores and loads); ids and
+    of each tile (per-tile arrival counters; device-coherent partial stores and loads, or, by
+    default, plain ones through the L2 of the one XCD every chunk of a tile runs on); ids and
     logits of several decode steps, eager and HIP-graph replays, are bit-identical to the plan
     whose partials are reduced by the split-K epilogue kernel (narrow_reduce=0), and every
-    counter is back at zero between launches (a later launch sums the right chunks)."""
+    counter is back at zero between launches (a later launch sums the right chunks; the
+    executor checks the XCD-local counters after every run)."""
     # contractions of 32 k-steps (d-input: 4 of 8 clusters of 256) and 40 (FFN input: 5 of 10):
     # 2 and 3 chunks of <= 16 k-steps, the last one ragged
     spec = synth.LLMSpec(layers=2, d=2048, ffn=2560, vocab=1024, S=256, requests=4, prompt=64,
@@ -483,18 +485,23 @@ def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
     pre.execute(1)
     out = {}
     tuning("program", 0)  # split narrow waves exist only in kernel-by-kernel launches
-    for mode in ("kernel", "in_launch"):
+    for mode in ("kernel", "in_launch", "xcd_local"):
         tuning("narrow_reduce", 0 if mode == "kernel" else 1)
+        tuning("narrow_local", 1 if mode == "xcd_local" else 0)
         tuning("narrow_wgs", 512)  # many chunks per tile: every narrow wave splits
         p = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
         p.init_gpu()
         rep = p.exec_report()
         split = [w for w in rep["waves"] if w["path"] == "mfma_narrow" and w["ksplit"] > 1]
         inl = [w for w in split if w["reduce_in_kernel"]]
+        loc = [w for w in split if w["reduce_xcd_local"]]
         _log(f"[narrow reduce {mode}] {len(split)} split narrow waves, {len(inl)} reduced in "
-             f"their launch, chunks {sorted({w['ksplit'] for w in split})}, "
-             f"{rep['launches_per_run']} launches per run")
-        assert split and len(inl) == (len(split) if mode == "in_launch" else 0)
+             f"their launch ({len(loc)} XCD-locally), chunks "
+             f"{sorted({w['ksplit'] for w in split})}, {rep['launches_per_run']} launches per run")
+        assert split and len(inl) == (0 if mode == "kernel" else len(split))
+        # (XCD-local only where set-up found workgroups 8 apart sharing an XCD)
+        want_loc = mode == "xcd_local" and rep["xcd_local_ok"]
+        assert len(loc) == (len(split) if want_loc else 0)
         synth.llm_handoff(spec, pre, p)
         hd = next(c for c in p.cmds if c["name"].split("/")[0] == "head")
         ids, logits = [], []
@@ -507,8 +514,9 @@ def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
             logits.append(p.read_canvas(int(hd["y_off"]), spec.vocab * 64).reshape(-1, 64)[:, :R])
         out[mode] = (np.stack(ids), np.stack(logits))
         p.release_gpu()
-    assert np.array_equal(out["kernel"][0], out["in_launch"][0])
-    assert np.array_equal(out["kernel"][1], out["in_launch"][1])
+    for mode in ("in_launch", "xcd_local"):
+        assert np.array_equal(out["kernel"][0], out[mode][0])
+        assert np.array_equal(out["kernel"][1], out[mode][1])
 
 
 def test_prefill_multiply_chain_matches_launched(wavec, tuning):
