@@ -284,7 +284,9 @@ int wavec_gpu_read_canvas_2d(void *handle, unsigned long long elem_off, unsigned
  *   "narrow_local" 0 | 1 split narrow waves reduced in the launch meet through device-coherent
  *   memory / through the L2 of the XCD every chunk of a tile runs on (automatic, where a
  *   set-up probe finds workgroups 8 apart in launch order sharing an XCD; a tile whose chunks
- *   met no one leaves its counter nonzero and makes wavec_gpu_execute fail).
+ *   met no one leaves its counter nonzero and makes wavec_gpu_execute fail); "narrow_byy" 0 | 1
+ *   narrow group launches as 1-D grids (each workgroup's wave from the prefix sums) / as
+ *   (workgroups x waves) grids where those launch at most 1.5x the work items (automatic).
  * wavec_set_tuning returns -1 (with a message) for an unknown key or a value the key does not
  * honour: -1 is always accepted; "dma_stages" takes 2 | 4, "ksplit" 1 | 4, "xcd_order" 0..2,
  * "t64_ring" 0..2, "narrow_chunk" >= 16, "narrow_wgs" >= 1, "prog_spin_ms" >= 0, every

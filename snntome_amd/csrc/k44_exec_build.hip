@@ -1060,7 +1060,7 @@ void K44GpuExecutorState::upload_mfma_descriptors() {
         const k44dev::MfmaTileArgs one = mfma_args(w, scratch.p, false);
         w.one_args.upload({one});
         w.one_start.upload({0u, w.items});
-        w.one_pre = narrow_pre({one});
+        w.one_pre = w.narrow ? narrow_pre({one}, {}, nullptr) : k44dev::NarrowPre{};
     }
     for (auto &gp : groups) {
         MfmaGroupExec &g = *gp;
@@ -1092,11 +1092,12 @@ void K44GpuExecutorState::upload_mfma_descriptors() {
         }
         g.items = start.back();
         g.epi_items = epi_max;  // epilogue grid: epi_max x members
-        g.max_items = item_max;
+        g.max_items = item_max;  // (0: narrow launches find each workgroup's wave by prefix sums)
+        if (g.mt == 16u && tune(Tune::NarrowByy) == 0) g.max_items = 0u;
         if (xcd_order == 2u) check_balanced_order(start);
         g.args.upload(args);
         g.start.upload(start);
-        g.pre = narrow_pre(args);
+        if (g.mt == 16u) g.pre = narrow_pre(args, order, &g.pre_w);
     }
 }
 
@@ -1137,15 +1138,36 @@ void K44GpuExecutorState::check_placement() {
                              "narrow_local=0 avoids these reductions)");
 }
 
-// The first three descriptors' weights and geometry for the narrow kernels' preloaded
-// arguments (tuning key narrow_pre 0: none, every wave reads its descriptor).
-k44dev::NarrowPre K44GpuExecutorState::narrow_pre(const std::vector<k44dev::MfmaTileArgs> &args) {
+// Weights and geometry of up to six descriptors for the narrow kernels' preloaded arguments
+// (tuning key narrow_pre 0: none, every wave reads its descriptor).  One member: its own
+// weights; several: copies of their A fragments in *arena, member m at m << shift bytes
+// (shift: the largest member's bytes rounded up to a power of two).  members: the waves of
+// args, in the same order.
+k44dev::NarrowPre K44GpuExecutorState::narrow_pre(const std::vector<k44dev::MfmaTileArgs> &args,
+                                                  const std::vector<size_t> &members,
+                                                  DevBuf<__half> *arena) {
     k44dev::NarrowPre p;
-    if (tune(Tune::NarrowPre) == 0) return p;
-    for (size_t i = 0; i < args.size() && i < 3u; ++i) {
-        p.w[i] = args[i].Wf;
+    if (tune(Tune::NarrowPre) == 0 || args.empty()) return p;
+    const size_t n = std::min(args.size(), (size_t)k44dev::NarrowPre::N);
+    if (args.size() == 1u || !arena) {
+        p.base = args[0].Wf;
+        p.geo[0] = k44dev::narrow_geo(args[0]);
+        return p;
+    }
+    size_t most = 256u;
+    for (size_t i = 0; i < n; ++i) most = std::max(most, waves[members[i]]->w.n * sizeof(__half));
+    uint32_t sh = 8u;
+    while (((size_t)1 << sh) < most) ++sh;
+    arena->alloc((n << sh) / sizeof(__half));
+    for (size_t i = 0; i < n; ++i) {
+        const WaveExec &w = *waves[members[i]];
+        K44_HIP(hipMemcpyAsync(reinterpret_cast<char *>(arena->p) + (i << sh), w.w.p,
+                               w.w.n * sizeof(__half), hipMemcpyDeviceToDevice, stream));
         p.geo[i] = k44dev::narrow_geo(args[i]);
     }
+    K44_HIP(hipStreamSynchronize(stream));
+    p.base = arena->p;
+    p.shift = sh;
     return p;
 }
 

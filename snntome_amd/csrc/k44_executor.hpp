@@ -166,7 +166,8 @@ struct MfmaGroupExec {
     size_t part_floats = 0;
     DevBuf<k44dev::MfmaTileArgs> args;
     DevBuf<uint32_t> start;
-    k44dev::NarrowPre pre;  // narrow kernels: the first three members' weights and geometry
+    k44dev::NarrowPre pre;  // narrow kernels: up to six members' weights and geometry
+    DevBuf<__half> pre_w;   // those members' A fragments, member m at (m << pre.shift) bytes
 };
 
 // Sorted, merged [lo, hi) element ranges.
@@ -350,7 +351,8 @@ struct K44GpuExecutorState {
     static uint32_t epi_workgroups(const WaveExec &w);
     void upload_mfma_descriptors();
     static uint32_t item_stages(const WaveExec &w);
-    static k44dev::NarrowPre narrow_pre(const std::vector<k44dev::MfmaTileArgs> &args);
+    k44dev::NarrowPre narrow_pre(const std::vector<k44dev::MfmaTileArgs> &args,
+                                 const std::vector<size_t> &members, DevBuf<__half> *arena);
     void probe_xcd_placement();
     void check_placement();
     static void check_balanced_order(const std::vector<uint32_t> &start);

@@ -54,8 +54,8 @@ hipError_t launch_mfma_dma(const MfmaGroup &g, uint32_t nt, uint32_t items, hipS
 // contraction chunks per wave); nt in {16,32,64,128}.  prod: 0, or the element-wise product
 // form (MfmaTileArgs::xprod 2 / 3) every wave of the group gathers (nt 64 / 128 only).
 // max_items: the largest wave's workgroups (nt 64 / 128 take a (max_items x waves) grid when
-// that wastes little).  pre: the first three waves' weights and geometry as kernel arguments
-// (nt 64 / 128; zero entries: read from the descriptors).
+// that wastes little).  pre: up to six waves' weights and geometry as kernel arguments (nt 64
+// / 128; zero entries: read from the descriptors).
 hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items, hipStream_t stream,
                               uint32_t prod = 0, uint32_t max_items = 0,
                               const NarrowPre &pre = NarrowPre{});

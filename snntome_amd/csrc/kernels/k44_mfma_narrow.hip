@@ -435,13 +435,14 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_kernel(K44_GROUP_PARAMS) 
 // ms/step against refills clamped to the chunk's last k-step (re-reads of it); two sub-chunks
 // of fragments in flight per wave instead of one: 0.869 ms/step (each wave's first gather then
 // waits behind twice the weight bytes).
-// geo0..2 / pw0..2: NarrowPre (the first three waves' geometry and weights).  The parameters
-// fill the 14 SGPRs that gfx950 preloads (the group's XCD order is not used here).
+// nsh = waves | NarrowPre::shift << 8; geo0..5 / wbase: NarrowPre.  The parameters fill the
+// 14 SGPRs that gfx950 preloads (the group's XCD order is not used here).
 template <int NT, int PROD, bool BYY>
 __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
-    const MfmaTileArgs *grp_waves, const uint32_t *grp_start, uint32_t grp_n, uint32_t geo0,
-    uint32_t geo1, uint32_t geo2, const void *pw0, const void *pw1, const void *pw2) {
-    const MfmaGroup grp{grp_waves, grp_start, grp_n, 0u};
+    const MfmaTileArgs *grp_waves, const uint32_t *grp_start, uint32_t nsh, uint32_t geo0,
+    uint32_t geo1, uint32_t geo2, uint32_t geo3, uint32_t geo4, uint32_t geo5,
+    const void *wbase) {
+    const MfmaGroup grp{grp_waves, grp_start, nsh & 0xffu, 0u};
     constexpr int NB = NT / 16, BPW = NB / 4, SUBK = 16, AF = SUBK;
     static_assert(NT == 64 || NT == 128, "waves own whole 16-neuron blocks");
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][NARROW_MAX_ROWS][NARROW_PITCH];
@@ -459,7 +460,13 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
     // The wave's weights and geometry from the preloaded arguments where the launch gives them:
     // its first weight loads are then issued before the descriptor is read (the scheduling
     // barrier below keeps the descriptor's scalar loads, and their waits, after them).
-    const uint32_t geo = w == 0u ? geo0 : w == 1u ? geo1 : w == 2u ? geo2 : 0u;
+    const uint32_t geo = w == 0u   ? geo0
+                         : w == 1u ? geo1
+                         : w == 2u ? geo2
+                         : w == 3u ? geo3
+                         : w == 4u ? geo4
+                         : w == 5u ? geo5
+                                   : 0u;
     const int tid = (int)threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint32_t tiles, ksteps, chunk, kgroups, tile, zgroup, ks_begin, ks_end, local;
@@ -505,7 +512,8 @@ __global__ __launch_bounds__(256) void k44_mfma_narrow_long_kernel(
         ksteps = (geo >> 11) & 0xffu;
         chunk = (geo >> 19) & 0xffu;
         kgroups = geo >> 27;
-        if (!geometry(w == 0u ? pw0 : w == 1u ? pw1 : pw2)) return;
+        if (!geometry(reinterpret_cast<const char *>(wbase) + ((uint64_t)w << (nsh >> 8))))
+            return;
 #pragma unroll
         for (int u = 0; u < AF; ++u) load_a((uint32_t)u, af[u]);
     }
@@ -808,8 +816,11 @@ hipError_t launch_mfma_narrow(const MfmaGroup &g, uint32_t nt, uint32_t items,
     const dim3 grid_y(max_items, g.n);
     // a wave past the group's count never selects its preloaded entry
     NarrowPre p = pre;
-    for (uint32_t i = g.n; i < 3u; ++i) p.geo[i] = 0u;
-#define K44_PRE_ARGS g.waves, g.start, g.n, p.geo[0], p.geo[1], p.geo[2], p.w[0], p.w[1], p.w[2]
+    for (uint32_t i = g.n; i < (uint32_t)NarrowPre::N; ++i) p.geo[i] = 0u;
+    if (g.n > 255u || p.shift > 40u) return hipErrorInvalidValue;
+    const uint32_t nsh = g.n | (p.shift << 8);
+#define K44_PRE_ARGS                                                                         \
+    g.waves, g.start, nsh, p.geo[0], p.geo[1], p.geo[2], p.geo[3], p.geo[4], p.geo[5], p.base
 #define K44_NL(N, P)                                                                               \
     if (byy)                                                                                       \
         hipLaunchKernelGGL((k44_mfma_narrow_long_kernel<N, P, true>), grid_y, block, 0, stream, \

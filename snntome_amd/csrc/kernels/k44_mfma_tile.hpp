@@ -198,14 +198,17 @@ __device__ __forceinline__ uint32_t k44_xcc_id() {
     return v & 0xfu;
 }
 
-// Weights and contraction geometry of the first three waves of a narrow launch, passed as
-// scalar kernel arguments (preloaded into SGPRs like the group fields), so that a workgroup
-// issues its weight stream before its descriptor load has returned.  geo packs tiles (10
-// bits), red_local (1), ksteps (8), stage_chunk (8) and kgroups (5); 0 = the wave reads them
-// from its descriptor (more members, larger shapes, or the switch off).
+// Weights and contraction geometry of up to six waves of a narrow launch, passed as scalar
+// kernel arguments (preloaded into SGPRs like the group fields), so that a workgroup issues
+// its weight stream before its descriptor load has returned.  The waves' A fragments are
+// copies in one buffer, wave m's at base + (m << shift); geo[m] packs tiles (10 bits),
+// red_local (1), ksteps (8), stage_chunk (8) and kgroups (5); 0 = the wave reads them from its
+// descriptor (more members, larger shapes, or the switch off).
 struct NarrowPre {
-    const void *w[3] = {nullptr, nullptr, nullptr};
-    uint32_t geo[3] = {0u, 0u, 0u};
+    static constexpr int N = 6;
+    const void *base = nullptr;
+    uint32_t shift = 0;
+    uint32_t geo[N] = {0u, 0u, 0u, 0u, 0u, 0u};
 };
 inline uint32_t narrow_geo(const MfmaTileArgs &a) {
     if (a.tiles == 0u || a.tiles >= 1024u || a.ksteps >= 256u || a.stage_chunk >= 256u ||
