@@ -467,7 +467,8 @@ def test_folded_multiplies_match_unfolded(wavec, tuning, rf, requests):
 def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
     """Split narrow waves of 64-neuron tiles reduce their chunk partials in the last workgroup
     of each tile (per-tile arrival counters; device-coherent partial stores and loads, or, by
-    default, plain ones through the L2 of the one XCD every chunk of a tile runs on); ids and
+    default, plain ones through the L2 of the one XCD every chunk of a tile runs on; with the
+    waves' weight addresses and geometry preloaded as kernel arguments or not); ids and
     logits of several decode steps, eager and HIP-graph replays, are bit-identical to the plan
     whose partials are reduced by the split-K epilogue kernel (narrow_reduce=0), and every
     counter is back at zero between launches (a later launch sums the right chunks; the
@@ -485,9 +486,11 @@ def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
     pre.execute(1)
     out = {}
     tuning("program", 0)  # split narrow waves exist only in kernel-by-kernel launches
-    for mode in ("kernel", "in_launch", "xcd_local"):
+    for mode in ("kernel", "in_launch", "xcd_local", "no_preload"):
         tuning("narrow_reduce", 0 if mode == "kernel" else 1)
-        tuning("narrow_local", 1 if mode == "xcd_local" else 0)
+        tuning("narrow_local", 1 if mode in ("xcd_local", "no_preload") else 0)
+        # no_preload: every wave reads its weights' address and geometry from its descriptor
+        tuning("narrow_pre", 0 if mode == "no_preload" else 1)
         tuning("narrow_wgs", 512)  # many chunks per tile: every narrow wave splits
         p = synth.build_llm_graph(spec, wts, decode=True, wavec_mod=wavec).compile()
         p.init_gpu()
@@ -500,7 +503,7 @@ def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
              f"{sorted({w['ksplit'] for w in split})}, {rep['launches_per_run']} launches per run")
         assert split and len(inl) == (0 if mode == "kernel" else len(split))
         # (XCD-local only where set-up found workgroups 8 apart sharing an XCD)
-        want_loc = mode == "xcd_local" and rep["xcd_local_ok"]
+        want_loc = mode in ("xcd_local", "no_preload") and rep["xcd_local_ok"]
         assert len(loc) == (len(split) if want_loc else 0)
         synth.llm_handoff(spec, pre, p)
         hd = next(c for c in p.cmds if c["name"].split("/")[0] == "head")
@@ -514,7 +517,7 @@ def test_decode_inkernel_splitk_matches_epilogue_kernel(wavec, tuning):
             logits.append(p.read_canvas(int(hd["y_off"]), spec.vocab * 64).reshape(-1, 64)[:, :R])
         out[mode] = (np.stack(ids), np.stack(logits))
         p.release_gpu()
-    for mode in ("in_launch", "xcd_local"):
+    for mode in ("in_launch", "xcd_local", "no_preload"):
         assert np.array_equal(out["kernel"][0], out[mode][0])
         assert np.array_equal(out["kernel"][1], out[mode][1])
 
