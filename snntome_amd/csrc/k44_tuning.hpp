@@ -42,8 +42,8 @@ enum class Tune : int {
     ProgTrace,     // "prog_trace":    1 = the persistent launch records per-item timestamps
                    //                  (wavec_gpu_program_trace)
     NarrowPre,     // "narrow_pre":    0 = narrow waves read their weights' address and geometry
-                   //                  from their descriptors; automatic and 1: the first three
-                   //                  waves of a launch take them as preloaded kernel arguments
+                   //                  from their descriptors; automatic and 1: up to six waves
+                   //                  of a launch take them as preloaded kernel arguments
     NarrowLocal,   // "narrow_local":  0 = split narrow waves reduced in the launch meet through
                    //                  device-coherent memory; automatic and 1: through the L2 of
                    //                  the XCD all chunks of a tile run on (items renumbered so
