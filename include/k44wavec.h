@@ -286,7 +286,9 @@ int wavec_gpu_read_canvas_2d(void *handle, unsigned long long elem_off, unsigned
  *   set-up probe finds workgroups 8 apart in launch order sharing an XCD; a tile whose chunks
  *   met no one leaves its counter nonzero and makes wavec_gpu_execute fail); "narrow_byy" 0 | 1
  *   narrow group launches as 1-D grids (each workgroup's wave from the prefix sums) / as
- *   (workgroups x waves) grids where those launch at most 1.5x the work items (automatic).
+ *   (workgroups x waves) grids where those launch at most 1.5x the work items (automatic);
+ *   "embed_refresh" 0 | 1 a decode embedding never / also (automatic) refreshes the compact
+ *   state copy of the first layer's folded token shift (0: that RMSNorm + shift runs alone).
  * wavec_set_tuning returns -1 (with a message) for an unknown key or a value the key does not
  * honour: -1 is always accepted; "dma_stages" takes 2 | 4, "ksplit" 1 | 4, "xcd_order" 0..2,
  * "t64_ring" 0..2, "narrow_chunk" >= 16, "narrow_wgs" >= 1, "prog_spin_ms" >= 0, every

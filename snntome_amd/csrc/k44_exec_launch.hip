@@ -42,14 +42,26 @@ void K44GpuExecutorState::launch_aux(const AuxExec &a, bool whole) {
                                            a.stride, a.tokens, a.rf, a.seq_len,
                                            a.decode ? 1 : 0, stream));
         break;
-    case K44CmdType::EMBED_1D:
+    case K44CmdType::EMBED_1D: {
+        k44dev::EmbedCopy cp;
+        if (whole && a.cp_fold != SIZE_MAX) {  // the first layer's compact token-shift state
+            const NormFold &f = norm_folds[a.cp_fold];
+            const AuxExec &T = *aux[f.shift];
+            cp.src = cv + T.state_off;
+            cp.sstride = 64u;
+            cp.dst = shift_next.p + f.cur0;
+            cp.dstride = 16u;
+            cp.rows = T.D * (T.rf - 1u);
+        }
         K44_HIP(k44dev::launch_embed(
             cv + a.y_off, a.table.p, ids.p, a.D, a.vocab, a.stride, a.tokens, stream,
             whole && a.slot_fold != SIZE_MAX
                 ? reinterpret_cast<uint64_t *>(norm_slots.p) +
                       (norm_folds[a.slot_fold].slot0 + a.slot_tile0) * 32u
-                : nullptr));
+                : nullptr,
+            cp));
         break;
+    }
     case K44CmdType::S2D_2X2:
         K44_HIP(k44dev::launch_s2d(cv + a.y_off, cv + a.src_off, a.C, a.pin, a.pout, stream));
         K44_HIP(k44dev::launch_halo_clear(cv + a.y_off, a.out_channels, a.pout, stream));

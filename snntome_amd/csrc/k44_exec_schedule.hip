@@ -786,7 +786,8 @@ bool K44GpuExecutorState::fold_shift(size_t i, const std::pair<uint64_t, uint64_
                                      const std::vector<Ranges> &rd, const std::vector<Ranges> &wr,
                                      const Ranges &out_rng, std::vector<size_t> &cons,
                                      size_t &refresher, size_t &carrier,
-                                     std::vector<std::vector<uint64_t>> &owns) {
+                                     std::vector<std::vector<uint64_t>> &owns,
+                                     size_t embed_aux) {
     typedef std::pair<uint64_t, uint64_t> Rng;
     const AuxExec &N = *aux[ops[i].second];
     const AuxExec &T = *aux[N.shift_with];
@@ -833,13 +834,17 @@ bool K44GpuExecutorState::fold_shift(size_t i, const std::pair<uint64_t, uint64_
     if (carrier == SIZE_MAX) return false;
     for (size_t j = i + 1; j <= carrier; ++j)
         if (ranges_overlap(rd[j], Ranges{St}) || ranges_overlap(wr[j], Ranges{St})) return false;
-    // the refresher: the last narrow launch before the norm, with nothing after it writing the
-    // state before the readers
+    // the refresher: the last narrow launch before the norm, or else the decode embedding that
+    // produces the norm's input (embed_aux), with nothing after it writing the state before the
+    // readers
     refresher = SIZE_MAX;
     for (size_t j = i; j-- > 0 && refresher == SIZE_MAX;)
         if (ops[j].first && narrow_long(*waves[ops[j].second]) &&
             waves[ops[j].second]->cp_fold == SIZE_MAX)
             refresher = j;
+    if (refresher == SIZE_MAX && embed_aux != SIZE_MAX && aux[embed_aux]->cp_fold == SIZE_MAX)
+        for (size_t j = i; j-- > 0 && refresher == SIZE_MAX;)
+            if (!ops[j].first && ops[j].second == embed_aux) refresher = j;
     if (refresher == SIZE_MAX) return false;
     for (size_t j = refresher; j < i; ++j)
         if (ranges_overlap(wr[j], Ranges{St})) return false;
@@ -989,8 +994,8 @@ void K44GpuExecutorState::fuse_norms() {
         std::vector<std::vector<uint64_t>> owns;
         const bool shifted =
             !consume && tune(Tune::Program) != 1 &&
-            prod_embed == SIZE_MAX &&
-            fold_shift(i, X, Y, rd, wr, out_rng, cons, refresher, carrier, owns);
+            fold_shift(i, X, Y, rd, wr, out_rng, cons, refresher, carrier, owns,
+                       tune(Tune::EmbedRefresh) != 0 ? prod_embed : SIZE_MAX);
         if (consume) {
             size_t last = i;
             bool overwritten = false;
@@ -1061,11 +1066,15 @@ void K44GpuExecutorState::fuse_norms() {
             }
             // the compact copy is refreshed by the refresher's launch and the state written back
             // by the carrier's (neither grouped with a reader)
-            WaveExec &rw = *waves[ops[refresher].second];
-            rw.cp_fold = norm_folds.size();
-            rw.cp_refresh = true;
-            rw.carry_rng = {St};
-            rw.why += "; its workgroups refresh the compact state copy of a later token shift";
+            if (ops[refresher].first) {
+                WaveExec &rw = *waves[ops[refresher].second];
+                rw.cp_fold = norm_folds.size();
+                rw.cp_refresh = true;
+                rw.carry_rng = {St};
+                rw.why += "; its workgroups refresh the compact state copy of a later token shift";
+            } else {
+                aux[ops[refresher].second]->cp_fold = norm_folds.size();
+            }
             WaveExec &cw = *waves[ops[carrier].second];
             cw.cp_fold = norm_folds.size();
             cw.carry_rng = {St};
@@ -1245,6 +1254,9 @@ void K44GpuExecutorState::build_report() {
           << ", \"fused\": " << (aux[i]->fused ? "true" : "false")
           << ", \"fuse_note\": \"" << aux[i]->fuse_note << "\""
           << ", \"chain\": " << (aux[i]->chain_inner != SIZE_MAX ? "true" : "false")
+          << ", \"refreshes_state_of\": "
+          << (aux[i]->cp_fold != SIZE_MAX ? (long long)aux_cmd[norm_folds[aux[i]->cp_fold].shift]
+                                          : -1LL)
           << ", \"operands\": ["
           << (aux[i]->chain_inner != SIZE_MAX ? aux[i]->chain_other : aux[i]->src_off) << ", "
           << (aux[i]->chain_inner != SIZE_MAX ? aux[aux[i]->chain_inner]->src_off : aux[i]->src2_off)

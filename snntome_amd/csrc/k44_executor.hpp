@@ -214,6 +214,10 @@ struct AuxExec {
     // 64-channel blocks from slot slot_tile0 of the fold on)
     size_t slot_fold = SIZE_MAX;
     uint32_t slot_tile0 = 0;
+    // EMBED_1D (decode, whole-plan runs): the fold whose compact token-shift state copy this
+    // launch refreshes from the plan's state (the first layer's readers have no narrow launch
+    // before them to do it)
+    size_t cp_fold = SIZE_MAX;
     // SWIGLU_MUL_1D y = other * q where q = b * c is an inner multiply only this one reads:
     // whole plans run both as y = fp16(other * fp16(b * c)) (the inner one is not launched).
     size_t chain_inner = SIZE_MAX;
@@ -368,7 +372,7 @@ struct K44GpuExecutorState {
                     const std::pair<uint64_t, uint64_t> &Y, const std::vector<Ranges> &rd,
                     const std::vector<Ranges> &wr, const Ranges &out_rng,
                     std::vector<size_t> &cons, size_t &refresher, size_t &carrier,
-                    std::vector<std::vector<uint64_t>> &owns);
+                    std::vector<std::vector<uint64_t>> &owns, size_t embed_aux);
 
     void fuse_norms();
     void form_runs();

@@ -49,6 +49,9 @@ enum class Tune : int {
                    //                  the XCD all chunks of a tile run on (items renumbered so
                    //                  they are 8 workgroups apart), where set-up finds that
                    //                  workgroups 8 apart share an XCD
+    EmbedRefresh,  // "embed_refresh": 0 = a decode embedding never refreshes a folded token
+                   //                  shift's state copy (the first layer's RMSNorm + shift then
+                   //                  runs as its own kernel); automatic and 1: it does
     NarrowByy,     // "narrow_byy":    0 = narrow group launches find each workgroup's wave in the
                    //                  group's prefix sums; automatic: (workgroups x waves) grids
                    //                  where they launch at most 1.5x the work items

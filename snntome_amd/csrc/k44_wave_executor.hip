@@ -19,7 +19,7 @@ const char *const kTuneKeys[(int)Tune::Count] = {
     "path", "dma", "dma_stages", "nt", "splitk", "lane8", "ksplit", "stream_kernel", "narrow",
     "narrow_chunk", "group", "group_split", "fuse", "sort", "wlds", "t64_ring", "xcd_order",
     "narrow_wgs", "narrow_reduce", "dma_prod", "program", "prog_spin_ms", "prog_trace",
-    "narrow_pre", "narrow_local", "narrow_byy"};
+    "narrow_pre", "narrow_local", "embed_refresh", "narrow_byy"};
 // Values each switch honours besides -1: a set of small values (bit v of `set`), or every
 // value >= `min` when `set` is 0.  Anything else is refused, so an A/B run cannot measure a
 // configuration other than the one it asked for.
@@ -54,6 +54,7 @@ const TuneValues kTuneValues[(int)Tune::Count] = {
     {V01, 0},          // prog_trace
     {V01, 0},          // narrow_pre
     {V01, 0},          // narrow_local
+    {V01, 0},          // embed_refresh
     {V01, 0},          // narrow_byy
 };
 struct TuneInit {

@@ -657,10 +657,19 @@ __global__ __launch_bounds__(256) void k44_embed_vec_kernel(__half *__restrict__
                                                             const uint32_t *__restrict__ ids,
                                                             uint32_t D, uint32_t vocab,
                                                             uint32_t stride, uint32_t tokens,
-                                                            uint64_t *__restrict__ slots) {
+                                                            uint64_t *__restrict__ slots,
+                                                            EmbedCopy cp) {
     constexpr uint32_t PITCH = 72u;  // halves per token row: 16-byte rows, spread banks
     __shared__ __attribute__((aligned(16))) __half tile[64 * PITCH];
     const uint32_t t0 = blockIdx.x * 64u, c0 = blockIdx.y * 64u;
+    if (cp.rows) {  // the copy carried for a folded token shift (16 bytes per thread and step)
+        const uint32_t nth = gridDim.x * gridDim.y * 256u;
+        for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * 256u + threadIdx.x;
+             i < 2u * cp.rows; i += nth)
+            *reinterpret_cast<uint4 *>(cp.dst + (uint64_t)(i >> 1) * cp.dstride + (i & 1u) * 8u) =
+                *reinterpret_cast<const uint4 *>(cp.src + (uint64_t)(i >> 1) * cp.sstride +
+                                                 (i & 1u) * 8u);
+    }
     uint4 v[2];
     bool ok[2];
 #pragma unroll
@@ -1018,8 +1027,13 @@ hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __ha
 
 hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uint32_t D,
                         uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream,
-                        uint64_t *slots) {
+                        uint64_t *slots, const EmbedCopy &cp) {
     if (stride % 64u != 0u || D == 0u) return hipErrorInvalidValue;
+    // the carried copy: 16-byte aligned rows of 16 halves, with the slot form only
+    if (cp.rows && (!slots || reinterpret_cast<uintptr_t>(cp.src) % 16u != 0u ||
+                    reinterpret_cast<uintptr_t>(cp.dst) % 16u != 0u || cp.sstride % 8u != 0u ||
+                    cp.dstride % 8u != 0u))
+        return hipErrorInvalidValue;
     const dim3 grid(stride / 64u, (D + 63u) / 64u);
     const bool vec = tokens > 0u && D % 8u == 0u && reinterpret_cast<uintptr_t>(table) % 16u == 0u &&
                      reinterpret_cast<uintptr_t>(y) % 16u == 0u;
@@ -1028,7 +1042,7 @@ hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uin
         return hipErrorInvalidValue;
     if (vec)
         hipLaunchKernelGGL(k44_embed_vec_kernel, grid, dim3(256), 0, stream, y, table, ids, D,
-                           vocab, stride, tokens, slots);
+                           vocab, stride, tokens, slots, cp);
     else
         hipLaunchKernelGGL(k44_embed_kernel, grid, dim3(256), 0, stream, y, table, ids, D, vocab,
                            stride, tokens);

@@ -65,9 +65,16 @@ hipError_t launch_token_shift(__half *y, const __half *x, const __half *mu, __ha
 // every 64-channel block b of the output also stores the exact per-token sums of squares of
 // the values it stored (k44_sumsq.hpp) at slots[(b * 16 + t) * 2 + 0 / 1] (limbs 0 | 1, limb 2
 // | inf / NaN flags), the producer side of an RMSNorm folded into the readers of y.
+// cp (with slots only): rows of 16 halves copied from src + r * sstride to dst + r * dstride
+// by the same launch (a folded token shift's compact state copy, refreshed before its readers).
+struct EmbedCopy {
+    const __half *src = nullptr;
+    __half *dst = nullptr;
+    uint32_t rows = 0, sstride = 0, dstride = 0;
+};
 hipError_t launch_embed(__half *y, const __half *table, const uint32_t *ids, uint32_t D,
                         uint32_t vocab, uint32_t stride, uint32_t tokens, hipStream_t stream,
-                        uint64_t *slots = nullptr);
+                        uint64_t *slots = nullptr, const EmbedCopy &cp = EmbedCopy{});
 // history (nullable): ids are also stored at history[*step_ctr][t] while *step_ctr <
 // hist_steps, and *step_ctr is incremented after the argmax (device-side, graph-safe).
 // Two passes: per-chunk (value, index) partials in `scratch` (argmax_scratch_floats(V, stride)

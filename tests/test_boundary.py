@@ -138,7 +138,8 @@ def test_tuning_switches_set_get_reset(wavec):
     wavec.reset_tuning()
     for key, bad in (("dma_stages", 3), ("ksplit", 2), ("xcd_order", 7), ("path", 2),
                      ("narrow_chunk", 15), ("narrow_wgs", 0), ("narrow_reduce", 2),
-                     ("t64_ring", 3), ("dma_prod", 2), ("narrow_pre", 2), ("narrow_local", 2)):
+                     ("t64_ring", 3), ("dma_prod", 2), ("narrow_pre", 2), ("narrow_local", 2),
+                     ("embed_refresh", 2), ("narrow_byy", 2)):
         with pytest.raises(RuntimeError, match="not honoured"):
             wavec.set_tuning(key, bad)
         assert wavec.get_tuning(key) == -1

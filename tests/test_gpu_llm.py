@@ -430,12 +430,14 @@ def test_folded_multiplies_match_unfolded(wavec, tuning, rf, requests):
          f"{len(norm_scaled)} run with their producers' scales, xprod kinds {prods}, "
          f"{rep['launches_per_run']} vs {plans['launched'].exec_report()['launches_per_run']} "
          "launches per run")
-    assert len(fused) == 3 * spec.layers and prods == [0, 2, 3, 4, 5] and len(shifts) == spec.layers
-    # every layer's second norm and the final norm fold; so does the first norm of layers 1..
-    # (after a projection) with its token shift; layer 0's (after the embedding, which stores
-    # the sums of squares) runs with those sums
-    assert len(norm_folded) == 2 * spec.layers and len(norm_shifted) == spec.layers - 1
-    assert len(norm_scaled) == 1
+    assert len(fused) == 3 * spec.layers and prods == [2, 3, 4, 5] and len(shifts) == spec.layers
+    # every norm folds: the first of every layer with its token shift (layer 0's after the
+    # embedding, which stores the sums of squares and refreshes that shift's compact state
+    # copy), the second of every layer and the final one
+    assert len(norm_folded) == 2 * spec.layers + 1 and len(norm_shifted) == spec.layers
+    assert len(norm_scaled) == 0
+    embeds = [a for a in rep["aux"] if a["type"] == "EMBED_1D"]
+    assert len(embeds) == 1 and embeds[0]["refreshes_state_of"] >= 0
     assert not any(a["fused"] for a in plans["launched"].exec_report()["aux"])
     R = spec.requests
     pre.set_ids(np.random.default_rng(5).integers(0, spec.vocab, R * spec.prompt))
